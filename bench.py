@@ -1,0 +1,336 @@
+"""Benchmark of the MI355X attention hot path (one JSON line on stdout).
+
+Headline (BASELINE.json metric "decode-attn HBM GB/s (% of peak) at 32k ctx;
+prefill attn TFLOP/s"): one decode step of config 2 -- Qwen3-8B GQA
+(32 q / 8 kv heads, head_dim 128), 32 sequences with context lengths drawn
+uniformly from [1024, 32768], f16 KV in 16-token pages under a randomly
+permuted page table.  A step is one pi_attn_decode launch over the whole
+batch with K/V already resident in HBM.  `value` is algorithmic bytes (K and V
+of every cached token once, q, out, page-table entries) per second.
+
+Also reported (same line, "prefill"/"workloads"): config 3 causal prefill
+TFLOP/s, the all-32k variant of config 2, config 4 gated decode, config 1,
+and the gated-DeltaNet decode step.  Inputs are synthetic N(0,1) generated on
+the GPU from fixed seeds; RoPE is applied by the library's own kernel.
+
+cpu_baseline: the oracle (a C restatement of the reference's CPU loops,
+single core) on the same decode inputs read back from the pool.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+PAGE = 16
+
+
+def _args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--cpu-seconds", type=float, default=20.0,
+                   help="budget of the single-core CPU baseline sample")
+    p.add_argument("--only-headline", action="store_true")
+    return p.parse_args()
+
+
+class Timer:
+    """HIP events on the stream the library launches on (torch's current stream)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        t0 = time.perf_counter()
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = [a.elapsed_time(b) for a, b in ev]  # ms
+        return {"ms_avg": float(np.mean(per)), "ms_median": float(np.median(per)),
+                "ms_min": float(np.min(per)), "wall_s": wall}
+
+
+def _paged_decode_setup(torch, rt, dev, lens, hq, hkv, d, theta, seed, sections=None,
+                        rope_dim=None, qk_norm=False, eps=1e-6, pool_dtype=None):
+    """Builds a pool holding RoPE'd K and V for every sequence (generated on the GPU)."""
+    rng = np.random.default_rng(seed)
+    n_pages_seq = [(int(x) + PAGE - 1) // PAGE for x in lens]
+    total = sum(n_pages_seq)
+    max_pages = max(n_pages_seq)
+    perm = rng.permutation(total).astype(np.int32)
+    pt = np.full((len(lens), max_pages), -1, np.int32)
+    off = 0
+    for i, n in enumerate(n_pages_seq):
+        pt[i, :n] = perm[off:off + n]
+        off += n
+    pool_dtype = pool_dtype or torch.float16
+    pool = rt.KvPool(dev, total, hkv, d, dtype=pool_dtype)
+    kv_bytes = 2 if pool_dtype == torch.float16 else 4
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    tpt = torch.from_numpy(pt).cuda()
+    rd = rope_dim or d
+    qn = kn = None
+    if qk_norm:
+        qn = torch.rand(d, generator=g, device="cuda") + 0.5
+        kn = torch.rand(d, generator=g, device="cuda") + 0.5
+    zero = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for i, x in enumerate(lens):
+        x = int(x)
+        k = torch.randn((x, hkv, d), generator=g, device="cuda")
+        v = torch.randn((x, hkv, d), generator=g, device="cuda")
+        if kn is not None:
+            rt.head_rmsnorm(dev, k, kn, eps)
+        rt.rope(dev, k, None, torch.arange(x, dtype=torch.int32, device="cuda"), rd, theta,
+                sections)
+        pool.append(k[None], v[None], tpt[i:i + 1].contiguous(), zero)
+        del k, v
+    q = torch.randn((len(lens), hq, d), generator=g, device="cuda")
+    if qn is not None:
+        rt.head_rmsnorm(dev, q, qn, eps)
+    ctx = torch.tensor([int(x) for x in lens], dtype=torch.int32, device="cuda")
+    rt.rope(dev, q, None, ctx - 1, rd, theta, sections)
+    torch.cuda.synchronize()
+    algo = (sum(int(x) for x in lens) * hkv * d * 2 * kv_bytes  # K and V
+            + 2 * len(lens) * hq * d * 4                # q in, out
+            + total * 4 + len(lens) * 4)                # page-table entries, lengths
+    return pool, tpt, ctx, q, algo
+
+
+def _decode_fn(dev, pool, tpt, ctx, q, out, gate=None):
+    lib = dev.lib
+    args = (dev.h, ctypes.c_void_p(q.data_ptr()), pool.p, ctypes.c_void_p(tpt.data_ptr()),
+            tpt.shape[1], ctypes.c_void_p(ctx.data_ptr()), q.shape[0], q.shape[1], 0,
+            1.0 / math.sqrt(q.shape[2]),
+            None if gate is None else ctypes.c_void_p(gate.data_ptr()),
+            ctypes.c_void_p(out.data_ptr()), None)
+
+    def fn():
+        rc = lib.pi_attn_decode(*args)
+        if rc:
+            raise RuntimeError(lib.pi_last_error(dev.h).decode())
+    return fn
+
+
+def bench_decode(torch, rt, dev, timer, lens, hq, hkv, d, theta, seed, steps, warmup, **kw):
+    gate_on = kw.pop("gate", False)
+    pool, tpt, ctx, q, algo = _paged_decode_setup(torch, rt, dev, lens, hq, hkv, d, theta, seed,
+                                                  **kw)
+    out = torch.empty_like(q)
+    gate = torch.randn(q.shape, device="cuda") if gate_on else None
+    if gate is not None:
+        algo += gate.numel() * 4
+    t = timer.run(_decode_fn(dev, pool, tpt, ctx, q, out, gate), steps, warmup)
+    gbs = algo / (t["ms_avg"] * 1e-3) / 1e9
+    res = {"GB_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "ms_per_step": t["ms_avg"],
+           "ms_median": t["ms_median"], "bytes_per_launch": algo,
+           "tokens": int(sum(int(x) for x in lens))}
+    return res, (pool, tpt, ctx, q, out, gate)
+
+
+def cpu_baseline_decode(torch, rt, dev, state, lens, hq, hkv, d, budget_s):
+    """Oracle (single core) on sequences of the same workload until the budget is spent."""
+    from oracle import oracle as orc
+    pool, tpt, ctx, q, out, _ = state
+    qh = q.cpu().numpy()
+    oh = out.cpu().numpy()
+    t_cpu = 0.0
+    nbytes = 0
+    done = 0
+    max_rel = 0.0
+    for i, x in enumerate(lens):
+        x = int(x)
+        ko, vo = pool.read(tpt, i, 0, x)
+        torch.cuda.synchronize()
+        kh, vh = ko.cpu().numpy(), vo.cpu().numpy()
+        t0 = time.perf_counter()
+        ref = orc.attn_decode(qh[i], kh, vh)
+        t_cpu += time.perf_counter() - t0
+        nbytes += x * hkv * d * 2 * 2 + 2 * hq * d * 4
+        done += 1
+        rel = np.linalg.norm(oh[i] - ref, axis=1) / np.linalg.norm(ref, axis=1)
+        max_rel = max(max_rel, float(rel.max()))
+        if t_cpu >= budget_s:
+            break
+    return {"value": nbytes / t_cpu / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle or_attn_decode (C restatement of src/model/mod.rs:1154-1190, "
+                      f"gcc -O3 -msse4.1, 1 thread) on {done} of {len(lens)} sequences "
+                      f"({sum(int(x) for x in lens[:done])} tokens) read back from the pool as "
+                      f"f32; {t_cpu:.1f} s",
+            "parity_max_row_rel_err": max_rel}
+
+
+def bench_prefill(torch, rt, dev, timer, s, hq, hkv, d, theta, seed, steps, warmup):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    q = torch.randn((s, hq, d), generator=g, device="cuda")
+    k = torch.randn((s, hkv, d), generator=g, device="cuda")
+    v = torch.randn((s, hkv, d), generator=g, device="cuda")
+    pos = torch.arange(s, dtype=torch.int32, device="cuda")
+    rt.rope(dev, q, k, pos, d, theta)
+    qb, kb, vb = (t.to(torch.bfloat16)[None].contiguous() for t in (q, k, v))
+    out = torch.empty((1, s, hq, d), device="cuda")
+    lib = dev.lib
+    args = (dev.h, ctypes.c_void_p(qb.data_ptr()), ctypes.c_void_p(kb.data_ptr()),
+            ctypes.c_void_p(vb.data_ptr()), 2, 1, s, hq, hkv, d, 1, 0, 1.0 / math.sqrt(d),
+            ctypes.c_void_p(out.data_ptr()), None)
+
+    def fn():
+        rc = lib.pi_attn_prefill(*args)
+        if rc:
+            raise RuntimeError(lib.pi_last_error(dev.h).decode())
+
+    t = timer.run(fn, steps, warmup)
+    flops = 4.0 * hq * d * s * (s + 1) / 2
+    tf = flops / (t["ms_avg"] * 1e-3) / 1e12
+    return {"TFLOP_s": tf, "mfma_frac": tf / MFMA_F16_PEAK_TFLOPS, "ms_per_step": t["ms_avg"],
+            "flops_per_launch": flops, "tokens_per_s": s / (t["ms_avg"] * 1e-3)}
+
+
+def bench_gdn_decode(torch, rt, dev, timer, steps, warmup):
+    hk, hv, dk, dv = 16, 32, 128, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED0004)
+    q = torch.randn((1, hk, dk), generator=g, device="cuda")
+    k = torch.randn((1, hk, dk), generator=g, device="cuda")
+    v = torch.randn((1, hv, dv), generator=g, device="cuda")
+    beta = torch.sigmoid(torch.randn((1, hv), generator=g, device="cuda"))
+    gg = -torch.nn.functional.softplus(torch.randn((1, hv), generator=g, device="cuda"))
+    state = torch.zeros((1, hv, dk, dv), device="cuda")
+    out = torch.empty((1, hv, dv), device="cuda")
+    lib = dev.lib
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    args = (dev.h, P(q), P(k), P(v), P(beta), P(gg), P(state), P(out), 1, hk, hv, dk, dv, None)
+
+    def fn():
+        rc = lib.pi_gdn_decode(*args)
+        if rc:
+            raise RuntimeError(lib.pi_last_error(dev.h).decode())
+
+    t = timer.run(fn, steps, warmup)
+    algo = 2 * hv * dk * dv * 4 + (2 * hk * dk + 2 * hv * dv + 2 * hv) * 4
+    gbs = algo / (t["ms_avg"] * 1e-3) / 1e9
+    return {"us_per_step": t["ms_avg"] * 1e3, "tokens_per_s": 1e3 / t["ms_avg"], "GB_s": gbs,
+            "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_launch": algo}
+
+
+def _traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+    p = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if os.path.exists(p):
+        try:
+            return json.load(open(p)).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    a = _args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
+              f"(the hot path's sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from powerinfer_x64_amd import runtime as rt
+
+    dev = rt.Device(0)
+    timer = Timer(torch)
+
+    # ---- headline: config 2 decode ----
+    rng = np.random.default_rng(0x5EED0001)
+    lens = [int(x) for x in rng.integers(1024, 32769, size=32)]
+    c2, state = bench_decode(torch, rt, dev, timer, lens, 32, 8, 128, 1e6, 0x5EED0001, a.steps,
+                             a.warmup)
+    t_cpu0 = time.perf_counter()
+    cpu = cpu_baseline_decode(torch, rt, dev, state, lens, 32, 8, 128, a.cpu_seconds)
+    cpu_wall = time.perf_counter() - t_cpu0
+    del state
+    torch.cuda.empty_cache()
+
+    line = {
+        "metric": "decode-attn HBM GB/s (% of peak) at 32k ctx; prefill attn TFLOP/s",
+        "value": round(c2["GB_s"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(c2["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "config 2: Qwen3-8B GQA decode, 32 q / 8 kv heads, head_dim "
+                               "128, batch 32, ctx ~ U[1024, 32768] (seeded), f16 KV in "
+                               "16-token pages, permuted page table, RoPE theta 1e6",
+                   "batch": 32, "ctx_tokens_total": c2["tokens"], "max_ctx": max(lens),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(c2["GB_s"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(c2["hbm_frac"], 4),
+                     "traffic": _traffic("decode_c2")},
+        "cpu_baseline": {k: (round(v, 4) if isinstance(v, float) else v)
+                         for k, v in cpu.items()},
+    }
+
+    if not a.only_headline:
+        wl = {}
+        # config 2 with every context at 32768 (the "at 32k ctx" reading of the metric)
+        r32, st = bench_decode(torch, rt, dev, timer, [32768] * 32, 32, 8, 128, 1e6,
+                               0x5EED0011, a.steps, a.warmup)
+        del st
+        torch.cuda.empty_cache()
+        wl["c2_all_32k_decode"] = r32
+        pf = bench_prefill(torch, rt, dev, timer, 4096, 32, 8, 128, 1e6, 0x5EED0002, a.steps,
+                           a.warmup)
+        torch.cuda.empty_cache()
+        line["prefill"] = {"workload": "config 3: Qwen3-8B causal prefill, S 4096, 32/8 heads, "
+                                       "head_dim 128, bf16 in, f32 softmax/accumulate",
+                           "TFLOP_s": round(pf["TFLOP_s"], 2),
+                           "roofline": {"bound": "mfma", "achieved": round(pf["TFLOP_s"], 2),
+                                        "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                        "frac": round(pf["mfma_frac"], 4)},
+                           "ms_per_step": round(pf["ms_per_step"], 4),
+                           "tokens_per_s": round(pf["tokens_per_s"], 1)}
+        r4, st = bench_decode(torch, rt, dev, timer, [65536] * 8, 16, 2, 256, 1e7, 0x5EED0003,
+                              a.steps, a.warmup, sections=[11, 11, 10, 0], rope_dim=64,
+                              qk_norm=True, gate=True)
+        del st
+        torch.cuda.empty_cache()
+        wl["c4_gated_decode_64k"] = r4
+        r1, st = bench_decode(torch, rt, dev, timer, [513], 32, 32, 128, 1e4, 0x5EED0000,
+                              a.steps, a.warmup, pool_dtype=torch.float32)
+        del st
+        wl["c1_mha_decode_513"] = r1
+        wl["c5_gdn_decode_step"] = bench_gdn_decode(torch, rt, dev, timer, a.steps, a.warmup)
+        line["workloads"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                                 for kk, vv in v.items()} for k, v in wl.items()}
+    line["cpu_baseline_wall_s"] = round(cpu_wall, 2)
+    print(json.dumps(line), flush=True)
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,163 @@
+/*
+ * pi_attn.h -- C ABI of the MI355X (gfx950) attention + gated-DeltaNet path.
+ *
+ * Drop-in boundary for PowerInfer_x64's CPU attention / SSM path.  Each entry
+ * point names the reference code it replaces (paths relative to the
+ * PowerInfer_x64 repository root).  Conventions:
+ *   - every function returns pi_status (0 = PI_OK); on failure the text is in
+ *     pi_last_error(handle) -- the analogue of the reference's
+ *     Option<Result<(), String>> offload seam (src/cuda/mod.rs:527-537,
+ *     src/model/mod.rs:612-626): PI_OK = Some(Ok), an error = Some(Err(text)),
+ *     and a caller without a handle takes the CPU path (None);
+ *   - status classes follow BackendError (src/runtime/mod.rs:6-18);
+ *   - pointers named d_* are device pointers (HBM), h_* are host pointers;
+ *   - `stream` is a hipStream_t; NULL is HIP's default (null) stream.  Calls
+ *     are asynchronous on that stream except the h_* "sync" wrappers, which
+ *     run on the handle's own stream and synchronise before returning, like
+ *     GpuDevice::matvec (src/cuda/mod.rs:244-330);
+ *   - one handle per host thread; the library takes no locks;
+ *   - all arithmetic is fp32 except where a dtype argument says otherwise;
+ *   - page_tokens is 16; head_dim is 64, 128 or 256.
+ */
+#ifndef PI_ATTN_H
+#define PI_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PI_ATTN_ABI_VERSION 1
+
+/* src/runtime/mod.rs:6-18 (BackendError) */
+typedef enum pi_status {
+    PI_OK = 0,
+    PI_ERR_INVALID_ARG = 1,    /* bad pointer / shape (debug_assert_eq! in src/ops.rs:14-15) */
+    PI_ERR_OUT_OF_MEMORY = 2,  /* BackendError::OutOfMemory */
+    PI_ERR_INVALID_KERNEL = 3, /* BackendError::InvalidKernel: no gfx950 code object / launch failed */
+    PI_ERR_DEVICE = 4,         /* BackendError::CudaError(String): HIP runtime error */
+    PI_ERR_UNSUPPORTED = 5     /* BackendError::Unsupported: shape/dtype outside the kernels */
+} pi_status;
+
+typedef enum pi_dtype { PI_F32 = 0, PI_F16 = 1, PI_BF16 = 2 } pi_dtype;
+
+/* Q head h reads KV head h % n_kv_heads (src/model/mod.rs:1155, the reference's
+ * mapping) or h / (n_q_heads / n_kv_heads) (the usual grouped layout). */
+typedef enum pi_gqa_mode { PI_GQA_MODULO = 0, PI_GQA_GROUPED = 1 } pi_gqa_mode;
+
+typedef struct pi_handle_s* pi_handle;
+typedef struct pi_kv_pool_s* pi_kv_pool;
+
+/* ---- handle ---------------------------------------------------------------
+ * Replaces GpuDevice::new / GpuResources::init (src/cuda/mod.rs:196-242,
+ * :387-460): binds a device, creates the handle's stream and lazily-grown
+ * workspace (the reference's RefCell scratch, src/cuda/mod.rs:152,257-278). */
+int pi_create(int device, pi_handle* out);
+/* Drop ordering of src/cuda/mod.rs:166-178,540-573: frees with the device current. */
+void pi_destroy(pi_handle h);
+/* Text of the last error on this handle (or of the last pi_create failure when h is NULL). */
+const char* pi_last_error(pi_handle h);
+/* stream.synchronize() (src/cuda/mod.rs:312-314). */
+int pi_sync(pi_handle h, void* stream);
+int pi_abi_version(void);
+
+/* ---- paged KV cache --------------------------------------------------------
+ * Replaces LayerCache (src/model/mod.rs:73-106): instead of a growing f32
+ * Vec [T][n_kv][D], a pool of fixed 16-token pages in HBM, one K and one V
+ * block of 16 x head_dim per (page, kv head).  Sequences own pages through a
+ * caller-provided int32 page table [n_seq][max_pages]. */
+int pi_kv_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t n_kv_heads,
+                      int32_t head_dim, int32_t dtype, pi_kv_pool* out);
+void pi_kv_pool_destroy(pi_kv_pool pool);
+/* Total bytes of the K and V blocks (for capacity planning on 288 GB). */
+size_t pi_kv_pool_bytes(pi_kv_pool pool);
+
+/* Append (src/model/mod.rs:1140-1146, extend_from_slice): sequence s writes
+ * n_tok tokens at positions d_start_pos[s] .. +n_tok-1.  d_k/d_v:
+ * [n_seq][n_tok][n_kv_heads][head_dim] in src_dtype (converted, RNE, to the
+ * pool dtype). */
+int pi_kv_append(pi_handle h, pi_kv_pool pool, const void* d_k, const void* d_v, int32_t src_dtype,
+                 const int32_t* d_page_table, int32_t max_pages, const int32_t* d_start_pos,
+                 int32_t n_seq, int32_t n_tok, void* stream);
+/* Read tokens [start, start+n_tok) of sequence `seq` back as f32 [n_tok][n_kv][D]
+ * (the reference cache layout; used for dumps and parity checks). */
+int pi_kv_read(pi_handle h, pi_kv_pool pool, const int32_t* d_page_table, int32_t max_pages,
+               int32_t seq, int32_t start, int32_t n_tok, float* d_k_out, float* d_v_out,
+               void* stream);
+/* reset() (src/model/mod.rs:1847-1873) needs no device work: a sequence is
+ * reset by giving it length 0; pages are owned by the caller's table. */
+
+/* ---- decode prologue -------------------------------------------------------
+ * Per-head RMSNorm in place (ops::rms_norm, src/ops.rs:13-27, as called at
+ * src/model/mod.rs:1035-1070): rows of `dim` values at stride `row_stride`. */
+int pi_head_rmsnorm(pi_handle h, float* d_x, const float* d_w, int32_t n_rows, int32_t dim,
+                    int32_t row_stride, float eps, void* stream);
+/* RoPE in place on q [n_tok][n_q_heads][head_dim] and k [n_tok][n_kv_heads][head_dim]
+ * at positions d_pos[n_tok].  h_sections == NULL: ops::apply_rope (src/ops.rs:35-67,
+ * adjacent pairs, rope_dim dims).  Otherwise ops::compute_imrope_freqs +
+ * apply_rope_with_freqs (src/ops.rs:78-157, NeoX pairs over rope_dim dims).
+ * Frequencies are built on the host with the reference's f32 formula.  d_k may
+ * be NULL (rotate q only, the src/model/mod.rs:1113-1134 dummy-k branch). */
+int pi_rope(pi_handle h, float* d_q, float* d_k, const int32_t* d_pos, int32_t n_tok,
+            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t rope_dim,
+            float base, const int32_t* h_sections, void* stream);
+
+/* ---- attention ---------------------------------------------------------------
+ * Decode: one query token per sequence against its paged cache
+ * (src/model/mod.rs:1148-1190; append-then-attend: the caller appends the
+ * token's K/V first, so d_ctx_len counts it).  d_q [batch][n_q_heads][D] f32
+ * (normed, rotated); out [batch][n_q_heads][D] f32.  scale multiplies q.k
+ * (1/sqrt(D) in the reference).  d_gate (nullable) [batch][n_q_heads][D]:
+ * out *= sigmoid(gate) (src/model/mod.rs:1192-1196).  Split-K flash decoding,
+ * one launch; n_q_heads/n_kv_heads <= 16. */
+int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t* d_page_table,
+                   int32_t max_pages, const int32_t* d_ctx_len, int32_t batch,
+                   int32_t n_q_heads, int32_t gqa_mode, float scale, const float* d_gate,
+                   float* d_out, void* stream);
+
+/* Causal prefill of a whole prompt: row i attends keys 0..i, which is what the
+ * reference's per-token loop computes (src/model/mod.rs:668,1140-1190).
+ * d_q [batch][seq_len][n_q_heads][D], d_k/d_v [batch][seq_len][n_kv_heads][D]
+ * in dtype (PI_BF16 or PI_F16); d_out [batch][seq_len][n_q_heads][D] f32.
+ * MFMA flash attention with fp32 softmax/accumulation; D = 128. */
+int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d_v, int32_t dtype,
+                    int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
+                    int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale, float* d_out,
+                    void* stream);
+
+/* ---- gated DeltaNet ----------------------------------------------------------
+ * Gates (src/model/mod.rs:796-839): beta = sigmoid(beta_raw),
+ * g = ssm_a * softplus(a_raw + dt_bias) (identity above 10).
+ * beta_raw/a_raw/beta/g: [n_tok][n_v_heads]; ssm_a/dt_bias: [n_v_heads]. */
+int pi_gdn_gates(pi_handle h, const float* d_beta_raw, const float* d_a_raw, const float* d_ssm_a,
+                 const float* d_dt_bias, float* d_beta, float* d_g, int32_t n_tok,
+                 int32_t n_v_heads, void* stream);
+/* One recurrent step per sequence (src/model/mod.rs:841-916): q/k raw
+ * [batch][n_k_heads][k_hd], v [batch][n_v_heads][v_hd], beta/g [batch][n_v_heads],
+ * state [batch][n_v_heads][k_hd][v_hd] f32 in/out (ssm::create_ssm_state,
+ * src/ssm/mod.rs:164-166: zero-initialised by the caller), out
+ * [batch][n_v_heads][v_hd] (before RMSNormGated).  k_hd = v_hd = 128. */
+int pi_gdn_decode(pi_handle h, const float* d_q, const float* d_k, const float* d_v,
+                  const float* d_beta, const float* d_g, float* d_state, float* d_out,
+                  int32_t batch, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
+                  int32_t v_hd, void* stream);
+/* n_tok tokens of one sequence, equal to n_tok consecutive pi_gdn_decode steps
+ * (the reference's per-token prefill), computed in chunks of `chunk` tokens
+ * (64).  Layouts as pi_gdn_decode with batch replaced by n_tok; state in/out. */
+int pi_gdn_prefill(pi_handle h, const float* d_q, const float* d_k, const float* d_v,
+                   const float* d_beta, const float* d_g, float* d_state, float* d_out,
+                   int32_t n_tok, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
+                   int32_t v_hd, int32_t chunk, void* stream);
+
+/* ---- host-slice drop-ins (synchronous) ---------------------------------------
+ * ops::attention_head (src/ops.rs:213-247) with host slices: copies in,
+ * runs the decode kernel, copies out.  k/v caches [seq_len][head_dim]. */
+int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const float* h_k_cache,
+                          const float* h_v_cache, size_t seq_len, size_t head_dim);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PI_ATTN_H */

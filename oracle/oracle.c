@@ -1,0 +1,399 @@
+/*
+ * oracle.c -- CPU restatement of PowerInfer_x64's attention + gated-DeltaNet path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker and timed CPU baseline); the
+ * product never links or loads it.  Build: oracle/Makefile
+ * (gcc -O3 -msse4.1 -ffp-contract=off).  Each function cites the reference
+ * function it restates; see oracle.h for the contract of every entry.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* The reference's SSE horizontal sum (src/simd.rs:43-53):
+ * movehdup + add gives [a+b, ., c+d, .]; movehl + add_ss gives (a+b)+(c+d). */
+static float hsum4(const float l[4]) { return (l[0] + l[1]) + (l[2] + l[3]); }
+
+float or_dot_product(const float* a, const float* b, size_t n) {
+    /* src/simd.rs:14-40: four lane accumulators, sum += a*b (mul then add). */
+    float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    size_t i = 0;
+    for (; i + 4 <= n; i += 4) {
+        for (int j = 0; j < 4; ++j) {
+            float p = a[i + j] * b[i + j];
+            lane[j] = lane[j] + p;
+        }
+    }
+    float r = hsum4(lane);
+    for (; i < n; ++i) r += a[i] * b[i];
+    return r;
+}
+
+float or_sum_squares(const float* a, size_t n) {
+    /* src/simd.rs:115-135 */
+    float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    size_t i = 0;
+    for (; i + 4 <= n; i += 4) {
+        for (int j = 0; j < 4; ++j) {
+            float p = a[i + j] * a[i + j];
+            lane[j] = lane[j] + p;
+        }
+    }
+    float r = hsum4(lane);
+    for (; i < n; ++i) r += a[i] * a[i];
+    return r;
+}
+
+void or_scale(float* out, const float* a, float s, size_t n) {
+    /* src/simd.rs:139-156 */
+    for (size_t i = 0; i < n; ++i) out[i] = a[i] * s;
+}
+
+void or_rms_norm(float* out, const float* x, const float* w, size_t n, float eps) {
+    /* src/ops.rs:13-27: rms = sqrt(sum_sq/n + eps); out = (x * (1/rms)) * w. */
+    float sum_sq = or_sum_squares(x, n);
+    float rms = sqrtf(sum_sq / (float)n + eps);
+    float inv_rms = 1.0f / rms;
+    or_scale(out, x, inv_rms, n);
+    for (size_t i = 0; i < n; ++i) out[i] *= w[i];
+}
+
+void or_apply_rope(float* q, float* k, size_t position, size_t head_dim, size_t rope_dim,
+                   float base) {
+    /* src/ops.rs:35-67: freq_i = 1/base^(2i/rope_dim) in f32; theta = pos * freq. */
+    size_t half = rope_dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        float expo = 2.0f * (float)i / (float)rope_dim;
+        float freq = 1.0f / powf(base, expo);
+        float theta = (float)position * freq;
+        float c = cosf(theta);
+        float s = sinf(theta);
+        if (2 * i + 1 < head_dim) {
+            float q0 = q[2 * i], q1 = q[2 * i + 1];
+            q[2 * i] = q0 * c - q1 * s;
+            q[2 * i + 1] = q0 * s + q1 * c;
+        }
+        if (2 * i + 1 < head_dim) {
+            float k0 = k[2 * i], k1 = k[2 * i + 1];
+            k[2 * i] = k0 * c - k1 * s;
+            k[2 * i + 1] = k0 * s + k1 * c;
+        }
+    }
+}
+
+void or_compute_imrope_freqs(float base, size_t n_rot, const int32_t sections[4], float* freqs) {
+    /* src/ops.rs:78-122: theta_scale = base^(-2/n_rot); four tracks that all
+     * start at 1 and advance by one f32 multiply per pair, so every track
+     * holds theta_scale^k obtained by repeated multiplication. */
+    float theta_scale = powf(base, -2.0f / (float)n_rot);
+    size_t sect_dims = (size_t)(sections[0] + sections[1] + sections[2] + sections[3]);
+    size_t n_pairs = n_rot / 2;
+    float t_t = 1.0f, t_h = 1.0f, t_w = 1.0f, t_e = 1.0f;
+    for (size_t pair = 0; pair < n_pairs; ++pair) {
+        size_t sector = sect_dims > 0 ? pair % sect_dims : pair;
+        float theta;
+        if (sector % 3 == 0 && sector < 3 * (size_t)sections[0])
+            theta = t_t;
+        else if (sector % 3 == 1 && sector < 3 * (size_t)sections[1])
+            theta = t_h;
+        else if (sector % 3 == 2 && sector < 3 * (size_t)sections[2])
+            theta = t_w;
+        else
+            theta = t_e;
+        freqs[pair] = theta;
+        t_t *= theta_scale;
+        t_h *= theta_scale;
+        t_w *= theta_scale;
+        t_e *= theta_scale;
+    }
+}
+
+void or_apply_rope_with_freqs(float* q, float* k, size_t position, size_t head_dim,
+                              const float* freqs, size_t n_freqs) {
+    /* src/ops.rs:130-157 */
+    size_t half = n_freqs;
+    for (size_t i = 0; i < n_freqs; ++i) {
+        float theta = (float)position * freqs[i];
+        float c = cosf(theta);
+        float s = sinf(theta);
+        if (i + half < head_dim) {
+            float q0 = q[i], q1 = q[i + half];
+            q[i] = q0 * c - q1 * s;
+            q[i + half] = q0 * s + q1 * c;
+        }
+        if (i + half < head_dim) {
+            float k0 = k[i], k1 = k[i + half];
+            k[i] = k0 * c - k1 * s;
+            k[i + half] = k0 * s + k1 * c;
+        }
+    }
+}
+
+void or_softmax(float* x, size_t n) {
+    /* src/ops.rs:160-180: max fold, exp(x-max) with a sequential f32 sum, x *= 1/sum. */
+    if (n == 0) return;
+    float max_val = -INFINITY;
+    for (size_t i = 0; i < n; ++i) max_val = fmaxf(max_val, x[i]);
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        x[i] = expf(x[i] - max_val);
+        sum += x[i];
+    }
+    float inv_sum = 1.0f / sum;
+    for (size_t i = 0; i < n; ++i) x[i] *= inv_sum;
+}
+
+void or_attention_head(float* out, const float* q, const float* k_cache, const float* v_cache,
+                       size_t seq_len, size_t head_dim) {
+    /* src/ops.rs:213-247 -- scalar dot (not the SSE one), scores * scale, softmax, t-outer V sum. */
+    float scale = 1.0f / sqrtf((float)head_dim);
+    float* scores = (float*)malloc((seq_len ? seq_len : 1) * sizeof(float));
+    for (size_t t = 0; t < seq_len; ++t) {
+        float dot = 0.0f;
+        for (size_t d = 0; d < head_dim; ++d) dot += q[d] * k_cache[t * head_dim + d];
+        scores[t] = dot * scale;
+    }
+    or_softmax(scores, seq_len);
+    for (size_t d = 0; d < head_dim; ++d) out[d] = 0.0f;
+    for (size_t t = 0; t < seq_len; ++t)
+        for (size_t d = 0; d < head_dim; ++d) out[d] += scores[t] * v_cache[t * head_dim + d];
+    free(scores);
+}
+
+void or_attn_decode(float* out, const float* q, size_t q_head_dim, const float* key_cache,
+                    const float* value_cache, size_t total_seq, size_t n_heads, size_t n_kv_heads,
+                    size_t kv_head_dim, size_t v_head_dim) {
+    /* src/model/mod.rs:1154-1190 (f32 cache path). */
+    float scale = 1.0f / sqrtf((float)kv_head_dim);
+    float* scores = (float*)malloc((total_seq ? total_seq : 1) * sizeof(float));
+    size_t n = kv_head_dim < v_head_dim ? kv_head_dim : v_head_dim;
+    for (size_t h = 0; h < n_heads; ++h) {
+        size_t kv_h = h % n_kv_heads; /* modulo GQA, :1155 */
+        const float* q_attn = q + h * q_head_dim;
+        for (size_t t = 0; t < total_seq; ++t) {
+            const float* ks = key_cache + t * n_kv_heads * kv_head_dim + kv_h * kv_head_dim;
+            scores[t] = or_dot_product(q_attn, ks, kv_head_dim) * scale;
+        }
+        or_softmax(scores, total_seq);
+        float* ho = out + h * kv_head_dim;
+        for (size_t d = 0; d < kv_head_dim; ++d) ho[d] = 0.0f;
+        for (size_t t = 0; t < total_seq; ++t) {
+            float w = scores[t];
+            const float* vs = value_cache + t * n_kv_heads * v_head_dim + kv_h * v_head_dim;
+            for (size_t d = 0; d < n; ++d) ho[d] += w * vs[d];
+        }
+    }
+    free(scores);
+}
+
+void or_apply_gate(float* out, const float* gate, size_t n) {
+    /* src/model/mod.rs:1192-1196 */
+    for (size_t i = 0; i < n; ++i) {
+        float s = 1.0f / (1.0f + expf(-gate[i]));
+        out[i] *= s;
+    }
+}
+
+/* The Q/K norm + RoPE part of one token (src/model/mod.rs:1035-1138). */
+static void prepare_token(float* qt, float* kt, size_t n_heads, size_t n_kv_heads,
+                          size_t q_head_dim, size_t kv_head_dim, const float* q_norm_w,
+                          const float* k_norm_w, float eps, size_t attn_rope_dim,
+                          float rope_base, const float* freqs, size_t n_attn_freqs,
+                          size_t abs_pos, float* tmp, float* dummy_k) {
+    size_t norm_end = kv_head_dim < q_head_dim ? kv_head_dim : q_head_dim;
+    /* Q/K RMSNorm (:1035-1070): first norm_end dims of each Q head, whole K head. */
+    if (q_norm_w && qt)
+        for (size_t h = 0; h < n_heads; ++h) {
+            or_rms_norm(tmp, qt + h * q_head_dim, q_norm_w, norm_end, eps);
+            memcpy(qt + h * q_head_dim, tmp, norm_end * sizeof(float));
+        }
+    if (k_norm_w && kt)
+        for (size_t h = 0; h < n_kv_heads; ++h) {
+            or_rms_norm(tmp, kt + h * kv_head_dim, k_norm_w, kv_head_dim, eps);
+            memcpy(kt + h * kv_head_dim, tmp, kv_head_dim * sizeof(float));
+        }
+    /* RoPE driver (:1072-1138): every Q head; K head h only when h < n_kv_heads. */
+    for (size_t h = 0; h < n_heads; ++h) {
+        float* qh = qt ? qt + h * q_head_dim : NULL;
+        float* kh = (kt && h < n_kv_heads) ? kt + (h % n_kv_heads) * kv_head_dim : NULL;
+        if (!qh) {
+            memset(tmp, 0, kv_head_dim * sizeof(float));
+            qh = tmp;
+        }
+        if (!kh) memset(dummy_k, 0, kv_head_dim * sizeof(float));
+        float* kk = kh ? kh : dummy_k;
+        if (freqs)
+            or_apply_rope_with_freqs(qh, kk, abs_pos, kv_head_dim, freqs, n_attn_freqs);
+        else
+            or_apply_rope(qh, kk, abs_pos, kv_head_dim, attn_rope_dim, rope_base);
+    }
+}
+
+static size_t cap_rope(size_t rope_dim, size_t kv_head_dim) {
+    return rope_dim < kv_head_dim ? rope_dim : kv_head_dim;
+}
+
+void or_attn_prepare(float* q, float* k, size_t n_tokens, size_t n_heads, size_t n_kv_heads,
+                     size_t q_head_dim, size_t kv_head_dim, const float* q_norm_w,
+                     const float* k_norm_w, float eps, size_t rope_dim, float rope_base,
+                     const float* freqs, size_t n_freqs, size_t pos0) {
+    size_t attn_rope_dim = cap_rope(rope_dim, kv_head_dim);
+    size_t n_attn_freqs = freqs ? attn_rope_dim / 2 : 0;
+    if (n_attn_freqs > n_freqs) n_attn_freqs = n_freqs;
+    size_t mx = kv_head_dim > q_head_dim ? kv_head_dim : q_head_dim;
+    float* tmp = (float*)malloc(mx * sizeof(float));
+    float* dummy_k = (float*)calloc(kv_head_dim, sizeof(float));
+    for (size_t pos = 0; pos < n_tokens; ++pos)
+        prepare_token(q ? q + pos * n_heads * q_head_dim : NULL,
+                      k ? k + pos * n_kv_heads * kv_head_dim : NULL, n_heads, n_kv_heads,
+                      q_head_dim, kv_head_dim, q_norm_w, k_norm_w, eps, attn_rope_dim, rope_base,
+                      freqs, n_attn_freqs, pos0 + pos, tmp, dummy_k);
+    free(tmp);
+    free(dummy_k);
+}
+
+void or_attn_layer_tokens(float* out, float* q, const float* gate, float* k, const float* v,
+                          size_t n_tokens, size_t n_heads, size_t n_kv_heads, size_t q_head_dim,
+                          size_t kv_head_dim, size_t v_head_dim, const float* q_norm_w,
+                          const float* k_norm_w, float eps, size_t rope_dim, float rope_base,
+                          const float* freqs, size_t n_freqs, float* key_cache,
+                          float* value_cache, size_t prev_seq_len) {
+    size_t attn_rope_dim = cap_rope(rope_dim, kv_head_dim);
+    size_t n_attn_freqs = freqs ? attn_rope_dim / 2 : 0;
+    if (n_attn_freqs > n_freqs) n_attn_freqs = n_freqs;
+    size_t mx = kv_head_dim > q_head_dim ? kv_head_dim : q_head_dim;
+    float* tmp = (float*)malloc(mx * sizeof(float));
+    float* dummy_k = (float*)calloc(kv_head_dim, sizeof(float));
+    for (size_t pos = 0; pos < n_tokens; ++pos) {
+        float* qt = q + pos * n_heads * q_head_dim;
+        float* kt = k + pos * n_kv_heads * kv_head_dim;
+        const float* vt = v + pos * n_kv_heads * v_head_dim;
+        size_t t_idx = prev_seq_len + pos;
+        prepare_token(qt, kt, n_heads, n_kv_heads, q_head_dim, kv_head_dim, q_norm_w, k_norm_w,
+                      eps, attn_rope_dim, rope_base, freqs, n_attn_freqs, t_idx, tmp, dummy_k);
+        /* Append-then-attend (:1140-1148). */
+        memcpy(key_cache + t_idx * n_kv_heads * kv_head_dim, kt,
+               n_kv_heads * kv_head_dim * sizeof(float));
+        memcpy(value_cache + t_idx * n_kv_heads * v_head_dim, vt,
+               n_kv_heads * v_head_dim * sizeof(float));
+        float* ot = out + pos * n_heads * kv_head_dim;
+        or_attn_decode(ot, qt, q_head_dim, key_cache, value_cache, t_idx + 1, n_heads, n_kv_heads,
+                       kv_head_dim, v_head_dim);
+        if (gate) or_apply_gate(ot, gate + pos * n_heads * q_head_dim, n_heads * kv_head_dim);
+    }
+    free(tmp);
+    free(dummy_k);
+}
+
+void or_gdn_gates(float* beta, float* g, const float* beta_raw, const float* a_raw,
+                  const float* ssm_a, const float* dt_bias, size_t n_v_heads) {
+    /* src/model/mod.rs:806-809 (beta) and :826-839 (g). */
+    for (size_t h = 0; h < n_v_heads; ++h) beta[h] = 1.0f / (1.0f + expf(-beta_raw[h]));
+    for (size_t h = 0; h < n_v_heads; ++h) {
+        float sp_in = a_raw[h] + dt_bias[h];
+        float sp = sp_in > 10.0f ? sp_in : logf(1.0f + expf(sp_in));
+        g[h] = ssm_a[h] * sp;
+    }
+}
+
+/* Iterator::sum::<f32>() over x*x: a sequential left fold. */
+static float seq_sum_sq(const float* x, size_t n) {
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i) s += x[i] * x[i];
+    return s;
+}
+
+void or_gdn_step(float* out, float* state, const float* q_raw, const float* k_raw, const float* v,
+                 const float* beta, const float* g, size_t n_k_heads, size_t n_v_heads,
+                 size_t k_hd, size_t v_hd) {
+    float* qh = (float*)malloc(k_hd * sizeof(float));
+    float* kh = (float*)malloc(k_hd * sizeof(float));
+    float* kv_mem = (float*)malloc(v_hd * sizeof(float));
+    float q_scale = 1.0f / sqrtf((float)k_hd); /* :859 */
+    for (size_t vh = 0; vh < n_v_heads; ++vh) {
+        /* Tiled repeat (:845-853): V head vh reads K head vh % n_k_heads. */
+        size_t src = (vh % n_k_heads) * k_hd;
+        memcpy(qh, q_raw + src, k_hd * sizeof(float));
+        memcpy(kh, k_raw + src, k_hd * sizeof(float));
+        /* L2 norm with max(norm, 1e-12), q additionally scaled (:860-875). */
+        float nq = sqrtf(seq_sum_sq(qh, k_hd));
+        if (nq < 1e-12f) nq = 1e-12f;
+        for (size_t i = 0; i < k_hd; ++i) qh[i] = qh[i] / nq * q_scale;
+        float nk = sqrtf(seq_sum_sq(kh, k_hd));
+        if (nk < 1e-12f) nk = 1e-12f;
+        for (size_t i = 0; i < k_hd; ++i) kh[i] /= nk;
+
+        /* Delta rule (:883-916). */
+        float decay = expf(g[vh]);
+        float beta_h = beta[vh];
+        const float* v_h = v + vh * v_hd;
+        float* S = state + vh * k_hd * v_hd;
+        for (size_t i = 0; i < k_hd * v_hd; ++i) S[i] *= decay;
+        for (size_t vi = 0; vi < v_hd; ++vi) kv_mem[vi] = 0.0f;
+        for (size_t ki = 0; ki < k_hd; ++ki) {
+            float kval = kh[ki];
+            const float* row = S + ki * v_hd;
+            for (size_t vi = 0; vi < v_hd; ++vi) kv_mem[vi] += row[vi] * kval;
+        }
+        float* o = out + vh * v_hd;
+        for (size_t vi = 0; vi < v_hd; ++vi) o[vi] = 0.0f;
+        for (size_t ki = 0; ki < k_hd; ++ki) {
+            float kval = kh[ki], qval = qh[ki];
+            float* row = S + ki * v_hd;
+            for (size_t vi = 0; vi < v_hd; ++vi) {
+                float delta = (v_h[vi] - kv_mem[vi]) * beta_h;
+                row[vi] += kval * delta;
+                o[vi] += row[vi] * qval;
+            }
+        }
+    }
+    free(qh);
+    free(kh);
+    free(kv_mem);
+}
+
+void or_gdn_tokens(float* out, float* state, const float* q_raw, const float* k_raw,
+                   const float* v, const float* beta, const float* g, size_t n_tokens,
+                   size_t n_k_heads, size_t n_v_heads, size_t k_hd, size_t v_hd) {
+    for (size_t t = 0; t < n_tokens; ++t)
+        or_gdn_step(out + t * n_v_heads * v_hd, state, q_raw + t * n_k_heads * k_hd,
+                    k_raw + t * n_k_heads * k_hd, v + t * n_v_heads * v_hd, beta + t * n_v_heads,
+                    g + t * n_v_heads, n_k_heads, n_v_heads, k_hd, v_hd);
+}
+
+void or_rmsnorm_gated(float* o, const float* z, const float* w, size_t n_v_heads, size_t v_hd,
+                      float eps) {
+    /* src/model/mod.rs:918-932 */
+    for (size_t vh = 0; vh < n_v_heads; ++vh) {
+        float* oh = o + vh * v_hd;
+        const float* zh = z + vh * v_hd;
+        float var = seq_sum_sq(oh, v_hd) / (float)v_hd;
+        float scale = 1.0f / sqrtf(var + eps);
+        for (size_t i = 0; i < v_hd; ++i) {
+            float normed = oh[i] * scale * w[i];
+            float zv = zh[i];
+            float silu_z = zv / (1.0f + expf(-zv));
+            oh[i] = normed * silu_z;
+        }
+    }
+}
+
+void or_conv1d_silu(float* x, float* hist, const float* w, size_t conv_dim, size_t d_conv) {
+    /* src/model/mod.rs:750-776: window = the d_conv-1 previous raw inputs plus
+     * this one, oldest first; w[i*d_conv + k] multiplies window[k][i]. */
+    size_t nh = d_conv - 1;
+    for (size_t i = 0; i < conv_dim; ++i) {
+        float raw = x[i];
+        float val = 0.0f;
+        for (size_t kk = 0; kk < d_conv; ++kk) {
+            float cs = kk < nh ? hist[kk * conv_dim + i] : raw;
+            val += w[i * d_conv + kk] * cs;
+        }
+        /* shift the raw input into the history */
+        for (size_t kk = 0; kk + 1 < nh; ++kk) hist[kk * conv_dim + i] = hist[(kk + 1) * conv_dim + i];
+        if (nh > 0) hist[(nh - 1) * conv_dim + i] = raw;
+        x[i] = val / (1.0f + expf(-val));
+    }
+}

@@ -1,0 +1,265 @@
+"""ctypes front end of the CPU oracle (oracle.c).
+
+TEST INFRASTRUCTURE ONLY: tests/, ``__graft_entry__.smoke()`` and bench.py's
+``cpu_baseline`` leg import this module as the parity checker and CPU
+baseline.  The product package never imports it.
+
+Each wrapper takes numpy arrays, checks shapes and dtypes, and calls the C
+restatement of the reference function named in oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_sz = ctypes.c_size_t
+
+
+def build() -> str:
+    """Compile oracle.c with oracle/Makefile; returns the library path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        sig = {
+            "or_dot_product": (ctypes.c_float, [_f32p, _f32p, _sz]),
+            "or_sum_squares": (ctypes.c_float, [_f32p, _sz]),
+            "or_scale": (None, [_f32p, _f32p, ctypes.c_float, _sz]),
+            "or_rms_norm": (None, [_f32p, _f32p, _f32p, _sz, ctypes.c_float]),
+            "or_apply_rope": (None, [_f32p, _f32p, _sz, _sz, _sz, ctypes.c_float]),
+            "or_compute_imrope_freqs": (None, [ctypes.c_float, _sz, _i32p, _f32p]),
+            "or_apply_rope_with_freqs": (None, [_f32p, _f32p, _sz, _sz, _f32p, _sz]),
+            "or_softmax": (None, [_f32p, _sz]),
+            "or_attention_head": (None, [_f32p, _f32p, _f32p, _f32p, _sz, _sz]),
+            "or_attn_decode": (None, [_f32p, _f32p, _sz, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz]),
+            "or_apply_gate": (None, [_f32p, _f32p, _sz]),
+            "or_attn_layer_tokens": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz,
+                                            _sz, _sz, _f32p, _f32p, ctypes.c_float, _sz,
+                                            ctypes.c_float, _f32p, _sz, _f32p, _f32p, _sz]),
+            "or_attn_prepare": (None, [_f32p, _f32p, _sz, _sz, _sz, _sz, _sz, _f32p, _f32p,
+                                       ctypes.c_float, _sz, ctypes.c_float, _f32p, _sz, _sz]),
+            "or_gdn_gates": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _sz]),
+            "or_gdn_step": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz,
+                                   _sz, _sz]),
+            "or_gdn_tokens": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz,
+                                     _sz, _sz, _sz]),
+            "or_rmsnorm_gated": (None, [_f32p, _f32p, _f32p, _sz, _sz, ctypes.c_float]),
+            "or_conv1d_silu": (None, [_f32p, _f32p, _f32p, _sz, _sz]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _f32(a, writable=False):
+    """Return a C-contiguous float32 view (copy if needed) and its pointer."""
+    arr = np.ascontiguousarray(a, dtype=np.float32)
+    if writable and arr is not a:
+        arr = arr.copy()
+    return arr
+
+
+def _p(arr):
+    if arr is None:
+        return None
+    assert arr.dtype == np.float32 and arr.flags.c_contiguous
+    return arr.ctypes.data_as(_f32p)
+
+
+# ---- src/simd.rs -----------------------------------------------------------
+
+def dot_product(a, b) -> float:
+    a, b = _f32(a), _f32(b)
+    assert a.shape == b.shape
+    return float(lib().or_dot_product(_p(a), _p(b), a.size))
+
+
+def sum_squares(a) -> float:
+    a = _f32(a)
+    return float(lib().or_sum_squares(_p(a), a.size))
+
+
+def scale(a, s: float):
+    a = _f32(a)
+    out = np.empty_like(a)
+    lib().or_scale(_p(out), _p(a), float(s), a.size)
+    return out
+
+
+# ---- src/ops.rs ------------------------------------------------------------
+
+def rms_norm(x, w, eps: float):
+    x, w = _f32(x), _f32(w)
+    assert x.shape == w.shape
+    out = np.empty_like(x)
+    lib().or_rms_norm(_p(out), _p(x), _p(w), x.size, float(eps))
+    return out
+
+
+def apply_rope(q, k, position: int, head_dim: int, rope_dim: int, base: float):
+    """Returns rotated copies of q and k (the reference rotates in place)."""
+    q = np.array(q, dtype=np.float32, copy=True)
+    k = np.array(k, dtype=np.float32, copy=True)
+    lib().or_apply_rope(_p(q), _p(k), position, head_dim, rope_dim, float(base))
+    return q, k
+
+
+def compute_imrope_freqs(base: float, n_rot: int, sections):
+    sec = (ctypes.c_int32 * 4)(*[int(s) for s in sections])
+    out = np.empty(n_rot // 2, dtype=np.float32)
+    lib().or_compute_imrope_freqs(float(base), n_rot, sec, _p(out))
+    return out
+
+
+def apply_rope_with_freqs(q, k, position: int, head_dim: int, freqs):
+    q = np.array(q, dtype=np.float32, copy=True)
+    k = np.array(k, dtype=np.float32, copy=True)
+    f = _f32(freqs)
+    lib().or_apply_rope_with_freqs(_p(q), _p(k), position, head_dim, _p(f), f.size)
+    return q, k
+
+
+def softmax(x):
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().or_softmax(_p(x), x.size)
+    return x
+
+
+def attention_head(q, k_cache, v_cache, seq_len: int, head_dim: int):
+    q, k, v = _f32(q), _f32(k_cache), _f32(v_cache)
+    out = np.zeros(head_dim, dtype=np.float32)
+    lib().or_attention_head(_p(out), _p(q), _p(k), _p(v), seq_len, head_dim)
+    return out
+
+
+# ---- src/model/mod.rs attention block -------------------------------------
+
+def attn_decode(q, key_cache, value_cache):
+    """q [Hq, D]; caches [T, Hkv, D] (already rotated); returns out [Hq, D]."""
+    q, kc, vc = _f32(q), _f32(key_cache), _f32(value_cache)
+    hq, dq = q.shape
+    t, hkv, dk = kc.shape
+    dv = vc.shape[2]
+    assert vc.shape[:2] == (t, hkv)
+    out = np.zeros((hq, dk), dtype=np.float32)
+    lib().or_attn_decode(_p(out), _p(q), dq, _p(kc), _p(vc), t, hq, hkv, dk, dv)
+    return out
+
+
+def apply_gate(out, gate):
+    out = np.array(out, dtype=np.float32, copy=True)
+    g = _f32(gate)
+    assert g.size >= out.size
+    lib().or_apply_gate(_p(out), _p(g), out.size)
+    return out
+
+
+def attn_layer_tokens(q, k, v, gate=None, q_norm_w=None, k_norm_w=None, eps=1e-6,
+                      rope_dim=None, rope_base=10000.0, freqs=None,
+                      key_cache=None, value_cache=None, prev_seq_len=0):
+    """Per-token attention block for n consecutive tokens of one sequence.
+
+    q [n, Hq, Dq], k [n, Hkv, Dk], v [n, Hkv, Dv] (raw, pre-norm/pre-RoPE),
+    optional previous caches [prev, Hkv, D].  Returns (out [n, Hq, Dk],
+    key_cache, value_cache) with the caches grown by n tokens.
+    """
+    q = np.array(q, dtype=np.float32, copy=True)
+    k = np.array(k, dtype=np.float32, copy=True)
+    v = _f32(v)
+    n, hq, dq = q.shape
+    _, hkv, dk = k.shape
+    dv = v.shape[2]
+    total = prev_seq_len + n
+    kc = np.zeros((total, hkv, dk), dtype=np.float32)
+    vc = np.zeros((total, hkv, dv), dtype=np.float32)
+    if prev_seq_len:
+        kc[:prev_seq_len] = key_cache[:prev_seq_len]
+        vc[:prev_seq_len] = value_cache[:prev_seq_len]
+    out = np.zeros((n, hq, dk), dtype=np.float32)
+    g = _f32(gate) if gate is not None else None
+    qn = _f32(q_norm_w) if q_norm_w is not None else None
+    kn = _f32(k_norm_w) if k_norm_w is not None else None
+    f = _f32(freqs) if freqs is not None else None
+    lib().or_attn_layer_tokens(_p(out), _p(q), _p(g), _p(k), _p(v), n, hq, hkv, dq, dk, dv,
+                               _p(qn), _p(kn), float(eps), rope_dim if rope_dim else dk,
+                               float(rope_base), _p(f), 0 if f is None else f.size,
+                               _p(kc), _p(vc), prev_seq_len)
+    return out, kc, vc
+
+
+def attn_prepare(q, k, n_heads, n_kv_heads, head_dim, q_norm_w=None, k_norm_w=None, eps=1e-6,
+                 rope_dim=None, rope_base=10000.0, freqs=None, pos0=0):
+    """Q/K norm + RoPE driver for n consecutive tokens (no attention); returns copies.
+
+    q [n, Hq, D] or None, k [n, Hkv, D] or None; token i at position pos0 + i."""
+    qq = None if q is None else np.array(q, dtype=np.float32, copy=True)
+    kk = None if k is None else np.array(k, dtype=np.float32, copy=True)
+    n = (qq if qq is not None else kk).shape[0]
+    qn = _f32(q_norm_w) if q_norm_w is not None else None
+    kn = _f32(k_norm_w) if k_norm_w is not None else None
+    f = _f32(freqs) if freqs is not None else None
+    lib().or_attn_prepare(_p(qq), _p(kk), n, n_heads, n_kv_heads, head_dim, head_dim, _p(qn),
+                          _p(kn), float(eps), rope_dim if rope_dim else head_dim,
+                          float(rope_base), _p(f), 0 if f is None else f.size, pos0)
+    return qq, kk
+
+
+# ---- src/model/mod.rs gated-DeltaNet block ---------------------------------
+
+def gdn_gates(beta_raw, a_raw, ssm_a, dt_bias):
+    br, ar, sa, db = (_f32(x) for x in (beta_raw, a_raw, ssm_a, dt_bias))
+    beta = np.empty_like(br)
+    g = np.empty_like(br)
+    lib().or_gdn_gates(_p(beta), _p(g), _p(br), _p(ar), _p(sa), _p(db), br.size)
+    return beta, g
+
+
+def gdn_tokens(q_raw, k_raw, v, beta, g, state=None):
+    """q_raw/k_raw [T, Hk, Dk], v [T, Hv, Dv], beta/g [T, Hv]; state [Hv, Dk, Dv].
+
+    Returns (out [T, Hv, Dv], final state)."""
+    q, k, vv, b, gg = (_f32(x) for x in (q_raw, k_raw, v, beta, g))
+    t, hk, dk = q.shape
+    _, hv, dv = vv.shape
+    assert k.shape == q.shape and b.shape == (t, hv) and gg.shape == (t, hv)
+    st = (np.zeros((hv, dk, dv), dtype=np.float32) if state is None
+          else np.array(state, dtype=np.float32, copy=True))
+    out = np.zeros((t, hv, dv), dtype=np.float32)
+    lib().or_gdn_tokens(_p(out), _p(st), _p(q), _p(k), _p(vv), _p(b), _p(gg), t, hk, hv, dk, dv)
+    return out, st
+
+
+def rmsnorm_gated(o, z, w, eps):
+    o = np.array(o, dtype=np.float32, copy=True)
+    zz, ww = _f32(z), _f32(w)
+    hv, dv = o.shape[-2], o.shape[-1]
+    rows = o.size // (hv * dv)
+    lib().or_rmsnorm_gated(_p(o), _p(zz), _p(ww), rows * hv, dv, float(eps))
+    return o
+
+
+def conv1d_silu(x, hist, w, d_conv):
+    """One token: returns (activation, new history)."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    h = np.array(hist, dtype=np.float32, copy=True)
+    ww = _f32(w)
+    lib().or_conv1d_silu(_p(x), _p(h), _p(ww), x.size, d_conv)
+    return x, h

@@ -1,0 +1,492 @@
+// api.cpp -- the C ABI (include/pi_attn.h): handles, the paged KV pool,
+// argument validation, error reporting and dispatch to the gfx950 kernels.
+//
+// Error behaviour mirrors the reference's offload seam: every failure is a
+// status code plus text (Some(Err(String)) in src/cuda/mod.rs:527-537), never
+// an exception or an abort across the ABI.
+#include "../../include/pi_attn.h"
+#include "pi_launch.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+struct pi_handle_s {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    pi::DecodeWorkspace dws{};
+    pi::GdnWorkspace gws{};
+    float* h2d_scratch = nullptr;  // device staging for the host-slice drop-ins
+    size_t h2d_floats = 0;
+};
+
+struct pi_kv_pool_s {
+    pi_handle owner;
+    pi::KvGeom g;
+    size_t bytes;
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+int fail(pi_handle h, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (h)
+        h->err = buf;
+    else
+        g_create_err = buf;
+    return code;
+}
+
+int hip_fail(pi_handle h, hipError_t e, const char* what) {
+    if (e == hipErrorOutOfMemory)
+        return fail(h, PI_ERR_OUT_OF_MEMORY, "%s: out of device memory", what);
+    if (e == hipErrorInvalidDeviceFunction || e == hipErrorNoBinaryForGpu)
+        return fail(h, PI_ERR_INVALID_KERNEL, "%s: no gfx950 kernel for this device (%s)", what,
+                    hipGetErrorString(e));
+    return fail(h, PI_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define PI_CHECK_HANDLE(h)                                                     \
+    do {                                                                       \
+        if (!(h)) return fail(nullptr, PI_ERR_INVALID_ARG, "null pi_handle");  \
+    } while (0)
+
+#define PI_HIP(h, call, what)                       \
+    do {                                            \
+        hipError_t e_ = (call);                     \
+        if (e_ != hipSuccess) return hip_fail(h, e_, what); \
+    } while (0)
+
+// NULL is HIP's default (null) stream, as for every HIP API; work is then
+// ordered with everything else the caller issues on that stream.
+hipStream_t pick(pi_handle, void* stream) { return reinterpret_cast<hipStream_t>(stream); }
+
+bool dim_ok(int d) { return d == 64 || d == 128 || d == 256; }
+
+// Grow-only device buffer (the reference grows its scratch lazily the same
+// way, src/cuda/mod.rs:257-278).  Freed buffers are released after the
+// stream drains so in-flight kernels never see freed memory.
+template <typename T>
+int grow(pi_handle h, T** ptr, size_t* cap, size_t need, hipStream_t s, const char* what,
+         bool zero) {
+    if (need <= *cap) return PI_OK;
+    size_t n = need + need / 4;
+    PI_HIP(h, hipStreamSynchronize(s), what);
+    if (*ptr) PI_HIP(h, hipFree(*ptr), what);
+    *ptr = nullptr;
+    *cap = 0;
+    PI_HIP(h, hipMalloc(reinterpret_cast<void**>(ptr), n * sizeof(T)), what);
+    if (zero) PI_HIP(h, hipMemset(*ptr, 0, n * sizeof(T)), what);
+    *cap = n;
+    return PI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pi_abi_version(void) { return PI_ATTN_ABI_VERSION; }
+
+int pi_create(int device, pi_handle* out) {
+    if (!out) return fail(nullptr, PI_ERR_INVALID_ARG, "pi_create: out is null");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+        return fail(nullptr, PI_ERR_DEVICE, "pi_create: no HIP device (%s)",
+                    e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+    if (device < 0 || device >= n)
+        return fail(nullptr, PI_ERR_INVALID_ARG, "pi_create: device %d of %d", device, n);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return fail(nullptr, PI_ERR_DEVICE, "pi_create: %s", hipGetErrorString(e));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, PI_ERR_UNSUPPORTED, "pi_create: device %d is %s; kernels are built for gfx950",
+                    device, prop.gcnArchName);
+    pi_handle h = new (std::nothrow) pi_handle_s();
+    if (!h) return fail(nullptr, PI_ERR_OUT_OF_MEMORY, "pi_create: host allocation");
+    h->device = device;
+    e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete h;
+        return fail(nullptr, PI_ERR_DEVICE, "pi_create: %s", hipGetErrorString(e));
+    }
+    *out = h;
+    return PI_OK;
+}
+
+void pi_destroy(pi_handle h) {
+    if (!h) return;
+    (void)hipSetDevice(h->device);
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    (void)hipFree(h->dws.partial_o);
+    (void)hipFree(h->dws.partial_ml);
+    (void)hipFree(h->dws.counters);
+    (void)hipFree(h->gws.buf);
+    (void)hipFree(h->h2d_scratch);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+const char* pi_last_error(pi_handle h) { return h ? h->err.c_str() : g_create_err.c_str(); }
+
+int pi_sync(pi_handle h, void* stream) {
+    PI_CHECK_HANDLE(h);
+    PI_HIP(h, hipSetDevice(h->device), "pi_sync");
+    PI_HIP(h, hipStreamSynchronize(pick(h, stream)), "pi_sync");
+    return PI_OK;
+}
+
+// ---- KV pool ---------------------------------------------------------------
+
+int pi_kv_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t n_kv_heads,
+                      int32_t head_dim, int32_t dtype, pi_kv_pool* out) {
+    PI_CHECK_HANDLE(h);
+    if (!out) return fail(h, PI_ERR_INVALID_ARG, "pi_kv_pool_create: out is null");
+    *out = nullptr;
+    if (page_tokens != pi::kPageTokens)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_kv_pool_create: page_tokens must be 16 (got %d)", page_tokens);
+    if (n_pages <= 0 || n_kv_heads <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_kv_pool_create: n_pages=%d n_kv_heads=%d", n_pages, n_kv_heads);
+    if (!dim_ok(head_dim))
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_kv_pool_create: head_dim %d (64/128/256)", head_dim);
+    if (dtype != PI_F32 && dtype != PI_F16)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_kv_pool_create: pool dtype %d (f32 or f16)", dtype);
+    if (dtype == PI_F32 && head_dim == 256)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_kv_pool_create: f32 pool with head_dim 256");
+    const int eb = dtype == PI_F32 ? 4 : 2;
+    const size_t bytes = (size_t)n_pages * n_kv_heads * pi::kPageTokens * head_dim * eb;
+    PI_HIP(h, hipSetDevice(h->device), "pi_kv_pool_create");
+    pi_kv_pool p = new (std::nothrow) pi_kv_pool_s();
+    if (!p) return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_kv_pool_create: host allocation");
+    p->owner = h;
+    p->bytes = 2 * bytes;
+    p->g = pi::KvGeom{nullptr, nullptr, n_pages, n_kv_heads, head_dim, dtype, eb};
+    hipError_t e = hipMalloc(&p->g.k, bytes);
+    if (e == hipSuccess) e = hipMalloc(&p->g.v, bytes);
+    // Zero once so slack slots of partially filled pages hold finite values.
+    if (e == hipSuccess) e = hipMemset(p->g.k, 0, bytes);
+    if (e == hipSuccess) e = hipMemset(p->g.v, 0, bytes);
+    if (e != hipSuccess) {
+        (void)hipFree(p->g.k);
+        (void)hipFree(p->g.v);
+        delete p;
+        return hip_fail(h, e, "pi_kv_pool_create");
+    }
+    *out = p;
+    return PI_OK;
+}
+
+void pi_kv_pool_destroy(pi_kv_pool pool) {
+    if (!pool) return;
+    (void)hipSetDevice(pool->owner->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(pool->g.k);
+    (void)hipFree(pool->g.v);
+    delete pool;
+}
+
+size_t pi_kv_pool_bytes(pi_kv_pool pool) { return pool ? pool->bytes : 0; }
+
+int pi_kv_append(pi_handle h, pi_kv_pool pool, const void* d_k, const void* d_v, int32_t src_dtype,
+                 const int32_t* d_page_table, int32_t max_pages, const int32_t* d_start_pos,
+                 int32_t n_seq, int32_t n_tok, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!pool || !d_k || !d_v || !d_page_table || !d_start_pos)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_kv_append: null argument");
+    if (n_seq < 0 || n_tok < 0 || max_pages <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_kv_append: n_seq=%d n_tok=%d max_pages=%d", n_seq, n_tok, max_pages);
+    if (src_dtype < PI_F32 || src_dtype > PI_BF16)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_kv_append: src dtype %d", src_dtype);
+    if (n_seq == 0 || n_tok == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_kv_append");
+    PI_HIP(h, pi::launch_kv_append(pool->g, d_k, d_v, src_dtype, d_page_table, max_pages,
+                                   d_start_pos, n_seq, n_tok, pick(h, stream)),
+           "pi_kv_append");
+    return PI_OK;
+}
+
+int pi_kv_read(pi_handle h, pi_kv_pool pool, const int32_t* d_page_table, int32_t max_pages,
+               int32_t seq, int32_t start, int32_t n_tok, float* d_k_out, float* d_v_out,
+               void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!pool || !d_page_table || !d_k_out || !d_v_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_kv_read: null argument");
+    if (seq < 0 || start < 0 || n_tok < 0 || max_pages <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_kv_read: seq=%d start=%d n_tok=%d", seq, start, n_tok);
+    if (n_tok == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_kv_read");
+    PI_HIP(h, pi::launch_kv_read(pool->g, d_page_table, max_pages, seq, start, n_tok, d_k_out,
+                                 d_v_out, pick(h, stream)),
+           "pi_kv_read");
+    return PI_OK;
+}
+
+// ---- prologue ----------------------------------------------------------------
+
+int pi_head_rmsnorm(pi_handle h, float* d_x, const float* d_w, int32_t n_rows, int32_t dim,
+                    int32_t row_stride, float eps, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_x || !d_w) return fail(h, PI_ERR_INVALID_ARG, "pi_head_rmsnorm: null argument");
+    if (n_rows < 0 || dim <= 0 || dim > 256 || row_stride < dim)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_head_rmsnorm: n_rows=%d dim=%d row_stride=%d", n_rows, dim, row_stride);
+    if (n_rows == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_head_rmsnorm");
+    PI_HIP(h, pi::launch_head_rmsnorm(d_x, d_w, n_rows, dim, row_stride, eps, pick(h, stream)),
+           "pi_head_rmsnorm");
+    return PI_OK;
+}
+
+int pi_rope(pi_handle h, float* d_q, float* d_k, const int32_t* d_pos, int32_t n_tok,
+            int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t rope_dim, float base,
+            const int32_t* h_sections, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_q || !d_pos) return fail(h, PI_ERR_INVALID_ARG, "pi_rope: null argument");
+    if (n_tok < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim > 256)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_rope: n_tok=%d heads=%d/%d head_dim=%d", n_tok, n_q_heads, n_kv_heads, head_dim);
+    // src/model/mod.rs:574-597,1074: rope dims are capped to the head dim.
+    int rd = rope_dim <= 0 ? head_dim : (rope_dim < head_dim ? rope_dim : head_dim);
+    const int n_pairs = rd / 2;
+    if (n_pairs > 128) return fail(h, PI_ERR_UNSUPPORTED, "pi_rope: rope_dim %d", rd);
+    if (n_tok == 0 || n_pairs == 0) return PI_OK;
+    pi::RopeFreqs f;
+    std::memset(&f, 0, sizeof f);
+    if (h_sections == nullptr) {
+        // ops::apply_rope (src/ops.rs:45-46): freq_i = 1 / base^(2i/rope_dim) in f32.
+        for (int i = 0; i < n_pairs; ++i) {
+            const float expo = 2.0f * (float)i / (float)rd;
+            f.f[i] = 1.0f / powf(base, expo);
+        }
+    } else {
+        // ops::compute_imrope_freqs (src/ops.rs:78-122): every track is
+        // theta_scale^k by repeated f32 multiplication; the first rd/2 are kept
+        // (src/model/mod.rs:1080-1083).
+        const float theta_scale = powf(base, -2.0f / (float)rd);
+        float t = 1.0f;
+        for (int i = 0; i < n_pairs; ++i) {
+            f.f[i] = t;
+            t *= theta_scale;
+        }
+    }
+    PI_HIP(h, hipSetDevice(h->device), "pi_rope");
+    PI_HIP(h, pi::launch_rope(d_q, d_k, d_pos, n_tok, n_q_heads, n_kv_heads, head_dim, n_pairs,
+                              h_sections ? 1 : 0, f, pick(h, stream)),
+           "pi_rope");
+    return PI_OK;
+}
+
+// ---- attention -------------------------------------------------------------------
+
+int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t* d_page_table,
+                   int32_t max_pages, const int32_t* d_ctx_len, int32_t batch, int32_t n_q_heads,
+                   int32_t gqa_mode, float scale, const float* d_gate, float* d_out,
+                   void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!pool || !d_q || !d_page_table || !d_ctx_len || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode: null argument");
+    const pi::KvGeom& g = pool->g;
+    if (batch < 0 || max_pages <= 0 || n_q_heads <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode: batch=%d max_pages=%d n_q_heads=%d", batch, max_pages, n_q_heads);
+    if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode: gqa_mode %d", gqa_mode);
+    if (n_q_heads % g.n_kv_heads != 0)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: n_q_heads %d not a multiple of n_kv_heads %d", n_q_heads, g.n_kv_heads);
+    const int group = n_q_heads / g.n_kv_heads;
+    if (group > 16 || group * g.head_dim > 2048)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: %d q heads per kv head at head_dim %d", group, g.head_dim);
+    if (batch == 0) return PI_OK;
+    hipStream_t s = pick(h, stream);
+    PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode");
+    int32_t pps = 0, n_splits = 0;
+    pi::decode_plan(g, batch, max_pages, &pps, &n_splits);
+    const size_t need_o = pi::decode_ws_floats_o(g, batch, n_q_heads, n_splits);
+    const size_t need_ml = need_o / g.head_dim * 2;
+    const size_t need_c = (size_t)batch * g.n_kv_heads;
+    int rc;
+    if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_attn_decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_attn_decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->dws.counters, &h->dws.capacity_cnt, need_c, s, "pi_attn_decode workspace", true))) return rc;
+    pi::DecodeParams p;
+    p.q = d_q;
+    p.page_table = d_page_table;
+    p.ctx_len = d_ctx_len;
+    p.gate = d_gate;
+    p.out = d_out;
+    p.max_pages = max_pages;
+    p.batch = batch;
+    p.n_q_heads = n_q_heads;
+    p.gqa_mode = gqa_mode;
+    p.scale = scale;
+    PI_HIP(h, pi::launch_decode(g, p, h->dws, pps, n_splits, s), "pi_attn_decode");
+    return PI_OK;
+}
+
+int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d_v, int32_t dtype,
+                    int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
+                    int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale, float* d_out,
+                    void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_q || !d_k || !d_v || !d_out) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill: null argument");
+    if (batch < 0 || seq_len < 0 || n_q_heads <= 0 || n_kv_heads <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill: batch=%d seq_len=%d heads=%d/%d", batch, seq_len, n_q_heads, n_kv_heads);
+    if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill: gqa_mode %d", gqa_mode);
+    if (dtype != PI_BF16 && dtype != PI_F16)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: dtype %d (bf16 or f16)", dtype);
+    if (head_dim != 128) return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: head_dim %d (128)", head_dim);
+    if (n_q_heads % n_kv_heads != 0)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: n_q_heads %d not a multiple of n_kv_heads %d", n_q_heads, n_kv_heads);
+    if (batch == 0 || seq_len == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_attn_prefill");
+    PI_HIP(h, pi::launch_prefill(d_q, d_k, d_v, dtype, batch, seq_len, n_q_heads, n_kv_heads,
+                                 head_dim, causal ? 1 : 0, gqa_mode, scale, d_out, pick(h, stream)),
+           "pi_attn_prefill");
+    return PI_OK;
+}
+
+// ---- gated DeltaNet ------------------------------------------------------------------
+
+int pi_gdn_gates(pi_handle h, const float* d_beta_raw, const float* d_a_raw, const float* d_ssm_a,
+                 const float* d_dt_bias, float* d_beta, float* d_g, int32_t n_tok,
+                 int32_t n_v_heads, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_beta_raw || !d_a_raw || !d_ssm_a || !d_dt_bias || !d_beta || !d_g)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_gates: null argument");
+    if (n_tok < 0 || n_v_heads <= 0) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_gates: n_tok=%d n_v_heads=%d", n_tok, n_v_heads);
+    if (n_tok == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_gdn_gates");
+    PI_HIP(h, pi::launch_gdn_gates(d_beta_raw, d_a_raw, d_ssm_a, d_dt_bias, d_beta, d_g, n_tok,
+                                   n_v_heads, pick(h, stream)),
+           "pi_gdn_gates");
+    return PI_OK;
+}
+
+static int gdn_shape_check(pi_handle h, const char* fn, int32_t n_k_heads, int32_t n_v_heads,
+                           int32_t k_hd, int32_t v_hd) {
+    if (n_k_heads <= 0 || n_v_heads <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "%s: n_k_heads=%d n_v_heads=%d", fn, n_k_heads, n_v_heads);
+    if (k_hd != 128 || v_hd != 128)
+        return fail(h, PI_ERR_UNSUPPORTED, "%s: k_hd=%d v_hd=%d (128)", fn, k_hd, v_hd);
+    return PI_OK;
+}
+
+int pi_gdn_decode(pi_handle h, const float* d_q, const float* d_k, const float* d_v,
+                  const float* d_beta, const float* d_g, float* d_state, float* d_out,
+                  int32_t batch, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd, int32_t v_hd,
+                  void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_q || !d_k || !d_v || !d_beta || !d_g || !d_state || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_decode: null argument");
+    if (batch < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_decode: batch=%d", batch);
+    int rc = gdn_shape_check(h, "pi_gdn_decode", n_k_heads, n_v_heads, k_hd, v_hd);
+    if (rc) return rc;
+    if (batch == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_gdn_decode");
+    PI_HIP(h, pi::launch_gdn_decode(d_q, d_k, d_v, d_beta, d_g, d_state, d_out, batch, n_k_heads,
+                                    n_v_heads, pick(h, stream)),
+           "pi_gdn_decode");
+    return PI_OK;
+}
+
+int pi_gdn_prefill(pi_handle h, const float* d_q, const float* d_k, const float* d_v,
+                   const float* d_beta, const float* d_g, float* d_state, float* d_out,
+                   int32_t n_tok, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd, int32_t v_hd,
+                   int32_t chunk, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_q || !d_k || !d_v || !d_beta || !d_g || !d_state || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_prefill: null argument");
+    if (n_tok < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_prefill: n_tok=%d", n_tok);
+    int rc = gdn_shape_check(h, "pi_gdn_prefill", n_k_heads, n_v_heads, k_hd, v_hd);
+    if (rc) return rc;
+    if (chunk != 64) return fail(h, PI_ERR_UNSUPPORTED, "pi_gdn_prefill: chunk %d (64)", chunk);
+    if (n_tok == 0) return PI_OK;
+    hipStream_t s = pick(h, stream);
+    PI_HIP(h, hipSetDevice(h->device), "pi_gdn_prefill");
+    const size_t need = pi::gdn_prefill_ws_floats(n_tok, n_v_heads, chunk);
+    if (need) {
+        rc = grow(h, &h->gws.buf, &h->gws.capacity, need, s, "pi_gdn_prefill workspace", false);
+        if (rc) return rc;
+    }
+    hipError_t e = pi::launch_gdn_prefill(d_q, d_k, d_v, d_beta, d_g, d_state, d_out, n_tok,
+                                          n_k_heads, n_v_heads, chunk, h->gws, s);
+    if (e == hipErrorNotSupported) return fail(h, PI_ERR_UNSUPPORTED, "pi_gdn_prefill: not built yet");
+    if (e != hipSuccess) return hip_fail(h, e, "pi_gdn_prefill");
+    return PI_OK;
+}
+
+// ---- host-slice drop-ins -------------------------------------------------------------
+
+int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const float* h_k_cache,
+                          const float* h_v_cache, size_t seq_len, size_t head_dim) {
+    PI_CHECK_HANDLE(h);
+    if (!h_out || !h_q || (seq_len && (!h_k_cache || !h_v_cache)))
+        return fail(h, PI_ERR_INVALID_ARG, "attention_head: null slice");
+    if (head_dim != 64 && head_dim != 128)
+        return fail(h, PI_ERR_UNSUPPORTED, "attention_head: head_dim %zu (64/128 on the device)", head_dim);
+    if (seq_len > (size_t)1 << 24) return fail(h, PI_ERR_UNSUPPORTED, "attention_head: seq_len %zu", seq_len);
+    PI_HIP(h, hipSetDevice(h->device), "attention_head");
+    hipStream_t s = h->stream;
+    // One f32 sequence, one head: a pool with ceil(seq_len/16) pages and the identity table.
+    const int n_pages = (int)((seq_len + 15) / 16) + 1;
+    pi_kv_pool pool = nullptr;
+    int rc = pi_kv_pool_create(h, n_pages, 16, 1, (int)head_dim, PI_F32, &pool);
+    if (rc) return rc;
+    const size_t kv = seq_len * head_dim;
+    const size_t need = 2 * kv + 2 * head_dim + (size_t)n_pages + 2;
+    rc = grow(h, &h->h2d_scratch, &h->h2d_floats, need, s, "attention_head staging", false);
+    if (rc) {
+        pi_kv_pool_destroy(pool);
+        return rc;
+    }
+    float* dk = h->h2d_scratch;
+    float* dv = dk + kv;
+    float* dq = dv + kv;
+    float* dout = dq + head_dim;
+    int32_t* dpt = reinterpret_cast<int32_t*>(dout + head_dim);
+    int32_t* dmeta = dpt + n_pages;  // [start_pos=0, ctx_len]
+    int32_t* hpt = new (std::nothrow) int32_t[n_pages + 2];
+    if (!hpt) {
+        pi_kv_pool_destroy(pool);
+        return fail(h, PI_ERR_OUT_OF_MEMORY, "attention_head: host allocation");
+    }
+    for (int i = 0; i < n_pages; ++i) hpt[i] = i;
+    hpt[n_pages] = 0;
+    hpt[n_pages + 1] = (int32_t)seq_len;
+    hipError_t e = hipSuccess;
+    if (kv) e = hipMemcpyAsync(dk, h_k_cache, kv * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && kv) e = hipMemcpyAsync(dv, h_v_cache, kv * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(dq, h_q, head_dim * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(dpt, hpt, (n_pages + 2) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    delete[] hpt;
+    if (e != hipSuccess) {
+        pi_kv_pool_destroy(pool);
+        return hip_fail(h, e, "attention_head");
+    }
+    rc = seq_len ? pi_kv_append(h, pool, dk, dv, PI_F32, dpt, n_pages, dmeta, 1, (int)seq_len, s) : PI_OK;
+    if (!rc)
+        rc = pi_attn_decode(h, dq, pool, dpt, n_pages, dmeta + 1, 1, 1, PI_GQA_MODULO,
+                            1.0f / std::sqrt((float)head_dim), nullptr, dout, s);
+    if (!rc) {
+        e = hipMemcpyAsync(h_out, dout, head_dim * 4, hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = hip_fail(h, e, "attention_head");
+    }
+    pi_kv_pool_destroy(pool);
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// pi_launch.hpp -- host-side launchers implemented in the .hip files and
+// called by the C ABI layer (api.cpp).  Arguments are validated by the
+// caller; launchers only check what the kernels themselves assume.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pi {
+
+constexpr int kPageTokens = 16;  // tokens per KV page
+
+// KV pool geometry: one K and one V block of kPageTokens x head_dim elements
+// per (page, kv head).  K block layout: [head_dim/E][16 tokens][E] with
+// E = 16 bytes / element size (16-byte chunks, chunk-major), V block layout:
+// [head_dim][16 tokens] (dim-major).  Both match the MFMA operand order the
+// decode kernel loads with one linear 16-byte (K) or 8/16-byte (V) access
+// per lane.
+struct KvGeom {
+    void* k;            // device base of K blocks
+    void* v;            // device base of V blocks
+    int32_t n_pages;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t dtype;      // PI_F32 / PI_F16
+    int32_t elem_bytes;
+};
+
+struct DecodeWorkspace {
+    float* partial_o;     // [batch][n_kv][n_splits][G][D]
+    float* partial_ml;    // [batch][n_kv][n_splits][G][2]  (running max, sum) in log2 units
+    uint32_t* counters;   // [batch][n_kv], zero between launches
+    size_t capacity_o;    // floats
+    size_t capacity_ml;   // floats
+    size_t capacity_cnt;  // counters
+};
+
+struct DecodeParams {
+    const float* q;
+    const int32_t* page_table;
+    const int32_t* ctx_len;
+    const float* gate;
+    float* out;
+    int32_t max_pages;
+    int32_t batch;
+    int32_t n_q_heads;
+    int32_t gqa_mode;
+    float scale;
+};
+
+// Chooses pages-per-split and the split count for a decode launch.
+void decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t* pages_per_split,
+                 int32_t* n_splits);
+size_t decode_ws_floats_o(const KvGeom& g, int32_t batch, int32_t n_q_heads, int32_t n_splits);
+hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,
+                         int32_t pages_per_split, int32_t n_splits, hipStream_t s);
+
+hipError_t launch_kv_append(const KvGeom& g, const void* k, const void* v, int32_t src_dtype,
+                            const int32_t* page_table, int32_t max_pages,
+                            const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
+                            hipStream_t s);
+hipError_t launch_kv_read(const KvGeom& g, const int32_t* page_table, int32_t max_pages,
+                          int32_t seq, int32_t start, int32_t n_tok, float* k_out, float* v_out,
+                          hipStream_t s);
+
+struct RopeFreqs {
+    float f[128];  // up to head_dim 256 -> 128 pairs
+};
+hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, int32_t n_q_heads,
+                       int32_t n_kv_heads, int32_t head_dim, int32_t n_pairs, int32_t neox,
+                       const RopeFreqs& freqs, hipStream_t s);
+hipError_t launch_head_rmsnorm(float* x, const float* w, int32_t n_rows, int32_t dim,
+                               int32_t row_stride, float eps, hipStream_t s);
+
+hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
+                          int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
+                          int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale,
+                          float* out, hipStream_t s);
+
+hipError_t launch_gdn_gates(const float* beta_raw, const float* a_raw, const float* ssm_a,
+                            const float* dt_bias, float* beta, float* g, int32_t n_tok,
+                            int32_t n_v_heads, hipStream_t s);
+hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, const float* beta,
+                             const float* g, float* state, float* out, int32_t batch,
+                             int32_t n_k_heads, int32_t n_v_heads, hipStream_t s);
+
+struct GdnWorkspace {
+    float* buf;
+    size_t capacity;  // floats
+};
+size_t gdn_prefill_ws_floats(int32_t n_tok, int32_t n_v_heads, int32_t chunk);
+hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, const float* beta,
+                              const float* g, float* state, float* out, int32_t n_tok,
+                              int32_t n_k_heads, int32_t n_v_heads, int32_t chunk,
+                              const GdnWorkspace& ws, hipStream_t s);
+
+}  // namespace pi

@@ -1,0 +1,200 @@
+// prologue.hip -- the steps in front of attention: paged KV append/read,
+// rotary embedding and per-head RMSNorm (gfx950).
+//
+//   kv_append   : LayerCache append (src/model/mod.rs:1140-1146) into the paged pool
+//   kv_read     : pool -> reference layout [T][n_kv][D] f32
+//   rope        : ops::apply_rope / apply_rope_with_freqs (src/ops.rs:35-67,130-157)
+//                 as driven by src/model/mod.rs:1072-1138
+//   head_rmsnorm: ops::rms_norm per head (src/ops.rs:13-27; src/model/mod.rs:1035-1070)
+#include "pi_device.hpp"
+#include "pi_launch.hpp"
+
+namespace pi {
+namespace {
+
+template <typename PT>
+__device__ __forceinline__ size_t k_index(int tok, int d) {
+    constexpr int E = 16 / (int)sizeof(PT);
+    return ((size_t)(d / E) * kPageTokens + tok) * E + (d % E);
+}
+__device__ __forceinline__ size_t v_index(int tok, int d) { return (size_t)d * kPageTokens + tok; }
+
+template <typename ST, typename PT>
+__global__ __launch_bounds__(256) void kv_append_kernel(KvGeom g, const ST* __restrict__ k,
+                                                        const ST* __restrict__ v,
+                                                        const int32_t* __restrict__ pt,
+                                                        int max_pages,
+                                                        const int32_t* __restrict__ start_pos,
+                                                        int n_seq, int n_tok) {
+    const int D = g.head_dim, H = g.n_kv_heads;
+    const size_t total = (size_t)n_seq * n_tok * H * D;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int d = (int)(idx % D);
+        const int h = (int)((idx / D) % H);
+        const int t = (int)((idx / ((size_t)D * H)) % n_tok);
+        const int s = (int)(idx / ((size_t)D * H * n_tok));
+        const int pos = start_pos[s] + t;
+        const int lp = pos / kPageTokens;
+        if (pos < 0 || lp >= max_pages) continue;  // outside the sequence's table: dropped
+        const int page = pt[(size_t)s * max_pages + lp];
+        if (page < 0 || page >= g.n_pages) continue;
+        const int tok = pos % kPageTokens;
+        const size_t blk = ((size_t)page * H + h) * kPageTokens * D;
+        PT* kp = reinterpret_cast<PT*>(g.k) + blk;
+        PT* vp = reinterpret_cast<PT*>(g.v) + blk;
+        kp[k_index<PT>(tok, d)] = from_f32<PT>(to_f32(k[idx]));
+        vp[v_index(tok, d)] = from_f32<PT>(to_f32(v[idx]));
+    }
+}
+
+template <typename PT>
+__global__ __launch_bounds__(256) void kv_read_kernel(KvGeom g, const int32_t* __restrict__ pt,
+                                                      int max_pages, int seq, int start,
+                                                      int n_tok, float* __restrict__ ko,
+                                                      float* __restrict__ vo) {
+    const int D = g.head_dim, H = g.n_kv_heads;
+    const size_t total = (size_t)n_tok * H * D;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int d = (int)(idx % D);
+        const int h = (int)((idx / D) % H);
+        const int t = (int)(idx / ((size_t)D * H));
+        const int pos = start + t;
+        const int lp = pos / kPageTokens;
+        float kv = 0.f, vv = 0.f;
+        if (pos >= 0 && lp < max_pages) {
+            const int page = pt[(size_t)seq * max_pages + lp];
+            if (page >= 0 && page < g.n_pages) {
+                const int tok = pos % kPageTokens;
+                const size_t blk = ((size_t)page * H + h) * kPageTokens * D;
+                kv = to_f32(reinterpret_cast<const PT*>(g.k)[blk + k_index<PT>(tok, d)]);
+                vv = to_f32(reinterpret_cast<const PT*>(g.v)[blk + v_index(tok, d)]);
+            }
+        }
+        ko[idx] = kv;
+        vo[idx] = vv;
+    }
+}
+
+// One thread per (token, head, rotated pair).  theta = (f32)position * freq,
+// freq from the host-built table (the reference's own f32 formula), so only
+// cos/sin are evaluated on the device.
+__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ q, float* __restrict__ k,
+                                                   const int32_t* __restrict__ pos, int n_tok,
+                                                   int hq, int hkv, int D, int n_pairs, int neox,
+                                                   RopeFreqs f) {
+    const int heads = hq + (k ? hkv : 0);
+    const size_t total = (size_t)n_tok * heads * n_pairs;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int i = (int)(idx % n_pairs);
+        const int hh = (int)((idx / n_pairs) % heads);
+        const int t = (int)(idx / ((size_t)n_pairs * heads));
+        float* x = hh < hq ? q + ((size_t)t * hq + hh) * D : k + ((size_t)t * hkv + (hh - hq)) * D;
+        const int a = neox ? i : 2 * i;
+        const int b = neox ? i + n_pairs : 2 * i + 1;
+        if (b >= D) continue;
+        const float theta = (float)pos[t] * f.f[i];
+        const float c = cosf(theta), s = sinf(theta);
+        const float x0 = x[a], x1 = x[b];
+        x[a] = x0 * c - x1 * s;
+        x[b] = x0 * s + x1 * c;
+    }
+}
+
+// One wavefront per row; dim <= 256.
+__global__ __launch_bounds__(256) void head_rmsnorm_kernel(float* __restrict__ x,
+                                                           const float* __restrict__ w,
+                                                           int n_rows, int dim, int row_stride,
+                                                           float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n_rows) return;
+    float* xr = x + (size_t)row * row_stride;
+    float v[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = lane + 64 * i;
+        v[i] = d < dim ? xr[d] : 0.f;
+        ss += v[i] * v[i];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
+    const float rms = sqrtf(ss / (float)dim + eps);
+    const float inv = 1.0f / rms;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = lane + 64 * i;
+        if (d < dim) xr[d] = (v[i] * inv) * w[d];
+    }
+}
+
+int grid_for(size_t total) {
+    size_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks == 0) blocks = 1;
+    return (int)blocks;
+}
+
+template <typename ST>
+hipError_t append_src(const KvGeom& g, const void* k, const void* v, const int32_t* pt,
+                      int32_t max_pages, const int32_t* sp, int32_t n_seq, int32_t n_tok,
+                      hipStream_t s) {
+    const size_t total = (size_t)n_seq * n_tok * g.n_kv_heads * g.head_dim;
+    const ST* ks = reinterpret_cast<const ST*>(k);
+    const ST* vs = reinterpret_cast<const ST*>(v);
+    if (g.dtype == 1)
+        hipLaunchKernelGGL((kv_append_kernel<ST, f16>), dim3(grid_for(total)), dim3(256), 0, s, g,
+                           ks, vs, pt, max_pages, sp, n_seq, n_tok);
+    else
+        hipLaunchKernelGGL((kv_append_kernel<ST, float>), dim3(grid_for(total)), dim3(256), 0, s,
+                           g, ks, vs, pt, max_pages, sp, n_seq, n_tok);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_kv_append(const KvGeom& g, const void* k, const void* v, int32_t src_dtype,
+                            const int32_t* page_table, int32_t max_pages,
+                            const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
+                            hipStream_t s) {
+    switch (src_dtype) {
+        case 0: return append_src<float>(g, k, v, page_table, max_pages, start_pos, n_seq, n_tok, s);
+        case 1: return append_src<f16>(g, k, v, page_table, max_pages, start_pos, n_seq, n_tok, s);
+        case 2: return append_src<bf16>(g, k, v, page_table, max_pages, start_pos, n_seq, n_tok, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_kv_read(const KvGeom& g, const int32_t* page_table, int32_t max_pages,
+                          int32_t seq, int32_t start, int32_t n_tok, float* k_out, float* v_out,
+                          hipStream_t s) {
+    const size_t total = (size_t)n_tok * g.n_kv_heads * g.head_dim;
+    if (g.dtype == 1)
+        hipLaunchKernelGGL((kv_read_kernel<f16>), dim3(grid_for(total)), dim3(256), 0, s, g,
+                           page_table, max_pages, seq, start, n_tok, k_out, v_out);
+    else
+        hipLaunchKernelGGL((kv_read_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, g,
+                           page_table, max_pages, seq, start, n_tok, k_out, v_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, int32_t n_q_heads,
+                       int32_t n_kv_heads, int32_t head_dim, int32_t n_pairs, int32_t neox,
+                       const RopeFreqs& freqs, hipStream_t s) {
+    const size_t total = (size_t)n_tok * (n_q_heads + (k ? n_kv_heads : 0)) * n_pairs;
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(total)), dim3(256), 0, s, q, k, pos, n_tok,
+                       n_q_heads, n_kv_heads, head_dim, n_pairs, neox, freqs);
+    return hipGetLastError();
+}
+
+hipError_t launch_head_rmsnorm(float* x, const float* w, int32_t n_rows, int32_t dim,
+                               int32_t row_stride, float eps, hipStream_t s) {
+    hipLaunchKernelGGL(head_rmsnorm_kernel, dim3((n_rows + 3) / 4), dim3(256), 0, s, x, w, n_rows,
+                       dim, row_stride, eps);
+    return hipGetLastError();
+}
+
+}  // namespace pi

@@ -1,0 +1,306 @@
+"""torch-tensor front end of libpi_attn.so (include/pi_attn.h).
+
+torch provides device memory and the stream; every computation runs in the
+library's HIP kernels.  Calls are issued on torch's current stream so they
+order with surrounding torch work.  Errors raise PiError subclasses that
+mirror the reference's BackendError (src/runtime/mod.rs:6-18).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _abi
+
+F32, F16, BF16 = 0, 1, 2
+MODULO, GROUPED = 0, 1
+PAGE_TOKENS = 16
+
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+
+class PiError(RuntimeError):
+    code = -1
+
+
+class InvalidArg(PiError):
+    code = 1
+
+
+class OutOfMemory(PiError):
+    code = 2
+
+
+class InvalidKernel(PiError):
+    code = 3
+
+
+class DeviceError(PiError):
+    code = 4
+
+
+class Unsupported(PiError):
+    code = 5
+
+
+_ERRORS = {c.code: c for c in (InvalidArg, OutOfMemory, InvalidKernel, DeviceError, Unsupported)}
+
+
+def _vp(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _need(t: torch.Tensor, name: str, dtype=None, shape=None, dev=None):
+    if not isinstance(t, torch.Tensor):
+        raise InvalidArg(f"{name}: expected a torch.Tensor")
+    if dev is not None and t.device != dev:
+        raise InvalidArg(f"{name}: on {t.device}, expected {dev}")
+    if dtype is not None and t.dtype != dtype:
+        raise InvalidArg(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise InvalidArg(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if not t.is_contiguous():
+        raise InvalidArg(f"{name}: must be contiguous")
+
+
+class Device:
+    """One pi_handle bound to a GPU (GpuDevice / GpuResources, src/cuda/mod.rs:141-460)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _abi.load()
+        self.index = device
+        self.torch_device = torch.device("cuda", device)
+        h = ctypes.c_void_p()
+        rc = self.lib.pi_create(device, ctypes.byref(h))
+        if rc != 0:
+            raise _ERRORS.get(rc, PiError)(self.lib.pi_last_error(None).decode())
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.pi_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def stream(self):
+        return ctypes.c_void_p(torch.cuda.current_stream(self.torch_device).cuda_stream)
+
+    def check(self, rc: int):
+        if rc != 0:
+            raise _ERRORS.get(rc, PiError)(self.lib.pi_last_error(self.h).decode())
+
+    def sync(self):
+        self.check(self.lib.pi_sync(self.h, self.stream()))
+
+
+class KvPool:
+    """Paged KV cache in HBM: 16-token pages, one K and one V block per (page, kv head)."""
+
+    def __init__(self, dev: Device, n_pages: int, n_kv_heads: int, head_dim: int,
+                 dtype: torch.dtype = torch.float16, page_tokens: int = PAGE_TOKENS):
+        self.dev = dev
+        self.n_pages, self.n_kv_heads, self.head_dim = n_pages, n_kv_heads, head_dim
+        self.dtype = dtype
+        p = ctypes.c_void_p()
+        code = _DTYPE_CODE.get(dtype, -1)
+        dev.check(dev.lib.pi_kv_pool_create(dev.h, n_pages, page_tokens, n_kv_heads, head_dim,
+                                            code, ctypes.byref(p)))
+        self.p = p
+
+    @property
+    def nbytes(self) -> int:
+        return int(self.dev.lib.pi_kv_pool_bytes(self.p))
+
+    def close(self):
+        if self.p:
+            self.dev.lib.pi_kv_pool_destroy(self.p)
+            self.p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def append(self, k: torch.Tensor, v: torch.Tensor, page_table: torch.Tensor,
+               start_pos: torch.Tensor):
+        """k, v: [n_seq, n_tok, n_kv_heads, head_dim] (f32/f16/bf16)."""
+        d = self.dev
+        if k.dim() != 4 or k.shape[2:] != (self.n_kv_heads, self.head_dim):
+            raise InvalidArg(f"k: shape {tuple(k.shape)}")
+        for name, t in (("k", k), ("v", v)):
+            _need(t, name, dtype=k.dtype, shape=k.shape, dev=d.torch_device)
+        n_seq, n_tok = k.shape[:2]
+        _need(page_table, "page_table", torch.int32, dev=d.torch_device)
+        _need(start_pos, "start_pos", torch.int32, (n_seq,), d.torch_device)
+        if page_table.dim() != 2 or page_table.shape[0] < n_seq:
+            raise InvalidArg(f"page_table: shape {tuple(page_table.shape)}")
+        d.check(d.lib.pi_kv_append(d.h, self.p, _vp(k), _vp(v), _DTYPE_CODE.get(k.dtype, -1),
+                                   _vp(page_table), page_table.shape[1], _vp(start_pos), n_seq,
+                                   n_tok, d.stream()))
+
+    def read(self, page_table: torch.Tensor, seq: int, start: int, n_tok: int):
+        d = self.dev
+        _need(page_table, "page_table", torch.int32, dev=d.torch_device)
+        ko = torch.empty((n_tok, self.n_kv_heads, self.head_dim), dtype=torch.float32,
+                         device=d.torch_device)
+        vo = torch.empty_like(ko)
+        d.check(d.lib.pi_kv_read(d.h, self.p, _vp(page_table), page_table.shape[1], seq, start,
+                                 n_tok, _vp(ko), _vp(vo), d.stream()))
+        return ko, vo
+
+
+def head_rmsnorm(dev: Device, x: torch.Tensor, w: torch.Tensor, eps: float):
+    """In place: every row of the last dimension of x (f32) is RMS-normalised and scaled by w."""
+    _need(x, "x", torch.float32, dev=dev.torch_device)
+    dim = x.shape[-1]
+    _need(w, "w", torch.float32, (dim,), dev.torch_device)
+    dev.check(dev.lib.pi_head_rmsnorm(dev.h, _vp(x), _vp(w), x.numel() // dim, dim, dim,
+                                      float(eps), dev.stream()))
+    return x
+
+
+def rope(dev: Device, q: torch.Tensor, k: Optional[torch.Tensor], pos: torch.Tensor,
+         rope_dim: int, base: float, sections: Optional[Sequence[int]] = None):
+    """In place on q [n_tok, Hq, D] and k [n_tok, Hkv, D] (f32) at positions pos [n_tok]."""
+    _need(q, "q", torch.float32, dev=dev.torch_device)
+    n_tok, hq, dh = q.shape
+    hkv = 1
+    if k is not None:
+        _need(k, "k", torch.float32, dev=dev.torch_device)
+        if k.shape[0] != n_tok or k.shape[2] != dh:
+            raise InvalidArg(f"k: shape {tuple(k.shape)}")
+        hkv = k.shape[1]
+    _need(pos, "pos", torch.int32, (n_tok,), dev.torch_device)
+    sec = None
+    if sections is not None:
+        sec = (ctypes.c_int32 * 4)(*[int(s) for s in sections])
+    dev.check(dev.lib.pi_rope(dev.h, _vp(q), _vp(k), _vp(pos), n_tok, hq, hkv, dh, rope_dim,
+                              float(base), sec, dev.stream()))
+    return q, k
+
+
+def attn_decode(dev: Device, q: torch.Tensor, pool: KvPool, page_table: torch.Tensor,
+                ctx_len: torch.Tensor, gqa_mode: int = MODULO, scale: Optional[float] = None,
+                gate: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+    """q [B, Hq, D] f32 -> out [B, Hq, D] f32 over each sequence's ctx_len[b] cached tokens."""
+    _need(q, "q", torch.float32, dev=dev.torch_device)
+    b, hq, dh = q.shape
+    if dh != pool.head_dim:
+        raise InvalidArg(f"q head_dim {dh} != pool head_dim {pool.head_dim}")
+    _need(page_table, "page_table", torch.int32, dev=dev.torch_device)
+    if page_table.dim() != 2 or page_table.shape[0] != b:
+        raise InvalidArg(f"page_table: shape {tuple(page_table.shape)}")
+    _need(ctx_len, "ctx_len", torch.int32, (b,), dev.torch_device)
+    if gate is not None:
+        _need(gate, "gate", torch.float32, q.shape, dev.torch_device)
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, "out", torch.float32, q.shape, dev.torch_device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(dh)
+    dev.check(dev.lib.pi_attn_decode(dev.h, _vp(q), pool.p, _vp(page_table), page_table.shape[1],
+                                     _vp(ctx_len), b, hq, gqa_mode, float(scale), _vp(gate),
+                                     _vp(out), dev.stream()))
+    return out
+
+
+def attn_prefill(dev: Device, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                 causal: bool = True, gqa_mode: int = MODULO, scale: Optional[float] = None,
+                 out: Optional[torch.Tensor] = None):
+    """q [B, S, Hq, D], k/v [B, S, Hkv, D] (bf16/f16) -> out [B, S, Hq, D] f32."""
+    _need(q, "q", dev=dev.torch_device)
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise Unsupported(f"q: dtype {q.dtype} (bf16 or f16)")
+    bsz, s, hq, dh = q.shape
+    _need(k, "k", q.dtype, dev=dev.torch_device)
+    hkv = k.shape[2]
+    _need(k, "k", q.dtype, (bsz, s, hkv, dh), dev.torch_device)
+    _need(v, "v", q.dtype, (bsz, s, hkv, dh), dev.torch_device)
+    if out is None:
+        out = torch.empty((bsz, s, hq, dh), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32, (bsz, s, hq, dh), dev.torch_device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(dh)
+    dev.check(dev.lib.pi_attn_prefill(dev.h, _vp(q), _vp(k), _vp(v), _DTYPE_CODE[q.dtype], bsz,
+                                      s, hq, hkv, dh, 1 if causal else 0, gqa_mode, float(scale),
+                                      _vp(out), dev.stream()))
+    return out
+
+
+def gdn_gates(dev: Device, beta_raw, a_raw, ssm_a, dt_bias):
+    """beta_raw/a_raw [n_tok, Hv], ssm_a/dt_bias [Hv] (f32) -> (beta, g)."""
+    n_tok, hv = beta_raw.shape
+    for name, t, shp in (("beta_raw", beta_raw, (n_tok, hv)), ("a_raw", a_raw, (n_tok, hv)),
+                         ("ssm_a", ssm_a, (hv,)), ("dt_bias", dt_bias, (hv,))):
+        _need(t, name, torch.float32, shp, dev.torch_device)
+    beta = torch.empty_like(beta_raw)
+    g = torch.empty_like(beta_raw)
+    dev.check(dev.lib.pi_gdn_gates(dev.h, _vp(beta_raw), _vp(a_raw), _vp(ssm_a), _vp(dt_bias),
+                                   _vp(beta), _vp(g), n_tok, hv, dev.stream()))
+    return beta, g
+
+
+def _gdn_check(dev, q, k, v, beta, g, state, lead):
+    hk, dk = q.shape[-2:]
+    hv, dv = v.shape[-2:]
+    _need(q, "q", torch.float32, (lead, hk, dk), dev.torch_device)
+    _need(k, "k", torch.float32, (lead, hk, dk), dev.torch_device)
+    _need(v, "v", torch.float32, (lead, hv, dv), dev.torch_device)
+    _need(beta, "beta", torch.float32, (lead, hv), dev.torch_device)
+    _need(g, "g", torch.float32, (lead, hv), dev.torch_device)
+    return hk, hv, dk, dv
+
+
+def gdn_decode(dev: Device, q, k, v, beta, g, state, out=None):
+    """One step per sequence: q/k [B, Hk, Dk] raw, v [B, Hv, Dv], beta/g [B, Hv],
+    state [B, Hv, Dk, Dv] (in/out)."""
+    b = q.shape[0]
+    hk, hv, dk, dv = _gdn_check(dev, q, k, v, beta, g, state, b)
+    _need(state, "state", torch.float32, (b, hv, dk, dv), dev.torch_device)
+    if out is None:
+        out = torch.empty((b, hv, dv), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32, (b, hv, dv), dev.torch_device)
+    dev.check(dev.lib.pi_gdn_decode(dev.h, _vp(q), _vp(k), _vp(v), _vp(beta), _vp(g), _vp(state),
+                                    _vp(out), b, hk, hv, dk, dv, dev.stream()))
+    return out
+
+
+def gdn_prefill(dev: Device, q, k, v, beta, g, state, out=None, chunk: int = 64):
+    """n_tok tokens of one sequence: q/k [T, Hk, Dk], v [T, Hv, Dv], beta/g [T, Hv],
+    state [Hv, Dk, Dv] (in/out)."""
+    t = q.shape[0]
+    hk, hv, dk, dv = _gdn_check(dev, q, k, v, beta, g, state, t)
+    _need(state, "state", torch.float32, (hv, dk, dv), dev.torch_device)
+    if out is None:
+        out = torch.empty((t, hv, dv), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32, (t, hv, dv), dev.torch_device)
+    dev.check(dev.lib.pi_gdn_prefill(dev.h, _vp(q), _vp(k), _vp(v), _vp(beta), _vp(g),
+                                     _vp(state), _vp(out), t, hk, hv, dk, dv, chunk,
+                                     dev.stream()))
+    return out
+
+
+def attention_head(dev: Device, q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                   seq_len: int, head_dim: int) -> np.ndarray:
+    """ops::attention_head (src/ops.rs:213-247) on host slices, computed on the GPU."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k_cache, dtype=np.float32)
+    v = np.ascontiguousarray(v_cache, dtype=np.float32)
+    if q.size < head_dim or k.size < seq_len * head_dim or v.size < seq_len * head_dim:
+        raise InvalidArg("attention_head: slice shorter than seq_len * head_dim")
+    out = np.zeros(head_dim, dtype=np.float32)
+    fp = ctypes.POINTER(ctypes.c_float)
+    dev.check(dev.lib.pi_ops_attention_head(dev.h, out.ctypes.data_as(fp), q.ctypes.data_as(fp),
+                                            k.ctypes.data_as(fp), v.ctypes.data_as(fp), seq_len,
+                                            head_dim))
+    return out

@@ -1,0 +1,97 @@
+"""Causal prefill attention on the GPU vs the CPU oracle.
+
+The reference's prefill runs the decode attention once per prompt token with
+append-then-attend (src/model/mod.rs:668,1140-1190), so row i of the oracle
+is or_attn_decode over keys 0..i.  Inputs follow config 3: q/k/v drawn in f32,
+RoPE (theta 1e6, adjacent pairs) applied in f32 by the oracle on the host,
+then rounded to bf16 -- the kernel's input; the oracle reads the same bf16
+values upcast.  Tolerance: <= 1e-2 relative per row (bf16 class), exact
+argmax of synthetic logits.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests import ref64
+from tests.gpu_util import argmax_agreement, device, row_rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(rng, s, hq, hkv, d, theta=1e6, dtype=torch.bfloat16):
+    q = rng.standard_normal((s, hq, d)).astype(np.float32)
+    k = rng.standard_normal((s, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((s, hkv, d)).astype(np.float32)
+    qr, kr = orc.attn_prepare(q, k, hq, hkv, d, rope_base=theta, pos0=0)
+    tq = torch.from_numpy(qr).to(dtype)
+    tk = torch.from_numpy(kr).to(dtype)
+    tv = torch.from_numpy(v).to(dtype)
+    return tq, tk, tv
+
+
+def _oracle_rows(tq, tk, tv, rows):
+    qf, kf, vf = (t.float().numpy() for t in (tq, tk, tv))
+    return np.stack([orc.attn_decode(qf[i], kf[:i + 1], vf[:i + 1]) for i in rows])
+
+
+def _run(tq, tk, tv, causal=True, gqa_mode=0):
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    out = rt.attn_prefill(dev, tq[None].cuda(), tk[None].cuda(), tv[None].cuda(), causal=causal,
+                          gqa_mode=gqa_mode)
+    torch.cuda.synchronize()
+    return out[0].cpu().numpy()
+
+
+@pytest.mark.parametrize("s", [1, 31, 64, 200, 513])
+def test_prefill_small_all_rows(s):
+    rng = np.random.default_rng(100 + s)
+    tq, tk, tv = _inputs(rng, s, 32, 8, 128)
+    out = _run(tq, tk, tv)
+    ref = _oracle_rows(tq, tk, tv, range(s))
+    assert row_rel_err(out, ref) <= 1e-2
+    n, mism, ties = argmax_agreement(out, ref)
+    assert mism == 0
+
+
+def test_c3_qwen3_prefill_4096_sampled_rows():
+    """Config 3: S 4096, 32/8 heads, D 128, bf16, causal; rows sampled across the prompt."""
+    rng = np.random.default_rng(0x5EED0002)
+    tq, tk, tv = _inputs(rng, 4096, 32, 8, 128)
+    out = _run(tq, tk, tv)
+    rows = [0, 1, 2, 31, 32, 63, 64, 65, 127, 128, 1000, 2047, 2048, 3071, 4094, 4095]
+    rows += list(np.random.default_rng(5).integers(0, 4096, 16))
+    ref = _oracle_rows(tq, tk, tv, rows)
+    assert row_rel_err(out[rows], ref) <= 1e-2
+    n, mism, ties = argmax_agreement(out[rows], ref)
+    assert mism == 0
+    assert np.isfinite(out).all()
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 4), (4, 4), (12, 4), (16, 2)])
+def test_prefill_gqa_groupings(hq, hkv):
+    """Groups of 2, 1, 3 (128-row workgroups) and 8 (packed 4-head workgroups)."""
+    rng = np.random.default_rng(hq * 7 + hkv)
+    tq, tk, tv = _inputs(rng, 300, hq, hkv, 128)
+    out = _run(tq, tk, tv)
+    ref = _oracle_rows(tq, tk, tv, range(300))
+    assert row_rel_err(out, ref) <= 1e-2
+
+
+def test_prefill_f16_inputs():
+    rng = np.random.default_rng(21)
+    tq, tk, tv = _inputs(rng, 257, 32, 8, 128, dtype=torch.float16)
+    out = _run(tq, tk, tv)
+    ref = _oracle_rows(tq, tk, tv, range(257))
+    assert row_rel_err(out, ref) <= 1e-2
+
+
+def test_prefill_noncausal_and_grouped_vs_f64():
+    """Options outside the reference (no mask; grouped GQA) against float64 brute force."""
+    rng = np.random.default_rng(22)
+    tq, tk, tv = _inputs(rng, 160, 16, 4, 128)
+    qf, kf, vf = (t.float().numpy() for t in (tq, tk, tv))
+    out = _run(tq, tk, tv, causal=False, gqa_mode=1)
+    ref = np.stack([ref64.attention(qf[i], kf, vf, lambda h: h // 4) for i in range(160)])
+    assert row_rel_err(out, ref) <= 1e-2

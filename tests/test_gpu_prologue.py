@@ -1,0 +1,99 @@
+"""Decode prologue kernels vs the oracle: RoPE (src/ops.rs:35-157), per-head
+RMSNorm (src/ops.rs:13-27) and the paged KV append/read round trip
+(src/model/mod.rs:1140-1146)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.gpu_util import device, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _rt():
+    from powerinfer_x64_amd import runtime as rt
+    return rt
+
+
+@pytest.mark.parametrize("mode", ["norm", "imrope"])
+def test_rope_matches_oracle(mode):
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(1 if mode == "norm" else 2)
+    n, hq, hkv, d = 64, 8, 2, 256 if mode == "imrope" else 128
+    pos = np.concatenate([np.arange(32), rng.integers(0, 65536, 32)]).astype(np.int32)
+    q = rng.standard_normal((n, hq, d)).astype(np.float32)
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    if mode == "norm":
+        theta, rd, sec, freqs = 1e6, 128, None, None
+    else:
+        theta, rd, sec = 1e7, 64, [11, 11, 10, 0]
+        freqs = orc.compute_imrope_freqs(theta, rd, sec)
+    tq, tk = to_dev(q), to_dev(k)
+    rt.rope(dev, tq, tk, to_dev(pos), rd, theta, sec)
+    torch.cuda.synchronize()
+    gq, gk = tq.cpu().numpy(), tk.cpu().numpy()
+    for i in range(n):
+        eq, ek = orc.attn_prepare(q[i][None], k[i][None], hq, hkv, d, rope_dim=rd,
+                                  rope_base=theta, freqs=freqs, pos0=int(pos[i]))
+        # same f32 angle; cos/sin may differ by an ulp between the GPU and glibc
+        np.testing.assert_allclose(gq[i], eq[0], atol=2e-6, rtol=0)
+        np.testing.assert_allclose(gk[i], ek[0], atol=2e-6, rtol=0)
+
+
+def test_head_rmsnorm_matches_oracle():
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((50, 16, 256)).astype(np.float32) * 3
+    w = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    tx = to_dev(x)
+    rt.head_rmsnorm(dev, tx, to_dev(w), 1e-6)
+    torch.cuda.synchronize()
+    g = tx.cpu().numpy().reshape(-1, 256)
+    ref = np.stack([orc.rms_norm(r, w, 1e-6) for r in x.reshape(-1, 256)])
+    np.testing.assert_allclose(g, ref, rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("pool_dtype,src", [(torch.float32, torch.float32),
+                                            (torch.float16, torch.float32),
+                                            (torch.float16, torch.float16),
+                                            (torch.float16, torch.bfloat16)])
+def test_kv_append_read_roundtrip(pool_dtype, src):
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(4)
+    hkv, d = 4, 128
+    pool = rt.KvPool(dev, 40, hkv, d, dtype=pool_dtype)
+    pt = to_dev(rng.permutation(40)[:36].reshape(2, 18).astype(np.int32))
+    k = rng.standard_normal((2, 100, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((2, 100, hkv, d)).astype(np.float32)
+    tk, tv = to_dev(k, src), to_dev(v, src)
+    # prompt of 100 tokens, then 3 single-token appends (decode steps)
+    pool.append(tk[:, :97].contiguous(), tv[:, :97].contiguous(), pt,
+                to_dev(np.zeros(2, np.int32)))
+    for t in range(97, 100):
+        pool.append(tk[:, t:t + 1].contiguous(), tv[:, t:t + 1].contiguous(), pt,
+                    to_dev(np.full(2, t, np.int32)))
+    for s in range(2):
+        ko, vo = pool.read(pt, s, 0, 100)
+        torch.cuda.synchronize()
+        ek = tk[s].to(pool_dtype).float().cpu().numpy()
+        ev = tv[s].to(pool_dtype).float().cpu().numpy()
+        np.testing.assert_array_equal(ko.cpu().numpy(), ek)
+        np.testing.assert_array_equal(vo.cpu().numpy(), ev)
+
+
+def test_pool_rejects_bad_shapes():
+    rt = _rt()
+    dev = device()
+    with pytest.raises(rt.Unsupported):
+        rt.KvPool(dev, 4, 2, 96)
+    with pytest.raises(rt.Unsupported):
+        rt.KvPool(dev, 4, 2, 128, page_tokens=32)
+    pool = rt.KvPool(dev, 4, 3, 128)
+    q = torch.zeros((1, 4, 128), device="cuda")
+    with pytest.raises(rt.Unsupported):  # 4 q heads over 3 kv heads
+        rt.attn_decode(dev, q, pool, torch.zeros((1, 1), dtype=torch.int32, device="cuda"),
+                       torch.ones(1, dtype=torch.int32, device="cuda"))
