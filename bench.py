@@ -44,6 +44,9 @@ def _args():
     p.add_argument("--cpu-seconds", type=float, default=20.0,
                    help="budget of the single-core CPU baseline sample")
     p.add_argument("--only-headline", action="store_true")
+    p.add_argument("--workload", default=None,
+                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn"],
+                   help="time one workload only and print its figures (for sweeps)")
     return p.parse_args()
 
 
@@ -247,6 +250,27 @@ def _traffic(name):
     return None
 
 
+def _single(torch, rt, dev, timer, a):
+    w, st, wu = a.workload, a.steps, a.warmup
+    if w == "c2":
+        rng = np.random.default_rng(0x5EED0001)
+        lens = [int(x) for x in rng.integers(1024, 32769, size=32)]
+        return bench_decode(torch, rt, dev, timer, lens, 32, 8, 128, 1e6, 0x5EED0001, st, wu)[0]
+    if w == "c2_32k":
+        return bench_decode(torch, rt, dev, timer, [32768] * 32, 32, 8, 128, 1e6, 0x5EED0011, st,
+                            wu)[0]
+    if w == "c4":
+        return bench_decode(torch, rt, dev, timer, [65536] * 8, 16, 2, 256, 1e7, 0x5EED0003, st,
+                            wu, sections=[11, 11, 10, 0], rope_dim=64, qk_norm=True,
+                            gate=True)[0]
+    if w == "c1":
+        return bench_decode(torch, rt, dev, timer, [513], 32, 32, 128, 1e4, 0x5EED0000, st, wu,
+                            pool_dtype=torch.float32)[0]
+    if w == "c3":
+        return bench_prefill(torch, rt, dev, timer, 4096, 32, 8, 128, 1e6, 0x5EED0002, st, wu)
+    return bench_gdn_decode(torch, rt, dev, timer, st, wu)
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -258,6 +282,10 @@ def main():
 
     dev = rt.Device(0)
     timer = Timer(torch)
+    if a.workload:
+        print(json.dumps({"workload": a.workload, "pps_env": os.environ.get("PI_DECODE_PPS"),
+                          **_single(torch, rt, dev, timer, a)}), flush=True)
+        return
 
     # ---- headline: config 2 decode ----
     rng = np.random.default_rng(0x5EED0001)

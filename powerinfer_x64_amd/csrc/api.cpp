@@ -134,7 +134,6 @@ void pi_destroy(pi_handle h) {
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     (void)hipFree(h->dws.partial_o);
     (void)hipFree(h->dws.partial_ml);
-    (void)hipFree(h->dws.counters);
     (void)hipFree(h->gws.buf);
     (void)hipFree(h->h2d_scratch);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -307,18 +306,19 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
     const int group = n_q_heads / g.n_kv_heads;
     if (group > 16 || group * g.head_dim > 2048)
         return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: %d q heads per kv head at head_dim %d", group, g.head_dim);
+    if (batch > pi::kMaxBatch)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: batch %d > %d", batch, pi::kMaxBatch);
+    if ((long long)batch * g.n_kv_heads * ((max_pages + pi::kItemPages - 1) / pi::kItemPages) > (1LL << 30))
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: batch x kv heads x pages too large");
     if (batch == 0) return PI_OK;
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode");
-    int32_t pps = 0, n_splits = 0;
-    pi::decode_plan(g, batch, max_pages, &pps, &n_splits);
-    const size_t need_o = pi::decode_ws_floats_o(g, batch, n_q_heads, n_splits);
+    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
+    const size_t need_o = pi::decode_ws_floats_o(g, plan);
     const size_t need_ml = need_o / g.head_dim * 2;
-    const size_t need_c = (size_t)batch * g.n_kv_heads;
     int rc;
     if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_attn_decode workspace", false))) return rc;
     if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_attn_decode workspace", false))) return rc;
-    if ((rc = grow(h, &h->dws.counters, &h->dws.capacity_cnt, need_c, s, "pi_attn_decode workspace", true))) return rc;
     pi::DecodeParams p;
     p.q = d_q;
     p.page_table = d_page_table;
@@ -330,7 +330,7 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
     p.n_q_heads = n_q_heads;
     p.gqa_mode = gqa_mode;
     p.scale = scale;
-    PI_HIP(h, pi::launch_decode(g, p, h->dws, pps, n_splits, s), "pi_attn_decode");
+    PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), "pi_attn_decode");
     return PI_OK;
 }
 

@@ -5,17 +5,32 @@
 // over the sequence's cached keys, weighted sum of V, then the optional
 // sigmoid gate (:1192-1196).
 //
-// Work decomposition: one workgroup (4 wavefronts) per (sequence, KV head,
-// split of `pps` pages).  All query heads that share the KV head (up to 16)
-// ride in the N dimension of the MFMA tiles, so every K/V byte is read from
-// HBM exactly once.  Per 16-token page a wavefront computes
+// Work decomposition: a persistent grid of exactly as many workgroups (4
+// wavefronts each) as the GPU holds at once.  The launch's work is the list of
+// 16-page items of every (sequence, KV head) segment; each workgroup takes an
+// equal contiguous range of items, found from a prefix scan of the context
+// lengths, so ragged batches are balanced to within one item and no workgroup
+// is left idle.  All query heads that share the KV head (up to 16) ride in the
+// N dimension of the MFMA tiles, so every K/V byte is read from HBM once.
+// Per 16-token page a wavefront computes
 //   S^T[16 tok x 16 heads] = K[16 x D] . Q^T[D x 16]      (QK^T)
 //   O^T[D x 16]           += V^T[D x 16 tok] . P^T[16 x 16] (PV)
 // with f16 MFMA (f16 pool) or f32 MFMA (f32 pool); softmax statistics stay in
 // f32.  The page layouts (pi_launch.hpp) make each MFMA operand one linear
-// load per lane.  The 4 wavefronts interleave pages, merge their (max, sum, O)
-// in LDS, and the last workgroup of a (sequence, KV head) to finish merges the
-// splits from the workspace, so a decode step is a single launch.
+// load per lane.
+//
+// Memory pipeline: within a run the 4 wavefronts interleave pages; a
+// wavefront's page ids sit in one VGPR (lane j = j-th page) and are read with
+// readlane, so no scalar load sits between two pages.  NP pages are processed
+// per iteration while the next NP pages are in flight; the last iteration is
+// peeled so the in-loop wait count is exact.  The running softmax max is
+// raised lazily: it only moves when a score exceeds it by 2^8, so most pages
+// skip the rescale of the accumulators.
+//
+// The 4 wavefronts merge (max, sum, O) in LDS.  A run that covers its whole
+// segment writes the output; otherwise it writes a partial and
+// decode_merge_kernel (same stream, next launch) combines the runs -- no
+// cross-workgroup synchronisation inside a kernel.
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -27,7 +42,9 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kMaxGD = 2048;  // G * D limit of the LDS merge buffer
+constexpr int kMaxGD = 2048;            // G * D limit of the LDS merge buffer
+constexpr float kLazyThreshold = 8.0f;  // log2 headroom before the running max moves
+constexpr int kMaxRuns = 1024;          // runs of one segment the merge kernel stages
 
 template <typename KT, int D>
 struct Tile;
@@ -52,13 +69,18 @@ struct Tile<f16, D> {
         for (int t = 0; t < NV; ++t)
             v[t] = *reinterpret_cast<const f16x4*>(vb + (16 * t + col) * 16 + 4 * grp);
     }
-    static __device__ __forceinline__ void load_q(Q& q, const float* qrow, float qs, bool on,
-                                                  int grp) {
+    // qrow is always a valid row; `qs` is 0 for padding columns.
+    static __device__ __forceinline__ void load_q(Q& q, const float* qrow, float qs, int grp) {
 #pragma unroll
-        for (int j = 0; j < NK; ++j)
+        for (int j = 0; j < NK; ++j) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(qrow + 32 * j + 8 * grp);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(qrow + 32 * j + 8 * grp + 4);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                q.r[j][i] = on ? to_f16(qrow[32 * j + 8 * grp + i] * qs) : (f16)0.0f;
+            for (int i = 0; i < 4; ++i) {
+                q.r[j][i] = to_f16(a[i] * qs);
+                q.r[j][4 + i] = to_f16(b[i] * qs);
+            }
+        }
     }
     __device__ __forceinline__ f32x4 scores(const Q& q) const {
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
@@ -66,13 +88,13 @@ struct Tile<f16, D> {
         for (int j = 0; j < NK; ++j) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[j], q.r[j], s, 0, 0, 0);
         return s;
     }
-    __device__ __forceinline__ void mask_v(int valid_from_grp) {
-        // zero V rows of tokens >= valid (their weight is 0, but pool slack may hold NaN)
+    __device__ __forceinline__ void mask_v(int valid) {
+        // zero V of tokens >= valid (their weight is 0, but slack slots may hold NaN)
 #pragma unroll
         for (int t = 0; t < NV; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (i >= valid_from_grp) v[t][i] = (f16)0.0f;
+                if (i >= valid) v[t][i] = (f16)0.0f;
     }
     __device__ __forceinline__ void pv(f32x4* o, const float p[4]) const {
         f16x4 pb = {to_f16(p[0]), to_f16(p[1]), to_f16(p[2]), to_f16(p[3])};
@@ -101,12 +123,13 @@ struct Tile<float, D> {
         for (int t = 0; t < NV; ++t)
             v[t] = *reinterpret_cast<const f32x4*>(vb + (16 * t + col) * 16 + 4 * grp);
     }
-    static __device__ __forceinline__ void load_q(Q& q, const float* qrow, float qs, bool on,
-                                                  int grp) {
+    static __device__ __forceinline__ void load_q(Q& q, const float* qrow, float qs, int grp) {
 #pragma unroll
-        for (int j = 0; j < NK; ++j)
+        for (int j = 0; j < NK; ++j) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(qrow + 16 * j + 4 * grp);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) q.r[4 * j + e] = on ? qrow[16 * j + 4 * grp + e] * qs : 0.f;
+            for (int e = 0; e < 4; ++e) q.r[4 * j + e] = a[e] * qs;
+        }
     }
     __device__ __forceinline__ f32x4 scores(const Q& q) const {
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
@@ -117,12 +140,12 @@ struct Tile<float, D> {
                 s = __builtin_amdgcn_mfma_f32_16x16x4f32(k[j][e], q.r[4 * j + e], s, 0, 0, 0);
         return s;
     }
-    __device__ __forceinline__ void mask_v(int valid_from_grp) {
+    __device__ __forceinline__ void mask_v(int valid) {
 #pragma unroll
         for (int t = 0; t < NV; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (i >= valid_from_grp) v[t][i] = 0.f;
+                if (i >= valid) v[t][i] = 0.f;
     }
     __device__ __forceinline__ void pv(f32x4* o, const float p[4]) const {
 #pragma unroll
@@ -138,225 +161,390 @@ __device__ __forceinline__ int head_of(int kvh, int col, int n_kv, int group, in
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-template <typename KT, int D>
+// Work items of a sequence: ceil(pages / kItemPages) (0 for an empty context).
+__device__ __forceinline__ int items_of(int len) {
+    const int pages = (max(len, 0) + kPageTokens - 1) / kPageTokens;
+    return (pages + kItemPages - 1) / kItemPages;
+}
+
+// Softmax/PV state of one wavefront: O^T accumulators (lane = head column
+// `col`, dims 16t + 4*grp + r), the lazily raised running max, and the
+// per-lane partial sum (reduced over the 4 lane groups at the end).
+template <int D>
+struct Acc {
+    f32x4 o[D / 16];
+    float m, l;
+};
+
+template <typename KT, int D, int NP>
+__device__ __forceinline__ void process(Acc<D>& acc, const Tile<KT, D>* tl, const int* valid,
+                                        const typename Tile<KT, D>::Q& q, int grp) {
+    f32x4 s[NP];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+        s[u] = tl[u].scores(q);
+        const int vg = valid[u] - 4 * grp;  // valid tokens among this lane's 4
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (r >= vg) s[u][r] = -INFINITY;
+            mx = fmaxf(mx, s[u][r]);
+        }
+    }
+    // Raise the running max only when some score exceeds it by the threshold;
+    // all lanes of a head column then agree on the new max.
+    if (__any(mx > acc.m + kLazyThreshold)) {
+        mx = wave_max_xor(mx, 16);
+        mx = wave_max_xor(mx, 32);
+        const float m_new = fmaxf(acc.m, mx);
+        const float alpha = fast_exp2(acc.m - m_new);
+        acc.l *= alpha;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) acc.o[t] *= alpha;
+        acc.m = m_new;
+    }
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = fast_exp2(s[u][r] - acc.m);
+        acc.l += (p[0] + p[1]) + (p[2] + p[3]);
+        Tile<KT, D> t = tl[u];
+        if (valid[u] < kPageTokens) t.mask_v(valid[u] - 4 * grp);
+        t.pv(acc.o, p);
+    }
+}
+
+// Prefix scan of per-sequence work items into LDS: s_cum[b] = items of
+// sequences < b (per KV head); returns the total over all sequences.
+__device__ __forceinline__ int scan_items(const int32_t* ctx_len, int batch, int* s_cum,
+                                          int* s_red) {
+    const int tid = threadIdx.x;
+    int carry = 0;
+    for (int base = 0; base < batch; base += kThreads) {
+        const int b = base + tid;
+        const int n = b < batch ? items_of(ctx_len[b]) : 0;
+        // inclusive scan of n across the block
+        int x = n;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o, 64);
+            if ((tid & 63) >= o) x += y;
+        }
+        if ((tid & 63) == 63) s_red[tid >> 6] = x;
+        __syncthreads();
+        int wsum = 0;
+        for (int w = 0; w < (tid >> 6); ++w) wsum += s_red[w];
+        const int incl = carry + wsum + x;
+        if (b < batch) s_cum[b] = incl - n;
+        carry += s_red[0] + s_red[1] + s_red[2] + s_red[3];
+        __syncthreads();
+    }
+    if (tid == 0) s_cum[batch] = carry;
+    __syncthreads();
+    return carry;
+}
+
+// Largest b with Hkv * s_cum[b] <= item (s_cum non-decreasing, s_cum[0] = 0).
+__device__ __forceinline__ int find_seq(const int* s_cum, int batch, int n_kv, int item) {
+    int lo = 0, hi = batch - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (n_kv * s_cum[mid] <= item) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Persistent, balanced decode.  The work of a launch is the list of "items"
+// (kItemPages pages of one (sequence, KV head) segment), ordered by sequence
+// then KV head.  Workgroup w owns the contiguous item range
+// [w*chunk, (w+1)*chunk), chunk = ceil(items / gridDim.x), so every
+// workgroup streams the same number of pages and the launch has no tail.
+// Consecutive items of one segment form a "run" that is accumulated without
+// leaving registers; a run covering its whole segment writes the output,
+// otherwise it writes a partial into the slot of its first item.
+template <typename KT, int D, int NP>
 __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams p,
-                                                          DecodeWorkspace ws, int pps,
-                                                          int n_splits, int group) {
+                                                          DecodeWorkspace ws, int group) {
     using T = Tile<KT, D>;
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int b = blockIdx.z;
+    __shared__ int s_cum[kMaxBatch + 1];
+    __shared__ int s_red[4];
+    __shared__ float s_m[kWaves][16];
+    __shared__ float s_l[kWaves][16];
+    __shared__ __attribute__((aligned(16))) float s_o[kWaves][kMaxGD];
+
     const int n_kv = g.n_kv_heads;
     const int tid = threadIdx.x;
-    const int L = p.ctx_len[b];
-    const int n_pages_b = (L + kPageTokens - 1) / kPageTokens;
-    const int n_active = (n_pages_b + pps - 1) / pps;
-    const int GD = group * D;
-
-    if (n_active == 0) {  // empty context: softmax over nothing leaves zeros (src/ops.rs:161)
-        if (split == 0)
-            for (int idx = tid; idx < GD; idx += kThreads) {
-                int c = idx / D, d = idx - c * D;
-                int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
-                p.out[((size_t)b * p.n_q_heads + h) * D + d] = 0.f;
-            }
-        return;
-    }
-    if (split >= n_active) return;
+    const int per_kv = scan_items(p.ctx_len, p.batch, s_cum, s_red);
+    const int n_items = n_kv * per_kv;
+    const int chunk = (n_items + gridDim.x - 1) / gridDim.x;
+    int cur = blockIdx.x * chunk;
+    const int end = min(n_items, cur + chunk);
+    if (cur >= end) return;
 
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
     const bool col_on = col < group;
-    const int head = head_of(kvh, col_on ? col : 0, n_kv, group, p.gqa_mode);
-
-    typename T::Q q;
-    T::load_q(q, p.q + ((size_t)b * p.n_q_heads + head) * D, p.scale * kLog2e, col_on, grp);
-
-    f32x4 o[D / 16];
-#pragma unroll
-    for (int t = 0; t < D / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -1e30f, l_run = 0.f;
-
-    const int page_begin = split * pps;
-    const int page_end = min(page_begin + pps, n_pages_b);
-    const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
+    const int GD = group * D;
     const size_t blk = (size_t)kPageTokens * D;
     const KT* kpool = reinterpret_cast<const KT*>(g.k);
     const KT* vpool = reinterpret_cast<const KT*>(g.v);
 
-    T cur, nxt;
-    int pg = page_begin + wave;
-    if (pg < page_end) {
-        size_t off = ((size_t)pt[pg] * n_kv + kvh) * blk;
-        cur.load(kpool + off, vpool + off, lane);
-    }
-    for (; pg < page_end; pg += kWaves) {
-        const int pn = pg + kWaves;
-        if (pn < page_end) {
-            size_t off = ((size_t)pt[pn] * n_kv + kvh) * blk;
-            nxt.load(kpool + off, vpool + off, lane);
+    int b = find_seq(s_cum, p.batch, n_kv, cur);
+    while (cur < end) {
+        // segment of item `cur`
+        int nb = s_cum[b + 1] - s_cum[b];
+        while (nb == 0 || cur >= n_kv * s_cum[b + 1]) {  // skip empty / finished sequences
+            ++b;
+            nb = s_cum[b + 1] - s_cum[b];
         }
-        f32x4 s = cur.scores(q);
-        const int valid = L - pg * kPageTokens;  // tokens of this page inside the context
-        if (valid < kPageTokens) {
-            const int vg = valid - 4 * grp;  // valid tokens among this lane's 4
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (r >= vg) s[r] = -INFINITY;
-            cur.mask_v(vg);
-        }
-        float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        mx = wave_max_xor(mx, 16);
-        mx = wave_max_xor(mx, 32);
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        float pr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(s[r] - m_new);
-        l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < D / 16; ++t) o[t] *= alpha;
-        cur.pv(o, pr);
-        if (pn < page_end) cur = nxt;
-    }
-    l_run = wave_sum_xor(l_run, 16);
-    l_run = wave_sum_xor(l_run, 32);
+        const int kvh = (cur - n_kv * s_cum[b]) / nb;
+        const int seg0 = n_kv * s_cum[b] + kvh * nb;
+        const int run_end = min(end, seg0 + nb);
+        const int L = p.ctx_len[b];
+        const int n_pages_b = (L + kPageTokens - 1) / kPageTokens;
+        const int pg0 = (cur - seg0) * kItemPages;
+        const int pg1 = min(n_pages_b, (run_end - seg0) * kItemPages);
+        const bool whole = (cur == seg0) && (run_end == seg0 + nb);
 
-    // ---- merge the 4 wavefronts in LDS ----
-    __shared__ float s_m[kWaves][16];
-    __shared__ float s_l[kWaves][16];
-    __shared__ __attribute__((aligned(16))) float s_o[kWaves][kMaxGD];
-    if (col_on) {
+        const int head = head_of(kvh, col_on ? col : 0, n_kv, group, p.gqa_mode);
+        typename T::Q q;
+        T::load_q(q, p.q + ((size_t)b * p.n_q_heads + head) * D,
+                  col_on ? p.scale * kLog2e : 0.f, grp);
+        Acc<D> acc;
 #pragma unroll
-        for (int t = 0; t < D / 16; ++t)
-            *reinterpret_cast<f32x4*>(&s_o[wave][col * D + 16 * t + 4 * grp]) = o[t];
-        if (grp == 0) {
-            s_m[wave][col] = m_run;
-            s_l[wave][col] = l_run;
-        }
-    }
-    __syncthreads();
+        for (int t = 0; t < D / 16; ++t) acc.o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc.m = -1e30f;
+        acc.l = 0.f;
+        const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
 
-    const size_t bk = (size_t)b * n_kv + kvh;
-    if (n_active == 1) {
+        // sub-runs of up to 256 pages: a wavefront's page ids fit one VGPR
+        for (int sub = pg0; sub < pg1; sub += 64 * kWaves) {
+            const int sub_end = min(sub + 64 * kWaves, pg1);
+            const int first = sub + wave;  // this wave's pages: first + 4j, j < n_my
+            const int n_my = first < sub_end ? (sub_end - first + kWaves - 1) / kWaves : 0;
+            const int pid_v = lane < n_my ? pt[first + kWaves * lane] : 0;
+            const int first_pid = __builtin_amdgcn_readfirstlane(pid_v);
+            auto load_group = [&](T* dst, int i) {
+#pragma unroll
+                for (int u = 0; u < NP; ++u) {
+                    const int j = NP * i + u;
+                    const int pid = j < n_my ? __builtin_amdgcn_readlane(pid_v, j) : first_pid;
+                    const size_t off = ((size_t)pid * n_kv + kvh) * blk;
+                    dst[u].load(kpool + off, vpool + off, lane);
+                }
+            };
+            auto valid_of = [&](int* valid, int i) {
+#pragma unroll
+                for (int u = 0; u < NP; ++u) {
+                    const int j = NP * i + u;
+                    const int tok0 = (first + kWaves * j) * kPageTokens;
+                    valid[u] = j < n_my ? min(L - tok0, kPageTokens) : 0;
+                }
+            };
+            const int n_iter = (n_my + NP - 1) / NP;
+            if (n_iter > 0) {
+                T tcur[NP], tnxt[NP];
+                int valid[NP];
+                load_group(tcur, 0);
+                for (int i = 0; i < n_iter - 1; ++i) {
+                    load_group(tnxt, i + 1);
+                    valid_of(valid, i);
+                    process<KT, D, NP>(acc, tcur, valid, q, grp);
+#pragma unroll
+                    for (int u = 0; u < NP; ++u) tcur[u] = tnxt[u];
+                }
+                valid_of(valid, n_iter - 1);
+                process<KT, D, NP>(acc, tcur, valid, q, grp);
+            }
+        }
+        acc.l = wave_sum_xor(acc.l, 16);
+        acc.l = wave_sum_xor(acc.l, 32);
+
+        // ---- merge the 4 wavefronts in LDS ----
+        if (col_on) {
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t)
+                *reinterpret_cast<f32x4*>(&s_o[wave][col * D + 16 * t + 4 * grp]) = acc.o[t];
+            if (grp == 0) {
+                s_m[wave][col] = acc.m;
+                s_l[wave][col] = acc.l;
+            }
+        }
+        __syncthreads();
+        float* po = ws.partial_o + (size_t)cur * GD;
+        float* pml = ws.partial_ml + (size_t)cur * group * 2;
         for (int idx = tid; idx < GD; idx += kThreads) {
             const int c = idx / D, d = idx - c * D;
             float M = s_m[0][c];
 #pragma unroll
             for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][c]);
-            float acc = 0.f, lsum = 0.f;
+            float o = 0.f, lsum = 0.f;
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
                 const float f = fast_exp2(s_m[w][c] - M);
-                acc += f * s_o[w][idx];
+                o += f * s_o[w][idx];
                 lsum += f * s_l[w][c];
             }
-            const int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
-            const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
-            float r = acc / lsum;
-            if (p.gate) r *= sigmoidf_(p.gate[oi]);
-            p.out[oi] = r;
+            if (whole) {
+                const int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
+                const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
+                float r = o / lsum;
+                if (p.gate) r *= sigmoidf_(p.gate[oi]);
+                p.out[oi] = r;
+            } else {
+                po[idx] = o;
+                if (d == 0) {
+                    pml[2 * c] = M;
+                    pml[2 * c + 1] = lsum;
+                }
+            }
+        }
+        __syncthreads();  // LDS is reused by the next run
+        cur = run_end;
+    }
+}
+
+// Combines the run partials of every (sequence, KV head) segment that spans
+// more than one workgroup range; zero-length sequences get zeros.  Runs of a
+// segment [I, I+n) start at I and at every multiple of `chunk` inside it.
+// Grid (ceil(G*D / 256), n_kv, batch): one thread per output element.
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, DecodeWorkspace ws,
+                                                           int n_kv, int D, int group,
+                                                           int n_wg) {
+    __shared__ int s_cum[kMaxBatch + 1];
+    __shared__ int s_red[4];
+    __shared__ float s_w[4][kMaxRuns];  // per column (<= 4 per 256 elements) and run
+    __shared__ int s_slot[kMaxRuns];
+    __shared__ float s_inv[4];
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int per_kv = scan_items(p.ctx_len, p.batch, s_cum, s_red);
+    const int chunk = (n_kv * per_kv + n_wg - 1) / n_wg;
+    const int nb = s_cum[b + 1] - s_cum[b];
+    const int GD = group * D;
+    const int e0 = blockIdx.x * 256;
+    const int idx = e0 + tid;
+    if (nb == 0) {  // empty context: softmax over nothing leaves zeros (src/ops.rs:161)
+        if (idx < GD) {
+            const int c = idx / D, d = idx - c * D;
+            p.out[((size_t)b * p.n_q_heads + head_of(kvh, c, n_kv, group, p.gqa_mode)) * D + d] = 0.f;
         }
         return;
     }
-
-    float* po = ws.partial_o + (bk * n_splits + split) * GD;
-    float* pml = ws.partial_ml + (bk * n_splits + split) * group * 2;
-    for (int idx = tid; idx < GD; idx += kThreads) {
-        const int c = idx / D, d = idx - c * D;
-        float M = s_m[0][c];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][c]);
-        float acc = 0.f, lsum = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float f = fast_exp2(s_m[w][c] - M);
-            acc += f * s_o[w][idx];
-            lsum += f * s_l[w][c];
-        }
-        po[idx] = acc;
-        if (d == 0) {
-            pml[2 * c] = M;
-            pml[2 * c + 1] = lsum;
-        }
-    }
-
-    // ---- last workgroup of this (sequence, KV head) merges the splits ----
-    __shared__ int s_last;
-    __threadfence();
+    const int seg0 = n_kv * s_cum[b] + kvh * nb;
+    const int seg1 = seg0 + nb;
+    const int first_cut = (seg0 / chunk + 1) * chunk;  // first workgroup boundary after seg0
+    if (first_cut >= seg1) return;  // one run: written directly by decode_kernel
+    const int n_runs = 1 + (seg1 - 1 - first_cut) / chunk + 1;
+    for (int r = tid; r < n_runs && r < kMaxRuns; r += 256) s_slot[r] = r == 0 ? seg0 : first_cut + (r - 1) * chunk;
     __syncthreads();
-    if (tid == 0) {
-        unsigned prev = __hip_atomic_fetch_add(ws.counters + bk, 1u, __ATOMIC_ACQ_REL,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (unsigned)(n_active - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    const float* po0 = ws.partial_o + bk * n_splits * GD;
-    const float* pml0 = ws.partial_ml + bk * n_splits * group * 2;
-    for (int idx = tid; idx < GD; idx += kThreads) {
-        const int c = idx / D, d = idx - c * D;
+    const int c_lo = e0 / D, c_hi = min(group - 1, (e0 + 255) / D);
+    const int lane = tid & 63, wave = tid >> 6;
+    const float* pml = ws.partial_ml;
+    if (wave <= c_hi - c_lo) {  // one wavefront per column
+        const int c = c_lo + wave;
         float M = -1e30f;
-        for (int s = 0; s < n_active; ++s) M = fmaxf(M, __builtin_nontemporal_load(&pml0[(s * group + c) * 2]));
-        float acc = 0.f, lsum = 0.f;
-        for (int s = 0; s < n_active; ++s) {
-            const float ms = __builtin_nontemporal_load(&pml0[(s * group + c) * 2]);
-            const float ls = __builtin_nontemporal_load(&pml0[(s * group + c) * 2 + 1]);
-            const float f = fast_exp2(ms - M);
-            acc += f * __builtin_nontemporal_load(&po0[(size_t)s * GD + idx]);
-            lsum += f * ls;
+        for (int r = lane; r < n_runs; r += 64) M = fmaxf(M, pml[((size_t)s_slot[r] * group + c) * 2]);
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) M = wave_max_xor(M, m);
+        float lsum = 0.f;
+        for (int r = lane; r < n_runs; r += 64) {
+            const size_t mi = ((size_t)s_slot[r] * group + c) * 2;
+            const float w = fast_exp2(pml[mi] - M);
+            s_w[wave][r] = w;
+            lsum += w * pml[mi + 1];
         }
-        const int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
-        const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
-        float r = acc / lsum;
-        if (p.gate) r *= sigmoidf_(p.gate[oi]);
-        p.out[oi] = r;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
+        if (lane == 0) s_inv[wave] = 1.0f / lsum;
     }
-    if (tid == 0) __hip_atomic_store(ws.counters + bk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (idx >= GD) return;
+    const int c = idx / D, d = idx - c * D;
+    const float* w = s_w[c - c_lo];
+    float o0 = 0.f, o1 = 0.f;
+    int r = 0;
+    for (; r + 2 <= n_runs; r += 2) {
+        o0 += w[r] * ws.partial_o[(size_t)s_slot[r] * GD + idx];
+        o1 += w[r + 1] * ws.partial_o[(size_t)s_slot[r + 1] * GD + idx];
+    }
+    if (r < n_runs) o0 += w[r] * ws.partial_o[(size_t)s_slot[r] * GD + idx];
+    const int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
+    const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
+    float res = (o0 + o1) * s_inv[c - c_lo];
+    if (p.gate) res *= sigmoidf_(p.gate[oi]);
+    p.out[oi] = res;
 }
 
 template <typename KT, int D>
-hipError_t launch_t(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws, int pps,
-                    int n_splits, hipStream_t s) {
+constexpr int np_of() { return (sizeof(KT) == 2 && D <= 128) ? 2 : 1; }
+
+template <typename KT, int D>
+int wgs_per_cu() {
+    static int n = -1;
+    if (n < 0) {
+        int v = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, decode_kernel<KT, D, np_of<KT, D>()>,
+                                                         kThreads, 0) != hipSuccess || v <= 0)
+            v = 1;
+        n = v;
+    }
+    return n;
+}
+
+template <typename KT, int D>
+hipError_t launch_t(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,
+                    const DecodePlan& plan, hipStream_t s) {
     const int group = p.n_q_heads / g.n_kv_heads;
-    dim3 grid(n_splits, g.n_kv_heads, p.batch);
-    hipLaunchKernelGGL((decode_kernel<KT, D>), grid, dim3(kThreads), 0, s, g, p, ws, pps, n_splits,
-                       group);
+    hipLaunchKernelGGL((decode_kernel<KT, D, np_of<KT, D>()>), dim3(plan.grid), dim3(kThreads), 0,
+                       s, g, p, ws, group);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3((group * D + 255) / 256, g.n_kv_heads, p.batch),
+                       dim3(256), 0, s, p, ws, g.n_kv_heads, D, group, plan.grid);
     return hipGetLastError();
 }
 
 }  // namespace
 
-void decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t* pages_per_split,
-                 int32_t* n_splits) {
-    // Aim for ~8k workgroups over the table's upper bound so that ragged
-    // batches still leave many active workgroups per CU (256 CUs).
-    long long total = (long long)batch * g.n_kv_heads * max_pages;
-    int pps = 4;
-    while (pps < 256 && total / pps > 8192) pps *= 2;
-    if (const char* e = std::getenv("PI_DECODE_PPS")) {
-        int v = std::atoi(e);
-        if (v >= 4 && v <= 4096 && (v & (v - 1)) == 0) pps = v;
+DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
+                       int device) {
+    DecodePlan plan;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        cus <= 0)
+        cus = 256;
+    int per_cu = 1;
+    const bool hp = g.dtype == 1;
+    switch (g.head_dim) {
+        case 64: per_cu = hp ? wgs_per_cu<f16, 64>() : wgs_per_cu<float, 64>(); break;
+        case 128: per_cu = hp ? wgs_per_cu<f16, 128>() : wgs_per_cu<float, 128>(); break;
+        default: per_cu = wgs_per_cu<f16, 256>(); break;
     }
-    *pages_per_split = pps;
-    *n_splits = (max_pages + pps - 1) / pps;
+    plan.grid = cus * per_cu;
+    if (const char* e = std::getenv("PI_DECODE_GRID")) {
+        const int v = std::atoi(e);
+        if (v >= 1 && v < kMaxRuns) plan.grid = v;
+    }
+    const long long items_per_seq = (max_pages + kItemPages - 1) / kItemPages;
+    plan.n_slots = (long long)batch * g.n_kv_heads * items_per_seq;
+    plan.group = n_q_heads / g.n_kv_heads;
+    return plan;
 }
 
-size_t decode_ws_floats_o(const KvGeom& g, int32_t batch, int32_t n_q_heads, int32_t n_splits) {
-    return (size_t)batch * g.n_kv_heads * n_splits * (n_q_heads / g.n_kv_heads) * g.head_dim;
+size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan) {
+    return (size_t)plan.n_slots * plan.group * g.head_dim;
 }
 
 hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,
-                         int32_t pps, int32_t n_splits, hipStream_t s) {
+                         const DecodePlan& plan, hipStream_t s) {
     const bool hp = g.dtype == 1;
     switch (g.head_dim) {
-        case 64: return hp ? launch_t<f16, 64>(g, p, ws, pps, n_splits, s) : launch_t<float, 64>(g, p, ws, pps, n_splits, s);
-        case 128: return hp ? launch_t<f16, 128>(g, p, ws, pps, n_splits, s) : launch_t<float, 128>(g, p, ws, pps, n_splits, s);
-        case 256: return hp ? launch_t<f16, 256>(g, p, ws, pps, n_splits, s) : hipErrorInvalidValue;
+        case 64: return hp ? launch_t<f16, 64>(g, p, ws, plan, s) : launch_t<float, 64>(g, p, ws, plan, s);
+        case 128: return hp ? launch_t<f16, 128>(g, p, ws, plan, s) : launch_t<float, 128>(g, p, ws, plan, s);
+        case 256: return hp ? launch_t<f16, 256>(g, p, ws, plan, s) : hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }

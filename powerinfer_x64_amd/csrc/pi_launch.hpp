@@ -9,6 +9,8 @@
 namespace pi {
 
 constexpr int kPageTokens = 16;  // tokens per KV page
+constexpr int kItemPages = 16;   // pages per decode work item (the balancing unit)
+constexpr int kMaxBatch = 4096;  // sequences per decode launch (LDS prefix scan)
 
 // KV pool geometry: one K and one V block of kPageTokens x head_dim elements
 // per (page, kv head).  K block layout: [head_dim/E][16 tokens][E] with
@@ -27,12 +29,10 @@ struct KvGeom {
 };
 
 struct DecodeWorkspace {
-    float* partial_o;     // [batch][n_kv][n_splits][G][D]
-    float* partial_ml;    // [batch][n_kv][n_splits][G][2]  (running max, sum) in log2 units
-    uint32_t* counters;   // [batch][n_kv], zero between launches
+    float* partial_o;     // [item slot][G][D]  (only run-start slots are written)
+    float* partial_ml;    // [item slot][G][2]  (running max, sum) in log2 units
     size_t capacity_o;    // floats
     size_t capacity_ml;   // floats
-    size_t capacity_cnt;  // counters
 };
 
 struct DecodeParams {
@@ -48,12 +48,17 @@ struct DecodeParams {
     float scale;
 };
 
-// Chooses pages-per-split and the split count for a decode launch.
-void decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t* pages_per_split,
-                 int32_t* n_splits);
-size_t decode_ws_floats_o(const KvGeom& g, int32_t batch, int32_t n_q_heads, int32_t n_splits);
+struct DecodePlan {
+    int32_t grid;       // persistent workgroups (CUs x resident workgroups per CU)
+    long long n_slots;  // upper bound of work items (partial slots)
+    int32_t group;      // q heads per kv head
+};
+// Grid size and workspace bound of a decode launch on `device`.
+DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
+                       int device);
+size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan);
 hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,
-                         int32_t pages_per_split, int32_t n_splits, hipStream_t s);
+                         const DecodePlan& plan, hipStream_t s);
 
 hipError_t launch_kv_append(const KvGeom& g, const void* k, const void* v, int32_t src_dtype,
                             const int32_t* page_table, int32_t max_pages,

@@ -25,6 +25,7 @@ constexpr int BN = 64;         // keys per block
 constexpr int ROWS = 32;       // query rows per wavefront
 constexpr int KSTR = D + 8;    // LDS row stride of K (elements)
 constexpr int VSTR = BN + 4;   // LDS row stride of V^T (elements)
+constexpr float kLazy = 8.0f;  // log2 headroom before the running max moves
 
 template <typename T>
 struct Mfma;
@@ -59,28 +60,29 @@ __device__ __forceinline__ int head_of(int kvh, int c, int hkv, int group, int m
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     typedef typename Mfma<T>::v8 v8;
     typedef typename Mfma<T>::v4 v4;
-    __shared__ __attribute__((aligned(16))) T sk[BN * KSTR];
-    __shared__ __attribute__((aligned(16))) T sv[D * VSTR];
+    // double-buffered K [64 x D] and V^T [D x 64] tiles
+    __shared__ __attribute__((aligned(16))) T sk[2][BN * KSTR];
+    __shared__ __attribute__((aligned(16))) T sv[2][D * VSTR];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.z;
     const int S = a.S;
-    const int qb = gridDim.x - 1 - blockIdx.x;  // heaviest (latest) query blocks first
+    const int qb = gridDim.y - 1 - blockIdx.y;  // heaviest (latest) query blocks first
 
     int kvh, head, p0, p_last;
     if (a.pack4) {
-        const int cg = blockIdx.y % (a.group / 4);
-        kvh = blockIdx.y / (a.group / 4);
+        const int cg = blockIdx.x % (a.group / 4);
+        kvh = blockIdx.x / (a.group / 4);
         head = head_of(kvh, 4 * cg + wave, a.hkv, a.group, a.gqa_mode);
         p0 = qb * ROWS;
         p_last = p0 + ROWS - 1;
     } else {
-        head = blockIdx.y;
+        head = blockIdx.x;
         kvh = a.gqa_mode == 0 ? head % a.hkv : head / a.group;
         p0 = qb * 4 * ROWS + wave * ROWS;
         p_last = qb * 4 * ROWS + 4 * ROWS - 1;
@@ -109,18 +111,18 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     f32x16 o[D / 32];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) o[i] = f32x16{};
-    float m_run = -1e30f, l_run = 0.f;
+    float m_run = -1e30f, l_run = 0.f;  // running max in scaled log2 units
 
     const T* kg = reinterpret_cast<const T*>(a.k);
     const T* vg = reinterpret_cast<const T*>(a.v);
     const size_t tok_stride = (size_t)a.hkv * D;
     const T* kbase = kg + ((size_t)b * S * a.hkv + kvh) * D;
     const T* vbase = vg + ((size_t)b * S * a.hkv + kvh) * D;
+    const int tg = tid & 15, dc = tid >> 4;
 
-    for (int kb = 0; kb < n_blocks; ++kb) {
+    v8 kreg[4], vreg[4];
+    auto load_tile = [&](int kb) {
         const int k0 = kb * BN;
-        // ---- global -> registers (K rows and 4-token V column groups) ----
-        v8 kreg[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int id = tid + 256 * i;
@@ -129,8 +131,6 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
             if (k0 + tk < S) t = *reinterpret_cast<const v8*>(kbase + (size_t)(k0 + tk) * tok_stride + 8 * c);
             kreg[i] = t;
         }
-        v8 vreg[4];
-        const int tg = tid & 15, dc = tid >> 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tk = 4 * tg + i;
@@ -138,87 +138,105 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
             if (k0 + tk < S) t = *reinterpret_cast<const v8*>(vbase + (size_t)(k0 + tk) * tok_stride + 8 * dc);
             vreg[i] = t;
         }
-        __syncthreads();  // previous block's LDS reads are done
+    };
+    auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int id = tid + 256 * i;
             const int tk = id >> 4, c = id & 15;
-            *reinterpret_cast<v8*>(&sk[tk * KSTR + 8 * c]) = kreg[i];
+            *reinterpret_cast<v8*>(&sk[buf][tk * KSTR + 8 * c]) = kreg[i];
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             v4 t = {vreg[0][e], vreg[1][e], vreg[2][e], vreg[3][e]};
-            *reinterpret_cast<v4*>(&sv[(8 * dc + e) * VSTR + 4 * tg]) = t;
+            *reinterpret_cast<v4*>(&sv[buf][(8 * dc + e) * VSTR + 4 * tg]) = t;
         }
-        __syncthreads();
+    };
 
-        if (a.causal && k0 > p0 + ROWS - 1) continue;  // every key of this block is in this wave's future
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int kb = 0; kb < n_blocks; ++kb) {
+        const int k0 = kb * BN;
+        const int buf = kb & 1;
+        const bool more = kb + 1 < n_blocks;
+        if (more) load_tile(kb + 1);  // in flight while this block computes
 
-        // ---- S^T = K . Q^T : two 32x32 tiles (keys 0-31, 32-63) ----
-        f32x16 s[2];
+        // every key of this block in this wave's future: nothing to do
+        if (!(a.causal && k0 > p0 + ROWS - 1)) {
+            // ---- S^T = K . Q^T : two 32x32 tiles (keys 0-31, 32-63) ----
+            f32x16 s[2];
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            f32x16 acc = f32x16{};
+            for (int tt = 0; tt < 2; ++tt) {
+                f32x16 acc = f32x16{};
 #pragma unroll
-            for (int kk = 0; kk < D / 16; ++kk) {
-                const v8 ka = *reinterpret_cast<const v8*>(&sk[(32 * tt + r) * KSTR + 16 * kk + 8 * hh]);
-                acc = Mfma<T>::mma(ka, qr[kk], acc);
+                for (int kk = 0; kk < D / 16; ++kk) {
+                    const v8 ka = *reinterpret_cast<const v8*>(&sk[buf][(32 * tt + r) * KSTR + 16 * kk + 8 * hh]);
+                    acc = Mfma<T>::mma(ka, qr[kk], acc);
+                }
+                s[tt] = acc;
             }
-            s[tt] = acc;
-        }
-        // scale + mask; lane holds key rows 32*tt + 8*i + 4*hh + j for query qpos
-        const bool need_mask = (a.causal && k0 + BN - 1 > p0) || (k0 + BN > S);
-        float mx = -INFINITY;
+            // mask; lane holds key rows 32*tt + 8*i + 4*hh + j for query qpos
+            const bool need_mask = (a.causal && k0 + BN - 1 > p0) || (k0 + BN > S);
+            float mx = -INFINITY;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+            for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        float x = s[tt][4 * i + j];
+                        if (need_mask) {
+                            const int key = k0 + 32 * tt + 8 * i + 4 * hh + j;
+                            if (key >= S || (a.causal && key > qpos)) x = -INFINITY;
+                        }
+                        s[tt][4 * i + j] = x;
+                        mx = fmaxf(mx, x);
+                    }
+            // lazily raised running max (scaled units); the scale is fused into exp2
+            const float c = a.qk_scale;
+            if (__any(mx * c > m_run + kLazy)) {
+                mx = wave_max_xor(mx, 32);
+                const float m_new = fmaxf(m_run, mx * c);
+                const float alpha = fast_exp2(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int i = 0; i < D / 32; ++i) o[i] *= alpha;
+                m_run = m_new;
+            }
+            float ls = 0.f;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float pe = fast_exp2(__builtin_fmaf(s[tt][e], c, -m_run));
+                    s[tt][e] = pe;
+                    ls += pe;
+                }
+            l_run += ls;
+
+            // ---- O^T += V^T . P^T : 4 key steps of 16, 4 dim tiles of 32 ----
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int tt = ks >> 1, i0 = 2 * (ks & 1);
+                v8 pb;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    float x = s[tt][4 * i + j] * a.qk_scale;
-                    if (need_mask) {
-                        const int key = k0 + 32 * tt + 8 * i + 4 * hh + j;
-                        if (key >= S || (a.causal && key > qpos)) x = -INFINITY;
-                    }
-                    s[tt][4 * i + j] = x;
-                    mx = fmaxf(mx, x);
+                    pb[j] = (T)s[tt][4 * i0 + j];
+                    pb[4 + j] = (T)s[tt][4 * (i0 + 1) + j];
                 }
-        mx = wave_max_xor(mx, 32);
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        float ls = 0.f;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float pe = fast_exp2(s[tt][e] - m_new);
-                s[tt][e] = pe;
-                ls += pe;
-            }
-        l_run = l_run * alpha + ls;
-        m_run = m_new;
-#pragma unroll
-        for (int i = 0; i < D / 32; ++i) o[i] *= alpha;
-
-        // ---- O^T += V^T . P^T : 4 key steps of 16, 4 dim tiles of 32 ----
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int tt = ks >> 1, i0 = 2 * (ks & 1);
-            v8 pb;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                pb[j] = (T)s[tt][4 * i0 + j];
-                pb[4 + j] = (T)s[tt][4 * (i0 + 1) + j];
-            }
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const T* vrow = &sv[(32 * dt + r) * VSTR + 16 * ks + 4 * hh];
-                const v4 lo = *reinterpret_cast<const v4*>(vrow);
-                const v4 hi = *reinterpret_cast<const v4*>(vrow + 8);
-                const v8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[dt] = Mfma<T>::mma(va, pb, o[dt]);
+                for (int dt = 0; dt < D / 32; ++dt) {
+                    const T* vrow = &sv[buf][(32 * dt + r) * VSTR + 16 * ks + 4 * hh];
+                    const v4 lo = *reinterpret_cast<const v4*>(vrow);
+                    const v4 hi = *reinterpret_cast<const v4*>(vrow + 8);
+                    const v8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[dt] = Mfma<T>::mma(va, pb, o[dt]);
+                }
             }
         }
+        if (more) store_tile(buf ^ 1);
+        __syncthreads();
     }
 
     l_run = wave_sum_xor(l_run, 32);
@@ -256,10 +274,12 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     a.pack4 = (a.group % 4) == 0;
     a.qk_scale = scale * kLog2e;
     dim3 grid;
+    // x = head group (fastest), y = query block (reversed in the kernel), so the
+    // heaviest query blocks of every head group are dispatched first.
     if (a.pack4)
-        grid = dim3((seq_len + ROWS - 1) / ROWS, n_kv_heads * (a.group / 4), batch);
+        grid = dim3(n_kv_heads * (a.group / 4), (seq_len + ROWS - 1) / ROWS, batch);
     else
-        grid = dim3((seq_len + 4 * ROWS - 1) / (4 * ROWS), n_q_heads, batch);
+        grid = dim3(n_q_heads, (seq_len + 4 * ROWS - 1) / (4 * ROWS), batch);
     if (dtype == 2)
         hipLaunchKernelGGL(prefill_kernel<bf16>, grid, dim3(256), 0, s, a);
     else

@@ -162,3 +162,38 @@ def test_attention_head_host_dropin():
         v3[i, i] = 10 * (i + 1)
     out = rt.attention_head(dev, q4 * math.sqrt(64 / 4), k3, v3, 3, 64)
     np.testing.assert_allclose(out[:4], [4.51863, 5.48137, 8.22206, 0], rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("grid", [None, "1", "7", "1000"])
+def test_decode_balanced_schedule_edges(grid, monkeypatch):
+    """Ragged batch with empty sequences in between, under several persistent-grid
+    sizes (PI_DECODE_GRID): runs split a segment across many workgroups."""
+    if grid is not None:
+        monkeypatch.setenv("PI_DECODE_GRID", grid)
+    dev = device()
+    rng = np.random.default_rng(31)
+    lens = [0, 5, 0, 0, 3000, 1, 0, 257, 4096, 16, 17]
+    case = PagedCase(rng, lens, 8, 2, 128, theta=1e6)
+    case.gpu_build(dev, torch.float16)
+    out = case.gpu_decode(dev)
+    for i, x in enumerate(lens):
+        if x == 0:
+            np.testing.assert_array_equal(out[i], 0)
+        else:
+            ref = case.oracle_out(i, kv_round=np.float16)
+            assert row_rel_err(out[i], ref) <= 1e-2, (grid, i, x)
+
+
+def test_decode_large_batch_scan():
+    """More sequences than threads in a workgroup (multi-chunk prefix scan)."""
+    dev = device()
+    rng = np.random.default_rng(32)
+    lens = rng.integers(0, 200, size=300)
+    case = PagedCase(rng, lens, 4, 1, 64, theta=1e4)
+    case.gpu_build(dev, torch.float16)
+    out = case.gpu_decode(dev)
+    for i in list(range(0, 300, 13)) + [299]:
+        if lens[i] == 0:
+            np.testing.assert_array_equal(out[i], 0)
+        else:
+            assert row_rel_err(out[i], case.oracle_out(i, kv_round=np.float16)) <= 1e-2
