@@ -45,7 +45,7 @@ def _args():
                    help="budget of the single-core CPU baseline sample")
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--workload", default=None,
-                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn"],
+                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill"],
                    help="time one workload only and print its figures (for sweeps)")
     return p.parse_args()
 
@@ -239,6 +239,40 @@ def bench_gdn_decode(torch, rt, dev, timer, steps, warmup):
             "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_launch": algo}
 
 
+def bench_gdn_prefill(torch, rt, dev, timer, steps, warmup, t=4096):
+    """Config 5 prefill: 4096 tokens, chunk 64, from a zero state."""
+    hk, hv, dk, dv = 16, 32, 128, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED0005)
+    q = torch.randn((t, hk, dk), generator=g, device="cuda")
+    k = torch.randn((t, hk, dk), generator=g, device="cuda")
+    v = torch.randn((t, hv, dv), generator=g, device="cuda")
+    beta = torch.sigmoid(torch.randn((t, hv), generator=g, device="cuda"))
+    gg = -torch.nn.functional.softplus(torch.randn((t, hv), generator=g, device="cuda"))
+    state = torch.zeros((hv, dk, dv), device="cuda")
+    out = torch.empty((t, hv, dv), device="cuda")
+    lib = dev.lib
+    P = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    args = (dev.h, P(q), P(k), P(v), P(beta), P(gg), P(state), P(out), t, hk, hv, dk, dv, 64,
+            None)
+
+    def fn():
+        rc = lib.pi_gdn_prefill(*args)
+        if rc:
+            raise RuntimeError(lib.pi_last_error(dev.h).decode())
+
+    r = timer.run(fn, steps, warmup)
+    nc = (t + 63) // 64
+    # algorithmic bytes: f32 q, k, v, beta, g in; out and state in + out
+    algo = (2 * t * hk * dk + t * hv * dv + 2 * t * hv + t * hv * dv + 2 * hv * dk * dv) * 4
+    c = 64
+    flops = nc * hv * (6 * c * dk * dv + 6 * c * c * dk + 4 * c * c * dv + (2 / 3) * c ** 3)
+    s = r["ms_avg"] * 1e-3
+    return {"ms_per_step": r["ms_avg"], "tokens_per_s": t / s, "GB_s": algo / s / 1e9,
+            "hbm_frac": algo / s / 1e9 / HBM_PEAK_GBS, "TFLOP_s": flops / s / 1e12,
+            "bytes_per_launch": algo, "flops_per_launch": flops}
+
+
 def _traffic(name):
     """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
     p = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
@@ -268,6 +302,8 @@ def _single(torch, rt, dev, timer, a):
                             pool_dtype=torch.float32)[0]
     if w == "c3":
         return bench_prefill(torch, rt, dev, timer, 4096, 32, 8, 128, 1e6, 0x5EED0002, st, wu)
+    if w == "gdn_prefill":
+        return bench_gdn_prefill(torch, rt, dev, timer, st, wu)
     return bench_gdn_decode(torch, rt, dev, timer, st, wu)
 
 
@@ -353,6 +389,7 @@ def main():
         del st
         wl["c1_mha_decode_513"] = r1
         wl["c5_gdn_decode_step"] = bench_gdn_decode(torch, rt, dev, timer, a.steps, a.warmup)
+        wl["c5_gdn_prefill_4096"] = bench_gdn_prefill(torch, rt, dev, timer, a.steps, a.warmup)
         line["workloads"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                                  for kk, vv in v.items()} for k, v in wl.items()}
     line["cpu_baseline_wall_s"] = round(cpu_wall, 2)

@@ -415,7 +415,7 @@ int pi_gdn_prefill(pi_handle h, const float* d_q, const float* d_k, const float*
     if (n_tok == 0) return PI_OK;
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_gdn_prefill");
-    const size_t need = pi::gdn_prefill_ws_floats(n_tok, n_v_heads, chunk);
+    const size_t need = pi::gdn_prefill_ws_floats(n_tok, n_k_heads, n_v_heads, chunk);
     if (need) {
         rc = grow(h, &h->gws.buf, &h->gws.capacity, need, s, "pi_gdn_prefill workspace", false);
         if (rc) return rc;

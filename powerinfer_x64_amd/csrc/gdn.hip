@@ -115,6 +115,328 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict
     }
 }
 
+// ---------------------------------------------------------------------------
+// Chunked prefill.  For a chunk of C = 64 tokens of one V head, with q/k
+// normalised, gamma_i = exp(lg_i), lg = inclusive cumsum of g over the chunk
+// and S the state entering the chunk, the per-token recurrence above equals
+//   (I + A) Delta = diag(beta) (V - diag(gamma) K S),
+//       A_ij = beta_i exp(lg_i - lg_j) k_i.k_j  (j < i)
+//   O = diag(gamma) Q S + M Delta,  M_ij = exp(lg_i - lg_j) q_i.k_j  (j <= i)
+//   S' = exp(lg_C) S + K^T diag(exp(lg_C - lg_i)) Delta
+// gdn_prep_kernel (parallel over chunks x V heads) builds T = (I + A)^-1, M,
+// lg and the q/k inverse norms; gdn_scan_kernel walks the chunks in order for
+// one (V head, 16 state columns) with the state tile in LDS.  Matrix products
+// use the f32 MFMA (v_mfma_f32_16x16x4f32).
+// ---------------------------------------------------------------------------
+constexpr int GC = 64;          // chunk length
+constexpr int KS_ = DK + 4;     // LDS row stride of [64][128] tiles
+constexpr int TS_ = GC + 4;     // LDS row stride of [64][64] / [16][64] tiles
+constexpr int SCOLS = 16;       // state columns per scan workgroup
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// acc += X[row0 + (l%16)][k] * Yt[col0 + (l%16)][k] summed over k < 16*ns.
+// Lane (l%16, g = l/16) reads 4 consecutive k per operand (k = 16s + 4g + r).
+__device__ __forceinline__ f32x4 tile_mm(const float* X, int xs, int row0, const float* Yt,
+                                         int ys, int col0, int ns, f32x4 acc) {
+    const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
+    for (int s = 0; s < ns; ++s) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(X + (row0 + i) * xs + 16 * s + 4 * g);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(Yt + (col0 + i) * ys + 16 * s + 4 * g);
+        acc = mfma4(x[0], y[0], acc);
+        acc = mfma4(x[1], y[1], acc);
+        acc = mfma4(x[2], y[2], acc);
+        acc = mfma4(x[3], y[3], acc);
+    }
+    return acc;
+}
+
+struct GdnWs {
+    float* rq;  // [T][Hk] 1/max(|q|,1e-12) * 1/sqrt(Dk)
+    float* rk;  // [T][Hk] 1/max(|k|,1e-12)
+    float* tm;  // [n_chunks][Hv][64][64] (I + A)^-1
+    float* mm;  // [n_chunks][Hv][64][64] M
+    float* lg;  // [n_chunks][Hv][64] cumulative log decay
+};
+
+__global__ __launch_bounds__(256) void gdn_prep_kernel(const float* __restrict__ q,
+                                                       const float* __restrict__ k,
+                                                       const float* __restrict__ beta,
+                                                       const float* __restrict__ g, int n_tok,
+                                                       int hk, int hv, GdnWs w) {
+    __shared__ __attribute__((aligned(16))) float sk[GC * KS_];
+    __shared__ __attribute__((aligned(16))) float sq[GC * KS_];
+    __shared__ __attribute__((aligned(16))) float sa[GC * TS_];  // A, then T
+    __shared__ float slg[GC], sb[GC];
+    const int n = blockIdx.x, vh = blockIdx.y, kh = vh % hk;
+    const int t0 = n * GC;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    // raw rows of the K head (zeros past the end of the prompt)
+    for (int e = tid; e < GC * DK / 4; e += 256) {
+        const int row = e / (DK / 4), c4 = e % (DK / 4);
+        const int t = t0 + row;
+        f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+        if (t < n_tok) {
+            a = *reinterpret_cast<const f32x4*>(q + ((size_t)t * hk + kh) * DK + 4 * c4);
+            b = *reinterpret_cast<const f32x4*>(k + ((size_t)t * hk + kh) * DK + 4 * c4);
+        }
+        *reinterpret_cast<f32x4*>(sq + row * KS_ + 4 * c4) = a;
+        *reinterpret_cast<f32x4*>(sk + row * KS_ + 4 * c4) = b;
+    }
+    if (wave == 0) {  // inclusive cumsum of g, and beta (0 past the end)
+        const int t = t0 + lane;
+        float x = t < n_tok ? g[(size_t)t * hv + vh] : 0.f;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        slg[lane] = x;
+        sb[lane] = t < n_tok ? beta[(size_t)t * hv + vh] : 0.f;
+        w.lg[((size_t)n * hv + vh) * GC + lane] = x;
+    }
+    __syncthreads();
+    // L2 norms (src/model/mod.rs:860-875); wave w handles rows 16w..16w+15
+    for (int rr = 0; rr < 16; ++rr) {
+        const int row = 16 * wave + rr;
+        const float q0 = sq[row * KS_ + lane], q1 = sq[row * KS_ + 64 + lane];
+        const float k0 = sk[row * KS_ + lane], k1 = sk[row * KS_ + 64 + lane];
+        float ssq = q0 * q0 + q1 * q1, ssk = k0 * k0 + k1 * k1;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            ssq = wave_sum_xor(ssq, m);
+            ssk = wave_sum_xor(ssk, m);
+        }
+        const float iq = 1.0f / fmaxf(sqrtf(ssq), 1e-12f) * (1.0f / sqrtf((float)DK));
+        const float ik = 1.0f / fmaxf(sqrtf(ssk), 1e-12f);
+        sq[row * KS_ + lane] = q0 * iq;
+        sq[row * KS_ + 64 + lane] = q1 * iq;
+        sk[row * KS_ + lane] = k0 * ik;
+        sk[row * KS_ + 64 + lane] = k1 * ik;
+        const int t = t0 + row;
+        if (lane == 0 && vh < hk && t < n_tok) {  // one writer per (token, K head)
+            w.rq[(size_t)t * hk + kh] = iq;
+            w.rk[(size_t)t * hk + kh] = ik;
+        }
+    }
+    __syncthreads();
+    // lower-triangular 16x16 tiles of K K^T (-> A) and Q K^T (-> M)
+    const int ln = lane & 15, lg4 = lane >> 4;
+    float* mm = w.mm + ((size_t)n * hv + vh) * GC * GC;
+    for (int tix = wave; tix < 10; tix += 4) {
+        int ib = 0, jb = tix;
+        while (jb > ib) { jb -= ib + 1; ++ib; }  // enumerate (ib, jb), jb <= ib
+        f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
+        kk = tile_mm(sk, KS_, 16 * ib, sk, KS_, 16 * jb, DK / 16, kk);
+        qk = tile_mm(sq, KS_, 16 * ib, sk, KS_, 16 * jb, DK / 16, qk);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = 16 * ib + 4 * lg4 + r, j = 16 * jb + ln;
+            const float dec = expf(slg[i] - slg[j]);
+            sa[i * TS_ + j] = j < i ? sb[i] * dec * kk[r] : 0.f;
+            mm[i * GC + j] = j <= i ? dec * qk[r] : 0.f;
+        }
+        if (ib != jb)  // the mirrored upper tile of M is zero
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mm[(16 * jb + ln) * GC + 16 * ib + 4 * lg4 + r] = 0.f;
+    }
+    __syncthreads();
+    // T = (I + A)^-1 by forward substitution (one wavefront, lane = column):
+    // T[i][m] = -sum_{m <= j < i} A[i][j] T[j][m]  (T[i][i] = 1)
+    if (wave == 0) {
+        float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
+        // sa rows are read as A and overwritten in place with T, row by row
+        float trow_prev[1];
+        (void)trow_prev;
+        for (int i = 0; i < GC; ++i) {
+            float acc = 0.f;
+            for (int j = lane; j < i; ++j) acc -= sa[i * TS_ + j] * sa[j * TS_ + lane];
+            // sa[j][lane] for j < i already holds T[j][lane] (T[j][m] = 0 for m > j)
+            __builtin_amdgcn_wave_barrier();
+            const float tv = lane < i ? acc : (lane == i ? 1.f : 0.f);
+            sa[i * TS_ + lane] = tv;
+            __builtin_amdgcn_wave_barrier();
+            tm[i * GC + lane] = tv;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__ q,
+                                                       const float* __restrict__ k,
+                                                       const float* __restrict__ v,
+                                                       const float* __restrict__ beta,
+                                                       float* __restrict__ state,
+                                                       float* __restrict__ out, int n_tok,
+                                                       int hk, int hv, GdnWs w) {
+    __shared__ __attribute__((aligned(16))) float sk[GC * KS_];
+    __shared__ __attribute__((aligned(16))) float sq[GC * KS_];
+    __shared__ __attribute__((aligned(16))) float st_[GC * TS_];      // T
+    __shared__ __attribute__((aligned(16))) float sm[GC * TS_];       // M
+    __shared__ __attribute__((aligned(16))) float sst[SCOLS * KS_];   // S^T [16][128]
+    __shared__ __attribute__((aligned(16))) float srt[SCOLS * TS_];   // R^T
+    __shared__ __attribute__((aligned(16))) float sdt[SCOLS * TS_];   // Delta^T
+    __shared__ __attribute__((aligned(16))) float sdp[SCOLS * TS_];   // (gamma_C/gamma) Delta, ^T
+    __shared__ float slg[GC], sb[GC];
+    // blockIdx.x = tile * hv + vh: with hv a multiple of 8 the tiles of one
+    // head share an XCD (and its L2) under round-robin dispatch.
+    const int vh = blockIdx.x % hv, tile = blockIdx.x / hv, kh = vh % hk;
+    const int c0 = tile * SCOLS;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ln = lane & 15, g4 = lane >> 4;
+    const int n_chunks = (n_tok + GC - 1) / GC;
+    float* S = state + (size_t)vh * DK * DV;
+
+    // S^T tile from the state (row k, column c0 + c)
+    for (int e = tid; e < SCOLS * DK; e += 256) {
+        const int c = e % SCOLS, row = e / SCOLS;
+        sst[c * KS_ + row] = S[(size_t)row * DV + c0 + c];
+    }
+
+    // chunk data staged in registers (prefetch of the next chunk)
+    f32x4 pq[8], pk[8];
+    f32x4 pt[4], pm[4];
+    float pv[4], plg = 0.f, pb = 0.f;
+    auto fetch = [&](int n) {
+        const int t0 = n * GC;
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int e = tid + 256 * it;
+            const int row = e / (DK / 4), c4 = e % (DK / 4);
+            const int t = t0 + row;
+            f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+            if (t < n_tok) {
+                const float iq = w.rq[(size_t)t * hk + kh], ik = w.rk[(size_t)t * hk + kh];
+                a = *reinterpret_cast<const f32x4*>(q + ((size_t)t * hk + kh) * DK + 4 * c4) * iq;
+                b = *reinterpret_cast<const f32x4*>(k + ((size_t)t * hk + kh) * DK + 4 * c4) * ik;
+            }
+            pq[it] = a;
+            pk[it] = b;
+        }
+        const float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
+        const float* mm = w.mm + ((size_t)n * hv + vh) * GC * GC;
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int e = tid + 256 * it;
+            pt[it] = *reinterpret_cast<const f32x4*>(tm + 4 * e);
+            pm[it] = *reinterpret_cast<const f32x4*>(mm + 4 * e);
+        }
+        // V tile in the MFMA C layout of wave `wave`: rows 16w + 4g + r, column ln
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 16 * wave + 4 * g4 + r;
+            pv[r] = t < n_tok ? v[((size_t)t * hv + vh) * DV + c0 + ln] : 0.f;
+        }
+        if (tid < GC) {
+            plg = w.lg[((size_t)n * hv + vh) * GC + tid];
+            const int t = t0 + tid;
+            pb = t < n_tok ? beta[(size_t)t * hv + vh] : 0.f;
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int e = tid + 256 * it;
+            const int row = e / (DK / 4), c4 = e % (DK / 4);
+            *reinterpret_cast<f32x4*>(sq + row * KS_ + 4 * c4) = pq[it];
+            *reinterpret_cast<f32x4*>(sk + row * KS_ + 4 * c4) = pk[it];
+        }
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int e = tid + 256 * it;
+            const int row = (4 * e) / GC, c = (4 * e) % GC;
+            *reinterpret_cast<f32x4*>(st_ + row * TS_ + c) = pt[it];
+            *reinterpret_cast<f32x4*>(sm + row * TS_ + c) = pm[it];
+        }
+        if (tid < GC) {
+            slg[tid] = plg;
+            sb[tid] = pb;
+        }
+    };
+
+    float vcur[4];
+    fetch(0);
+    stage();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vcur[r] = pv[r];
+    __syncthreads();
+    for (int n = 0; n < n_chunks; ++n) {
+        const int t0 = n * GC;
+        if (n + 1 < n_chunks) fetch(n + 1);
+        const float lgC = slg[GC - 1];
+        // KS and QS rows 16w.. of this wave
+        f32x4 ks = {0.f, 0.f, 0.f, 0.f}, qs = ks;
+        ks = tile_mm(sk, KS_, 16 * wave, sst, KS_, 0, DK / 16, ks);
+        qs = tile_mm(sq, KS_, 16 * wave, sst, KS_, 0, DK / 16, qs);
+        // R = beta (V - gamma KS), written transposed
+        {
+            f32x4 rv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * wave + 4 * g4 + r;
+                rv[r] = sb[i] * (vcur[r] - expf(slg[i]) * ks[r]);
+            }
+            *reinterpret_cast<f32x4*>(srt + ln * TS_ + 16 * wave + 4 * g4) = rv;
+        }
+        __syncthreads();
+        // Delta = T R (T lower triangular: column blocks <= wave)
+        f32x4 dl = {0.f, 0.f, 0.f, 0.f};
+        dl = tile_mm(st_, TS_, 16 * wave, srt, TS_, 0, wave + 1, dl);
+        {
+            f32x4 dp;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * wave + 4 * g4 + r;
+                dp[r] = expf(lgC - slg[i]) * dl[r];
+            }
+            *reinterpret_cast<f32x4*>(sdt + ln * TS_ + 16 * wave + 4 * g4) = dl;
+            *reinterpret_cast<f32x4*>(sdp + ln * TS_ + 16 * wave + 4 * g4) = dp;
+        }
+        __syncthreads();
+        // O = gamma QS + M Delta
+        f32x4 o = {0.f, 0.f, 0.f, 0.f};
+        o = tile_mm(sm, TS_, 16 * wave, sdt, TS_, 0, wave + 1, o);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = 16 * wave + 4 * g4 + r;
+            const int t = t0 + i;
+            if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = expf(slg[i]) * qs[r] + o[r];
+        }
+        // S^T' = exp(lgC) S^T + Dp^T K : wave w owns state rows 32w .. 32w+31
+        const float gC = expf(lgC);
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            const int row0 = 32 * wave + 16 * blk;
+            f32x4 acc;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = gC * sst[(4 * g4 + r) * KS_ + row0 + ln];
+            for (int s = 0; s < GC / 16; ++s) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(sdp + ln * TS_ + 16 * s + 4 * g4);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc = mfma4(a[r], sk[(16 * s + 4 * g4 + r) * KS_ + row0 + ln], acc);
+            }
+            // every wave read S^T for KS/QS before the first barrier; rows
+            // row0.. of S^T are only touched by this wave from here on
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sst[(4 * g4 + r) * KS_ + row0 + ln] = acc[r];
+        }
+        __syncthreads();
+        if (n + 1 < n_chunks) {
+            stage();
+#pragma unroll
+            for (int r = 0; r < 4; ++r) vcur[r] = pv[r];
+        }
+        __syncthreads();
+    }
+    for (int e = tid; e < SCOLS * DK; e += 256) {
+        const int c = e % SCOLS, row = e / SCOLS;
+        S[(size_t)row * DV + c0 + c] = sst[c * KS_ + row];
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gdn_gates(const float* beta_raw, const float* a_raw, const float* ssm_a,
@@ -134,12 +456,30 @@ hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, con
     return hipGetLastError();
 }
 
-size_t gdn_prefill_ws_floats(int32_t, int32_t, int32_t) { return 0; }
+size_t gdn_prefill_ws_floats(int32_t n_tok, int32_t n_k_heads, int32_t n_v_heads, int32_t chunk) {
+    const size_t nc = (size_t)(n_tok + chunk - 1) / chunk;
+    return 2 * (size_t)n_tok * n_k_heads + 2 * nc * n_v_heads * GC * GC + nc * n_v_heads * GC;
+}
 
-hipError_t launch_gdn_prefill(const float*, const float*, const float*, const float*,
-                              const float*, float*, float*, int32_t, int32_t, int32_t, int32_t,
-                              const GdnWorkspace&, hipStream_t) {
-    return hipErrorNotSupported;
+hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, const float* beta,
+                              const float* g, float* state, float* out, int32_t n_tok,
+                              int32_t n_k_heads, int32_t n_v_heads, int32_t chunk,
+                              const GdnWorkspace& ws, hipStream_t s) {
+    if (chunk != GC) return hipErrorInvalidValue;
+    const size_t nc = (size_t)(n_tok + GC - 1) / GC;
+    GdnWs w;
+    w.rq = ws.buf;
+    w.rk = w.rq + (size_t)n_tok * n_k_heads;
+    w.tm = w.rk + (size_t)n_tok * n_k_heads;
+    w.mm = w.tm + nc * n_v_heads * GC * GC;
+    w.lg = w.mm + nc * n_v_heads * GC * GC;
+    hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)nc, n_v_heads), dim3(256), 0, s, q, k, beta, g,
+                       n_tok, n_k_heads, n_v_heads, w);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(n_v_heads * (DV / SCOLS)), dim3(256), 0, s, q, k, v,
+                       beta, state, out, n_tok, n_k_heads, n_v_heads, w);
+    return hipGetLastError();
 }
 
 }  // namespace pi

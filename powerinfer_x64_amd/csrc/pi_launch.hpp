@@ -93,7 +93,7 @@ struct GdnWorkspace {
     float* buf;
     size_t capacity;  // floats
 };
-size_t gdn_prefill_ws_floats(int32_t n_tok, int32_t n_v_heads, int32_t chunk);
+size_t gdn_prefill_ws_floats(int32_t n_tok, int32_t n_k_heads, int32_t n_v_heads, int32_t chunk);
 hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, const float* beta,
                               const float* g, float* state, float* out, int32_t n_tok,
                               int32_t n_k_heads, int32_t n_v_heads, int32_t chunk,

@@ -96,3 +96,62 @@ def test_gdn_decode_zero_state_closed_form():
         kk = k[0, h % HK].astype(np.float64)
         qk = (qq / np.linalg.norm(qq) / np.sqrt(DK)) @ (kk / np.linalg.norm(kk))
         np.testing.assert_allclose(out[h], beta[0, h] * qk * v[0, h], atol=1e-5)
+
+
+@pytest.mark.parametrize("t", [1, 63, 64, 65, 200, 1024])
+def test_gdn_prefill_matches_oracle(t):
+    """Chunked (64-token) prefill == the reference's per-token recurrence."""
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(1000 + t)
+    q, k, v, beta, g = _inputs(rng, t)
+    s0 = (0.2 * rng.standard_normal((HV, DK, DV))).astype(np.float32) if t % 2 else \
+        np.zeros((HV, DK, DV), np.float32)
+    ref_out, ref_state = orc.gdn_tokens(q, k, v, beta, g, state=s0)
+    state = to_dev(s0)
+    out = rt.gdn_prefill(dev, to_dev(q), to_dev(k), to_dev(v), to_dev(beta), to_dev(g), state)
+    torch.cuda.synchronize()
+    assert np.abs(out.cpu().numpy() - ref_out).max() <= 2e-3
+    assert np.abs(state.cpu().numpy() - ref_state).max() <= 2e-3
+
+
+def test_gdn_prefill_strong_decay_and_zero_beta():
+    """Edge gates: g -> -1e4 (state reset each token) and beta = 0 (pure decay)."""
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(77)
+    t = 130
+    q, k, v, beta, g = _inputs(rng, t)
+    g[::3] = -1e4
+    beta[1::5] = 0.0
+    s0 = (0.2 * rng.standard_normal((HV, DK, DV))).astype(np.float32)
+    ref_out, ref_state = orc.gdn_tokens(q, k, v, beta, g, state=s0)
+    state = to_dev(s0)
+    out = rt.gdn_prefill(dev, to_dev(q), to_dev(k), to_dev(v), to_dev(beta), to_dev(g), state)
+    torch.cuda.synchronize()
+    assert np.abs(out.cpu().numpy() - ref_out).max() <= 2e-3
+    assert np.abs(state.cpu().numpy() - ref_state).max() <= 2e-3
+
+
+def test_c5_gdn_prefill_4096_then_256_decode():
+    """Config 5: chunked prefill of 4096 tokens, then 256 recurrent decode steps,
+    continuing the same state; outputs and final state vs the oracle."""
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(0x5EED0004)
+    tp, td = 4096, 256
+    q, k, v, beta, g = _inputs(rng, tp + td)
+    ref_out, ref_state = orc.gdn_tokens(q, k, v, beta, g)
+    state = torch.zeros((HV, DK, DV), device="cuda")
+    out_p = rt.gdn_prefill(dev, to_dev(q[:tp]), to_dev(k[:tp]), to_dev(v[:tp]),
+                           to_dev(beta[:tp]), to_dev(g[:tp]), state)
+    st = state[None]
+    outs = []
+    for i in range(tp, tp + td):
+        o = rt.gdn_decode(dev, to_dev(q[i][None]), to_dev(k[i][None]), to_dev(v[i][None]),
+                          to_dev(beta[i][None]), to_dev(g[i][None]), st)
+        outs.append(o[0])
+    torch.cuda.synchronize()
+    out = np.concatenate([out_p.cpu().numpy(), torch.stack(outs).cpu().numpy()])
+    assert np.abs(out - ref_out).max() <= 2e-3
+    assert np.abs(st[0].cpu().numpy() - ref_state).max() <= 2e-3
