@@ -45,7 +45,7 @@ def _args():
                    help="budget of the single-core CPU baseline sample")
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--workload", default=None,
-                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill"],
+                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "copy"],
                    help="time one workload only and print its figures (for sweeps)")
     return p.parse_args()
 
@@ -273,15 +273,35 @@ def bench_gdn_prefill(torch, rt, dev, timer, steps, warmup, t=4096):
             "bytes_per_launch": algo, "flops_per_launch": flops}
 
 
-def _traffic(name):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
-    p = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
-    if os.path.exists(p):
-        try:
-            return json.load(open(p)).get("bytes_per_launch")
-        except Exception:
-            return None
-    return None
+def bench_copy(torch, timer, steps, warmup, nbytes=1 << 30):
+    """A plain device copy of known size: the calibration kernel for the
+    FETCH_SIZE / WRITE_SIZE counters, and the practical HBM ceiling."""
+    src = torch.randn(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    t = timer.run(lambda: dst.copy_(src), steps, warmup)
+    moved = 2 * nbytes
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "ms_per_step": t["ms_avg"],
+            "GB_s": moved / (t["ms_avg"] * 1e-3) / 1e9,
+            "hbm_frac": moved / (t["ms_avg"] * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def _traffic(summary, kernels):
+    """HBM bytes per launch (read + write, copy-calibrated FETCH_SIZE / WRITE_SIZE)
+    summed over `kernels`, from the committed rocprofv3 PMC table in
+    profiles/<summary>.txt; None when the summary has no such table."""
+    p = os.path.join(ROOT, "profiles", f"{summary}.txt")
+    if not os.path.exists(p):
+        return None
+    total, seen, in_table = 0, set(), False
+    for line in open(p):
+        f = line.split()
+        if f[:3] == ["kernel", "FETCH_KiB", "WRITE_KiB"]:
+            in_table = True
+            continue
+        if in_table and len(f) == 5 and f[0] in kernels:
+            total += int(float(f[3])) + int(float(f[4]))
+            seen.add(f[0])
+    return total if seen == set(kernels) else None
 
 
 def _single(torch, rt, dev, timer, a):
@@ -304,6 +324,8 @@ def _single(torch, rt, dev, timer, a):
         return bench_prefill(torch, rt, dev, timer, 4096, 32, 8, 128, 1e6, 0x5EED0002, st, wu)
     if w == "gdn_prefill":
         return bench_gdn_prefill(torch, rt, dev, timer, st, wu)
+    if w == "copy":
+        return bench_copy(torch, timer, st, wu)
     return bench_gdn_decode(torch, rt, dev, timer, st, wu)
 
 
@@ -354,7 +376,8 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(c2["GB_s"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(c2["hbm_frac"], 4),
-                     "traffic": _traffic("decode_c2")},
+                     "traffic": _traffic("decode_kernel_c2",
+                                         ["decode_kernel<f16,128,2>", "decode_merge_kernel"])},
         "cpu_baseline": {k: (round(v, 4) if isinstance(v, float) else v)
                          for k, v in cpu.items()},
     }

@@ -523,7 +523,9 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
         case 128: per_cu = hp ? wgs_per_cu<f16, 128>() : wgs_per_cu<float, 128>(); break;
         default: per_cu = wgs_per_cu<f16, 256>(); break;
     }
-    plan.grid = cus * per_cu;
+    // A segment splits into at most grid + 1 runs; the merge kernel stages
+    // kMaxRuns of them in LDS, so the grid stays below that.
+    plan.grid = std::min(cus * per_cu, kMaxRuns - 1);
     if (const char* e = std::getenv("PI_DECODE_GRID")) {
         const int v = std::atoi(e);
         if (v >= 1 && v < kMaxRuns) plan.grid = v;
