@@ -9,7 +9,10 @@ from __future__ import annotations
 import ctypes
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpi_attn.so")
+# PI_ATTN_LIB names another build of the same library (an A/B comparison of
+# two builds); by default the in-tree build is loaded.
+LIB_PATH = os.environ.get("PI_ATTN_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libpi_attn.so")
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -4,7 +4,7 @@
 // Error behaviour mirrors the reference's offload seam: every failure is a
 // status code plus text (Some(Err(String)) in src/cuda/mod.rs:527-537), never
 // an exception or an abort across the ABI.
-#include "../../include/pi_attn.h"
+#include "pi_attn.h"
 #include "pi_launch.hpp"
 
 #include <hip/hip_runtime.h>
