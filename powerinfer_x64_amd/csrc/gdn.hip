@@ -153,6 +153,16 @@ __device__ __forceinline__ f32x4 tile_mm(const float* X, int xs, int row0, const
     return acc;
 }
 
+// C += X . Y for 16x16 f32 blocks in LDS (row-major, strides xs / ys).  Lane
+// l: A operand X[l%16][k], B operand Y[k][l%16], k = 4s + l/16; returns the
+// lane's C[4*(l/16) + r][l%16], r = 0..3.
+__device__ __forceinline__ f32x4 mm16(const float* X, int xs, const float* Y, int ys, f32x4 acc) {
+    const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc = mfma4(X[i * xs + 4 * s + g], Y[(4 * s + g) * ys + i], acc);
+    return acc;
+}
+
 struct GdnWs {
     float* rq;  // [T][Hk] 1/max(|q|,1e-12) * 1/sqrt(Dk)
     float* rk;  // [T][Hk] 1/max(|k|,1e-12)
@@ -168,7 +178,9 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(const float* __restrict__
                                                        int hk, int hv, GdnWs w) {
     __shared__ __attribute__((aligned(16))) float sk[GC * KS_];
     __shared__ __attribute__((aligned(16))) float sq[GC * KS_];
-    __shared__ __attribute__((aligned(16))) float sa[GC * TS_];  // A, then T
+    __shared__ __attribute__((aligned(16))) float sa[GC * TS_];  // A
+    __shared__ __attribute__((aligned(16))) float st[GC * TS_];  // T = (I + A)^-1
+    __shared__ __attribute__((aligned(16))) float sx[4 * 16 * TS_];  // per-wave 16x16 scratch
     __shared__ float slg[GC], sb[GC];
     const int n = blockIdx.x, vh = blockIdx.y, kh = vh % hk;
     const int t0 = n * GC;
@@ -244,23 +256,46 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(const float* __restrict__
             for (int r = 0; r < 4; ++r) mm[(16 * jb + ln) * GC + 16 * ib + 4 * lg4 + r] = 0.f;
     }
     __syncthreads();
-    // T = (I + A)^-1 by forward substitution (one wavefront, lane = column):
-    // T[i][m] = -sum_{m <= j < i} A[i][j] T[j][m]  (T[i][i] = 1)
-    if (wave == 0) {
-        float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
-        // sa rows are read as A and overwritten in place with T, row by row
-        float trow_prev[1];
-        (void)trow_prev;
-        for (int i = 0; i < GC; ++i) {
-            float acc = 0.f;
-            for (int j = lane; j < i; ++j) acc -= sa[i * TS_ + j] * sa[j * TS_ + lane];
-            // sa[j][lane] for j < i already holds T[j][lane] (T[j][m] = 0 for m > j)
-            __builtin_amdgcn_wave_barrier();
-            const float tv = lane < i ? acc : (lane == i ? 1.f : 0.f);
-            sa[i * TS_ + lane] = tv;
-            __builtin_amdgcn_wave_barrier();
-            tm[i * GC + lane] = tv;
+    // T = (I + A)^-1, A strictly lower triangular, by 16x16 blocks:
+    //   T_ii = (I + A_ii)^-1                      (forward substitution, wave i)
+    //   T_ij = -T_ii . sum_{j <= k < i} A_ik T_kj  (i > j, by block distance)
+    for (int e = tid; e < GC * GC; e += 256) st[(e / GC) * TS_ + (e % GC)] = 0.f;
+    __syncthreads();
+    if (lane < 16) {
+        // lane m holds column m of T_ww: t[i] = d_im - sum_{j < i} A[i][j] t[j]
+        const float* ab = sa + 16 * wave * TS_ + 16 * wave;
+        float t[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float acc = i == lane ? 1.f : 0.f;
+#pragma unroll
+            for (int j = 0; j < i; ++j) acc -= ab[i * TS_ + j] * t[j];
+            t[i] = acc;
+            st[(16 * wave + i) * TS_ + 16 * wave + lane] = acc;
         }
+    }
+    __syncthreads();
+    float* sxw = sx + wave * 16 * TS_;  // this wave's 16x16 scratch
+    for (int d = 1; d < 4; ++d) {
+        if (wave < 4 - d) {
+            const int j = wave, i = wave + d;
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            for (int kb = j; kb < i; ++kb)
+                x = mm16(sa + 16 * i * TS_ + 16 * kb, TS_, st + 16 * kb * TS_ + 16 * j, TS_, x);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sxw[(4 * lg4 + r) * TS_ + ln] = x[r];
+            __builtin_amdgcn_wave_barrier();
+            f32x4 y = {0.f, 0.f, 0.f, 0.f};
+            y = mm16(st + 16 * i * TS_ + 16 * i, TS_, sxw, TS_, y);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) st[(16 * i + 4 * lg4 + r) * TS_ + 16 * j + ln] = -y[r];
+        }
+        __syncthreads();
+    }
+    float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
+    for (int e = tid; e < GC * GC / 4; e += 256) {
+        const int row = e / (GC / 4), c4 = e % (GC / 4);
+        *reinterpret_cast<f32x4*>(tm + row * GC + 4 * c4) = *reinterpret_cast<const f32x4*>(st + row * TS_ + 4 * c4);
     }
 }
 
