@@ -91,7 +91,8 @@ int pi_kv_read(pi_handle h, pi_kv_pool pool, const int32_t* d_page_table, int32_
 
 /* ---- decode prologue -------------------------------------------------------
  * Per-head RMSNorm in place (ops::rms_norm, src/ops.rs:13-27, as called at
- * src/model/mod.rs:1035-1070): rows of `dim` values at stride `row_stride`. */
+ * src/model/mod.rs:1035-1070): rows of `dim` values (any dim) at stride
+ * `row_stride`. */
 int pi_head_rmsnorm(pi_handle h, float* d_x, const float* d_w, int32_t n_rows, int32_t dim,
                     int32_t row_stride, float eps, void* stream);
 /* RoPE in place on q [n_tok][n_q_heads][head_dim] and k [n_tok][n_kv_heads][head_dim]
@@ -153,9 +154,36 @@ int pi_gdn_prefill(pi_handle h, const float* d_q, const float* d_k, const float*
 
 /* ---- host-slice drop-ins (synchronous) ---------------------------------------
  * ops::attention_head (src/ops.rs:213-247) with host slices: copies in,
- * runs the decode kernel, copies out.  k/v caches [seq_len][head_dim]. */
+ * runs the decode kernel, copies out.  k/v caches [seq_len][head_dim],
+ * head_dim 1..128 (rows are zero-padded to the kernel's 64 or 128; the scale
+ * stays 1/sqrt(head_dim)). */
 int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const float* h_k_cache,
                           const float* h_v_cache, size_t seq_len, size_t head_dim);
+/* ops::rms_norm (src/ops.rs:13-27): out = x * (1/sqrt(sum(x^2)/n + eps)) * w, n values. */
+int pi_ops_rms_norm(pi_handle h, float* h_out, const float* h_x, const float* h_w, size_t n,
+                    float eps);
+/* ops::softmax (src/ops.rs:160-180), in place; n == 0 is a no-op. */
+int pi_ops_softmax(pi_handle h, float* h_x, size_t n);
+/* ops::apply_rope (src/ops.rs:35-67): one q head and one k head in place,
+ * adjacent pairs (2i, 2i+1) for i < rope_dim/2 with 2i+1 < head_dim. */
+int pi_ops_apply_rope(pi_handle h, float* h_q, float* h_k, size_t position, size_t head_dim,
+                      size_t rope_dim, float base_freq);
+/* ops::apply_rope_with_freqs (src/ops.rs:130-157): NeoX pairs (i, i+n_freqs). */
+int pi_ops_apply_rope_with_freqs(pi_handle h, float* h_q, float* h_k, size_t position,
+                                 size_t head_dim, const float* h_freqs, size_t n_freqs);
+/* ops::compute_imrope_freqs (src/ops.rs:78-122), host only: writes n_rot/2
+ * values theta_scale^k by repeated f32 multiplication.  `sections` is the
+ * reference's argument; for text (all position tracks equal) it does not
+ * change the values.  Errors are reported through pi_last_error(NULL). */
+int pi_compute_imrope_freqs(float base, size_t n_rot, const int32_t* sections, float* out);
+/* One gated-delta step on host slices (src/model/mod.rs:841-916 for one
+ * token): q/k raw [n_k_heads][k_hd], v [n_v_heads][v_hd], beta/g [n_v_heads],
+ * state [n_v_heads][k_hd][v_hd] in/out (ssm::create_ssm_state layout,
+ * src/ssm/mod.rs:164-166), out [n_v_heads][v_hd]. */
+int pi_ssm_gated_delta_step(pi_handle h, float* h_out, float* h_state, const float* h_q,
+                            const float* h_k, const float* h_v, const float* h_beta,
+                            const float* h_g, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
+                            int32_t v_hd);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,218 @@
+// pi_ops.hpp -- C++ mirror of PowerInfer_x64's attention / SSM call signatures
+// over the C ABI in pi_attn.h (header-only, C++20).
+//
+// The reference is Rust; this header keeps its function names, argument order
+// and meaning so a C++ caller (or a test written like the reference's own
+// #[test]s) reads the same:
+//   powerinfer::ops  -- src/ops.rs: rms_norm, apply_rope, compute_imrope_freqs,
+//                       apply_rope_with_freqs, softmax, attention_head
+//   powerinfer::ssm  -- src/ssm/mod.rs: create_ssm_state, plus the gated-delta
+//                       step of src/model/mod.rs:841-916
+//   powerinfer::rocm -- the offload seam of src/cuda/mod.rs:373-537:
+//                       Device::init() -> std::optional (None = CPU path) and
+//                       try_* calls -> std::optional<Result> (Option<Result<(),
+//                       String>>).
+// The ops / ssm free functions run on the calling thread's default device and
+// throw BackendError where the reference would panic (a size mismatch, its
+// debug_assert_eq!) or where the device fails.
+#pragma once
+
+#include "pi_attn.h"
+
+#include <array>
+#include <cstddef>
+#include <cstdint>
+#include <optional>
+#include <span>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace powerinfer {
+
+// src/runtime/mod.rs:6-18 (BackendError), keyed by pi_status.
+enum class ErrorKind : int {
+    InvalidArgument = PI_ERR_INVALID_ARG,
+    OutOfMemory = PI_ERR_OUT_OF_MEMORY,
+    InvalidKernel = PI_ERR_INVALID_KERNEL,
+    Device = PI_ERR_DEVICE,
+    Unsupported = PI_ERR_UNSUPPORTED,
+};
+
+class BackendError : public std::runtime_error {
+public:
+    BackendError(int status, std::string msg)
+        : std::runtime_error(std::move(msg)), kind_(static_cast<ErrorKind>(status)) {}
+    ErrorKind kind() const { return kind_; }
+
+private:
+    ErrorKind kind_;
+};
+
+// Result<(), String>: ok() or the error text (with its status class).
+struct Result {
+    int status = PI_OK;
+    std::string message;
+    bool ok() const { return status == PI_OK; }
+};
+
+namespace rocm {
+
+// One pi_handle bound to a GPU (GpuResources / GpuDevice, src/cuda/mod.rs:141-460).
+class Device {
+public:
+    // GpuResources::init: None when no gfx950 device can be opened (the caller
+    // then takes the CPU path, src/model/mod.rs:373-375).
+    static std::optional<Device> init(int device = 0) {
+        pi_handle h = nullptr;
+        if (pi_create(device, &h) != PI_OK) return std::nullopt;
+        return Device(h);
+    }
+    // Text of the last pi_create failure on this thread.
+    static std::string init_error() { return pi_last_error(nullptr); }
+
+    Device(Device&& o) noexcept : h_(std::exchange(o.h_, nullptr)) {}
+    Device& operator=(Device&& o) noexcept {
+        if (this != &o) {
+            pi_destroy(h_);
+            h_ = std::exchange(o.h_, nullptr);
+        }
+        return *this;
+    }
+    Device(const Device&) = delete;
+    Device& operator=(const Device&) = delete;
+    ~Device() { pi_destroy(h_); }
+
+    pi_handle raw() const { return h_; }
+    Result result(int rc) const { return rc == PI_OK ? Result{} : Result{rc, pi_last_error(h_)}; }
+    void check(int rc) const {
+        if (rc != PI_OK) throw BackendError(rc, pi_last_error(h_));
+    }
+
+    // The seams (Option<Result<(), String>>): always Some on a live device.
+    std::optional<Result> try_attention_head(std::span<float> out, std::span<const float> q,
+                                             std::span<const float> k_cache,
+                                             std::span<const float> v_cache, size_t seq_len,
+                                             size_t head_dim) const {
+        if (out.size() < head_dim || q.size() < head_dim || k_cache.size() < seq_len * head_dim ||
+            v_cache.size() < seq_len * head_dim)
+            return Result{PI_ERR_INVALID_ARG, "attention_head: slice shorter than seq_len * head_dim"};
+        return result(pi_ops_attention_head(h_, out.data(), q.data(), k_cache.data(),
+                                            v_cache.data(), seq_len, head_dim));
+    }
+    std::optional<Result> try_gated_delta_step(std::span<float> out, std::span<float> state,
+                                               std::span<const float> q, std::span<const float> k,
+                                               std::span<const float> v,
+                                               std::span<const float> beta,
+                                               std::span<const float> g, size_t n_k_heads,
+                                               size_t n_v_heads, size_t k_hd, size_t v_hd) const {
+        if (q.size() != n_k_heads * k_hd || k.size() != q.size() || v.size() != n_v_heads * v_hd ||
+            out.size() != v.size() || beta.size() != n_v_heads || g.size() != n_v_heads ||
+            state.size() != n_v_heads * k_hd * v_hd)
+            return Result{PI_ERR_INVALID_ARG, "gated_delta_step: slice sizes do not match the heads"};
+        return result(pi_ssm_gated_delta_step(h_, out.data(), state.data(), q.data(), k.data(),
+                                              v.data(), beta.data(), g.data(), (int32_t)n_k_heads,
+                                              (int32_t)n_v_heads, (int32_t)k_hd, (int32_t)v_hd));
+    }
+
+private:
+    explicit Device(pi_handle h) : h_(h) {}
+    pi_handle h_ = nullptr;
+};
+
+// The calling thread's default device (device 0), opened on first use.
+inline Device& current() {
+    thread_local std::optional<Device> dev = Device::init(0);
+    if (!dev) throw BackendError(PI_ERR_DEVICE, Device::init_error());
+    return *dev;
+}
+
+}  // namespace rocm
+
+namespace detail {
+inline void require(bool ok, const char* what) {
+    if (!ok) throw BackendError(PI_ERR_INVALID_ARG, what);
+}
+}  // namespace detail
+
+namespace ops {
+
+// src/ops.rs:13-27
+inline void rms_norm(std::span<float> out, std::span<const float> x, std::span<const float> weight,
+                     float eps) {
+    detail::require(out.size() == x.size() && weight.size() == x.size(), "rms_norm: length mismatch");
+    if (x.empty()) return;
+    auto& d = rocm::current();
+    d.check(pi_ops_rms_norm(d.raw(), out.data(), x.data(), weight.data(), x.size(), eps));
+}
+
+// src/ops.rs:35-67 (one q head and one k head, adjacent pairs)
+inline void apply_rope(std::span<float> q, std::span<float> k, size_t position, size_t head_dim,
+                       size_t rope_dim, float base_freq) {
+    detail::require(q.size() >= head_dim && k.size() >= head_dim, "apply_rope: slice shorter than head_dim");
+    auto& d = rocm::current();
+    d.check(pi_ops_apply_rope(d.raw(), q.data(), k.data(), position, head_dim, rope_dim, base_freq));
+}
+
+// src/ops.rs:78-122
+inline std::vector<float> compute_imrope_freqs(float base_freq, size_t n_rot,
+                                               const std::array<int32_t, 4>& sections) {
+    std::vector<float> f(n_rot / 2);
+    const int rc = pi_compute_imrope_freqs(base_freq, n_rot, sections.data(), f.data());
+    if (rc != PI_OK) throw BackendError(rc, pi_last_error(nullptr));
+    return f;
+}
+
+// src/ops.rs:130-157 (NeoX pairs (i, i + freqs.len()))
+inline void apply_rope_with_freqs(std::span<float> q, std::span<float> k, size_t position,
+                                  size_t head_dim, std::span<const float> freqs) {
+    detail::require(q.size() >= head_dim && k.size() >= head_dim,
+                    "apply_rope_with_freqs: slice shorter than head_dim");
+    auto& d = rocm::current();
+    d.check(pi_ops_apply_rope_with_freqs(d.raw(), q.data(), k.data(), position, head_dim,
+                                         freqs.data(), freqs.size()));
+}
+
+// src/ops.rs:160-180
+inline void softmax(std::span<float> x) {
+    if (x.empty()) return;
+    auto& d = rocm::current();
+    d.check(pi_ops_softmax(d.raw(), x.data(), x.size()));
+}
+
+// src/ops.rs:213-247
+inline void attention_head(std::span<float> out, std::span<const float> q,
+                           std::span<const float> k_cache, std::span<const float> v_cache,
+                           size_t seq_len, size_t head_dim) {
+    auto& d = rocm::current();
+    const Result r = *d.try_attention_head(out, q, k_cache, v_cache, seq_len, head_dim);
+    if (!r.ok()) throw BackendError(r.status, r.message);
+}
+
+}  // namespace ops
+
+namespace ssm {
+
+// src/ssm/mod.rs:164-166: a zeroed [d_state * d_inner] state.  For a Qwen3.5
+// gated-DeltaNet layer d_state * d_inner = n_v_heads * k_hd * v_hd, laid out
+// [n_v_heads][k_hd][v_hd] (src/model/mod.rs:877-916).
+inline std::vector<float> create_ssm_state(size_t d_state, size_t d_inner) {
+    return std::vector<float>(d_state * d_inner, 0.0f);
+}
+
+// One token of the gated delta rule (src/model/mod.rs:841-916): q/k raw (the
+// L2 norm and the 1/sqrt(k_hd) q scale are applied inside), beta and g
+// per V head, state updated in place, out = S^T q before RMSNormGated.
+inline void gated_delta_step(std::span<float> out, std::span<float> state, std::span<const float> q,
+                             std::span<const float> k, std::span<const float> v,
+                             std::span<const float> beta, std::span<const float> g,
+                             size_t n_k_heads, size_t n_v_heads, size_t k_hd, size_t v_hd) {
+    auto& d = rocm::current();
+    const Result r =
+        *d.try_gated_delta_step(out, state, q, k, v, beta, g, n_k_heads, n_v_heads, k_hd, v_hd);
+    if (!r.ok()) throw BackendError(r.status, r.message);
+}
+
+}  // namespace ssm
+}  // namespace powerinfer

@@ -44,6 +44,13 @@ SIGNATURES = {
     "pi_gdn_prefill": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                               _i32, _i32, _vp]),
     "pi_ops_attention_head": (_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz]),
+    "pi_ops_rms_norm": (_int, [_vp, _vp, _vp, _vp, _sz, _f32]),
+    "pi_ops_softmax": (_int, [_vp, _vp, _sz]),
+    "pi_ops_apply_rope": (_int, [_vp, _vp, _vp, _sz, _sz, _sz, _f32]),
+    "pi_ops_apply_rope_with_freqs": (_int, [_vp, _vp, _vp, _sz, _sz, _vp, _sz]),
+    "pi_compute_imrope_freqs": (_int, [_f32, _sz, _vp, _vp]),
+    "pi_ssm_gated_delta_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
+                                       _i32]),
 }
 
 _lib = None

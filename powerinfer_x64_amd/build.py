@@ -53,7 +53,29 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_cpp_tests(verbose)
     return LIB
+
+
+CPP_TESTS = os.path.join(HERE, "..", "tests", "cpp")
+
+
+def build_cpp_tests(verbose: bool = False) -> None:
+    """The C++ tests of the C ABI / C++ mirror (host code only, linked against
+    the in-tree library through an rpath)."""
+    out_dir = os.path.join(CPP_TESTS, "_build")
+    os.makedirs(out_dir, exist_ok=True)
+    for src in sorted(f for f in os.listdir(CPP_TESTS) if f.endswith(".cpp")):
+        exe = os.path.join(out_dir, src[:-4])
+        cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-Wextra", "-I", os.path.join(HERE, "..", "include"),
+               os.path.join(CPP_TESTS, src), "-L", HERE, "-lpi_attn",
+               "-Wl,-rpath,$ORIGIN/../../../powerinfer_x64_amd", "-o", exe + ".tmp"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"g++ failed on {src}:\n{r.stderr}")
+        os.replace(exe + ".tmp", exe)
+        if verbose:
+            print(f"built {exe}")
 
 
 if __name__ == "__main__":

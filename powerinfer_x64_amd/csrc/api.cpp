@@ -93,6 +93,27 @@ int grow(pi_handle h, T** ptr, size_t* cap, size_t need, hipStream_t s, const ch
     return PI_OK;
 }
 
+// ops::apply_rope (src/ops.rs:45-46): freq_i = 1 / base^(2i/rope_dim) in f32.
+void norm_rope_freqs(float base, int rope_dim, float* f) {
+    for (int i = 0; i < rope_dim / 2; ++i) {
+        const float expo = 2.0f * (float)i / (float)rope_dim;
+        f[i] = 1.0f / powf(base, expo);
+    }
+}
+
+// ops::compute_imrope_freqs (src/ops.rs:78-122): every section track starts at
+// 1 and advances by one f32 multiply by theta_scale = base^(-2/n_rot) per pair,
+// so pair k gets theta_scale^k by repeated multiplication whatever its section
+// (src/model/mod.rs:1080-1083 keeps the first n_rot/2).
+void imrope_freqs(float base, int n_rot, float* f) {
+    const float theta_scale = powf(base, -2.0f / (float)n_rot);
+    float t = 1.0f;
+    for (int i = 0; i < n_rot / 2; ++i) {
+        f[i] = t;
+        t *= theta_scale;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -240,7 +261,7 @@ int pi_head_rmsnorm(pi_handle h, float* d_x, const float* d_w, int32_t n_rows, i
                     int32_t row_stride, float eps, void* stream) {
     PI_CHECK_HANDLE(h);
     if (!d_x || !d_w) return fail(h, PI_ERR_INVALID_ARG, "pi_head_rmsnorm: null argument");
-    if (n_rows < 0 || dim <= 0 || dim > 256 || row_stride < dim)
+    if (n_rows < 0 || dim <= 0 || row_stride < dim)
         return fail(h, PI_ERR_INVALID_ARG, "pi_head_rmsnorm: n_rows=%d dim=%d row_stride=%d", n_rows, dim, row_stride);
     if (n_rows == 0) return PI_OK;
     PI_HIP(h, hipSetDevice(h->device), "pi_head_rmsnorm");
@@ -263,23 +284,10 @@ int pi_rope(pi_handle h, float* d_q, float* d_k, const int32_t* d_pos, int32_t n
     if (n_tok == 0 || n_pairs == 0) return PI_OK;
     pi::RopeFreqs f;
     std::memset(&f, 0, sizeof f);
-    if (h_sections == nullptr) {
-        // ops::apply_rope (src/ops.rs:45-46): freq_i = 1 / base^(2i/rope_dim) in f32.
-        for (int i = 0; i < n_pairs; ++i) {
-            const float expo = 2.0f * (float)i / (float)rd;
-            f.f[i] = 1.0f / powf(base, expo);
-        }
-    } else {
-        // ops::compute_imrope_freqs (src/ops.rs:78-122): every track is
-        // theta_scale^k by repeated f32 multiplication; the first rd/2 are kept
-        // (src/model/mod.rs:1080-1083).
-        const float theta_scale = powf(base, -2.0f / (float)rd);
-        float t = 1.0f;
-        for (int i = 0; i < n_pairs; ++i) {
-            f.f[i] = t;
-            t *= theta_scale;
-        }
-    }
+    if (h_sections == nullptr)
+        norm_rope_freqs(base, rd, f.f);
+    else
+        imrope_freqs(base, rd, f.f);
     PI_HIP(h, hipSetDevice(h->device), "pi_rope");
     PI_HIP(h, pi::launch_rope(d_q, d_k, d_pos, n_tok, n_q_heads, n_kv_heads, head_dim, n_pairs,
                               h_sections ? 1 : 0, f, pick(h, stream)),
@@ -434,18 +442,22 @@ int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const flo
     PI_CHECK_HANDLE(h);
     if (!h_out || !h_q || (seq_len && (!h_k_cache || !h_v_cache)))
         return fail(h, PI_ERR_INVALID_ARG, "attention_head: null slice");
-    if (head_dim != 64 && head_dim != 128)
-        return fail(h, PI_ERR_UNSUPPORTED, "attention_head: head_dim %zu (64/128 on the device)", head_dim);
+    if (head_dim == 0 || head_dim > 128)
+        return fail(h, PI_ERR_UNSUPPORTED, "attention_head: head_dim %zu (1..128 on the device)", head_dim);
     if (seq_len > (size_t)1 << 24) return fail(h, PI_ERR_UNSUPPORTED, "attention_head: seq_len %zu", seq_len);
     PI_HIP(h, hipSetDevice(h->device), "attention_head");
     hipStream_t s = h->stream;
+    // Rows are zero-padded to a kernel head size (64 or 128): zero q and key
+    // dims leave every dot product unchanged, the scale stays 1/sqrt(head_dim),
+    // and the padded output dims are dropped.
+    const size_t pd = head_dim <= 64 ? 64 : 128;
     // One f32 sequence, one head: a pool with ceil(seq_len/16) pages and the identity table.
     const int n_pages = (int)((seq_len + 15) / 16) + 1;
     pi_kv_pool pool = nullptr;
-    int rc = pi_kv_pool_create(h, n_pages, 16, 1, (int)head_dim, PI_F32, &pool);
+    int rc = pi_kv_pool_create(h, n_pages, 16, 1, (int)pd, PI_F32, &pool);
     if (rc) return rc;
-    const size_t kv = seq_len * head_dim;
-    const size_t need = 2 * kv + 2 * head_dim + (size_t)n_pages + 2;
+    const size_t kv = seq_len * pd;
+    const size_t need = 2 * kv + 2 * pd + (size_t)n_pages + 2;
     rc = grow(h, &h->h2d_scratch, &h->h2d_floats, need, s, "attention_head staging", false);
     if (rc) {
         pi_kv_pool_destroy(pool);
@@ -454,8 +466,8 @@ int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const flo
     float* dk = h->h2d_scratch;
     float* dv = dk + kv;
     float* dq = dv + kv;
-    float* dout = dq + head_dim;
-    int32_t* dpt = reinterpret_cast<int32_t*>(dout + head_dim);
+    float* dout = dq + pd;
+    int32_t* dpt = reinterpret_cast<int32_t*>(dout + pd);
     int32_t* dmeta = dpt + n_pages;  // [start_pos=0, ctx_len]
     int32_t* hpt = new (std::nothrow) int32_t[n_pages + 2];
     if (!hpt) {
@@ -465,10 +477,11 @@ int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const flo
     for (int i = 0; i < n_pages; ++i) hpt[i] = i;
     hpt[n_pages] = 0;
     hpt[n_pages + 1] = (int32_t)seq_len;
-    hipError_t e = hipSuccess;
-    if (kv) e = hipMemcpyAsync(dk, h_k_cache, kv * 4, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess && kv) e = hipMemcpyAsync(dv, h_v_cache, kv * 4, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(dq, h_q, head_dim * 4, hipMemcpyHostToDevice, s);
+    const size_t rb = head_dim * 4, pb = pd * 4;
+    hipError_t e = hipMemsetAsync(dk, 0, (2 * kv + pd) * 4, s);
+    if (e == hipSuccess && kv) e = hipMemcpy2DAsync(dk, pb, h_k_cache, rb, rb, seq_len, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && kv) e = hipMemcpy2DAsync(dv, pb, h_v_cache, rb, rb, seq_len, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(dq, h_q, rb, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(dpt, hpt, (n_pages + 2) * 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     delete[] hpt;
@@ -481,12 +494,141 @@ int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const flo
         rc = pi_attn_decode(h, dq, pool, dpt, n_pages, dmeta + 1, 1, 1, PI_GQA_MODULO,
                             1.0f / std::sqrt((float)head_dim), nullptr, dout, s);
     if (!rc) {
-        e = hipMemcpyAsync(h_out, dout, head_dim * 4, hipMemcpyDeviceToHost, s);
+        e = hipMemcpyAsync(h_out, dout, rb, hipMemcpyDeviceToHost, s);
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e != hipSuccess) rc = hip_fail(h, e, "attention_head");
     }
     pi_kv_pool_destroy(pool);
     return rc;
+}
+
+// Synchronous host-slice calls: copy in on the handle's stream, run, copy out.
+static int stage_in(pi_handle h, size_t floats, float** dev) {
+    int rc = grow(h, &h->h2d_scratch, &h->h2d_floats, floats, h->stream, "host-slice staging", false);
+    if (rc) return rc;
+    *dev = h->h2d_scratch;
+    return PI_OK;
+}
+
+static int copy_sync(pi_handle h, void* dst, const void* src, size_t bytes, hipMemcpyKind kind,
+                     const char* what) {
+    if (bytes) PI_HIP(h, hipMemcpyAsync(dst, src, bytes, kind, h->stream), what);
+    return PI_OK;
+}
+
+int pi_ops_rms_norm(pi_handle h, float* h_out, const float* h_x, const float* h_w, size_t n,
+                    float eps) {
+    PI_CHECK_HANDLE(h);
+    if (!h_out || !h_x || !h_w) return fail(h, PI_ERR_INVALID_ARG, "rms_norm: null slice");
+    if (n == 0 || n > (1u << 24)) return fail(h, PI_ERR_INVALID_ARG, "rms_norm: n=%zu", n);
+    PI_HIP(h, hipSetDevice(h->device), "rms_norm");
+    float* d;
+    int rc = stage_in(h, 2 * n, &d);
+    if (rc) return rc;
+    if ((rc = copy_sync(h, d, h_x, n * 4, hipMemcpyHostToDevice, "rms_norm"))) return rc;
+    if ((rc = copy_sync(h, d + n, h_w, n * 4, hipMemcpyHostToDevice, "rms_norm"))) return rc;
+    PI_HIP(h, pi::launch_head_rmsnorm(d, d + n, 1, (int)n, (int)n, eps, h->stream), "rms_norm");
+    if ((rc = copy_sync(h, h_out, d, n * 4, hipMemcpyDeviceToHost, "rms_norm"))) return rc;
+    PI_HIP(h, hipStreamSynchronize(h->stream), "rms_norm");
+    return PI_OK;
+}
+
+int pi_ops_softmax(pi_handle h, float* h_x, size_t n) {
+    PI_CHECK_HANDLE(h);
+    if (n == 0) return PI_OK;  // src/ops.rs:161-163
+    if (!h_x) return fail(h, PI_ERR_INVALID_ARG, "softmax: null slice");
+    if (n > (1u << 28)) return fail(h, PI_ERR_UNSUPPORTED, "softmax: n=%zu", n);
+    PI_HIP(h, hipSetDevice(h->device), "softmax");
+    float* d;
+    int rc = stage_in(h, n, &d);
+    if (rc) return rc;
+    if ((rc = copy_sync(h, d, h_x, n * 4, hipMemcpyHostToDevice, "softmax"))) return rc;
+    PI_HIP(h, pi::launch_softmax(d, (int)n, h->stream), "softmax");
+    if ((rc = copy_sync(h, h_x, d, n * 4, hipMemcpyDeviceToHost, "softmax"))) return rc;
+    PI_HIP(h, hipStreamSynchronize(h->stream), "softmax");
+    return PI_OK;
+}
+
+// One q head and one k head rotated in place at `position` with the frequency
+// table f (n_pairs entries), NORM (adjacent pairs) or NeoX pairing.
+static int rope_one(pi_handle h, float* h_q, float* h_k, size_t position, size_t head_dim,
+                    const pi::RopeFreqs& f, int n_pairs, int neox, const char* what) {
+    PI_CHECK_HANDLE(h);
+    if (!h_q || !h_k) return fail(h, PI_ERR_INVALID_ARG, "%s: null slice", what);
+    if (head_dim == 0 || head_dim > 256) return fail(h, PI_ERR_UNSUPPORTED, "%s: head_dim %zu", what, head_dim);
+    if (position > (size_t)INT32_MAX) return fail(h, PI_ERR_UNSUPPORTED, "%s: position %zu", what, position);
+    if (n_pairs == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), what);
+    float* d;
+    int rc = stage_in(h, 2 * head_dim + 1, &d);
+    if (rc) return rc;
+    int32_t* dpos = reinterpret_cast<int32_t*>(d + 2 * head_dim);
+    const int32_t pos32 = (int32_t)position;
+    if ((rc = copy_sync(h, d, h_q, head_dim * 4, hipMemcpyHostToDevice, what))) return rc;
+    if ((rc = copy_sync(h, d + head_dim, h_k, head_dim * 4, hipMemcpyHostToDevice, what))) return rc;
+    if ((rc = copy_sync(h, dpos, &pos32, 4, hipMemcpyHostToDevice, what))) return rc;
+    PI_HIP(h, pi::launch_rope(d, d + head_dim, dpos, 1, 1, 1, (int)head_dim, n_pairs, neox, f, h->stream), what);
+    if ((rc = copy_sync(h, h_q, d, head_dim * 4, hipMemcpyDeviceToHost, what))) return rc;
+    if ((rc = copy_sync(h, h_k, d + head_dim, head_dim * 4, hipMemcpyDeviceToHost, what))) return rc;
+    PI_HIP(h, hipStreamSynchronize(h->stream), what);
+    return PI_OK;
+}
+
+int pi_ops_apply_rope(pi_handle h, float* h_q, float* h_k, size_t position, size_t head_dim,
+                      size_t rope_dim, float base_freq) {
+    if (rope_dim > 256) return fail(h, PI_ERR_UNSUPPORTED, "apply_rope: rope_dim %zu", rope_dim);
+    pi::RopeFreqs f;
+    std::memset(&f, 0, sizeof f);
+    norm_rope_freqs(base_freq, (int)rope_dim, f.f);
+    // src/ops.rs:52-64: pairs with 2i+1 >= head_dim are skipped (the kernel checks)
+    return rope_one(h, h_q, h_k, position, head_dim, f, (int)(rope_dim / 2), 0, "apply_rope");
+}
+
+int pi_ops_apply_rope_with_freqs(pi_handle h, float* h_q, float* h_k, size_t position,
+                                 size_t head_dim, const float* h_freqs, size_t n_freqs) {
+    if (n_freqs && !h_freqs) return fail(h, PI_ERR_INVALID_ARG, "apply_rope_with_freqs: null freqs");
+    if (n_freqs > 128) return fail(h, PI_ERR_UNSUPPORTED, "apply_rope_with_freqs: %zu freqs", n_freqs);
+    pi::RopeFreqs f;
+    std::memset(&f, 0, sizeof f);
+    for (size_t i = 0; i < n_freqs; ++i) f.f[i] = h_freqs[i];
+    return rope_one(h, h_q, h_k, position, head_dim, f, (int)n_freqs, 1, "apply_rope_with_freqs");
+}
+
+int pi_compute_imrope_freqs(float base, size_t n_rot, const int32_t* sections, float* out) {
+    if (!sections || (!out && n_rot >= 2)) return fail(nullptr, PI_ERR_INVALID_ARG, "compute_imrope_freqs: null argument");
+    if (n_rot / 2 > 128) return fail(nullptr, PI_ERR_UNSUPPORTED, "compute_imrope_freqs: n_rot %zu", n_rot);
+    if (n_rot >= 2) imrope_freqs(base, (int)n_rot, out);
+    return PI_OK;
+}
+
+int pi_ssm_gated_delta_step(pi_handle h, float* h_out, float* h_state, const float* h_q,
+                            const float* h_k, const float* h_v, const float* h_beta,
+                            const float* h_g, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
+                            int32_t v_hd) {
+    PI_CHECK_HANDLE(h);
+    if (!h_out || !h_state || !h_q || !h_k || !h_v || !h_beta || !h_g)
+        return fail(h, PI_ERR_INVALID_ARG, "gated_delta_step: null slice");
+    int rc = gdn_shape_check(h, "gated_delta_step", n_k_heads, n_v_heads, k_hd, v_hd);
+    if (rc) return rc;
+    PI_HIP(h, hipSetDevice(h->device), "gated_delta_step");
+    const size_t nq = (size_t)n_k_heads * k_hd, nv = (size_t)n_v_heads * v_hd;
+    const size_t ns = (size_t)n_v_heads * k_hd * v_hd, nh = (size_t)n_v_heads;
+    float* d;
+    if ((rc = stage_in(h, ns + 2 * nq + 2 * nv + 2 * nh, &d))) return rc;
+    float *ds = d, *dq = ds + ns, *dk = dq + nq, *dv = dk + nq, *db = dv + nv, *dg = db + nh,
+          *dout = dg + nh;
+    if ((rc = copy_sync(h, ds, h_state, ns * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
+    if ((rc = copy_sync(h, dq, h_q, nq * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
+    if ((rc = copy_sync(h, dk, h_k, nq * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
+    if ((rc = copy_sync(h, dv, h_v, nv * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
+    if ((rc = copy_sync(h, db, h_beta, nh * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
+    if ((rc = copy_sync(h, dg, h_g, nh * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
+    PI_HIP(h, pi::launch_gdn_decode(dq, dk, dv, db, dg, ds, dout, 1, n_k_heads, n_v_heads, h->stream),
+           "gated_delta_step");
+    if ((rc = copy_sync(h, h_state, ds, ns * 4, hipMemcpyDeviceToHost, "gated_delta_step"))) return rc;
+    if ((rc = copy_sync(h, h_out, dout, nv * 4, hipMemcpyDeviceToHost, "gated_delta_step"))) return rc;
+    PI_HIP(h, hipStreamSynchronize(h->stream), "gated_delta_step");
+    return PI_OK;
 }
 
 }  // extern "C"

@@ -76,6 +76,7 @@ hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, in
                        const RopeFreqs& freqs, hipStream_t s);
 hipError_t launch_head_rmsnorm(float* x, const float* w, int32_t n_rows, int32_t dim,
                                int32_t row_stride, float eps, hipStream_t s);
+hipError_t launch_softmax(float* x, int32_t n, hipStream_t s);
 
 hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
                           int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,

@@ -6,6 +6,7 @@
 //   rope        : ops::apply_rope / apply_rope_with_freqs (src/ops.rs:35-67,130-157)
 //                 as driven by src/model/mod.rs:1072-1138
 //   head_rmsnorm: ops::rms_norm per head (src/ops.rs:13-27; src/model/mod.rs:1035-1070)
+//   softmax     : ops::softmax on one row (src/ops.rs:160-180)
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ q, float*
     }
 }
 
-// One wavefront per row; dim <= 256.
+// One wavefront per row (any dim): sum of squares, then x * (1/rms) * w.
 __global__ __launch_bounds__(256) void head_rmsnorm_kernel(float* __restrict__ x,
                                                            const float* __restrict__ w,
                                                            int n_rows, int dim, int row_stride,
@@ -112,23 +113,43 @@ __global__ __launch_bounds__(256) void head_rmsnorm_kernel(float* __restrict__ x
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n_rows) return;
     float* xr = x + (size_t)row * row_stride;
-    float v[4];
     float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        v[i] = d < dim ? xr[d] : 0.f;
-        ss += v[i] * v[i];
-    }
+    for (int d = lane; d < dim; d += 64) ss += xr[d] * xr[d];
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
     const float rms = sqrtf(ss / (float)dim + eps);
     const float inv = 1.0f / rms;
+    for (int d = lane; d < dim; d += 64) xr[d] = (xr[d] * inv) * w[d];
+}
+
+// ops::softmax (src/ops.rs:160-180) on one row of n values, in place: max,
+// exp(x - max), sum, x * (1 / sum).  One workgroup.
+__global__ __launch_bounds__(1024) void softmax_row_kernel(float* __restrict__ x, int n) {
+    __shared__ float red[16];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    float m = -INFINITY;
+    for (int i = tid; i < n; i += 1024) m = fmaxf(m, x[i]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int d = lane + 64 * i;
-        if (d < dim) xr[d] = (v[i] * inv) * w[d];
+    for (int o = 32; o >= 1; o >>= 1) m = wave_max_xor(m, o);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    m = red[0];
+    for (int i = 1; i < 16; ++i) m = fmaxf(m, red[i]);
+    __syncthreads();
+    float sum = 0.f;
+    for (int i = tid; i < n; i += 1024) {
+        const float e = expf(x[i] - m);
+        x[i] = e;
+        sum += e;
     }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum = wave_sum_xor(sum, o);
+    if (lane == 0) red[wv] = sum;
+    __syncthreads();
+    sum = 0.f;
+    for (int i = 0; i < 16; ++i) sum += red[i];
+    const float inv = 1.0f / sum;
+    for (int i = tid; i < n; i += 1024) x[i] *= inv;
 }
 
 int grid_for(size_t total) {
@@ -187,6 +208,11 @@ hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, in
     const size_t total = (size_t)n_tok * (n_q_heads + (k ? n_kv_heads : 0)) * n_pairs;
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(total)), dim3(256), 0, s, q, k, pos, n_tok,
                        n_q_heads, n_kv_heads, head_dim, n_pairs, neox, freqs);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax(float* x, int32_t n, hipStream_t s) {
+    hipLaunchKernelGGL(softmax_row_kernel, dim3(1), dim3(1024), 0, s, x, n);
     return hipGetLastError();
 }
 

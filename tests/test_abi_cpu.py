@@ -66,3 +66,34 @@ def test_create_without_device_reports_device_error():
     assert b"pi_create" in lib.pi_last_error(None)
     with pytest.raises(runtime.DeviceError):
         runtime.Device(0)
+
+
+CPP_TEST = os.path.join(ROOT, "tests", "cpp", "_build", "test_ops")
+
+
+def test_cpp_mirror_reports_missing_device():
+    """The C++ mirror (include/pi_ops.hpp) returns None from Device::init and the
+    test binary exits 2 naming the device error when no GPU is visible."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    assert os.path.exists(CPP_TEST), "tests/cpp not built (python -m powerinfer_x64_amd.build)"
+    r = subprocess.run([CPP_TEST], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2, r.stdout + r.stderr
+    assert r.stdout.startswith("NO_DEVICE pi_create")
+
+
+def test_compute_imrope_freqs_host_export_matches_oracle(orc):
+    """pi_compute_imrope_freqs is host code in the product; it must equal the
+    oracle's restatement of src/ops.rs:78-122 bit for bit."""
+    import numpy as np
+    from powerinfer_x64_amd import _abi
+    lib = _abi.load()
+    for base, n_rot, sec in ((1e7, 64, (11, 11, 10, 0)), (1e6, 128, (24, 20, 20, 0)),
+                             (1e4, 2, (1, 0, 0, 0))):
+        out = np.zeros(n_rot // 2, np.float32)
+        s = (ctypes.c_int32 * 4)(*sec)
+        assert lib.pi_compute_imrope_freqs(base, n_rot, s, out.ctypes.data_as(ctypes.c_void_p)) == 0
+        ref = orc.compute_imrope_freqs(base, n_rot, list(sec))
+        assert np.array_equal(out, ref)
+    assert lib.pi_compute_imrope_freqs(1e4, 512, s, out.ctypes.data_as(ctypes.c_void_p)) == 5
