@@ -135,6 +135,22 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
 int pi_gdn_gates(pi_handle h, const float* d_beta_raw, const float* d_a_raw, const float* d_ssm_a,
                  const float* d_dt_bias, float* d_beta, float* d_g, int32_t n_tok,
                  int32_t n_v_heads, void* stream);
+/* Depthwise causal conv1d + SiLU over the QKV channels (src/model/mod.rs:750-776)
+ * for n_tok tokens of n_seq sequences.  d_x, d_out [n_seq][n_tok][conv_dim]
+ * (d_out must not alias d_x); d_conv_state [n_seq][d_conv-1][conv_dim] in/out
+ * holds the previous d_conv-1 raw inputs, oldest first (the reference's
+ * ssm_conv_states ring, :125-127; zero-initialised, as its lazy init at
+ * :752-756); d_w [conv_dim][d_conv] (GGML [ne0=d_conv, ne1=conv_dim]).
+ * out[t][i] = silu(sum_k w[i][k] * window[k][i]). */
+int pi_gdn_conv1d(pi_handle h, const float* d_x, float* d_conv_state, const float* d_w,
+                  float* d_out, int32_t n_seq, int32_t n_tok, int32_t conv_dim, int32_t d_conv,
+                  void* stream);
+/* RMSNormGated in place (src/model/mod.rs:918-932): for each row and V head,
+ * o = o * (1/sqrt(mean(o^2) + eps)) * w * silu(z).  d_o, d_z
+ * [n_rows][n_v_heads][v_hd], d_w [v_hd]. */
+int pi_gdn_rmsnorm_gated(pi_handle h, float* d_o, const float* d_z, const float* d_w,
+                         int32_t n_rows, int32_t n_v_heads, int32_t v_hd, float eps,
+                         void* stream);
 /* One recurrent step per sequence (src/model/mod.rs:841-916): q/k raw
  * [batch][n_k_heads][k_hd], v [batch][n_v_heads][v_hd], beta/g [batch][n_v_heads],
  * state [batch][n_v_heads][k_hd][v_hd] f32 in/out (ssm::create_ssm_state,

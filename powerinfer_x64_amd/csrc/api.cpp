@@ -382,6 +382,39 @@ int pi_gdn_gates(pi_handle h, const float* d_beta_raw, const float* d_a_raw, con
     return PI_OK;
 }
 
+int pi_gdn_conv1d(pi_handle h, const float* d_x, float* d_conv_state, const float* d_w,
+                  float* d_out, int32_t n_seq, int32_t n_tok, int32_t conv_dim, int32_t d_conv,
+                  void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_x || !d_conv_state || !d_w || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_conv1d: null argument");
+    if (d_out == d_x) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_conv1d: d_out must not alias d_x");
+    if (n_seq < 0 || n_tok < 0 || conv_dim <= 0 || d_conv < 1 || d_conv > 16)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_conv1d: n_seq=%d n_tok=%d conv_dim=%d d_conv=%d",
+                    n_seq, n_tok, conv_dim, d_conv);
+    if (n_seq == 0 || n_tok == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_gdn_conv1d");
+    PI_HIP(h, pi::launch_gdn_conv1d(d_x, d_conv_state, d_w, d_out, n_seq, n_tok, conv_dim, d_conv,
+                                    pick(h, stream)),
+           "pi_gdn_conv1d");
+    return PI_OK;
+}
+
+int pi_gdn_rmsnorm_gated(pi_handle h, float* d_o, const float* d_z, const float* d_w,
+                         int32_t n_rows, int32_t n_v_heads, int32_t v_hd, float eps,
+                         void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_o || !d_z || !d_w) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_rmsnorm_gated: null argument");
+    if (n_rows < 0 || n_v_heads <= 0 || v_hd <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_rmsnorm_gated: n_rows=%d n_v_heads=%d v_hd=%d",
+                    n_rows, n_v_heads, v_hd);
+    if (n_rows == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_gdn_rmsnorm_gated");
+    PI_HIP(h, pi::launch_gdn_rmsnorm_gated(d_o, d_z, d_w, n_rows, n_v_heads, v_hd, eps, pick(h, stream)),
+           "pi_gdn_rmsnorm_gated");
+    return PI_OK;
+}
+
 static int gdn_shape_check(pi_handle h, const char* fn, int32_t n_k_heads, int32_t n_v_heads,
                            int32_t k_hd, int32_t v_hd) {
     if (n_k_heads <= 0 || n_v_heads <= 0)

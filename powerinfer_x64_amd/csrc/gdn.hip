@@ -39,6 +39,98 @@ __global__ __launch_bounds__(256) void gdn_gates_kernel(const float* __restrict_
     g[idx] = ssm_a[h] * sp;
 }
 
+// Depthwise causal conv1d + SiLU over the QKV channels (src/model/mod.rs:750-776).
+// For sequence s, token t and channel i the window is rows t .. t+d_conv-1 of
+// X_ext = [state_s (d_conv-1 rows, oldest first); x_s (n_tok rows)], and
+//   out[t][i] = silu(sum_k w[i*d_conv + k] * X_ext[t + k][i]).
+// One thread per (s, t, i); channels are the fastest index, so loads coalesce.
+__global__ __launch_bounds__(256) void gdn_conv1d_kernel(const float* __restrict__ x,
+                                                         const float* __restrict__ state,
+                                                         const float* __restrict__ w,
+                                                         float* __restrict__ out, int n_seq,
+                                                         int n_tok, int conv_dim, int d_conv) {
+    const size_t total = (size_t)n_seq * n_tok * conv_dim;
+    const int nh = d_conv - 1;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int i = (int)(idx % conv_dim);
+        const int t = (int)((idx / conv_dim) % n_tok);
+        const int sq = (int)(idx / ((size_t)conv_dim * n_tok));
+        const float* xs = x + (size_t)sq * n_tok * conv_dim;
+        const float* ss = state + (size_t)sq * nh * conv_dim;
+        float val = 0.f;
+        for (int k = 0; k < d_conv; ++k) {
+            const int r = t + k;  // row of X_ext
+            const float v = r < nh ? ss[(size_t)r * conv_dim + i] : xs[(size_t)(r - nh) * conv_dim + i];
+            val += w[(size_t)i * d_conv + k] * v;
+        }
+        out[idx] = val / (1.0f + expf(-val));
+    }
+}
+
+// New state = the last d_conv-1 rows of X_ext (after gdn_conv1d_kernel has
+// read the old one; same stream, next launch).
+__global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __restrict__ x,
+                                                             float* __restrict__ state, int n_seq,
+                                                             int n_tok, int conv_dim, int d_conv) {
+    const int nh = d_conv - 1;
+    const size_t total = (size_t)n_seq * nh * conv_dim;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int i = (int)(idx % conv_dim);
+        const int j = (int)((idx / conv_dim) % nh);
+        const int sq = (int)(idx / ((size_t)conv_dim * nh));
+        float* ss = state + (size_t)sq * nh * conv_dim;
+        if (n_tok >= nh) {
+            ss[(size_t)j * conv_dim + i] = x[((size_t)sq * n_tok + n_tok - nh + j) * conv_dim + i];
+        }
+    }
+}
+
+// Short prompts (n_tok < d_conv-1): shift the state by n_tok rows in one
+// thread per (sequence, channel), so no row is overwritten before it is read.
+__global__ __launch_bounds__(256) void gdn_conv_state_shift_kernel(const float* __restrict__ x,
+                                                                   float* __restrict__ state,
+                                                                   int n_seq, int n_tok,
+                                                                   int conv_dim, int d_conv) {
+    const int nh = d_conv - 1;
+    const size_t total = (size_t)n_seq * conv_dim;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int i = (int)(idx % conv_dim);
+        const int sq = (int)(idx / conv_dim);
+        float* ss = state + (size_t)sq * nh * conv_dim;
+        for (int j = 0; j < nh; ++j) {
+            const int r = j + n_tok;  // X_ext row that becomes state row j
+            ss[(size_t)j * conv_dim + i] =
+                r < nh ? ss[(size_t)r * conv_dim + i] : x[((size_t)sq * n_tok + r - nh) * conv_dim + i];
+        }
+    }
+}
+
+// RMSNormGated (src/model/mod.rs:918-932) in place: for every (row, V head),
+// o * (1/sqrt(mean(o^2) + eps)) * w * silu(z).  One wavefront per (row, head).
+__global__ __launch_bounds__(256) void gdn_rmsnorm_gated_kernel(float* __restrict__ o,
+                                                                const float* __restrict__ z,
+                                                                const float* __restrict__ w,
+                                                                int n_heads_total, int v_hd,
+                                                                float eps) {
+    const int lane = threadIdx.x & 63;
+    const int hrow = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (hrow >= n_heads_total) return;
+    float* oh = o + (size_t)hrow * v_hd;
+    const float* zh = z + (size_t)hrow * v_hd;
+    float ss = 0.f;
+    for (int d = lane; d < v_hd; d += 64) ss += oh[d] * oh[d];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
+    const float scale = 1.0f / sqrtf(ss / (float)v_hd + eps);
+    for (int d = lane; d < v_hd; d += 64) {
+        const float zv = zh[d];
+        oh[d] = (oh[d] * scale * w[d]) * (zv / (1.0f + expf(-zv)));
+    }
+}
+
 // Block-wide sum of one value per thread; all threads get the result.
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
@@ -481,6 +573,36 @@ hipError_t launch_gdn_gates(const float* beta_raw, const float* a_raw, const flo
     const int n = n_tok * n_v_heads;
     hipLaunchKernelGGL(gdn_gates_kernel, dim3((n + 255) / 256), dim3(256), 0, s, beta_raw, a_raw,
                        ssm_a, dt_bias, beta, g, n_tok, n_v_heads);
+    return hipGetLastError();
+}
+
+static int grid_of(size_t total) {
+    size_t b = (total + 255) / 256;
+    return (int)(b > 65536 ? 65536 : (b == 0 ? 1 : b));
+}
+
+hipError_t launch_gdn_conv1d(const float* x, float* state, const float* w, float* out,
+                             int32_t n_seq, int32_t n_tok, int32_t conv_dim, int32_t d_conv,
+                             hipStream_t s) {
+    const size_t total = (size_t)n_seq * n_tok * conv_dim;
+    hipLaunchKernelGGL(gdn_conv1d_kernel, dim3(grid_of(total)), dim3(256), 0, s, x, state, w, out,
+                       n_seq, n_tok, conv_dim, d_conv);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || d_conv < 2) return e;
+    if (n_tok >= d_conv - 1)
+        hipLaunchKernelGGL(gdn_conv_state_kernel, dim3(grid_of((size_t)n_seq * (d_conv - 1) * conv_dim)),
+                           dim3(256), 0, s, x, state, n_seq, n_tok, conv_dim, d_conv);
+    else
+        hipLaunchKernelGGL(gdn_conv_state_shift_kernel, dim3(grid_of((size_t)n_seq * conv_dim)),
+                           dim3(256), 0, s, x, state, n_seq, n_tok, conv_dim, d_conv);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_rmsnorm_gated(float* o, const float* z, const float* w, int32_t n_rows,
+                                    int32_t n_v_heads, int32_t v_hd, float eps, hipStream_t s) {
+    const int n = n_rows * n_v_heads;
+    hipLaunchKernelGGL(gdn_rmsnorm_gated_kernel, dim3((n + 3) / 4), dim3(256), 0, s, o, z, w, n,
+                       v_hd, eps);
     return hipGetLastError();
 }
 

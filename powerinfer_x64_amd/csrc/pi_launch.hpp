@@ -86,6 +86,11 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
 hipError_t launch_gdn_gates(const float* beta_raw, const float* a_raw, const float* ssm_a,
                             const float* dt_bias, float* beta, float* g, int32_t n_tok,
                             int32_t n_v_heads, hipStream_t s);
+hipError_t launch_gdn_conv1d(const float* x, float* state, const float* w, float* out,
+                             int32_t n_seq, int32_t n_tok, int32_t conv_dim, int32_t d_conv,
+                             hipStream_t s);
+hipError_t launch_gdn_rmsnorm_gated(float* o, const float* z, const float* w, int32_t n_rows,
+                                    int32_t n_v_heads, int32_t v_hd, float eps, hipStream_t s);
 hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, const float* beta,
                              const float* g, float* state, float* out, int32_t batch,
                              int32_t n_k_heads, int32_t n_v_heads, hipStream_t s);

@@ -304,3 +304,31 @@ def attention_head(dev: Device, q: np.ndarray, k_cache: np.ndarray, v_cache: np.
                                             k.ctypes.data_as(fp), v.ctypes.data_as(fp), seq_len,
                                             head_dim))
     return out
+
+
+def gdn_conv1d(dev: Device, x, conv_state, w, out=None):
+    """Depthwise causal conv1d + SiLU: x [n_seq, n_tok, conv_dim], conv_state
+    [n_seq, d_conv-1, conv_dim] (in/out), w [conv_dim, d_conv] -> out like x."""
+    n_seq, n_tok, conv_dim = x.shape
+    d_conv = w.shape[1]
+    _need(x, "x", torch.float32, dev=dev.torch_device)
+    _need(conv_state, "conv_state", torch.float32, (n_seq, d_conv - 1, conv_dim), dev.torch_device)
+    _need(w, "w", torch.float32, (conv_dim, d_conv), dev.torch_device)
+    if out is None:
+        out = torch.empty_like(x)
+    _need(out, "out", torch.float32, x.shape, dev.torch_device)
+    dev.check(dev.lib.pi_gdn_conv1d(dev.h, _vp(x), _vp(conv_state), _vp(w), _vp(out), n_seq, n_tok,
+                                    conv_dim, d_conv, dev.stream()))
+    return out
+
+
+def gdn_rmsnorm_gated(dev: Device, o, z, w, eps: float):
+    """In place on o [..., n_v_heads, v_hd]: o * rsqrt(mean(o^2) + eps) * w * silu(z)."""
+    hv, dv = o.shape[-2:]
+    _need(o, "o", torch.float32, dev=dev.torch_device)
+    _need(z, "z", torch.float32, o.shape, dev.torch_device)
+    _need(w, "w", torch.float32, (dv,), dev.torch_device)
+    rows = o.numel() // (hv * dv)
+    dev.check(dev.lib.pi_gdn_rmsnorm_gated(dev.h, _vp(o), _vp(z), _vp(w), rows, hv, dv, float(eps),
+                                           dev.stream()))
+    return o
