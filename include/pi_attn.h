@@ -105,6 +105,21 @@ int pi_rope(pi_handle h, float* d_q, float* d_k, const int32_t* d_pos, int32_t n
             int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t rope_dim,
             float base, const int32_t* h_sections, void* stream);
 
+/* The whole prologue of a full-attention layer step in one launch
+ * (src/model/mod.rs:1035-1146): for token t of sequence s at position
+ * d_start_pos[s] + t, per-head RMSNorm of q and k (when d_q_norm_w /
+ * d_k_norm_w are non-NULL, [head_dim] each), RoPE (as pi_rope: NORM pairs, or
+ * IMRoPE NeoX pairs when h_sections != NULL), q and k rewritten in place, and
+ * k and v appended to the pool (append-then-attend).  d_q
+ * [n_seq][n_tok][n_q_heads][D], d_k/d_v [n_seq][n_tok][n_kv_heads][D] f32,
+ * D = the pool's head_dim. */
+int pi_attn_prologue(pi_handle h, float* d_q, float* d_k, const float* d_v,
+                     const float* d_q_norm_w, const float* d_k_norm_w, float eps,
+                     int32_t rope_dim, float rope_base, const int32_t* h_sections,
+                     pi_kv_pool pool, const int32_t* d_page_table, int32_t max_pages,
+                     const int32_t* d_start_pos, int32_t n_seq, int32_t n_tok,
+                     int32_t n_q_heads, void* stream);
+
 /* ---- attention ---------------------------------------------------------------
  * Decode: one query token per sequence against its paged cache
  * (src/model/mod.rs:1148-1190; append-then-attend: the caller appends the

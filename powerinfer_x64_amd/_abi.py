@@ -34,6 +34,8 @@ SIGNATURES = {
     "pi_kv_read": (_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "pi_head_rmsnorm": (_int, [_vp, _vp, _vp, _i32, _i32, _i32, _f32, _vp]),
     "pi_rope": (_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp]),
+    "pi_attn_prologue": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _f32, _i32, _f32, _vp, _vp, _vp,
+                                _i32, _vp, _i32, _i32, _i32, _vp]),
     "pi_attn_decode": (_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp, _vp,
                               _vp]),
     "pi_attn_prefill": (_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,

@@ -295,6 +295,38 @@ int pi_rope(pi_handle h, float* d_q, float* d_k, const int32_t* d_pos, int32_t n
     return PI_OK;
 }
 
+int pi_attn_prologue(pi_handle h, float* d_q, float* d_k, const float* d_v,
+                     const float* d_q_norm_w, const float* d_k_norm_w, float eps,
+                     int32_t rope_dim, float rope_base, const int32_t* h_sections,
+                     pi_kv_pool pool, const int32_t* d_page_table, int32_t max_pages,
+                     const int32_t* d_start_pos, int32_t n_seq, int32_t n_tok,
+                     int32_t n_q_heads, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_q || !d_k || !d_v || !pool || !d_page_table || !d_start_pos)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prologue: null argument");
+    if (n_seq < 0 || n_tok < 0 || max_pages <= 0 || n_q_heads <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prologue: n_seq=%d n_tok=%d max_pages=%d n_q_heads=%d",
+                    n_seq, n_tok, max_pages, n_q_heads);
+    const pi::KvGeom& g = pool->g;
+    // src/model/mod.rs:1074: the rotation is capped to the head dim
+    const int rd = rope_dim <= 0 ? g.head_dim : (rope_dim < g.head_dim ? rope_dim : g.head_dim);
+    const int n_pairs = rd / 2;
+    if (n_pairs > 128) return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prologue: rope_dim %d", rd);
+    if (n_seq == 0 || n_tok == 0) return PI_OK;
+    pi::RopeFreqs f;
+    std::memset(&f, 0, sizeof f);
+    if (h_sections == nullptr)
+        norm_rope_freqs(rope_base, rd, f.f);
+    else
+        imrope_freqs(rope_base, rd, f.f);
+    PI_HIP(h, hipSetDevice(h->device), "pi_attn_prologue");
+    PI_HIP(h, pi::launch_attn_prologue(d_q, d_k, d_v, d_q_norm_w, d_k_norm_w, eps, f, n_pairs,
+                                       h_sections ? 1 : 0, g, d_page_table, max_pages, d_start_pos,
+                                       n_seq, n_tok, n_q_heads, pick(h, stream)),
+           "pi_attn_prologue");
+    return PI_OK;
+}
+
 // ---- attention -------------------------------------------------------------------
 
 int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t* d_page_table,

@@ -77,6 +77,12 @@ hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, in
 hipError_t launch_head_rmsnorm(float* x, const float* w, int32_t n_rows, int32_t dim,
                                int32_t row_stride, float eps, hipStream_t s);
 hipError_t launch_softmax(float* x, int32_t n, hipStream_t s);
+hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
+                                const float* k_norm_w, float eps, const RopeFreqs& freqs,
+                                int32_t n_pairs, int32_t neox, const KvGeom& g,
+                                const int32_t* page_table, int32_t max_pages,
+                                const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
+                                int32_t n_q_heads, hipStream_t s);
 
 hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
                           int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,

@@ -7,6 +7,8 @@
 //                 as driven by src/model/mod.rs:1072-1138
 //   head_rmsnorm: ops::rms_norm per head (src/ops.rs:13-27; src/model/mod.rs:1035-1070)
 //   softmax     : ops::softmax on one row (src/ops.rs:160-180)
+//   attn_prologue: the three above fused for a whole layer step
+//                 (src/model/mod.rs:1035-1146): norm, RoPE, append
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -152,6 +154,75 @@ __global__ __launch_bounds__(1024) void softmax_row_kernel(float* __restrict__ x
     for (int i = tid; i < n; i += 1024) x[i] *= inv;
 }
 
+// Fused decode / prefill prologue of a full-attention layer
+// (src/model/mod.rs:1035-1146): for token t of sequence s at position
+// start_pos[s] + t, every q head and k head is RMS-normed (optional weights)
+// and rotated (NORM adjacent pairs or NeoX pairs with the host-built
+// frequency table), q in place, k in place and appended with v to the paged
+// pool.  One wavefront per (sequence, token, head); the row is staged in LDS.
+template <typename PT>
+__global__ __launch_bounds__(256) void attn_prologue_kernel(
+    float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ qn, const float* __restrict__ kn, float eps, RopeFreqs f,
+    int n_pairs, int neox, KvGeom g, const int32_t* __restrict__ pt, int max_pages,
+    const int32_t* __restrict__ start_pos, int n_seq, int n_tok, int hq) {
+    __shared__ float row_s[4][256];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int D = g.head_dim, hkv = g.n_kv_heads, heads = hq + hkv;
+    const int row = blockIdx.x * 4 + wv;
+    if (row >= n_seq * n_tok * heads) return;
+    const int head = row % heads;
+    const int t = (row / heads) % n_tok;
+    const int sq = row / (heads * n_tok);
+    const bool is_q = head < hq;
+    const int kvh = head - hq;
+    float* x = is_q ? q + (((size_t)sq * n_tok + t) * hq + head) * D
+                    : k + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
+    const float* nw = is_q ? qn : kn;
+    float* r = row_s[wv];
+    float ss = 0.f;
+    for (int d = lane; d < D; d += 64) {
+        const float xv = x[d];
+        r[d] = xv;
+        ss += xv * xv;
+    }
+    if (nw) {  // ops::rms_norm (src/ops.rs:13-27) per head
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
+        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+        for (int d = lane; d < D; d += 64) r[d] = (r[d] * inv) * nw[d];
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int pos = start_pos[sq] + t;
+    for (int i = lane; i < n_pairs; i += 64) {  // ops::apply_rope / apply_rope_with_freqs
+        const int a = neox ? i : 2 * i;
+        const int b = neox ? i + n_pairs : 2 * i + 1;
+        if (b >= D) continue;
+        const float theta = (float)pos * f.f[i];
+        const float c = cosf(theta), sn = sinf(theta);
+        const float x0 = r[a], x1 = r[b];
+        r[a] = x0 * c - x1 * sn;
+        r[b] = x0 * sn + x1 * c;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int d = lane; d < D; d += 64) x[d] = r[d];
+    if (is_q) return;
+    // append-then-attend (src/model/mod.rs:1140-1146): K (normed, rotated) and V at pos
+    const int lp = pos / kPageTokens;
+    if (pos < 0 || lp >= max_pages) return;
+    const int page = pt[(size_t)sq * max_pages + lp];
+    if (page < 0 || page >= g.n_pages) return;
+    const int tok = pos % kPageTokens;
+    const size_t blk = ((size_t)page * hkv + kvh) * kPageTokens * D;
+    PT* kp = reinterpret_cast<PT*>(g.k) + blk;
+    PT* vp = reinterpret_cast<PT*>(g.v) + blk;
+    const float* vr = v + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
+    for (int d = lane; d < D; d += 64) {
+        kp[k_index<PT>(tok, d)] = from_f32<PT>(r[d]);
+        vp[v_index(tok, d)] = from_f32<PT>(vr[d]);
+    }
+}
+
 int grid_for(size_t total) {
     size_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
@@ -199,6 +270,25 @@ hipError_t launch_kv_read(const KvGeom& g, const int32_t* page_table, int32_t ma
     else
         hipLaunchKernelGGL((kv_read_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, g,
                            page_table, max_pages, seq, start, n_tok, k_out, v_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
+                                const float* k_norm_w, float eps, const RopeFreqs& freqs,
+                                int32_t n_pairs, int32_t neox, const KvGeom& g,
+                                const int32_t* page_table, int32_t max_pages,
+                                const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
+                                int32_t n_q_heads, hipStream_t s) {
+    const long long rows = (long long)n_seq * n_tok * (n_q_heads + g.n_kv_heads);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (g.dtype == 1)
+        hipLaunchKernelGGL(attn_prologue_kernel<f16>, grid, dim3(256), 0, s, q, k, v, q_norm_w,
+                           k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages,
+                           start_pos, n_seq, n_tok, n_q_heads);
+    else
+        hipLaunchKernelGGL(attn_prologue_kernel<float>, grid, dim3(256), 0, s, q, k, v, q_norm_w,
+                           k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages,
+                           start_pos, n_seq, n_tok, n_q_heads);
     return hipGetLastError();
 }
 

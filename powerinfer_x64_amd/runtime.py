@@ -332,3 +332,27 @@ def gdn_rmsnorm_gated(dev: Device, o, z, w, eps: float):
     dev.check(dev.lib.pi_gdn_rmsnorm_gated(dev.h, _vp(o), _vp(z), _vp(w), rows, hv, dv, float(eps),
                                            dev.stream()))
     return o
+
+
+def attn_prologue(dev: Device, q, k, v, pool: KvPool, page_table, start_pos, q_norm_w=None,
+                  k_norm_w=None, eps: float = 1e-6, rope_dim: int = 0, rope_base: float = 10000.0,
+                  sections: Optional[Sequence[int]] = None):
+    """Norm + RoPE + append for q [n_seq, n_tok, Hq, D], k/v [n_seq, n_tok, Hkv, D]
+    (f32; q and k rewritten in place, k and v appended at start_pos[s] + t)."""
+    n_seq, n_tok, hq, dh = q.shape
+    _need(q, "q", torch.float32, dev=dev.torch_device)
+    _need(k, "k", torch.float32, (n_seq, n_tok, pool.n_kv_heads, pool.head_dim), dev.torch_device)
+    _need(v, "v", torch.float32, k.shape, dev.torch_device)
+    if dh != pool.head_dim:
+        raise InvalidArg(f"q head_dim {dh} != pool head_dim {pool.head_dim}")
+    _need(page_table, "page_table", torch.int32, dev=dev.torch_device)
+    _need(start_pos, "start_pos", torch.int32, (n_seq,), dev.torch_device)
+    for name, w in (("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w)):
+        if w is not None:
+            _need(w, name, torch.float32, (dh,), dev.torch_device)
+    sec = None if sections is None else (ctypes.c_int32 * 4)(*[int(s) for s in sections])
+    dev.check(dev.lib.pi_attn_prologue(dev.h, _vp(q), _vp(k), _vp(v), _vp(q_norm_w), _vp(k_norm_w),
+                                       float(eps), int(rope_dim), float(rope_base), sec, pool.p,
+                                       _vp(page_table), page_table.shape[1], _vp(start_pos), n_seq,
+                                       n_tok, hq, dev.stream()))
+    return q, k
