@@ -370,6 +370,7 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
     p.n_q_heads = n_q_heads;
     p.gqa_mode = gqa_mode;
     p.scale = scale;
+    p.item_pages = plan.item_pages;
     PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), "pi_attn_decode");
     return PI_OK;
 }

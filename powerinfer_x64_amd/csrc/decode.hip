@@ -7,7 +7,8 @@
 //
 // Work decomposition: a persistent grid of exactly as many workgroups (4
 // wavefronts each) as the GPU holds at once.  The launch's work is the list of
-// 16-page items of every (sequence, KV head) segment; each workgroup takes an
+// items (16 pages, fewer for small launches) of every (sequence, KV head)
+// segment; each workgroup takes an
 // equal contiguous range of items, found from a prefix scan of the context
 // lengths, so ragged batches are balanced to within one item and no workgroup
 // is left idle.  All query heads that share the KV head (up to 16) ride in the
@@ -161,10 +162,10 @@ __device__ __forceinline__ int head_of(int kvh, int col, int n_kv, int group, in
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Work items of a sequence: ceil(pages / kItemPages) (0 for an empty context).
-__device__ __forceinline__ int items_of(int len) {
+// Work items of a sequence: ceil(pages / item_pages) (0 for an empty context).
+__device__ __forceinline__ int items_of(int len, int item_pages) {
     const int pages = (max(len, 0) + kPageTokens - 1) / kPageTokens;
-    return (pages + kItemPages - 1) / kItemPages;
+    return (pages + item_pages - 1) / item_pages;
 }
 
 // Softmax/PV state of one wavefront: O^T accumulators (lane = head column
@@ -217,13 +218,13 @@ __device__ __forceinline__ void process(Acc<D>& acc, const Tile<KT, D>* tl, cons
 
 // Prefix scan of per-sequence work items into LDS: s_cum[b] = items of
 // sequences < b (per KV head); returns the total over all sequences.
-__device__ __forceinline__ int scan_items(const int32_t* ctx_len, int batch, int* s_cum,
-                                          int* s_red) {
+__device__ __forceinline__ int scan_items(const int32_t* ctx_len, int batch, int item_pages,
+                                          int* s_cum, int* s_red) {
     const int tid = threadIdx.x;
     int carry = 0;
     for (int base = 0; base < batch; base += kThreads) {
         const int b = base + tid;
-        const int n = b < batch ? items_of(ctx_len[b]) : 0;
+        const int n = b < batch ? items_of(ctx_len[b], item_pages) : 0;
         // inclusive scan of n across the block
         int x = n;
 #pragma unroll
@@ -256,7 +257,7 @@ __device__ __forceinline__ int find_seq(const int* s_cum, int batch, int n_kv, i
 }
 
 // Persistent, balanced decode.  The work of a launch is the list of "items"
-// (kItemPages pages of one (sequence, KV head) segment), ordered by sequence
+// (p.item_pages pages of one (sequence, KV head) segment), ordered by sequence
 // then KV head.  Workgroup w owns the contiguous item range
 // [w*chunk, (w+1)*chunk), chunk = ceil(items / gridDim.x), so every
 // workgroup streams the same number of pages and the launch has no tail.
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
 
     const int n_kv = g.n_kv_heads;
     const int tid = threadIdx.x;
-    const int per_kv = scan_items(p.ctx_len, p.batch, s_cum, s_red);
+    const int per_kv = scan_items(p.ctx_len, p.batch, p.item_pages, s_cum, s_red);
     const int n_items = n_kv * per_kv;
     const int chunk = (n_items + gridDim.x - 1) / gridDim.x;
     int cur = blockIdx.x * chunk;
@@ -304,8 +305,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
         const int run_end = min(end, seg0 + nb);
         const int L = p.ctx_len[b];
         const int n_pages_b = (L + kPageTokens - 1) / kPageTokens;
-        const int pg0 = (cur - seg0) * kItemPages;
-        const int pg1 = min(n_pages_b, (run_end - seg0) * kItemPages);
+        const int pg0 = (cur - seg0) * p.item_pages;
+        const int pg1 = min(n_pages_b, (run_end - seg0) * p.item_pages);
         const bool whole = (cur == seg0) && (run_end == seg0 + nb);
 
         const int head = head_of(kvh, col_on ? col : 0, n_kv, group, p.gqa_mode);
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     __shared__ float s_inv[4];
     const int kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
-    const int per_kv = scan_items(p.ctx_len, p.batch, s_cum, s_red);
+    const int per_kv = scan_items(p.ctx_len, p.batch, p.item_pages, s_cum, s_red);
     const int chunk = (n_kv * per_kv + n_wg - 1) / n_wg;
     const int nb = s_cum[b + 1] - s_cum[b];
     const int GD = group * D;
@@ -530,7 +531,14 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
         const int v = std::atoi(e);
         if (v >= 1 && v < kMaxRuns) plan.grid = v;
     }
-    const long long items_per_seq = (max_pages + kItemPages - 1) / kItemPages;
+    // Item size: kItemPages pages, halved while the launch's upper bound of
+    // items would not give every workgroup two items (small batches and short
+    // contexts then still spread over the whole chip).
+    const long long max_seg_pages = (long long)batch * g.n_kv_heads * max_pages;
+    int ip = kItemPages;
+    while (ip > 1 && max_seg_pages / ip < 2LL * plan.grid) ip >>= 1;
+    plan.item_pages = ip;
+    const long long items_per_seq = (max_pages + ip - 1) / ip;
     plan.n_slots = (long long)batch * g.n_kv_heads * items_per_seq;
     plan.group = n_q_heads / g.n_kv_heads;
     return plan;

@@ -7,10 +7,9 @@
 // on a per-head fp32 state S[k_hd][v_hd] (row k, v contiguous).
 //
 // Decode: state columns evolve independently (delta[v] only reads column v),
-// so a workgroup owns (sequence, V head, 16 state columns) -- 256 workgroups
-// for one Qwen3.5 token: 16 row groups of 16 lanes; each thread keeps 8 state
-// values in registers, and the two column sums (S^T k and S^T q) are reduced
-// across the row groups in LDS.
+// so a workgroup owns (sequence, V head, 32 state columns): 8 row groups of
+// 32 lanes; each thread keeps 16 state values in registers, and the two
+// column sums (S^T k and S^T q) are reduced across the row groups in LDS.
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -19,9 +18,9 @@ namespace {
 
 constexpr int DK = 128;
 constexpr int DV = 128;
-constexpr int COLS = 16;             // state columns per decode workgroup
-constexpr int RG = 256 / COLS;       // row groups (16)
-constexpr int RPT = DK / RG;         // state rows per thread (8)
+constexpr int COLS = 32;             // state columns per decode workgroup
+constexpr int RG = 256 / COLS;       // row groups (8)
+constexpr int RPT = DK / RG;         // state rows per thread (16)
 
 __global__ __launch_bounds__(256) void gdn_gates_kernel(const float* __restrict__ beta_raw,
                                                         const float* __restrict__ a_raw,

@@ -9,7 +9,7 @@
 namespace pi {
 
 constexpr int kPageTokens = 16;  // tokens per KV page
-constexpr int kItemPages = 16;   // pages per decode work item (the balancing unit)
+constexpr int kItemPages = 16;   // max pages per decode work item (the balancing unit)
 constexpr int kMaxBatch = 4096;  // sequences per decode launch (LDS prefix scan)
 
 // KV pool geometry: one K and one V block of kPageTokens x head_dim elements
@@ -46,12 +46,14 @@ struct DecodeParams {
     int32_t n_q_heads;
     int32_t gqa_mode;
     float scale;
+    int32_t item_pages;  // pages per work item (power of 2, <= kItemPages), set by decode_plan
 };
 
 struct DecodePlan {
-    int32_t grid;       // persistent workgroups (CUs x resident workgroups per CU)
-    long long n_slots;  // upper bound of work items (partial slots)
-    int32_t group;      // q heads per kv head
+    int32_t grid;        // persistent workgroups (CUs x resident workgroups per CU)
+    long long n_slots;   // upper bound of work items (partial slots)
+    int32_t group;       // q heads per kv head
+    int32_t item_pages;  // pages per work item
 };
 // Grid size and workspace bound of a decode launch on `device`.
 DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
