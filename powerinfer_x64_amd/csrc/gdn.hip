@@ -391,7 +391,13 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(const float* __restrict__
     }
 }
 
-__global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__ q,
+// gdn_scan_kernel: 8 wavefronts walk the chunks in order for one (V head, 16
+// state columns).  Waves 0-3 own the K side (KS, R, Delta) and waves 4-7 the
+// Q side (QS, O) of chunk row block w % 4; the state update is split over all
+// 8 (16 state rows each).  Chunk n+1 is loaded into registers while chunk n
+// computes; the q/k inverse norms are applied when the registers are written
+// to LDS, so no arithmetic waits on those loads.
+__global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__ q,
                                                        const float* __restrict__ k,
                                                        const float* __restrict__ v,
                                                        const float* __restrict__ beta,
@@ -413,48 +419,50 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__
     const int c0 = tile * SCOLS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ln = lane & 15, g4 = lane >> 4;
+    const int rb = wave & 3;          // chunk row block of this wave
+    const bool kside = wave < 4;      // wave-uniform
     const int n_chunks = (n_tok + GC - 1) / GC;
     float* S = state + (size_t)vh * DK * DV;
 
     // S^T tile from the state (row k, column c0 + c)
-    for (int e = tid; e < SCOLS * DK; e += 256) {
+    for (int e = tid; e < SCOLS * DK; e += 512) {
         const int c = e % SCOLS, row = e / SCOLS;
         sst[c * KS_ + row] = S[(size_t)row * DV + c0 + c];
     }
 
     // chunk data staged in registers (prefetch of the next chunk)
-    f32x4 pq[8], pk[8];
-    f32x4 pt[4], pm[4];
+    f32x4 pq[4], pk[4], pt[2], pm[2];
+    float pnq[4], pnk[4];
     float pv[4], plg = 0.f, pb = 0.f;
     auto fetch = [&](int n) {
         const int t0 = n * GC;
 #pragma unroll
-        for (int it = 0; it < 8; ++it) {
-            const int e = tid + 256 * it;
+        for (int it = 0; it < 4; ++it) {
+            const int e = tid + 512 * it;
             const int row = e / (DK / 4), c4 = e % (DK / 4);
             const int t = t0 + row;
-            f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
-            if (t < n_tok) {
-                const float iq = w.rq[(size_t)t * hk + kh], ik = w.rk[(size_t)t * hk + kh];
-                a = *reinterpret_cast<const f32x4*>(q + ((size_t)t * hk + kh) * DK + 4 * c4) * iq;
-                b = *reinterpret_cast<const f32x4*>(k + ((size_t)t * hk + kh) * DK + 4 * c4) * ik;
-            }
-            pq[it] = a;
-            pk[it] = b;
+            const bool in = t < n_tok;
+            const size_t r = (size_t)(in ? t : 0) * hk + kh;
+            pq[it] = *reinterpret_cast<const f32x4*>(q + r * DK + 4 * c4);
+            pk[it] = *reinterpret_cast<const f32x4*>(k + r * DK + 4 * c4);
+            pnq[it] = in ? w.rq[r] : 0.f;
+            pnk[it] = in ? w.rk[r] : 0.f;
         }
         const float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
         const float* mm = w.mm + ((size_t)n * hv + vh) * GC * GC;
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int e = tid + 256 * it;
+        for (int it = 0; it < 2; ++it) {
+            const int e = tid + 512 * it;
             pt[it] = *reinterpret_cast<const f32x4*>(tm + 4 * e);
             pm[it] = *reinterpret_cast<const f32x4*>(mm + 4 * e);
         }
-        // V tile in the MFMA C layout of wave `wave`: rows 16w + 4g + r, column ln
+        // V tile in the MFMA C layout of the K-side waves: rows 16 rb + 4 g + r, column ln
+        if (kside) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = t0 + 16 * wave + 4 * g4 + r;
-            pv[r] = t < n_tok ? v[((size_t)t * hv + vh) * DV + c0 + ln] : 0.f;
+            for (int r = 0; r < 4; ++r) {
+                const int t = t0 + 16 * rb + 4 * g4 + r;
+                pv[r] = t < n_tok ? v[((size_t)t * hv + vh) * DV + c0 + ln] : 0.f;
+            }
         }
         if (tid < GC) {
             plg = w.lg[((size_t)n * hv + vh) * GC + tid];
@@ -464,15 +472,15 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__
     };
     auto stage = [&]() {
 #pragma unroll
-        for (int it = 0; it < 8; ++it) {
-            const int e = tid + 256 * it;
+        for (int it = 0; it < 4; ++it) {
+            const int e = tid + 512 * it;
             const int row = e / (DK / 4), c4 = e % (DK / 4);
-            *reinterpret_cast<f32x4*>(sq + row * KS_ + 4 * c4) = pq[it];
-            *reinterpret_cast<f32x4*>(sk + row * KS_ + 4 * c4) = pk[it];
+            *reinterpret_cast<f32x4*>(sq + row * KS_ + 4 * c4) = pq[it] * pnq[it];
+            *reinterpret_cast<f32x4*>(sk + row * KS_ + 4 * c4) = pk[it] * pnk[it];
         }
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int e = tid + 256 * it;
+        for (int it = 0; it < 2; ++it) {
+            const int e = tid + 512 * it;
             const int row = (4 * e) / GC, c = (4 * e) % GC;
             *reinterpret_cast<f32x4*>(st_ + row * TS_ + c) = pt[it];
             *reinterpret_cast<f32x4*>(sm + row * TS_ + c) = pm[it];
@@ -483,7 +491,7 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__
         }
     };
 
-    float vcur[4];
+    float vcur[4] = {0.f, 0.f, 0.f, 0.f};
     fetch(0);
     stage();
 #pragma unroll
@@ -493,60 +501,60 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__
         const int t0 = n * GC;
         if (n + 1 < n_chunks) fetch(n + 1);
         const float lgC = slg[GC - 1];
-        // KS and QS rows 16w.. of this wave
-        f32x4 ks = {0.f, 0.f, 0.f, 0.f}, qs = ks;
-        ks = tile_mm(sk, KS_, 16 * wave, sst, KS_, 0, DK / 16, ks);
-        qs = tile_mm(sq, KS_, 16 * wave, sst, KS_, 0, DK / 16, qs);
-        // R = beta (V - gamma KS), written transposed
-        {
+        // phase 1: KS (waves 0-3) or QS (waves 4-7), rows 16 rb ..
+        f32x4 xs = {0.f, 0.f, 0.f, 0.f};
+        xs = tile_mm(kside ? sk : sq, KS_, 16 * rb, sst, KS_, 0, DK / 16, xs);
+        if (kside) {  // R = beta (V - gamma KS), written transposed
             f32x4 rv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int i = 16 * wave + 4 * g4 + r;
-                rv[r] = sb[i] * (vcur[r] - expf(slg[i]) * ks[r]);
+                const int i = 16 * rb + 4 * g4 + r;
+                rv[r] = sb[i] * (vcur[r] - expf(slg[i]) * xs[r]);
             }
-            *reinterpret_cast<f32x4*>(srt + ln * TS_ + 16 * wave + 4 * g4) = rv;
+            *reinterpret_cast<f32x4*>(srt + ln * TS_ + 16 * rb + 4 * g4) = rv;
         }
         __syncthreads();
-        // Delta = T R (T lower triangular: column blocks <= wave)
-        f32x4 dl = {0.f, 0.f, 0.f, 0.f};
-        dl = tile_mm(st_, TS_, 16 * wave, srt, TS_, 0, wave + 1, dl);
-        {
+        // phase 2: Delta = T R (T lower triangular: column blocks <= rb)
+        if (kside) {
+            f32x4 dl = {0.f, 0.f, 0.f, 0.f};
+            dl = tile_mm(st_, TS_, 16 * rb, srt, TS_, 0, rb + 1, dl);
             f32x4 dp;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int i = 16 * wave + 4 * g4 + r;
+                const int i = 16 * rb + 4 * g4 + r;
                 dp[r] = expf(lgC - slg[i]) * dl[r];
             }
-            *reinterpret_cast<f32x4*>(sdt + ln * TS_ + 16 * wave + 4 * g4) = dl;
-            *reinterpret_cast<f32x4*>(sdp + ln * TS_ + 16 * wave + 4 * g4) = dp;
+            *reinterpret_cast<f32x4*>(sdt + ln * TS_ + 16 * rb + 4 * g4) = dl;
+            *reinterpret_cast<f32x4*>(sdp + ln * TS_ + 16 * rb + 4 * g4) = dp;
         }
         __syncthreads();
-        // O = gamma QS + M Delta
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-        o = tile_mm(sm, TS_, 16 * wave, sdt, TS_, 0, wave + 1, o);
+        // phase 3a: O = gamma QS + M Delta (waves 4-7)
+        if (!kside) {
+            f32x4 o = {0.f, 0.f, 0.f, 0.f};
+            o = tile_mm(sm, TS_, 16 * rb, sdt, TS_, 0, rb + 1, o);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = 16 * wave + 4 * g4 + r;
-            const int t = t0 + i;
-            if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = expf(slg[i]) * qs[r] + o[r];
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * rb + 4 * g4 + r;
+                const int t = t0 + i;
+                if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = expf(slg[i]) * xs[r] + o[r];
+            }
         }
-        // S^T' = exp(lgC) S^T + Dp^T K : wave w owns state rows 32w .. 32w+31
-        const float gC = expf(lgC);
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            const int row0 = 32 * wave + 16 * blk;
+        // phase 3b: S^T' = exp(lgC) S^T + Dp^T K for state rows 16 w .. 16 w + 15.
+        // Every wave read S^T in phase 1; these rows are only touched by this
+        // wave until the next barrier.
+        {
+            const float gC = expf(lgC);
+            const int row0 = 16 * wave;
             f32x4 acc;
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[r] = gC * sst[(4 * g4 + r) * KS_ + row0 + ln];
+#pragma unroll
             for (int s = 0; s < GC / 16; ++s) {
                 const f32x4 a = *reinterpret_cast<const f32x4*>(sdp + ln * TS_ + 16 * s + 4 * g4);
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     acc = mfma4(a[r], sk[(16 * s + 4 * g4 + r) * KS_ + row0 + ln], acc);
             }
-            // every wave read S^T for KS/QS before the first barrier; rows
-            // row0.. of S^T are only touched by this wave from here on
 #pragma unroll
             for (int r = 0; r < 4; ++r) sst[(4 * g4 + r) * KS_ + row0 + ln] = acc[r];
         }
@@ -558,7 +566,7 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const float* __restrict__
         }
         __syncthreads();
     }
-    for (int e = tid; e < SCOLS * DK; e += 256) {
+    for (int e = tid; e < SCOLS * DK; e += 512) {
         const int c = e % SCOLS, row = e / SCOLS;
         S[(size_t)row * DV + c0 + c] = sst[c * KS_ + row];
     }
@@ -634,7 +642,7 @@ hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, co
                        n_tok, n_k_heads, n_v_heads, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3(n_v_heads * (DV / SCOLS)), dim3(256), 0, s, q, k, v,
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(n_v_heads * (DV / SCOLS)), dim3(512), 0, s, q, k, v,
                        beta, state, out, n_tok, n_k_heads, n_v_heads, w);
     return hipGetLastError();
 }

@@ -62,7 +62,7 @@ __device__ __forceinline__ int head_of(int kvh, int c, int hkv, int group, int m
 // a workgroup covers HPW heads x 256/HPW rows and every K/V byte it stages in
 // LDS serves 8 wavefronts.
 //
-// K and V tiles (64 keys x D) are staged through registers into three LDS
+// K and V tiles (64 keys x D) are staged through registers into four LDS
 // buffers (one barrier per tile): K in its [key][dim] order with 272-byte
 // rows, V transposed to V^T [dim][key] with 136-byte rows, both bank-conflict
 // free for the fragment reads, whose addresses are one base register plus an
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
     constexpr int NW = 8;
     constexpr int RT = NW / HPW;      // row tiles per workgroup
     constexpr int WROWS = ROWS * RT;  // query rows per workgroup
-    constexpr int NBUF = 3;
+    constexpr int NBUF = 4;
     constexpr int KS = D + 8;   // K [key][dim] row stride (elements): 272 B
     constexpr int VT = BN + 4;  // V^T [dim][key] row stride (elements): 136 B
     __shared__ __attribute__((aligned(16))) T sk[NBUF][BN * KS];
@@ -194,14 +194,13 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
     };
     constexpr int PF = 4;  // fragments in flight
 
-    auto tile = [&](int t, bool masked) {
-        const int buf = t % NBUF;
-        const lds_ptr kt = k_lane + buf * (BN * KS);
-        const lds_ptr vt = v_lane + buf * (D * VT);
-        const int k0 = t * BN;
-        // S^T = K . Q^T : two 32x32 tiles (keys 0-31, 32-63), interleaved so
-        // consecutive MFMAs are independent; K fragments read PF ahead
-        f32x16 s[2] = {f32x16{}, f32x16{}};
+    // S^T = K . Q^T for tile t: two 32x32 tiles (keys 0-31, 32-63),
+    // interleaved so consecutive MFMAs are independent; K fragments read PF
+    // ahead
+    auto tile_qk = [&](int t, f32x16* s) {
+        const lds_ptr kt = k_lane + (t % NBUF) * (BN * KS);
+        s[0] = f32x16{};
+        s[1] = f32x16{};
         {
             v8 kf[PF];
 #pragma unroll
@@ -221,7 +220,13 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
             }
             __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
         }
-        // lane holds keys k0 + 32*tt + 8*i + 4*hh + j of query qpos
+    };
+    // The rest of tile t on its scores s: mask, running max, P = exp2, and
+    // O^T += V^T . P^T.  Lane holds keys k0 + 32*tt + 8*i + 4*hh + j of query
+    // qpos.
+    auto tile_rest = [&](int t, f32x16* s, bool masked) {
+        const lds_ptr vt = v_lane + (t % NBUF) * (D * VT);
+        const int k0 = t * BN;
         if (masked) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
@@ -278,12 +283,25 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
         store_tile(1);
     }
     __syncthreads();
-    for (int t = 0; t < n_tiles; ++t) {
+    // Two wave groups in opposite phases.  Between two barriers, waves 0-3
+    // run QK of tile t and then the softmax + PV of tile t; waves 4-7 run the
+    // softmax + PV of tile t-1 (scores kept in registers across the barrier)
+    // and then QK of tile t.  Each SIMD holds one wave of each group, so one
+    // wave's MFMAs overlap the other's softmax.  Tile t lives in buffer
+    // t % 4; the store of tile t+2 goes to the buffer of tile t-2, last read
+    // (V by waves 4-7) before the previous barrier.
+    // The loop runs one step past the last tile for the lagging group.
+    f32x16 s[2];
+    const bool lag = wave >= NW / 2;
+    for (int t = 0; t <= n_tiles; ++t) {
         const bool pre = t + 2 < n_tiles;
         if (pre) load_tile(t + 2);  // in flight while tile t computes
-        if (t < w_tiles) tile(t, t == w_tiles - 1 && last_masked);
-        if (pre) store_tile((t + 2) % NBUF);  // buffer (t+2)%3 was last read at tile t-1
-        __syncthreads();
+        if (!lag && t < w_tiles) tile_qk(t, s);
+        const int tr = lag ? t - 1 : t;  // tile whose softmax + PV runs now
+        if (tr >= 0 && tr < w_tiles) tile_rest(tr, s, tr == w_tiles - 1 && last_masked);
+        if (lag && t < w_tiles) tile_qk(t, s);
+        if (pre) store_tile((t + 2) % NBUF);
+        if (t < n_tiles) __syncthreads();
     }
 
     l_run = wave_sum_xor(l_run, 32);
