@@ -32,6 +32,19 @@ struct Mfma<bf16> {
     static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
+    // sum of the 8 packed values (f32 accumulation, v_dot2 against ones)
+    static __device__ __forceinline__ float sum8(v8 p) {
+        typedef bf16 v2 __attribute__((ext_vector_type(2)));
+        const v2 one = {(bf16)1.0f, (bf16)1.0f};
+        const float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 0, 1), one,
+                                                        0.f, false);
+        const float b = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 4, 5), one,
+                                                        0.f, false);
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 6, 7), one,
+                                               __builtin_amdgcn_fdot2_f32_bf16(
+                                                   __builtin_shufflevector(p, p, 2, 3), one, a, false),
+                                               false) + b;
+    }
 };
 template <>
 struct Mfma<f16> {
@@ -39,6 +52,16 @@ struct Mfma<f16> {
     typedef f16x4 v4;
     static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float sum8(v8 p) {
+        typedef f16 v2 __attribute__((ext_vector_type(2)));
+        const v2 one = {(f16)1.0f, (f16)1.0f};
+        const float a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 0, 1), one, 0.f, false);
+        const float b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 4, 5), one, 0.f, false);
+        return __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 6, 7), one,
+                                      __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 2, 3),
+                                                             one, a, false),
+                                      false) + b;
     }
 };
 
@@ -264,7 +287,8 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) pb[j] = (T)p[j];
-            ls[ks] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            // row sum of the rounded P that the PV product uses
+            ls[ks] = Mfma<T>::sum8(pb);
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) {
                 const int i = 4 * ks + dt;
