@@ -397,3 +397,305 @@ void or_conv1d_silu(float* x, float* hist, const float* w, size_t conv_dim, size
         x[i] = val / (1.0f + expf(-val));
     }
 }
+
+/* ---- TurboQuant compressed KV (src/turboquant/mod.rs) ---------------------------------- */
+
+/* Lloyd-Max centroids for N(0,1) by bit width 1..4 (src/turboquant/mod.rs:27-40). */
+static const float tq_c1[2] = {-0.7979f, 0.7979f};
+static const float tq_c2[4] = {-1.4996f, -0.4950f, 0.4950f, 1.4996f};
+static const float tq_c3[8] = {-2.1520f, -1.3440f, -0.7560f, -0.2451f,
+                               0.2451f,  0.7560f,  1.3440f,  2.1520f};
+static const float tq_c4[16] = {-2.7330f, -2.0690f, -1.6180f, -1.2560f, -0.9424f, -0.6568f,
+                                -0.3880f, -0.1284f, 0.1284f,  0.3880f,  0.6568f,  0.9424f,
+                                1.2560f,  1.6180f,  2.0690f,  2.7330f};
+static const float* tq_centroids(size_t bits) {
+    return bits == 1 ? tq_c1 : bits == 2 ? tq_c2 : bits == 3 ? tq_c3 : tq_c4;
+}
+float or_tq_centroid(size_t bits, size_t j) { return tq_centroids(bits)[j]; }
+
+/* expected_distortion (:372-379) */
+static float tq_distortion(size_t bits) {
+    return bits == 2 ? 0.17f : bits == 3 ? 0.043f : bits == 4 ? 0.011f : 0.17f;
+}
+
+uint64_t or_splitmix64_next(uint64_t* state) {
+    /* :725-731 */
+    *state += 0x9E3779B97F4A7C15ULL;
+    uint64_t z = *state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+float or_splitmix64_gaussian(uint64_t* state) {
+    /* :733-745: u1 = max(next_f64, 1e-10), Box-Muller cosine branch in f64, rounded to f32 */
+    double u1 = (double)(or_splitmix64_next(state) >> 11) / (double)(1ULL << 53);
+    double u2 = (double)(or_splitmix64_next(state) >> 11) / (double)(1ULL << 53);
+    if (u1 < 1e-10) u1 = 1e-10;
+    double r = sqrt(-2.0 * log(u1));
+    double theta = 2.0 * 3.14159265358979323846 * u2;
+    return (float)(r * cos(theta));
+}
+
+void or_tq_gaussian_matrix(float* m, size_t rows, size_t cols, uint64_t seed) {
+    uint64_t st = seed;
+    for (size_t i = 0; i < rows * cols; ++i) m[i] = or_splitmix64_gaussian(&st);
+}
+
+void or_tq_orthogonal(float* q, size_t dim, uint64_t seed) {
+    /* :657-701: Gaussian A (row-major), then per column j: q_j = a_j minus its projections
+     * (dot taken against the original column a_j) on q_0..q_{j-1}, then q_j /= |q_j|. */
+    float* a = (float*)malloc(dim * dim * sizeof(float));
+    or_tq_gaussian_matrix(a, dim, dim, seed);
+    for (size_t j = 0; j < dim; ++j) {
+        for (size_t i = 0; i < dim; ++i) q[i * dim + j] = a[i * dim + j];
+        for (size_t k = 0; k < j; ++k) {
+            float dot = 0.0f;
+            for (size_t i = 0; i < dim; ++i) dot += q[i * dim + k] * a[i * dim + j];
+            for (size_t i = 0; i < dim; ++i) q[i * dim + j] -= dot * q[i * dim + k];
+        }
+        float norm = 0.0f;
+        for (size_t i = 0; i < dim; ++i) norm += q[i * dim + j] * q[i * dim + j];
+        norm = sqrtf(norm);
+        if (norm > 1e-10f)
+            for (size_t i = 0; i < dim; ++i) q[i * dim + j] /= norm;
+    }
+    free(a);
+}
+
+size_t or_tq_compressed_bytes(size_t bits, size_t dim, size_t qjl_bits) {
+    return (bits * dim + 7) / 8 + (qjl_bits + 7) / 8;
+}
+
+void or_tq_pack(uint8_t* out, const uint8_t* idx, size_t n, size_t bits, const uint8_t* signs,
+                size_t n_signs) {
+    /* :591-617 (pack_indices :572-588 is the n_signs == 0 case) */
+    memset(out, 0, (n * bits + n_signs + 7) / 8);
+    size_t pos = 0;
+    for (size_t i = 0; i < n; ++i)
+        for (size_t b = 0; b < bits; ++b, ++pos)
+            if ((idx[i] >> b) & 1) out[pos / 8] |= (uint8_t)(1u << (pos % 8));
+    for (size_t i = 0; i < n_signs; ++i, ++pos)
+        if (signs[i]) out[pos / 8] |= (uint8_t)(1u << (pos % 8));
+}
+
+void or_tq_unpack(uint8_t* idx, uint8_t* signs, const uint8_t* packed, size_t n, size_t bits,
+                  size_t n_signs) {
+    /* :620-654 */
+    size_t pos = 0;
+    for (size_t i = 0; i < n; ++i) {
+        idx[i] = 0;
+        for (size_t b = 0; b < bits; ++b, ++pos)
+            if ((packed[pos / 8] >> (pos % 8)) & 1) idx[i] |= (uint8_t)(1u << b);
+    }
+    for (size_t i = 0; i < n_signs; ++i, ++pos)
+        if (signs) signs[i] = (packed[pos / 8] >> (pos % 8)) & 1;
+}
+
+void or_tq_quantize(uint8_t* packed, const float* x, const float* R, const float* G, size_t dim,
+                    size_t bits, size_t qjl_bits) {
+    /* :128-187 */
+    const float* c = tq_centroids(bits);
+    const size_t nc = (size_t)1 << bits;
+    float* rot = (float*)malloc(dim * sizeof(float));
+    uint8_t* idx = (uint8_t*)malloc(dim);
+    const float scale = sqrtf((float)dim);
+    for (size_t i = 0; i < dim; ++i) {
+        float sum = 0.0f;
+        for (size_t j = 0; j < dim; ++j) sum += R[i * dim + j] * x[j];
+        rot[i] = sum;
+    }
+    for (size_t i = 0; i < dim; ++i) rot[i] *= scale;
+    for (size_t i = 0; i < dim; ++i) {
+        uint8_t best = 0;
+        float best_d = 3.40282347e+38f;
+        for (size_t j = 0; j < nc; ++j) {
+            const float d = fabsf(rot[i] - c[j]);
+            if (d < best_d) {
+                best_d = d;
+                best = (uint8_t)j;
+            }
+        }
+        idx[i] = best;
+    }
+    if (qjl_bits == 0) {
+        or_tq_pack(packed, idx, dim, bits, NULL, 0);
+    } else {
+        uint8_t* sg = (uint8_t*)malloc(qjl_bits);
+        for (size_t i = 0; i < dim; ++i) rot[i] = rot[i] - c[idx[i]]; /* residual */
+        for (size_t i = 0; i < qjl_bits; ++i) {
+            float proj = 0.0f;
+            for (size_t j = 0; j < dim; ++j) proj += G[i * dim + j] * rot[j];
+            sg[i] = proj >= 0.0f;
+        }
+        or_tq_pack(packed, idx, dim, bits, sg, qjl_bits);
+        free(sg);
+    }
+    free(idx);
+    free(rot);
+}
+
+void or_tq_dequantize(float* out, const uint8_t* packed, const float* R, size_t dim, size_t bits) {
+    /* :194-216 */
+    const float* c = tq_centroids(bits);
+    uint8_t* idx = (uint8_t*)malloc(dim);
+    float* rec = (float*)malloc(dim * sizeof(float));
+    or_tq_unpack(idx, NULL, packed, dim, bits, 0);
+    const float inv_scale = 1.0f / sqrtf((float)dim);
+    for (size_t i = 0; i < dim; ++i) rec[i] = c[idx[i]] * inv_scale;
+    for (size_t i = 0; i < dim; ++i) {
+        float sum = 0.0f;
+        for (size_t j = 0; j < dim; ++j) sum += R[j * dim + i] * rec[j];
+        out[i] = sum;
+    }
+    free(rec);
+    free(idx);
+}
+
+float or_tq_dot(const float* q, const uint8_t* packed, const float* R, const float* G, size_t dim,
+                size_t bits, size_t qjl_bits) {
+    if (qjl_bits == 0) { /* :229-238 */
+        float* kd = (float*)malloc(dim * sizeof(float));
+        or_tq_dequantize(kd, packed, R, dim, bits);
+        float dot = 0.0f;
+        for (size_t i = 0; i < dim; ++i) dot += q[i] * kd[i];
+        free(kd);
+        return dot;
+    }
+    /* asymmetric_dot (:323-369) */
+    const float* c = tq_centroids(bits);
+    uint8_t* idx = (uint8_t*)malloc(dim);
+    uint8_t* sg = (uint8_t*)malloc(qjl_bits);
+    float* qr = (float*)malloc(dim * sizeof(float));
+    or_tq_unpack(idx, sg, packed, dim, bits, qjl_bits);
+    const float inv_scale = 1.0f / sqrtf((float)dim);
+    for (size_t i = 0; i < dim; ++i) {
+        float sum = 0.0f;
+        for (size_t j = 0; j < dim; ++j) sum += R[i * dim + j] * q[j];
+        qr[i] = sum;
+    }
+    float mse = 0.0f;
+    for (size_t i = 0; i < dim; ++i) mse += qr[i] * c[idx[i]] * inv_scale;
+    const float residual_norm = sqrtf(tq_distortion(bits) * inv_scale);
+    float qjl = 0.0f;
+    for (size_t i = 0; i < qjl_bits; ++i) {
+        float proj = 0.0f;
+        for (size_t j = 0; j < dim; ++j) proj += G[i * dim + j] * qr[j];
+        qjl += proj * (sg[i] ? 1.0f : -1.0f);
+    }
+    const float qjl_scale = sqrtf(3.14159274f / (2.0f * (float)qjl_bits));
+    const float corr = residual_norm * qjl_scale * qjl * inv_scale;
+    free(qr);
+    free(sg);
+    free(idx);
+    return mse + corr;
+}
+
+void or_tq_precompute_query(float* q_rot, float* qjl_proj, const float* q, const float* R,
+                            const float* G, size_t dim, size_t qjl_bits) {
+    /* :244-278 */
+    const float scale = sqrtf((float)dim);
+    const float inv_scale = 1.0f / scale;
+    for (size_t i = 0; i < dim; ++i) {
+        float sum = 0.0f;
+        for (size_t j = 0; j < dim; ++j) sum += R[i * dim + j] * q[j];
+        q_rot[i] = sum;
+    }
+    for (size_t i = 0; i < qjl_bits; ++i) {
+        float proj = 0.0f;
+        for (size_t j = 0; j < dim; ++j) proj += G[i * dim + j] * q_rot[j];
+        qjl_proj[i] = proj * inv_scale;
+    }
+    for (size_t i = 0; i < dim; ++i) q_rot[i] *= inv_scale;
+}
+
+float or_tq_dot_precomputed(const float* q_rot, const float* qjl_proj, const uint8_t* packed,
+                            size_t dim, size_t bits, size_t qjl_bits) {
+    /* :281-320 */
+    const float* c = tq_centroids(bits);
+    uint8_t* idx = (uint8_t*)malloc(dim);
+    uint8_t* sg = (uint8_t*)malloc(qjl_bits ? qjl_bits : 1);
+    or_tq_unpack(idx, sg, packed, dim, bits, qjl_bits);
+    float mse = 0.0f;
+    for (size_t i = 0; i < dim; ++i) mse += q_rot[i] * c[idx[i]];
+    float res = mse;
+    if (qjl_bits > 0) {
+        const float inv_scale = 1.0f / sqrtf((float)dim);
+        const float residual_norm = sqrtf(tq_distortion(bits) * inv_scale);
+        float qjl = 0.0f;
+        for (size_t i = 0; i < qjl_bits; ++i) qjl += qjl_proj[i] * (sg[i] ? 1.0f : -1.0f);
+        const float qjl_scale = sqrtf(3.14159274f / (2.0f * (float)qjl_bits));
+        res = mse + residual_norm * qjl_scale * qjl;
+    }
+    free(sg);
+    free(idx);
+    return res;
+}
+
+void or_tq_cache_append_keys(uint8_t* packed, float* norms, const float* keys, const float* R,
+                             const float* G, size_t n_kv, size_t dim) {
+    /* :455-486 with TurboQuant::new(3, dim, dim, .) per head (:430-437) */
+    const size_t nb = or_tq_compressed_bytes(3, dim, dim);
+    float* xn = (float*)malloc(dim * sizeof(float));
+    for (size_t h = 0; h < n_kv; ++h) {
+        const float* x = keys + h * dim;
+        float ss = 0.0f;
+        for (size_t i = 0; i < dim; ++i) ss += x[i] * x[i];
+        const float norm = sqrtf(ss);
+        const float inv = norm > 1e-12f ? 1.0f / norm : 0.0f;
+        for (size_t i = 0; i < dim; ++i) xn[i] = x[i] * inv;
+        or_tq_quantize(packed + h * nb, xn, R + h * dim * dim, G + h * dim * dim, dim, 3, dim);
+        norms[h] = norm;
+    }
+    free(xn);
+}
+
+/* IEEE binary16 bits -> float (exact). */
+static float half_to_float(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31, m = h & 1023;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = s;
+        } else { /* subnormal: m * 2^-24 */
+            float f = (float)m * 5.9604644775390625e-08f;
+            return (h >> 15) ? -f : f;
+        }
+    } else if (e == 31) {
+        bits = s | 0x7F800000u | (m << 13);
+    } else {
+        bits = s | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+void or_tq_cache_attend(float* out, const float* q_head, const uint8_t* packed, const float* norms,
+                        const uint16_t* values, const float* R, const float* G, size_t T,
+                        size_t n_kv, size_t kv_h, size_t dim) {
+    /* attention_scores (:489-516) with the precomputed query, ops::softmax (src/ops.rs:160-180),
+     * weighted_value_sum (:519-536), which skips weights below 1e-7. */
+    const size_t nb = or_tq_compressed_bytes(3, dim, dim);
+    const float scale = 1.0f / sqrtf((float)dim);
+    float* qr = (float*)malloc(dim * sizeof(float));
+    float* qp = (float*)malloc(dim * sizeof(float));
+    float* sc = (float*)malloc((T ? T : 1) * sizeof(float));
+    or_tq_precompute_query(qr, qp, q_head, R, G, dim, dim);
+    for (size_t t = 0; t < T; ++t) {
+        const float kn = norms[t * n_kv + kv_h];
+        sc[t] = kn * or_tq_dot_precomputed(qr, qp, packed + (t * n_kv + kv_h) * nb, dim, 3, dim) *
+                scale;
+    }
+    or_softmax(sc, T);
+    for (size_t d = 0; d < dim; ++d) out[d] = 0.0f;
+    for (size_t t = 0; t < T; ++t) {
+        const float w = sc[t];
+        if (w < 1e-7f) continue;
+        const uint16_t* v = values + (t * n_kv + kv_h) * dim;
+        for (size_t d = 0; d < dim; ++d) out[d] += w * half_to_float(v[d]);
+    }
+    free(sc);
+    free(qp);
+    free(qr);
+}

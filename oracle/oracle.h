@@ -114,6 +114,48 @@ void or_rmsnorm_gated(float* o, const float* z, const float* w, size_t n_v_heads
  * x: [conv_dim] new input, overwritten with the activation; hist is shifted. */
 void or_conv1d_silu(float* x, float* hist, const float* w, size_t conv_dim, size_t d_conv);
 
+/* ---- TurboQuant compressed KV (src/turboquant/mod.rs) ---------------------------------- */
+/* SplitMix64 step and its Box-Muller Gaussian (:719-746). */
+uint64_t or_splitmix64_next(uint64_t* state);
+float or_splitmix64_gaussian(uint64_t* state);
+/* Random orthogonal [dim x dim] by Gram-Schmidt of a seeded Gaussian matrix (:657-701). */
+void or_tq_orthogonal(float* q, size_t dim, uint64_t seed);
+/* Seeded Gaussian [rows x cols] (:704-711). */
+void or_tq_gaussian_matrix(float* m, size_t rows, size_t cols, uint64_t seed);
+/* Lloyd-Max centroid j of the bits-wide codebook (:27-40). */
+float or_tq_centroid(size_t bits, size_t j);
+/* Packed bytes of one vector (:111-118). */
+size_t or_tq_compressed_bytes(size_t bits, size_t dim, size_t qjl_bits);
+/* Bit packing, LSB first: indices then sign bits (:572-654). */
+void or_tq_pack(uint8_t* out, const uint8_t* idx, size_t n, size_t bits, const uint8_t* signs,
+                size_t n_signs);
+void or_tq_unpack(uint8_t* idx, uint8_t* signs, const uint8_t* packed, size_t n, size_t bits,
+                  size_t n_signs);
+/* quantize_vector (:128-187): rotation R [dim][dim], QJL matrix G [qjl_bits][dim] (NULL
+ * when qjl_bits == 0); writes or_tq_compressed_bytes() bytes. */
+void or_tq_quantize(uint8_t* packed, const float* x, const float* R, const float* G, size_t dim,
+                    size_t bits, size_t qjl_bits);
+/* dequantize_vector (:194-216). */
+void or_tq_dequantize(float* out, const uint8_t* packed, const float* R, size_t dim, size_t bits);
+/* dot (:225-241) -- MSE-only dequantize-and-dot, or the asymmetric QJL estimator (:323-369). */
+float or_tq_dot(const float* q, const uint8_t* packed, const float* R, const float* G, size_t dim,
+                size_t bits, size_t qjl_bits);
+/* precompute_query (:244-278) and dot_precomputed (:281-320). */
+void or_tq_precompute_query(float* q_rot, float* qjl_proj, const float* q, const float* R,
+                            const float* G, size_t dim, size_t qjl_bits);
+float or_tq_dot_precomputed(const float* q_rot, const float* qjl_proj, const uint8_t* packed,
+                            size_t dim, size_t bits, size_t qjl_bits);
+/* CompressedKVCache::append for one token (:455-486), keys only: per KV head the L2 norm and
+ * the 3-bit + QJL packed key.  R, G: [n_kv][dim][dim].  packed: [n_kv][bytes]. */
+void or_tq_cache_append_keys(uint8_t* packed, float* norms, const float* keys, const float* R,
+                             const float* G, size_t n_kv, size_t dim);
+/* attention_scores (:489-516) + ops::softmax + weighted_value_sum (:519-536) for one query
+ * head over T tokens of KV head kv_h.  packed [T][n_kv][bytes], norms [T][n_kv], values
+ * [T][n_kv][dim] as f16 bits, R, G of that KV head. */
+void or_tq_cache_attend(float* out, const float* q_head, const uint8_t* packed, const float* norms,
+                        const uint16_t* values, const float* R, const float* G, size_t T,
+                        size_t n_kv, size_t kv_h, size_t dim);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,9 @@ _lib = None
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _sz = ctypes.c_size_t
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
 
 
 def build() -> str:
@@ -60,6 +63,22 @@ def lib():
                                      _sz, _sz, _sz]),
             "or_rmsnorm_gated": (None, [_f32p, _f32p, _f32p, _sz, _sz, ctypes.c_float]),
             "or_conv1d_silu": (None, [_f32p, _f32p, _f32p, _sz, _sz]),
+            "or_splitmix64_next": (ctypes.c_uint64, [_u64p]),
+            "or_splitmix64_gaussian": (ctypes.c_float, [_u64p]),
+            "or_tq_orthogonal": (None, [_f32p, _sz, ctypes.c_uint64]),
+            "or_tq_gaussian_matrix": (None, [_f32p, _sz, _sz, ctypes.c_uint64]),
+            "or_tq_compressed_bytes": (_sz, [_sz, _sz, _sz]),
+            "or_tq_centroid": (ctypes.c_float, [_sz, _sz]),
+            "or_tq_pack": (None, [_u8p, _u8p, _sz, _sz, _u8p, _sz]),
+            "or_tq_unpack": (None, [_u8p, _u8p, _u8p, _sz, _sz, _sz]),
+            "or_tq_quantize": (None, [_u8p, _f32p, _f32p, _f32p, _sz, _sz, _sz]),
+            "or_tq_dequantize": (None, [_f32p, _u8p, _f32p, _sz, _sz]),
+            "or_tq_dot": (ctypes.c_float, [_f32p, _u8p, _f32p, _f32p, _sz, _sz, _sz]),
+            "or_tq_precompute_query": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz]),
+            "or_tq_dot_precomputed": (ctypes.c_float, [_f32p, _f32p, _u8p, _sz, _sz, _sz]),
+            "or_tq_cache_append_keys": (None, [_u8p, _f32p, _f32p, _f32p, _f32p, _sz, _sz]),
+            "or_tq_cache_attend": (None, [_f32p, _f32p, _u8p, _f32p, _u16p, _f32p, _f32p, _sz,
+                                          _sz, _sz, _sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -263,3 +282,117 @@ def conv1d_silu(x, hist, w, d_conv):
     ww = _f32(w)
     lib().or_conv1d_silu(_p(x), _p(h), _p(ww), x.size, d_conv)
     return x, h
+
+
+# ---- src/turboquant/mod.rs -------------------------------------------------
+
+def _u8(a):
+    arr = np.ascontiguousarray(a, dtype=np.uint8)
+    return arr, arr.ctypes.data_as(_u8p)
+
+
+def splitmix64(seed: int, n: int):
+    """First n outputs of SplitMix64(seed) (src/turboquant/mod.rs:725-731)."""
+    st = ctypes.c_uint64(seed)
+    return [int(lib().or_splitmix64_next(ctypes.byref(st))) for _ in range(n)]
+
+
+def splitmix64_gaussians(seed: int, n: int):
+    st = ctypes.c_uint64(seed)
+    return np.array([lib().or_splitmix64_gaussian(ctypes.byref(st)) for _ in range(n)],
+                    dtype=np.float32)
+
+
+def tq_orthogonal(dim: int, seed: int):
+    out = np.empty((dim, dim), dtype=np.float32)
+    lib().or_tq_orthogonal(_p(out), dim, seed)
+    return out
+
+
+def tq_gaussian_matrix(rows: int, cols: int, seed: int):
+    out = np.empty((rows, cols), dtype=np.float32)
+    lib().or_tq_gaussian_matrix(_p(out), rows, cols, seed)
+    return out
+
+
+def tq_matrices(dim: int, seed: int, qjl_bits: int = None):
+    """(rotation, QJL matrix) of TurboQuant::new(bits, dim, qjl_bits, seed) (:76-103)."""
+    qjl_bits = dim if qjl_bits is None else qjl_bits
+    g = tq_gaussian_matrix(qjl_bits, dim, seed ^ 0xDEADBEEF) if qjl_bits else None
+    return tq_orthogonal(dim, seed), g
+
+
+def tq_centroids(bits: int):
+    return np.array([lib().or_tq_centroid(bits, j) for j in range(1 << bits)], dtype=np.float32)
+
+
+def tq_compressed_bytes(bits: int, dim: int, qjl_bits: int) -> int:
+    return int(lib().or_tq_compressed_bytes(bits, dim, qjl_bits))
+
+
+def tq_pack(idx, bits: int, signs=()):
+    idx, pi = _u8(idx)
+    sg, ps = _u8(np.asarray(signs, dtype=np.uint8).reshape(-1))
+    out = np.zeros((idx.size * bits + sg.size + 7) // 8, dtype=np.uint8)
+    lib().or_tq_pack(out.ctypes.data_as(_u8p), pi, idx.size, bits, ps, sg.size)
+    return out
+
+
+def tq_unpack(packed, n: int, bits: int, n_signs: int = 0):
+    pk, pp = _u8(packed)
+    idx = np.zeros(n, dtype=np.uint8)
+    sg = np.zeros(max(n_signs, 1), dtype=np.uint8)
+    lib().or_tq_unpack(idx.ctypes.data_as(_u8p), sg.ctypes.data_as(_u8p), pp, n, bits, n_signs)
+    return idx, sg[:n_signs]
+
+
+def tq_quantize(x, R, G, bits: int, qjl_bits: int):
+    x, R = _f32(x), _f32(R)
+    G = _f32(G) if G is not None else None
+    dim = x.size
+    out = np.zeros(tq_compressed_bytes(bits, dim, qjl_bits), dtype=np.uint8)
+    lib().or_tq_quantize(out.ctypes.data_as(_u8p), _p(x), _p(R), _p(G), dim, bits, qjl_bits)
+    return out
+
+
+def tq_dequantize(packed, R, bits: int):
+    R = _f32(R)
+    dim = R.shape[0]
+    pk, pp = _u8(packed)
+    out = np.empty(dim, dtype=np.float32)
+    lib().or_tq_dequantize(_p(out), pp, _p(R), dim, bits)
+    return out
+
+
+def tq_dot(q, packed, R, G, bits: int, qjl_bits: int) -> float:
+    q, R = _f32(q), _f32(R)
+    G = _f32(G) if G is not None else None
+    pk, pp = _u8(packed)
+    return float(lib().or_tq_dot(_p(q), pp, _p(R), _p(G), q.size, bits, qjl_bits))
+
+
+def tq_cache_append_keys(keys, R, G):
+    """keys [n_kv, dim] of one token -> (packed [n_kv, 64-byte records], norms [n_kv]);
+    R, G [n_kv, dim, dim] (CompressedKVCache::append, :455-486)."""
+    k, R, G = _f32(keys), _f32(R), _f32(G)
+    n_kv, dim = k.shape
+    nb = tq_compressed_bytes(3, dim, dim)
+    packed = np.zeros((n_kv, nb), dtype=np.uint8)
+    norms = np.zeros(n_kv, dtype=np.float32)
+    lib().or_tq_cache_append_keys(packed.ctypes.data_as(_u8p), _p(norms), _p(k), _p(R), _p(G),
+                                  n_kv, dim)
+    return packed, norms
+
+
+def tq_cache_attend(q_head, packed, norms, values_f16, R, G, kv_h: int):
+    """One query head over a compressed cache: packed [T, n_kv, nb] uint8, norms [T, n_kv],
+    values_f16 [T, n_kv, dim] float16, R, G [dim, dim] of KV head kv_h."""
+    q, nm, R, G = _f32(q_head), _f32(norms), _f32(R), _f32(G)
+    pk, pp = _u8(packed)
+    vals = np.ascontiguousarray(values_f16, dtype=np.float16).view(np.uint16)
+    T, n_kv, dim = vals.shape
+    out = np.zeros(dim, dtype=np.float32)
+    lib().or_tq_cache_attend(_p(out), _p(q), pp, _p(nm), vals.ctypes.data_as(_u16p), _p(R),
+                             _p(G), T, n_kv, kv_h, dim)
+    return out
+

@@ -25,6 +25,12 @@ CFLAGS = [
 ]
 
 
+# Per-file additions: the TurboQuant quantizer (device) and its matrix
+# generation (host) reproduce the reference's separately rounded multiply and
+# add, so nothing in them may fuse into an FMA.
+FILE_FLAGS = {"turboquant.hip": ["-ffp-contract=off"], "api.cpp": ["-ffp-contract=off"]}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC)
                   if f.endswith(".hip") or f.endswith(".cpp"))
@@ -33,7 +39,7 @@ def sources():
 def _compile(src: str) -> str:
     obj = os.path.join(OUT_DIR, os.path.basename(src) + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
-    cmd = [HIPCC, *CFLAGS, *lang, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(os.path.basename(src), []), *lang, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

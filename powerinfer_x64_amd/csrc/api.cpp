@@ -13,8 +13,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <new>
 #include <string>
+#include <vector>
 
 struct pi_handle_s {
     int device = 0;
@@ -24,11 +26,19 @@ struct pi_handle_s {
     pi::GdnWorkspace gws{};
     float* h2d_scratch = nullptr;  // device staging for the host-slice drop-ins
     size_t h2d_floats = 0;
+    float* tq_qv = nullptr;        // TurboQuant virtual queries [batch][Hq][256]
+    size_t tq_qv_floats = 0;
 };
 
 struct pi_kv_pool_s {
     pi_handle owner;
     pi::KvGeom g;
+    size_t bytes;
+};
+
+struct pi_tq_pool_s {
+    pi_handle owner;
+    pi::TqPool t;
     size_t bytes;
 };
 
@@ -114,6 +124,55 @@ void imrope_freqs(float base, int n_rot, float* f) {
     }
 }
 
+// ---- TurboQuant matrices (src/turboquant/mod.rs:657-746) ----------------------
+// SplitMix64 with the reference's Box-Muller Gaussian: two f64 uniforms from
+// the top 53 bits, u1 clamped to 1e-10, r * cos(theta) rounded to f32.
+struct SplitMix64 {
+    uint64_t state;
+    uint64_t next() {
+        state += 0x9E3779B97F4A7C15ULL;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        return z ^ (z >> 31);
+    }
+    double uniform() { return (double)(next() >> 11) / (double)(1ULL << 53); }
+    float gaussian() {
+        const double u1 = std::max(uniform(), 1e-10);
+        const double u2 = uniform();
+        return (float)(std::sqrt(-2.0 * std::log(u1)) * std::cos(2.0 * M_PI * u2));
+    }
+};
+
+// Orthogonal Q of a seeded Gaussian A by Gram-Schmidt over columns, in f32
+// with separately rounded operations (this file is built without FMA
+// contraction): q_j = a_j - sum_k (q_k . a_j) q_k, then q_j /= |q_j| when
+// |q_j| > 1e-10.  The projections use the original column a_j.
+void tq_orthogonal(float* q, int dim, uint64_t seed) {
+    std::vector<float> a((size_t)dim * dim);
+    SplitMix64 rng{seed};
+    for (float& x : a) x = rng.gaussian();
+    for (int j = 0; j < dim; ++j) {
+        for (int i = 0; i < dim; ++i) q[(size_t)i * dim + j] = a[(size_t)i * dim + j];
+        for (int k = 0; k < j; ++k) {
+            float dot = 0.0f;
+            for (int i = 0; i < dim; ++i) dot += q[(size_t)i * dim + k] * a[(size_t)i * dim + j];
+            for (int i = 0; i < dim; ++i) q[(size_t)i * dim + j] -= dot * q[(size_t)i * dim + k];
+        }
+        float nrm = 0.0f;
+        for (int i = 0; i < dim; ++i) nrm += q[(size_t)i * dim + j] * q[(size_t)i * dim + j];
+        nrm = std::sqrt(nrm);
+        if (nrm > 1e-10f)
+            for (int i = 0; i < dim; ++i) q[(size_t)i * dim + j] /= nrm;
+    }
+}
+
+void tq_matrices(int dim, uint64_t seed, float* rot, float* qjl) {
+    tq_orthogonal(rot, dim, seed);
+    SplitMix64 rng{seed ^ 0xDEADBEEFULL};
+    for (size_t i = 0; i < (size_t)dim * dim; ++i) qjl[i] = rng.gaussian();
+}
+
 }  // namespace
 
 extern "C" {
@@ -157,6 +216,7 @@ void pi_destroy(pi_handle h) {
     (void)hipFree(h->dws.partial_ml);
     (void)hipFree(h->gws.buf);
     (void)hipFree(h->h2d_scratch);
+    (void)hipFree(h->tq_qv);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
 }
@@ -694,6 +754,169 @@ int pi_ssm_gated_delta_step(pi_handle h, float* h_out, float* h_state, const flo
     if ((rc = copy_sync(h, h_state, ds, ns * 4, hipMemcpyDeviceToHost, "gated_delta_step"))) return rc;
     if ((rc = copy_sync(h, h_out, dout, nv * 4, hipMemcpyDeviceToHost, "gated_delta_step"))) return rc;
     PI_HIP(h, hipStreamSynchronize(h->stream), "gated_delta_step");
+    return PI_OK;
+}
+
+// ---- TurboQuant compressed KV ------------------------------------------------------
+
+int pi_tq_generate(int32_t dim, uint64_t seed, float* h_rotation, float* h_qjl) {
+    if (!h_rotation || !h_qjl) return fail(nullptr, PI_ERR_INVALID_ARG, "pi_tq_generate: null argument");
+    if (dim <= 0 || dim > 4096) return fail(nullptr, PI_ERR_INVALID_ARG, "pi_tq_generate: dim %d", dim);
+    tq_matrices(dim, seed, h_rotation, h_qjl);
+    return PI_OK;
+}
+
+int pi_tq_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t n_kv_heads,
+                      int32_t head_dim, pi_tq_pool* out) {
+    PI_CHECK_HANDLE(h);
+    if (!out) return fail(h, PI_ERR_INVALID_ARG, "pi_tq_pool_create: out is null");
+    *out = nullptr;
+    if (page_tokens != pi::kPageTokens)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_pool_create: page_tokens must be 16 (got %d)", page_tokens);
+    if (n_pages <= 0 || n_kv_heads <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_pool_create: n_pages=%d n_kv_heads=%d", n_pages, n_kv_heads);
+    if (head_dim != 128)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_pool_create: head_dim %d (128)", head_dim);
+    const int D = 128;
+    const size_t nblk = (size_t)n_pages * n_kv_heads;
+    const size_t kbytes = nblk * pi::kPageTokens * (pi::kTqKeyBytes + 4);
+    const size_t vbytes = nblk * pi::kPageTokens * D * 2;
+    const size_t mbytes = (size_t)n_kv_heads * D * D * sizeof(float);
+    // per-head matrices, transposed for the kernels (TurboQuant::new(3, 128, 128,
+    // 0xCAFE_BABE + h), src/turboquant/mod.rs:430-437)
+    std::vector<float> rot((size_t)D * D), qjl((size_t)D * D);
+    std::vector<float> rt((size_t)n_kv_heads * D * D), gt((size_t)n_kv_heads * D * D);
+    for (int kh = 0; kh < n_kv_heads; ++kh) {
+        tq_matrices(D, 0xCAFEBABEULL + (uint64_t)kh, rot.data(), qjl.data());
+        for (int i = 0; i < D; ++i)
+            for (int j = 0; j < D; ++j) {
+                rt[((size_t)kh * D + j) * D + i] = rot[(size_t)i * D + j];
+                gt[((size_t)kh * D + j) * D + i] = qjl[(size_t)i * D + j];
+            }
+    }
+    PI_HIP(h, hipSetDevice(h->device), "pi_tq_pool_create");
+    pi_tq_pool p = new (std::nothrow) pi_tq_pool_s();
+    if (!p) return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_tq_pool_create: host allocation");
+    p->owner = h;
+    p->bytes = kbytes + vbytes + 2 * mbytes;
+    pi::TqPool& t = p->t;
+    t.g = pi::KvGeom{nullptr, nullptr, n_pages, n_kv_heads, D, pi::kTqDtype, 0};
+    t.rt = t.gt = nullptr;
+    t.scale = std::sqrt((float)D);
+    // residual_norm * qjl_scale of the 3-bit estimator (src/turboquant/mod.rs:297-316)
+    t.corr = std::sqrt(0.043f * (1.0f / t.scale)) * std::sqrt(3.14159274f / (2.0f * (float)D));
+    hipError_t e = hipMalloc(&t.g.k, kbytes);
+    if (e == hipSuccess) e = hipMalloc(&t.g.v, vbytes);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&t.rt), mbytes);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&t.gt), mbytes);
+    if (e == hipSuccess) e = hipMemset(t.g.k, 0, kbytes);
+    if (e == hipSuccess) e = hipMemset(t.g.v, 0, vbytes);
+    if (e == hipSuccess) e = hipMemcpy(t.rt, rt.data(), mbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(t.gt, gt.data(), mbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(t.g.k);
+        (void)hipFree(t.g.v);
+        (void)hipFree(t.rt);
+        (void)hipFree(t.gt);
+        delete p;
+        return hip_fail(h, e, "pi_tq_pool_create");
+    }
+    *out = p;
+    return PI_OK;
+}
+
+void pi_tq_pool_destroy(pi_tq_pool pool) {
+    if (!pool) return;
+    (void)hipSetDevice(pool->owner->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(pool->t.g.k);
+    (void)hipFree(pool->t.g.v);
+    (void)hipFree(pool->t.rt);
+    (void)hipFree(pool->t.gt);
+    delete pool;
+}
+
+size_t pi_tq_pool_bytes(pi_tq_pool pool) { return pool ? pool->bytes : 0; }
+
+int pi_tq_append(pi_handle h, pi_tq_pool pool, const float* d_k, const float* d_v,
+                 const int32_t* d_page_table, int32_t max_pages, const int32_t* d_start_pos,
+                 int32_t n_seq, int32_t n_tok, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!pool || !d_k || !d_v || !d_page_table || !d_start_pos)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_append: null argument");
+    if (n_seq < 0 || n_tok < 0 || max_pages <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_append: n_seq=%d n_tok=%d max_pages=%d", n_seq, n_tok, max_pages);
+    if (n_seq == 0 || n_tok == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_tq_append");
+    PI_HIP(h, pi::launch_tq_append(pool->t, d_k, d_v, d_page_table, max_pages, d_start_pos, n_seq,
+                                   n_tok, pick(h, stream)),
+           "pi_tq_append");
+    return PI_OK;
+}
+
+int pi_tq_read(pi_handle h, pi_tq_pool pool, const int32_t* d_page_table, int32_t max_pages,
+               int32_t seq, int32_t start, int32_t n_tok, uint8_t* d_keys_out, float* d_norms_out,
+               uint16_t* d_values_out, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!pool || !d_page_table || !d_keys_out || !d_norms_out || !d_values_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_read: null argument");
+    if (seq < 0 || start < 0 || n_tok < 0 || max_pages <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_read: seq=%d start=%d n_tok=%d", seq, start, n_tok);
+    if (n_tok == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_tq_read");
+    PI_HIP(h, pi::launch_tq_read(pool->t, d_page_table, max_pages, seq, start, n_tok, d_keys_out,
+                                 d_norms_out, d_values_out, pick(h, stream)),
+           "pi_tq_read");
+    return PI_OK;
+}
+
+int pi_tq_attn_decode(pi_handle h, const float* d_q, pi_tq_pool pool, const int32_t* d_page_table,
+                      int32_t max_pages, const int32_t* d_ctx_len, int32_t batch,
+                      int32_t n_q_heads, int32_t gqa_mode, const float* d_gate, float* d_out,
+                      void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!pool || !d_q || !d_page_table || !d_ctx_len || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_attn_decode: null argument");
+    const pi::KvGeom& g = pool->t.g;
+    if (batch < 0 || max_pages <= 0 || n_q_heads <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_attn_decode: batch=%d max_pages=%d n_q_heads=%d", batch, max_pages, n_q_heads);
+    if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_attn_decode: gqa_mode %d", gqa_mode);
+    if (n_q_heads % g.n_kv_heads != 0)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_attn_decode: n_q_heads %d not a multiple of n_kv_heads %d", n_q_heads, g.n_kv_heads);
+    const int group = n_q_heads / g.n_kv_heads;
+    if (group > 16)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_attn_decode: %d q heads per kv head", group);
+    if (batch > pi::kMaxBatch)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_attn_decode: batch %d > %d", batch, pi::kMaxBatch);
+    if ((long long)batch * g.n_kv_heads * ((max_pages + pi::kItemPages - 1) / pi::kItemPages) > (1LL << 30))
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_attn_decode: batch x kv heads x pages too large");
+    if (batch == 0) return PI_OK;
+    hipStream_t s = pick(h, stream);
+    PI_HIP(h, hipSetDevice(h->device), "pi_tq_attn_decode");
+    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
+    const size_t need_o = pi::decode_ws_floats_o(g, plan);
+    const size_t need_ml = need_o / g.head_dim * 2;
+    const size_t need_qv = (size_t)batch * n_q_heads * 2 * g.head_dim;
+    int rc;
+    if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_tq_attn_decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_tq_attn_decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->tq_qv, &h->tq_qv_floats, need_qv, s, "pi_tq_attn_decode workspace", false))) return rc;
+    PI_HIP(h, pi::launch_tq_query(pool->t, d_q, h->tq_qv, batch, n_q_heads, gqa_mode, s),
+           "pi_tq_attn_decode");
+    pi::DecodeParams p;
+    p.q = h->tq_qv;
+    p.page_table = d_page_table;
+    p.ctx_len = d_ctx_len;
+    p.gate = d_gate;
+    p.out = d_out;
+    p.max_pages = max_pages;
+    p.batch = batch;
+    p.n_q_heads = n_q_heads;
+    p.gqa_mode = gqa_mode;
+    p.scale = 1.0f / std::sqrt((float)g.head_dim);  // src/turboquant/mod.rs:490
+    p.item_pages = plan.item_pages;
+    PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), "pi_tq_attn_decode");
     return PI_OK;
 }
 

@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 namespace pi {
 namespace {
@@ -55,14 +56,18 @@ template <int D>
 struct Tile<f16, D> {
     static constexpr int NK = D / 32;  // K loads (16 B) per lane per page
     static constexpr int NV = D / 16;  // V loads (8 B) per lane per page
+    static constexpr size_t KBLK = (size_t)kPageTokens * D * 2;  // bytes per (page, KV head)
+    static constexpr size_t VBLK = KBLK;
+    static constexpr int QD = D;  // floats per query row
     f16x8 k[NK];
     f16x4 v[NV];
     struct Q {
         f16x8 r[NK];
     };
 
-    __device__ __forceinline__ void load(const f16* kb, const f16* vb, int lane) {
-        const f16x8* k8 = reinterpret_cast<const f16x8*>(kb);
+    __device__ __forceinline__ void load(const char* kbp, const char* vbp, int lane) {
+        const f16* vb = reinterpret_cast<const f16*>(vbp);
+        const f16x8* k8 = reinterpret_cast<const f16x8*>(kbp);
 #pragma unroll
         for (int j = 0; j < NK; ++j) k[j] = k8[j * 64 + lane];
         const int col = lane & 15, grp = lane >> 4;
@@ -109,14 +114,18 @@ template <int D>
 struct Tile<float, D> {
     static constexpr int NK = D / 16;
     static constexpr int NV = D / 16;
+    static constexpr size_t KBLK = (size_t)kPageTokens * D * 4;  // bytes per (page, KV head)
+    static constexpr size_t VBLK = KBLK;
+    static constexpr int QD = D;
     f32x4 k[NK];
     f32x4 v[NV];
     struct Q {
         float r[D / 4];
     };
 
-    __device__ __forceinline__ void load(const float* kb, const float* vb, int lane) {
-        const f32x4* k4 = reinterpret_cast<const f32x4*>(kb);
+    __device__ __forceinline__ void load(const char* kbp, const char* vbp, int lane) {
+        const float* vb = reinterpret_cast<const float*>(vbp);
+        const f32x4* k4 = reinterpret_cast<const f32x4*>(kbp);
 #pragma unroll
         for (int j = 0; j < NK; ++j) k[j] = k4[j * 64 + lane];
         const int col = lane & 15, grp = lane >> 4;
@@ -153,6 +162,126 @@ struct Tile<float, D> {
         for (int t = 0; t < NV; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[t][r], p[r], o[t], 0, 0, 0);
+    }
+};
+
+// TurboQuant pool (src/turboquant/mod.rs:408-566): per (page, KV head) a K
+// block of 16 packed keys (64 B each: 3-bit Lloyd-Max codes of the rotated,
+// sqrt(d)-scaled unit key, LSB first, then 128 QJL sign bits) followed by the
+// 16 f32 key norms, and a V block [128 dims][16 tokens] of f16 values.  The
+// query row is the 256-wide "virtual query" [R.q / sqrt(d) | c * G.R.q / d]
+// (tq_query_kernel), so a key's score is norm * <virtual key, virtual query>
+// with the virtual key [centroid(code_i) | +-1 sign_i].  The dot runs on
+// v_mfma_f32_16x16x32_f16: the k index of MFMA block kb, lane group g,
+// element e is dim 32g + 8kb + e (kb < 4) or sign 32g + 8(kb-4) + e, so a
+// lane decodes only the 32 codes (3 dwords) and 32 signs (1 dword) of its
+// quarter of the key.  The centroid half of the query is split into f16
+// hi + lo parts; centroids are f16 (relative rounding <= 1.9e-4).
+struct TqKey {};
+constexpr uint64_t kTqMagF16 =       // f16 bits of 0.2451, 0.756, 1.344, 2.152
+    0x33D8ull | (0x3A0Cull << 16) | (0x3D60ull << 32) | (0x404Eull << 48);
+
+// f16 bits of Lloyd-Max centroid `c` (0..7): codes 4..7 are +M[c-4], codes
+// 0..3 are -M[3-c] (the 3-bit codebook is symmetric).
+__device__ __forceinline__ uint32_t tq_centroid_f16(uint32_t c) {
+    const uint32_t k = (c ^ ((c >> 2) - 1u)) & 3u;
+    return ((uint32_t)(kTqMagF16 >> (16 * k)) & 0xFFFFu) | ((c & 4u) ? 0u : 0x8000u);
+}
+
+template <>
+struct Tile<TqKey, 128> {
+    static constexpr int D = 128;
+    static constexpr int NV = D / 16;
+    static constexpr size_t KBLK = (size_t)kPageTokens * (kTqKeyBytes + 4);
+    static constexpr size_t VBLK = (size_t)kPageTokens * D * 2;
+    static constexpr int QD = 2 * D;
+    uint32_t code[3];  // 3-bit codes of dims 32g .. 32g+31 of token lane%16
+    uint32_t sign;     // QJL signs 32g .. 32g+31 of token lane%16
+    f32x4 norm;        // norms of tokens 4g .. 4g+3 (the rows of this lane's scores)
+    f16x4 v[NV];
+    struct Q {
+        f16x8 hi[8];
+        f16x8 lo[4];
+    };
+
+    __device__ __forceinline__ void load(const char* kbp, const char* vbp, int lane) {
+        const int tok = lane & 15, grp = lane >> 4;
+        const uint32_t* rec = reinterpret_cast<const uint32_t*>(kbp + tok * kTqKeyBytes);
+        code[0] = rec[3 * grp];
+        code[1] = rec[3 * grp + 1];
+        code[2] = rec[3 * grp + 2];
+        sign = rec[12 + grp];
+        norm = *reinterpret_cast<const f32x4*>(kbp + kPageTokens * kTqKeyBytes + 16 * grp);
+        const f16* vb = reinterpret_cast<const f16*>(vbp);
+#pragma unroll
+        for (int t = 0; t < NV; ++t)
+            v[t] = *reinterpret_cast<const f16x4*>(vb + (16 * t + tok) * 16 + 4 * grp);
+    }
+    static __device__ __forceinline__ void load_q(Q& q, const float* qrow, float qs, int grp) {
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            const float* src = qrow + (kb < 4 ? 32 * grp + 8 * kb : D + 32 * grp + 8 * (kb - 4));
+            const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = (i < 4 ? a[i] : b[i - 4]) * qs;
+                const f16 h = to_f16(x);
+                q.hi[kb][i] = h;
+                if (kb < 4) q.lo[kb][i] = to_f16(x - (float)h);
+            }
+        }
+    }
+    // code of element j (0..31) of this lane's quarter: bits 3j .. 3j+2
+    __device__ __forceinline__ uint32_t code_of(int j) const {
+        const int bit = 3 * j, w = bit >> 5, off = bit & 31;
+        uint32_t x = code[w] >> off;
+        if (off > 29) x |= code[w + 1] << (32 - off);
+        return x & 7u;
+    }
+    __device__ __forceinline__ f32x4 scores(const Q& q) const {
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            f16x8 kf;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t pr = tq_centroid_f16(code_of(8 * kb + e)) |
+                                    (tq_centroid_f16(code_of(8 * kb + e + 1)) << 16);
+                const f16x2 h2 = __builtin_bit_cast(f16x2, pr);
+                kf[e] = h2[0];
+                kf[e + 1] = h2[1];
+            }
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.hi[kb], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.lo[kb], s, 0, 0, 0);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            f16x8 sf;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t b0 = (sign >> (8 * kb + e)) & 1u, b1 = (sign >> (8 * kb + e + 1)) & 1u;
+                // +1.0 = 0x3C00 when the bit is set, -1.0 = 0xBC00 otherwise
+                const uint32_t pr = 0xBC00BC00u - ((b0 << 15) | (b1 << 31));
+                const f16x2 h2 = __builtin_bit_cast(f16x2, pr);
+                sf[e] = h2[0];
+                sf[e + 1] = h2[1];
+            }
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, q.hi[4 + kb], s, 0, 0, 0);
+        }
+        return s * norm;
+    }
+    __device__ __forceinline__ void mask_v(int valid) {
+#pragma unroll
+        for (int t = 0; t < NV; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (i >= valid) v[t][i] = (f16)0.0f;
+    }
+    __device__ __forceinline__ void pv(f32x4* o, const float p[4]) const {
+        f16x4 pb = {to_f16(p[0]), to_f16(p[1]), to_f16(p[2]), to_f16(p[3])};
+#pragma unroll
+        for (int t = 0; t < NV; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(v[t], pb, o[t], 0, 0, 0);
     }
 };
 
@@ -288,9 +417,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
     const int col = lane & 15, grp = lane >> 4;
     const bool col_on = col < group;
     const int GD = group * D;
-    const size_t blk = (size_t)kPageTokens * D;
-    const KT* kpool = reinterpret_cast<const KT*>(g.k);
-    const KT* vpool = reinterpret_cast<const KT*>(g.v);
+    const char* kpool = reinterpret_cast<const char*>(g.k);
+    const char* vpool = reinterpret_cast<const char*>(g.v);
 
     int b = find_seq(s_cum, p.batch, n_kv, cur);
     while (cur < end) {
@@ -311,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
 
         const int head = head_of(kvh, col_on ? col : 0, n_kv, group, p.gqa_mode);
         typename T::Q q;
-        T::load_q(q, p.q + ((size_t)b * p.n_q_heads + head) * D,
+        T::load_q(q, p.q + ((size_t)b * p.n_q_heads + head) * T::QD,
                   col_on ? p.scale * kLog2e : 0.f, grp);
         Acc<D> acc;
 #pragma unroll
@@ -332,8 +460,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
                 for (int u = 0; u < NP; ++u) {
                     const int j = NP * i + u;
                     const int pid = j < n_my ? __builtin_amdgcn_readlane(pid_v, j) : first_pid;
-                    const size_t off = ((size_t)pid * n_kv + kvh) * blk;
-                    dst[u].load(kpool + off, vpool + off, lane);
+                    const size_t blk = (size_t)pid * n_kv + kvh;
+                    dst[u].load(kpool + blk * T::KBLK, vpool + blk * T::VBLK, lane);
                 }
             };
             auto valid_of = [&](int* valid, int i) {
@@ -480,7 +608,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
 }
 
 template <typename KT, int D>
-constexpr int np_of() { return (sizeof(KT) == 2 && D <= 128) ? 2 : 1; }
+constexpr int np_of() {
+    return std::is_same<KT, TqKey>::value ? 2 : (sizeof(KT) == 2 && D <= 128) ? 2 : 1;
+}
 
 template <typename KT, int D>
 int wgs_per_cu() {
@@ -519,7 +649,8 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
         cus = 256;
     int per_cu = 1;
     const bool hp = g.dtype == 1;
-    switch (g.head_dim) {
+    if (g.dtype == kTqDtype) per_cu = wgs_per_cu<TqKey, 128>();
+    else switch (g.head_dim) {
         case 64: per_cu = hp ? wgs_per_cu<f16, 64>() : wgs_per_cu<float, 64>(); break;
         case 128: per_cu = hp ? wgs_per_cu<f16, 128>() : wgs_per_cu<float, 128>(); break;
         default: per_cu = wgs_per_cu<f16, 256>(); break;
@@ -550,6 +681,8 @@ size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan) {
 
 hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,
                          const DecodePlan& plan, hipStream_t s) {
+    if (g.dtype == kTqDtype)
+        return g.head_dim == 128 ? launch_t<TqKey, 128>(g, p, ws, plan, s) : hipErrorInvalidValue;
     const bool hp = g.dtype == 1;
     switch (g.head_dim) {
         case 64: return hp ? launch_t<f16, 64>(g, p, ws, plan, s) : launch_t<float, 64>(g, p, ws, plan, s);

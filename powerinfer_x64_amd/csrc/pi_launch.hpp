@@ -11,6 +11,8 @@ namespace pi {
 constexpr int kPageTokens = 16;  // tokens per KV page
 constexpr int kItemPages = 16;   // max pages per decode work item (the balancing unit)
 constexpr int kMaxBatch = 4096;  // sequences per decode launch (LDS prefix scan)
+constexpr int kTqDtype = 3;      // KvGeom::dtype of a TurboQuant pool (head_dim 128)
+constexpr int kTqKeyBytes = 64;  // packed TurboQuant key: 3 x 128 code bits + 128 sign bits
 
 // KV pool geometry: one K and one V block of kPageTokens x head_dim elements
 // per (page, kv head).  K block layout: [head_dim/E][16 tokens][E] with
@@ -26,6 +28,18 @@ struct KvGeom {
     int32_t head_dim;
     int32_t dtype;      // PI_F32 / PI_F16
     int32_t elem_bytes;
+};
+
+// TurboQuant compressed pool (head_dim 128): g.k holds per (page, KV head)
+// 16 packed keys of kTqKeyBytes then their 16 f32 norms, g.v the f16 V block
+// [128][16]; rt / gt are the per-head rotation and QJL matrices, transposed
+// ([h][j][i] = M[h][i][j]) so that lane i reads row i coalesced.
+struct TqPool {
+    KvGeom g;
+    float* rt;
+    float* gt;
+    float scale;  // sqrt(128) in f32: the quantizer's per-coordinate scale
+    float corr;   // residual_norm * qjl_scale of the 3-bit estimator
 };
 
 struct DecodeWorkspace {
@@ -69,6 +83,16 @@ hipError_t launch_kv_append(const KvGeom& g, const void* k, const void* v, int32
 hipError_t launch_kv_read(const KvGeom& g, const int32_t* page_table, int32_t max_pages,
                           int32_t seq, int32_t start, int32_t n_tok, float* k_out, float* v_out,
                           hipStream_t s);
+
+hipError_t launch_tq_append(const TqPool& t, const float* k, const float* v,
+                            const int32_t* page_table, int32_t max_pages, const int32_t* start_pos,
+                            int32_t n_seq, int32_t n_tok, hipStream_t s);
+hipError_t launch_tq_read(const TqPool& t, const int32_t* page_table, int32_t max_pages,
+                          int32_t seq, int32_t start, int32_t n_tok, uint8_t* keys_out,
+                          float* norms_out, uint16_t* v_out, hipStream_t s);
+// Virtual queries [batch][n_q_heads][256] for the TurboQuant decode.
+hipError_t launch_tq_query(const TqPool& t, const float* q, float* qv, int32_t batch,
+                           int32_t n_q_heads, int32_t gqa_mode, hipStream_t s);
 
 struct RopeFreqs {
     float f[128];  // up to head_dim 256 -> 128 pairs

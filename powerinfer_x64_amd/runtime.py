@@ -159,6 +159,101 @@ class KvPool:
         return ko, vo
 
 
+class TqPool:
+    """TurboQuant compressed KV cache (CompressedKVCache, src/turboquant/mod.rs:408-566) in
+    16-token pages: 64-byte 3-bit + QJL key records with f32 norms, f16 values; head_dim 128."""
+
+    KEY_BYTES = 64
+
+    def __init__(self, dev: Device, n_pages: int, n_kv_heads: int, head_dim: int = 128,
+                 page_tokens: int = PAGE_TOKENS):
+        self.dev = dev
+        self.n_pages, self.n_kv_heads, self.head_dim = n_pages, n_kv_heads, head_dim
+        p = ctypes.c_void_p()
+        dev.check(dev.lib.pi_tq_pool_create(dev.h, n_pages, page_tokens, n_kv_heads, head_dim,
+                                            ctypes.byref(p)))
+        self.p = p
+
+    @property
+    def nbytes(self) -> int:
+        return int(self.dev.lib.pi_tq_pool_bytes(self.p))
+
+    def close(self):
+        if self.p:
+            self.dev.lib.pi_tq_pool_destroy(self.p)
+            self.p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def append(self, k: torch.Tensor, v: torch.Tensor, page_table: torch.Tensor,
+               start_pos: torch.Tensor):
+        """k, v: [n_seq, n_tok, n_kv_heads, 128] f32."""
+        d = self.dev
+        if k.dim() != 4 or k.shape[2:] != (self.n_kv_heads, self.head_dim):
+            raise InvalidArg(f"k: shape {tuple(k.shape)}")
+        for name, t in (("k", k), ("v", v)):
+            _need(t, name, dtype=torch.float32, shape=k.shape, dev=d.torch_device)
+        n_seq, n_tok = k.shape[:2]
+        _need(page_table, "page_table", torch.int32, dev=d.torch_device)
+        _need(start_pos, "start_pos", torch.int32, (n_seq,), d.torch_device)
+        if page_table.dim() != 2 or page_table.shape[0] < n_seq:
+            raise InvalidArg(f"page_table: shape {tuple(page_table.shape)}")
+        d.check(d.lib.pi_tq_append(d.h, self.p, _vp(k), _vp(v), _vp(page_table),
+                                   page_table.shape[1], _vp(start_pos), n_seq, n_tok, d.stream()))
+
+    def read(self, page_table: torch.Tensor, seq: int, start: int, n_tok: int):
+        """(keys [n_tok, Hkv, 64] uint8, norms [n_tok, Hkv] f32, values [n_tok, Hkv, 128] f16)."""
+        d = self.dev
+        _need(page_table, "page_table", torch.int32, dev=d.torch_device)
+        ko = torch.empty((n_tok, self.n_kv_heads, self.KEY_BYTES), dtype=torch.uint8,
+                         device=d.torch_device)
+        no = torch.empty((n_tok, self.n_kv_heads), dtype=torch.float32, device=d.torch_device)
+        vo = torch.empty((n_tok, self.n_kv_heads, self.head_dim), dtype=torch.float16,
+                         device=d.torch_device)
+        d.check(d.lib.pi_tq_read(d.h, self.p, _vp(page_table), page_table.shape[1], seq, start,
+                                 n_tok, _vp(ko), _vp(no), _vp(vo), d.stream()))
+        return ko, no, vo
+
+
+def tq_generate(dim: int, seed: int):
+    """Host only: (rotation, QJL matrix) of TurboQuant::new(bits, dim, dim, seed)."""
+    lib = _abi.load()
+    rot = np.empty((dim, dim), dtype=np.float32)
+    qjl = np.empty((dim, dim), dtype=np.float32)
+    rc = lib.pi_tq_generate(dim, seed, rot.ctypes.data_as(ctypes.c_void_p),
+                            qjl.ctypes.data_as(ctypes.c_void_p))
+    if rc != 0:
+        raise _ERRORS.get(rc, PiError)(lib.pi_last_error(None).decode())
+    return rot, qjl
+
+
+def tq_attn_decode(dev: Device, q: torch.Tensor, pool: TqPool, page_table: torch.Tensor,
+                   ctx_len: torch.Tensor, gqa_mode: int = MODULO,
+                   gate: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+    """q [B, Hq, 128] f32 -> out [B, Hq, 128] f32 over each sequence's compressed cache."""
+    _need(q, "q", torch.float32, dev=dev.torch_device)
+    b, hq, dh = q.shape
+    if dh != pool.head_dim:
+        raise InvalidArg(f"q head_dim {dh} != pool head_dim {pool.head_dim}")
+    _need(page_table, "page_table", torch.int32, dev=dev.torch_device)
+    if page_table.dim() != 2 or page_table.shape[0] != b:
+        raise InvalidArg(f"page_table: shape {tuple(page_table.shape)}")
+    _need(ctx_len, "ctx_len", torch.int32, (b,), dev.torch_device)
+    if gate is not None:
+        _need(gate, "gate", torch.float32, q.shape, dev.torch_device)
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, "out", torch.float32, q.shape, dev.torch_device)
+    dev.check(dev.lib.pi_tq_attn_decode(dev.h, _vp(q), pool.p, _vp(page_table),
+                                        page_table.shape[1], _vp(ctx_len), b, hq, gqa_mode,
+                                        _vp(gate), _vp(out), dev.stream()))
+    return out
+
+
 def head_rmsnorm(dev: Device, x: torch.Tensor, w: torch.Tensor, eps: float):
     """In place: every row of the last dimension of x (f32) is RMS-normalised and scaled by w."""
     _need(x, "x", torch.float32, dev=dev.torch_device)

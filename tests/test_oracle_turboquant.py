@@ -1,0 +1,196 @@
+"""Pins the TurboQuant restatement in oracle/ (src/turboquant/mod.rs).
+
+Known answers: SplitMix64's published test vector, hand-derived bit packing,
+the reference's own unit tests (src/turboquant/mod.rs:752-951: centroid
+order/symmetry, orthogonality, reconstruction MSE, QJL dot accuracy, packing
+round trips, compressed sizes, cache compression ratio).  Properties: the
+QJL estimator is unbiased, the precomputed-query path equals the direct one,
+and a float64 numpy evaluation of the cache attention from the unpacked
+fields agrees with the f32 restatement.  A planted sign slip in the QJL
+correction is caught.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+
+
+def test_splitmix64_published_vector():
+    # the reference generator's test vector for seed 1234567
+    assert o.splitmix64(1234567, 5) == [6457827717110365317, 3203168211198807973,
+                                        9817491932198370423, 4593380528125082431,
+                                        16408922859458223821]
+
+
+def test_box_muller_gaussians_are_standard_normal():
+    x = o.splitmix64_gaussians(0xCAFEBABE, 200000).astype(np.float64)
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
+    # kurtosis of a normal is 3
+    assert abs(((x - x.mean()) ** 4).mean() / x.var() ** 2 - 3.0) < 0.05
+
+
+def test_centroids_sorted_symmetric():
+    # src/turboquant/mod.rs:752-769
+    for bw in range(1, 5):
+        c = o.tq_centroids(bw)
+        assert c.size == 1 << bw
+        assert np.all(np.diff(c) > 0)
+        assert np.all(np.abs(c + c[::-1]) < 0.01)
+
+
+@pytest.mark.parametrize("dim,seed", [(8, 42), (128, 0xCAFEBABE)])
+def test_orthogonal_matrix(dim, seed):
+    # src/turboquant/mod.rs:771-790 (dim 8, seed 42, 0.01) and the cache's dim
+    q = o.tq_orthogonal(dim, seed).astype(np.float64)
+    assert np.abs(q.T @ q - np.eye(dim)).max() < (0.01 if dim == 8 else 1e-4)
+
+
+def test_bit_packing_known_bytes():
+    # src/turboquant/mod.rs:896-916; bytes derived by hand, LSB first:
+    # 2-bit codes 0,1,2,3 -> 0b11_10_01_00 = 0xE4; 1,0,3,2 -> 0b10_11_00_01 = 0xB1;
+    # signs 1,0,1,1 -> 0b1101 = 0x0D
+    idx = [0, 1, 2, 3, 1, 0, 3, 2]
+    packed = o.tq_pack(idx, 2, [1, 0, 1, 1])
+    assert list(packed) == [0xE4, 0xB1, 0x0D]
+    i2, s2 = o.tq_unpack(packed, 8, 2, 4)
+    assert list(i2) == idx and list(s2) == [1, 0, 1, 1]
+    assert list(o.tq_pack(idx, 2)) == [0xE4, 0xB1]
+
+
+def test_bit_packing_round_trip_3bit():
+    rng = np.random.default_rng(1)
+    idx = rng.integers(0, 8, 128).astype(np.uint8)
+    sg = rng.integers(0, 2, 128).astype(np.uint8)
+    packed = o.tq_pack(idx, 3, sg)
+    assert packed.size == 64
+    i2, s2 = o.tq_unpack(packed, 128, 3, 128)
+    assert np.array_equal(i2, idx) and np.array_equal(s2, sg)
+    # code i occupies bits 3i .. 3i+2
+    bits = np.unpackbits(packed, bitorder="little")
+    assert np.array_equal(bits[0:384:3] + 2 * bits[1:384:3] + 4 * bits[2:384:3], idx)
+    assert np.array_equal(bits[384:], sg)
+
+
+def test_compressed_sizes():
+    # src/turboquant/mod.rs:918-951
+    assert o.tq_compressed_bytes(3, 128, 128) == 64
+    assert o.tq_compressed_bytes(4, 128, 128) == 80
+    assert o.tq_compressed_bytes(3, 128, 0) == 48
+    assert o.tq_compressed_bytes(4, 128, 0) == 64
+
+
+@pytest.mark.parametrize("qjl", [16, 0])
+def test_quantize_dequantize_mse(qjl):
+    # src/turboquant/mod.rs:792-834
+    dim = 16
+    R, G = o.tq_matrices(dim, 123, qjl)
+    x = np.sin(np.arange(dim, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    x = (x / np.sqrt((x * x).sum())).astype(np.float32)
+    rec = o.tq_dequantize(o.tq_quantize(x, R, G, 3, qjl), R, 3)
+    assert float(((x - rec) ** 2).mean()) < 0.2
+
+
+def test_dot_accuracy_qjl():
+    # src/turboquant/mod.rs:836-865: 50 random unit pairs, mean |err| < 0.15
+    dim = 64
+    R, G = o.tq_matrices(dim, 456)
+    g = o.splitmix64_gaussians(789, 50 * 2 * dim).reshape(50, 2, dim)
+    err = []
+    for a, b in g:
+        a = a / np.float32(np.sqrt((a * a).sum()))
+        b = b / np.float32(np.sqrt((b * b).sum()))
+        est = o.tq_dot(a, o.tq_quantize(b, R, G, 3, dim), R, G, 3, dim)
+        err.append(abs(float(a @ b) - est))
+    assert np.mean(err) < 0.15
+
+
+def _estimator_errors(n, flip=False):
+    dim = 64
+    R, G = o.tq_matrices(dim, 7)
+    rng = np.random.default_rng(3)
+    errs = []
+    for _ in range(n):
+        a, b = rng.standard_normal((2, dim)).astype(np.float32)
+        a /= np.linalg.norm(a)
+        b /= np.linalg.norm(b)
+        pk = o.tq_quantize(b, R, G, 3, dim)
+        if flip:  # planted slip: every QJL sign inverted
+            idx, sg = o.tq_unpack(pk, dim, 3, dim)
+            pk = o.tq_pack(idx, 3, 1 - sg)
+        errs.append(o.tq_dot(a, pk, R, G, 3, dim) - float(a @ b))
+    return np.array(errs)
+
+
+def test_qjl_estimator_unbiased_and_sign_slip_caught():
+    e = _estimator_errors(400)
+    assert abs(e.mean()) < 3 * e.std() / np.sqrt(e.size)
+    bad = _estimator_errors(400, flip=True)
+    assert np.abs(bad).mean() > 1.5 * np.abs(e).mean()
+
+
+def test_precomputed_query_matches_direct_dot():
+    dim = 128
+    R, G = o.tq_matrices(dim, 0xCAFEBABE)
+    rng = np.random.default_rng(5)
+    qrot = np.zeros(dim, np.float32)
+    qp = np.zeros(dim, np.float32)
+    for _ in range(20):
+        q = rng.standard_normal(dim).astype(np.float32)
+        k = rng.standard_normal(dim).astype(np.float32)
+        k /= np.linalg.norm(k)
+        pk = o.tq_quantize(k, R, G, 3, dim)
+        o.lib().or_tq_precompute_query(o._p(qrot), o._p(qp), o._p(q), o._p(o._f32(R)),
+                                       o._p(o._f32(G)), dim, dim)
+        a = float(o.lib().or_tq_dot_precomputed(o._p(qrot), o._p(qp),
+                                                pk.ctypes.data_as(o._u8p), dim, 3, dim))
+        b = o.tq_dot(q, pk, R, G, 3, dim)
+        assert abs(a - b) <= 1e-5 * (1 + abs(b))
+
+
+def _attend_f64(q, packed, norms, vals, R, G, kv_h):
+    """float64 numpy evaluation of the cache attention from the unpacked fields."""
+    T, n_kv, dim = vals.shape
+    c = o.tq_centroids(3).astype(np.float64)
+    R64, G64 = R.astype(np.float64), G.astype(np.float64)
+    qr = R64 @ q.astype(np.float64)
+    qp = (G64 @ qr) / np.sqrt(dim)
+    qr /= np.sqrt(dim)
+    rn = np.sqrt(0.043 / np.sqrt(dim))
+    qs = np.sqrt(np.pi / (2 * dim))
+    sc = np.zeros(T)
+    for t in range(T):
+        idx, sg = o.tq_unpack(packed[t, kv_h], dim, 3, dim)
+        mse = qr @ c[idx]
+        corr = rn * qs * (qp @ np.where(sg == 1, 1.0, -1.0))
+        sc[t] = norms[t, kv_h] * (mse + corr) / np.sqrt(dim)
+    w = np.exp(sc - sc.max())
+    w /= w.sum()
+    w[w < 1e-7] = 0.0
+    return w @ vals[:, kv_h, :].astype(np.float64)
+
+
+def test_cache_attention_matches_f64_evaluation():
+    dim, n_kv, T = 128, 2, 40
+    rng = np.random.default_rng(11)
+    Rs, Gs = zip(*[o.tq_matrices(dim, 0xCAFEBABE + h) for h in range(n_kv)])
+    R = np.stack(Rs)
+    G = np.stack(Gs)
+    keys = rng.standard_normal((T, n_kv, dim)).astype(np.float32)
+    vals = rng.standard_normal((T, n_kv, dim)).astype(np.float16)
+    packed = np.zeros((T, n_kv, 64), np.uint8)
+    norms = np.zeros((T, n_kv), np.float32)
+    for t in range(T):
+        packed[t], norms[t] = o.tq_cache_append_keys(keys[t], R, G)
+        assert np.allclose(norms[t], np.linalg.norm(keys[t].astype(np.float64), axis=1), rtol=1e-6)
+    q = rng.standard_normal(dim).astype(np.float32) * 2
+    for kv_h in range(n_kv):
+        got = o.tq_cache_attend(q, packed, norms, vals, R[kv_h], G[kv_h], kv_h)
+        ref = _attend_f64(q, packed, norms, vals, R[kv_h], G[kv_h], kv_h)
+        assert np.abs(got - ref).max() < 1e-4
+
+
+def test_cache_compression_ratio():
+    # src/turboquant/mod.rs:867-894: 10 tokens, 2 heads, dim 16 -> ratio > 2
+    T, n_kv, dim = 10, 2, 16
+    mem = T * n_kv * (o.tq_compressed_bytes(3, dim, dim) + 4 + 2 * dim)
+    assert T * n_kv * dim * 4 * 2 / mem > 2.0
