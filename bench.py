@@ -45,7 +45,7 @@ def _args():
                    help="budget of the single-core CPU baseline sample")
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--workload", default=None,
-                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "copy"],
+                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "tq", "copy"],
                    help="time one workload only and print its figures (for sweeps)")
     return p.parse_args()
 
@@ -151,6 +151,60 @@ def bench_decode(torch, rt, dev, timer, lens, hq, hkv, d, theta, seed, steps, wa
            "ms_median": t["ms_median"], "bytes_per_launch": algo,
            "tokens": int(sum(int(x) for x in lens))}
     return res, (pool, tpt, ctx, q, out, gate)
+
+
+def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup):
+    """TurboQuant compressed-KV decode (pi_tq_attn_decode) over the config 2 shape: the
+    cache is appended through pi_tq_append (K, V ~ N(0,1) generated on the GPU); the timed
+    call includes the per-query precompute and the merge."""
+    d = 128
+    rng = np.random.default_rng(seed)
+    n_pages_seq = [(int(x) + PAGE - 1) // PAGE for x in lens]
+    total = sum(n_pages_seq)
+    perm = rng.permutation(total).astype(np.int32)
+    pt = np.full((len(lens), max(n_pages_seq)), -1, np.int32)
+    off = 0
+    for i, n in enumerate(n_pages_seq):
+        pt[i, :n] = perm[off:off + n]
+        off += n
+    pool = rt.TqPool(dev, total, hkv)
+    tpt = torch.from_numpy(pt).cuda()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    zero = torch.zeros(1, dtype=torch.int32, device="cuda")
+    t0 = time.perf_counter()
+    for i, x in enumerate(lens):
+        k = torch.randn((1, int(x), hkv, d), generator=g, device="cuda")
+        v = torch.randn((1, int(x), hkv, d), generator=g, device="cuda")
+        pool.append(k, v, tpt[i:i + 1].contiguous(), zero)
+        del k, v
+    torch.cuda.synchronize()
+    append_s = time.perf_counter() - t0
+    q = torch.randn((len(lens), hq, d), generator=g, device="cuda")
+    ctx = torch.tensor([int(x) for x in lens], dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    lib = dev.lib
+    args = (dev.h, ctypes.c_void_p(q.data_ptr()), pool.p, ctypes.c_void_p(tpt.data_ptr()),
+            tpt.shape[1], ctypes.c_void_p(ctx.data_ptr()), len(lens), hq, 0, None,
+            ctypes.c_void_p(out.data_ptr()), None)
+
+    def fn():
+        rc = lib.pi_tq_attn_decode(*args)
+        if rc:
+            raise RuntimeError(lib.pi_last_error(dev.h).decode())
+    t = timer.run(fn, steps, warmup)
+    tokens = sum(int(x) for x in lens)
+    # per token and KV head: 64-byte key record + f32 norm + 128 f16 values
+    algo = (tokens * hkv * (64 + 4 + d * 2) + 2 * len(lens) * hq * d * 4
+            + total * 4 + len(lens) * 4 + 2 * hkv * d * d * 4)
+    gbs = algo / (t["ms_avg"] * 1e-3) / 1e9
+    f16_equiv = tokens * hkv * d * 2 * 2
+    res = {"GB_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "ms_per_step": t["ms_avg"],
+           "ms_median": t["ms_median"], "bytes_per_launch": algo, "tokens": tokens,
+           "kv_bytes_vs_f16_pool": round(tokens * hkv * (68 + d * 2) / f16_equiv, 4),
+           "append_tokens_per_s": tokens / append_s}
+    del pool
+    return res
 
 
 def cpu_baseline_decode(torch, rt, dev, state, lens, hq, hkv, d, budget_s):
@@ -324,6 +378,10 @@ def _single(torch, rt, dev, timer, a):
         return bench_prefill(torch, rt, dev, timer, 4096, 32, 8, 128, 1e6, 0x5EED0002, st, wu)
     if w == "gdn_prefill":
         return bench_gdn_prefill(torch, rt, dev, timer, st, wu)
+    if w == "tq":
+        rng = np.random.default_rng(0x5EED0001)
+        lens = [int(x) for x in rng.integers(1024, 32769, size=32)]
+        return bench_tq_decode(torch, rt, dev, timer, lens, 32, 8, 0x5EED0004, st, wu)
     if w == "copy":
         return bench_copy(torch, timer, st, wu)
     return bench_gdn_decode(torch, rt, dev, timer, st, wu)

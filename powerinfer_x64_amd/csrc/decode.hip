@@ -609,7 +609,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
 
 template <typename KT, int D>
 constexpr int np_of() {
-    return std::is_same<KT, TqKey>::value ? 2 : (sizeof(KT) == 2 && D <= 128) ? 2 : 1;
+    return std::is_same<KT, TqKey>::value ? 1 : (sizeof(KT) == 2 && D <= 128) ? 2 : 1;
 }
 
 template <typename KT, int D>

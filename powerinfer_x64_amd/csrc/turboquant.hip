@@ -182,7 +182,8 @@ __global__ __launch_bounds__(256) void tq_read_kernel(TqPool t, const int32_t* _
 // Virtual query of (sequence b, query head h) (precompute_query,
 // :244-278): [R.q / sqrt(d) | corr * G.(R.q) / sqrt(d)], corr =
 // residual_norm * qjl_scale of the 3-bit estimator (:297-316).  One
-// workgroup of 128 threads per row; thread i owns output i.
+// workgroup of 128 threads per row; thread i owns output i (the matrices are
+// stored transposed, so the reads of a row step are coalesced).
 __global__ __launch_bounds__(128) void tq_query_kernel(TqPool t, const float* __restrict__ q,
                                                        float* __restrict__ qv, int n_q_heads,
                                                        int gqa_mode) {
