@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict
 //       A_ij = beta_i exp(lg_i - lg_j) k_i.k_j  (j < i)
 //   O = diag(gamma) Q S + M Delta,  M_ij = exp(lg_i - lg_j) q_i.k_j  (j <= i)
 //   S' = exp(lg_C) S + K^T diag(exp(lg_C - lg_i)) Delta
-// gdn_prep_kernel (parallel over chunks x V heads) builds T = (I + A)^-1, M,
+// gdn_prep_kernel (parallel over chunks x K heads) builds T = (I + A)^-1, M,
 // lg and the q/k inverse norms; gdn_scan_kernel walks the chunks in order for
 // one (V head, 16 state columns) with the state tile in LDS.  Matrix products
 // use the f32 MFMA (v_mfma_f32_16x16x4f32).
@@ -263,23 +263,33 @@ struct GdnWs {
     float* lg;  // [n_chunks][Hv][64] cumulative log decay
 };
 
-__global__ __launch_bounds__(256) void gdn_prep_kernel(const float* __restrict__ q,
+// One workgroup of 8 wavefronts per (chunk, K head).  Phase A stages the
+// chunk's q and k rows of the K head, L2-normalises them, and forms the lower
+// 16x16 tiles of K K^T and Q K^T once; phase B derives, for the V heads tiled
+// onto this K head (vh = kh + r * hk, src/model/mod.rs:845-853), two at a time
+// (waves 0-3 and 4-7), the decayed
+//   A_ij = beta_i exp(lg_i - lg_j) k_i.k_j  (j < i),  M_ij = exp(lg_i - lg_j) q_i.k_j  (j <= i)
+// and T = (I + A)^-1.  Phase B reuses the LDS of phase A's q / k rows.
+constexpr int PREP_B = 3 * GC * TS_;  // floats of one half's A | T | scratch
+
+__global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__ q,
                                                        const float* __restrict__ k,
                                                        const float* __restrict__ beta,
                                                        const float* __restrict__ g, int n_tok,
                                                        int hk, int hv, GdnWs w) {
-    __shared__ __attribute__((aligned(16))) float sk[GC * KS_];
-    __shared__ __attribute__((aligned(16))) float sq[GC * KS_];
-    __shared__ __attribute__((aligned(16))) float sa[GC * TS_];  // A
-    __shared__ __attribute__((aligned(16))) float st[GC * TS_];  // T = (I + A)^-1
-    __shared__ __attribute__((aligned(16))) float sx[4 * 16 * TS_];  // per-wave 16x16 scratch
-    __shared__ float slg[GC], sb[GC];
-    const int n = blockIdx.x, vh = blockIdx.y, kh = vh % hk;
+    constexpr int BIG = 2 * PREP_B > 2 * GC * KS_ ? 2 * PREP_B : 2 * GC * KS_;
+    __shared__ __attribute__((aligned(16))) float s_big[BIG];   // sk | sq, then 2 x (sa | st | sx)
+    __shared__ __attribute__((aligned(16))) float skk[GC * TS_];  // K K^T (lower tiles)
+    __shared__ __attribute__((aligned(16))) float sqk[GC * TS_];  // Q K^T (lower tiles)
+    __shared__ float slg[2][GC], sb[2][GC];
+    float* sk = s_big;
+    float* sq = s_big + GC * KS_;
+    const int n = blockIdx.x, kh = blockIdx.y;
     const int t0 = n * GC;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     // raw rows of the K head (zeros past the end of the prompt)
-    for (int e = tid; e < GC * DK / 4; e += 256) {
+    for (int e = tid; e < GC * DK / 4; e += 512) {
         const int row = e / (DK / 4), c4 = e % (DK / 4);
         const int t = t0 + row;
         f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
@@ -290,22 +300,10 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(const float* __restrict__
         *reinterpret_cast<f32x4*>(sq + row * KS_ + 4 * c4) = a;
         *reinterpret_cast<f32x4*>(sk + row * KS_ + 4 * c4) = b;
     }
-    if (wave == 0) {  // inclusive cumsum of g, and beta (0 past the end)
-        const int t = t0 + lane;
-        float x = t < n_tok ? g[(size_t)t * hv + vh] : 0.f;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float y = __shfl_up(x, o, 64);
-            if (lane >= o) x += y;
-        }
-        slg[lane] = x;
-        sb[lane] = t < n_tok ? beta[(size_t)t * hv + vh] : 0.f;
-        w.lg[((size_t)n * hv + vh) * GC + lane] = x;
-    }
     __syncthreads();
-    // L2 norms (src/model/mod.rs:860-875); wave w handles rows 16w..16w+15
-    for (int rr = 0; rr < 16; ++rr) {
-        const int row = 16 * wave + rr;
+    // L2 norms (src/model/mod.rs:860-875); wave w handles rows 8w..8w+7
+    for (int rr = 0; rr < 8; ++rr) {
+        const int row = 8 * wave + rr;
         const float q0 = sq[row * KS_ + lane], q1 = sq[row * KS_ + 64 + lane];
         const float k0 = sk[row * KS_ + lane], k1 = sk[row * KS_ + 64 + lane];
         float ssq = q0 * q0 + q1 * q1, ssk = k0 * k0 + k1 * k1;
@@ -321,73 +319,106 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(const float* __restrict__
         sk[row * KS_ + lane] = k0 * ik;
         sk[row * KS_ + 64 + lane] = k1 * ik;
         const int t = t0 + row;
-        if (lane == 0 && vh < hk && t < n_tok) {  // one writer per (token, K head)
+        if (lane == 0 && t < n_tok) {
             w.rq[(size_t)t * hk + kh] = iq;
             w.rk[(size_t)t * hk + kh] = ik;
         }
     }
     __syncthreads();
-    // lower-triangular 16x16 tiles of K K^T (-> A) and Q K^T (-> M)
+    // lower-triangular 16x16 tiles: 10 of K K^T, then 10 of Q K^T
     const int ln = lane & 15, lg4 = lane >> 4;
-    float* mm = w.mm + ((size_t)n * hv + vh) * GC * GC;
-    for (int tix = wave; tix < 10; tix += 4) {
-        int ib = 0, jb = tix;
+    for (int tix = wave; tix < 20; tix += 8) {
+        const bool isq = tix >= 10;
+        int ib = 0, jb = isq ? tix - 10 : tix;
         while (jb > ib) { jb -= ib + 1; ++ib; }  // enumerate (ib, jb), jb <= ib
-        f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
-        kk = tile_mm(sk, KS_, 16 * ib, sk, KS_, 16 * jb, DK / 16, kk);
-        qk = tile_mm(sq, KS_, 16 * ib, sk, KS_, 16 * jb, DK / 16, qk);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = tile_mm(isq ? sq : sk, KS_, 16 * ib, sk, KS_, 16 * jb, DK / 16, acc);
+        float* dst = isq ? sqk : skk;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = 16 * ib + 4 * lg4 + r, j = 16 * jb + ln;
-            const float dec = expf(slg[i] - slg[j]);
-            sa[i * TS_ + j] = j < i ? sb[i] * dec * kk[r] : 0.f;
-            mm[i * GC + j] = j <= i ? dec * qk[r] : 0.f;
-        }
-        if (ib != jb)  // the mirrored upper tile of M is zero
-#pragma unroll
-            for (int r = 0; r < 4; ++r) mm[(16 * jb + ln) * GC + 16 * ib + 4 * lg4 + r] = 0.f;
+        for (int r = 0; r < 4; ++r) dst[(16 * ib + 4 * lg4 + r) * TS_ + 16 * jb + ln] = acc[r];
     }
-    __syncthreads();
-    // T = (I + A)^-1, A strictly lower triangular, by 16x16 blocks:
-    //   T_ii = (I + A_ii)^-1                      (forward substitution, wave i)
-    //   T_ij = -T_ii . sum_{j <= k < i} A_ik T_kj  (i > j, by block distance)
-    for (int e = tid; e < GC * GC; e += 256) st[(e / GC) * TS_ + (e % GC)] = 0.f;
-    __syncthreads();
-    if (lane < 16) {
-        // lane m holds column m of T_ww: t[i] = d_im - sum_{j < i} A[i][j] t[j]
-        const float* ab = sa + 16 * wave * TS_ + 16 * wave;
-        float t[16];
+    __syncthreads();  // q / k rows are dead: s_big now holds two halves of A, T, scratch
+
+    const int half = wave >> 2, wl = wave & 3, ht = tid & 255;
+    float* sa = s_big + half * PREP_B;  // A
+    float* st = sa + GC * TS_;          // T = (I + A)^-1
+    float* sx = st + GC * TS_;          // per-wave 16x16 scratch
+    float* hlg = slg[half];
+    float* hb = sb[half];
+    for (int v0 = kh; v0 < hv; v0 += 2 * hk) {
+        const int vh = v0 + half * hk;
+        const bool on = vh < hv;  // uniform per half; barriers stay uniform per workgroup
+        if (on && wl == 0) {      // inclusive cumsum of g, and beta (0 past the end)
+            const int t = t0 + lane;
+            float x = t < n_tok ? g[(size_t)t * hv + vh] : 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float acc = i == lane ? 1.f : 0.f;
-#pragma unroll
-            for (int j = 0; j < i; ++j) acc -= ab[i * TS_ + j] * t[j];
-            t[i] = acc;
-            st[(16 * wave + i) * TS_ + 16 * wave + lane] = acc;
-        }
-    }
-    __syncthreads();
-    float* sxw = sx + wave * 16 * TS_;  // this wave's 16x16 scratch
-    for (int d = 1; d < 4; ++d) {
-        if (wave < 4 - d) {
-            const int j = wave, i = wave + d;
-            f32x4 x = {0.f, 0.f, 0.f, 0.f};
-            for (int kb = j; kb < i; ++kb)
-                x = mm16(sa + 16 * i * TS_ + 16 * kb, TS_, st + 16 * kb * TS_ + 16 * j, TS_, x);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sxw[(4 * lg4 + r) * TS_ + ln] = x[r];
-            __builtin_amdgcn_wave_barrier();
-            f32x4 y = {0.f, 0.f, 0.f, 0.f};
-            y = mm16(st + 16 * i * TS_ + 16 * i, TS_, sxw, TS_, y);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) st[(16 * i + 4 * lg4 + r) * TS_ + 16 * j + ln] = -y[r];
+            for (int o = 1; o < 64; o <<= 1) {
+                const float y = __shfl_up(x, o, 64);
+                if (lane >= o) x += y;
+            }
+            hlg[lane] = x;
+            hb[lane] = t < n_tok ? beta[(size_t)t * hv + vh] : 0.f;
+            w.lg[((size_t)n * hv + vh) * GC + lane] = x;
         }
         __syncthreads();
-    }
-    float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
-    for (int e = tid; e < GC * GC / 4; e += 256) {
-        const int row = e / (GC / 4), c4 = e % (GC / 4);
-        *reinterpret_cast<f32x4*>(tm + row * GC + 4 * c4) = *reinterpret_cast<const f32x4*>(st + row * TS_ + 4 * c4);
+        if (on) {
+            float* mm = w.mm + ((size_t)n * hv + vh) * GC * GC;
+            for (int e = ht; e < GC * GC; e += 256) {
+                const int i = e / GC, j = e % GC;
+                float a = 0.f, m = 0.f;
+                if (j <= i) {
+                    const float dec = expf(hlg[i] - hlg[j]);
+                    if (j < i) a = hb[i] * dec * skk[i * TS_ + j];
+                    m = dec * sqk[i * TS_ + j];
+                }
+                sa[i * TS_ + j] = a;
+                st[i * TS_ + j] = 0.f;
+                mm[e] = m;
+            }
+        }
+        __syncthreads();
+        // T = (I + A)^-1, A strictly lower triangular, by 16x16 blocks:
+        //   T_ii = (I + A_ii)^-1                      (forward substitution, wave i)
+        //   T_ij = -T_ii . sum_{j <= k < i} A_ik T_kj  (i > j, by block distance)
+        if (on && lane < 16) {
+            // lane m holds column m of T_ww: t[i] = d_im - sum_{j < i} A[i][j] t[j]
+            const float* ab = sa + 16 * wl * TS_ + 16 * wl;
+            float tv[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float acc = i == lane ? 1.f : 0.f;
+#pragma unroll
+                for (int j = 0; j < i; ++j) acc -= ab[i * TS_ + j] * tv[j];
+                tv[i] = acc;
+                st[(16 * wl + i) * TS_ + 16 * wl + lane] = acc;
+            }
+        }
+        __syncthreads();
+        float* sxw = sx + wl * 16 * TS_;  // this wave's 16x16 scratch
+        for (int d = 1; d < 4; ++d) {
+            if (on && wl < 4 - d) {
+                const int j = wl, i = wl + d;
+                f32x4 x = {0.f, 0.f, 0.f, 0.f};
+                for (int kb = j; kb < i; ++kb)
+                    x = mm16(sa + 16 * i * TS_ + 16 * kb, TS_, st + 16 * kb * TS_ + 16 * j, TS_, x);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sxw[(4 * lg4 + r) * TS_ + ln] = x[r];
+                __builtin_amdgcn_wave_barrier();
+                f32x4 y = {0.f, 0.f, 0.f, 0.f};
+                y = mm16(st + 16 * i * TS_ + 16 * i, TS_, sxw, TS_, y);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) st[(16 * i + 4 * lg4 + r) * TS_ + 16 * j + ln] = -y[r];
+            }
+            __syncthreads();
+        }
+        if (on) {
+            float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
+            for (int e = ht; e < GC * GC / 4; e += 256) {
+                const int row = e / (GC / 4), c4 = e % (GC / 4);
+                *reinterpret_cast<f32x4*>(tm + row * GC + 4 * c4) = *reinterpret_cast<const f32x4*>(st + row * TS_ + 4 * c4);
+            }
+        }
+        __syncthreads();  // A, T and the scratch are rewritten for the next V heads
     }
 }
 
@@ -638,7 +669,7 @@ hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, co
     w.tm = w.rk + (size_t)n_tok * n_k_heads;
     w.mm = w.tm + nc * n_v_heads * GC * GC;
     w.lg = w.mm + nc * n_v_heads * GC * GC;
-    hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)nc, n_v_heads), dim3(256), 0, s, q, k, beta, g,
+    hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)nc, n_k_heads), dim3(512), 0, s, q, k, beta, g,
                        n_tok, n_k_heads, n_v_heads, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
