@@ -256,8 +256,9 @@ __device__ __forceinline__ f32x4 mm16(const float* X, int xs, const float* Y, in
 }
 
 struct GdnWs {
-    float* rq;  // [T][Hk] 1/max(|q|,1e-12) * 1/sqrt(Dk)
-    float* rk;  // [T][Hk] 1/max(|k|,1e-12)
+    f16* q16;   // [n_chunks][Hk][64][128] q / max(|q|,1e-12) / sqrt(Dk), f16
+    f16* k16;   // [n_chunks][Hk][64][128] k / max(|k|,1e-12), f16
+    f16* kt16;  // [n_chunks][Hk][128][64] the same k, transposed
     float* tm;  // [n_chunks][Hv][64][64] (I + A)^-1
     float* mm;  // [n_chunks][Hv][64][64] M
     float* lg;  // [n_chunks][Hv][64] cumulative log decay
@@ -318,13 +319,32 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
         sq[row * KS_ + 64 + lane] = q1 * iq;
         sk[row * KS_ + lane] = k0 * ik;
         sk[row * KS_ + 64 + lane] = k1 * ik;
-        const int t = t0 + row;
-        if (lane == 0 && t < n_tok) {
-            w.rq[(size_t)t * hk + kh] = iq;
-            w.rk[(size_t)t * hk + kh] = ik;
-        }
     }
     __syncthreads();
+    // the normalised rows in f16 for the scan: q, k row-major and k transposed
+    {
+        const size_t base = ((size_t)n * hk + kh) * GC * DK;
+        for (int e = tid; e < GC * DK / 4; e += 512) {
+            const int row = e / (DK / 4), c4 = e % (DK / 4);
+            const f32x4 a = *reinterpret_cast<const f32x4*>(sq + row * KS_ + 4 * c4);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(sk + row * KS_ + 4 * c4);
+            *reinterpret_cast<f16x4*>(w.q16 + base + row * DK + 4 * c4) =
+                f16x4{to_f16(a[0]), to_f16(a[1]), to_f16(a[2]), to_f16(a[3])};
+            *reinterpret_cast<f16x4*>(w.k16 + base + row * DK + 4 * c4) =
+                f16x4{to_f16(b[0]), to_f16(b[1]), to_f16(b[2]), to_f16(b[3])};
+        }
+        // thread (dim d, token group tg) writes K^T[d][16 tg .. 16 tg + 15]
+        const int d = tid & (DK - 1), tg = tid >> 7;
+        f16x8 lo, hi;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            lo[j] = to_f16(sk[(16 * tg + j) * KS_ + d]);
+            hi[j] = to_f16(sk[(16 * tg + 8 + j) * KS_ + d]);
+        }
+        f16* kt = w.kt16 + base + (size_t)d * GC + 16 * tg;
+        *reinterpret_cast<f16x8*>(kt) = lo;
+        *reinterpret_cast<f16x8*>(kt + 8) = hi;
+    }
     // lower-triangular 16x16 tiles: 10 of K K^T, then 10 of Q K^T
     const int ln = lane & 15, lg4 = lane >> 4;
     for (int tix = wave; tix < 20; tix += 8) {
@@ -423,11 +443,24 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
 }
 
 // gdn_scan_kernel: 8 wavefronts walk the chunks in order for one (V head, 16
-// state columns).  Waves 0-3 own the K side (KS, R, Delta) and waves 4-7 the
-// Q side (QS, O) of chunk row block w % 4; the state update is split over all
-// 8 (16 state rows each).  Chunk n+1 is loaded into registers while chunk n
-// computes; the q/k inverse norms are applied when the registers are written
-// to LDS, so no arithmetic waits on those loads.
+// state columns).  Waves 0-3 own the K side (K.S, R, Delta) and waves 4-7 the
+// Q side (Q.S, O) of chunk row block w % 4; the state update is split over all
+// 8 (16 state rows each).
+//
+// Precision: the state S stays in f32 in registers (wave w holds rows
+// 16w..16w+15 of S^T in the MFMA C layout).  The K.S, Q.S and K^T.Dp
+// products run on v_mfma_f32_16x16x32_f16 with q / k rounded once to f16 and
+// S^T / Dp split into f16 hi + lo parts (two MFMAs per 32-wide block); with
+// normalised q, k this keeps the products within ~1e-5 of f32.  Delta = T.R
+// and M.Delta stay on the f32 MFMA.  Chunk n+1 is loaded into registers while
+// chunk n computes.
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+constexpr int KH_ = DK + 8;  // f16 row stride of [64][128] q / k tiles (272 B)
+constexpr int KT_ = GC + 8;  // f16 row stride of K^T [128][64] and Dp^T [16][64] (144 B)
+
 __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__ q,
                                                        const float* __restrict__ k,
                                                        const float* __restrict__ v,
@@ -435,14 +468,17 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
                                                        float* __restrict__ state,
                                                        float* __restrict__ out, int n_tok,
                                                        int hk, int hv, GdnWs w) {
-    __shared__ __attribute__((aligned(16))) float sk[GC * KS_];
-    __shared__ __attribute__((aligned(16))) float sq[GC * KS_];
-    __shared__ __attribute__((aligned(16))) float st_[GC * TS_];      // T
-    __shared__ __attribute__((aligned(16))) float sm[GC * TS_];       // M
-    __shared__ __attribute__((aligned(16))) float sst[SCOLS * KS_];   // S^T [16][128]
-    __shared__ __attribute__((aligned(16))) float srt[SCOLS * TS_];   // R^T
-    __shared__ __attribute__((aligned(16))) float sdt[SCOLS * TS_];   // Delta^T
-    __shared__ __attribute__((aligned(16))) float sdp[SCOLS * TS_];   // (gamma_C/gamma) Delta, ^T
+    __shared__ __attribute__((aligned(16))) f16 skh[GC * KH_];      // k (normalised)
+    __shared__ __attribute__((aligned(16))) f16 sqh[GC * KH_];      // q (normalised)
+    __shared__ __attribute__((aligned(16))) f16 skt[DK * KT_];      // K^T
+    __shared__ __attribute__((aligned(16))) float st_[GC * TS_];    // T
+    __shared__ __attribute__((aligned(16))) float sm[GC * TS_];     // M
+    __shared__ __attribute__((aligned(16))) f16 ssh[SCOLS * KH_];   // S^T hi
+    __shared__ __attribute__((aligned(16))) f16 ssl[SCOLS * KH_];   // S^T lo
+    __shared__ __attribute__((aligned(16))) float srt[SCOLS * TS_];  // R^T
+    __shared__ __attribute__((aligned(16))) float sdt[SCOLS * TS_];  // Delta^T
+    __shared__ __attribute__((aligned(16))) f16 sdph[SCOLS * KT_];  // (gamma_C/gamma) Delta, ^T, hi
+    __shared__ __attribute__((aligned(16))) f16 sdpl[SCOLS * KT_];  // ... lo
     __shared__ float slg[GC], sb[GC];
     // blockIdx.x = tile * hv + vh: with hv a multiple of 8 the tiles of one
     // head share an XCD (and its L2) under round-robin dispatch.
@@ -452,40 +488,44 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     const int ln = lane & 15, g4 = lane >> 4;
     const int rb = wave & 3;          // chunk row block of this wave
     const bool kside = wave < 4;      // wave-uniform
+    const int row0 = 16 * wave;       // state rows (dims) this wave updates
     const int n_chunks = (n_tok + GC - 1) / GC;
     float* S = state + (size_t)vh * DK * DV;
 
-    // S^T tile from the state (row k, column c0 + c)
-    for (int e = tid; e < SCOLS * DK; e += 512) {
-        const int c = e % SCOLS, row = e / SCOLS;
-        sst[c * KS_ + row] = S[(size_t)row * DV + c0 + c];
-    }
+    // master state: sv[r] = S^T[c = 4 g4 + r][dim = row0 + ln] (MFMA C layout)
+    f32x4 sv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sv[r] = S[(size_t)(row0 + ln) * DV + c0 + 4 * g4 + r];
+    auto put_state = [&]() {  // S^T hi / lo parts for the next K.S, Q.S
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const f16 h = to_f16(sv[r]);
+            ssh[(4 * g4 + r) * KH_ + row0 + ln] = h;
+            ssl[(4 * g4 + r) * KH_ + row0 + ln] = to_f16(sv[r] - (float)h);
+        }
+    };
+    put_state();
 
-    // chunk data staged in registers (prefetch of the next chunk)
-    f32x4 pq[4], pk[4], pt[2], pm[2];
-    float pnq[4], pnk[4];
+    // chunk data staged in registers (prefetch of the next chunk): 16-byte
+    // pieces of q16, k16, kt16 (2 each per thread), T and M (2 each)
+    f32x4 pc[10];
     float pv[4], plg = 0.f, pb = 0.f;
     auto fetch = [&](int n) {
         const int t0 = n * GC;
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int e = tid + 512 * it;
-            const int row = e / (DK / 4), c4 = e % (DK / 4);
-            const int t = t0 + row;
-            const bool in = t < n_tok;
-            const size_t r = (size_t)(in ? t : 0) * hk + kh;
-            pq[it] = *reinterpret_cast<const f32x4*>(q + r * DK + 4 * c4);
-            pk[it] = *reinterpret_cast<const f32x4*>(k + r * DK + 4 * c4);
-            pnq[it] = in ? w.rq[r] : 0.f;
-            pnk[it] = in ? w.rk[r] : 0.f;
-        }
-        const float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
-        const float* mm = w.mm + ((size_t)n * hv + vh) * GC * GC;
+        const size_t qb = ((size_t)n * hk + kh) * GC * DK;
+        const f32x4* q4 = reinterpret_cast<const f32x4*>(w.q16 + qb);
+        const f32x4* k4 = reinterpret_cast<const f32x4*>(w.k16 + qb);
+        const f32x4* kt4 = reinterpret_cast<const f32x4*>(w.kt16 + qb);
+        const f32x4* tm4 = reinterpret_cast<const f32x4*>(w.tm + ((size_t)n * hv + vh) * GC * GC);
+        const f32x4* mm4 = reinterpret_cast<const f32x4*>(w.mm + ((size_t)n * hv + vh) * GC * GC);
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
             const int e = tid + 512 * it;
-            pt[it] = *reinterpret_cast<const f32x4*>(tm + 4 * e);
-            pm[it] = *reinterpret_cast<const f32x4*>(mm + 4 * e);
+            pc[it] = q4[e];
+            pc[2 + it] = k4[e];
+            pc[4 + it] = kt4[e];
+            pc[6 + it] = tm4[e];
+            pc[8 + it] = mm4[e];
         }
         // V tile in the MFMA C layout of the K-side waves: rows 16 rb + 4 g + r, column ln
         if (kside) {
@@ -503,18 +543,16 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     };
     auto stage = [&]() {
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int e = tid + 512 * it;
-            const int row = e / (DK / 4), c4 = e % (DK / 4);
-            *reinterpret_cast<f32x4*>(sq + row * KS_ + 4 * c4) = pq[it] * pnq[it];
-            *reinterpret_cast<f32x4*>(sk + row * KS_ + 4 * c4) = pk[it] * pnk[it];
-        }
-#pragma unroll
         for (int it = 0; it < 2; ++it) {
             const int e = tid + 512 * it;
-            const int row = (4 * e) / GC, c = (4 * e) % GC;
-            *reinterpret_cast<f32x4*>(st_ + row * TS_ + c) = pt[it];
-            *reinterpret_cast<f32x4*>(sm + row * TS_ + c) = pm[it];
+            const int r16 = e >> 4, c16 = (e & 15) * 8;  // [64][128] f16: 16 pieces per row
+            *reinterpret_cast<f32x4*>(sqh + r16 * KH_ + c16) = pc[it];
+            *reinterpret_cast<f32x4*>(skh + r16 * KH_ + c16) = pc[2 + it];
+            const int rt = e >> 3, ct = (e & 7) * 8;     // [128][64] f16: 8 pieces per row
+            *reinterpret_cast<f32x4*>(skt + rt * KT_ + ct) = pc[4 + it];
+            const int rm = e >> 4, cm = (e & 15) * 4;    // [64][64] f32: 16 pieces per row
+            *reinterpret_cast<f32x4*>(st_ + rm * TS_ + cm) = pc[6 + it];
+            *reinterpret_cast<f32x4*>(sm + rm * TS_ + cm) = pc[8 + it];
         }
         if (tid < GC) {
             slg[tid] = plg;
@@ -532,9 +570,19 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         const int t0 = n * GC;
         if (n + 1 < n_chunks) fetch(n + 1);
         const float lgC = slg[GC - 1];
-        // phase 1: KS (waves 0-3) or QS (waves 4-7), rows 16 rb ..
+        // phase 1: K.S (waves 0-3) or Q.S (waves 4-7), rows 16 rb ..
         f32x4 xs = {0.f, 0.f, 0.f, 0.f};
-        xs = tile_mm(kside ? sk : sq, KS_, 16 * rb, sst, KS_, 0, DK / 16, xs);
+        {
+            const f16* xr = (kside ? skh : sqh) + (16 * rb + ln) * KH_ + 8 * g4;
+            const f16* sh = ssh + ln * KH_ + 8 * g4;
+            const f16* sl = ssl + ln * KH_ + 8 * g4;
+#pragma unroll
+            for (int kb = 0; kb < DK / 32; ++kb) {
+                const f16x8 a = *reinterpret_cast<const f16x8*>(xr + 32 * kb);
+                xs = mfma16(a, *reinterpret_cast<const f16x8*>(sh + 32 * kb), xs);
+                xs = mfma16(a, *reinterpret_cast<const f16x8*>(sl + 32 * kb), xs);
+            }
+        }
         if (kside) {  // R = beta (V - gamma KS), written transposed
             f32x4 rv;
 #pragma unroll
@@ -549,14 +597,17 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         if (kside) {
             f32x4 dl = {0.f, 0.f, 0.f, 0.f};
             dl = tile_mm(st_, TS_, 16 * rb, srt, TS_, 0, rb + 1, dl);
-            f32x4 dp;
+            f16x4 dh, dlo;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
-                dp[r] = expf(lgC - slg[i]) * dl[r];
+                const float dp = expf(lgC - slg[i]) * dl[r];
+                dh[r] = to_f16(dp);
+                dlo[r] = to_f16(dp - (float)dh[r]);
             }
             *reinterpret_cast<f32x4*>(sdt + ln * TS_ + 16 * rb + 4 * g4) = dl;
-            *reinterpret_cast<f32x4*>(sdp + ln * TS_ + 16 * rb + 4 * g4) = dp;
+            *reinterpret_cast<f16x4*>(sdph + ln * KT_ + 16 * rb + 4 * g4) = dh;
+            *reinterpret_cast<f16x4*>(sdpl + ln * KT_ + 16 * rb + 4 * g4) = dlo;
         }
         __syncthreads();
         // phase 3a: O = gamma QS + M Delta (waves 4-7)
@@ -570,26 +621,22 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
                 if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = expf(slg[i]) * xs[r] + o[r];
             }
         }
-        // phase 3b: S^T' = exp(lgC) S^T + Dp^T K for state rows 16 w .. 16 w + 15.
-        // Every wave read S^T in phase 1; these rows are only touched by this
-        // wave until the next barrier.
+        // phase 3b: S'^T = exp(lgC) S^T + Dp^T K for state rows row0 .. row0 + 15
         {
-            const float gC = expf(lgC);
-            const int row0 = 16 * wave;
-            f32x4 acc;
+            f32x4 acc = sv * expf(lgC);
+            const f16* ah = sdph + ln * KT_ + 8 * g4;
+            const f16* al = sdpl + ln * KT_ + 8 * g4;
+            const f16* kt = skt + (row0 + ln) * KT_ + 8 * g4;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = gC * sst[(4 * g4 + r) * KS_ + row0 + ln];
-#pragma unroll
-            for (int s = 0; s < GC / 16; ++s) {
-                const f32x4 a = *reinterpret_cast<const f32x4*>(sdp + ln * TS_ + 16 * s + 4 * g4);
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    acc = mfma4(a[r], sk[(16 * s + 4 * g4 + r) * KS_ + row0 + ln], acc);
+            for (int kb = 0; kb < GC / 32; ++kb) {
+                const f16x8 b = *reinterpret_cast<const f16x8*>(kt + 32 * kb);
+                acc = mfma16(*reinterpret_cast<const f16x8*>(ah + 32 * kb), b, acc);
+                acc = mfma16(*reinterpret_cast<const f16x8*>(al + 32 * kb), b, acc);
             }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sst[(4 * g4 + r) * KS_ + row0 + ln] = acc[r];
+            sv = acc;
         }
-        __syncthreads();
+        __syncthreads();  // every wave has read S^T hi / lo and this chunk's tiles
+        put_state();
         if (n + 1 < n_chunks) {
             stage();
 #pragma unroll
@@ -597,10 +644,8 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         }
         __syncthreads();
     }
-    for (int e = tid; e < SCOLS * DK; e += 512) {
-        const int c = e % SCOLS, row = e / SCOLS;
-        S[(size_t)row * DV + c0 + c] = sst[c * KS_ + row];
-    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[(size_t)(row0 + ln) * DV + c0 + 4 * g4 + r] = sv[r];
 }
 
 }  // namespace
@@ -654,7 +699,8 @@ hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, con
 
 size_t gdn_prefill_ws_floats(int32_t n_tok, int32_t n_k_heads, int32_t n_v_heads, int32_t chunk) {
     const size_t nc = (size_t)(n_tok + chunk - 1) / chunk;
-    return 2 * (size_t)n_tok * n_k_heads + 2 * nc * n_v_heads * GC * GC + nc * n_v_heads * GC;
+    // three f16 [64][128] tiles per (chunk, K head) = 1.5 x 8192 floats
+    return 3 * nc * n_k_heads * GC * DK / 2 + 2 * nc * n_v_heads * GC * GC + nc * n_v_heads * GC;
 }
 
 hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, const float* beta,
@@ -664,9 +710,11 @@ hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, co
     if (chunk != GC) return hipErrorInvalidValue;
     const size_t nc = (size_t)(n_tok + GC - 1) / GC;
     GdnWs w;
-    w.rq = ws.buf;
-    w.rk = w.rq + (size_t)n_tok * n_k_heads;
-    w.tm = w.rk + (size_t)n_tok * n_k_heads;
+    const size_t qk = nc * n_k_heads * GC * DK;  // f16 elements of one of q16 / k16 / kt16
+    w.q16 = reinterpret_cast<f16*>(ws.buf);
+    w.k16 = w.q16 + qk;
+    w.kt16 = w.k16 + qk;
+    w.tm = reinterpret_cast<float*>(w.kt16 + qk);
     w.mm = w.tm + nc * n_v_heads * GC * GC;
     w.lg = w.mm + nc * n_v_heads * GC * GC;
     hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)nc, n_k_heads), dim3(512), 0, s, q, k, beta, g,
