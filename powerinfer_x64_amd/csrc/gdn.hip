@@ -479,7 +479,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     __shared__ __attribute__((aligned(16))) float sdt[SCOLS * TS_];  // Delta^T
     __shared__ __attribute__((aligned(16))) f16 sdph[SCOLS * KT_];  // (gamma_C/gamma) Delta, ^T, hi
     __shared__ __attribute__((aligned(16))) f16 sdpl[SCOLS * KT_];  // ... lo
-    __shared__ float slg[GC], sb[GC];
+    __shared__ float sgam[GC], sdec[GC], sb[GC];  // exp(lg_i), exp(lg_C - lg_i), beta
     // blockIdx.x = tile * hv + vh: with hv a multiple of 8 the tiles of one
     // head share an XCD (and its L2) under round-robin dispatch.
     const int vh = blockIdx.x % hv, tile = blockIdx.x / hv, kh = vh % hk;
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     // chunk data staged in registers (prefetch of the next chunk): 16-byte
     // pieces of q16, k16, kt16 (2 each per thread), T and M (2 each)
     f32x4 pc[10];
-    float pv[4], plg = 0.f, pb = 0.f;
+    float pv[4], plg = 0.f, plc = 0.f, pb = 0.f;
     auto fetch = [&](int n) {
         const int t0 = n * GC;
         const size_t qb = ((size_t)n * hk + kh) * GC * DK;
@@ -537,6 +537,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         }
         if (tid < GC) {
             plg = w.lg[((size_t)n * hv + vh) * GC + tid];
+            plc = w.lg[((size_t)n * hv + vh) * GC + GC - 1];
             const int t = t0 + tid;
             pb = t < n_tok ? beta[(size_t)t * hv + vh] : 0.f;
         }
@@ -555,7 +556,8 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             *reinterpret_cast<f32x4*>(sm + rm * TS_ + cm) = pc[8 + it];
         }
         if (tid < GC) {
-            slg[tid] = plg;
+            sgam[tid] = expf(plg);
+            sdec[tid] = expf(plc - plg);
             sb[tid] = pb;
         }
     };
@@ -569,7 +571,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     for (int n = 0; n < n_chunks; ++n) {
         const int t0 = n * GC;
         if (n + 1 < n_chunks) fetch(n + 1);
-        const float lgC = slg[GC - 1];
+        const float gC = sgam[GC - 1];
         // phase 1: K.S (waves 0-3) or Q.S (waves 4-7), rows 16 rb ..
         f32x4 xs = {0.f, 0.f, 0.f, 0.f};
         {
@@ -588,7 +590,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
-                rv[r] = sb[i] * (vcur[r] - expf(slg[i]) * xs[r]);
+                rv[r] = sb[i] * (vcur[r] - sgam[i] * xs[r]);
             }
             *reinterpret_cast<f32x4*>(srt + ln * TS_ + 16 * rb + 4 * g4) = rv;
         }
@@ -601,7 +603,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
-                const float dp = expf(lgC - slg[i]) * dl[r];
+                const float dp = sdec[i] * dl[r];
                 dh[r] = to_f16(dp);
                 dlo[r] = to_f16(dp - (float)dh[r]);
             }
@@ -618,12 +620,12 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
                 const int t = t0 + i;
-                if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = expf(slg[i]) * xs[r] + o[r];
+                if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = sgam[i] * xs[r] + o[r];
             }
         }
         // phase 3b: S'^T = exp(lgC) S^T + Dp^T K for state rows row0 .. row0 + 15
         {
-            f32x4 acc = sv * expf(lgC);
+            f32x4 acc = sv * gC;
             const f16* ah = sdph + ln * KT_ + 8 * g4;
             const f16* al = sdpl + ln * KT_ + 8 * g4;
             const f16* kt = skt + (row0 + ln) * KT_ + 8 * g4;
