@@ -259,8 +259,8 @@ struct GdnWs {
     f16* q16;   // [n_chunks][Hk][64][128] q / max(|q|,1e-12) / sqrt(Dk), f16
     f16* k16;   // [n_chunks][Hk][64][128] k / max(|k|,1e-12), f16
     f16* kt16;  // [n_chunks][Hk][128][64] the same k, transposed
-    float* tm;  // [n_chunks][Hv][64][64] (I + A)^-1
-    float* mm;  // [n_chunks][Hv][64][64] M
+    float* tm;  // [n_chunks][Hv] (I + A)^-1 as f16 hi [64][64] then f16 lo [64][64]
+    float* mm;  // [n_chunks][Hv] M, the same hi / lo form
     float* lg;  // [n_chunks][Hv][64] cumulative log decay
 };
 
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
         }
         __syncthreads();
         if (on) {
-            float* mm = w.mm + ((size_t)n * hv + vh) * GC * GC;
+            f16* mm = reinterpret_cast<f16*>(w.mm + ((size_t)n * hv + vh) * GC * GC);
             for (int e = ht; e < GC * GC; e += 256) {
                 const int i = e / GC, j = e % GC;
                 float a = 0.f, m = 0.f;
@@ -393,7 +393,9 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
                 }
                 sa[i * TS_ + j] = a;
                 st[i * TS_ + j] = 0.f;
-                mm[e] = m;
+                const f16 mh = to_f16(m);
+                mm[e] = mh;
+                mm[GC * GC + e] = to_f16(m - (float)mh);
             }
         }
         __syncthreads();
@@ -432,10 +434,18 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
             __syncthreads();
         }
         if (on) {
-            float* tm = w.tm + ((size_t)n * hv + vh) * GC * GC;
+            f16* tm = reinterpret_cast<f16*>(w.tm + ((size_t)n * hv + vh) * GC * GC);
             for (int e = ht; e < GC * GC / 4; e += 256) {
                 const int row = e / (GC / 4), c4 = e % (GC / 4);
-                *reinterpret_cast<f32x4*>(tm + row * GC + 4 * c4) = *reinterpret_cast<const f32x4*>(st + row * TS_ + 4 * c4);
+                const f32x4 x = *reinterpret_cast<const f32x4*>(st + row * TS_ + 4 * c4);
+                f16x4 h, l;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    h[r] = to_f16(x[r]);
+                    l[r] = to_f16(x[r] - (float)h[r]);
+                }
+                *reinterpret_cast<f16x4*>(tm + row * GC + 4 * c4) = h;
+                *reinterpret_cast<f16x4*>(tm + GC * GC + row * GC + 4 * c4) = l;
             }
         }
         __syncthreads();  // A, T and the scratch are rewritten for the next V heads
@@ -452,14 +462,34 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
 // products run on v_mfma_f32_16x16x32_f16 with q / k rounded once to f16 and
 // S^T / Dp split into f16 hi + lo parts (two MFMAs per 32-wide block); with
 // normalised q, k this keeps the products within ~1e-5 of f32.  Delta = T.R
-// and M.Delta stay on the f32 MFMA.  Chunk n+1 is loaded into registers while
-// chunk n computes.
+// and M.Delta split both operands (three MFMAs per block).  Chunk n+1 is
+// loaded into registers while chunk n computes.
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 constexpr int KH_ = DK + 8;  // f16 row stride of [64][128] q / k tiles (272 B)
-constexpr int KT_ = GC + 8;  // f16 row stride of K^T [128][64] and Dp^T [16][64] (144 B)
+constexpr int KT_ = GC + 8;  // f16 row stride of [.][64] tiles: K^T, T, M, R^T, Delta^T (144 B)
+
+// C[16 x 16] = X[row0 .. row0+15][0 .. 32 nkb) . Y^T, X and Y^T [16][64] given
+// as f16 hi + lo parts (row stride KT_): hi.hi + hi.lo + lo.hi on the f16
+// MFMA, so the product keeps ~22 bits.  Lane: A rows row0 + ln, B column ln.
+__device__ __forceinline__ f32x4 mm_split(const f16* xh, const f16* xl, const f16* yh,
+                                          const f16* yl, int row0, int nkb) {
+    const int l = threadIdx.x & 63, ln = l & 15, g4 = l >> 4;
+    const int xo = (row0 + ln) * KT_ + 8 * g4, yo = ln * KT_ + 8 * g4;
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nkb; ++kb) {
+        const f16x8 ah = *reinterpret_cast<const f16x8*>(xh + xo + 32 * kb);
+        const f16x8 al = *reinterpret_cast<const f16x8*>(xl + xo + 32 * kb);
+        const f16x8 bh = *reinterpret_cast<const f16x8*>(yh + yo + 32 * kb);
+        const f16x8 bl = *reinterpret_cast<const f16x8*>(yl + yo + 32 * kb);
+        c = mfma16(ah, bh, c);
+        c = mfma16(ah, bl, c);
+        c = mfma16(al, bh, c);
+    }
+    return c;
+}
 
 __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__ q,
                                                        const float* __restrict__ k,
@@ -471,12 +501,16 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     __shared__ __attribute__((aligned(16))) f16 skh[GC * KH_];      // k (normalised)
     __shared__ __attribute__((aligned(16))) f16 sqh[GC * KH_];      // q (normalised)
     __shared__ __attribute__((aligned(16))) f16 skt[DK * KT_];      // K^T
-    __shared__ __attribute__((aligned(16))) float st_[GC * TS_];    // T
-    __shared__ __attribute__((aligned(16))) float sm[GC * TS_];     // M
+    __shared__ __attribute__((aligned(16))) f16 sth[GC * KT_];      // T hi
+    __shared__ __attribute__((aligned(16))) f16 stl[GC * KT_];      // T lo
+    __shared__ __attribute__((aligned(16))) f16 smh[GC * KT_];      // M hi
+    __shared__ __attribute__((aligned(16))) f16 sml[GC * KT_];      // M lo
     __shared__ __attribute__((aligned(16))) f16 ssh[SCOLS * KH_];   // S^T hi
     __shared__ __attribute__((aligned(16))) f16 ssl[SCOLS * KH_];   // S^T lo
-    __shared__ __attribute__((aligned(16))) float srt[SCOLS * TS_];  // R^T
-    __shared__ __attribute__((aligned(16))) float sdt[SCOLS * TS_];  // Delta^T
+    __shared__ __attribute__((aligned(16))) f16 srth[SCOLS * KT_];  // R^T hi
+    __shared__ __attribute__((aligned(16))) f16 srtl[SCOLS * KT_];  // R^T lo
+    __shared__ __attribute__((aligned(16))) f16 sdth[SCOLS * KT_];  // Delta^T hi
+    __shared__ __attribute__((aligned(16))) f16 sdtl[SCOLS * KT_];  // Delta^T lo
     __shared__ __attribute__((aligned(16))) f16 sdph[SCOLS * KT_];  // (gamma_C/gamma) Delta, ^T, hi
     __shared__ __attribute__((aligned(16))) f16 sdpl[SCOLS * KT_];  // ... lo
     __shared__ float sgam[GC], sdec[GC], sb[GC];  // exp(lg_i), exp(lg_C - lg_i), beta
@@ -551,9 +585,10 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             *reinterpret_cast<f32x4*>(skh + r16 * KH_ + c16) = pc[2 + it];
             const int rt = e >> 3, ct = (e & 7) * 8;     // [128][64] f16: 8 pieces per row
             *reinterpret_cast<f32x4*>(skt + rt * KT_ + ct) = pc[4 + it];
-            const int rm = e >> 4, cm = (e & 15) * 4;    // [64][64] f32: 16 pieces per row
-            *reinterpret_cast<f32x4*>(st_ + rm * TS_ + cm) = pc[6 + it];
-            *reinterpret_cast<f32x4*>(sm + rm * TS_ + cm) = pc[8 + it];
+            // T, M: hi [64][64] f16 (pieces 0..511), then lo (512..1023)
+            const int rm = tid >> 3, cm = (tid & 7) * 8;
+            *reinterpret_cast<f32x4*>((it ? stl : sth) + rm * KT_ + cm) = pc[6 + it];
+            *reinterpret_cast<f32x4*>((it ? sml : smh) + rm * KT_ + cm) = pc[8 + it];
         }
         if (tid < GC) {
             sgam[tid] = expf(plg);
@@ -585,37 +620,41 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
                 xs = mfma16(a, *reinterpret_cast<const f16x8*>(sl + 32 * kb), xs);
             }
         }
-        if (kside) {  // R = beta (V - gamma KS), written transposed
-            f32x4 rv;
+        if (kside) {  // R = beta (V - gamma KS), written transposed as hi / lo
+            f16x4 rh, rl;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
-                rv[r] = sb[i] * (vcur[r] - sgam[i] * xs[r]);
+                const float rv = sb[i] * (vcur[r] - sgam[i] * xs[r]);
+                rh[r] = to_f16(rv);
+                rl[r] = to_f16(rv - (float)rh[r]);
             }
-            *reinterpret_cast<f32x4*>(srt + ln * TS_ + 16 * rb + 4 * g4) = rv;
+            *reinterpret_cast<f16x4*>(srth + ln * KT_ + 16 * rb + 4 * g4) = rh;
+            *reinterpret_cast<f16x4*>(srtl + ln * KT_ + 16 * rb + 4 * g4) = rl;
         }
         __syncthreads();
         // phase 2: Delta = T R (T lower triangular: column blocks <= rb)
         if (kside) {
-            f32x4 dl = {0.f, 0.f, 0.f, 0.f};
-            dl = tile_mm(st_, TS_, 16 * rb, srt, TS_, 0, rb + 1, dl);
-            f16x4 dh, dlo;
+            const f32x4 dl = mm_split(sth, stl, srth, srtl, 16 * rb, (rb >> 1) + 1);
+            f16x4 dh, dlo, ph, pl;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
+                dh[r] = to_f16(dl[r]);
+                dlo[r] = to_f16(dl[r] - (float)dh[r]);
                 const float dp = sdec[i] * dl[r];
-                dh[r] = to_f16(dp);
-                dlo[r] = to_f16(dp - (float)dh[r]);
+                ph[r] = to_f16(dp);
+                pl[r] = to_f16(dp - (float)ph[r]);
             }
-            *reinterpret_cast<f32x4*>(sdt + ln * TS_ + 16 * rb + 4 * g4) = dl;
-            *reinterpret_cast<f16x4*>(sdph + ln * KT_ + 16 * rb + 4 * g4) = dh;
-            *reinterpret_cast<f16x4*>(sdpl + ln * KT_ + 16 * rb + 4 * g4) = dlo;
+            *reinterpret_cast<f16x4*>(sdth + ln * KT_ + 16 * rb + 4 * g4) = dh;
+            *reinterpret_cast<f16x4*>(sdtl + ln * KT_ + 16 * rb + 4 * g4) = dlo;
+            *reinterpret_cast<f16x4*>(sdph + ln * KT_ + 16 * rb + 4 * g4) = ph;
+            *reinterpret_cast<f16x4*>(sdpl + ln * KT_ + 16 * rb + 4 * g4) = pl;
         }
         __syncthreads();
         // phase 3a: O = gamma QS + M Delta (waves 4-7)
         if (!kside) {
-            f32x4 o = {0.f, 0.f, 0.f, 0.f};
-            o = tile_mm(sm, TS_, 16 * rb, sdt, TS_, 0, rb + 1, o);
+            const f32x4 o = mm_split(smh, sml, sdth, sdtl, 16 * rb, (rb >> 1) + 1);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
