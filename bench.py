@@ -471,6 +471,10 @@ def main():
         wl["c1_mha_decode_513"] = r1
         wl["c5_gdn_decode_step"] = bench_gdn_decode(torch, rt, dev, timer, a.steps, a.warmup)
         wl["c5_gdn_prefill_4096"] = bench_gdn_prefill(torch, rt, dev, timer, a.steps, a.warmup)
+        torch.cuda.empty_cache()
+        # TurboQuant compressed-KV decode on the config 2 shape (3-bit + QJL keys, f16 values)
+        wl["c2_turboquant_decode"] = bench_tq_decode(torch, rt, dev, timer, lens, 32, 8, 0x5EED0004,
+                                                     a.steps, a.warmup)
         line["workloads"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                                  for kk, vv in v.items()} for k, v in wl.items()}
     line["cpu_baseline_wall_s"] = round(cpu_wall, 2)
