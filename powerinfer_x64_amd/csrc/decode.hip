@@ -59,6 +59,7 @@ struct Tile<f16, D> {
     static constexpr size_t KBLK = (size_t)kPageTokens * D * 2;  // bytes per (page, KV head)
     static constexpr size_t VBLK = KBLK;
     static constexpr int QD = D;  // floats per query row
+    static __device__ __forceinline__ void prepare() {}
     f16x8 k[NK];
     f16x4 v[NV];
     struct Q {
@@ -117,6 +118,7 @@ struct Tile<float, D> {
     static constexpr size_t KBLK = (size_t)kPageTokens * D * 4;  // bytes per (page, KV head)
     static constexpr size_t VBLK = KBLK;
     static constexpr int QD = D;
+    static __device__ __forceinline__ void prepare() {}
     f32x4 k[NK];
     f32x4 v[NV];
     struct Q {
@@ -188,6 +190,29 @@ __device__ __forceinline__ uint32_t tq_centroid_f16(uint32_t c) {
     return ((uint32_t)(kTqMagF16 >> (16 * k)) & 0xFFFFu) | ((c & 4u) ? 0u : 0x8000u);
 }
 
+// Decoding tables in LDS, built once per workgroup: a pair of 3-bit codes
+// (6 bits, first code low) -> its two f16 centroids; a byte of QJL sign bits
+// -> eight f16 +-1 values.
+struct TqLut {
+    uint32_t pair[64];
+    f16x8 sign[256];
+};
+__device__ __forceinline__ TqLut& tq_lut() {
+    __shared__ TqLut lut;
+    return lut;
+}
+__device__ __forceinline__ void tq_lut_build() {
+    TqLut& L = tq_lut();
+    const int t = threadIdx.x;
+    if (t < 64) L.pair[t] = tq_centroid_f16(t & 7) | (tq_centroid_f16(t >> 3) << 16);
+    for (int b = t; b < 256; b += blockDim.x) {
+        f16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = ((b >> e) & 1) ? (f16)1.0f : (f16)-1.0f;
+        L.sign[b] = v;
+    }
+}
+
 template <>
 struct Tile<TqKey, 128> {
     static constexpr int D = 128;
@@ -232,41 +257,29 @@ struct Tile<TqKey, 128> {
             }
         }
     }
-    // code of element j (0..31) of this lane's quarter: bits 3j .. 3j+2
-    __device__ __forceinline__ uint32_t code_of(int j) const {
-        const int bit = 3 * j, w = bit >> 5, off = bit & 31;
-        uint32_t x = code[w] >> off;
-        if (off > 29) x |= code[w + 1] << (32 - off);
-        return x & 7u;
+    static __device__ __forceinline__ void prepare() { tq_lut_build(); }
+    // the 6-bit code pair of elements 2p, 2p+1 of this lane's quarter
+    __device__ __forceinline__ uint32_t pair_of(int p) const {
+        const int bit = 6 * p, w = bit >> 5, off = bit & 31;
+        const uint32_t x = off <= 26 ? code[w] >> off
+                                     : __builtin_amdgcn_alignbit(code[w + 1], code[w], off);
+        return x & 63u;
     }
     __device__ __forceinline__ f32x4 scores(const Q& q) const {
+        const TqLut& L = tq_lut();
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            f16x8 kf;
+            u32x4 w;
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const uint32_t pr = tq_centroid_f16(code_of(8 * kb + e)) |
-                                    (tq_centroid_f16(code_of(8 * kb + e + 1)) << 16);
-                const f16x2 h2 = __builtin_bit_cast(f16x2, pr);
-                kf[e] = h2[0];
-                kf[e + 1] = h2[1];
-            }
+            for (int p = 0; p < 4; ++p) w[p] = L.pair[pair_of(4 * kb + p)];
+            const f16x8 kf = __builtin_bit_cast(f16x8, w);
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.hi[kb], s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.lo[kb], s, 0, 0, 0);
         }
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            f16x8 sf;
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const uint32_t b0 = (sign >> (8 * kb + e)) & 1u, b1 = (sign >> (8 * kb + e + 1)) & 1u;
-                // +1.0 = 0x3C00 when the bit is set, -1.0 = 0xBC00 otherwise
-                const uint32_t pr = 0xBC00BC00u - ((b0 << 15) | (b1 << 31));
-                const f16x2 h2 = __builtin_bit_cast(f16x2, pr);
-                sf[e] = h2[0];
-                sf[e + 1] = h2[1];
-            }
+            const f16x8 sf = L.sign[(sign >> (8 * kb)) & 255u];
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, q.hi[4 + kb], s, 0, 0, 0);
         }
         return s * norm;
@@ -405,6 +418,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
 
     const int n_kv = g.n_kv_heads;
     const int tid = threadIdx.x;
+    T::prepare();  // tile tables in LDS; the scan below has barriers
     const int per_kv = scan_items(p.ctx_len, p.batch, p.item_pages, s_cum, s_red);
     const int n_items = n_kv * per_kv;
     const int chunk = (n_items + gridDim.x - 1) / gridDim.x;
