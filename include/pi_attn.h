@@ -216,6 +216,31 @@ int pi_ssm_gated_delta_step(pi_handle h, float* h_out, float* h_state, const flo
                             const float* h_g, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
                             int32_t v_hd);
 
+/* ---- Attention layer cache (the seam in InferenceContext::forward) -------------------
+ * LayerCache (src/model/mod.rs:73-106) of one attention layer for one sequence, held on the
+ * device: a paged pool of max_tokens tokens, the per-head Q/K RMSNorm weights (NULL when the
+ * layer has none, src/model/mod.rs:1035-1070), the RoPE mode (NORM when h_sections is NULL,
+ * else the sectioned NeoX rotation, :1072-1138) and the KV dtype (PI_F32 or PI_F16; PI_F16
+ * needs head_dim 128 or 256, PI_F32 head_dim 64 or 128). */
+typedef struct pi_attn_layer_s* pi_attn_layer;
+int pi_attn_layer_create(pi_handle h, int32_t max_tokens, int32_t n_heads, int32_t n_kv_heads,
+                         int32_t head_dim, int32_t kv_dtype, const float* h_q_norm_w,
+                         const float* h_k_norm_w, float eps, int32_t rope_dim, float rope_base,
+                         const int32_t* h_sections, int32_t gqa_mode, pi_attn_layer* out);
+void pi_attn_layer_destroy(pi_attn_layer layer);
+/* src/model/mod.rs:1035-1196 for n_tokens consecutive tokens of the sequence (the :668 token
+ * loop as one call): norm, RoPE at positions seq_len .. seq_len + n_tokens - 1, append, then
+ * for every token attention over all cached keys up to and including its own, and the sigmoid
+ * gate when h_gate is not NULL.  Host slices: q [n_tokens][n_heads][head_dim] and k
+ * [n_tokens][n_kv_heads][head_dim] are normalised and rotated in place, as in the reference;
+ * v like k; gate and out like q.  A full cache fails with PI_ERR_OUT_OF_MEMORY and changes
+ * nothing.  Synchronous. */
+int pi_attn_layer_forward(pi_handle h, pi_attn_layer layer, float* h_q, float* h_k,
+                          const float* h_v, const float* h_gate, int32_t n_tokens, float* h_out);
+/* LayerCache::reset (src/model/mod.rs:1854-1856): the sequence restarts at position 0. */
+void pi_attn_layer_reset(pi_attn_layer layer);
+int32_t pi_attn_layer_seq_len(pi_attn_layer layer);
+
 /* ---- TurboQuant compressed KV (src/turboquant/mod.rs:408-566) -------------------------
  * CompressedKVCache with head_dim 128: per KV head h a TurboQuant(3 bits, 128, 128 QJL bits,
  * seed 0xCAFEBABE + h) key quantizer (:430-437) and f16 values.  Keys are stored as 64-byte

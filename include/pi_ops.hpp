@@ -11,7 +11,8 @@
 //   powerinfer::rocm -- the offload seam of src/cuda/mod.rs:373-537:
 //                       Device::init() -> std::optional (None = CPU path) and
 //                       try_* calls -> std::optional<Result> (Option<Result<(),
-//                       String>>).
+//                       String>>); DeviceLayerCache, the device-resident
+//                       LayerCache with forward's attention step.
 // The ops / ssm free functions run on the calling thread's default device and
 // throw BackendError where the reference would panic (a size mismatch, its
 // debug_assert_eq!) or where the device fails.
@@ -119,6 +120,58 @@ public:
 private:
     explicit Device(pi_handle h) : h_(h) {}
     pi_handle h_ = nullptr;
+};
+
+// LayerCache (src/model/mod.rs:73-106) of one attention layer for one sequence on the device,
+// with the attention step of forward (src/model/mod.rs:1035-1196) as the offload seam: the
+// caller hands over host slices as forward holds them; try_forward returns Some(Ok) or
+// Some(Err(text)), and the caller aborts forward on an error as at src/model/mod.rs:619.
+class DeviceLayerCache {
+public:
+    struct Config {
+        size_t max_tokens = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0;
+        int kv_dtype = PI_F16;
+        std::span<const float> q_norm, k_norm;  // empty: the layer has no Q/K norm
+        float eps = 1e-6f;
+        size_t rope_dim = 0;  // 0: head_dim
+        float rope_base = 1e6f;
+        std::optional<std::array<int32_t, 4>> sections;  // IMRoPE sections, else NORM RoPE
+        int gqa_mode = PI_GQA_MODULO;
+    };
+    DeviceLayerCache(const Device& dev, const Config& c) : dev_(&dev), c_(c) {
+        const int32_t rd = (int32_t)(c.rope_dim ? c.rope_dim : c.head_dim);
+        dev.check(pi_attn_layer_create(dev.raw(), (int32_t)c.max_tokens, (int32_t)c.n_heads,
+                                       (int32_t)c.n_kv_heads, (int32_t)c.head_dim, c.kv_dtype,
+                                       c.q_norm.empty() ? nullptr : c.q_norm.data(),
+                                       c.k_norm.empty() ? nullptr : c.k_norm.data(), c.eps, rd,
+                                       c.rope_base, c.sections ? c.sections->data() : nullptr,
+                                       c.gqa_mode, &l_));
+    }
+    DeviceLayerCache(const DeviceLayerCache&) = delete;
+    DeviceLayerCache& operator=(const DeviceLayerCache&) = delete;
+    ~DeviceLayerCache() { pi_attn_layer_destroy(l_); }
+
+    // The tokens of this forward call: q, k rotated in place; out written.
+    std::optional<Result> try_forward(std::span<float> q, std::span<float> k,
+                                      std::span<const float> v, std::span<const float> gate,
+                                      size_t n_tokens, std::span<float> out) {
+        const size_t nq = n_tokens * c_.n_heads * c_.head_dim;
+        const size_t nk = n_tokens * c_.n_kv_heads * c_.head_dim;
+        if (q.size() != nq || out.size() != nq || k.size() != nk || v.size() != nk ||
+            (!gate.empty() && gate.size() != nq))
+            return Result{PI_ERR_INVALID_ARG, "layer forward: slice sizes do not match the heads"};
+        return dev_->result(pi_attn_layer_forward(dev_->raw(), l_, q.data(), k.data(), v.data(),
+                                                  gate.empty() ? nullptr : gate.data(),
+                                                  (int32_t)n_tokens, out.data()));
+    }
+    // LayerCache::reset (src/model/mod.rs:1854-1856)
+    void reset() { pi_attn_layer_reset(l_); }
+    size_t seq_len() const { return (size_t)pi_attn_layer_seq_len(l_); }
+
+private:
+    const Device* dev_;
+    Config c_;
+    pi_attn_layer l_ = nullptr;
 };
 
 // The calling thread's default device (device 0), opened on first use.

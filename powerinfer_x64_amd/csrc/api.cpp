@@ -36,6 +36,23 @@ struct pi_kv_pool_s {
     size_t bytes;
 };
 
+struct pi_attn_layer_s {
+    pi_handle owner;
+    pi_kv_pool pool = nullptr;      // max_pages pages, page i at physical page i
+    int32_t max_pages = 0, n_heads = 0, n_kv = 0, dim = 0, kv_dtype = 0;
+    int32_t rope_dim = 0, gqa_mode = 0;
+    float eps = 0.f, rope_base = 0.f;
+    int32_t sections[4] = {0, 0, 0, 0};
+    bool has_sections = false;
+    float* d_qn = nullptr;          // per-head RMSNorm weights (null: no norm)
+    float* d_kn = nullptr;
+    int32_t* d_pt = nullptr;        // kLayerRows identical rows of the identity page table
+    int32_t* d_ctx = nullptr;       // per-row context lengths, then the start position
+    float* d_buf = nullptr;         // staging: q, k, v, gate, out, f16 q / k / v
+    size_t buf_floats = 0;
+    int32_t seq_len = 0;
+};
+
 struct pi_tq_pool_s {
     pi_handle owner;
     pi::TqPool t;
@@ -754,6 +771,152 @@ int pi_ssm_gated_delta_step(pi_handle h, float* h_out, float* h_state, const flo
     if ((rc = copy_sync(h, h_state, ds, ns * 4, hipMemcpyDeviceToHost, "gated_delta_step"))) return rc;
     if ((rc = copy_sync(h, h_out, dout, nv * 4, hipMemcpyDeviceToHost, "gated_delta_step"))) return rc;
     PI_HIP(h, hipStreamSynchronize(h->stream), "gated_delta_step");
+    return PI_OK;
+}
+
+// ---- attention layer cache ------------------------------------------------------------
+
+namespace {
+constexpr int kLayerRows = 256;  // query rows per decode launch of a multi-token forward
+}
+
+int pi_attn_layer_create(pi_handle h, int32_t max_tokens, int32_t n_heads, int32_t n_kv_heads,
+                         int32_t head_dim, int32_t kv_dtype, const float* h_q_norm_w,
+                         const float* h_k_norm_w, float eps, int32_t rope_dim, float rope_base,
+                         const int32_t* h_sections, int32_t gqa_mode, pi_attn_layer* out) {
+    PI_CHECK_HANDLE(h);
+    if (!out) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: out is null");
+    *out = nullptr;
+    if (max_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: max_tokens=%d n_heads=%d n_kv_heads=%d",
+                    max_tokens, n_heads, n_kv_heads);
+    if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: gqa_mode %d", gqa_mode);
+    pi_attn_layer L = new (std::nothrow) pi_attn_layer_s();
+    if (!L) return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_attn_layer_create: host allocation");
+    L->owner = h;
+    L->max_pages = (max_tokens + pi::kPageTokens - 1) / pi::kPageTokens;
+    L->n_heads = n_heads;
+    L->n_kv = n_kv_heads;
+    L->dim = head_dim;
+    L->kv_dtype = kv_dtype;
+    L->rope_dim = rope_dim;
+    L->gqa_mode = gqa_mode;
+    L->eps = eps;
+    L->rope_base = rope_base;
+    if (h_sections) {
+        L->has_sections = true;
+        std::memcpy(L->sections, h_sections, sizeof L->sections);
+    }
+    auto undo = [&](int rc) {
+        pi_attn_layer_destroy(L);
+        return rc;
+    };
+    int rc = pi_kv_pool_create(h, L->max_pages, pi::kPageTokens, n_kv_heads, head_dim, kv_dtype, &L->pool);
+    if (rc) return undo(rc);
+    hipError_t e = hipSuccess;
+    const size_t pt = (size_t)kLayerRows * L->max_pages;
+    e = hipMalloc(reinterpret_cast<void**>(&L->d_pt), pt * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&L->d_ctx), (kLayerRows + 1) * sizeof(int32_t));
+    if (e == hipSuccess && h_q_norm_w) e = hipMalloc(reinterpret_cast<void**>(&L->d_qn), head_dim * sizeof(float));
+    if (e == hipSuccess && h_k_norm_w) e = hipMalloc(reinterpret_cast<void**>(&L->d_kn), head_dim * sizeof(float));
+    if (e == hipSuccess && L->d_qn) e = hipMemcpy(L->d_qn, h_q_norm_w, head_dim * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess && L->d_kn) e = hipMemcpy(L->d_kn, h_k_norm_w, head_dim * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        std::vector<int32_t> rows(pt);
+        for (size_t i = 0; i < pt; ++i) rows[i] = (int32_t)(i % L->max_pages);
+        e = hipMemcpy(L->d_pt, rows.data(), pt * sizeof(int32_t), hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) return undo(hip_fail(h, e, "pi_attn_layer_create"));
+    *out = L;
+    return PI_OK;
+}
+
+void pi_attn_layer_destroy(pi_attn_layer L) {
+    if (!L) return;
+    (void)hipSetDevice(L->owner->device);
+    (void)hipDeviceSynchronize();
+    pi_kv_pool_destroy(L->pool);
+    (void)hipFree(L->d_pt);
+    (void)hipFree(L->d_ctx);
+    (void)hipFree(L->d_qn);
+    (void)hipFree(L->d_kn);
+    (void)hipFree(L->d_buf);
+    delete L;
+}
+
+void pi_attn_layer_reset(pi_attn_layer L) {
+    if (L) L->seq_len = 0;
+}
+
+int32_t pi_attn_layer_seq_len(pi_attn_layer L) { return L ? L->seq_len : 0; }
+
+int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, const float* h_v,
+                          const float* h_gate, int32_t n_tokens, float* h_out) {
+    PI_CHECK_HANDLE(h);
+    if (!L || !h_q || !h_k || !h_v || !h_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward: null argument");
+    if (n_tokens < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward: n_tokens=%d", n_tokens);
+    if (n_tokens == 0) return PI_OK;
+    const int prev = L->seq_len;
+    if ((long long)prev + n_tokens > (long long)L->max_pages * pi::kPageTokens)
+        return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_attn_layer_forward: %d + %d tokens exceed the layer cache of %d",
+                    prev, n_tokens, L->max_pages * pi::kPageTokens);
+    hipStream_t s = h->stream;
+    void* sv = reinterpret_cast<void*>(s);
+    PI_HIP(h, hipSetDevice(h->device), "pi_attn_layer_forward");
+    const int D = L->dim;
+    const size_t nq = (size_t)n_tokens * L->n_heads * D, nk = (size_t)n_tokens * L->n_kv * D;
+    const size_t need = 3 * nq + 2 * nk + (nq + 2 * nk + 1) / 2;  // q, gate, out, k, v, f16 copies
+    int rc = grow(h, &L->d_buf, &L->buf_floats, need, s, "pi_attn_layer_forward staging", false);
+    if (rc) return rc;
+    float *dq = L->d_buf, *dg = dq + nq, *dout = dg + nq, *dk = dout + nq, *dv = dk + nk;
+    void* hq16 = dv + nk;
+    void* hk16 = reinterpret_cast<char*>(hq16) + nq * 2;
+    void* hv16 = reinterpret_cast<char*>(hk16) + nk * 2;
+    if ((rc = copy_sync(h, dq, h_q, nq * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
+    if ((rc = copy_sync(h, dk, h_k, nk * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
+    if ((rc = copy_sync(h, dv, h_v, nk * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
+    if (h_gate && (rc = copy_sync(h, dg, h_gate, nq * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
+    // norm + RoPE + append at positions prev .. prev + n_tokens - 1
+    int32_t* d_start = L->d_ctx + kLayerRows;
+    PI_HIP(h, hipMemcpyAsync(d_start, &prev, sizeof(int32_t), hipMemcpyHostToDevice, s), "pi_attn_layer_forward");
+    if ((rc = pi_attn_prologue(h, dq, dk, dv, L->d_qn, L->d_kn, L->eps, L->rope_dim, L->rope_base,
+                               L->has_sections ? L->sections : nullptr, L->pool, L->d_pt,
+                               L->max_pages, d_start, 1, n_tokens, L->n_heads, sv)))
+        return rc;
+    const float scale = 1.0f / std::sqrt((float)D);
+    if (prev == 0 && n_tokens > 1 && D == 128 && L->kv_dtype == PI_F16) {
+        // a fresh prompt: causal flash attention over the rotated rows (f16 inputs)
+        PI_HIP(h, pi::launch_to_half(dq, hq16, nq, s), "pi_attn_layer_forward");
+        PI_HIP(h, pi::launch_to_half(dk, hk16, nk, s), "pi_attn_layer_forward");
+        PI_HIP(h, pi::launch_to_half(dv, hv16, nk, s), "pi_attn_layer_forward");
+        if ((rc = pi_attn_prefill(h, hq16, hk16, hv16, PI_F16, 1, n_tokens, L->n_heads, L->n_kv, D,
+                                  1, L->gqa_mode, scale, dout, sv)))
+            return rc;
+        if (h_gate) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "pi_attn_layer_forward");
+    } else {
+        // one decode row per token over the paged cache: row i sees prev + i + 1 keys
+        std::vector<int32_t> ctx(kLayerRows);
+        for (int r0 = 0; r0 < n_tokens; r0 += kLayerRows) {
+            const int rows = std::min(kLayerRows, n_tokens - r0);
+            for (int i = 0; i < rows; ++i) ctx[i] = prev + r0 + i + 1;
+            PI_HIP(h, hipMemcpyAsync(L->d_ctx, ctx.data(), rows * sizeof(int32_t), hipMemcpyHostToDevice, s),
+                   "pi_attn_layer_forward");
+            const size_t off = (size_t)r0 * L->n_heads * D;
+            if ((rc = pi_attn_decode(h, dq + off, L->pool, L->d_pt, L->max_pages, L->d_ctx, rows,
+                                     L->n_heads, L->gqa_mode, scale, h_gate ? dg + off : nullptr,
+                                     dout + off, sv)))
+                return rc;
+            // the host row of context lengths is reused by the next chunk
+            PI_HIP(h, hipStreamSynchronize(s), "pi_attn_layer_forward");
+        }
+    }
+    if ((rc = copy_sync(h, h_out, dout, nq * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
+    if ((rc = copy_sync(h, h_q, dq, nq * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
+    if ((rc = copy_sync(h, h_k, dk, nk * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
+    PI_HIP(h, hipStreamSynchronize(s), "pi_attn_layer_forward");
+    L->seq_len = prev + n_tokens;
     return PI_OK;
 }
 

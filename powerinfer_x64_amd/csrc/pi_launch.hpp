@@ -103,6 +103,8 @@ hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, in
 hipError_t launch_head_rmsnorm(float* x, const float* w, int32_t n_rows, int32_t dim,
                                int32_t row_stride, float eps, hipStream_t s);
 hipError_t launch_softmax(float* x, int32_t n, hipStream_t s);
+hipError_t launch_to_half(const float* x, void* y, size_t n, hipStream_t s);
+hipError_t launch_apply_gate(float* out, const float* gate, size_t n, hipStream_t s);
 hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
                                 const float* k_norm_w, float eps, const RopeFreqs& freqs,
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,

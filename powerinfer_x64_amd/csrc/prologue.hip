@@ -301,6 +301,37 @@ hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, in
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void to_half_kernel(const float* __restrict__ x,
+                                                      f16* __restrict__ y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        y[i] = to_f16(x[i]);
+}
+
+// out *= sigmoid(gate) (src/model/mod.rs:1192-1196)
+__global__ __launch_bounds__(256) void apply_gate_kernel(float* __restrict__ out,
+                                                         const float* __restrict__ gate, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        out[i] *= 1.0f / (1.0f + expf(-gate[i]));
+}
+
+static unsigned grid_1d(size_t n) {
+    const size_t b = (n + 255) / 256;
+    return (unsigned)(b > 65536 ? 65536 : (b == 0 ? 1 : b));
+}
+
+hipError_t launch_to_half(const float* x, void* y, size_t n, hipStream_t s) {
+    hipLaunchKernelGGL(to_half_kernel, dim3(grid_1d(n)), dim3(256), 0, s, x,
+                       reinterpret_cast<f16*>(y), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_apply_gate(float* out, const float* gate, size_t n, hipStream_t s) {
+    hipLaunchKernelGGL(apply_gate_kernel, dim3(grid_1d(n)), dim3(256), 0, s, out, gate, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_softmax(float* x, int32_t n, hipStream_t s) {
     hipLaunchKernelGGL(softmax_row_kernel, dim3(1), dim3(1024), 0, s, x, n);
     return hipGetLastError();

@@ -159,6 +159,68 @@ class KvPool:
         return ko, vo
 
 
+class AttnLayer:
+    """LayerCache of one attention layer for one sequence, on the device
+    (src/model/mod.rs:73-106), with the forward step of src/model/mod.rs:1035-1196 on host
+    slices (numpy float32), as the reference's InferenceContext::forward hands them over."""
+
+    def __init__(self, dev: Device, max_tokens: int, n_heads: int, n_kv_heads: int,
+                 head_dim: int, kv_dtype: torch.dtype = torch.float16, q_norm_w=None,
+                 k_norm_w=None, eps: float = 1e-6, rope_dim: int = None,
+                 rope_base: float = 1e6, sections=None, gqa_mode: int = MODULO):
+        self.dev = dev
+        self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
+        qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, np.float32)
+        kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, np.float32)
+        sec = None if sections is None else (ctypes.c_int32 * 4)(*[int(x) for x in sections])
+        p = ctypes.c_void_p()
+        dev.check(dev.lib.pi_attn_layer_create(
+            dev.h, max_tokens, n_heads, n_kv_heads, head_dim, _DTYPE_CODE.get(kv_dtype, -1),
+            None if qn is None else qn.ctypes.data_as(ctypes.c_void_p),
+            None if kn is None else kn.ctypes.data_as(ctypes.c_void_p), float(eps),
+            head_dim if rope_dim is None else rope_dim, float(rope_base), sec, gqa_mode,
+            ctypes.byref(p)))
+        self.p = p
+
+    def close(self):
+        if self.p:
+            self.dev.lib.pi_attn_layer_destroy(self.p)
+            self.p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def seq_len(self) -> int:
+        return int(self.dev.lib.pi_attn_layer_seq_len(self.p))
+
+    def reset(self):
+        self.dev.lib.pi_attn_layer_reset(self.p)
+
+    def forward(self, q: np.ndarray, k: np.ndarray, v: np.ndarray, gate=None):
+        """q [n, Hq, D], k, v [n, Hkv, D] float32 (q, k normalised / rotated in place);
+        returns out [n, Hq, D]."""
+        n = q.shape[0]
+        for name, a, h in (("q", q, self.n_heads), ("k", k, self.n_kv_heads),
+                           ("v", v, self.n_kv_heads)):
+            if (not isinstance(a, np.ndarray) or a.dtype != np.float32 or
+                    not a.flags.c_contiguous or a.shape != (n, h, self.head_dim)):
+                raise InvalidArg(f"{name}: expected C-contiguous float32 [{n}, {h}, {self.head_dim}]")
+        g = None
+        if gate is not None:
+            g = np.ascontiguousarray(gate, np.float32)
+            if g.shape != q.shape:
+                raise InvalidArg(f"gate: shape {g.shape}")
+        out = np.empty_like(q)
+        vp = lambda a: None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+        self.dev.check(self.dev.lib.pi_attn_layer_forward(self.dev.h, self.p, vp(q), vp(k), vp(v),
+                                                          vp(g), n, vp(out)))
+        return out
+
+
 class TqPool:
     """TurboQuant compressed KV cache (CompressedKVCache, src/turboquant/mod.rs:408-566) in
     16-token pages: 64-byte 3-bit + QJL key records with f32 norms, f16 values; head_dim 128."""

@@ -1,0 +1,108 @@
+"""The device-resident LayerCache with forward's attention step (pi_attn_layer_*), fed host
+slices the way InferenceContext::forward holds them (src/model/mod.rs:668-1219), against the
+oracle's per-token restatement (or_attn_layer_tokens) of the same calls.
+
+A sequence is driven through a prompt, single decode tokens and a continued multi-token chunk
+(the three paths of the forward: causal prefill, one decode row, decode rows over the cached
+history).  Tolerances as for the other attention tests: max-abs <= 2e-3 with an f32 cache,
+per-row relative <= 1e-2 with an f16 cache; q and k come back normalised and rotated as in the
+reference (<= 1e-5).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.gpu_util import device, row_rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _drive(layer, chunks, oracle_kw, check, rng, hq, hkv, d, gate=False):
+    kc = vc = None
+    prev = 0
+    for n in chunks:
+        q = rng.standard_normal((n, hq, d)).astype(np.float32)
+        k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+        v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+        g = rng.standard_normal((n, hq, d)).astype(np.float32) if gate else None
+        ref, kc, vc = orc.attn_layer_tokens(q, k, v, gate=g, key_cache=kc, value_cache=vc,
+                                            prev_seq_len=prev, **oracle_kw)
+        qr, kr = orc.attn_prepare(q, k, hq, hkv, d, pos0=prev,
+                                  **{x: oracle_kw[x] for x in oracle_kw if x != "gate"})
+        qg, kg = q.copy(), k.copy()
+        out = layer.forward(qg, kg, v, gate=g)
+        check(out, ref, f"chunk of {n} at position {prev}")
+        assert np.abs(qg - qr).max() <= 1e-5 and np.abs(kg - kr).max() <= 1e-5
+        prev += n
+        assert layer.seq_len == prev
+
+
+def _rel(tol):
+    def check(out, ref, what):
+        for i in range(out.shape[0]):
+            err = row_rel_err(out[i], ref[i])
+            assert err <= tol, f"{what}: token {i} rel err {err}"
+    return check
+
+
+def _abs(tol):
+    def check(out, ref, what):
+        err = float(np.abs(out - ref).max())
+        assert err <= tol, f"{what}: max-abs {err}"
+    return check
+
+
+def test_layer_qwen3_gqa_f16_prompt_decode_continuation():
+    """32/8 heads, D 128, NORM RoPE theta 1e6, f16 cache: a 300-token prompt (causal
+    prefill), three decode tokens, then a 70-token chunk over the cached history."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    layer = rt.AttnLayer(dev, 512, 32, 8, 128, torch.float16, rope_base=1e6)
+    _drive(layer, [300, 1, 1, 1, 70], dict(rope_base=1e6), _rel(1e-2),
+           np.random.default_rng(0x1A1), 32, 8, 128)
+
+
+def test_layer_qwen35_gated_d256_norm_imrope():
+    """16/2 heads, D 256, per-head Q/K RMSNorm, IMRoPE (64 rotated dims, sections
+    [11, 11, 10, 0], base 1e7), sigmoid gate, f16 cache."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    rng = np.random.default_rng(0x1A2)
+    qn = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    sec = [11, 11, 10, 0]
+    freqs = orc.compute_imrope_freqs(1e7, 64, sec)
+    layer = rt.AttnLayer(dev, 256, 16, 2, 256, torch.float16, q_norm_w=qn, k_norm_w=kn,
+                         rope_dim=64, rope_base=1e7, sections=sec)
+    kw = dict(q_norm_w=qn, k_norm_w=kn, rope_dim=64, rope_base=1e7, freqs=freqs)
+    _drive(layer, [100, 1, 1, 20], kw, _rel(1e-2), rng, 16, 2, 256, gate=True)
+
+
+def test_layer_llama2_mha_f32_cache():
+    """32/32 heads, D 128, theta 1e4, f32 cache: max-abs <= 2e-3."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    layer = rt.AttnLayer(dev, 128, 32, 32, 128, torch.float32, rope_base=1e4)
+    _drive(layer, [64, 1, 1, 5], dict(rope_base=1e4), _abs(2e-3),
+           np.random.default_rng(0x1A3), 32, 32, 128)
+
+
+def test_layer_reset_and_full_cache():
+    """reset() restarts the sequence (the same prompt gives the same output); a forward that
+    would overflow the cache fails with OutOfMemory and leaves the sequence as it was."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    rng = np.random.default_rng(0x1A4)
+    layer = rt.AttnLayer(dev, 48, 4, 2, 128, torch.float16, rope_base=1e6)
+    q = rng.standard_normal((40, 4, 128)).astype(np.float32)
+    k = rng.standard_normal((40, 2, 128)).astype(np.float32)
+    v = rng.standard_normal((40, 2, 128)).astype(np.float32)
+    a = layer.forward(q.copy(), k.copy(), v)
+    with pytest.raises(rt.OutOfMemory):
+        layer.forward(q[:9].copy(), k[:9].copy(), v[:9])
+    assert layer.seq_len == 40
+    layer.reset()
+    assert layer.seq_len == 0
+    b = layer.forward(q.copy(), k.copy(), v)
+    assert np.array_equal(a, b)
