@@ -241,6 +241,28 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer layer, float* h_q, float* h
 void pi_attn_layer_reset(pi_attn_layer layer);
 int32_t pi_attn_layer_seq_len(pi_attn_layer layer);
 
+/* ---- Gated-DeltaNet layer state (the seam in InferenceContext::forward) ----------------
+ * One GDN layer of one sequence on the device: the rolling conv state ssm_conv_states[layer]
+ * (src/model/mod.rs:125-127) and the recurrent state ssm_states[layer] (:122-124), both zero,
+ * with the layer's conv1d weights [conv_dim][d_conv] (GGML layout, :765-769), ssm_a and
+ * dt_bias [n_v_heads], and the RMSNormGated weight [v_hd]; conv_dim = 2 n_k_heads k_hd +
+ * n_v_heads v_hd. */
+typedef struct pi_gdn_layer_s* pi_gdn_layer;
+int pi_gdn_layer_create(pi_handle h, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
+                        int32_t v_hd, int32_t d_conv, const float* h_conv_w, const float* h_ssm_a,
+                        const float* h_dt_bias, const float* h_norm_w, float eps,
+                        pi_gdn_layer* out);
+void pi_gdn_layer_destroy(pi_gdn_layer layer);
+/* src/model/mod.rs:750-932 for n_tokens consecutive tokens: conv1d + SiLU over the projected
+ * qkv rows [n_tokens][conv_dim], split into q, k, v, beta / g from beta_raw, a_raw
+ * [n_tokens][n_v_heads], the gated delta rule (chunked for n_tokens > 1), and
+ * RMSNormGated x SiLU(z) with z [n_tokens][n_v_heads][v_hd]; out like z.  Synchronous. */
+int pi_gdn_layer_forward(pi_handle h, pi_gdn_layer layer, const float* h_qkv, const float* h_z,
+                         const float* h_beta_raw, const float* h_a_raw, int32_t n_tokens,
+                         float* h_out);
+/* The GDN part of InferenceContext::reset (src/model/mod.rs:1867-1869): both states to zero. */
+int pi_gdn_layer_reset(pi_handle h, pi_gdn_layer layer);
+
 /* ---- TurboQuant compressed KV (src/turboquant/mod.rs:408-566) -------------------------
  * CompressedKVCache with head_dim 128: per KV head h a TurboQuant(3 bits, 128, 128 QJL bits,
  * seed 0xCAFEBABE + h) key quantizer (:430-437) and f16 values.  Keys are stored as 64-byte

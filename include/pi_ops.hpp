@@ -174,6 +174,56 @@ private:
     pi_attn_layer l_ = nullptr;
 };
 
+// One gated-DeltaNet layer of one sequence on the device: the rolling conv state and the
+// recurrent state (src/model/mod.rs:122-127), with the layer's GDN step (src/model/mod.rs:
+// 750-932) as the offload seam over host slices: qkv [n][conv_dim], z [n][n_v_heads][v_hd],
+// beta_raw, a_raw [n][n_v_heads]; out like z.
+class DeviceGdnLayer {
+public:
+    struct Config {
+        size_t n_k_heads = 0, n_v_heads = 0, k_hd = 128, v_hd = 128, d_conv = 4;
+        std::span<const float> conv_w;   // [conv_dim][d_conv]
+        std::span<const float> ssm_a, dt_bias;  // [n_v_heads]
+        std::span<const float> norm_w;   // [v_hd]
+        float eps = 1e-6f;
+    };
+    DeviceGdnLayer(const Device& dev, const Config& c) : dev_(&dev), c_(c) {
+        conv_dim_ = 2 * c.n_k_heads * c.k_hd + c.n_v_heads * c.v_hd;
+        if (c.conv_w.size() != conv_dim_ * c.d_conv || c.ssm_a.size() != c.n_v_heads ||
+            c.dt_bias.size() != c.n_v_heads || c.norm_w.size() != c.v_hd)
+            throw BackendError(PI_ERR_INVALID_ARG, "DeviceGdnLayer: weight sizes do not match");
+        dev.check(pi_gdn_layer_create(dev.raw(), (int32_t)c.n_k_heads, (int32_t)c.n_v_heads,
+                                      (int32_t)c.k_hd, (int32_t)c.v_hd, (int32_t)c.d_conv,
+                                      c.conv_w.data(), c.ssm_a.data(), c.dt_bias.data(),
+                                      c.norm_w.data(), c.eps, &l_));
+    }
+    DeviceGdnLayer(const DeviceGdnLayer&) = delete;
+    DeviceGdnLayer& operator=(const DeviceGdnLayer&) = delete;
+    ~DeviceGdnLayer() { pi_gdn_layer_destroy(l_); }
+
+    std::optional<Result> try_forward(std::span<const float> qkv, std::span<const float> z,
+                                      std::span<const float> beta_raw,
+                                      std::span<const float> a_raw, size_t n_tokens,
+                                      std::span<float> out) {
+        const size_t nz = n_tokens * c_.n_v_heads * c_.v_hd, nh = n_tokens * c_.n_v_heads;
+        if (qkv.size() != n_tokens * conv_dim_ || z.size() != nz || out.size() != nz ||
+            beta_raw.size() != nh || a_raw.size() != nh)
+            return Result{PI_ERR_INVALID_ARG, "gdn layer forward: slice sizes do not match the heads"};
+        return dev_->result(pi_gdn_layer_forward(dev_->raw(), l_, qkv.data(), z.data(),
+                                                 beta_raw.data(), a_raw.data(),
+                                                 (int32_t)n_tokens, out.data()));
+    }
+    // The GDN part of InferenceContext::reset (src/model/mod.rs:1867-1869)
+    void reset() { dev_->check(pi_gdn_layer_reset(dev_->raw(), l_)); }
+    size_t conv_dim() const { return conv_dim_; }
+
+private:
+    const Device* dev_;
+    Config c_;
+    size_t conv_dim_ = 0;
+    pi_gdn_layer l_ = nullptr;
+};
+
 // The calling thread's default device (device 0), opened on first use.
 inline Device& current() {
     thread_local std::optional<Device> dev = Device::init(0);

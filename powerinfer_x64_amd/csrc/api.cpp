@@ -53,6 +53,20 @@ struct pi_attn_layer_s {
     int32_t seq_len = 0;
 };
 
+struct pi_gdn_layer_s {
+    pi_handle owner;
+    int32_t hk = 0, hv = 0, dk = 0, dv = 0, d_conv = 0, conv_dim = 0;
+    float eps = 0.f;
+    float* d_w = nullptr;       // conv1d weights [conv_dim][d_conv]
+    float* d_ssm_a = nullptr;   // [hv]
+    float* d_dt = nullptr;      // [hv]
+    float* d_norm = nullptr;    // [dv]
+    float* d_conv_state = nullptr;  // [d_conv - 1][conv_dim]
+    float* d_state = nullptr;       // [hv][dk][dv]
+    float* d_buf = nullptr;         // staging
+    size_t buf_floats = 0;
+};
+
 struct pi_tq_pool_s {
     pi_handle owner;
     pi::TqPool t;
@@ -917,6 +931,119 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
     if ((rc = copy_sync(h, h_k, dk, nk * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
     PI_HIP(h, hipStreamSynchronize(s), "pi_attn_layer_forward");
     L->seq_len = prev + n_tokens;
+    return PI_OK;
+}
+
+// ---- gated-DeltaNet layer state -------------------------------------------------------
+
+int pi_gdn_layer_create(pi_handle h, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
+                        int32_t v_hd, int32_t d_conv, const float* h_conv_w, const float* h_ssm_a,
+                        const float* h_dt_bias, const float* h_norm_w, float eps,
+                        pi_gdn_layer* out) {
+    PI_CHECK_HANDLE(h);
+    if (!out || !h_conv_w || !h_ssm_a || !h_dt_bias || !h_norm_w)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_layer_create: null argument");
+    *out = nullptr;
+    int rc = gdn_shape_check(h, "pi_gdn_layer_create", n_k_heads, n_v_heads, k_hd, v_hd);
+    if (rc) return rc;
+    if (d_conv < 1 || d_conv > 8) return fail(h, PI_ERR_UNSUPPORTED, "pi_gdn_layer_create: d_conv %d", d_conv);
+    pi_gdn_layer L = new (std::nothrow) pi_gdn_layer_s();
+    if (!L) return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_gdn_layer_create: host allocation");
+    L->owner = h;
+    L->hk = n_k_heads;
+    L->hv = n_v_heads;
+    L->dk = k_hd;
+    L->dv = v_hd;
+    L->d_conv = d_conv;
+    L->conv_dim = 2 * n_k_heads * k_hd + n_v_heads * v_hd;
+    L->eps = eps;
+    const size_t wn = (size_t)L->conv_dim * d_conv, cs = (size_t)(d_conv - 1) * L->conv_dim;
+    const size_t sn = (size_t)n_v_heads * k_hd * v_hd;
+    hipError_t e = hipSetDevice(h->device);
+    auto alloc = [&](float** p, size_t n) {
+        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(p), std::max<size_t>(n, 1) * sizeof(float));
+    };
+    alloc(&L->d_w, wn);
+    alloc(&L->d_ssm_a, n_v_heads);
+    alloc(&L->d_dt, n_v_heads);
+    alloc(&L->d_norm, v_hd);
+    alloc(&L->d_conv_state, cs);
+    alloc(&L->d_state, sn);
+    if (e == hipSuccess) e = hipMemcpy(L->d_w, h_conv_w, wn * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(L->d_ssm_a, h_ssm_a, n_v_heads * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(L->d_dt, h_dt_bias, n_v_heads * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(L->d_norm, h_norm_w, v_hd * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess && cs) e = hipMemset(L->d_conv_state, 0, cs * 4);
+    if (e == hipSuccess) e = hipMemset(L->d_state, 0, sn * 4);
+    if (e != hipSuccess) {
+        rc = hip_fail(h, e, "pi_gdn_layer_create");
+        pi_gdn_layer_destroy(L);
+        return rc;
+    }
+    *out = L;
+    return PI_OK;
+}
+
+void pi_gdn_layer_destroy(pi_gdn_layer L) {
+    if (!L) return;
+    (void)hipSetDevice(L->owner->device);
+    (void)hipDeviceSynchronize();
+    for (float* p : {L->d_w, L->d_ssm_a, L->d_dt, L->d_norm, L->d_conv_state, L->d_state, L->d_buf})
+        (void)hipFree(p);
+    delete L;
+}
+
+int pi_gdn_layer_reset(pi_handle h, pi_gdn_layer L) {
+    PI_CHECK_HANDLE(h);
+    if (!L) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_layer_reset: null layer");
+    PI_HIP(h, hipSetDevice(h->device), "pi_gdn_layer_reset");
+    PI_HIP(h, hipStreamSynchronize(h->stream), "pi_gdn_layer_reset");
+    const size_t cs = (size_t)(L->d_conv - 1) * L->conv_dim;
+    if (cs) PI_HIP(h, hipMemset(L->d_conv_state, 0, cs * 4), "pi_gdn_layer_reset");
+    PI_HIP(h, hipMemset(L->d_state, 0, (size_t)L->hv * L->dk * L->dv * 4), "pi_gdn_layer_reset");
+    return PI_OK;
+}
+
+int pi_gdn_layer_forward(pi_handle h, pi_gdn_layer L, const float* h_qkv, const float* h_z,
+                         const float* h_beta_raw, const float* h_a_raw, int32_t n_tokens,
+                         float* h_out) {
+    PI_CHECK_HANDLE(h);
+    if (!L || !h_qkv || !h_z || !h_beta_raw || !h_a_raw || !h_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_layer_forward: null argument");
+    if (n_tokens < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_layer_forward: n_tokens=%d", n_tokens);
+    if (n_tokens == 0) return PI_OK;
+    hipStream_t s = h->stream;
+    void* sv = reinterpret_cast<void*>(s);
+    PI_HIP(h, hipSetDevice(h->device), "pi_gdn_layer_forward");
+    const size_t n = (size_t)n_tokens, C = L->conv_dim, kd = (size_t)L->hk * L->dk;
+    const size_t vd = (size_t)L->hv * L->dv, nh = (size_t)L->hv;
+    // qkv, activation, q, k, v, z, beta_raw, a_raw, beta, g, out
+    const size_t need = 2 * n * C + 2 * n * kd + 3 * n * vd + 4 * n * nh;
+    int rc = grow(h, &L->d_buf, &L->buf_floats, need, s, "pi_gdn_layer_forward staging", false);
+    if (rc) return rc;
+    float *dx = L->d_buf, *act = dx + n * C, *dq = act + n * C, *dk = dq + n * kd, *dv = dk + n * kd;
+    float *dz = dv + n * vd, *dbr = dz + n * vd, *dar = dbr + n * nh, *db = dar + n * nh;
+    float *dg = db + n * nh, *dout = dg + n * nh;
+    if ((rc = copy_sync(h, dx, h_qkv, n * C * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+    if ((rc = copy_sync(h, dz, h_z, n * vd * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+    if ((rc = copy_sync(h, dbr, h_beta_raw, n * nh * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+    if ((rc = copy_sync(h, dar, h_a_raw, n * nh * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+    // conv1d + SiLU with the rolling state (:750-776), then the q / k / v split (:779-781)
+    if ((rc = pi_gdn_conv1d(h, dx, L->d_conv_state, L->d_w, act, 1, n_tokens, (int32_t)C, L->d_conv, sv)))
+        return rc;
+    PI_HIP(h, hipMemcpy2DAsync(dq, kd * 4, act, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "pi_gdn_layer_forward");
+    PI_HIP(h, hipMemcpy2DAsync(dk, kd * 4, act + kd, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "pi_gdn_layer_forward");
+    PI_HIP(h, hipMemcpy2DAsync(dv, vd * 4, act + 2 * kd, C * 4, vd * 4, n, hipMemcpyDeviceToDevice, s), "pi_gdn_layer_forward");
+    if ((rc = pi_gdn_gates(h, dbr, dar, L->d_ssm_a, L->d_dt, db, dg, n_tokens, L->hv, sv))) return rc;
+    if (n_tokens > 1)
+        rc = pi_gdn_prefill(h, dq, dk, dv, db, dg, L->d_state, dout, n_tokens, L->hk, L->hv, L->dk,
+                            L->dv, 64, sv);
+    else
+        rc = pi_gdn_decode(h, dq, dk, dv, db, dg, L->d_state, dout, 1, L->hk, L->hv, L->dk, L->dv, sv);
+    if (rc) return rc;
+    if ((rc = pi_gdn_rmsnorm_gated(h, dout, dz, L->d_norm, n_tokens, L->hv, L->dv, L->eps, sv))) return rc;
+    if ((rc = copy_sync(h, h_out, dout, n * vd * 4, hipMemcpyDeviceToHost, "pi_gdn_layer_forward"))) return rc;
+    PI_HIP(h, hipStreamSynchronize(s), "pi_gdn_layer_forward");
     return PI_OK;
 }
 

@@ -221,6 +221,61 @@ class AttnLayer:
         return out
 
 
+class GdnLayer:
+    """Gated-DeltaNet layer of one sequence, on the device: the rolling conv state and the
+    recurrent state (src/model/mod.rs:122-127), with the step of src/model/mod.rs:750-932 on
+    host slices (numpy float32): conv1d + SiLU, q / k / v split, gates, the delta rule and
+    RMSNormGated."""
+
+    def __init__(self, dev: Device, n_k_heads: int, n_v_heads: int, k_hd: int, v_hd: int,
+                 conv_w, ssm_a, dt_bias, norm_w, eps: float = 1e-6):
+        self.dev = dev
+        self.hk, self.hv, self.dk, self.dv = n_k_heads, n_v_heads, k_hd, v_hd
+        self.conv_dim = 2 * n_k_heads * k_hd + n_v_heads * v_hd
+        w = np.ascontiguousarray(conv_w, np.float32)
+        if w.ndim != 2 or w.shape[0] != self.conv_dim:
+            raise InvalidArg(f"conv_w: expected [{self.conv_dim}, d_conv], got {w.shape}")
+        arrs = [np.ascontiguousarray(a, np.float32).reshape(-1) for a in (ssm_a, dt_bias, norm_w)]
+        for name, a, m in zip(("ssm_a", "dt_bias", "norm_w"), arrs, (n_v_heads, n_v_heads, v_hd)):
+            if a.size != m:
+                raise InvalidArg(f"{name}: expected {m} values, got {a.size}")
+        vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+        p = ctypes.c_void_p()
+        dev.check(dev.lib.pi_gdn_layer_create(dev.h, n_k_heads, n_v_heads, k_hd, v_hd,
+                                              w.shape[1], vp(w), vp(arrs[0]), vp(arrs[1]),
+                                              vp(arrs[2]), float(eps), ctypes.byref(p)))
+        self.p = p
+
+    def close(self):
+        if self.p:
+            self.dev.lib.pi_gdn_layer_destroy(self.p)
+            self.p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        self.dev.check(self.dev.lib.pi_gdn_layer_reset(self.dev.h, self.p))
+
+    def forward(self, qkv: np.ndarray, z: np.ndarray, beta_raw: np.ndarray, a_raw: np.ndarray):
+        """qkv [n, conv_dim], z [n, Hv, Dv], beta_raw, a_raw [n, Hv] float32; returns the
+        gated, normalised output [n, Hv, Dv]."""
+        n = qkv.shape[0]
+        for name, a, shp in (("qkv", qkv, (n, self.conv_dim)), ("z", z, (n, self.hv, self.dv)),
+                             ("beta_raw", beta_raw, (n, self.hv)), ("a_raw", a_raw, (n, self.hv))):
+            if (not isinstance(a, np.ndarray) or a.dtype != np.float32 or
+                    not a.flags.c_contiguous or a.shape != shp):
+                raise InvalidArg(f"{name}: expected C-contiguous float32 {list(shp)}")
+        out = np.empty((n, self.hv, self.dv), np.float32)
+        vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+        self.dev.check(self.dev.lib.pi_gdn_layer_forward(self.dev.h, self.p, vp(qkv), vp(z),
+                                                         vp(beta_raw), vp(a_raw), n, vp(out)))
+        return out
+
+
 class TqPool:
     """TurboQuant compressed KV cache (CompressedKVCache, src/turboquant/mod.rs:408-566) in
     16-token pages: 64-byte 3-bit + QJL key records with f32 norms, f16 values; head_dim 128."""

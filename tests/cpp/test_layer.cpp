@@ -3,7 +3,8 @@
 // (src/model/mod.rs:668-1219): a prompt in one call must give the same outputs as the same
 // tokens fed one forward call at a time (the reference's own per-token loop), the try_* seam
 // reports errors as Some(Err) without changing the cache, and reset() restarts the sequence
-// (src/model/mod.rs:1854-1856).
+// (src/model/mod.rs:1854-1856).  The same for a gated-DeltaNet layer (DeviceGdnLayer over
+// pi_gdn_layer_*, src/model/mod.rs:750-932): a chunked prompt against its own token loop.
 //
 // Exit status: 0 all passed, 1 a test failed, 2 no usable device.
 #include "pi_ops.hpp"
@@ -14,6 +15,7 @@
 #include <vector>
 
 using powerinfer::rocm::Device;
+using powerinfer::rocm::DeviceGdnLayer;
 using powerinfer::rocm::DeviceLayerCache;
 
 static int g_failed = 0;
@@ -111,6 +113,45 @@ static void test_errors_and_reset(const Device& dev) {
     CHECK(qc == qa && kc == ka);  // the same rotated q / k
 }
 
+static void test_gdn_prompt_equals_token_loop(const Device& dev) {
+    const size_t HK = 2, HV = 4, D = 128, N = 130, DC = 4;
+    const size_t C = 2 * HK * D + HV * D;
+    std::mt19937 g(13);
+    auto w = randn(C * DC, g);
+    for (float& x : w) x *= 0.5f;
+    std::vector<float> a(HV), dt = randn(HV, g), nw(D);
+    for (size_t i = 0; i < HV; ++i) a[i] = -0.5f - 0.4f * (float)i;
+    for (size_t i = 0; i < D; ++i) nw[i] = 0.5f + (float)i / D;
+    DeviceGdnLayer::Config c;
+    c.n_k_heads = HK;
+    c.n_v_heads = HV;
+    c.d_conv = DC;
+    c.conv_w = w;
+    c.ssm_a = a;
+    c.dt_bias = dt;
+    c.norm_w = nw;
+    DeviceGdnLayer whole(dev, c), loop(dev, c);
+    CHECK(whole.conv_dim() == C);
+    auto qkv = randn(N * C, g), z = randn(N * HV * D, g), br = randn(N * HV, g), ar = randn(N * HV, g);
+    std::vector<float> out_whole(N * HV * D), out_loop(N * HV * D), again(N * HV * D);
+    CHECK(whole.try_forward(qkv, z, br, ar, N, out_whole)->ok());
+    for (size_t t = 0; t < N; ++t) {
+        std::span<const float> xs(qkv.data() + t * C, C), zs(z.data() + t * HV * D, HV * D);
+        std::span<const float> bs(br.data() + t * HV, HV), as(ar.data() + t * HV, HV);
+        auto r = loop.try_forward(xs, zs, bs, as, 1, std::span<float>(out_loop.data() + t * HV * D, HV * D));
+        CHECK(r && r->ok());
+    }
+    // per (token, V head) row: RMSNormGated rescales each row by 1 / rms, so compare rows
+    const double err = max_row_rel(out_whole, out_loop, D);
+    std::printf("    gdn prompt vs token loop: max row rel err %.3e\n", err);
+    CHECK(err <= 1e-2);
+    auto r = whole.try_forward(qkv, z, br, ar, N, std::span<float>(again.data(), 7));
+    CHECK(r && r->status == PI_ERR_INVALID_ARG);
+    whole.reset();
+    CHECK(whole.try_forward(qkv, z, br, ar, N, again)->ok());
+    CHECK(again == out_whole);
+}
+
 int main() {
     auto dev = Device::init(0);
     if (!dev) {
@@ -121,7 +162,8 @@ int main() {
         const char* name;
         void (*fn)(const Device&);
     } tests[] = {{"prompt_equals_token_loop", test_prompt_equals_token_loop},
-                 {"errors_and_reset", test_errors_and_reset}};
+                 {"errors_and_reset", test_errors_and_reset},
+                 {"gdn_prompt_equals_token_loop", test_gdn_prompt_equals_token_loop}};
     for (const T& t : tests) {
         const int before = g_failed;
         try {

@@ -22,10 +22,11 @@ def test_reference_op_tests_on_gpu():
 
 
 def test_device_layer_cache_cpp():
-    """DeviceLayerCache (the forward seam in C++): prompt == token loop, errors, reset."""
+    """DeviceLayerCache and DeviceGdnLayer (the forward seam in C++): prompt == token loop,
+    errors, reset."""
     exe = os.path.join(ROOT, "tests", "cpp", "_build", "test_layer")
     assert os.path.exists(exe), "tests/cpp not built (python -m powerinfer_x64_amd.build)"
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert r.stdout.count("PASS") == 2
+    assert r.stdout.count("PASS") == 3
