@@ -12,6 +12,14 @@
 // with the softmax in f32 on S^T, where a lane owns one query column, so the
 // row max / sum need one cross-lane step.  Tiles past the diagonal are
 // skipped; workgroups are launched heaviest-first.
+//
+// gfx950 facts the schedule is built on (measured with in-kernel timers):
+// within one wavefront an MFMA followed by v_exp serialises, while the MFMAs
+// of one wavefront and the VALU work of another on the same SIMD overlap; a
+// v_dot2 queues behind the other wavefront's MFMAs; LDS serves one wave64
+// read per ~4 clocks (256 B/clk for 16-byte reads).  So each wavefront
+// alternates a pure MFMA phase and a pure VALU (softmax) phase, and the two
+// wavefronts of a SIMD run in opposite phases.
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -32,19 +40,6 @@ struct Mfma<bf16> {
     static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
-    // sum of the 8 packed values (f32 accumulation, v_dot2 against ones)
-    static __device__ __forceinline__ float sum8(v8 p) {
-        typedef bf16 v2 __attribute__((ext_vector_type(2)));
-        const v2 one = {(bf16)1.0f, (bf16)1.0f};
-        const float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 0, 1), one,
-                                                        0.f, false);
-        const float b = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 4, 5), one,
-                                                        0.f, false);
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 6, 7), one,
-                                               __builtin_amdgcn_fdot2_f32_bf16(
-                                                   __builtin_shufflevector(p, p, 2, 3), one, a, false),
-                                               false) + b;
-    }
 };
 template <>
 struct Mfma<f16> {
@@ -52,16 +47,6 @@ struct Mfma<f16> {
     typedef f16x4 v4;
     static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ float sum8(v8 p) {
-        typedef f16 v2 __attribute__((ext_vector_type(2)));
-        const v2 one = {(f16)1.0f, (f16)1.0f};
-        const float a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 0, 1), one, 0.f, false);
-        const float b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 4, 5), one, 0.f, false);
-        return __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 6, 7), one,
-                                      __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 2, 3),
-                                                             one, a, false),
-                                      false) + b;
     }
 };
 
@@ -85,13 +70,15 @@ __device__ __forceinline__ int head_of(int kvh, int c, int hkv, int group, int m
 // a workgroup covers HPW heads x 256/HPW rows and every K/V byte it stages in
 // LDS serves 8 wavefronts.
 //
-// K and V tiles (64 keys x D) are staged through registers into four LDS
-// buffers (one barrier per tile): K in its [key][dim] order with 272-byte
-// rows, V transposed to V^T [dim][key] with 136-byte rows, both bank-conflict
-// free for the fragment reads, whose addresses are one base register plus an
-// immediate.  K and V^T fragments are read PF ahead of their MFMAs.
-// Only a wavefront's last tile can need the causal / prompt-end mask; the
-// mask is one wave-uniform branch around a straight-line select block.
+// A "unit" u holds K of tile u and V of tile u - 1 in one of four LDS
+// buffers; it arrives by direct global -> LDS loads (no registers, no LDS
+// stores): K in [key][dim] order with 272-byte rows, V in [key][dim] order
+// with 256-byte rows whose 16-byte chunks are XOR-swizzled by row.  K
+// fragments are 16-byte reads; V^T fragments come from two transposing reads
+// (ds_read_b64_tr_b16).  All fragment reads are conflict-free and run PF
+// ahead of their MFMAs.  Only a wavefront's last tile can need the causal /
+// prompt-end mask; the mask is one wave-uniform branch around a straight-line
+// select block.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float max16(const f32x16& s) {
     const float a = fmaxf(fmaxf(s[0], s[1]), s[2]);
@@ -106,14 +93,18 @@ template <typename T, int HPW>
 __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
     typedef typename Mfma<T>::v8 v8;
     typedef typename Mfma<T>::v4 v4;
+    typedef short s4 __attribute__((ext_vector_type(4)));
     constexpr int NW = 8;
     constexpr int RT = NW / HPW;      // row tiles per workgroup
     constexpr int WROWS = ROWS * RT;  // query rows per workgroup
-    constexpr int NBUF = 4;
-    constexpr int KS = D + 8;   // K [key][dim] row stride (elements): 272 B
-    constexpr int VT = BN + 4;  // V^T [dim][key] row stride (elements): 136 B
-    __shared__ __attribute__((aligned(16))) T sk[NBUF][BN * KS];
-    __shared__ __attribute__((aligned(16))) T sv[NBUF][D * VT];
+    constexpr int NB = 4;             // unit buffers
+    constexpr int KS = D + 8;         // K [key][dim] row stride (elements): 272 B, 17 chunks
+    constexpr int KCH = KS / 8;       // 16-byte chunks per K row
+    constexpr int K_INSTR = BN * KCH / 64;  // 17 direct loads of 1 KB per K tile
+    // buffer u % NB holds K of tile u ([key][dim], padded rows) and V of tile
+    // u - 1 ([key][dim], 256-byte rows, chunk c of row r at c ^ 4*(r % 4))
+    __shared__ __attribute__((aligned(1024))) T sk[NB][BN * KS];
+    __shared__ __attribute__((aligned(1024))) T sv[NB][BN * D];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -153,102 +144,169 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
     f32x16 o[D / 32];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) o[i] = f32x16{};
-    float m_run = -1e30f, l_run = 0.f;  // running max (scaled log2 units), lane partial sum
+    float m_run = -1e30f, l_run = 0.f;
 
     const size_t tok_stride = (size_t)a.hkv * D;
     const T* kbase = reinterpret_cast<const T*>(a.k) + ((size_t)b * S * a.hkv + kvh) * D;
     const T* vbase = reinterpret_cast<const T*>(a.v) + ((size_t)b * S * a.hkv + kvh) * D;
 
-    // Tile t (64 keys) is staged through registers: thread i loads two
-    // 16-byte K chunks (rows (i + 512j) / 16) and, for key pair i % 32, the
-    // 8 dims 8*(i/32) .. +7 of both keys of V, which it writes transposed as
-    // V^T.  Rows past the prompt read as zeros (their scores are masked).
-    v8 kreg[2], vreg[2];
-    const int kp = tid & 31, vdc = tid >> 5;
-    auto load_tile = [&](int t) {
-        const int k0 = t * BN;
+    // Direct global -> LDS loads (16 bytes per lane, lane i lands at base +
+    // 16 i).  K: load i of a tile covers chunks 64 i .. 64 i + 63 of the padded
+    // tile (row = chunk / 17; chunk 16 of a row is padding and reloads chunk
+    // 0).  V: load i covers rows 4 i .. 4 i + 3.  Rows past the prompt reload
+    // row S-1 (finite values; their scores are masked to -inf, P = 0).
+    typedef __attribute__((address_space(3))) void lds_void;
+    // The load is issued from inline assembly so that the compiler does not
+    // add vmcnt waits before LDS reads (it cannot tell the buffers apart);
+    // the kernel waits for each unit explicitly before the barrier that
+    // publishes it.
+    auto dma16 = [](const void* src, lds_void* dst) {
+        const unsigned m0 = (unsigned)(uintptr_t)dst;
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                     :: "v"(src), "s"(m0) : "memory", "m0");
+    };
+    // scalar base + 32-bit lane byte offset form, for the common full tile
+    auto dma16s = [](const void* base, unsigned voff, lds_void* dst) {
+        const unsigned m0 = (unsigned)(uintptr_t)dst;
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                     :: "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
+    };
+    // this lane's row and byte offset (within a tile) for each of its loads
+    int k_row[3], v_row[2];
+    unsigned k_off[3], v_off[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int id = tid + 512 * i;
-            const int row = id >> 4, ch = id & 15;
-            v8 x = v8{};
-            if (k0 + row < S) x = *reinterpret_cast<const v8*>(kbase + (size_t)(k0 + row) * tok_stride + 8 * ch);
-            kreg[i] = x;
+    for (int j = 0; j < 3; ++j) {
+        const int i = wave + NW * j;
+        const int L = 64 * (i < K_INSTR ? i : 0) + lane;
+        const int row = L / KCH, ch = L - row * KCH;
+        k_row[j] = row;
+        k_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * (ch < 16 ? ch : 0)) * sizeof(T));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = 2 * wave + j;
+        const int row = 4 * i + (lane >> 4);
+        const int cc = (lane & 15) ^ (4 * (row & 3));
+        v_row[j] = row;
+        v_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * cc) * sizeof(T));
+    }
+    auto issue_unit = [&](int u) {
+        const int buf = u % NB;
+        const int k0 = u * BN;
+        if (k0 + BN <= S) {
+            const T* kb = kbase + (size_t)k0 * tok_stride;
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int i = wave + NW * j;
+                if (i < K_INSTR) dma16s(kb, k_off[j], (lds_void*)&sk[buf][512 * i]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int i = wave + NW * j;
+                if (i < K_INSTR) {
+                    const int key = min(k0 + k_row[j], S - 1);
+                    const T* src = kbase + (size_t)key * tok_stride +
+                                   (k_off[j] - (size_t)k_row[j] * tok_stride * sizeof(T)) / sizeof(T);
+                    dma16(src, (lds_void*)&sk[buf][512 * i]);
+                }
+            }
         }
+        if (u >= 1) {
+            const int v0 = k0 - BN;
+            const T* vb = vbase + (size_t)v0 * tok_stride;
+            if (v0 + BN <= S) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int key = k0 + 2 * kp + i;
-            v8 x = v8{};
-            if (key < S) x = *reinterpret_cast<const v8*>(vbase + (size_t)key * tok_stride + 8 * vdc);
-            vreg[i] = x;
+                for (int j = 0; j < 2; ++j) dma16s(vb, v_off[j], (lds_void*)&sv[buf][512 * (2 * wave + j)]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int key = min(v0 + v_row[j], S - 1);
+                    const T* src = vbase + (size_t)key * tok_stride +
+                                   (v_off[j] - (size_t)v_row[j] * tok_stride * sizeof(T)) / sizeof(T);
+                    dma16(src, (lds_void*)&sv[buf][512 * (2 * wave + j)]);
+                }
+            }
         }
     };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int id = tid + 512 * i;
-            const int row = id >> 4, ch = id & 15;
-            *reinterpret_cast<v8*>(&sk[buf][row * KS + 8 * ch]) = kreg[i];
-        }
-        typedef T v2 __attribute__((ext_vector_type(2)));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const v2 x = {vreg[0][e], vreg[1][e]};
-            *reinterpret_cast<v2*>(&sv[buf][(8 * vdc + e) * VT + 2 * kp]) = x;
-        }
+    // barrier without the compiler's fence: LDS visibility is handled by the
+    // explicit waits; the empty asm keeps memory accesses on their side
+    auto barrier = [&]() {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
 
     const float c = a.qk_scale;
-    // Per-lane LDS bases in buffer 0: every fragment of a tile is base +
-    // buffer offset + an immediate offset.
     typedef __attribute__((address_space(3))) const T* lds_ptr;
+    typedef __attribute__((address_space(3))) const v8* lds_v8;
+    typedef __attribute__((address_space(3))) s4* lds_s4;
     const lds_ptr k_lane = (lds_ptr)&sk[0][r * KS + 8 * hh];
-    const lds_ptr v_lane = (lds_ptr)&sv[0][r * VT + 4 * hh];
     auto kfrag = [&](lds_ptr kt, int i) {  // i = 2*kk + tt
-        return *reinterpret_cast<__attribute__((address_space(3))) const v8*>(kt + (i & 1) * 32 * KS + (i >> 1) * 16);
+        return *reinterpret_cast<lds_v8>(kt + (i & 1) * 32 * KS + (i >> 1) * 16);
     };
-    // V^T operand: dims 32*dt + r, keys 16*ks + 4*hh + (0..3) and +8 -- the
-    // key order of the P^T operand.
-    auto vfrag = [&](lds_ptr vt, int i) {  // i = 4*ks + dt
-        const lds_ptr p1 = vt + (i & 3) * 32 * VT + (i >> 2) * 16;
-        const v4 lo = *reinterpret_cast<__attribute__((address_space(3))) const v4*>(p1);
-        const v4 hi = *reinterpret_cast<__attribute__((address_space(3))) const v4*>(p1 + 8);
-        return v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    // V^T operand by two transposing reads: in each 16-lane group, lane j
+    // points at key row kb + j/4, dims db + 4 (j % 4) .. +3; lane i then holds
+    // keys kb .. kb+3 of dim db + i.  Lane offsets (elements) per dim tile dt:
+    const int jg = lane & 15, grp = lane >> 4;
+    const int vrow = 4 * hh + (jg >> 2);
+    const int vq = 2 * (grp & 1) + ((jg & 3) >> 1);
+    int voff[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+        voff[dt] = vrow * D + 32 * (dt ^ ((jg >> 2) & 3)) + 8 * vq + 4 * (jg & 1);
+    auto vfrag = [&](int buf, int i) {  // i = 4*ks + dt: keys 16 ks + {4hh..+3, 8+4hh..+3}
+        const int dt = i & 3, ks = i >> 2;
+        const lds_ptr base = (lds_ptr)&sv[buf][0] + voff[dt] + (16 * ks) * D;
+        const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)base);
+        const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(base + 8 * D));
+        const v4 l4 = __builtin_bit_cast(v4, lo), h4 = __builtin_bit_cast(v4, hi);
+        return v8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
     };
-    constexpr int PF = 4;  // fragments in flight
+    constexpr int PF = 4;
 
-    // S^T = K . Q^T for tile t: two 32x32 tiles (keys 0-31, 32-63),
-    // interleaved so consecutive MFMAs are independent; K fragments read PF
-    // ahead
-    auto tile_qk = [&](int t, f32x16* s) {
-        const lds_ptr kt = k_lane + (t % NBUF) * (BN * KS);
+    f32x16 s[2];
+    v8 pb[4];  // P^T operand of the tile whose PV is pending
+    auto run_pv = [&](int buf) {
+        v8 vf[PF];
+#pragma unroll
+        for (int i = 0; i < PF; ++i) vf[i] = vfrag(buf, i);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const v8 va = vf[i % PF];
+            if (i + PF < 16) vf[i % PF] = vfrag(buf, i + PF);
+            o[i & 3] = Mfma<T>::mma(va, pb[i >> 2], o[i & 3]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
+#pragma unroll
+        for (int i = 0; i < 16 - PF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+    };
+    auto run_qk = [&](int buf) {
+        const lds_ptr kt = k_lane + buf * (BN * KS);
         s[0] = f32x16{};
         s[1] = f32x16{};
-        {
-            v8 kf[PF];
+        v8 kf[PF];
 #pragma unroll
-            for (int i = 0; i < PF; ++i) kf[i] = kfrag(kt, i);
+        for (int i = 0; i < PF; ++i) kf[i] = kfrag(kt, i);
 #pragma unroll
-            for (int i = 0; i < 2 * (D / 16); ++i) {
-                const v8 ka = kf[i % PF];
-                if (i + PF < 2 * (D / 16)) kf[i % PF] = kfrag(kt, i + PF);
-                s[i & 1] = Mfma<T>::mma(ka, qr[i >> 1], s[i & 1]);
-            }
-            // keep PF fragment reads in flight ahead of the MFMAs
-            __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
-#pragma unroll
-            for (int i = 0; i < 2 * (D / 16) - PF; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+        for (int i = 0; i < 16; ++i) {
+            const v8 ka = kf[i % PF];
+            if (i + PF < 16) kf[i % PF] = kfrag(kt, i + PF);
+            s[i & 1] = Mfma<T>::mma(ka, qr[i >> 1], s[i & 1]);
         }
+        __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+        for (int i = 0; i < 16 - PF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
     };
-    // The rest of tile t on its scores s: mask, running max, P = exp2, and
-    // O^T += V^T . P^T.  Lane holds keys k0 + 32*tt + 8*i + 4*hh + j of query
-    // qpos.
-    auto tile_rest = [&](int t, f32x16* s, bool masked) {
-        const lds_ptr vt = v_lane + (t % NBUF) * (D * VT);
+    auto phase_softmax = [&](int t, bool masked) {
         const int k0 = t * BN;
         if (masked) {
 #pragma unroll
@@ -269,16 +327,10 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
             for (int i = 0; i < D / 32; ++i) o[i] *= alpha;
             m_run = m_new;
         }
-        // O^T += V^T . P^T : 4 key steps of 16 x 4 dim tiles of 32; the exps of
-        // key step ks+1 overlap the MFMAs of key step ks
-        v8 vf[PF];
-#pragma unroll
-        for (int i = 0; i < PF; ++i) vf[i] = vfrag(vt, i);
         float ls[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int tt = ks >> 1, i0 = 2 * (ks & 1);
-            v8 pb;
             float p[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -286,46 +338,83 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
                 p[4 + j] = fast_exp2(__builtin_fmaf(s[tt][4 * (i0 + 1) + j], c, -m_run));
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) pb[j] = (T)p[j];
-            // row sum of the rounded P that the PV product uses
-            ls[ks] = Mfma<T>::sum8(pb);
-#pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const int i = 4 * ks + dt;
-                const v8 va = vf[i % PF];
-                if (i + PF < 16) vf[i % PF] = vfrag(vt, i + PF);
-                o[dt] = Mfma<T>::mma(va, pb, o[dt]);
-            }
+            for (int j = 0; j < 8; ++j) pb[ks][j] = (T)p[j];
+            ls[ks] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
         }
         l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
 
-    load_tile(0);
-    store_tile(0);
-    if (n_tiles > 1) {
-        load_tile(1);
-        store_tile(1);
-    }
-    __syncthreads();
-    // Two wave groups in opposite phases.  Between two barriers, waves 0-3
-    // run QK of tile t and then the softmax + PV of tile t; waves 4-7 run the
-    // softmax + PV of tile t-1 (scores kept in registers across the barrier)
-    // and then QK of tile t.  Each SIMD holds one wave of each group, so one
-    // wave's MFMAs overlap the other's softmax.  Tile t lives in buffer
-    // t % 4; the store of tile t+2 goes to the buffer of tile t-2, last read
-    // (V by waves 4-7) before the previous barrier.
-    // The loop runs one step past the last tile for the lagging group.
-    f32x16 s[2];
-    const bool lag = wave >= NW / 2;
-    for (int t = 0; t <= n_tiles; ++t) {
-        const bool pre = t + 2 < n_tiles;
-        if (pre) load_tile(t + 2);  // in flight while tile t computes
-        if (!lag && t < w_tiles) tile_qk(t, s);
-        const int tr = lag ? t - 1 : t;  // tile whose softmax + PV runs now
-        if (tr >= 0 && tr < w_tiles) tile_rest(tr, s, tr == w_tiles - 1 && last_masked);
-        if (lag && t < w_tiles) tile_qk(t, s);
-        if (pre) store_tile((t + 2) % NBUF);
-        if (t < n_tiles) __syncthreads();
+    // Slots k = 0 .. 2*n_tiles+1, a barrier after each but the last.  Lead
+    // group (waves 0-3): slot 2t = MFMA phase of tile t (PV of tile t-1, QK
+    // of tile t, from unit t), slot 2t+1 = VALU phase of tile t; the lag group
+    // (waves 4-7) runs each one slot later, so each SIMD has one wave in each
+    // phase.  Each wave issues its loads of a unit in a VALU phase (4 waves
+    // per slot): unit u >= 4 in slot 2u-5 (lead) and 2u-6 (lag), after the
+    // last read of unit u-4 (slot 2u-7) in the same buffer; each wave waits
+    // for its part of unit u before the barrier that ends slot 2u-1, when its
+    // loads of units u+1 and u+2 may still be in flight.
+    issue_unit(0);
+    if (n_tiles >= 1) issue_unit(1);
+    __builtin_amdgcn_s_waitcnt(0);  // all counters (Q loads, units 0 and 1)
+    barrier();
+    const int nl = (wave == 0 ? 3 : 2) + 2;  // this wave's loads per unit (K + V)
+    // Wait until this wave's loads of unit u are complete while its loads of
+    // the next `ahead` units (0, 1 or 2) may still be in flight.
+    // vmcnt(n) on gfx9: bits 3:0 and 15:14; expcnt 6:4 = 7; lgkmcnt 11:8 = 15
+    auto wait_unit = [&](int ahead) {
+        if (ahead == 2) {
+            if (nl == 5) __builtin_amdgcn_s_waitcnt(0x0F7A);
+            else __builtin_amdgcn_s_waitcnt(0x0F78);
+        } else if (ahead == 1) {
+            if (nl == 5) __builtin_amdgcn_s_waitcnt(0x0F75);
+            else __builtin_amdgcn_s_waitcnt(0x0F74);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
+    };
+    auto ahead_of = [&](int u) { return min(2, max(0, n_tiles - u)); };
+    // The MFMA phase runs at a raised wave priority so that its MFMA and LDS
+    // issues win over the other wave's softmax VALU stream on the same SIMD.
+    auto mfma_phase = [&](int t) {
+        const bool pv = t >= 1 && t - 1 < w_tiles;
+        const bool qk = t < w_tiles;
+        __builtin_amdgcn_s_setprio(2);
+        if (pv) run_pv(t % NB);
+        if (qk) run_qk(t % NB);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    if (wave < NW / 2) {
+        if (2 <= n_tiles) issue_unit(2);
+        for (int t = 0; t <= n_tiles; ++t) {
+            // slot 2t: MFMA phase of tile t
+            mfma_phase(t);
+            barrier();
+            if (t < n_tiles) {
+                // slot 2t+1: VALU phase of tile t, then issue unit t+3; unit
+                // t+1 must be complete at the barrier
+                if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
+                if (t + 3 <= n_tiles) issue_unit(t + 3);
+                wait_unit(ahead_of(t + 1));
+                barrier();
+            }
+        }
+    } else {
+        // slot 0: issue units 2 and 3
+        if (2 <= n_tiles) issue_unit(2);
+        if (3 <= n_tiles) issue_unit(3);
+        barrier();
+        for (int t = 0; t <= n_tiles; ++t) {
+            // slot 2t+1: MFMA phase of tile t; unit t+1 must be complete
+            mfma_phase(t);
+            if (t < n_tiles) {
+                wait_unit(ahead_of(t + 1));
+                barrier();
+                // slot 2t+2: issue unit t+4, VALU phase of tile t
+                if (t + 4 <= n_tiles) issue_unit(t + 4);
+                if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
+                barrier();
+            }
+        }
     }
 
     l_run = wave_sum_xor(l_run, 32);
