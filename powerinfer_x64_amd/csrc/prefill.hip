@@ -160,16 +160,22 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
     // add vmcnt waits before LDS reads (it cannot tell the buffers apart);
     // the kernel waits for each unit explicitly before the barrier that
     // publishes it.
+    // M0 (the LDS destination) is a register the compiler reserves, so the
+    // assembly saves and restores it around the load.
     auto dma16 = [](const void* src, lds_void* dst) {
-        const unsigned m0 = (unsigned)(uintptr_t)dst;
-        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                     :: "v"(src), "s"(m0) : "memory", "m0");
+        const unsigned lds = (unsigned)(uintptr_t)dst;
+        unsigned saved;
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\t"
+                     "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
     };
     // scalar base + 32-bit lane byte offset form, for the common full tile
     auto dma16s = [](const void* base, unsigned voff, lds_void* dst) {
-        const unsigned m0 = (unsigned)(uintptr_t)dst;
-        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
-                     :: "v"(voff), "s"(base), "s"(m0) : "memory", "m0");
+        const unsigned lds = (unsigned)(uintptr_t)dst;
+        unsigned saved;
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+                     "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(voff), "s"(base), "s"(lds) : "memory");
     };
     // this lane's row and byte offset (within a tile) for each of its loads
     int k_row[3], v_row[2];
