@@ -258,7 +258,6 @@ __device__ __forceinline__ f32x4 mm16(const float* X, int xs, const float* Y, in
 struct GdnWs {
     f16* q16;   // [n_chunks][Hk][64][128] q / max(|q|,1e-12) / sqrt(Dk), f16
     f16* k16;   // [n_chunks][Hk][64][128] k / max(|k|,1e-12), f16
-    f16* kt16;  // [n_chunks][Hk][128][64] the same k, transposed
     float* tm;  // [n_chunks][Hv] (I + A)^-1 as f16 hi [64][64] then f16 lo [64][64]
     float* mm;  // [n_chunks][Hv] M, the same hi / lo form
     float* lg;  // [n_chunks][Hv][64] cumulative log decay
@@ -321,7 +320,7 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
         sk[row * KS_ + 64 + lane] = k1 * ik;
     }
     __syncthreads();
-    // the normalised rows in f16 for the scan: q, k row-major and k transposed
+    // the normalised rows in f16 for the scan: q, k row-major
     {
         const size_t base = ((size_t)n * hk + kh) * GC * DK;
         for (int e = tid; e < GC * DK / 4; e += 512) {
@@ -333,17 +332,6 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
             *reinterpret_cast<f16x4*>(w.k16 + base + row * DK + 4 * c4) =
                 f16x4{to_f16(b[0]), to_f16(b[1]), to_f16(b[2]), to_f16(b[3])};
         }
-        // thread (dim d, token group tg) writes K^T[d][16 tg .. 16 tg + 15]
-        const int d = tid & (DK - 1), tg = tid >> 7;
-        f16x8 lo, hi;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            lo[j] = to_f16(sk[(16 * tg + j) * KS_ + d]);
-            hi[j] = to_f16(sk[(16 * tg + 8 + j) * KS_ + d]);
-        }
-        f16* kt = w.kt16 + base + (size_t)d * GC + 16 * tg;
-        *reinterpret_cast<f16x8*>(kt) = lo;
-        *reinterpret_cast<f16x8*>(kt + 8) = hi;
     }
     // lower-triangular 16x16 tiles: 10 of K K^T, then 10 of Q K^T
     const int ln = lane & 15, lg4 = lane >> 4;
@@ -462,34 +450,20 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
 // products run on v_mfma_f32_16x16x32_f16 with q / k rounded once to f16 and
 // S^T / Dp split into f16 hi + lo parts (two MFMAs per 32-wide block); with
 // normalised q, k this keeps the products within ~1e-5 of f32.  Delta = T.R
-// and M.Delta split both operands (three MFMAs per block).  Chunk n+1 is
-// loaded into registers while chunk n computes.
+// and M.Delta split both operands (three MFMAs per block).
+//
+// Data movement: chunk n+1's q, k, T and M tiles (64 KB) arrive in the other
+// half of a double buffer by direct global -> LDS loads while chunk n
+// computes, issued by each wave group in the phase where it would otherwise
+// wait (Q side in phase 2, K side in phase 3); K^T comes from transposing
+// reads of the k tile.  The small per-chunk loads are unmasked (clamped), so
+// no compiler-inserted wait lands inside a phase.
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-constexpr int KH_ = DK + 8;  // f16 row stride of [64][128] q / k tiles (272 B)
-constexpr int KT_ = GC + 8;  // f16 row stride of [.][64] tiles: K^T, T, M, R^T, Delta^T (144 B)
-
-// C[16 x 16] = X[row0 .. row0+15][0 .. 32 nkb) . Y^T, X and Y^T [16][64] given
-// as f16 hi + lo parts (row stride KT_): hi.hi + hi.lo + lo.hi on the f16
-// MFMA, so the product keeps ~22 bits.  Lane: A rows row0 + ln, B column ln.
-__device__ __forceinline__ f32x4 mm_split(const f16* xh, const f16* xl, const f16* yh,
-                                          const f16* yl, int row0, int nkb) {
-    const int l = threadIdx.x & 63, ln = l & 15, g4 = l >> 4;
-    const int xo = (row0 + ln) * KT_ + 8 * g4, yo = ln * KT_ + 8 * g4;
-    f32x4 c = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = 0; kb < nkb; ++kb) {
-        const f16x8 ah = *reinterpret_cast<const f16x8*>(xh + xo + 32 * kb);
-        const f16x8 al = *reinterpret_cast<const f16x8*>(xl + xo + 32 * kb);
-        const f16x8 bh = *reinterpret_cast<const f16x8*>(yh + yo + 32 * kb);
-        const f16x8 bl = *reinterpret_cast<const f16x8*>(yl + yo + 32 * kb);
-        c = mfma16(ah, bh, c);
-        c = mfma16(ah, bl, c);
-        c = mfma16(al, bh, c);
-    }
-    return c;
-}
+constexpr int KH_ = DK + 8;  // f16 row stride of the [16][128] S^T tiles (272 B)
+constexpr int KT_ = GC + 8;  // f16 row stride of the [16][64] R^T, Delta^T tiles (144 B)
 
 __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__ q,
                                                        const float* __restrict__ k,
@@ -498,13 +472,13 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
                                                        float* __restrict__ state,
                                                        float* __restrict__ out, int n_tok,
                                                        int hk, int hv, GdnWs w) {
-    __shared__ __attribute__((aligned(16))) f16 skh[GC * KH_];      // k (normalised)
-    __shared__ __attribute__((aligned(16))) f16 sqh[GC * KH_];      // q (normalised)
-    __shared__ __attribute__((aligned(16))) f16 skt[DK * KT_];      // K^T
-    __shared__ __attribute__((aligned(16))) f16 sth[GC * KT_];      // T hi
-    __shared__ __attribute__((aligned(16))) f16 stl[GC * KT_];      // T lo
-    __shared__ __attribute__((aligned(16))) f16 smh[GC * KT_];      // M hi
-    __shared__ __attribute__((aligned(16))) f16 sml[GC * KT_];      // M lo
+    // Chunk tiles, double-buffered, filled by direct global -> LDS loads:
+    // q, k [64][128] f16 (256-byte rows, 16-byte chunk c of row r at c ^ (r % 16)),
+    // T, M hi + lo [64][64] f16 each (128-byte rows, chunk c of row r at c ^ (r/2 % 8)).
+    __shared__ __attribute__((aligned(1024))) f16 sq_[2][GC * DK];
+    __shared__ __attribute__((aligned(1024))) f16 sk_[2][GC * DK];
+    __shared__ __attribute__((aligned(1024))) f16 st_[2][2 * GC * GC];  // T hi, then lo
+    __shared__ __attribute__((aligned(1024))) f16 sm_[2][2 * GC * GC];  // M hi, then lo
     __shared__ __attribute__((aligned(16))) f16 ssh[SCOLS * KH_];   // S^T hi
     __shared__ __attribute__((aligned(16))) f16 ssl[SCOLS * KH_];   // S^T lo
     __shared__ __attribute__((aligned(16))) f16 srth[SCOLS * KT_];  // R^T hi
@@ -513,12 +487,13 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     __shared__ __attribute__((aligned(16))) f16 sdtl[SCOLS * KT_];  // Delta^T lo
     __shared__ __attribute__((aligned(16))) f16 sdph[SCOLS * KT_];  // (gamma_C/gamma) Delta, ^T, hi
     __shared__ __attribute__((aligned(16))) f16 sdpl[SCOLS * KT_];  // ... lo
-    __shared__ float sgam[GC], sdec[GC], sb[GC];  // exp(lg_i), exp(lg_C - lg_i), beta
+    __shared__ float sgam[2][GC], sdec[2][GC], sb[2][GC];  // exp(lg_i), exp(lg_C - lg_i), beta
     // blockIdx.x = tile * hv + vh: with hv a multiple of 8 the tiles of one
     // head share an XCD (and its L2) under round-robin dispatch.
     const int vh = blockIdx.x % hv, tile = blockIdx.x / hv, kh = vh % hk;
     const int c0 = tile * SCOLS;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ln = lane & 15, g4 = lane >> 4;
     const int rb = wave & 3;          // chunk row block of this wave
     const bool kside = wave < 4;      // wave-uniform
@@ -540,82 +515,148 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     };
     put_state();
 
-    // chunk data staged in registers (prefetch of the next chunk): 16-byte
-    // pieces of q16, k16, kt16 (2 each per thread), T and M (2 each)
-    f32x4 pc[10];
-    float pv[4], plg = 0.f, plc = 0.f, pb = 0.f;
-    auto fetch = [&](int n) {
-        const int t0 = n * GC;
-        const size_t qb = ((size_t)n * hk + kh) * GC * DK;
-        const f32x4* q4 = reinterpret_cast<const f32x4*>(w.q16 + qb);
-        const f32x4* k4 = reinterpret_cast<const f32x4*>(w.k16 + qb);
-        const f32x4* kt4 = reinterpret_cast<const f32x4*>(w.kt16 + qb);
-        const f32x4* tm4 = reinterpret_cast<const f32x4*>(w.tm + ((size_t)n * hv + vh) * GC * GC);
-        const f32x4* mm4 = reinterpret_cast<const f32x4*>(w.mm + ((size_t)n * hv + vh) * GC * GC);
+    // Direct loads (16 bytes per lane; lane i lands at base + 16 i), issued
+    // from inline assembly so that the compiler adds no waits before LDS
+    // reads; M0 (the LDS destination) is saved and restored.  Wave w issues
+    // loads 8w .. 8w+7 of a chunk: 0-15 q, 16-31 k (4 rows each), 32-47 T,
+    // 48-63 M (8 rows each).
+    typedef __attribute__((address_space(3))) void lds_void;
+    auto dma16s = [](const void* base, unsigned voff, lds_void* dst) {
+        const unsigned lds = (unsigned)(uintptr_t)dst;
+        unsigned saved;
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+                     "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(voff), "s"(base), "s"(lds) : "memory");
+    };
+    // this lane's source byte offset within its tile for each of its 8 loads;
+    // the Q-side waves load q and k (in phase 2, where they are idle), the
+    // K-side waves T and M (in phase 3)
+    const int lw = kside ? 4 + wave : wave - 4;
+    unsigned doff[8];
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int e = tid + 512 * it;
-            pc[it] = q4[e];
-            pc[2 + it] = k4[e];
-            pc[4 + it] = kt4[e];
-            pc[6 + it] = tm4[e];
-            pc[8 + it] = mm4[e];
+    for (int j = 0; j < 8; ++j) {
+        const int i = 8 * lw + j, ti = i & 15;
+        if (i < 32) {  // q or k: rows 4 ti + lane / 16
+            const int r = 4 * ti + (lane >> 4), c = (lane & 15) ^ (r & 15);
+            doff[j] = (unsigned)((r * DK + 8 * c) * 2);
+        } else {       // T or M hi / lo: rows 8 ti' + lane / 8 of the [128][64] pair
+            const int r = 8 * ti + (lane >> 3), rr = r & 63, c = (lane & 7) ^ ((rr >> 1) & 7);
+            doff[j] = (unsigned)(((r >> 6) * GC * GC + rr * GC + 8 * c) * 2);
         }
-        // V tile in the MFMA C layout of the K-side waves: rows 16 rb + 4 g + r, column ln
+    }
+    auto issue = [&](int n) {
+        const int b = n & 1;
+        const size_t qb = ((size_t)n * hk + kh) * GC * DK;
+        const size_t tb = ((size_t)n * hv + vh) * GC * GC * 2;  // f16 elements of a T / M pair
+        const f16* tm = reinterpret_cast<const f16*>(w.tm);
+        const f16* mm = reinterpret_cast<const f16*>(w.mm);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = 8 * lw + j, ti = i & 15;
+            if (i < 16) dma16s(w.q16 + qb, doff[j], (lds_void*)&sq_[b][512 * ti]);
+            else if (i < 32) dma16s(w.k16 + qb, doff[j], (lds_void*)&sk_[b][512 * ti]);
+            else if (i < 48) dma16s(tm + tb, doff[j], (lds_void*)&st_[b][512 * ti]);
+            else dma16s(mm + tb, doff[j], (lds_void*)&sm_[b][512 * ti]);
+        }
+    };
+    // V tile (K-side waves, MFMA C layout: rows 16 rb + 4 g4 + r, column ln), lg and beta
+    float pv[4], plg = 0.f, plc = 0.f, pb = 0.f;
+    bool pbm = false;
+    // Rows past the prompt reload the last token (finite values; their beta
+    // is 0, so R = 0 there); no lane is masked, so no load waits on another.
+    auto fetch_small = [&](int n) {
+        const int t0 = n * GC;
         if (kside) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int t = t0 + 16 * rb + 4 * g4 + r;
-                pv[r] = t < n_tok ? v[((size_t)t * hv + vh) * DV + c0 + ln] : 0.f;
+                const int t = min(t0 + 16 * rb + 4 * g4 + r, n_tok - 1);
+                pv[r] = v[((size_t)t * hv + vh) * DV + c0 + ln];
             }
         }
-        if (tid < GC) {
-            plg = w.lg[((size_t)n * hv + vh) * GC + tid];
+        if (wave == 0) {
+            const int tl = min(lane, GC - 1);
+            plg = w.lg[((size_t)n * hv + vh) * GC + tl];
             plc = w.lg[((size_t)n * hv + vh) * GC + GC - 1];
-            const int t = t0 + tid;
-            pb = t < n_tok ? beta[(size_t)t * hv + vh] : 0.f;
+            const int t = t0 + tl;
+            pb = beta[(size_t)min(t, n_tok - 1) * hv + vh];  // masked in stage_small
+            pbm = t < n_tok;
         }
     };
-    auto stage = [&]() {
+    auto stage_small = [&](int n) {
+        if (wave == 0) {
+            sgam[n & 1][tid] = expf(plg);
+            sdec[n & 1][tid] = expf(plc - plg);
+            sb[n & 1][tid] = pbm ? pb : 0.f;
+        }
+    };
+    // A-operand tile reads (row r, 8 elements at column 8 c)
+    auto frag_qk = [&](const f16* t, int r, int c) {
+        return *reinterpret_cast<const f16x8*>(t + r * DK + 8 * (c ^ (r & 15)));
+    };
+    auto frag_tm = [&](const f16* t, int r, int c) {
+        return *reinterpret_cast<const f16x8*>(t + r * GC + 8 * (c ^ ((r >> 1) & 7)));
+    };
+    // C[16 x 16] = X[row0 .. +15][0 .. 32 nkb) . Y^T with X (swizzled [64][64]
+    // hi, lo) and Y^T ([16][64] hi, lo, row stride KT_): hi.hi + hi.lo + lo.hi
+    auto mm_split_sw = [&](const f16* xh, const f16* xl, const f16* yh, const f16* yl, int r0,
+                           int nkb) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = 0; kb < nkb; ++kb) {
+            const f16x8 ah = frag_tm(xh, r0 + ln, 4 * kb + g4);
+            const f16x8 al = frag_tm(xl, r0 + ln, 4 * kb + g4);
+            const f16x8 bh = *reinterpret_cast<const f16x8*>(yh + ln * KT_ + 8 * g4 + 32 * kb);
+            const f16x8 bl = *reinterpret_cast<const f16x8*>(yl + ln * KT_ + 8 * g4 + 32 * kb);
+            c = mfma16(ah, bh, c);
+            c = mfma16(ah, bl, c);
+            c = mfma16(al, bh, c);
+        }
+        return c;
+    };
+    // K^T operand of the state update by two transposing reads: in each
+    // 16-lane group, lane j points at token kb0 + j/4, dims row0 + 4 (j % 4)
+    // .. +3; lane i then holds tokens kb0 .. kb0+3 of dim row0 + i.
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4* lds_s4;
+    typedef f16 f16x4_ __attribute__((ext_vector_type(4)));
+    auto frag_kt = [&](const f16* kt, int kb) {  // tokens 32 kb + 8 g4 .. +7, dim row0 + ln
+        f16x8 res;
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int e = tid + 512 * it;
-            const int r16 = e >> 4, c16 = (e & 15) * 8;  // [64][128] f16: 16 pieces per row
-            *reinterpret_cast<f32x4*>(sqh + r16 * KH_ + c16) = pc[it];
-            *reinterpret_cast<f32x4*>(skh + r16 * KH_ + c16) = pc[2 + it];
-            const int rt = e >> 3, ct = (e & 7) * 8;     // [128][64] f16: 8 pieces per row
-            *reinterpret_cast<f32x4*>(skt + rt * KT_ + ct) = pc[4 + it];
-            // T, M: hi [64][64] f16 (pieces 0..511), then lo (512..1023)
-            const int rm = tid >> 3, cm = (tid & 7) * 8;
-            *reinterpret_cast<f32x4*>((it ? stl : sth) + rm * KT_ + cm) = pc[6 + it];
-            *reinterpret_cast<f32x4*>((it ? sml : smh) + rm * KT_ + cm) = pc[8 + it];
+        for (int h = 0; h < 2; ++h) {
+            const int tok = 32 * kb + 8 * g4 + 4 * h + (ln >> 2);
+            const int dim = row0 + 4 * (ln & 3);
+            const int c = (dim >> 3) ^ (tok & 15);
+            const f16* p = kt + tok * DK + 8 * c + (dim & 7);
+            const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(p));
+            const f16x4_ y = __builtin_bit_cast(f16x4_, x);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) res[4 * h + e] = y[e];
         }
-        if (tid < GC) {
-            sgam[tid] = expf(plg);
-            sdec[tid] = expf(plc - plg);
-            sb[tid] = pb;
-        }
+        return res;
     };
 
     float vcur[4] = {0.f, 0.f, 0.f, 0.f};
-    fetch(0);
-    stage();
+    issue(0);
+    fetch_small(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    stage_small(0);
 #pragma unroll
     for (int r = 0; r < 4; ++r) vcur[r] = pv[r];
     __syncthreads();
     for (int n = 0; n < n_chunks; ++n) {
-        const int t0 = n * GC;
-        if (n + 1 < n_chunks) fetch(n + 1);
-        const float gC = sgam[GC - 1];
+        const int t0 = n * GC, cb = n & 1;
+        if (n + 1 < n_chunks) fetch_small(n + 1);
+        const f16* tq = sq_[cb];
+        const f16* tk = sk_[cb];
+        const float gC = sgam[cb][GC - 1];
         // phase 1: K.S (waves 0-3) or Q.S (waves 4-7), rows 16 rb ..
         f32x4 xs = {0.f, 0.f, 0.f, 0.f};
         {
-            const f16* xr = (kside ? skh : sqh) + (16 * rb + ln) * KH_ + 8 * g4;
+            const f16* xt = kside ? tk : tq;
             const f16* sh = ssh + ln * KH_ + 8 * g4;
             const f16* sl = ssl + ln * KH_ + 8 * g4;
 #pragma unroll
             for (int kb = 0; kb < DK / 32; ++kb) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(xr + 32 * kb);
+                const f16x8 a = frag_qk(xt, 16 * rb + ln, 4 * kb + g4);
                 xs = mfma16(a, *reinterpret_cast<const f16x8*>(sh + 32 * kb), xs);
                 xs = mfma16(a, *reinterpret_cast<const f16x8*>(sl + 32 * kb), xs);
             }
@@ -625,7 +666,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
-                const float rv = sb[i] * (vcur[r] - sgam[i] * xs[r]);
+                const float rv = sb[cb][i] * (vcur[r] - sgam[cb][i] * xs[r]);
                 rh[r] = to_f16(rv);
                 rl[r] = to_f16(rv - (float)rh[r]);
             }
@@ -633,16 +674,17 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             *reinterpret_cast<f16x4*>(srtl + ln * KT_ + 16 * rb + 4 * g4) = rl;
         }
         __syncthreads();
+        if (!kside && n + 1 < n_chunks) issue(n + 1);
         // phase 2: Delta = T R (T lower triangular: column blocks <= rb)
         if (kside) {
-            const f32x4 dl = mm_split(sth, stl, srth, srtl, 16 * rb, (rb >> 1) + 1);
+            const f32x4 dl = mm_split_sw(st_[cb], st_[cb] + GC * GC, srth, srtl, 16 * rb, (rb >> 1) + 1);
             f16x4 dh, dlo, ph, pl;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
                 dh[r] = to_f16(dl[r]);
                 dlo[r] = to_f16(dl[r] - (float)dh[r]);
-                const float dp = sdec[i] * dl[r];
+                const float dp = sdec[cb][i] * dl[r];
                 ph[r] = to_f16(dp);
                 pl[r] = to_f16(dp - (float)ph[r]);
             }
@@ -652,14 +694,16 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             *reinterpret_cast<f16x4*>(sdpl + ln * KT_ + 16 * rb + 4 * g4) = pl;
         }
         __syncthreads();
+        // chunk n+1's tiles go to the other buffer (last read in chunk n-1)
+        if (kside && n + 1 < n_chunks) issue(n + 1);
         // phase 3a: O = gamma QS + M Delta (waves 4-7)
         if (!kside) {
-            const f32x4 o = mm_split(smh, sml, sdth, sdtl, 16 * rb, (rb >> 1) + 1);
+            const f32x4 o = mm_split_sw(sm_[cb], sm_[cb] + GC * GC, sdth, sdtl, 16 * rb, (rb >> 1) + 1);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * rb + 4 * g4 + r;
                 const int t = t0 + i;
-                if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = sgam[i] * xs[r] + o[r];
+                if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = sgam[cb][i] * xs[r] + o[r];
             }
         }
         // phase 3b: S'^T = exp(lgC) S^T + Dp^T K for state rows row0 .. row0 + 15
@@ -667,19 +711,19 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             f32x4 acc = sv * gC;
             const f16* ah = sdph + ln * KT_ + 8 * g4;
             const f16* al = sdpl + ln * KT_ + 8 * g4;
-            const f16* kt = skt + (row0 + ln) * KT_ + 8 * g4;
 #pragma unroll
             for (int kb = 0; kb < GC / 32; ++kb) {
-                const f16x8 b = *reinterpret_cast<const f16x8*>(kt + 32 * kb);
+                const f16x8 b = frag_kt(tk, kb);
                 acc = mfma16(*reinterpret_cast<const f16x8*>(ah + 32 * kb), b, acc);
                 acc = mfma16(*reinterpret_cast<const f16x8*>(al + 32 * kb), b, acc);
             }
             sv = acc;
         }
-        __syncthreads();  // every wave has read S^T hi / lo and this chunk's tiles
+        // S^T hi / lo were last read in phase 1 (before two barriers)
         put_state();
+        __builtin_amdgcn_s_waitcnt(0);  // chunk n+1's loads (direct and small)
         if (n + 1 < n_chunks) {
-            stage();
+            stage_small(n + 1);
 #pragma unroll
             for (int r = 0; r < 4; ++r) vcur[r] = pv[r];
         }
@@ -740,8 +784,8 @@ hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, con
 
 size_t gdn_prefill_ws_floats(int32_t n_tok, int32_t n_k_heads, int32_t n_v_heads, int32_t chunk) {
     const size_t nc = (size_t)(n_tok + chunk - 1) / chunk;
-    // three f16 [64][128] tiles per (chunk, K head) = 1.5 x 8192 floats
-    return 3 * nc * n_k_heads * GC * DK / 2 + 2 * nc * n_v_heads * GC * GC + nc * n_v_heads * GC;
+    // two f16 [64][128] tiles (q, k) per (chunk, K head) = 8192 floats
+    return nc * n_k_heads * GC * DK + 2 * nc * n_v_heads * GC * GC + nc * n_v_heads * GC;
 }
 
 hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, const float* beta,
@@ -751,11 +795,10 @@ hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, co
     if (chunk != GC) return hipErrorInvalidValue;
     const size_t nc = (size_t)(n_tok + GC - 1) / GC;
     GdnWs w;
-    const size_t qk = nc * n_k_heads * GC * DK;  // f16 elements of one of q16 / k16 / kt16
+    const size_t qk = nc * n_k_heads * GC * DK;  // f16 elements of one of q16 / k16
     w.q16 = reinterpret_cast<f16*>(ws.buf);
     w.k16 = w.q16 + qk;
-    w.kt16 = w.k16 + qk;
-    w.tm = reinterpret_cast<float*>(w.kt16 + qk);
+    w.tm = reinterpret_cast<float*>(w.k16 + qk);
     w.mm = w.tm + nc * n_v_heads * GC * GC;
     w.lg = w.mm + nc * n_v_heads * GC * GC;
     hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)nc, n_k_heads), dim3(512), 0, s, q, k, beta, g,
