@@ -288,51 +288,62 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
     const int t0 = n * GC;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    // raw rows of the K head (zeros past the end of the prompt)
-    for (int e = tid; e < GC * DK / 4; e += 512) {
-        const int row = e / (DK / 4), c4 = e % (DK / 4);
-        const int t = t0 + row;
-        f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
-        if (t < n_tok) {
-            a = *reinterpret_cast<const f32x4*>(q + ((size_t)t * hk + kh) * DK + 4 * c4);
-            b = *reinterpret_cast<const f32x4*>(k + ((size_t)t * hk + kh) * DK + 4 * c4);
-        }
-        *reinterpret_cast<f32x4*>(sq + row * KS_ + 4 * c4) = a;
-        *reinterpret_cast<f32x4*>(sk + row * KS_ + 4 * c4) = b;
-    }
-    __syncthreads();
-    // L2 norms (src/model/mod.rs:860-875); wave w handles rows 8w..8w+7
-    for (int rr = 0; rr < 8; ++rr) {
-        const int row = 8 * wave + rr;
-        const float q0 = sq[row * KS_ + lane], q1 = sq[row * KS_ + 64 + lane];
-        const float k0 = sk[row * KS_ + lane], k1 = sk[row * KS_ + 64 + lane];
-        float ssq = q0 * q0 + q1 * q1, ssk = k0 * k0 + k1 * k1;
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            ssq = wave_sum_xor(ssq, m);
-            ssk = wave_sum_xor(ssk, m);
-        }
-        const float iq = 1.0f / fmaxf(sqrtf(ssq), 1e-12f) * (1.0f / sqrtf((float)DK));
-        const float ik = 1.0f / fmaxf(sqrtf(ssk), 1e-12f);
-        sq[row * KS_ + lane] = q0 * iq;
-        sq[row * KS_ + 64 + lane] = q1 * iq;
-        sk[row * KS_ + lane] = k0 * ik;
-        sk[row * KS_ + 64 + lane] = k1 * ik;
-    }
-    __syncthreads();
-    // the normalised rows in f16 for the scan: q, k row-major
+    // g and beta of the first V-head pair, fetched early (their latency
+    // hides under the q / k loads): waves 0 and 4, lane = token of the chunk
+    const int half = wave >> 2, wl = wave & 3, ht = tid & 255;
+    float g_pre = 0.f, b_pre = 0.f;
     {
-        const size_t base = ((size_t)n * hk + kh) * GC * DK;
-        for (int e = tid; e < GC * DK / 4; e += 512) {
-            const int row = e / (DK / 4), c4 = e % (DK / 4);
-            const f32x4 a = *reinterpret_cast<const f32x4*>(sq + row * KS_ + 4 * c4);
-            const f32x4 b = *reinterpret_cast<const f32x4*>(sk + row * KS_ + 4 * c4);
-            *reinterpret_cast<f16x4*>(w.q16 + base + row * DK + 4 * c4) =
-                f16x4{to_f16(a[0]), to_f16(a[1]), to_f16(a[2]), to_f16(a[3])};
-            *reinterpret_cast<f16x4*>(w.k16 + base + row * DK + 4 * c4) =
-                f16x4{to_f16(b[0]), to_f16(b[1]), to_f16(b[2]), to_f16(b[3])};
+        const int vh = kh + half * hk, t = min(t0 + lane, n_tok - 1);
+        if (wl == 0 && vh < hv) {
+            g_pre = g[(size_t)t * hv + vh];
+            b_pre = beta[(size_t)t * hv + vh];
         }
     }
+    // raw rows of the K head, L2-normalised on the way in (src/model/mod.rs:
+    // 860-875): thread t owns 16 values of row t / 8 (pieces (t % 8) + 8 j);
+    // the row sums reduce over 8 lanes.  Rows past the prompt are zero (their
+    // inverse norm is then irrelevant).  The normalised rows go to LDS in f32
+    // and to the workspace in f16 for the scan.
+    {
+        const int row = tid >> 3, part = tid & 7;
+        const int t = t0 + row;
+        const bool ok = t < n_tok;
+        const size_t src = ((size_t)min(t, n_tok - 1) * hk + kh) * DK;
+        f32x4 a[4], b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            a[j] = *reinterpret_cast<const f32x4*>(q + src + 4 * (part + 8 * j));
+            b[j] = *reinterpret_cast<const f32x4*>(k + src + 4 * (part + 8 * j));
+        }
+        float ssq = 0.f, ssk = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                ssq += a[j][e] * a[j][e];
+                ssk += b[j][e] * b[j][e];
+            }
+#pragma unroll
+        for (int m = 1; m < 8; m <<= 1) {
+            ssq += __shfl_xor(ssq, m, 64);
+            ssk += __shfl_xor(ssk, m, 64);
+        }
+        const float iq = ok ? 1.0f / fmaxf(sqrtf(ssq), 1e-12f) * (1.0f / sqrtf((float)DK)) : 0.f;
+        const float ik = ok ? 1.0f / fmaxf(sqrtf(ssk), 1e-12f) : 0.f;
+        const size_t base = ((size_t)n * hk + kh) * GC * DK + (size_t)row * DK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 4 * (part + 8 * j);
+            const f32x4 x = a[j] * iq, y = b[j] * ik;
+            *reinterpret_cast<f32x4*>(sq + row * KS_ + c) = x;
+            *reinterpret_cast<f32x4*>(sk + row * KS_ + c) = y;
+            *reinterpret_cast<f16x4*>(w.q16 + base + c) =
+                f16x4{to_f16(x[0]), to_f16(x[1]), to_f16(x[2]), to_f16(x[3])};
+            *reinterpret_cast<f16x4*>(w.k16 + base + c) =
+                f16x4{to_f16(y[0]), to_f16(y[1]), to_f16(y[2]), to_f16(y[3])};
+        }
+    }
+    __syncthreads();
     // lower-triangular 16x16 tiles: 10 of K K^T, then 10 of Q K^T
     const int ln = lane & 15, lg4 = lane >> 4;
     for (int tix = wave; tix < 20; tix += 8) {
@@ -347,7 +358,6 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
     }
     __syncthreads();  // q / k rows are dead: s_big now holds two halves of A, T, scratch
 
-    const int half = wave >> 2, wl = wave & 3, ht = tid & 255;
     float* sa = s_big + half * PREP_B;  // A
     float* st = sa + GC * TS_;          // T = (I + A)^-1
     float* sx = st + GC * TS_;          // per-wave 16x16 scratch
@@ -358,32 +368,51 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
         const bool on = vh < hv;  // uniform per half; barriers stay uniform per workgroup
         if (on && wl == 0) {      // inclusive cumsum of g, and beta (0 past the end)
             const int t = t0 + lane;
-            float x = t < n_tok ? g[(size_t)t * hv + vh] : 0.f;
+            if (v0 != kh) {
+                const int tc = min(t, n_tok - 1);
+                g_pre = g[(size_t)tc * hv + vh];
+                b_pre = beta[(size_t)tc * hv + vh];
+            }
+            float x = t < n_tok ? g_pre : 0.f;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const float y = __shfl_up(x, o, 64);
                 if (lane >= o) x += y;
             }
-            hlg[lane] = x;
-            hb[lane] = t < n_tok ? beta[(size_t)t * hv + vh] : 0.f;
+            hlg[lane] = x * kLog2e;  // log2 units for exp2
+            hb[lane] = t < n_tok ? b_pre : 0.f;
             w.lg[((size_t)n * hv + vh) * GC + lane] = x;
         }
         __syncthreads();
         if (on) {
+            // thread: row i, columns 4 j4 .. 4 j4 + 3; entries above the
+            // diagonal are 0 (and need no exp)
             f16* mm = reinterpret_cast<f16*>(w.mm + ((size_t)n * hv + vh) * GC * GC);
-            for (int e = ht; e < GC * GC; e += 256) {
-                const int i = e / GC, j = e % GC;
-                float a = 0.f, m = 0.f;
-                if (j <= i) {
-                    const float dec = expf(hlg[i] - hlg[j]);
-                    if (j < i) a = hb[i] * dec * skk[i * TS_ + j];
-                    m = dec * sqk[i * TS_ + j];
+            for (int e = ht; e < GC * GC / 4; e += 256) {
+                const int i = e / (GC / 4), j0 = 4 * (e % (GC / 4));
+                f32x4 av = {0.f, 0.f, 0.f, 0.f}, mv = av;
+                if (j0 <= i) {
+                    const float li = hlg[i], bi = hb[i];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int j = j0 + r;
+                        if (j <= i) {
+                            const float dec = fast_exp2(li - hlg[j]);
+                            if (j < i) av[r] = bi * dec * skk[i * TS_ + j];
+                            mv[r] = dec * sqk[i * TS_ + j];
+                        }
+                    }
                 }
-                sa[i * TS_ + j] = a;
-                st[i * TS_ + j] = 0.f;
-                const f16 mh = to_f16(m);
-                mm[e] = mh;
-                mm[GC * GC + e] = to_f16(m - (float)mh);
+                *reinterpret_cast<f32x4*>(sa + i * TS_ + j0) = av;
+                *reinterpret_cast<f32x4*>(st + i * TS_ + j0) = f32x4{0.f, 0.f, 0.f, 0.f};
+                f16x4 mh, ml;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    mh[r] = to_f16(mv[r]);
+                    ml[r] = to_f16(mv[r] - (float)mh[r]);
+                }
+                *reinterpret_cast<f16x4*>(mm + i * GC + j0) = mh;
+                *reinterpret_cast<f16x4*>(mm + GC * GC + i * GC + j0) = ml;
             }
         }
         __syncthreads();
