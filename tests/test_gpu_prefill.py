@@ -95,3 +95,26 @@ def test_prefill_noncausal_and_grouped_vs_f64():
     out = _run(tq, tk, tv, causal=False, gqa_mode=1)
     ref = np.stack([ref64.attention(qf[i], kf, vf, lambda h: h // 4) for i in range(160)])
     assert row_rel_err(out, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_batch_of_two(causal):
+    """Two sequences in one launch (the batch offsets of q, k, v and out): each
+    against its own oracle rows, S = 200 (a partial last tile)."""
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    rng = np.random.default_rng(31 + causal)
+    seqs = [_inputs(rng, 200, 32, 8, 128) for _ in range(2)]
+    q = torch.stack([s[0] for s in seqs]).cuda()
+    k = torch.stack([s[1] for s in seqs]).cuda()
+    v = torch.stack([s[2] for s in seqs]).cuda()
+    out = rt.attn_prefill(dev, q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    for bi, (tq, tk, tv) in enumerate(seqs):
+        if causal:
+            ref = _oracle_rows(tq, tk, tv, range(200))
+        else:
+            qf, kf, vf = (t.float().numpy() for t in (tq, tk, tv))
+            ref = np.stack([ref64.attention(qf[i], kf, vf, lambda h: h % 8) for i in range(200)])
+        assert row_rel_err(out[bi], ref) <= 1e-2, bi
