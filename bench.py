@@ -13,6 +13,11 @@ TFLOP/s, the all-32k variant of config 2, config 4 gated decode, config 1,
 and the gated-DeltaNet decode step.  Inputs are synthetic N(0,1) generated on
 the GPU from fixed seeds; RoPE is applied by the library's own kernel.
 
+Timing: after `warmup` calls and a synchronize, one HIP event pair on the
+library's stream brackets `steps` back-to-back calls, followed by a
+synchronize; ms_per_step is that interval / steps.  A second pass with an
+event pair per call gives the median and minimum.
+
 cpu_baseline: the oracle (a C restatement of the reference's CPU loops,
 single core) on the same decode inputs read back from the pool.
 """
@@ -57,21 +62,31 @@ class Timer:
         self.torch = torch
 
     def run(self, fn, steps, warmup):
+        """ms_avg: one event pair around `steps` back-to-back calls (the timed
+        region, host submission overlapped with the GPU); ms_median / ms_min:
+        a second pass with an event pair around each call."""
         torch = self.torch
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
-        for a, b in ev:
-            a.record()
+        a.record()
+        for _ in range(steps):
             fn()
-            b.record()
+        b.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        per = [a.elapsed_time(b) for a, b in ev]  # ms
-        return {"ms_avg": float(np.mean(per)), "ms_median": float(np.median(per)),
+        avg = a.elapsed_time(b) / steps
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        for x, y in ev:
+            x.record()
+            fn()
+            y.record()
+        torch.cuda.synchronize()
+        per = [x.elapsed_time(y) for x, y in ev]  # ms
+        return {"ms_avg": float(avg), "ms_median": float(np.median(per)),
                 "ms_min": float(np.min(per)), "wall_s": wall}
 
 
