@@ -350,15 +350,6 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
         l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     };
 
-    // Slots k = 0 .. 2*n_tiles+1, a barrier after each but the last.  Lead
-    // group (waves 0-3): slot 2t = MFMA phase of tile t (PV of tile t-1, QK
-    // of tile t, from unit t), slot 2t+1 = VALU phase of tile t; the lag group
-    // (waves 4-7) runs each one slot later, so each SIMD has one wave in each
-    // phase.  Each wave issues its loads of a unit in a VALU phase (4 waves
-    // per slot): unit u >= 4 in slot 2u-5 (lead) and 2u-6 (lag), after the
-    // last read of unit u-4 (slot 2u-7) in the same buffer; each wave waits
-    // for its part of unit u before the barrier that ends slot 2u-1, when its
-    // loads of units u+1 and u+2 may still be in flight.
     issue_unit(0);
     if (n_tiles >= 1) issue_unit(1);
     __builtin_amdgcn_s_waitcnt(0);  // all counters (Q loads, units 0 and 1)
@@ -389,35 +380,36 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
         if (qk) run_qk(t % NB);
         __builtin_amdgcn_s_setprio(0);
     };
+    // One barrier per tile step t = 0 .. n_tiles.  Lead waves: MFMA phase of
+    // tile t, then the softmax of tile t; lag waves: the softmax of tile t-1,
+    // then the MFMA phase of tile t.  So each SIMD's two wavefronts alternate
+    // phases inside the step.  Each wave issues its loads of unit t+3 in step
+    // t (unit t-1, the buffer's previous occupant, was last read in step t-1)
+    // and waits for unit t+1 before the barrier.
+    // One barrier per tile step t = 0 .. n_tiles.  Lead waves (0-3): the
+    // MFMA phase of tile t, then the softmax of tile t; lag waves (4-7): the
+    // softmax of tile t-1, then the MFMA phase of tile t; so the two
+    // wavefronts of each SIMD alternate phases inside a step.  Each wave
+    // issues its loads of unit t+3 in step t (the buffer's previous unit, t-1,
+    // was last read in step t-1) and waits for unit t+1 before the barrier.
+    if (2 <= n_tiles) issue_unit(2);
     if (wave < NW / 2) {
-        if (2 <= n_tiles) issue_unit(2);
         for (int t = 0; t <= n_tiles; ++t) {
-            // slot 2t: MFMA phase of tile t
             mfma_phase(t);
-            barrier();
+            if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
+            if (t + 3 <= n_tiles) issue_unit(t + 3);
             if (t < n_tiles) {
-                // slot 2t+1: VALU phase of tile t, then issue unit t+3; unit
-                // t+1 must be complete at the barrier
-                if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
-                if (t + 3 <= n_tiles) issue_unit(t + 3);
                 wait_unit(ahead_of(t + 1));
                 barrier();
             }
         }
     } else {
-        // slot 0: issue units 2 and 3
-        if (2 <= n_tiles) issue_unit(2);
-        if (3 <= n_tiles) issue_unit(3);
-        barrier();
         for (int t = 0; t <= n_tiles; ++t) {
-            // slot 2t+1: MFMA phase of tile t; unit t+1 must be complete
+            if (t >= 1 && t - 1 < w_tiles) phase_softmax(t - 1, t - 1 == w_tiles - 1 && last_masked);
+            if (t + 3 <= n_tiles) issue_unit(t + 3);
             mfma_phase(t);
             if (t < n_tiles) {
                 wait_unit(ahead_of(t + 1));
-                barrier();
-                // slot 2t+2: issue unit t+4, VALU phase of tile t
-                if (t + 4 <= n_tiles) issue_unit(t + 4);
-                if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
                 barrier();
             }
         }
