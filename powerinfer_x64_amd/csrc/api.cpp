@@ -478,7 +478,8 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill: gqa_mode %d", gqa_mode);
     if (dtype != PI_BF16 && dtype != PI_F16)
         return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: dtype %d (bf16 or f16)", dtype);
-    if (head_dim != 128) return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: head_dim %d (128)", head_dim);
+    if (head_dim != 128 && head_dim != 256)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: head_dim %d (128 or 256)", head_dim);
     if (n_q_heads % n_kv_heads != 0)
         return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: n_q_heads %d not a multiple of n_kv_heads %d", n_q_heads, n_kv_heads);
     if (batch == 0 || seq_len == 0) return PI_OK;
@@ -900,7 +901,7 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
                                L->max_pages, d_start, 1, n_tokens, L->n_heads, sv)))
         return rc;
     const float scale = 1.0f / std::sqrt((float)D);
-    if (prev == 0 && n_tokens > 1 && D == 128 && L->kv_dtype == PI_F16) {
+    if (prev == 0 && n_tokens > 1 && (D == 128 || D == 256) && L->kv_dtype == PI_F16) {
         // a fresh prompt: causal flash attention over the rotated rows (f16 inputs)
         PI_HIP(h, pi::launch_to_half(dq, hq16, nq, s), "pi_attn_layer_forward");
         PI_HIP(h, pi::launch_to_half(dk, hk16, nk, s), "pi_attn_layer_forward");

@@ -26,7 +26,6 @@
 namespace pi {
 namespace {
 
-constexpr int D = 128;
 constexpr int BN = 64;         // keys per block
 constexpr int ROWS = 32;       // query rows per wavefront
 constexpr float kLazy = 8.0f;  // log2 headroom before the running max moves
@@ -89,20 +88,35 @@ __device__ __forceinline__ float max16(const f32x16& s) {
     return fmaxf(fmaxf(fmaxf(a, b), fmaxf(c, d)), fmaxf(e, s[15]));
 }
 
-template <typename T, int HPW>
-__global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
+// Head dims 128 and 256.  D = 128: 8 wavefronts (two per SIMD, in opposite
+// phases, see below) and four unit buffers.  D = 256: O and Q^T take 192
+// registers at 32 query rows, so the workgroup has 4 wavefronts (one per SIMD,
+// up to 512 registers each) and two unit buffers; each wavefront runs its MFMA
+// and softmax phases back to back.
+template <int D> struct PrefillCfg;
+template <> struct PrefillCfg<128> { static constexpr int NW = 8, NB = 4; };
+template <> struct PrefillCfg<256> { static constexpr int NW = 4, NB = 2; };
+
+template <typename T, int HPW, int D>
+__global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(PrefillArgs a) {
     typedef typename Mfma<T>::v8 v8;
     typedef typename Mfma<T>::v4 v4;
     typedef short s4 __attribute__((ext_vector_type(4)));
-    constexpr int NW = 8;
+    constexpr int NW = PrefillCfg<D>::NW;
     constexpr int RT = NW / HPW;      // row tiles per workgroup
     constexpr int WROWS = ROWS * RT;  // query rows per workgroup
-    constexpr int NB = 4;             // unit buffers
-    constexpr int KS = D + 8;         // K [key][dim] row stride (elements): 272 B, 17 chunks
-    constexpr int KCH = KS / 8;       // 16-byte chunks per K row
-    constexpr int K_INSTR = BN * KCH / 64;  // 17 direct loads of 1 KB per K tile
+    constexpr int NB = PrefillCfg<D>::NB;  // unit buffers
+    constexpr int NDT = D / 32;       // 32-dim tiles of O^T
+    constexpr int KS = D + 8;         // K [key][dim] row stride (elements): 16 bytes of padding
+    constexpr int KCH = KS / 8;       // 16-byte chunks per K row (17 or 33)
+    constexpr int K_INSTR = BN * KCH / 64;  // direct loads of 1 KB per K tile (17 or 33)
+    constexpr int KJ = (K_INSTR + NW - 1) / NW;  // K loads per wavefront
+    constexpr int V_INSTR = BN * D * 2 / 1024;  // direct loads of 1 KB per V tile (16 or 32)
+    constexpr int VJ = V_INSTR / NW;  // V loads per wavefront
+    constexpr int VRPI = 1024 / (2 * D);  // V rows per load (4 or 2)
+    constexpr int VCPR = D / 8;       // 16-byte chunks per V row (16 or 32)
     // buffer u % NB holds K of tile u ([key][dim], padded rows) and V of tile
-    // u - 1 ([key][dim], 256-byte rows, chunk c of row r at c ^ 4*(r % 4))
+    // u - 1 ([key][dim], 2D-byte rows, chunk c of row r at c ^ 4*(r % 4))
     __shared__ __attribute__((aligned(1024))) T sk[NB][BN * KS];
     __shared__ __attribute__((aligned(1024))) T sv[NB][BN * D];
 
@@ -163,36 +177,47 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
     // M0 (the LDS destination) is a register the compiler reserves, so the
     // assembly saves and restores it around the load.
     auto dma16 = [](const void* src, lds_void* dst) {
-        const unsigned lds = (unsigned)(uintptr_t)dst;
+        unsigned lds = (unsigned)(uintptr_t)dst;
+        if constexpr (D == 256) lds = __builtin_amdgcn_readfirstlane(lds);
         unsigned saved;
         asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\t"
                      "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
                      : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
     };
-    // scalar base + 32-bit lane byte offset form, for the common full tile
+    // scalar base + 32-bit lane byte offset form, for the common full tile.
+    // The base and the LDS address are wave-uniform; at D = 256 the compiler
+    // would otherwise hand the base over in vector registers, so readfirstlane
+    // pins both to scalar registers, as the instruction requires.
     auto dma16s = [](const void* base, unsigned voff, lds_void* dst) {
-        const unsigned lds = (unsigned)(uintptr_t)dst;
+        unsigned lds = (unsigned)(uintptr_t)dst;
+        if constexpr (D == 256) {
+            const uintptr_t bp = (uintptr_t)base;
+            const unsigned blo = __builtin_amdgcn_readfirstlane((unsigned)bp);
+            const unsigned bhi = __builtin_amdgcn_readfirstlane((unsigned)(bp >> 32));
+            base = (const void*)(((uintptr_t)bhi << 32) | blo);
+            lds = __builtin_amdgcn_readfirstlane(lds);
+        }
         unsigned saved;
         asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
                      "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
                      : "=&s"(saved) : "v"(voff), "s"(base), "s"(lds) : "memory");
     };
     // this lane's row and byte offset (within a tile) for each of its loads
-    int k_row[3], v_row[2];
-    unsigned k_off[3], v_off[2];
+    int k_row[KJ], v_row[VJ];
+    unsigned k_off[KJ], v_off[VJ];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < KJ; ++j) {
         const int i = wave + NW * j;
         const int L = 64 * (i < K_INSTR ? i : 0) + lane;
         const int row = L / KCH, ch = L - row * KCH;
         k_row[j] = row;
-        k_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * (ch < 16 ? ch : 0)) * sizeof(T));
+        k_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * (ch < KCH - 1 ? ch : 0)) * sizeof(T));
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int i = 2 * wave + j;
-        const int row = 4 * i + (lane >> 4);
-        const int cc = (lane & 15) ^ (4 * (row & 3));
+    for (int j = 0; j < VJ; ++j) {
+        const int i = VJ * wave + j;
+        const int row = VRPI * i + lane / VCPR;
+        const int cc = (lane % VCPR) ^ (4 * (row & 3));
         v_row[j] = row;
         v_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * cc) * sizeof(T));
     }
@@ -202,13 +227,13 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
         if (k0 + BN <= S) {
             const T* kb = kbase + (size_t)k0 * tok_stride;
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
+            for (int j = 0; j < KJ; ++j) {
                 const int i = wave + NW * j;
                 if (i < K_INSTR) dma16s(kb, k_off[j], (lds_void*)&sk[buf][512 * i]);
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
+            for (int j = 0; j < KJ; ++j) {
                 const int i = wave + NW * j;
                 if (i < K_INSTR) {
                     const int key = min(k0 + k_row[j], S - 1);
@@ -223,14 +248,14 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
             const T* vb = vbase + (size_t)v0 * tok_stride;
             if (v0 + BN <= S) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) dma16s(vb, v_off[j], (lds_void*)&sv[buf][512 * (2 * wave + j)]);
+                for (int j = 0; j < VJ; ++j) dma16s(vb, v_off[j], (lds_void*)&sv[buf][512 * (VJ * wave + j)]);
             } else {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < VJ; ++j) {
                     const int key = min(v0 + v_row[j], S - 1);
                     const T* src = vbase + (size_t)key * tok_stride +
                                    (v_off[j] - (size_t)v_row[j] * tok_stride * sizeof(T)) / sizeof(T);
-                    dma16(src, (lds_void*)&sv[buf][512 * (2 * wave + j)]);
+                    dma16(src, (lds_void*)&sv[buf][512 * (VJ * wave + j)]);
                 }
             }
         }
@@ -261,8 +286,8 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
         voff[dt] = vrow * D + 32 * (dt ^ ((jg >> 2) & 3)) + 8 * vq + 4 * (jg & 1);
-    auto vfrag = [&](int buf, int i) {  // i = 4*ks + dt: keys 16 ks + {4hh..+3, 8+4hh..+3}
-        const int dt = i & 3, ks = i >> 2;
+    auto vfrag = [&](int buf, int i) {  // i = NDT*ks + dt: keys 16 ks + {4hh..+3, 8+4hh..+3}
+        const int dt = i % NDT, ks = i / NDT;
         const lds_ptr base = (lds_ptr)&sv[buf][0] + voff[dt] + (16 * ks) * D;
         const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)base);
         const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(base + 8 * D));
@@ -274,24 +299,26 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
     f32x16 s[2];
     v8 pb[4];  // P^T operand of the tile whose PV is pending
     auto run_pv = [&](int buf) {
+        constexpr int NM = 4 * NDT;  // MFMAs: 4 key steps x NDT dim tiles
         v8 vf[PF];
 #pragma unroll
         for (int i = 0; i < PF; ++i) vf[i] = vfrag(buf, i);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < NM; ++i) {
             const v8 va = vf[i % PF];
-            if (i + PF < 16) vf[i % PF] = vfrag(buf, i + PF);
-            o[i & 3] = Mfma<T>::mma(va, pb[i >> 2], o[i & 3]);
+            if (i + PF < NM) vf[i % PF] = vfrag(buf, i + PF);
+            o[i % NDT] = Mfma<T>::mma(va, pb[i / NDT], o[i % NDT]);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
 #pragma unroll
-        for (int i = 0; i < 16 - PF; ++i) {
+        for (int i = 0; i < NM - PF; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
     };
     auto run_qk = [&](int buf) {
+        constexpr int NM = 2 * (D / 16);  // MFMAs: 2 key halves x D/16 dim steps
         const lds_ptr kt = k_lane + buf * (BN * KS);
         s[0] = f32x16{};
         s[1] = f32x16{};
@@ -299,14 +326,14 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < PF; ++i) kf[i] = kfrag(kt, i);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < NM; ++i) {
             const v8 ka = kf[i % PF];
-            if (i + PF < 16) kf[i % PF] = kfrag(kt, i + PF);
+            if (i + PF < NM) kf[i % PF] = kfrag(kt, i + PF);
             s[i & 1] = Mfma<T>::mma(ka, qr[i >> 1], s[i & 1]);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
 #pragma unroll
-        for (int i = 0; i < 16 - PF; ++i) {
+        for (int i = 0; i < NM - PF; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
@@ -354,22 +381,6 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
     if (n_tiles >= 1) issue_unit(1);
     __builtin_amdgcn_s_waitcnt(0);  // all counters (Q loads, units 0 and 1)
     barrier();
-    const int nl = (wave == 0 ? 3 : 2) + 2;  // this wave's loads per unit (K + V)
-    // Wait until this wave's loads of unit u are complete while its loads of
-    // the next `ahead` units (0, 1 or 2) may still be in flight.
-    // vmcnt(n) on gfx9: bits 3:0 and 15:14; expcnt 6:4 = 7; lgkmcnt 11:8 = 15
-    auto wait_unit = [&](int ahead) {
-        if (ahead == 2) {
-            if (nl == 5) __builtin_amdgcn_s_waitcnt(0x0F7A);
-            else __builtin_amdgcn_s_waitcnt(0x0F78);
-        } else if (ahead == 1) {
-            if (nl == 5) __builtin_amdgcn_s_waitcnt(0x0F75);
-            else __builtin_amdgcn_s_waitcnt(0x0F74);
-        } else {
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-        }
-    };
-    auto ahead_of = [&](int u) { return min(2, max(0, n_tiles - u)); };
     // The MFMA phase runs at a raised wave priority so that its MFMA and LDS
     // issues win over the other wave's softmax VALU stream on the same SIMD.
     auto mfma_phase = [&](int t) {
@@ -380,36 +391,63 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
         if (qk) run_qk(t % NB);
         __builtin_amdgcn_s_setprio(0);
     };
-    // One barrier per tile step t = 0 .. n_tiles.  Lead waves: MFMA phase of
-    // tile t, then the softmax of tile t; lag waves: the softmax of tile t-1,
-    // then the MFMA phase of tile t.  So each SIMD's two wavefronts alternate
-    // phases inside the step.  Each wave issues its loads of unit t+3 in step
-    // t (unit t-1, the buffer's previous occupant, was last read in step t-1)
-    // and waits for unit t+1 before the barrier.
-    // One barrier per tile step t = 0 .. n_tiles.  Lead waves (0-3): the
-    // MFMA phase of tile t, then the softmax of tile t; lag waves (4-7): the
-    // softmax of tile t-1, then the MFMA phase of tile t; so the two
-    // wavefronts of each SIMD alternate phases inside a step.  Each wave
-    // issues its loads of unit t+3 in step t (the buffer's previous unit, t-1,
-    // was last read in step t-1) and waits for unit t+1 before the barrier.
-    if (2 <= n_tiles) issue_unit(2);
-    if (wave < NW / 2) {
-        for (int t = 0; t <= n_tiles; ++t) {
-            mfma_phase(t);
-            if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
-            if (t + 3 <= n_tiles) issue_unit(t + 3);
-            if (t < n_tiles) {
-                wait_unit(ahead_of(t + 1));
-                barrier();
+    if constexpr (NW == 8) {
+        const int nl = (wave == 0 ? 3 : 2) + 2;  // this wave's loads per unit (K + V)
+        // Wait until this wave's loads of unit u are complete while its loads of
+        // the next `ahead` units (0, 1 or 2) may still be in flight.
+        // vmcnt(n) on gfx9: bits 3:0 and 15:14; expcnt 6:4 = 7; lgkmcnt 11:8 = 15
+        auto wait_unit = [&](int ahead) {
+            if (ahead == 2) {
+                if (nl == 5) __builtin_amdgcn_s_waitcnt(0x0F7A);
+                else __builtin_amdgcn_s_waitcnt(0x0F78);
+            } else if (ahead == 1) {
+                if (nl == 5) __builtin_amdgcn_s_waitcnt(0x0F75);
+                else __builtin_amdgcn_s_waitcnt(0x0F74);
+            } else {
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+            }
+        };
+        auto ahead_of = [&](int u) { return min(2, max(0, n_tiles - u)); };
+        // One barrier per tile step t = 0 .. n_tiles.  Lead waves (0-3): the
+        // MFMA phase of tile t, then the softmax of tile t; lag waves (4-7): the
+        // softmax of tile t-1, then the MFMA phase of tile t; so the two
+        // wavefronts of each SIMD alternate phases inside a step.  Each wave
+        // issues its loads of unit t+3 in step t (the buffer's previous unit,
+        // t-1, was last read in step t-1) and waits for unit t+1 before the
+        // barrier.
+        if (2 <= n_tiles) issue_unit(2);
+        if (wave < NW / 2) {
+            for (int t = 0; t <= n_tiles; ++t) {
+                mfma_phase(t);
+                if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
+                if (t + 3 <= n_tiles) issue_unit(t + 3);
+                if (t < n_tiles) {
+                    wait_unit(ahead_of(t + 1));
+                    barrier();
+                }
+            }
+        } else {
+            for (int t = 0; t <= n_tiles; ++t) {
+                if (t >= 1 && t - 1 < w_tiles) phase_softmax(t - 1, t - 1 == w_tiles - 1 && last_masked);
+                if (t + 3 <= n_tiles) issue_unit(t + 3);
+                mfma_phase(t);
+                if (t < n_tiles) {
+                    wait_unit(ahead_of(t + 1));
+                    barrier();
+                }
             }
         }
     } else {
+        // One wavefront per SIMD and two buffers: in step t each wave issues
+        // its loads of unit t+1 (the buffer's previous unit, t-1, was last read
+        // in step t-1), runs the MFMA phase and the softmax of tile t, and
+        // waits for unit t+1 before the barrier.
         for (int t = 0; t <= n_tiles; ++t) {
-            if (t >= 1 && t - 1 < w_tiles) phase_softmax(t - 1, t - 1 == w_tiles - 1 && last_masked);
-            if (t + 3 <= n_tiles) issue_unit(t + 3);
+            if (t >= 1 && t + 1 <= n_tiles) issue_unit(t + 1);
             mfma_phase(t);
+            if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
             if (t < n_tiles) {
-                wait_unit(ahead_of(t + 1));
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
                 barrier();
             }
         }
@@ -431,11 +469,38 @@ __global__ __launch_bounds__(512, 1) void prefill_fa_kernel(PrefillArgs a) {
 
 }  // namespace
 
+namespace {
+template <int D>
+void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int batch, bool bf,
+              hipStream_t s) {
+    constexpr int NW = PrefillCfg<D>::NW;
+    // x = workgroup's head set (fastest), y = query block (reversed in the
+    // kernel so the heaviest blocks go first); with x = KV head and
+    // round-robin dispatch over the 8 XCDs, a KV head's K/V stays in one L2.
+    const int rows = ROWS * NW / hpw;
+    const dim3 grid(n_kv_heads * (a.group / hpw), (seq_len + rows - 1) / rows, batch);
+    const dim3 block(64 * NW);
+    switch (hpw) {
+        case 4:
+            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 4, D>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 4, D>), grid, block, 0, s, a);
+            break;
+        case 2:
+            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 2, D>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 2, D>), grid, block, 0, s, a);
+            break;
+        default:
+            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 1, D>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 1, D>), grid, block, 0, s, a);
+    }
+}
+}  // namespace
+
 hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
                           int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
                           int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale,
                           float* out, hipStream_t s) {
-    if (head_dim != D) return hipErrorInvalidValue;
+    if (head_dim != 128 && head_dim != 256) return hipErrorInvalidValue;
     PrefillArgs a;
     a.q = q;
     a.k = k;
@@ -448,26 +513,10 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     a.causal = causal;
     a.gqa_mode = gqa_mode;
     a.qk_scale = scale * kLog2e;
-    // x = workgroup's head set (fastest), y = query block (reversed in the
-    // kernel so the heaviest blocks go first); with x = KV head and
-    // round-robin dispatch over the 8 XCDs, a KV head's K/V stays in one L2.
     const int hpw = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
-    const int rows = ROWS * 8 / hpw;
-    const dim3 grid(n_kv_heads * (a.group / hpw), (seq_len + rows - 1) / rows, batch);
     const bool bf = dtype == 2;
-    switch (hpw) {
-        case 4:
-            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 4>), grid, dim3(512), 0, s, a);
-            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 4>), grid, dim3(512), 0, s, a);
-            break;
-        case 2:
-            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 2>), grid, dim3(512), 0, s, a);
-            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 2>), grid, dim3(512), 0, s, a);
-            break;
-        default:
-            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 1>), grid, dim3(512), 0, s, a);
-            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 1>), grid, dim3(512), 0, s, a);
-    }
+    if (head_dim == 128) launch_d<128>(a, hpw, n_kv_heads, seq_len, batch, bf, s);
+    else launch_d<256>(a, hpw, n_kv_heads, seq_len, batch, bf, s);
     return hipGetLastError();
 }
 

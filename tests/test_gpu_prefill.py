@@ -118,3 +118,26 @@ def test_prefill_batch_of_two(causal):
             qf, kf, vf = (t.float().numpy() for t in (tq, tk, tv))
             ref = np.stack([ref64.attention(qf[i], kf, vf, lambda h: h % 8) for i in range(200)])
         assert row_rel_err(out[bi], ref) <= 1e-2, bi
+
+
+@pytest.mark.parametrize("s,dtype", [(1, torch.bfloat16), (70, torch.bfloat16),
+                                     (300, torch.float16), (700, torch.bfloat16)])
+def test_prefill_head_dim_256(s, dtype):
+    """head_dim 256 (config 4's 16 q / 2 kv heads, the Qwen3.5 full-attention layers):
+    every row against the oracle's per-row decode."""
+    rng = np.random.default_rng(200 + s)
+    tq, tk, tv = _inputs(rng, s, 16, 2, 256, dtype=dtype)
+    out = _run(tq, tk, tv)
+    ref = _oracle_rows(tq, tk, tv, range(s))
+    assert row_rel_err(out, ref) <= 1e-2
+    n, mism, ties = argmax_agreement(out, ref)
+    assert mism == 0
+
+
+def test_prefill_head_dim_256_noncausal_grouped_vs_f64():
+    rng = np.random.default_rng(23)
+    tq, tk, tv = _inputs(rng, 150, 8, 2, 256)
+    qf, kf, vf = (t.float().numpy() for t in (tq, tk, tv))
+    out = _run(tq, tk, tv, causal=False, gqa_mode=1)
+    ref = np.stack([ref64.attention(qf[i], kf, vf, lambda h: h // 4) for i in range(150)])
+    assert row_rel_err(out, ref) <= 1e-2
