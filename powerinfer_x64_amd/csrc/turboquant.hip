@@ -181,31 +181,82 @@ __global__ __launch_bounds__(256) void tq_read_kernel(TqPool t, const int32_t* _
 
 // Virtual query of (sequence b, query head h) (precompute_query,
 // :244-278): [R.q / sqrt(d) | corr * G.(R.q) / sqrt(d)], corr =
-// residual_norm * qjl_scale of the 3-bit estimator (:297-316).  One
-// workgroup of 128 threads per row; thread i owns output i (the matrices are
-// stored transposed, so the reads of a row step are coalesced).
-__global__ __launch_bounds__(128) void tq_query_kernel(TqPool t, const float* __restrict__ q,
+// residual_norm * qjl_scale of the 3-bit estimator (:297-316).
+//
+// One workgroup of 256 threads per (sequence, KV head, chunk of up to
+// kQueryHeads query heads of that KV head): every matrix element read from
+// L2 serves all heads of the chunk.  Thread (half, i) owns output column i
+// and sums rows j of its half (the matrices are stored transposed, so a row
+// step reads 512 contiguous bytes per wavefront); the two halves meet in
+// LDS.  The queries sit in LDS as [row][head], one 16-byte read per row.
+constexpr int kQueryHeads = 4;
+
+__global__ __launch_bounds__(256) void tq_query_kernel(TqPool t, const float* __restrict__ q,
                                                        float* __restrict__ qv, int n_q_heads,
                                                        int gqa_mode) {
-    __shared__ float s_q[TD], s_r[TD];
-    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    __shared__ float4 s_x[TD];                    // query (pass 1) or R.q (pass 2), [row][head]
+    __shared__ float s_part[2][kQueryHeads][TD];  // per-half partial sums
     const int n_kv = t.g.n_kv_heads;
     const int group = n_q_heads / n_kv;
-    const int kvh = gqa_mode == 0 ? h % n_kv : h / group;
-    const size_t r = (size_t)b * n_q_heads + h;
-    s_q[i] = q[r * TD + i];
+    const int n_chunks = (group + kQueryHeads - 1) / kQueryHeads;
+    const int kvh = blockIdx.x / n_chunks, c0 = (blockIdx.x % n_chunks) * kQueryHeads;
+    const int nh = min(kQueryHeads, group - c0);
+    const int b = blockIdx.y, tid = threadIdx.x, half = tid >> 7, i = tid & (TD - 1);
+    auto head_of = [&](int k) { return gqa_mode == 0 ? kvh + (c0 + k) * n_kv : kvh * group + c0 + k; };
+
+    // stage the chunk's queries: thread (half, i) loads heads 2*half, 2*half + 1 of row i
+    float* sx = reinterpret_cast<float*>(s_x);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        const int k = 2 * half + kk;
+        sx[i * kQueryHeads + k] = k < nh ? q[((size_t)b * n_q_heads + head_of(k)) * TD + i] : 0.f;
+    }
     __syncthreads();
-    const float* rt = t.rt + (size_t)kvh * TD * TD;
-    float a = 0.f;
-    for (int j = 0; j < TD; ++j) a += rt[j * TD + i] * s_q[j];
-    s_r[i] = a;
-    __syncthreads();
-    const float* gt = t.gt + (size_t)kvh * TD * TD;
-    float p = 0.f;
-    for (int j = 0; j < TD; ++j) p += gt[j * TD + i] * s_r[j];
+
     const float inv = 1.0f / t.scale;
-    qv[r * 2 * TD + i] = a * inv;
-    qv[r * 2 * TD + TD + i] = t.corr * (p * inv);
+    float r_own[2] = {0.f, 0.f};  // R.q of (head 2*half + kk, column i), kept for the output
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const float* mt = (pass == 0 ? t.rt : t.gt) + (size_t)kvh * TD * TD + (size_t)half * (TD / 2) * TD + i;
+        const float4* xs = s_x + half * (TD / 2);
+        float acc[kQueryHeads] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 16
+        for (int j = 0; j < TD / 2; ++j) {
+            const float m = mt[(size_t)j * TD];
+            const float4 x = xs[j];
+            acc[0] = fmaf(m, x.x, acc[0]);
+            acc[1] = fmaf(m, x.y, acc[1]);
+            acc[2] = fmaf(m, x.z, acc[2]);
+            acc[3] = fmaf(m, x.w, acc[3]);
+        }
+#pragma unroll
+        for (int k = 0; k < kQueryHeads; ++k) s_part[half][k][i] = acc[k];
+        __syncthreads();
+        // thread (half, i) finishes heads 2*half, 2*half + 1 of column i
+        float out[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int k = 2 * half + kk;
+            out[kk] = s_part[0][k][i] + s_part[1][k][i];
+        }
+        if (pass == 0) {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                r_own[kk] = out[kk];
+                sx[i * kQueryHeads + 2 * half + kk] = out[kk];  // every read of pass 0 ended at the barrier
+            }
+            __syncthreads();
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int k = 2 * half + kk;
+                if (k >= nh) continue;
+                float* row = qv + ((size_t)b * n_q_heads + head_of(k)) * 2 * TD;
+                row[i] = r_own[kk] * inv;
+                row[TD + i] = t.corr * (out[kk] * inv);
+            }
+        }
+    }
 }
 
 }  // namespace
@@ -236,8 +287,10 @@ hipError_t launch_tq_read(const TqPool& t, const int32_t* page_table, int32_t ma
 hipError_t launch_tq_query(const TqPool& t, const float* q, float* qv, int32_t batch,
                            int32_t n_q_heads, int32_t gqa_mode, hipStream_t s) {
     if (batch <= 0) return hipSuccess;
-    hipLaunchKernelGGL(tq_query_kernel, dim3(n_q_heads, batch), dim3(TD), 0, s, t, q, qv,
-                       n_q_heads, gqa_mode);
+    const int group = n_q_heads / t.g.n_kv_heads;
+    const int n_chunks = (group + kQueryHeads - 1) / kQueryHeads;
+    hipLaunchKernelGGL(tq_query_kernel, dim3(t.g.n_kv_heads * n_chunks, batch), dim3(256), 0, s, t,
+                       q, qv, n_q_heads, gqa_mode);
     return hipGetLastError();
 }
 

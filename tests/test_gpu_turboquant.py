@@ -119,12 +119,13 @@ def test_append_in_chunks_and_edge_keys():
         _check_records(case, i)
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (12, 2), (3, 3)])
 @pytest.mark.parametrize("gqa_mode", [0, 1])
-def test_decode_matches_oracle_ragged(gqa_mode):
+def test_decode_matches_oracle_ragged(gqa_mode, hq, hkv):
+    """Groups of 4, 6 (a full and a partial chunk of the query precompute) and 1."""
     dev = device()
-    rng = np.random.default_rng(0x70C2 + gqa_mode)
+    rng = np.random.default_rng(0x70C2 + gqa_mode + 16 * hq)
     lens = [1, 16, 200, 1000, 37]
-    hq, hkv = 8, 2
     case = TqCase(rng, lens, hkv)
     case.build(dev)
     q = rng.standard_normal((len(lens), hq, D)).astype(np.float32) * 2
