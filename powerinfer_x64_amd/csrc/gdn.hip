@@ -573,20 +573,20 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             doff[j] = (unsigned)(((r >> 6) * GC * GC + rr * GC + 8 * c) * 2);
         }
     }
+    // A wave's 8 loads all come from one tile (lw / 2: q, k, T pair, M pair),
+    // so the source and LDS bases are picked once per call (wave-uniform
+    // selects) and the loads issue back to back, without branches between.
+    const int ltile = lw >> 1;
     auto issue = [&](int n) {
         const int b = n & 1;
         const size_t qb = ((size_t)n * hk + kh) * GC * DK;
         const size_t tb = ((size_t)n * hv + vh) * GC * GC * 2;  // f16 elements of a T / M pair
         const f16* tm = reinterpret_cast<const f16*>(w.tm);
         const f16* mm = reinterpret_cast<const f16*>(w.mm);
+        const f16* src = ltile == 0 ? w.q16 + qb : ltile == 1 ? w.k16 + qb : ltile == 2 ? tm + tb : mm + tb;
+        f16* dst = ltile == 0 ? sq_[b] : ltile == 1 ? sk_[b] : ltile == 2 ? st_[b] : sm_[b];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = 8 * lw + j, ti = i & 15;
-            if (i < 16) dma16s(w.q16 + qb, doff[j], (lds_void*)&sq_[b][512 * ti]);
-            else if (i < 32) dma16s(w.k16 + qb, doff[j], (lds_void*)&sk_[b][512 * ti]);
-            else if (i < 48) dma16s(tm + tb, doff[j], (lds_void*)&st_[b][512 * ti]);
-            else dma16s(mm + tb, doff[j], (lds_void*)&sm_[b][512 * ti]);
-        }
+        for (int j = 0; j < 8; ++j) dma16s(src, doff[j], (lds_void*)&dst[512 * ((8 * (lw & 1)) + j)]);
     };
     // V tile (K-side waves, MFMA C layout: rows 16 rb + 4 g4 + r, column ln), lg and beta
     float pv[4], plg = 0.f, plc = 0.f, pb = 0.f;
