@@ -664,6 +664,17 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     };
 
     float vcur[4] = {0.f, 0.f, 0.f, 0.f};
+    // O of the previous chunk (Q-side waves): stored in the next chunk's
+    // phase 2, where these waves only issue their loads, instead of in phase
+    // 3 beside the K side's loads
+    float opend[4] = {0.f, 0.f, 0.f, 0.f};
+    auto store_o = [&](int tp) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = tp + 16 * rb + 4 * g4 + r;
+            if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = opend[r];
+        }
+    };
     issue(0);
     fetch_small(0);
     __builtin_amdgcn_s_waitcnt(0);
@@ -704,6 +715,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         }
         __syncthreads();
         if (!kside && n + 1 < n_chunks) issue(n + 1);
+        if (!kside && n >= 1) store_o(t0 - GC);
         // phase 2: Delta = T R (T lower triangular: column blocks <= rb)
         if (kside) {
             const f32x4 dl = mm_split_sw(st_[cb], st_[cb] + GC * GC, srth, srtl, 16 * rb, (rb >> 1) + 1);
@@ -729,11 +741,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         if (!kside) {
             const f32x4 o = mm_split_sw(sm_[cb], sm_[cb] + GC * GC, sdth, sdtl, 16 * rb, (rb >> 1) + 1);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 16 * rb + 4 * g4 + r;
-                const int t = t0 + i;
-                if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = sgam[cb][i] * xs[r] + o[r];
-            }
+            for (int r = 0; r < 4; ++r) opend[r] = sgam[cb][16 * rb + 4 * g4 + r] * xs[r] + o[r];
         }
         // phase 3b: S'^T = exp(lgC) S^T + Dp^T K for state rows row0 .. row0 + 15
         {
@@ -758,6 +766,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         }
         __syncthreads();
     }
+    if (!kside && n_chunks >= 1) store_o((n_chunks - 1) * GC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) S[(size_t)(row0 + ln) * DV + c0 + 4 * g4 + r] = sv[r];
 }
