@@ -284,37 +284,44 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
     __shared__ float slg[2][GC], sb[2][GC];
     float* sk = s_big;
     float* sq = s_big + GC * KS_;
-    const int n = blockIdx.x, kh = blockIdx.y;
-    const int t0 = n * GC;
+    const int kh = blockIdx.y;
+    const int n_chunks = (n_tok + GC - 1) / GC;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-    // g and beta of the first V-head pair, fetched early (their latency
-    // hides under the q / k loads): waves 0 and 4, lane = token of the chunk
     const int half = wave >> 2, wl = wave & 3, ht = tid & 255;
-    float g_pre = 0.f, b_pre = 0.f;
-    {
-        const int vh = kh + half * hk, t = min(t0 + lane, n_tok - 1);
+
+    // The workgroup walks chunks blockIdx.x, + gridDim.x, ... of its K head.
+    // The next chunk's raw q / k rows (thread t: 16 values of row t / 8,
+    // pieces (t % 8) + 8 j) and the g, beta of its first V-head pair (waves 0
+    // and 4, lane = token) are loaded into registers while this chunk
+    // computes, so their latency hides under the compute.
+    const int row = tid >> 3, part = tid & 7;
+    f32x4 a[4], b[4];
+    float g_nx = 0.f, b_nx = 0.f;
+    auto fetch = [&](int n) {
+        const int t0 = n * GC;
+        const int vh = kh + half * hk, tg = min(t0 + lane, n_tok - 1);
         if (wl == 0 && vh < hv) {
-            g_pre = g[(size_t)t * hv + vh];
-            b_pre = beta[(size_t)t * hv + vh];
+            g_nx = g[(size_t)tg * hv + vh];
+            b_nx = beta[(size_t)tg * hv + vh];
         }
-    }
-    // raw rows of the K head, L2-normalised on the way in (src/model/mod.rs:
-    // 860-875): thread t owns 16 values of row t / 8 (pieces (t % 8) + 8 j);
-    // the row sums reduce over 8 lanes.  Rows past the prompt are zero (their
-    // inverse norm is then irrelevant).  The normalised rows go to LDS in f32
-    // and to the workspace in f16 for the scan.
-    {
-        const int row = tid >> 3, part = tid & 7;
-        const int t = t0 + row;
-        const bool ok = t < n_tok;
-        const size_t src = ((size_t)min(t, n_tok - 1) * hk + kh) * DK;
-        f32x4 a[4], b[4];
+        const size_t src = ((size_t)min(t0 + row, n_tok - 1) * hk + kh) * DK;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             a[j] = *reinterpret_cast<const f32x4*>(q + src + 4 * (part + 8 * j));
             b[j] = *reinterpret_cast<const f32x4*>(k + src + 4 * (part + 8 * j));
         }
+    };
+    fetch(blockIdx.x);
+    for (int n = blockIdx.x; n < n_chunks; n += gridDim.x) {
+    const int t0 = n * GC;
+    float g_pre = g_nx, b_pre = b_nx;
+    // raw rows of the K head, L2-normalised on the way in (src/model/mod.rs:
+    // 860-875); the row sums reduce over 8 lanes.  Rows past the prompt are
+    // zero (their inverse norm is then irrelevant).  The normalised rows go
+    // to LDS in f32 and to the workspace in f16 for the scan.
+    {
+        const int t = t0 + row;
+        const bool ok = t < n_tok;
         float ssq = 0.f, ssk = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -343,6 +350,7 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
                 f16x4{to_f16(y[0]), to_f16(y[1]), to_f16(y[2]), to_f16(y[3])};
         }
     }
+    if (n + (int)gridDim.x < n_chunks) fetch(n + gridDim.x);
     __syncthreads();
     // lower-triangular 16x16 tiles: 10 of K K^T, then 10 of Q K^T
     const int ln = lane & 15, lg4 = lane >> 4;
@@ -467,6 +475,7 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
         }
         __syncthreads();  // A, T and the scratch are rewritten for the next V heads
     }
+    }  // chunks
 }
 
 // gdn_scan_kernel: 8 wavefronts walk the chunks in order for one (V head, 16
@@ -839,7 +848,13 @@ hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, co
     w.tm = reinterpret_cast<float*>(w.k16 + qk);
     w.mm = w.tm + nc * n_v_heads * GC * GC;
     w.lg = w.mm + nc * n_v_heads * GC * GC;
-    hipLaunchKernelGGL(gdn_prep_kernel, dim3((unsigned)nc, n_k_heads), dim3(512), 0, s, q, k, beta, g,
+    // about one prep workgroup per CU: each walks nc / grid chunks of its K head
+    int dev = 0, n_cu = 0;
+    hipError_t e0 = hipGetDevice(&dev);
+    if (e0 == hipSuccess) e0 = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e0 != hipSuccess) return e0;
+    const unsigned gx = (unsigned)std::max<size_t>(1, std::min<size_t>(nc, (size_t)n_cu / n_k_heads));
+    hipLaunchKernelGGL(gdn_prep_kernel, dim3(gx, n_k_heads), dim3(512), 0, s, q, k, beta, g,
                        n_tok, n_k_heads, n_v_heads, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -106,9 +106,11 @@ def _check(out, ref_out, state, ref_state, tol=2e-3):
     assert es <= tol, f"state max-abs {es}"
 
 
-@pytest.mark.parametrize("t", [1, 63, 64, 65, 200, 1024])
+@pytest.mark.parametrize("t", [1, 63, 64, 65, 200, 1024, 1130])
 def test_gdn_prefill_matches_oracle(t):
-    """Chunked (64-token) prefill == the reference's per-token recurrence."""
+    """Chunked (64-token) prefill == the reference's per-token recurrence.  t = 1130 gives
+    18 chunks, more than one per prep workgroup on a 256-CU device (16 K heads), with the
+    ragged tail on a workgroup's second chunk."""
     rt = _rt()
     dev = device()
     rng = np.random.default_rng(1000 + t)
