@@ -217,32 +217,22 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict
 //   S' = exp(lg_C) S + K^T diag(exp(lg_C - lg_i)) Delta
 // gdn_prep_kernel (parallel over chunks x K heads) builds T = (I + A)^-1, M,
 // lg and the q/k inverse norms; gdn_scan_kernel walks the chunks in order for
-// one (V head, 16 state columns) with the state tile in LDS.  Matrix products
-// use the f32 MFMA (v_mfma_f32_16x16x4f32).
+// one (V head, 16 state columns) with the state tile in LDS.  The prep's
+// K K^T and Q K^T tiles run on the f16 MFMA over hi + lo parts, its 16x16
+// inverse blocks on the f32 MFMA (v_mfma_f32_16x16x4f32).
 // ---------------------------------------------------------------------------
 constexpr int GC = 64;          // chunk length
 constexpr int KS_ = DK + 4;     // LDS row stride of [64][128] tiles
 constexpr int TS_ = GC + 4;     // LDS row stride of [64][64] / [16][64] tiles
 constexpr int SCOLS = 16;       // state columns per scan workgroup
+constexpr int KH_ = DK + 8;     // f16 row stride of [rows][128] f16 tiles (272 B)
+
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-// acc += X[row0 + (l%16)][k] * Yt[col0 + (l%16)][k] summed over k < 16*ns.
-// Lane (l%16, g = l/16) reads 4 consecutive k per operand (k = 16s + 4g + r).
-__device__ __forceinline__ f32x4 tile_mm(const float* X, int xs, int row0, const float* Yt,
-                                         int ys, int col0, int ns, f32x4 acc) {
-    const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
-    for (int s = 0; s < ns; ++s) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(X + (row0 + i) * xs + 16 * s + 4 * g);
-        const f32x4 y = *reinterpret_cast<const f32x4*>(Yt + (col0 + i) * ys + 16 * s + 4 * g);
-        acc = mfma4(x[0], y[0], acc);
-        acc = mfma4(x[1], y[1], acc);
-        acc = mfma4(x[2], y[2], acc);
-        acc = mfma4(x[3], y[3], acc);
-    }
-    return acc;
 }
 
 // C += X . Y for 16x16 f32 blocks in LDS (row-major, strides xs / ys).  Lane
@@ -282,8 +272,13 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
     __shared__ __attribute__((aligned(16))) float skk[GC * TS_];  // K K^T (lower tiles)
     __shared__ __attribute__((aligned(16))) float sqk[GC * TS_];  // Q K^T (lower tiles)
     __shared__ float slg[2][GC], sb[2][GC];
-    float* sk = s_big;
-    float* sq = s_big + GC * KS_;
+    // phase A: the normalised k / q rows as f16 hi + lo parts (row stride KH_
+    // halves, 272 bytes: conflict-free 16-byte reads down 16 rows)
+    f16* skh = reinterpret_cast<f16*>(s_big);
+    f16* skl = skh + GC * KH_;
+    f16* sqh = skl + GC * KH_;
+    f16* sql = sqh + GC * KH_;
+    static_assert(4 * GC * KH_ * 2 <= BIG * 4, "phase A tiles fit s_big");
     const int kh = blockIdx.y;
     const int n_chunks = (n_tok + GC - 1) / GC;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -342,8 +337,18 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
         for (int j = 0; j < 4; ++j) {
             const int c = 4 * (part + 8 * j);
             const f32x4 x = a[j] * iq, y = b[j] * ik;
-            *reinterpret_cast<f32x4*>(sq + row * KS_ + c) = x;
-            *reinterpret_cast<f32x4*>(sk + row * KS_ + c) = y;
+            f16x4 xh, xl, yh, yl;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xh[e] = to_f16(x[e]);
+                xl[e] = to_f16(x[e] - (float)xh[e]);
+                yh[e] = to_f16(y[e]);
+                yl[e] = to_f16(y[e] - (float)yh[e]);
+            }
+            *reinterpret_cast<f16x4*>(sqh + row * KH_ + c) = xh;
+            *reinterpret_cast<f16x4*>(sql + row * KH_ + c) = xl;
+            *reinterpret_cast<f16x4*>(skh + row * KH_ + c) = yh;
+            *reinterpret_cast<f16x4*>(skl + row * KH_ + c) = yl;
             *reinterpret_cast<f16x4*>(w.q16 + base + c) =
                 f16x4{to_f16(x[0]), to_f16(x[1]), to_f16(x[2]), to_f16(x[3])};
             *reinterpret_cast<f16x4*>(w.k16 + base + c) =
@@ -358,8 +363,23 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
         const bool isq = tix >= 10;
         int ib = 0, jb = isq ? tix - 10 : tix;
         while (jb > ib) { jb -= ib + 1; ++ib; }  // enumerate (ib, jb), jb <= ib
+        // C = X Y^T over the 128 dims with v_mfma_f32_16x16x32_f16 on hi / lo
+        // parts (hi.hi + hi.lo + lo.hi; the lo.lo term is below f32 rounding)
+        const f16* xh = (isq ? sqh : skh) + (16 * ib + ln) * KH_ + 8 * lg4;
+        const f16* xl = (isq ? sql : skl) + (16 * ib + ln) * KH_ + 8 * lg4;
+        const f16* yh = skh + (16 * jb + ln) * KH_ + 8 * lg4;
+        const f16* yl = skl + (16 * jb + ln) * KH_ + 8 * lg4;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = tile_mm(isq ? sq : sk, KS_, 16 * ib, sk, KS_, 16 * jb, DK / 16, acc);
+#pragma unroll
+        for (int kb = 0; kb < DK / 32; ++kb) {
+            const f16x8 ah = *reinterpret_cast<const f16x8*>(xh + 32 * kb);
+            const f16x8 al = *reinterpret_cast<const f16x8*>(xl + 32 * kb);
+            const f16x8 bh = *reinterpret_cast<const f16x8*>(yh + 32 * kb);
+            const f16x8 bl = *reinterpret_cast<const f16x8*>(yl + 32 * kb);
+            acc = mfma16(ah, bh, acc);
+            acc = mfma16(ah, bl, acc);
+            acc = mfma16(al, bh, acc);
+        }
         float* dst = isq ? sqk : skk;
 #pragma unroll
         for (int r = 0; r < 4; ++r) dst[(16 * ib + 4 * lg4 + r) * TS_ + 16 * jb + ln] = acc[r];
@@ -496,11 +516,6 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
 // wait (Q side in phase 2, K side in phase 3); K^T comes from transposing
 // reads of the k tile.  The small per-chunk loads are unmasked (clamped), so
 // no compiler-inserted wait lands inside a phase.
-__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-constexpr int KH_ = DK + 8;  // f16 row stride of the [16][128] S^T tiles (272 B)
 constexpr int KT_ = GC + 8;  // f16 row stride of the [16][64] R^T, Delta^T tiles (144 B)
 
 __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__ q,
