@@ -601,7 +601,7 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     // so the source and LDS bases are picked once per call (wave-uniform
     // selects) and the loads issue back to back, without branches between.
     const int ltile = lw >> 1;
-    auto issue = [&](int n) {
+    auto issue = [&](int n, int j0 = 0, int j1 = 8) {
         const int b = n & 1;
         const size_t qb = ((size_t)n * hk + kh) * GC * DK;
         const size_t tb = ((size_t)n * hv + vh) * GC * GC * 2;  // f16 elements of a T / M pair
@@ -610,7 +610,8 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         const f16* src = ltile == 0 ? w.q16 + qb : ltile == 1 ? w.k16 + qb : ltile == 2 ? tm + tb : mm + tb;
         f16* dst = ltile == 0 ? sq_[b] : ltile == 1 ? sk_[b] : ltile == 2 ? st_[b] : sm_[b];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dma16s(src, doff[j], (lds_void*)&dst[512 * ((8 * (lw & 1)) + j)]);
+        for (int j = 0; j < 8; ++j)
+            if (j >= j0 && j < j1) dma16s(src, doff[j], (lds_void*)&dst[512 * ((8 * (lw & 1)) + j)]);
     };
     // V tile (K-side waves, MFMA C layout: rows 16 rb + 4 g4 + r, column ln), lg and beta
     float pv[4], plg = 0.f, plc = 0.f, pb = 0.f;
@@ -757,10 +758,13 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             *reinterpret_cast<f16x4*>(sdtl + ln * KT_ + 16 * rb + 4 * g4) = dlo;
             *reinterpret_cast<f16x4*>(sdph + ln * KT_ + 16 * rb + 4 * g4) = ph;
             *reinterpret_cast<f16x4*>(sdpl + ln * KT_ + 16 * rb + 4 * g4) = pl;
+            // chunk n+1's tiles go to the other buffer (last read in chunk
+            // n-1): the K side issues 3 of its 8 loads here, where it
+            // finishes phase 2 before the Q side, and the rest in phase 3
+            if (n + 1 < n_chunks) issue(n + 1, 0, 3);
         }
         __syncthreads();
-        // chunk n+1's tiles go to the other buffer (last read in chunk n-1)
-        if (kside && n + 1 < n_chunks) issue(n + 1);
+        if (kside && n + 1 < n_chunks) issue(n + 1, 3, 8);
         // phase 3a: O = gamma QS + M Delta (waves 4-7)
         if (!kside) {
             const f32x4 o = mm_split_sw(sm_[cb], sm_[cb] + GC * GC, sdth, sdtl, 16 * rb, (rb >> 1) + 1);
