@@ -124,6 +124,27 @@ def test_gdn_prefill_matches_oracle(t):
     _check(out.cpu().numpy(), ref_out, state.cpu().numpy(), ref_state)
 
 
+@pytest.mark.parametrize("hk,hv,t", [(32, 32, 1250), (4, 12, 300)])
+def test_gdn_prefill_other_head_counts(hk, hv, t):
+    """Other K/V head tilings (vh % hk): 32 K heads with one V head each (the prep's second
+    V-head half is idle, and on a 256-CU device each prep workgroup walks 3 chunks with the
+    ragged tail on the last), and 4 K heads with 3 V heads each (two V-head passes)."""
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(5000 + hk + t)
+    q = rng.standard_normal((t, hk, DK)).astype(np.float32)
+    k = rng.standard_normal((t, hk, DK)).astype(np.float32)
+    v = rng.standard_normal((t, hv, DV)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((t, hv))))).astype(np.float32)
+    g = (-np.log1p(np.exp(rng.standard_normal((t, hv))))).astype(np.float32)
+    s0 = (0.2 * rng.standard_normal((hv, DK, DV))).astype(np.float32)
+    ref_out, ref_state = orc.gdn_tokens(q, k, v, beta, g, state=s0)
+    state = to_dev(s0)
+    out = rt.gdn_prefill(dev, to_dev(q), to_dev(k), to_dev(v), to_dev(beta), to_dev(g), state)
+    torch.cuda.synchronize()
+    _check(out.cpu().numpy(), ref_out, state.cpu().numpy(), ref_state)
+
+
 def test_gdn_prefill_strong_decay_and_zero_beta():
     """Edge gates: g -> -1e4 (state reset each token) and beta = 0 (pure decay)."""
     rt = _rt()
