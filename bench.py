@@ -50,7 +50,8 @@ def _args():
                    help="budget of the single-core CPU baseline sample")
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--workload", default=None,
-                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "tq", "copy"],
+                   choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "tq", "copy",
+                            "rows_f"],
                    help="time one workload only and print its figures (for sweeps)")
     return p.parse_args()
 
@@ -342,6 +343,77 @@ def bench_gdn_prefill(torch, rt, dev, timer, steps, warmup, t=4096):
             "bytes_per_launch": algo, "flops_per_launch": flops}
 
 
+def _lib_fn(dev, entry, args):
+    """A timed call of one C entry point with prepared ctypes arguments."""
+    lib = dev.lib
+
+    def fn():
+        rc = entry(*args)
+        if rc:
+            raise RuntimeError(lib.pi_last_error(dev.h).decode())
+    return fn
+
+
+def _hbm(r, algo):
+    s = r["ms_avg"] * 1e-3
+    return {"us_per_call": r["ms_avg"] * 1e3, "GB_s": algo / s / 1e9,
+            "hbm_frac": algo / s / 1e9 / HBM_PEAK_GBS, "bytes_per_launch": algo}
+
+
+def bench_rows_f(torch, rt, dev, timer, steps, warmup):
+    """The steps either side of the path: the fused attention prologue (row f1:
+    per-head RMSNorm, RoPE, paged append in one launch) and the GDN conv1d and
+    RMSNormGated (row f2), at a prompt shape (HBM-bound) and a decode step."""
+    P = lambda x: None if x is None else ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    lib = dev.lib
+    res = {}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED00F1)
+
+    def prologue(n_seq, n_tok, hq, hkv, d, rope_dim, base, sections, norm, start):
+        pages = (start + n_tok + 15) // 16
+        pool = rt.KvPool(dev, n_seq * pages, hkv, d, torch.float16)
+        pt = torch.arange(n_seq * pages, dtype=torch.int32, device="cuda").view(n_seq, pages)
+        sp = torch.full((n_seq,), start, dtype=torch.int32, device="cuda")
+        q = torch.randn((n_seq, n_tok, hq, d), generator=g, device="cuda")
+        k = torch.randn((n_seq, n_tok, hkv, d), generator=g, device="cuda")
+        v = torch.randn((n_seq, n_tok, hkv, d), generator=g, device="cuda")
+        wq = torch.rand((d,), generator=g, device="cuda") + 0.5 if norm else None
+        wk = torch.rand((d,), generator=g, device="cuda") + 0.5 if norm else None
+        sec = None if sections is None else (ctypes.c_int32 * 4)(*sections)
+        args = (dev.h, P(q), P(k), P(v), P(wq), P(wk), 1e-6, rope_dim, base, sec, pool.p, P(pt),
+                pages, P(sp), n_seq, n_tok, hq, None)
+        r = timer.run(_lib_fn(dev, lib.pi_attn_prologue, args), steps, warmup)
+        # q and k read and rewritten (f32), v read, k and v appended (f16)
+        algo = n_seq * n_tok * d * (4 * (2 * hq + 3 * hkv) + 2 * 2 * hkv)
+        pool.close()
+        return _hbm(r, algo)
+
+    res["f1_prologue_prompt_c3"] = prologue(1, 4096, 32, 8, 128, 128, 1e6, None, False, 0)
+    res["f1_prologue_decode_c4"] = prologue(8, 1, 16, 2, 256, 64, 1e7, [11, 11, 10, 0], True,
+                                            65535)
+
+    hk, hv, dk, dv, d_conv = 16, 32, 128, 128, 4
+    conv_dim = 2 * hk * dk + hv * dv
+    w = torch.randn((conv_dim, d_conv), generator=g, device="cuda") * 0.5
+    nw = torch.rand((dv,), generator=g, device="cuda") + 0.5
+    for name, t in (("prompt_c5", 4096), ("decode_step", 1)):
+        x = torch.randn((1, t, conv_dim), generator=g, device="cuda")
+        cs = torch.randn((1, d_conv - 1, conv_dim), generator=g, device="cuda")
+        xo = torch.empty_like(x)
+        args = (dev.h, P(x), P(cs), P(w), P(xo), 1, t, conv_dim, d_conv, None)
+        r = timer.run(_lib_fn(dev, lib.pi_gdn_conv1d, args), steps, warmup)
+        # x read, out written, state read and written, weights read
+        res["f2_gdn_conv1d_" + name] = _hbm(
+            r, (2 * t * conv_dim + 2 * (d_conv - 1) * conv_dim + conv_dim * d_conv) * 4)
+        o = torch.randn((t, hv, dv), generator=g, device="cuda")
+        z = torch.randn((t, hv, dv), generator=g, device="cuda")
+        args = (dev.h, P(o), P(z), P(nw), t, hv, dv, 1e-6, None)
+        r = timer.run(_lib_fn(dev, lib.pi_gdn_rmsnorm_gated, args), steps, warmup)
+        res["f2_gdn_rmsnorm_gated_" + name] = _hbm(r, (3 * t * hv * dv + dv) * 4)
+    return res
+
+
 def bench_copy(torch, timer, steps, warmup, nbytes=1 << 30):
     """A plain device copy of known size: the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters, and the practical HBM ceiling."""
@@ -399,6 +471,8 @@ def _single(torch, rt, dev, timer, a):
         return bench_tq_decode(torch, rt, dev, timer, lens, 32, 8, 0x5EED0004, st, wu)
     if w == "copy":
         return bench_copy(torch, timer, st, wu)
+    if w == "rows_f":
+        return bench_rows_f(torch, rt, dev, timer, st, wu)
     return bench_gdn_decode(torch, rt, dev, timer, st, wu)
 
 
@@ -490,6 +564,7 @@ def main():
         # TurboQuant compressed-KV decode on the config 2 shape (3-bit + QJL keys, f16 values)
         wl["c2_turboquant_decode"] = bench_tq_decode(torch, rt, dev, timer, lens, 32, 8, 0x5EED0004,
                                                      a.steps, a.warmup)
+        wl.update(bench_rows_f(torch, rt, dev, timer, a.steps, a.warmup))
         line["workloads"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                                  for kk, vv in v.items()} for k, v in wl.items()}
     line["cpu_baseline_wall_s"] = round(cpu_wall, 2)

@@ -67,6 +67,53 @@ __global__ __launch_bounds__(256) void gdn_conv1d_kernel(const float* __restrict
     }
 }
 
+// The model's case, d_conv = 4 with 4 | conv_dim and 16-byte aligned rows: a
+// thread owns channels 4 c4 .. 4 c4 + 3 of one sequence and walks kConvTok
+// tokens with the three previous rows of X_ext in registers, so every input
+// is read once (16 bytes) and its taps once per thread; the 3-D grid needs no
+// index division.  Same arithmetic per element as gdn_conv1d_kernel.
+constexpr int kConvTok = 32;
+__global__ __launch_bounds__(256) void gdn_conv1d_k4_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ state,
+                                                            const float* __restrict__ w,
+                                                            float* __restrict__ out, int n_tok,
+                                                            int conv_dim) {
+    const int c4 = blockIdx.x * 256 + threadIdx.x;
+    if (4 * c4 >= conv_dim) return;
+    const int t0 = blockIdx.y * kConvTok, sq = blockIdx.z;
+    const size_t q4 = (size_t)conv_dim / 4;  // 16-byte groups per row
+    const f32x4* xs = reinterpret_cast<const f32x4*>(x + (size_t)sq * n_tok * conv_dim) + c4;
+    const f32x4* ss = reinterpret_cast<const f32x4*>(state + (size_t)sq * 3 * conv_dim) + c4;
+    f32x4* os = reinterpret_cast<f32x4*>(out + (size_t)sq * n_tok * conv_dim) + c4;
+    f32x4 wk[4];  // wk[k][e] = tap k of channel 4 c4 + e
+    {
+        const f32x4* wr = reinterpret_cast<const f32x4*>(w) + 4 * c4;
+        f32x4 wc[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wc[e] = wr[e];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wk[k] = f32x4{wc[0][k], wc[1][k], wc[2][k], wc[3][k]};
+    }
+    auto ext = [&](int r) { return r < 3 ? ss[(size_t)r * q4] : xs[(size_t)(r - 3) * q4]; };
+    f32x4 a = ext(t0), b = ext(t0 + 1), c = ext(t0 + 2);
+    const int t1 = min(n_tok, t0 + kConvTok);
+    for (int t = t0; t < t1; ++t) {
+        const f32x4 d = xs[(size_t)t * q4];  // X_ext row t + 3
+        f32x4 val = {0.f, 0.f, 0.f, 0.f};
+        val += wk[0] * a;
+        val += wk[1] * b;
+        val += wk[2] * c;
+        val += wk[3] * d;
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = val[e] / (1.0f + expf(-val[e]));
+        os[(size_t)t * q4] = o;
+        a = b;
+        b = c;
+        c = d;
+    }
+}
+
 // New state = the last d_conv-1 rows of X_ext (after gdn_conv1d_kernel has
 // read the old one; same stream, next launch).
 __global__ __launch_bounds__(256) void gdn_conv_state_kernel(const float* __restrict__ x,
@@ -819,8 +866,16 @@ hipError_t launch_gdn_conv1d(const float* x, float* state, const float* w, float
                              int32_t n_seq, int32_t n_tok, int32_t conv_dim, int32_t d_conv,
                              hipStream_t s) {
     const size_t total = (size_t)n_seq * n_tok * conv_dim;
-    hipLaunchKernelGGL(gdn_conv1d_kernel, dim3(grid_of(total)), dim3(256), 0, s, x, state, w, out,
-                       n_seq, n_tok, conv_dim, d_conv);
+    const bool aligned =
+        (((uintptr_t)x | (uintptr_t)state | (uintptr_t)w | (uintptr_t)out) & 15) == 0;
+    if (d_conv == 4 && conv_dim % 4 == 0 && aligned && n_seq <= 65535)
+        hipLaunchKernelGGL(gdn_conv1d_k4_kernel,
+                           dim3((unsigned)((conv_dim / 4 + 255) / 256), (unsigned)((n_tok + kConvTok - 1) / kConvTok),
+                                (unsigned)n_seq),
+                           dim3(256), 0, s, x, state, w, out, n_tok, conv_dim);
+    else
+        hipLaunchKernelGGL(gdn_conv1d_kernel, dim3(grid_of(total)), dim3(256), 0, s, x, state, w,
+                           out, n_seq, n_tok, conv_dim, d_conv);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || d_conv < 2) return e;
     if (n_tok >= d_conv - 1)

@@ -39,6 +39,23 @@ def test_conv1d_matches_oracle(n_tok):
     assert np.array_equal(st[0].cpu().numpy(), ref_hist)  # the state is a copy of raw inputs
 
 
+@pytest.mark.parametrize("c,d_conv,n_tok", [(1022, 4, 70), (512, 3, 33), (512, 3, 1)])
+def test_conv1d_general_shapes(c, d_conv, n_tok):
+    """Channel counts not divisible by 4 and d_conv != 4 (the general kernel)."""
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    rng = np.random.default_rng(47 + c + n_tok)
+    x = rng.standard_normal((n_tok, c)).astype(np.float32)
+    hist = rng.standard_normal((d_conv - 1, c)).astype(np.float32)
+    w = (rng.standard_normal((c, d_conv)) * 0.5).astype(np.float32)
+    ref, ref_hist = _conv_oracle(x, hist, w)
+    st = to_dev(hist[None])
+    out = rt.gdn_conv1d(dev, to_dev(x[None]), st, to_dev(w))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out[0].cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(st[0].cpu().numpy(), ref_hist)
+
+
 def test_conv1d_batched_decode_from_zero_state():
     """Three sequences, one token each, from the reference's zero initial window
     (src/model/mod.rs:752-756), then a second token."""
