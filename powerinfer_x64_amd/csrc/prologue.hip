@@ -159,7 +159,13 @@ __global__ __launch_bounds__(1024) void softmax_row_kernel(float* __restrict__ x
 // start_pos[s] + t, every q head and k head is RMS-normed (optional weights)
 // and rotated (NORM adjacent pairs or NeoX pairs with the host-built
 // frequency table), q in place, k in place and appended with v to the paged
-// pool.  One wavefront per (sequence, token, head); the row is staged in LDS.
+// pool.  Workgroup (x, y) = (sequence and token, y-th group of the token's
+// head rows): the token's cos / sin table is computed once into LDS (the angle
+// depends only on the position and the pair), then the 4 wavefronts take the
+// group's head rows in turn, each row staged in LDS.  Prompts use one group
+// per token (the table is shared by all heads); a launch of few tokens splits
+// the heads four to a group, so the rows still spread over the chip, and
+// computes each angle where it is used (no table, no barrier).
 template <typename PT>
 __global__ __launch_bounds__(256) void attn_prologue_kernel(
     float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
@@ -167,59 +173,78 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     int n_pairs, int neox, KvGeom g, const int32_t* __restrict__ pt, int max_pages,
     const int32_t* __restrict__ start_pos, int n_seq, int n_tok, int hq) {
     __shared__ float row_s[4][256];
+    __shared__ float cs_s[2][128];  // cos, sin of pair i at this token's position
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int D = g.head_dim, hkv = g.n_kv_heads, heads = hq + hkv;
-    const int row = blockIdx.x * 4 + wv;
-    if (row >= n_seq * n_tok * heads) return;
-    const int head = row % heads;
-    const int t = (row / heads) % n_tok;
-    const int sq = row / (heads * n_tok);
-    const bool is_q = head < hq;
-    const int kvh = head - hq;
-    float* x = is_q ? q + (((size_t)sq * n_tok + t) * hq + head) * D
-                    : k + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
-    const float* nw = is_q ? qn : kn;
-    float* r = row_s[wv];
-    float ss = 0.f;
-    for (int d = lane; d < D; d += 64) {
-        const float xv = x[d];
-        r[d] = xv;
-        ss += xv * xv;
-    }
-    if (nw) {  // ops::rms_norm (src/ops.rs:13-27) per head
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
-        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-        for (int d = lane; d < D; d += 64) r[d] = (r[d] * inv) * nw[d];
-    }
-    __builtin_amdgcn_wave_barrier();
+    const int t = blockIdx.x % n_tok, sq = blockIdx.x / n_tok;
     const int pos = start_pos[sq] + t;
-    for (int i = lane; i < n_pairs; i += 64) {  // ops::apply_rope / apply_rope_with_freqs
-        const int a = neox ? i : 2 * i;
-        const int b = neox ? i + n_pairs : 2 * i + 1;
-        if (b >= D) continue;
-        const float theta = (float)pos * f.f[i];
-        const float c = cosf(theta), sn = sinf(theta);
-        const float x0 = r[a], x1 = r[b];
-        r[a] = x0 * c - x1 * sn;
-        r[b] = x0 * sn + x1 * c;
+    const bool table = gridDim.y == 1;  // uniform per launch
+    if (table) {
+        for (int i = threadIdx.x; i < n_pairs; i += 256) {
+            const float theta = (float)pos * f.f[i];
+            cs_s[0][i] = cosf(theta);
+            cs_s[1][i] = sinf(theta);
+        }
+        __syncthreads();
     }
-    __builtin_amdgcn_wave_barrier();
-    for (int d = lane; d < D; d += 64) x[d] = r[d];
-    if (is_q) return;
-    // append-then-attend (src/model/mod.rs:1140-1146): K (normed, rotated) and V at pos
-    const int lp = pos / kPageTokens;
-    if (pos < 0 || lp >= max_pages) return;
-    const int page = pt[(size_t)sq * max_pages + lp];
-    if (page < 0 || page >= g.n_pages) return;
-    const int tok = pos % kPageTokens;
-    const size_t blk = ((size_t)page * hkv + kvh) * kPageTokens * D;
-    PT* kp = reinterpret_cast<PT*>(g.k) + blk;
-    PT* vp = reinterpret_cast<PT*>(g.v) + blk;
-    const float* vr = v + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
-    for (int d = lane; d < D; d += 64) {
-        kp[k_index<PT>(tok, d)] = from_f32<PT>(r[d]);
-        vp[v_index(tok, d)] = from_f32<PT>(vr[d]);
+    float* r = row_s[wv];
+    const int per = (heads + gridDim.y - 1) / gridDim.y;
+    const int h1 = min(heads, (int)(blockIdx.y + 1) * per);
+    for (int head = blockIdx.y * per + wv; head < h1; head += 4) {
+        const bool is_q = head < hq;
+        const int kvh = head - hq;
+        float* x = is_q ? q + (((size_t)sq * n_tok + t) * hq + head) * D
+                        : k + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
+        const float* nw = is_q ? qn : kn;
+        float ss = 0.f;
+        for (int d = lane; d < D; d += 64) {
+            const float xv = x[d];
+            r[d] = xv;
+            ss += xv * xv;
+        }
+        if (nw) {  // ops::rms_norm (src/ops.rs:13-27) per head
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
+            const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+            for (int d = lane; d < D; d += 64) r[d] = (r[d] * inv) * nw[d];
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (int i = lane; i < n_pairs; i += 64) {  // ops::apply_rope / apply_rope_with_freqs
+            const int a = neox ? i : 2 * i;
+            const int b = neox ? i + n_pairs : 2 * i + 1;
+            if (b >= D) continue;
+            float c, sn;
+            if (table) {
+                c = cs_s[0][i];
+                sn = cs_s[1][i];
+            } else {
+                const float theta = (float)pos * f.f[i];
+                c = cosf(theta);
+                sn = sinf(theta);
+            }
+            const float x0 = r[a], x1 = r[b];
+            r[a] = x0 * c - x1 * sn;
+            r[b] = x0 * sn + x1 * c;
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (int d = lane; d < D; d += 64) x[d] = r[d];
+        // append-then-attend (src/model/mod.rs:1140-1146): K (normed, rotated) and V at pos
+        const int lp = pos / kPageTokens;
+        if (!is_q && pos >= 0 && lp < max_pages) {
+            const int page = pt[(size_t)sq * max_pages + lp];
+            if (page >= 0 && page < g.n_pages) {
+                const int tok = pos % kPageTokens;
+                const size_t blk = ((size_t)page * hkv + kvh) * kPageTokens * D;
+                PT* kp = reinterpret_cast<PT*>(g.k) + blk;
+                PT* vp = reinterpret_cast<PT*>(g.v) + blk;
+                const float* vr = v + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
+                for (int d = lane; d < D; d += 64) {
+                    kp[k_index<PT>(tok, d)] = from_f32<PT>(r[d]);
+                    vp[v_index(tok, d)] = from_f32<PT>(vr[d]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the next row reuses r
     }
 }
 
@@ -279,8 +304,11 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
                                 const int32_t* page_table, int32_t max_pages,
                                 const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
                                 int32_t n_q_heads, hipStream_t s) {
-    const long long rows = (long long)n_seq * n_tok * (n_q_heads + g.n_kv_heads);
-    const dim3 grid((unsigned)((rows + 3) / 4));
+    const long long toks = (long long)n_seq * n_tok;
+    if (toks <= 0) return hipSuccess;
+    if (toks > 0x7fffffffLL || n_pairs > 128) return hipErrorInvalidValue;
+    const int heads = n_q_heads + g.n_kv_heads;
+    const dim3 grid((unsigned)toks, toks >= 1024 ? 1u : (unsigned)((heads + 3) / 4));
     if (g.dtype == 1)
         hipLaunchKernelGGL(attn_prologue_kernel<f16>, grid, dim3(256), 0, s, q, k, v, q_norm_w,
                            k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages,
