@@ -166,6 +166,31 @@ __global__ __launch_bounds__(256) void gdn_rmsnorm_gated_kernel(float* __restric
     if (hrow >= n_heads_total) return;
     float* oh = o + (size_t)hrow * v_hd;
     const float* zh = z + (size_t)hrow * v_hd;
+    if ((v_hd == 128 || v_hd == 64) && (((uintptr_t)oh | (uintptr_t)zh) & 7) == 0) {  // 8-byte accesses (v_hd 128)
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        const int npl = v_hd / 64;  // values per lane: 2 (one f2) or 1
+        float ov[2] = {0.f, 0.f}, zv[2] = {0.f, 0.f};
+        if (npl == 2) {
+            const f2 a = reinterpret_cast<const f2*>(oh)[lane], b = reinterpret_cast<const f2*>(zh)[lane];
+            ov[0] = a[0]; ov[1] = a[1]; zv[0] = b[0]; zv[1] = b[1];
+        } else {
+            ov[0] = oh[lane];
+            zv[0] = zh[lane];
+        }
+        float sq = ov[0] * ov[0] + ov[1] * ov[1];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) sq = wave_sum_xor(sq, m);
+        const float sc = 1.0f / sqrtf(sq / (float)v_hd + eps);
+        float r[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int d = npl * lane + e;
+            r[e] = e < npl ? (ov[e] * sc * w[d]) * (zv[e] / (1.0f + expf(-zv[e]))) : 0.f;
+        }
+        if (npl == 2) reinterpret_cast<f2*>(oh)[lane] = f2{r[0], r[1]};
+        else oh[lane] = r[0];
+        return;
+    }
     float ss = 0.f;
     for (int d = lane; d < v_hd; d += 64) ss += oh[d] * oh[d];
 #pragma unroll
