@@ -411,6 +411,56 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup):
         args = (dev.h, P(o), P(z), P(nw), t, hv, dv, 1e-6, None)
         r = timer.run(_lib_fn(dev, lib.pi_gdn_rmsnorm_gated, args), steps, warmup)
         res["f2_gdn_rmsnorm_gated_" + name] = _hbm(r, (3 * t * hv * dv + dv) * 4)
+
+    # row f3: one layer of `forward` through the host-slice seam (synchronous,
+    # host <-> device copies of the slices included): wall clock per call
+    rng = np.random.default_rng(0x5EED00F3)
+    f32 = np.float32
+    prompt, n_dec = 1024, 50
+
+    def layer_times(reset, step_prompt, step_token):
+        for _ in range(2):  # warm-up
+            reset()
+            step_prompt()
+        reps = []
+        for _ in range(3):
+            reset()
+            t0 = time.perf_counter()
+            step_prompt()
+            reps.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        for _ in range(n_dec):
+            step_token()
+        dec = (time.perf_counter() - t0) / n_dec
+        tp = float(np.median(reps))
+        return ({"ms_per_call": tp * 1e3, "tokens_per_s": prompt / tp},
+                {"us_per_token": dec * 1e6, "tokens_per_s": 1.0 / dec})
+
+    hq, hkv, d = 16, 2, 256
+    lay = rt.AttnLayer(dev, prompt + n_dec + 16, hq, hkv, d, torch.float16,
+                       q_norm_w=rng.uniform(0.5, 1.5, d).astype(f32),
+                       k_norm_w=rng.uniform(0.5, 1.5, d).astype(f32), rope_dim=64,
+                       rope_base=1e7, sections=[11, 11, 10, 0])
+    qa, ka, va, ga = (rng.standard_normal((prompt, h, d)).astype(f32)
+                      for h in (hq, hkv, hkv, hq))
+    q1, k1, v1, g1 = (np.ascontiguousarray(x[:1]) for x in (qa, ka, va, ga))
+    pr, dc = layer_times(lay.reset, lambda: lay.forward(qa, ka, va, ga),
+                         lambda: lay.forward(q1, k1, v1, g1))
+    res["f3_attn_layer_prompt_1024_c4"] = pr
+    res["f3_attn_layer_decode_token_c4"] = dc
+    lay.close()
+    gl = rt.GdnLayer(dev, hk, hv, dk, dv, (rng.standard_normal((conv_dim, d_conv)) * 0.5).astype(f32),
+                     -np.exp(rng.standard_normal(hv)).astype(f32),
+                     rng.standard_normal(hv).astype(f32), rng.uniform(0.5, 1.5, dv).astype(f32))
+    xa = rng.standard_normal((prompt, conv_dim)).astype(f32)
+    za = rng.standard_normal((prompt, hv, dv)).astype(f32)
+    ba, aa = (rng.standard_normal((prompt, hv)).astype(f32) for _ in range(2))
+    x1, z1, b1, a1 = (np.ascontiguousarray(x[:1]) for x in (xa, za, ba, aa))
+    pr, dc = layer_times(gl.reset, lambda: gl.forward(xa, za, ba, aa),
+                         lambda: gl.forward(x1, z1, b1, a1))
+    res["f3_gdn_layer_prompt_1024_c5"] = pr
+    res["f3_gdn_layer_decode_token_c5"] = dc
+    gl.close()
     return res
 
 
