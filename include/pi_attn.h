@@ -15,7 +15,10 @@
  *     are asynchronous on that stream except the h_* "sync" wrappers, which
  *     run on the handle's own stream and synchronise before returning, like
  *     GpuDevice::matvec (src/cuda/mod.rs:244-330);
- *   - one handle per host thread; the library takes no locks;
+ *   - one handle per host thread; the library takes no locks.  A handle's
+ *     workspaces (decode partials, GDN prefill buffers) may serve calls on
+ *     different streams: a call on another stream than the previous
+ *     workspace user waits (on the device) for that use first;
  *   - all arithmetic is fp32 except where a dtype argument says otherwise;
  *   - page_tokens is 16; head_dim is 64, 128 or 256.
  */
@@ -127,7 +130,10 @@ int pi_attn_prologue(pi_handle h, float* d_q, float* d_k, const float* d_v,
  * (normed, rotated); out [batch][n_q_heads][D] f32.  scale multiplies q.k
  * (1/sqrt(D) in the reference).  d_gate (nullable) [batch][n_q_heads][D]:
  * out *= sigmoid(gate) (src/model/mod.rs:1192-1196).  Split-K flash decoding,
- * one launch; n_q_heads/n_kv_heads <= 16. */
+ * one launch; n_q_heads/n_kv_heads <= 16.  Device tables are read, not
+ * trusted: d_ctx_len[b] is clamped to [0, 16 * max_pages], and a page id
+ * outside [0, n_pages) holds no tokens (its keys are masked; a sequence with
+ * no unmasked key gets zeros, as an empty context does). */
 int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t* d_page_table,
                    int32_t max_pages, const int32_t* d_ctx_len, int32_t batch,
                    int32_t n_q_heads, int32_t gqa_mode, float scale, const float* d_gate,

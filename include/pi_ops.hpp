@@ -139,6 +139,9 @@ public:
         int gqa_mode = PI_GQA_MODULO;
     };
     DeviceLayerCache(const Device& dev, const Config& c) : dev_(&dev), c_(c) {
+        if ((!c.q_norm.empty() && c.q_norm.size() != c.head_dim) ||
+            (!c.k_norm.empty() && c.k_norm.size() != c.head_dim))
+            throw BackendError(PI_ERR_INVALID_ARG, "DeviceLayerCache: norm weights must hold head_dim values");
         const int32_t rd = (int32_t)(c.rope_dim ? c.rope_dim : c.head_dim);
         dev.check(pi_attn_layer_create(dev.raw(), (int32_t)c.max_tokens, (int32_t)c.n_heads,
                                        (int32_t)c.n_kv_heads, (int32_t)c.head_dim, c.kv_dtype,

@@ -74,7 +74,7 @@ def build_cpp_tests(verbose: bool = False) -> None:
     for src in sorted(f for f in os.listdir(CPP_TESTS) if f.endswith(".cpp")):
         exe = os.path.join(out_dir, src[:-4])
         cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-Wextra", "-I", os.path.join(HERE, "..", "include"),
-               os.path.join(CPP_TESTS, src), "-L", HERE, "-lpi_attn",
+               "-I", CSRC, os.path.join(CPP_TESTS, src), "-L", HERE, "-lpi_attn",
                "-Wl,-rpath,$ORIGIN/../../../powerinfer_x64_amd", "-o", exe + ".tmp"]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:

@@ -28,6 +28,11 @@ struct pi_handle_s {
     size_t h2d_floats = 0;
     float* tq_qv = nullptr;        // TurboQuant virtual queries [batch][Hq][256]
     size_t tq_qv_floats = 0;
+    // Ordering of the workspaces above across caller streams: ws_event marks
+    // the last workspace use, issued on ws_stream.
+    hipEvent_t ws_event = nullptr;
+    hipStream_t ws_stream = nullptr;
+    bool ws_used = false;
 };
 
 struct pi_kv_pool_s {
@@ -134,6 +139,23 @@ int grow(pi_handle h, T** ptr, size_t* cap, size_t need, hipStream_t s, const ch
     return PI_OK;
 }
 
+// The handle's workspaces serve whatever stream a call names.  A call on a
+// different stream from the previous workspace user first makes its stream
+// wait for that use (ws_begin); every use is marked by an event on its own
+// stream (ws_end), so the wait never names a stream the caller may since have
+// destroyed.
+int ws_begin(pi_handle h, hipStream_t s, const char* what) {
+    if (h->ws_used && s != h->ws_stream) PI_HIP(h, hipStreamWaitEvent(s, h->ws_event, 0), what);
+    return PI_OK;
+}
+
+int ws_end(pi_handle h, hipStream_t s, const char* what) {
+    PI_HIP(h, hipEventRecord(h->ws_event, s), what);
+    h->ws_used = true;
+    h->ws_stream = s;
+    return PI_OK;
+}
+
 // ops::apply_rope (src/ops.rs:45-46): freq_i = 1 / base^(2i/rope_dim) in f32.
 void norm_rope_freqs(float base, int rope_dim, float* f) {
     for (int i = 0; i < rope_dim / 2; ++i) {
@@ -231,7 +253,10 @@ int pi_create(int device, pi_handle* out) {
     h->device = device;
     e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ws_event, hipEventDisableTiming);
     if (e != hipSuccess) {
+        if (h->ws_event) (void)hipEventDestroy(h->ws_event);
+        if (h->stream) (void)hipStreamDestroy(h->stream);
         delete h;
         return fail(nullptr, PI_ERR_DEVICE, "pi_create: %s", hipGetErrorString(e));
     }
@@ -243,11 +268,13 @@ void pi_destroy(pi_handle h) {
     if (!h) return;
     (void)hipSetDevice(h->device);
     if (h->stream) (void)hipStreamSynchronize(h->stream);
+    if (h->ws_used) (void)hipEventSynchronize(h->ws_event);
     (void)hipFree(h->dws.partial_o);
     (void)hipFree(h->dws.partial_ml);
     (void)hipFree(h->gws.buf);
     (void)hipFree(h->h2d_scratch);
     (void)hipFree(h->tq_qv);
+    if (h->ws_event) (void)hipEventDestroy(h->ws_event);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
 }
@@ -420,36 +447,32 @@ int pi_attn_prologue(pi_handle h, float* d_q, float* d_k, const float* d_v,
 
 // ---- attention -------------------------------------------------------------------
 
-int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t* d_page_table,
-                   int32_t max_pages, const int32_t* d_ctx_len, int32_t batch, int32_t n_q_heads,
-                   int32_t gqa_mode, float scale, const float* d_gate, float* d_out,
-                   void* stream) {
-    PI_CHECK_HANDLE(h);
-    if (!pool || !d_q || !d_page_table || !d_ctx_len || !d_out)
-        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode: null argument");
-    const pi::KvGeom& g = pool->g;
+// Shape checks shared by the decode entry points.
+static int decode_check(pi_handle h, const char* fn, const pi::KvGeom& g, const void* d_q,
+                        const void* d_page_table, const void* d_ctx_len, const void* d_out,
+                        int32_t max_pages, int32_t batch, int32_t n_q_heads, int32_t gqa_mode) {
+    if (!d_q || !d_page_table || !d_ctx_len || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "%s: null argument", fn);
     if (batch < 0 || max_pages <= 0 || n_q_heads <= 0)
-        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode: batch=%d max_pages=%d n_q_heads=%d", batch, max_pages, n_q_heads);
+        return fail(h, PI_ERR_INVALID_ARG, "%s: batch=%d max_pages=%d n_q_heads=%d", fn, batch, max_pages, n_q_heads);
     if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
-        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode: gqa_mode %d", gqa_mode);
+        return fail(h, PI_ERR_INVALID_ARG, "%s: gqa_mode %d", fn, gqa_mode);
     if (n_q_heads % g.n_kv_heads != 0)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: n_q_heads %d not a multiple of n_kv_heads %d", n_q_heads, g.n_kv_heads);
+        return fail(h, PI_ERR_UNSUPPORTED, "%s: n_q_heads %d not a multiple of n_kv_heads %d", fn, n_q_heads, g.n_kv_heads);
     const int group = n_q_heads / g.n_kv_heads;
     if (group > 16 || group * g.head_dim > 2048)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: %d q heads per kv head at head_dim %d", group, g.head_dim);
+        return fail(h, PI_ERR_UNSUPPORTED, "%s: %d q heads per kv head at head_dim %d", fn, group, g.head_dim);
     if (batch > pi::kMaxBatch)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: batch %d > %d", batch, pi::kMaxBatch);
+        return fail(h, PI_ERR_UNSUPPORTED, "%s: batch %d > %d", fn, batch, pi::kMaxBatch);
     if ((long long)batch * g.n_kv_heads * ((max_pages + pi::kItemPages - 1) / pi::kItemPages) > (1LL << 30))
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_decode: batch x kv heads x pages too large");
-    if (batch == 0) return PI_OK;
-    hipStream_t s = pick(h, stream);
-    PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode");
-    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
-    const size_t need_o = pi::decode_ws_floats_o(g, plan);
-    const size_t need_ml = need_o / g.head_dim * 2;
-    int rc;
-    if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_attn_decode workspace", false))) return rc;
-    if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_attn_decode workspace", false))) return rc;
+        return fail(h, PI_ERR_UNSUPPORTED, "%s: batch x kv heads x pages too large", fn);
+    return PI_OK;
+}
+
+static pi::DecodeParams decode_params(const float* d_q, const int32_t* d_page_table,
+                                      int32_t max_pages, const int32_t* d_ctx_len, int32_t batch,
+                                      int32_t n_q_heads, int32_t gqa_mode, float scale,
+                                      const float* d_gate, float* d_out, const pi::DecodePlan& plan) {
     pi::DecodeParams p;
     p.q = d_q;
     p.page_table = d_page_table;
@@ -462,8 +485,32 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
     p.gqa_mode = gqa_mode;
     p.scale = scale;
     p.item_pages = plan.item_pages;
+    return p;
+}
+
+int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t* d_page_table,
+                   int32_t max_pages, const int32_t* d_ctx_len, int32_t batch, int32_t n_q_heads,
+                   int32_t gqa_mode, float scale, const float* d_gate, float* d_out,
+                   void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!pool) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode: null argument");
+    const pi::KvGeom& g = pool->g;
+    int rc = decode_check(h, "pi_attn_decode", g, d_q, d_page_table, d_ctx_len, d_out, max_pages,
+                          batch, n_q_heads, gqa_mode);
+    if (rc) return rc;
+    if (batch == 0) return PI_OK;
+    hipStream_t s = pick(h, stream);
+    PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode");
+    if ((rc = ws_begin(h, s, "pi_attn_decode"))) return rc;
+    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
+    const size_t need_o = pi::decode_ws_floats_o(g, plan);
+    const size_t need_ml = need_o / g.head_dim * 2;
+    if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_attn_decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_attn_decode workspace", false))) return rc;
+    const pi::DecodeParams p = decode_params(d_q, d_page_table, max_pages, d_ctx_len, batch, n_q_heads,
+                                             gqa_mode, scale, d_gate, d_out, plan);
     PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), "pi_attn_decode");
-    return PI_OK;
+    return ws_end(h, s, "pi_attn_decode");
 }
 
 int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d_v, int32_t dtype,
@@ -581,6 +628,7 @@ int pi_gdn_prefill(pi_handle h, const float* d_q, const float* d_k, const float*
     if (n_tok == 0) return PI_OK;
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_gdn_prefill");
+    if ((rc = ws_begin(h, s, "pi_gdn_prefill"))) return rc;
     const size_t need = pi::gdn_prefill_ws_floats(n_tok, n_k_heads, n_v_heads, chunk);
     if (need) {
         rc = grow(h, &h->gws.buf, &h->gws.capacity, need, s, "pi_gdn_prefill workspace", false);
@@ -588,9 +636,8 @@ int pi_gdn_prefill(pi_handle h, const float* d_q, const float* d_k, const float*
     }
     hipError_t e = pi::launch_gdn_prefill(d_q, d_k, d_v, d_beta, d_g, d_state, d_out, n_tok,
                                           n_k_heads, n_v_heads, chunk, h->gws, s);
-    if (e == hipErrorNotSupported) return fail(h, PI_ERR_UNSUPPORTED, "pi_gdn_prefill: not built yet");
     if (e != hipSuccess) return hip_fail(h, e, "pi_gdn_prefill");
-    return PI_OK;
+    return ws_end(h, s, "pi_gdn_prefill");
 }
 
 // ---- host-slice drop-ins -------------------------------------------------------------
@@ -1166,49 +1213,30 @@ int pi_tq_attn_decode(pi_handle h, const float* d_q, pi_tq_pool pool, const int3
                       int32_t n_q_heads, int32_t gqa_mode, const float* d_gate, float* d_out,
                       void* stream) {
     PI_CHECK_HANDLE(h);
-    if (!pool || !d_q || !d_page_table || !d_ctx_len || !d_out)
-        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_attn_decode: null argument");
+    if (!pool) return fail(h, PI_ERR_INVALID_ARG, "pi_tq_attn_decode: null argument");
     const pi::KvGeom& g = pool->t.g;
-    if (batch < 0 || max_pages <= 0 || n_q_heads <= 0)
-        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_attn_decode: batch=%d max_pages=%d n_q_heads=%d", batch, max_pages, n_q_heads);
-    if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
-        return fail(h, PI_ERR_INVALID_ARG, "pi_tq_attn_decode: gqa_mode %d", gqa_mode);
-    if (n_q_heads % g.n_kv_heads != 0)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_attn_decode: n_q_heads %d not a multiple of n_kv_heads %d", n_q_heads, g.n_kv_heads);
-    const int group = n_q_heads / g.n_kv_heads;
-    if (group > 16)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_attn_decode: %d q heads per kv head", group);
-    if (batch > pi::kMaxBatch)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_attn_decode: batch %d > %d", batch, pi::kMaxBatch);
-    if ((long long)batch * g.n_kv_heads * ((max_pages + pi::kItemPages - 1) / pi::kItemPages) > (1LL << 30))
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_attn_decode: batch x kv heads x pages too large");
+    int rc = decode_check(h, "pi_tq_attn_decode", g, d_q, d_page_table, d_ctx_len, d_out, max_pages,
+                          batch, n_q_heads, gqa_mode);
+    if (rc) return rc;
     if (batch == 0) return PI_OK;
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_tq_attn_decode");
+    if ((rc = ws_begin(h, s, "pi_tq_attn_decode"))) return rc;
     const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
     const size_t need_o = pi::decode_ws_floats_o(g, plan);
     const size_t need_ml = need_o / g.head_dim * 2;
     const size_t need_qv = (size_t)batch * n_q_heads * 2 * g.head_dim;
-    int rc;
     if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_tq_attn_decode workspace", false))) return rc;
     if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_tq_attn_decode workspace", false))) return rc;
     if ((rc = grow(h, &h->tq_qv, &h->tq_qv_floats, need_qv, s, "pi_tq_attn_decode workspace", false))) return rc;
     PI_HIP(h, pi::launch_tq_query(pool->t, d_q, h->tq_qv, batch, n_q_heads, gqa_mode, s),
            "pi_tq_attn_decode");
-    pi::DecodeParams p;
-    p.q = h->tq_qv;
-    p.page_table = d_page_table;
-    p.ctx_len = d_ctx_len;
-    p.gate = d_gate;
-    p.out = d_out;
-    p.max_pages = max_pages;
-    p.batch = batch;
-    p.n_q_heads = n_q_heads;
-    p.gqa_mode = gqa_mode;
-    p.scale = 1.0f / std::sqrt((float)g.head_dim);  // src/turboquant/mod.rs:490
-    p.item_pages = plan.item_pages;
+    // the score scale is 1/sqrt(d) (src/turboquant/mod.rs:490)
+    const pi::DecodeParams p = decode_params(h->tq_qv, d_page_table, max_pages, d_ctx_len, batch,
+                                             n_q_heads, gqa_mode, 1.0f / std::sqrt((float)g.head_dim),
+                                             d_gate, d_out, plan);
     PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), "pi_tq_attn_decode");
-    return PI_OK;
+    return ws_end(h, s, "pi_tq_attn_decode");
 }
 
 }  // extern "C"

@@ -32,6 +32,7 @@
 // segment writes the output; otherwise it writes a partial and
 // decode_merge_kernel (same stream, next launch) combines the runs -- no
 // cross-workgroup synchronisation inside a kernel.
+#include "decode_sched.hpp"
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -47,6 +48,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxGD = 2048;            // G * D limit of the LDS merge buffer
 constexpr float kLazyThreshold = 8.0f;  // log2 headroom before the running max moves
 constexpr int kMaxRuns = 1024;          // runs of one segment the merge kernel stages
+static_assert(kWaves == sched::kWaves && kPageTokens == sched::kPage, "schedule constants");
 
 template <typename KT, int D>
 struct Tile;
@@ -304,12 +306,6 @@ __device__ __forceinline__ int head_of(int kvh, int col, int n_kv, int group, in
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Work items of a sequence: ceil(pages / item_pages) (0 for an empty context).
-__device__ __forceinline__ int items_of(int len, int item_pages) {
-    const int pages = (max(len, 0) + kPageTokens - 1) / kPageTokens;
-    return (pages + item_pages - 1) / item_pages;
-}
-
 // Softmax/PV state of one wavefront: O^T accumulators (lane = head column
 // `col`, dims 16t + 4*grp + r), the lazily raised running max, and the
 // per-lane partial sum (reduced over the 4 lane groups at the end).
@@ -360,13 +356,13 @@ __device__ __forceinline__ void process(Acc<D>& acc, const Tile<KT, D>* tl, cons
 
 // Prefix scan of per-sequence work items into LDS: s_cum[b] = items of
 // sequences < b (per KV head); returns the total over all sequences.
-__device__ __forceinline__ int scan_items(const int32_t* ctx_len, int batch, int item_pages,
-                                          int* s_cum, int* s_red) {
+__device__ __forceinline__ int scan_items(const DecodeParams& p, int* s_cum, int* s_red) {
     const int tid = threadIdx.x;
+    const int batch = p.batch;
     int carry = 0;
     for (int base = 0; base < batch; base += kThreads) {
         const int b = base + tid;
-        const int n = b < batch ? items_of(ctx_len[b], item_pages) : 0;
+        const int n = b < batch ? sched::items_of(sched::seq_tokens(p.ctx_len[b], p.max_pages), p.item_pages) : 0;
         // inclusive scan of n across the block
         int x = n;
 #pragma unroll
@@ -386,16 +382,6 @@ __device__ __forceinline__ int scan_items(const int32_t* ctx_len, int batch, int
     if (tid == 0) s_cum[batch] = carry;
     __syncthreads();
     return carry;
-}
-
-// Largest b with Hkv * s_cum[b] <= item (s_cum non-decreasing, s_cum[0] = 0).
-__device__ __forceinline__ int find_seq(const int* s_cum, int batch, int n_kv, int item) {
-    int lo = 0, hi = batch - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (n_kv * s_cum[mid] <= item) lo = mid; else hi = mid - 1;
-    }
-    return lo;
 }
 
 // Persistent, balanced decode.  The work of a launch is the list of "items"
@@ -419,7 +405,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
     const int n_kv = g.n_kv_heads;
     const int tid = threadIdx.x;
     T::prepare();  // tile tables in LDS; the scan below has barriers
-    const int per_kv = scan_items(p.ctx_len, p.batch, p.item_pages, s_cum, s_red);
+    const int per_kv = scan_items(p, s_cum, s_red);
     const int n_items = n_kv * per_kv;
     const int chunk = (n_items + gridDim.x - 1) / gridDim.x;
     int cur = blockIdx.x * chunk;
@@ -434,22 +420,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
     const char* kpool = reinterpret_cast<const char*>(g.k);
     const char* vpool = reinterpret_cast<const char*>(g.v);
 
-    int b = find_seq(s_cum, p.batch, n_kv, cur);
+    int b = sched::find_seq(s_cum, p.batch, n_kv, cur);
     while (cur < end) {
-        // segment of item `cur`
-        int nb = s_cum[b + 1] - s_cum[b];
-        while (nb == 0 || cur >= n_kv * s_cum[b + 1]) {  // skip empty / finished sequences
-            ++b;
-            nb = s_cum[b + 1] - s_cum[b];
-        }
-        const int kvh = (cur - n_kv * s_cum[b]) / nb;
-        const int seg0 = n_kv * s_cum[b] + kvh * nb;
-        const int run_end = min(end, seg0 + nb);
-        const int L = p.ctx_len[b];
-        const int n_pages_b = (L + kPageTokens - 1) / kPageTokens;
-        const int pg0 = (cur - seg0) * p.item_pages;
-        const int pg1 = min(n_pages_b, (run_end - seg0) * p.item_pages);
-        const bool whole = (cur == seg0) && (run_end == seg0 + nb);
+        const sched::Run run = sched::run_at(s_cum, p.ctx_len, p.max_pages, n_kv, p.item_pages, b,
+                                             cur, end);
+        b = run.b;
+        const int kvh = run.kvh, seg0 = run.seg0, run_end = run.run_end, L = run.len;
+        const int pg0 = run.pg0, pg1 = run.pg1;
+        const bool whole = run.whole;
 
         const int head = head_of(kvh, col_on ? col : 0, n_kv, group, p.gqa_mode);
         typename T::Q q;
@@ -463,11 +441,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
         const int32_t* pt = p.page_table + (size_t)b * p.max_pages;
 
         // sub-runs of up to 256 pages: a wavefront's page ids fit one VGPR
-        for (int sub = pg0; sub < pg1; sub += 64 * kWaves) {
-            const int sub_end = min(sub + 64 * kWaves, pg1);
-            const int first = sub + wave;  // this wave's pages: first + 4j, j < n_my
-            const int n_my = first < sub_end ? (sub_end - first + kWaves - 1) / kWaves : 0;
-            const int pid_v = lane < n_my ? pt[first + kWaves * lane] : 0;
+        for (int sub = pg0; sub < pg1; sub += sched::kSubPages) {
+            int first, n_my;  // this wave's pages: first + 4j, j < n_my
+            sched::sub_pages(sub, pg1, wave, &first, &n_my);
+            // A page id outside [0, n_pages) holds no tokens: page 0 is read in
+            // its place and every token of it is masked.
+            const int pid_raw = lane < n_my ? pt[first + kWaves * lane] : 0;
+            const bool bad = !sched::page_ok(pid_raw, g.n_pages);
+            const int pid_v = bad ? 0 : pid_raw;
+            const uint64_t bad_pages = __ballot(bad);
             const int first_pid = __builtin_amdgcn_readfirstlane(pid_v);
             auto load_group = [&](T* dst, int i) {
 #pragma unroll
@@ -483,7 +465,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
                 for (int u = 0; u < NP; ++u) {
                     const int j = NP * i + u;
                     const int tok0 = (first + kWaves * j) * kPageTokens;
-                    valid[u] = j < n_my ? min(L - tok0, kPageTokens) : 0;
+                    valid[u] = j < n_my && !((bad_pages >> j) & 1) ? min(L - tok0, kPageTokens) : 0;
                 }
             };
             const int n_iter = (n_my + NP - 1) / NP;
@@ -516,8 +498,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
             }
         }
         __syncthreads();
-        float* po = ws.partial_o + (size_t)cur * GD;
-        float* pml = ws.partial_ml + (size_t)cur * group * 2;
+        const size_t slot = (size_t)sched::run_slot(cur == seg0, b, kvh, n_kv, p.batch, blockIdx.x);
+        float* po = ws.partial_o + slot * GD;
+        float* pml = ws.partial_ml + slot * group * 2;
         for (int idx = tid; idx < GD; idx += kThreads) {
             const int c = idx / D, d = idx - c * D;
             float M = s_m[0][c];
@@ -533,7 +516,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
             if (whole) {
                 const int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
                 const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
-                float r = o / lsum;
+                float r = lsum > 0.f ? o / lsum : 0.f;  // every key masked: zeros
                 if (p.gate) r *= sigmoidf_(p.gate[oi]);
                 p.out[oi] = r;
             } else {
@@ -563,7 +546,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     __shared__ float s_inv[4];
     const int kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
-    const int per_kv = scan_items(p.ctx_len, p.batch, p.item_pages, s_cum, s_red);
+    const int per_kv = scan_items(p, s_cum, s_red);
     const int chunk = (n_kv * per_kv + n_wg - 1) / n_wg;
     const int nb = s_cum[b + 1] - s_cum[b];
     const int GD = group * D;
@@ -576,12 +559,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
         }
         return;
     }
-    const int seg0 = n_kv * s_cum[b] + kvh * nb;
-    const int seg1 = seg0 + nb;
-    const int first_cut = (seg0 / chunk + 1) * chunk;  // first workgroup boundary after seg0
-    if (first_cut >= seg1) return;  // one run: written directly by decode_kernel
-    const int n_runs = 1 + (seg1 - 1 - first_cut) / chunk + 1;
-    for (int r = tid; r < n_runs && r < kMaxRuns; r += 256) s_slot[r] = r == 0 ? seg0 : first_cut + (r - 1) * chunk;
+    int wg1;
+    const int n_runs = sched::merge_runs(s_cum, n_kv, chunk, b, kvh, &wg1);
+    if (n_runs == 1) return;  // one run: written directly by decode_kernel
+    for (int r = tid; r < n_runs && r < kMaxRuns; r += 256)
+        s_slot[r] = (int)sched::run_slot(r == 0, b, kvh, n_kv, p.batch, wg1 + r - 1);
     __syncthreads();
     const int c_lo = e0 / D, c_hi = min(group - 1, (e0 + 255) / D);
     const int lane = tid & 63, wave = tid >> 6;
@@ -601,7 +583,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
         }
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
-        if (lane == 0) s_inv[wave] = 1.0f / lsum;
+        if (lane == 0) s_inv[wave] = lsum > 0.f ? 1.0f / lsum : 0.f;
     }
     __syncthreads();
     if (idx >= GD) return;
@@ -683,8 +665,8 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
     int ip = kItemPages;
     while (ip > 1 && max_seg_pages / ip < 2LL * plan.grid) ip >>= 1;
     plan.item_pages = ip;
-    const long long items_per_seq = (max_pages + ip - 1) / ip;
-    plan.n_slots = (long long)batch * g.n_kv_heads * items_per_seq;
+    // one partial slot per segment and one per workgroup (run_slot)
+    plan.n_slots = (long long)batch * g.n_kv_heads + plan.grid;
     plan.group = n_q_heads / g.n_kv_heads;
     return plan;
 }

@@ -43,8 +43,8 @@ struct TqPool {
 };
 
 struct DecodeWorkspace {
-    float* partial_o;     // [item slot][G][D]  (only run-start slots are written)
-    float* partial_ml;    // [item slot][G][2]  (running max, sum) in log2 units
+    float* partial_o;     // [slot][G][D]: slot = segment (b * Hkv + kvh) or batch * Hkv + workgroup
+    float* partial_ml;    // [slot][G][2]  (running max, sum) in log2 units
     size_t capacity_o;    // floats
     size_t capacity_ml;   // floats
 };
@@ -65,7 +65,7 @@ struct DecodeParams {
 
 struct DecodePlan {
     int32_t grid;        // persistent workgroups (CUs x resident workgroups per CU)
-    long long n_slots;   // upper bound of work items (partial slots)
+    long long n_slots;   // partial slots: batch * n_kv_heads + grid
     int32_t group;       // q heads per kv head
     int32_t item_pages;  // pages per work item
 };

@@ -170,8 +170,11 @@ class AttnLayer:
                  rope_base: float = 1e6, sections=None, gqa_mode: int = MODULO):
         self.dev = dev
         self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
-        qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, np.float32)
-        kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, np.float32)
+        qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, np.float32).reshape(-1)
+        kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, np.float32).reshape(-1)
+        for name, w in (("q_norm_w", qn), ("k_norm_w", kn)):
+            if w is not None and w.size != head_dim:
+                raise InvalidArg(f"{name}: expected {head_dim} values, got {w.size}")
         sec = None if sections is None else (ctypes.c_int32 * 4)(*[int(x) for x in sections])
         p = ctypes.c_void_p()
         dev.check(dev.lib.pi_attn_layer_create(

@@ -111,6 +111,17 @@ static void test_errors_and_reset(const Device& dev) {
     CHECK(layer.try_forward(qc, kc, v, {}, 12, again)->ok());
     CHECK(again == out);
     CHECK(qc == qa && kc == ka);  // the same rotated q / k
+    // norm weights that do not hold head_dim values are refused before anything reads them
+    std::vector<float> short_norm(D / 2, 1.0f);
+    DeviceLayerCache::Config bad = c;
+    bad.k_norm = short_norm;
+    bool threw = false;
+    try {
+        DeviceLayerCache l2(dev, bad);
+    } catch (const powerinfer::BackendError& e) {
+        threw = e.kind() == powerinfer::ErrorKind::InvalidArgument;
+    }
+    CHECK(threw);
 }
 
 static void test_gdn_prompt_equals_token_loop(const Device& dev) {

@@ -3,6 +3,8 @@ the oracle-side cache preparation, and the parity metrics."""
 from __future__ import annotations
 
 import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import torch
@@ -27,6 +29,17 @@ def to_dev(a, dtype=None):
     if dtype is not None:
         t = t.to(dtype)
     return t.cuda()
+
+
+def oracle_workers():
+    """Threads for oracle work (ctypes releases the GIL): the GPU box's CPU share is 16."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def parallel_map(fn, items):
+    """fn over items on oracle_workers() threads, results in order."""
+    with ThreadPoolExecutor(max_workers=oracle_workers()) as ex:
+        return list(ex.map(fn, items))
 
 
 def row_rel_err(out, ref):
@@ -65,7 +78,7 @@ class PagedCase:
     """A batch of sequences with raw (pre-RoPE) K/V in a randomly permuted page table."""
 
     def __init__(self, rng, lens, hq, hkv, d, theta=1e6, rope_dim=None, sections=None,
-                 q_norm_w=None, k_norm_w=None, eps=1e-6, extra_pages=3):
+                 q_norm_w=None, k_norm_w=None, eps=1e-6, extra_pages=3, f32_draws=False):
         self.lens = [int(x) for x in lens]
         self.hq, self.hkv, self.d = hq, hkv, d
         self.theta, self.sections = theta, sections
@@ -84,9 +97,13 @@ class PagedCase:
             np_ = (x + 15) // 16
             self.page_table[i, :np_] = perm[off:off + np_]
             off += np_
-        self.k = [rng.standard_normal((x, hkv, d)).astype(np.float32) for x in self.lens]
-        self.v = [rng.standard_normal((x, hkv, d)).astype(np.float32) for x in self.lens]
-        self.q = rng.standard_normal((b, hq, d)).astype(np.float32)
+        if f32_draws:  # float32 draws directly (large caches)
+            draw = lambda shape: rng.standard_normal(shape, dtype=np.float32)  # noqa: E731
+        else:
+            draw = lambda shape: rng.standard_normal(shape).astype(np.float32)  # noqa: E731
+        self.k = [draw((x, hkv, d)) for x in self.lens]
+        self.v = [draw((x, hkv, d)) for x in self.lens]
+        self.q = draw((b, hq, d))
 
     # ---- oracle side (the reference's functions on the same raw inputs) ----
     def oracle_caches(self, i, kv_round=None):

@@ -88,6 +88,39 @@ def test_layer_llama2_mha_f32_cache():
            np.random.default_rng(0x1A3), 32, 32, 128)
 
 
+def test_layer_continued_chunk_over_256_rows():
+    """A 300-token chunk continuing a 200-token prompt (f16 cache, 32/8 heads): more rows
+    than one decode launch of the layer step takes (256), so the second launch reuses the
+    per-row context lengths after the first."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    layer = rt.AttnLayer(dev, 600, 32, 8, 128, torch.float16, rope_base=1e6)
+    _drive(layer, [200, 300, 1], dict(rope_base=1e6), _rel(1e-2),
+           np.random.default_rng(0x1A5), 32, 8, 128)
+
+
+def test_layer_f32_cache_prompt_over_256_rows():
+    """A 300-token prompt with an f32 cache (32/32 heads, D 128, theta 1e4), then a
+    continued 260-token chunk: max-abs <= 2e-3."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    layer = rt.AttnLayer(dev, 600, 32, 32, 128, torch.float32, rope_base=1e4)
+    _drive(layer, [300, 260], dict(rope_base=1e4), _abs(2e-3),
+           np.random.default_rng(0x1A6), 32, 32, 128)
+
+
+def test_layer_rejects_short_norm_weights():
+    """Norm weights must hold head_dim values: a shorter array is refused before anything
+    reads it."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    with pytest.raises(rt.InvalidArg):
+        rt.AttnLayer(dev, 64, 16, 2, 256, torch.float16, q_norm_w=np.ones(128, np.float32),
+                     k_norm_w=np.ones(256, np.float32))
+    with pytest.raises(rt.InvalidArg):
+        rt.AttnLayer(dev, 64, 16, 2, 256, torch.float16, k_norm_w=np.ones(255, np.float32))
+
+
 def test_layer_reset_and_full_cache():
     """reset() restarts the sequence (the same prompt gives the same output); a forward that
     would overflow the cache fails with OutOfMemory and leaves the sequence as it was."""

@@ -19,10 +19,11 @@ def _pool(rt, dev, n_seq, max_tokens, hkv, d, dtype, rng):
     return rt.KvPool(dev, n_seq * pages, hkv, d, dtype=dtype), to_dev(pt)
 
 
-@pytest.mark.parametrize("shape", ["c2", "c4", "c2_prompt"])
+@pytest.mark.parametrize("shape", ["c2", "c4", "c2_prompt", "c4_prompt"])
 def test_prologue_matches_oracle(shape):
-    """Three sequences, 5 tokens each at different offsets; c2_prompt: one 1100-token
-    prompt (a launch of >= 1024 tokens shares one cos / sin table per token)."""
+    """Three sequences, 5 tokens each at different offsets; *_prompt: one 1100-token
+    prompt (a launch of >= 1024 tokens shares one cos / sin table per token), with NORM
+    RoPE (c2) or Q/K RMSNorm and IMRoPE at D 256 (c4)."""
     from powerinfer_x64_amd import runtime as rt
     dev = device()
     rng = np.random.default_rng(50)
@@ -32,7 +33,7 @@ def test_prologue_matches_oracle(shape):
         hq, hkv, d, base, rd, sec, norm = 16, 2, 256, 1e7, 64, [11, 11, 10, 0], True
     n_seq, n_tok = 3, 5
     starts = np.array([0, 17, 40000], np.int32)
-    if shape == "c2_prompt":
+    if shape.endswith("_prompt"):
         n_seq, n_tok = 1, 1100
         starts = np.array([7], np.int32)
     q = rng.standard_normal((n_seq, n_tok, hq, d)).astype(np.float32)
