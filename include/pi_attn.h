@@ -139,6 +139,23 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
                    int32_t n_q_heads, int32_t gqa_mode, float scale, const float* d_gate,
                    float* d_out, void* stream);
 
+/* No counterpart in the reference.  pi_attn_decode for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): same arguments, kernels and results, but
+ * the split-run partials live in a fixed 16 MiB scratch array per GPU instead
+ * of the handle's grow-on-demand workspace, so the call allocates nothing.
+ * The scratch needs (batch * n_kv_heads + CUs * resident workgroups) *
+ * (n_q_heads / n_kv_heads) * (head_dim + 2) floats (at most 1023 workgroups);
+ * a launch needing more fails with PI_ERR_UNSUPPORTED and launches nothing.
+ * Every no-alloc call on one GPU, from any handle or stream, shares that
+ * array: calls that overlap on one GPU race and must be ordered by the
+ * caller. */
+int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
+                           const int32_t* d_page_table, int32_t max_pages,
+                           const int32_t* d_ctx_len, int32_t batch, int32_t n_q_heads,
+                           int32_t gqa_mode, float scale, const float* d_gate, float* d_out,
+                           void* stream);
+
 /* Causal prefill of a whole prompt: row i attends keys 0..i, which is what the
  * reference's per-token loop computes (src/model/mod.rs:668,1140-1190).
  * d_q [batch][seq_len][n_q_heads][D], d_k/d_v [batch][seq_len][n_kv_heads][D]

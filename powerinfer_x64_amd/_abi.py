@@ -38,6 +38,8 @@ SIGNATURES = {
                                 _i32, _vp, _i32, _i32, _i32, _vp]),
     "pi_attn_decode": (_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp, _vp,
                               _vp]),
+    "pi_attn_decode_noalloc": (_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp,
+                                      _vp, _vp]),
     "pi_attn_prefill": (_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                _i32, _f32, _vp, _vp]),
     "pi_gdn_gates": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),

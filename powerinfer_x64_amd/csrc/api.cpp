@@ -33,6 +33,7 @@ struct pi_handle_s {
     hipEvent_t ws_event = nullptr;
     hipStream_t ws_stream = nullptr;
     bool ws_used = false;
+    float* scratch = nullptr;      // this device's fixed scratch (pi_attn_decode_noalloc)
 };
 
 struct pi_kv_pool_s {
@@ -254,6 +255,8 @@ int pi_create(int device, pi_handle* out) {
     e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&h->ws_event, hipEventDisableTiming);
+    // the device address of this GPU's fixed scratch, looked up with it current
+    if (e == hipSuccess) e = pi::decode_scratch(device, &h->scratch);
     if (e != hipSuccess) {
         if (h->ws_event) (void)hipEventDestroy(h->ws_event);
         if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -511,6 +514,41 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
                                              gqa_mode, scale, d_gate, d_out, plan);
     PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), "pi_attn_decode");
     return ws_end(h, s, "pi_attn_decode");
+}
+
+int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
+                           const int32_t* d_page_table, int32_t max_pages,
+                           const int32_t* d_ctx_len, int32_t batch, int32_t n_q_heads,
+                           int32_t gqa_mode, float scale, const float* d_gate, float* d_out,
+                           void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!pool) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode_noalloc: null argument");
+    const pi::KvGeom& g = pool->g;
+    int rc = decode_check(h, "pi_attn_decode_noalloc", g, d_q, d_page_table, d_ctx_len, d_out,
+                          max_pages, batch, n_q_heads, gqa_mode);
+    if (rc) return rc;
+    if (batch == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode_noalloc");
+    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
+    // partial o, then (m, l) at the next 256-byte boundary, all inside the scratch
+    const size_t need_o = pi::decode_ws_floats_o(g, plan);
+    const size_t off_ml = (need_o + 63) / 64 * 64;
+    const size_t need_ml = need_o / g.head_dim * 2;
+    if (off_ml + need_ml > pi::kDecodeScratchFloats)
+        return fail(h, PI_ERR_UNSUPPORTED,
+                    "pi_attn_decode_noalloc: %zu scratch floats needed (batch %d x %d kv heads + %d "
+                    "workgroups, %d q heads per kv head, head_dim %d) > the fixed %zu",
+                    off_ml + need_ml, batch, g.n_kv_heads, plan.grid, plan.group, g.head_dim,
+                    pi::kDecodeScratchFloats);
+    pi::DecodeWorkspace ws;
+    ws.partial_o = h->scratch;
+    ws.partial_ml = h->scratch + off_ml;
+    ws.capacity_o = need_o;
+    ws.capacity_ml = need_ml;
+    const pi::DecodeParams p = decode_params(d_q, d_page_table, max_pages, d_ctx_len, batch, n_q_heads,
+                                             gqa_mode, scale, d_gate, d_out, plan);
+    PI_HIP(h, pi::launch_decode(g, p, ws, plan, pick(h, stream)), "pi_attn_decode_noalloc");
+    return PI_OK;
 }
 
 int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d_v, int32_t dtype,

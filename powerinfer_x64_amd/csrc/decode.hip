@@ -37,8 +37,17 @@
 #include "pi_launch.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
+
+// Fixed scratch of pi_attn_decode_noalloc: the run partials (o, then m and l)
+// for callers that cannot allocate device memory.  Each GPU holds one copy
+// until the process ends, and every no-alloc call on that GPU shares it.
+// Nothing in it needs to start at zero: a slot is written before the merge
+// kernel reads it.  Host code never passes this name to a kernel; it uses the
+// device address that decode_scratch() looks up.
+static __device__ __align__(256) float scratch[pi::kDecodeScratchFloats];
 
 namespace pi {
 namespace {
@@ -669,6 +678,27 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
     plan.n_slots = (long long)batch * g.n_kv_heads + plan.grid;
     plan.group = n_q_heads / g.n_kv_heads;
     return plan;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+}  // namespace
+
+hipError_t decode_scratch(int device, float** ptr) {
+    *ptr = nullptr;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    float* p = g_scratch[device].load(std::memory_order_acquire);
+    if (!p) {
+        // the device is current (pi_create sets it); each GPU has its own copy
+        void* a = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        p = static_cast<float*>(a);
+        g_scratch[device].store(p, std::memory_order_release);
+    }
+    *ptr = p;
+    return hipSuccess;
 }
 
 size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan) {

@@ -69,6 +69,12 @@ struct DecodePlan {
     int32_t group;       // q heads per kv head
     int32_t item_pages;  // pages per work item
 };
+// Floats of the per-GPU fixed scratch behind pi_attn_decode_noalloc (16 MiB).
+constexpr size_t kDecodeScratchFloats = (size_t)4 << 20;
+// Device address of that scratch on `device`, which must be current; looked up
+// once per device with hipGetSymbolAddress.
+hipError_t decode_scratch(int device, float** ptr);
+
 // Grid size and workspace bound of a decode launch on `device`.
 DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
                        int device);
