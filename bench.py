@@ -18,8 +18,9 @@ library's stream brackets `steps` back-to-back calls, followed by a
 synchronize; ms_per_step is that interval / steps.  A second pass with an
 event pair per call gives the median and minimum.
 
-cpu_baseline: the oracle (a C restatement of the reference's CPU loops,
-single core) on the same decode inputs read back from the pool.
+cpu_baseline: beside every entry, the oracle (a C restatement of the reference's
+single-threaded CPU loops) on one pinned core, on a bounded sample of that
+entry's own inputs (about --cpu-seconds in total), in the entry's unit.
 """
 from __future__ import annotations
 
@@ -153,7 +154,8 @@ def _decode_fn(dev, pool, tpt, ctx, q, out, gate=None):
     return fn
 
 
-def bench_decode(torch, rt, dev, timer, lens, hq, hkv, d, theta, seed, steps, warmup, **kw):
+def bench_decode(torch, rt, dev, timer, lens, hq, hkv, d, theta, seed, steps, warmup,
+                 cpu_s=0.0, **kw):
     gate_on = kw.pop("gate", False)
     pool, tpt, ctx, q, algo = _paged_decode_setup(torch, rt, dev, lens, hq, hkv, d, theta, seed,
                                                   **kw)
@@ -166,10 +168,22 @@ def bench_decode(torch, rt, dev, timer, lens, hq, hkv, d, theta, seed, steps, wa
     res = {"GB_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "ms_per_step": t["ms_avg"],
            "ms_median": t["ms_median"], "bytes_per_launch": algo,
            "tokens": int(sum(int(x) for x in lens))}
+    if cpu_s > 0:
+        torch.cuda.synchronize()
+        qh, oh = q.cpu().numpy(), out.cpu().numpy()
+        gh = None if gate is None else gate.cpu().numpy()
+        elem = 4 if kw.get("pool_dtype") == torch.float32 else 2
+
+        def load(i):
+            ko, vo = pool.read(tpt, i, 0, int(lens[i]))
+            torch.cuda.synchronize()
+            return ko.cpu().numpy(), vo.cpu().numpy()
+        with OneCore():
+            res["cpu_baseline"] = cpu_decode(qh, load, lens, hkv, d, elem, cpu_s, oh, gh)
     return res, (pool, tpt, ctx, q, out, gate)
 
 
-def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup):
+def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup, cpu_s=0.0):
     """TurboQuant compressed-KV decode (pi_tq_attn_decode) over the config 2 shape: the
     cache is appended through pi_tq_append (K, V ~ N(0,1) generated on the GPU); the timed
     call includes the per-query precompute and the merge."""
@@ -210,6 +224,9 @@ def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup):
             raise RuntimeError(lib.pi_last_error(dev.h).decode())
     t = timer.run(fn, steps, warmup)
     tokens = sum(int(x) for x in lens)
+    cpu = None
+    if cpu_s > 0:
+        cpu = cpu_tq_decode(torch, pool, tpt, q, out, lens, hq, hkv, cpu_s)
     # per token and KV head: 64-byte key record + f32 norm + 128 f16 values
     algo = (tokens * hkv * (64 + 4 + d * 2) + 2 * len(lens) * hq * d * 4
             + total * 4 + len(lens) * 4 + 2 * hkv * d * d * 4)
@@ -219,43 +236,180 @@ def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup):
            "ms_median": t["ms_median"], "bytes_per_launch": algo, "tokens": tokens,
            "kv_bytes_vs_f16_pool": round(tokens * hkv * (68 + d * 2) / f16_equiv, 4),
            "append_tokens_per_s": tokens / append_s}
+    if cpu is not None:
+        res["cpu_baseline"] = cpu
     del pool
     return res
 
 
-def cpu_baseline_decode(torch, rt, dev, state, lens, hq, hkv, d, budget_s):
-    """Oracle (single core) on sequences of the same workload until the budget is spent."""
+def cpu_tq_decode(torch, pool, tpt, q, out, lens, hq, hkv, budget_s):
+    """or_tq_cache_attend (the compressed-cache attention of src/turboquant/mod.rs:489-535 with
+    the precomputed query) per query head, over the stored records read back from the pool,
+    sequence by sequence until the budget is spent."""
     from oracle import oracle as orc
-    pool, tpt, ctx, q, out, _ = state
-    qh = q.cpu().numpy()
-    oh = out.cpu().numpy()
-    t_cpu = 0.0
-    nbytes = 0
+    torch.cuda.synchronize()
+    qh, oh = q.cpu().numpy(), out.cpu().numpy()
+    mats = [orc.tq_matrices(128, 0xCAFEBABE + h) for h in range(hkv)]
+    t = 0.0
+    nbytes = toks = done = 0
+    err = 0.0
+    with OneCore():
+        for i, L in enumerate(int(x) for x in lens):
+            ko, no, vo = pool.read(tpt, i, 0, L)
+            torch.cuda.synchronize()
+            kh, nh, vh = ko.cpu().numpy(), no.cpu().numpy(), vo.cpu().numpy()
+            t0 = time.perf_counter()
+            ref = np.stack([orc.tq_cache_attend(qh[i, h], kh, nh, vh, *mats[h % hkv], h % hkv)
+                            for h in range(hq)])
+            t += time.perf_counter() - t0
+            nbytes += L * hkv * (64 + 4 + 128 * 2) + 2 * hq * 128 * 4
+            toks += L
+            done += 1
+            err = max(err, _row_rel(oh[i], ref))
+            if t >= budget_s:
+                break
+    return _cpu(nbytes / t / 1e9, "GB/s",
+                f"or_tq_cache_attend per query head on {done} of {len(lens)} sequences ({toks} "
+                f"tokens) of stored records read back from the pool; bytes counted as the GPU "
+                f"entry's (324 B per token and KV head)", round(t, 3),
+                parity_max_row_rel_err=round(err, 6))
+
+
+# ---- CPU baselines ------------------------------------------------------------
+# The oracle (oracle/oracle.c: a C restatement of the reference's single-threaded CPU
+# loops, built gcc -O3 -msse4.1) timed on one pinned core on a bounded sample of each
+# workload's own inputs, copied back from the GPU outside the timed region.  Each
+# figure is in the unit of the GPU entry it sits beside (the workload's algorithmic
+# bytes, flops or tokens per second), so the two read side by side.
+
+def cpu_info():
+    """Host CPU model (from /proc/cpuinfo) and how many cores this process may use."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_cpus": os.cpu_count(),
+            "allowed_cpus": len(os.sched_getaffinity(0))}
+
+
+class OneCore:
+    """Pins the process to one core (the lowest it may use) and restores the mask."""
+
+    def __enter__(self):
+        self.mask = os.sched_getaffinity(0)
+        self.core = min(self.mask)
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.mask)
+
+
+def _cpu(value, unit, sample, seconds, **extra):
+    return {"value": value, "unit": unit, "cores": 1, "kind": "port", "sample": sample,
+            "cpu_seconds": seconds, **extra}
+
+
+def _row_rel(a, b):
+    a = np.asarray(a, np.float64).reshape(-1, np.shape(b)[-1])
+    b = np.asarray(b, np.float64).reshape(-1, np.shape(b)[-1])
+    return float((np.linalg.norm(a - b, axis=1) / np.maximum(np.linalg.norm(b, axis=1), 1e-30)).max())
+
+
+def cpu_decode(qh, load, lens, hkv, d, elem_bytes, budget_s, out_gpu, gate=None, order=None):
+    """or_attn_decode (src/model/mod.rs:1154-1190, + the gate :1192-1196) per sequence until
+    the budget is spent; load(i) -> (K, V) f32 [L, Hkv, D] is untimed."""
+    from oracle import oracle as orc
+    t = 0.0
+    nbytes = tokens = calls = 0
+    err = 0.0
+    order = list(order if order is not None else range(len(lens)))
+    kept = {}  # a workload that fits the budget more than once is repeated from memory
+    seen = set()
+    while t < budget_s:
+        for i in order:
+            kh, vh = kept[i] if i in kept else load(i)
+            if sum(int(lens[j]) for j in order) <= (1 << 20):
+                kept[i] = (kh, vh)
+            t0 = time.perf_counter()
+            ref = orc.attn_decode(qh[i], kh, vh)
+            if gate is not None:
+                ref = orc.apply_gate(ref, gate[i])
+            t += time.perf_counter() - t0
+            L = int(lens[i])
+            nbytes += L * hkv * d * 2 * elem_bytes + 2 * qh.shape[1] * d * 4
+            tokens += L
+            calls += 1
+            seen.add(i)
+            err = max(err, _row_rel(out_gpu[i], ref))
+            if t >= budget_s:
+                break
+    note = (f"; the {len(kept)} sequence(s) were repeated from host memory, so their "
+            f"{sum(k.nbytes + v.nbytes for k, v in kept.values()) / 1e6:.1f} MB can stay in the "
+            f"CPU caches" if calls > len(seen) else "")
+    return _cpu(nbytes / t / 1e9, "GB/s",
+                f"or_attn_decode{' + or_apply_gate' if gate is not None else ''} on {len(seen)} "
+                f"of {len(lens)} sequences ({calls} calls, {tokens} tokens) read back from the "
+                f"pool as f32; bytes counted as the GPU entry's ({elem_bytes}-byte K/V){note}",
+                round(t, 3), parity_max_row_rel_err=round(err, 6))
+
+
+def cpu_prefill(qf, kf, vf, out_gpu, budget_s, stride=97):
+    """The reference's prefill: or_attn_decode for row i over keys 0..i (src/model/mod.rs:668
+    token loop).  Rows go from the last down in steps of `stride` (mod S), so the sample
+    spreads over the triangle; flops per row are 4 * Hq * D * (i + 1)."""
+    from oracle import oracle as orc
+    s, hq, d = qf.shape
+    t = flops = 0.0
     done = 0
-    max_rel = 0.0
-    for i, x in enumerate(lens):
-        x = int(x)
-        ko, vo = pool.read(tpt, i, 0, x)
-        torch.cuda.synchronize()
-        kh, vh = ko.cpu().numpy(), vo.cpu().numpy()
+    err = 0.0
+    i = s - 1
+    while done < s:
         t0 = time.perf_counter()
-        ref = orc.attn_decode(qh[i], kh, vh)
-        t_cpu += time.perf_counter() - t0
-        nbytes += x * hkv * d * 2 * 2 + 2 * hq * d * 4
+        ref = orc.attn_decode(qf[i], kf[:i + 1], vf[:i + 1])
+        t += time.perf_counter() - t0
+        flops += 4.0 * hq * d * (i + 1)
+        err = max(err, _row_rel(out_gpu[i], ref))
         done += 1
-        rel = np.linalg.norm(oh[i] - ref, axis=1) / np.linalg.norm(ref, axis=1)
-        max_rel = max(max_rel, float(rel.max()))
-        if t_cpu >= budget_s:
+        i = (i - stride) % s
+        if t >= budget_s:
             break
-    return {"value": nbytes / t_cpu / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle or_attn_decode (C restatement of src/model/mod.rs:1154-1190, "
-                      f"gcc -O3 -msse4.1, 1 thread) on {done} of {len(lens)} sequences "
-                      f"({sum(int(x) for x in lens[:done])} tokens) read back from the pool as "
-                      f"f32; {t_cpu:.1f} s",
-            "parity_max_row_rel_err": max_rel}
+    full = 4.0 * hq * d * s * (s + 1) / 2
+    return _cpu(flops / t / 1e12, "TFLOP/s",
+                f"or_attn_decode rows i = {s - 1}, {s - 1 - stride}, ... (mod {s}): {done} of "
+                f"{s} rows, {flops / 1e9:.2f} of {full / 1e9:.1f} GFLOP", round(t, 3),
+                full_prompt_s_estimate=round(full / (flops / t), 1),
+                parity_max_row_rel_err=round(err, 6))
 
 
-def bench_prefill(torch, rt, dev, timer, s, hq, hkv, d, theta, seed, steps, warmup):
+def cpu_gdn_tokens(q, k, v, beta, g, out_gpu, budget_s, state=None, chunk=32):
+    """or_gdn_tokens (src/model/mod.rs:841-916, one token at a time) over the first tokens of
+    the workload, `chunk` tokens per call continuing the state, until the budget is spent.
+    Returns (figures, tokens done, seconds)."""
+    from oracle import oracle as orc
+    n_all = q.shape[0]
+    st = state
+    t = 0.0
+    n = 0
+    err = 0.0
+    while n < n_all:
+        m = min(chunk, n_all - n)
+        t0 = time.perf_counter()
+        o, st = orc.gdn_tokens(q[n:n + m], k[n:n + m], v[n:n + m], beta[n:n + m], g[n:n + m], st)
+        t += time.perf_counter() - t0
+        err = max(err, float(np.abs(o - out_gpu[n:n + m]).max()))
+        n += m
+        if t >= budget_s:
+            break
+    return n, t, err
+
+
+def bench_prefill(torch, rt, dev, timer, s, hq, hkv, d, theta, seed, steps, warmup, cpu_s=0.0):
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     q = torch.randn((s, hq, d), generator=g, device="cuda")
@@ -278,11 +432,17 @@ def bench_prefill(torch, rt, dev, timer, s, hq, hkv, d, theta, seed, steps, warm
     t = timer.run(fn, steps, warmup)
     flops = 4.0 * hq * d * s * (s + 1) / 2
     tf = flops / (t["ms_avg"] * 1e-3) / 1e12
-    return {"TFLOP_s": tf, "mfma_frac": tf / MFMA_F16_PEAK_TFLOPS, "ms_per_step": t["ms_avg"],
-            "flops_per_launch": flops, "tokens_per_s": s / (t["ms_avg"] * 1e-3)}
+    res = {"TFLOP_s": tf, "mfma_frac": tf / MFMA_F16_PEAK_TFLOPS, "ms_per_step": t["ms_avg"],
+           "flops_per_launch": flops, "tokens_per_s": s / (t["ms_avg"] * 1e-3)}
+    if cpu_s > 0:
+        torch.cuda.synchronize()
+        qf, kf, vf = (x[0].float().cpu().numpy() for x in (qb, kb, vb))
+        with OneCore():
+            res["cpu_baseline"] = cpu_prefill(qf, kf, vf, out[0].cpu().numpy(), cpu_s)
+    return res
 
 
-def bench_gdn_decode(torch, rt, dev, timer, steps, warmup):
+def bench_gdn_decode(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
     hk, hv, dk, dv = 16, 32, 128, 128
     g = torch.Generator(device="cuda")
     g.manual_seed(0x5EED0004)
@@ -305,11 +465,30 @@ def bench_gdn_decode(torch, rt, dev, timer, steps, warmup):
     t = timer.run(fn, steps, warmup)
     algo = 2 * hv * dk * dv * 4 + (2 * hk * dk + 2 * hv * dv + 2 * hv) * 4
     gbs = algo / (t["ms_avg"] * 1e-3) / 1e9
-    return {"us_per_step": t["ms_avg"] * 1e3, "tokens_per_s": 1e3 / t["ms_avg"], "GB_s": gbs,
-            "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_launch": algo}
+    res = {"us_per_step": t["ms_avg"] * 1e3, "tokens_per_s": 1e3 / t["ms_avg"], "GB_s": gbs,
+           "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_launch": algo}
+    if cpu_s > 0:
+        # the timed calls advanced the state: one GPU step from zero for the parity figure
+        state.zero_()
+        fn()
+        torch.cuda.synchronize()
+        h = [x.cpu().numpy() for x in (q, k, v, beta, gg)]
+        reps = 256  # the same token as 256 consecutive steps (the reference's per-token loop)
+        with OneCore():
+            n, sec, _ = cpu_gdn_tokens(*[np.repeat(x, reps, axis=0) for x in h],
+                                       np.repeat(out.cpu().numpy(), reps, axis=0), cpu_s)
+        from oracle import oracle as orc
+        o1, _ = orc.gdn_tokens(*h)
+        res["cpu_baseline"] = _cpu(
+            n * algo / sec / 1e9, "GB/s",
+            f"or_gdn_tokens: {n} steps from a zero state, per step {sec / n * 1e6:.1f} us "
+            f"({n / sec:.1f} tokens/s); bytes counted as the GPU entry's (state read + write, "
+            f"q, k, v, beta, g, out)", round(sec, 3), us_per_step=round(sec / n * 1e6, 2),
+            parity_max_abs_err=float(np.abs(o1 - out.cpu().numpy()).max()))
+    return res
 
 
-def bench_gdn_prefill(torch, rt, dev, timer, steps, warmup, t=4096):
+def bench_gdn_prefill(torch, rt, dev, timer, steps, warmup, t=4096, cpu_s=0.0):
     """Config 5 prefill: 4096 tokens, chunk 64, from a zero state."""
     hk, hv, dk, dv = 16, 32, 128, 128
     g = torch.Generator(device="cuda")
@@ -338,9 +517,24 @@ def bench_gdn_prefill(torch, rt, dev, timer, steps, warmup, t=4096):
     c = 64
     flops = nc * hv * (6 * c * dk * dv + 6 * c * c * dk + 4 * c * c * dv + (2 / 3) * c ** 3)
     s = r["ms_avg"] * 1e-3
-    return {"ms_per_step": r["ms_avg"], "tokens_per_s": t / s, "GB_s": algo / s / 1e9,
-            "hbm_frac": algo / s / 1e9 / HBM_PEAK_GBS, "TFLOP_s": flops / s / 1e12,
-            "bytes_per_launch": algo, "flops_per_launch": flops}
+    res = {"ms_per_step": r["ms_avg"], "tokens_per_s": t / s, "GB_s": algo / s / 1e9,
+           "hbm_frac": algo / s / 1e9 / HBM_PEAK_GBS, "TFLOP_s": flops / s / 1e12,
+           "bytes_per_launch": algo, "flops_per_launch": flops}
+    if cpu_s > 0:
+        state.zero_()  # the timed calls advanced the state: one call from zero for parity
+        fn()
+        torch.cuda.synchronize()
+        h = [x.cpu().numpy() for x in (q, k, v, beta, gg)]
+        with OneCore():
+            n, sec, err = cpu_gdn_tokens(*h, out.cpu().numpy(), cpu_s)
+        per_tok = (2 * hk * dk + 2 * hv * dv + 2 * hv) * 4
+        res["cpu_baseline"] = _cpu(
+            (n * per_tok + 2 * hv * dk * dv * 4) / sec / 1e9, "GB/s",
+            f"or_gdn_tokens (the reference's per-token recurrence) over the first {n} of {t} "
+            f"tokens from a zero state ({n / sec:.1f} tokens/s); bytes counted as the GPU "
+            f"entry's for those tokens", round(sec, 3), tokens_per_s=round(n / sec, 1),
+            full_prompt_s_estimate=round(t * sec / n, 1), parity_max_abs_err=err)
+    return res
 
 
 def _lib_fn(dev, entry, args):
@@ -360,15 +554,42 @@ def _hbm(r, algo):
             "hbm_frac": algo / s / 1e9 / HBM_PEAK_GBS, "bytes_per_launch": algo}
 
 
-def bench_rows_f(torch, rt, dev, timer, steps, warmup):
+def _fp(a, offset=0):
+    """float* into a C-contiguous float32 array, `offset` floats in."""
+    return ctypes.cast(ctypes.c_void_p(a.ctypes.data + 4 * offset), ctypes.POINTER(ctypes.c_float))
+
+
+def _cpu_repeat(fn, budget_s):
+    """Calls fn() until budget_s seconds of it (at least once); returns (seconds, calls)."""
+    t, n = 0.0, 0
+    while n == 0 or t < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        t += time.perf_counter() - t0
+        n += 1
+    return t, n
+
+
+def _cpu_hbm(name, sec, units, unit_bytes, sample, **extra):
+    """A CPU figure in the GPU entry's unit (algorithmic bytes per second)."""
+    return _cpu(units * unit_bytes / sec / 1e9, "GB/s", sample, round(sec, 3),
+                us_per_unit=round(sec / units * 1e6, 3), **extra)
+
+
+def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
     """The steps either side of the path: the fused attention prologue (row f1:
     per-head RMSNorm, RoPE, paged append in one launch) and the GDN conv1d and
-    RMSNormGated (row f2), at a prompt shape (HBM-bound) and a decode step."""
+    RMSNormGated (row f2), at a prompt shape (HBM-bound) and a decode step; and row
+    f3, one layer of `forward` through the host-slice seam.  With cpu_s > 0 every
+    entry also gets the oracle's figure for the same step (cpu_s / 10 seconds each)."""
+    from oracle import oracle as orc  # only for the CPU legs
     P = lambda x: None if x is None else ctypes.c_void_p(x.data_ptr())  # noqa: E731
     lib = dev.lib
     res = {}
     g = torch.Generator(device="cuda")
     g.manual_seed(0x5EED00F1)
+    leg_s = cpu_s / 10.0
+    host = lambda x: None if x is None else x.cpu().numpy()  # noqa: E731
 
     def prologue(n_seq, n_tok, hq, hkv, d, rope_dim, base, sections, norm, start):
         pages = (start + n_tok + 15) // 16
@@ -381,13 +602,34 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup):
         wq = torch.rand((d,), generator=g, device="cuda") + 0.5 if norm else None
         wk = torch.rand((d,), generator=g, device="cuda") + 0.5 if norm else None
         sec = None if sections is None else (ctypes.c_int32 * 4)(*sections)
+        hq_, hk_, wq_, wk_ = host(q), host(k), host(wq), host(wk)  # before the in-place calls
         args = (dev.h, P(q), P(k), P(v), P(wq), P(wk), 1e-6, rope_dim, base, sec, pool.p, P(pt),
                 pages, P(sp), n_seq, n_tok, hq, None)
         r = timer.run(_lib_fn(dev, lib.pi_attn_prologue, args), steps, warmup)
         # q and k read and rewritten (f32), v read, k and v appended (f16)
-        algo = n_seq * n_tok * d * (4 * (2 * hq + 3 * hkv) + 2 * 2 * hkv)
+        per_tok = d * (4 * (2 * hq + 3 * hkv) + 2 * 2 * hkv)
+        out = _hbm(r, n_seq * n_tok * per_tok)
         pool.close()
-        return _hbm(r, algo)
+        if leg_s > 0:
+            freqs = orc.compute_imrope_freqs(base, rope_dim, sections) if sections else None
+            chunk = min(n_tok, 256)
+            done = [0]
+
+            def step():  # or_attn_prepare (src/model/mod.rs:1035-1138) on the next chunk
+                s0 = done[0] % (n_seq * n_tok)
+                b, t0 = divmod(s0, n_tok)
+                m = min(chunk, n_tok - t0)
+                orc.attn_prepare(hq_[b, t0:t0 + m], hk_[b, t0:t0 + m], hq, hkv, d, q_norm_w=wq_,
+                                 k_norm_w=wk_, rope_dim=rope_dim, rope_base=base, freqs=freqs,
+                                 pos0=start + t0)
+                done[0] += m
+            with OneCore():
+                sec_, _ = _cpu_repeat(step, leg_s)
+            out["cpu_baseline"] = _cpu_hbm(
+                "prologue", sec_, done[0], per_tok,
+                f"or_attn_prepare (norm + RoPE) over {done[0]} tokens in chunks of {chunk}; bytes "
+                f"counted as the GPU entry's per token (the reference's append is a Vec copy)")
+        return out
 
     res["f1_prologue_prompt_c3"] = prologue(1, 4096, 32, 8, 128, 128, 1e6, None, False, 0)
     res["f1_prologue_decode_c4"] = prologue(8, 1, 16, 2, 256, 64, 1e7, [11, 11, 10, 0], True,
@@ -397,20 +639,52 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup):
     conv_dim = 2 * hk * dk + hv * dv
     w = torch.randn((conv_dim, d_conv), generator=g, device="cuda") * 0.5
     nw = torch.rand((dv,), generator=g, device="cuda") + 0.5
+    wh, nwh = host(w), host(nw)
     for name, t in (("prompt_c5", 4096), ("decode_step", 1)):
         x = torch.randn((1, t, conv_dim), generator=g, device="cuda")
         cs = torch.randn((1, d_conv - 1, conv_dim), generator=g, device="cuda")
         xo = torch.empty_like(x)
+        xh, csh = host(x), host(cs)
         args = (dev.h, P(x), P(cs), P(w), P(xo), 1, t, conv_dim, d_conv, None)
         r = timer.run(_lib_fn(dev, lib.pi_gdn_conv1d, args), steps, warmup)
         # x read, out written, state read and written, weights read
-        res["f2_gdn_conv1d_" + name] = _hbm(
-            r, (2 * t * conv_dim + 2 * (d_conv - 1) * conv_dim + conv_dim * d_conv) * 4)
+        per_call = (2 * t * conv_dim + 2 * (d_conv - 1) * conv_dim + conv_dim * d_conv) * 4
+        res["f2_gdn_conv1d_" + name] = _hbm(r, per_call)
+        if leg_s > 0:
+            xa = xh.reshape(t, conv_dim).copy()
+            hist = csh.reshape(d_conv - 1, conv_dim).copy()
+            c_lib = orc.lib()
+            pos = [0]
+
+            def conv_tok():  # or_conv1d_silu (src/model/mod.rs:750-776), one token in place
+                c_lib.or_conv1d_silu(_fp(xa, (pos[0] % t) * conv_dim), _fp(hist), _fp(wh),
+                                     conv_dim, d_conv)
+                pos[0] += 1
+            with OneCore():
+                sec_, n = _cpu_repeat(conv_tok, leg_s)
+            res["f2_gdn_conv1d_" + name]["cpu_baseline"] = _cpu_hbm(
+                "conv1d", sec_, n, per_call / t,
+                f"or_conv1d_silu over {n} tokens, one call per token as the reference's loop; "
+                f"bytes counted as the GPU entry's per token")
         o = torch.randn((t, hv, dv), generator=g, device="cuda")
         z = torch.randn((t, hv, dv), generator=g, device="cuda")
+        oh, zh = host(o), host(z)
         args = (dev.h, P(o), P(z), P(nw), t, hv, dv, 1e-6, None)
         r = timer.run(_lib_fn(dev, lib.pi_gdn_rmsnorm_gated, args), steps, warmup)
-        res["f2_gdn_rmsnorm_gated_" + name] = _hbm(r, (3 * t * hv * dv + dv) * 4)
+        per_call = (3 * t * hv * dv + dv) * 4
+        res["f2_gdn_rmsnorm_gated_" + name] = _hbm(r, per_call)
+        if leg_s > 0:
+            oa = oh.copy()
+            c_lib = orc.lib()
+
+            def norm_call():  # or_rmsnorm_gated (src/model/mod.rs:918-932) over every row
+                c_lib.or_rmsnorm_gated(_fp(oa), _fp(zh), _fp(nwh), t * hv, dv, 1e-6)
+            with OneCore():
+                sec_, n = _cpu_repeat(norm_call, leg_s)
+            res["f2_gdn_rmsnorm_gated_" + name]["cpu_baseline"] = _cpu_hbm(
+                "rmsnorm_gated", sec_, n, per_call,
+                f"or_rmsnorm_gated over the {t} x {hv} rows, {n} calls; bytes counted as the "
+                f"GPU entry's")
 
     # row f3: one layer of `forward` through the host-slice seam (synchronous,
     # host <-> device copies of the slices included): wall clock per call
@@ -437,21 +711,63 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup):
                 {"us_per_token": dec * 1e6, "tokens_per_s": 1.0 / dec})
 
     hq, hkv, d = 16, 2, 256
-    lay = rt.AttnLayer(dev, prompt + n_dec + 16, hq, hkv, d, torch.float16,
-                       q_norm_w=rng.uniform(0.5, 1.5, d).astype(f32),
-                       k_norm_w=rng.uniform(0.5, 1.5, d).astype(f32), rope_dim=64,
-                       rope_base=1e7, sections=[11, 11, 10, 0])
+    qn_w = rng.uniform(0.5, 1.5, d).astype(f32)
+    kn_w = rng.uniform(0.5, 1.5, d).astype(f32)
+    lay = rt.AttnLayer(dev, prompt + n_dec + 16, hq, hkv, d, torch.float16, q_norm_w=qn_w,
+                       k_norm_w=kn_w, rope_dim=64, rope_base=1e7, sections=[11, 11, 10, 0])
     qa, ka, va, ga = (rng.standard_normal((prompt, h, d)).astype(f32)
                       for h in (hq, hkv, hkv, hq))
     q1, k1, v1, g1 = (np.ascontiguousarray(x[:1]) for x in (qa, ka, va, ga))
+    raw = [x.copy() for x in (qa, ka, va, ga, q1, k1, v1, g1)]  # the seam rotates q, k in place
     pr, dc = layer_times(lay.reset, lambda: lay.forward(qa, ka, va, ga),
                          lambda: lay.forward(q1, k1, v1, g1))
     res["f3_attn_layer_prompt_1024_c4"] = pr
     res["f3_attn_layer_decode_token_c4"] = dc
     lay.close()
-    gl = rt.GdnLayer(dev, hk, hv, dk, dv, (rng.standard_normal((conv_dim, d_conv)) * 0.5).astype(f32),
-                     -np.exp(rng.standard_normal(hv)).astype(f32),
-                     rng.standard_normal(hv).astype(f32), rng.uniform(0.5, 1.5, dv).astype(f32))
+    if leg_s > 0:
+        freqs = orc.compute_imrope_freqs(1e7, 64, [11, 11, 10, 0])
+        kw = dict(q_norm_w=qn_w, k_norm_w=kn_w, rope_dim=64, rope_base=1e7, freqs=freqs)
+        rq, rk, rv, rg = raw[:4]
+        kc = vc = None
+        n, t = 0, 0.0
+        with OneCore():
+            while n < prompt and t < leg_s:  # or_attn_layer_tokens in chunks of 128 tokens
+                m = min(128, prompt - n)
+                t0 = time.perf_counter()
+                _, kc, vc = orc.attn_layer_tokens(rq[n:n + m], rk[n:n + m], rv[n:n + m],
+                                                  gate=rg[n:n + m], key_cache=kc, value_cache=vc,
+                                                  prev_seq_len=n, **kw)
+                t += time.perf_counter() - t0
+                n += m
+        res["f3_attn_layer_prompt_1024_c4"]["cpu_baseline"] = _cpu(
+            n / t, "tokens/s", f"or_attn_layer_tokens (norm, IMRoPE, append, attention over "
+            f"every cached key, gate; src/model/mod.rs:1035-1196) over the first {n} of "
+            f"{prompt} prompt tokens, 128 per call", round(t, 3))
+        # one decode token after those n: the C loop into caches with room for it
+        kcap = np.zeros((n + 1, hkv, d), f32)
+        vcap = np.zeros((n + 1, hkv, d), f32)
+        kcap[:n], vcap[:n] = kc[:n], vc[:n]
+        o1 = np.zeros((1, hq, d), f32)
+        qx, kx = raw[4].copy(), raw[5].copy()
+        fr = np.ascontiguousarray(freqs, f32)
+        c_lib = orc.lib()
+
+        def dec_tok():
+            qx[:], kx[:] = raw[4], raw[5]
+            c_lib.or_attn_layer_tokens(_fp(o1), _fp(qx), _fp(raw[7]), _fp(kx), _fp(raw[6]), 1, hq,
+                                       hkv, d, d, d, _fp(qn_w), _fp(kn_w), 1e-6, 64, 1e7, _fp(fr),
+                                       fr.size, _fp(kcap), _fp(vcap), n)
+        with OneCore():
+            sec_, m = _cpu_repeat(dec_tok, leg_s)
+        res["f3_attn_layer_decode_token_c4"]["cpu_baseline"] = _cpu(
+            m / sec_, "tokens/s", f"or_attn_layer_tokens for one token after {n} cached, {m} "
+            f"calls", round(sec_, 3), us_per_token=round(sec_ / m * 1e6, 2))
+
+    conv_w = (rng.standard_normal((conv_dim, d_conv)) * 0.5).astype(f32)
+    ssm_a = -np.exp(rng.standard_normal(hv)).astype(f32)
+    dt_b = rng.standard_normal(hv).astype(f32)
+    gn_w = rng.uniform(0.5, 1.5, dv).astype(f32)
+    gl = rt.GdnLayer(dev, hk, hv, dk, dv, conv_w, ssm_a, dt_b, gn_w)
     xa = rng.standard_normal((prompt, conv_dim)).astype(f32)
     za = rng.standard_normal((prompt, hv, dv)).astype(f32)
     ba, aa = (rng.standard_normal((prompt, hv)).astype(f32) for _ in range(2))
@@ -461,6 +777,44 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup):
     res["f3_gdn_layer_prompt_1024_c5"] = pr
     res["f3_gdn_layer_decode_token_c5"] = dc
     gl.close()
+    if leg_s > 0:
+        kd, vd = hk * dk, hv * dv
+        c_lib = orc.lib()
+
+        def gdn_chain(x, z, br, ar, hist, state):
+            """src/model/mod.rs:750-932 for x.shape[0] tokens: conv1d + SiLU per token, the
+            q / k / v split, gates, the per-token recurrence, RMSNormGated x SiLU(z)."""
+            act = x.copy()
+            for i in range(act.shape[0]):
+                c_lib.or_conv1d_silu(_fp(act, i * conv_dim), _fp(hist), _fp(conv_w), conv_dim,
+                                     d_conv)
+            m = act.shape[0]
+            q = act[:, :kd].reshape(m, hk, dk)
+            k = act[:, kd:2 * kd].reshape(m, hk, dk)
+            v = act[:, 2 * kd:].reshape(m, hv, dv)
+            beta, gg = orc.gdn_gates(br, ar, ssm_a, dt_b)
+            o, state = orc.gdn_tokens(q, k, v, beta, gg, state)
+            return orc.rmsnorm_gated(o, z, gn_w, 1e-6), state
+
+        hist = np.zeros((d_conv - 1, conv_dim), f32)
+        state = None
+        n, t = 0, 0.0
+        with OneCore():
+            while n < prompt and t < leg_s:
+                m = min(64, prompt - n)
+                t0 = time.perf_counter()
+                _, state = gdn_chain(xa[n:n + m], za[n:n + m], ba[n:n + m], aa[n:n + m], hist,
+                                     state)
+                t += time.perf_counter() - t0
+                n += m
+            res["f3_gdn_layer_prompt_1024_c5"]["cpu_baseline"] = _cpu(
+                n / t, "tokens/s", f"the oracle's GDN layer chain (or_conv1d_silu per token, "
+                f"or_gdn_gates, or_gdn_tokens, or_rmsnorm_gated) over the first {n} of {prompt} "
+                f"prompt tokens, 64 per call", round(t, 3))
+            sec_, m = _cpu_repeat(lambda: gdn_chain(x1, z1, b1, a1, hist.copy(), state), leg_s)
+        res["f3_gdn_layer_decode_token_c5"]["cpu_baseline"] = _cpu(
+            m / sec_, "tokens/s", f"the oracle's GDN layer chain for one token, {m} calls",
+            round(sec_, 3), us_per_token=round(sec_ / m * 1e6, 2))
     return res
 
 
@@ -526,6 +880,11 @@ def _single(torch, rt, dev, timer, a):
     return bench_gdn_decode(torch, rt, dev, timer, st, wu)
 
 
+def _rounded(d):
+    return {k: (round(v, 4) if isinstance(v, float) else _rounded(v) if isinstance(v, dict) else v)
+            for k, v in d.items()}
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -542,14 +901,19 @@ def main():
                           **_single(torch, rt, dev, timer, a)}), flush=True)
         return
 
+    # CPU baseline budget (seconds of single-core oracle work) per workload
+    cs = a.cpu_seconds
+    share = {"c2": 0.25, "c2_32k": 0.04, "c3": 0.15, "c4": 0.1, "c1": 0.03, "gdn_dec": 0.04,
+             "gdn_pre": 0.1, "tq": 0.07, "rows_f": 0.22}
+    budget = {k: v * cs for k, v in share.items()}
+    t_all0 = time.perf_counter()
+
     # ---- headline: config 2 decode ----
     rng = np.random.default_rng(0x5EED0001)
     lens = [int(x) for x in rng.integers(1024, 32769, size=32)]
     c2, state = bench_decode(torch, rt, dev, timer, lens, 32, 8, 128, 1e6, 0x5EED0001, a.steps,
-                             a.warmup)
-    t_cpu0 = time.perf_counter()
-    cpu = cpu_baseline_decode(torch, rt, dev, state, lens, 32, 8, 128, a.cpu_seconds)
-    cpu_wall = time.perf_counter() - t_cpu0
+                             a.warmup, cpu_s=budget["c2"])
+    cpu = c2.pop("cpu_baseline")
     del state
     torch.cuda.empty_cache()
 
@@ -575,20 +939,21 @@ def main():
                      "unit": "GB/s", "frac": round(c2["hbm_frac"], 4),
                      "traffic": _traffic("decode_kernel_c2",
                                          ["decode_kernel<f16,128,2>", "decode_merge_kernel"])},
-        "cpu_baseline": {k: (round(v, 4) if isinstance(v, float) else v)
-                         for k, v in cpu.items()},
+        "cpu_baseline": {**{k: (round(v, 4) if isinstance(v, float) else v)
+                            for k, v in cpu.items()}, **cpu_info(),
+                         "pinned": "os.sched_setaffinity to one core for the oracle calls"},
     }
 
     if not a.only_headline:
         wl = {}
         # config 2 with every context at 32768 (the "at 32k ctx" reading of the metric)
         r32, st = bench_decode(torch, rt, dev, timer, [32768] * 32, 32, 8, 128, 1e6,
-                               0x5EED0011, a.steps, a.warmup)
+                               0x5EED0011, a.steps, a.warmup, cpu_s=budget["c2_32k"])
         del st
         torch.cuda.empty_cache()
         wl["c2_all_32k_decode"] = r32
         pf = bench_prefill(torch, rt, dev, timer, 4096, 32, 8, 128, 1e6, 0x5EED0002, a.steps,
-                           a.warmup)
+                           a.warmup, cpu_s=budget["c3"])
         torch.cuda.empty_cache()
         line["prefill"] = {"workload": "config 3: Qwen3-8B causal prefill, S 4096, 32/8 heads, "
                                        "head_dim 128, bf16 in, f32 softmax/accumulate",
@@ -597,27 +962,31 @@ def main():
                                         "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                         "frac": round(pf["mfma_frac"], 4)},
                            "ms_per_step": round(pf["ms_per_step"], 4),
-                           "tokens_per_s": round(pf["tokens_per_s"], 1)}
+                           "tokens_per_s": round(pf["tokens_per_s"], 1),
+                           "cpu_baseline": pf["cpu_baseline"]}
         r4, st = bench_decode(torch, rt, dev, timer, [65536] * 8, 16, 2, 256, 1e7, 0x5EED0003,
                               a.steps, a.warmup, sections=[11, 11, 10, 0], rope_dim=64,
-                              qk_norm=True, gate=True)
+                              qk_norm=True, gate=True, cpu_s=budget["c4"])
         del st
         torch.cuda.empty_cache()
         wl["c4_gated_decode_64k"] = r4
         r1, st = bench_decode(torch, rt, dev, timer, [513], 32, 32, 128, 1e4, 0x5EED0000,
-                              a.steps, a.warmup, pool_dtype=torch.float32)
+                              a.steps, a.warmup, pool_dtype=torch.float32, cpu_s=budget["c1"])
         del st
         wl["c1_mha_decode_513"] = r1
-        wl["c5_gdn_decode_step"] = bench_gdn_decode(torch, rt, dev, timer, a.steps, a.warmup)
-        wl["c5_gdn_prefill_4096"] = bench_gdn_prefill(torch, rt, dev, timer, a.steps, a.warmup)
+        wl["c5_gdn_decode_step"] = bench_gdn_decode(torch, rt, dev, timer, a.steps, a.warmup,
+                                                    cpu_s=budget["gdn_dec"])
+        wl["c5_gdn_prefill_4096"] = bench_gdn_prefill(torch, rt, dev, timer, a.steps, a.warmup,
+                                                      cpu_s=budget["gdn_pre"])
         torch.cuda.empty_cache()
         # TurboQuant compressed-KV decode on the config 2 shape (3-bit + QJL keys, f16 values)
         wl["c2_turboquant_decode"] = bench_tq_decode(torch, rt, dev, timer, lens, 32, 8, 0x5EED0004,
-                                                     a.steps, a.warmup)
-        wl.update(bench_rows_f(torch, rt, dev, timer, a.steps, a.warmup))
-        line["workloads"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
-                                 for kk, vv in v.items()} for k, v in wl.items()}
-    line["cpu_baseline_wall_s"] = round(cpu_wall, 2)
+                                                     a.steps, a.warmup, cpu_s=budget["tq"])
+        wl.update(bench_rows_f(torch, rt, dev, timer, a.steps, a.warmup,
+                               cpu_s=budget["rows_f"]))
+        line["workloads"] = {k: _rounded(v) for k, v in wl.items()}
+        line["prefill"] = _rounded(line["prefill"])
+    line["bench_wall_s"] = round(time.perf_counter() - t_all0, 2)
     print(json.dumps(line), flush=True)
     dev.close()
 
