@@ -442,20 +442,47 @@ def bench_prefill(torch, rt, dev, timer, s, hq, hkv, d, theta, seed, steps, warm
     return res
 
 
-def bench_gdn_decode(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
+def graph_us_per_call(torch, fn, n_calls=64, replays=50):
+    """Microseconds per call of `fn` when n_calls of it are captured in one HIP graph and
+    the graph is replayed (the launch cost a serving loop with graphs pays per step)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr, stream=side):
+            for _ in range(n_calls):
+                fn()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        gr.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        gr.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (replays * n_calls) * 1e3
+
+
+def bench_gdn_decode(torch, rt, dev, timer, steps, warmup, cpu_s=0.0, batch=1, graph=True):
+    """Config 5 decode step(s): pi_gdn_decode on `batch` sequences (one token each)."""
     hk, hv, dk, dv = 16, 32, 128, 128
     g = torch.Generator(device="cuda")
     g.manual_seed(0x5EED0004)
-    q = torch.randn((1, hk, dk), generator=g, device="cuda")
-    k = torch.randn((1, hk, dk), generator=g, device="cuda")
-    v = torch.randn((1, hv, dv), generator=g, device="cuda")
-    beta = torch.sigmoid(torch.randn((1, hv), generator=g, device="cuda"))
-    gg = -torch.nn.functional.softplus(torch.randn((1, hv), generator=g, device="cuda"))
-    state = torch.zeros((1, hv, dk, dv), device="cuda")
-    out = torch.empty((1, hv, dv), device="cuda")
+    q = torch.randn((batch, hk, dk), generator=g, device="cuda")
+    k = torch.randn((batch, hk, dk), generator=g, device="cuda")
+    v = torch.randn((batch, hv, dv), generator=g, device="cuda")
+    beta = torch.sigmoid(torch.randn((batch, hv), generator=g, device="cuda"))
+    gg = -torch.nn.functional.softplus(torch.randn((batch, hv), generator=g, device="cuda"))
+    state = torch.zeros((batch, hv, dk, dv), device="cuda")
+    out = torch.empty((batch, hv, dv), device="cuda")
     lib = dev.lib
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    args = (dev.h, P(q), P(k), P(v), P(beta), P(gg), P(state), P(out), 1, hk, hv, dk, dv, None)
+    args = [dev.h, P(q), P(k), P(v), P(beta), P(gg), P(state), P(out), batch, hk, hv, dk, dv,
+            None]
 
     def fn():
         rc = lib.pi_gdn_decode(*args)
@@ -463,28 +490,44 @@ def bench_gdn_decode(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
             raise RuntimeError(lib.pi_last_error(dev.h).decode())
 
     t = timer.run(fn, steps, warmup)
-    algo = 2 * hv * dk * dv * 4 + (2 * hk * dk + 2 * hv * dv + 2 * hv) * 4
+    algo = batch * (2 * hv * dk * dv * 4 + (2 * hk * dk + 2 * hv * dv + 2 * hv) * 4)
     gbs = algo / (t["ms_avg"] * 1e-3) / 1e9
-    res = {"us_per_step": t["ms_avg"] * 1e3, "tokens_per_s": 1e3 / t["ms_avg"], "GB_s": gbs,
+    res = {"batch": batch, "us_per_step": t["ms_avg"] * 1e3,
+           "tokens_per_s": batch * 1e3 / t["ms_avg"], "GB_s": gbs,
            "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_launch": algo}
+    if graph:
+        # the same step launched from a captured graph of 64 steps, on the capture stream
+        args[-1] = ctypes.c_void_p(0)
+
+        def fn_cur():
+            args[-1] = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            fn()
+        us = graph_us_per_call(torch, fn_cur)
+        args[-1] = None
+        res.update({"us_per_step_graph": us, "GB_s_graph": algo / us / 1e3,
+                    "hbm_frac_graph": algo / us / 1e3 / HBM_PEAK_GBS})
     if cpu_s > 0:
         # the timed calls advanced the state: one GPU step from zero for the parity figure
         state.zero_()
         fn()
         torch.cuda.synchronize()
-        h = [x.cpu().numpy() for x in (q, k, v, beta, gg)]
-        reps = 256  # the same token as 256 consecutive steps (the reference's per-token loop)
+        # sequence 0's token as 256 consecutive steps (the reference's per-token loop); every
+        # sequence of a batch costs the reference the same, one after another
+        h = [x[:1].cpu().numpy() for x in (q, k, v, beta, gg)]
+        o_gpu = out[:1].cpu().numpy()
+        reps = 256
         with OneCore():
             n, sec, _ = cpu_gdn_tokens(*[np.repeat(x, reps, axis=0) for x in h],
-                                       np.repeat(out.cpu().numpy(), reps, axis=0), cpu_s)
+                                       np.repeat(o_gpu, reps, axis=0), cpu_s)
         from oracle import oracle as orc
         o1, _ = orc.gdn_tokens(*h)
         res["cpu_baseline"] = _cpu(
-            n * algo / sec / 1e9, "GB/s",
-            f"or_gdn_tokens: {n} steps from a zero state, per step {sec / n * 1e6:.1f} us "
-            f"({n / sec:.1f} tokens/s); bytes counted as the GPU entry's (state read + write, "
-            f"q, k, v, beta, g, out)", round(sec, 3), us_per_step=round(sec / n * 1e6, 2),
-            parity_max_abs_err=float(np.abs(o1 - out.cpu().numpy()).max()))
+            n * (algo / batch) / sec / 1e9, "GB/s",
+            f"or_gdn_tokens: {n} steps of one sequence from a zero state, per sequence step "
+            f"{sec / n * 1e6:.1f} us ({n / sec:.1f} tokens/s); bytes counted as the GPU entry's "
+            f"per sequence (state read + write, q, k, v, beta, g, out)", round(sec, 3),
+            us_per_step=round(sec / n * 1e6 * batch, 2),
+            parity_max_abs_err=float(np.abs(o1 - o_gpu).max()))
     return res
 
 
@@ -976,6 +1019,10 @@ def main():
         wl["c1_mha_decode_513"] = r1
         wl["c5_gdn_decode_step"] = bench_gdn_decode(torch, rt, dev, timer, a.steps, a.warmup,
                                                     cpu_s=budget["gdn_dec"])
+        # 32 sequences per step: the state stream of a serving batch
+        wl["c5_gdn_decode_step_batch32"] = bench_gdn_decode(torch, rt, dev, timer, a.steps,
+                                                            a.warmup, batch=32, graph=False,
+                                                            cpu_s=budget["gdn_dec"] / 2)
         wl["c5_gdn_prefill_4096"] = bench_gdn_prefill(torch, rt, dev, timer, a.steps, a.warmup,
                                                       cpu_s=budget["gdn_pre"])
         torch.cuda.empty_cache()

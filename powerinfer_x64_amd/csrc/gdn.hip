@@ -7,9 +7,8 @@
 // on a per-head fp32 state S[k_hd][v_hd] (row k, v contiguous).
 //
 // Decode: state columns evolve independently (delta[v] only reads column v),
-// so a workgroup owns (sequence, V head, 32 state columns): 8 row groups of
-// 32 lanes; each thread keeps 16 state values in registers, and the two
-// column sums (S^T k and S^T q) are reduced across the row groups in LDS.
+// so a workgroup owns (sequence, V head, 32 state columns) and streams that
+// tile of the state once in and once out (gdn_decode_kernel).
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -18,9 +17,6 @@ namespace {
 
 constexpr int DK = 128;
 constexpr int DV = 128;
-constexpr int COLS = 32;             // state columns per decode workgroup
-constexpr int RG = 256 / COLS;       // row groups (8)
-constexpr int RPT = DK / RG;         // state rows per thread (16)
 
 __global__ __launch_bounds__(256) void gdn_gates_kernel(const float* __restrict__ beta_raw,
                                                         const float* __restrict__ a_raw,
@@ -202,16 +198,14 @@ __global__ __launch_bounds__(256) void gdn_rmsnorm_gated_kernel(float* __restric
     }
 }
 
-// Block-wide sum of one value per thread; all threads get the result.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = wave_sum_xor(v, m);
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
+// Decode step.  A workgroup owns (sequence, V head, 32 state columns): a
+// 128 x 32 tile of the state, 16 KB, whose rows are 128-byte lines.  Thread t
+// holds rows t/8 + 32 i (i < 4), columns 4 (t % 8) .. +3, as four 16-byte
+// loads issued before anything else, so the step costs one memory round trip.
+// Every wavefront computes the q / k norms itself with shuffles (no barrier);
+// the two column sums (S^T k, then S^T q after the update) reduce over a
+// wavefront's rows with shuffles and over the 4 wavefronts in LDS.
+constexpr int DCOLS = 32;  // state columns per decode workgroup
 
 __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict__ q,
                                                          const float* __restrict__ k,
@@ -221,61 +215,80 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict
                                                          float* __restrict__ state,
                                                          float* __restrict__ out, int hk,
                                                          int hv) {
-    __shared__ float s_q[DK], s_k[DK];
-    __shared__ float s_red[4];
-    __shared__ float s_part[2][RG][COLS];
-    const int tid = threadIdx.x;
-    const int c0 = blockIdx.x * COLS;
-    const int vh = blockIdx.y;
-    const int b = blockIdx.z;
-    const int kh = vh % hk;
+    __shared__ __attribute__((aligned(16))) float s_part[2][4][DCOLS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c0 = blockIdx.x * DCOLS;
+    const int vh = blockIdx.y, b = blockIdx.z;
+    const int kh = vh % hk;  // K head tiled onto this V head (src/model/mod.rs:845-853)
+    const int cg = tid & 7, rr = tid >> 3;
+    const size_t sh = (size_t)b * hv + vh;
+    float* S = state + sh * DK * DV + c0 + 4 * cg;
+    f32x4 s[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = *reinterpret_cast<const f32x4*>(S + (size_t)(rr + 32 * i) * DV);
 
-    // q/k of the tiled K head, L2-normalised (src/model/mod.rs:855-875)
+    // q / k of the K head, L2-normalised with max(|x|, 1e-12); q also / sqrt(Dk)
+    // (src/model/mod.rs:855-875).  Lane l holds rows l and l + 64.
     const float* qr = q + ((size_t)b * hk + kh) * DK;
     const float* kr = k + ((size_t)b * hk + kh) * DK;
-    const float xq = tid < DK ? qr[tid] : 0.f;
-    const float xk = tid < DK ? kr[tid] : 0.f;
-    const float nq = fmaxf(sqrtf(block_sum(xq * xq, s_red)), 1e-12f);
-    const float nk = fmaxf(sqrtf(block_sum(xk * xk, s_red)), 1e-12f);
-    if (tid < DK) {
-        s_q[tid] = xq / nq * (1.0f / sqrtf((float)DK));
-        s_k[tid] = xk / nk;
+    const float q0 = qr[lane], q1 = qr[lane + 64], k0 = kr[lane], k1 = kr[lane + 64];
+    const f32x4 vv = *reinterpret_cast<const f32x4*>(v + sh * DV + c0 + 4 * cg);
+    const float decay = expf(g[sh]), bt = beta[sh];
+    float sq = q0 * q0 + q1 * q1, sk = k0 * k0 + k1 * k1;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        sq = wave_sum_xor(sq, m);
+        sk = wave_sum_xor(sk, m);
     }
-    __syncthreads();
+    const float nq = fmaxf(sqrtf(sq), 1e-12f), nk = fmaxf(sqrtf(sk), 1e-12f);
+    const float qs = 1.0f / sqrtf((float)DK);
+    // this thread's rows rr, rr + 32 (first halves) and rr + 64, rr + 96 (second)
+    float kn[4], qn[4];
+    kn[0] = __shfl(k0, rr, 64) / nk;
+    kn[1] = __shfl(k0, rr + 32, 64) / nk;
+    kn[2] = __shfl(k1, rr, 64) / nk;
+    kn[3] = __shfl(k1, rr + 32, 64) / nk;
+    qn[0] = __shfl(q0, rr, 64) / nq * qs;
+    qn[1] = __shfl(q0, rr + 32, 64) / nq * qs;
+    qn[2] = __shfl(q1, rr, 64) / nq * qs;
+    qn[3] = __shfl(q1, rr + 32, 64) / nq * qs;
 
-    const int c = tid % COLS, rg = tid / COLS;
-    const size_t sh = ((size_t)b * hv + vh);
-    float* S = state + sh * DK * DV + c0 + c;
-    const float decay = expf(g[sh]);
-    float s[RPT];
-    float kv = 0.f;
+    // S *= exp(g); kv_mem = S^T k (src/model/mod.rs:883-898)
+    f32x4 kv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-        const int row = rg * RPT + i;
-        s[i] = S[(size_t)row * DV] * decay;
-        kv += s[i] * s_k[row];
+    for (int i = 0; i < 4; ++i) {
+        s[i] *= decay;
+        kv += s[i] * kn[i];
     }
-    s_part[0][rg][c] = kv;
+#pragma unroll
+    for (int m = 8; m <= 32; m <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kv[c] = wave_sum_xor(kv[c], m);
+    if (lane < 8) *reinterpret_cast<f32x4*>(&s_part[0][wave][4 * lane]) = kv;
     __syncthreads();
-    float kv_mem = 0.f;
+    f32x4 kv_mem = *reinterpret_cast<const f32x4*>(&s_part[0][0][4 * cg]);
 #pragma unroll
-    for (int r = 0; r < RG; ++r) kv_mem += s_part[0][r][c];
-    const float delta = (v[sh * DV + c0 + c] - kv_mem) * beta[sh];
-    float o = 0.f;
+    for (int w = 1; w < 4; ++w) kv_mem += *reinterpret_cast<const f32x4*>(&s_part[0][w][4 * cg]);
+    // delta = (v - kv_mem) beta; S += k delta^T; o = S^T q (:899-916)
+    const f32x4 delta = (vv - kv_mem) * bt;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-        const int row = rg * RPT + i;
-        s[i] += s_k[row] * delta;
-        o += s[i] * s_q[row];
-        S[(size_t)row * DV] = s[i];
+    for (int i = 0; i < 4; ++i) {
+        s[i] += kn[i] * delta;
+        o += s[i] * qn[i];
+        *reinterpret_cast<f32x4*>(S + (size_t)(rr + 32 * i) * DV) = s[i];
     }
-    s_part[1][rg][c] = o;
-    __syncthreads();
-    if (rg == 0) {
-        float acc = 0.f;
 #pragma unroll
-        for (int r = 0; r < RG; ++r) acc += s_part[1][r][c];
-        out[sh * DV + c0 + c] = acc;
+    for (int m = 8; m <= 32; m <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = wave_sum_xor(o[c], m);
+    if (lane < 8) *reinterpret_cast<f32x4*>(&s_part[1][wave][4 * lane]) = o;
+    __syncthreads();
+    if (tid < 8) {
+        f32x4 acc = *reinterpret_cast<const f32x4*>(&s_part[1][0][4 * tid]);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) acc += *reinterpret_cast<const f32x4*>(&s_part[1][w][4 * tid]);
+        *reinterpret_cast<f32x4*>(out + sh * DV + c0 + 4 * tid) = acc;
     }
 }
 
@@ -923,7 +936,7 @@ hipError_t launch_gdn_rmsnorm_gated(float* o, const float* z, const float* w, in
 hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, const float* beta,
                              const float* g, float* state, float* out, int32_t batch,
                              int32_t n_k_heads, int32_t n_v_heads, hipStream_t s) {
-    hipLaunchKernelGGL(gdn_decode_kernel, dim3(DV / COLS, n_v_heads, batch), dim3(256), 0, s, q, k,
+    hipLaunchKernelGGL(gdn_decode_kernel, dim3(DV / DCOLS, n_v_heads, batch), dim3(256), 0, s, q, k,
                        v, beta, g, state, out, n_k_heads, n_v_heads);
     return hipGetLastError();
 }
