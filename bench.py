@@ -52,7 +52,7 @@ def _args():
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--workload", default=None,
                    choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "tq", "copy",
-                            "rows_f"],
+                            "rows_f", "chunk"],
                    help="time one workload only and print its figures (for sweeps)")
     return p.parse_args()
 
@@ -861,6 +861,137 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
     return res
 
 
+def bench_chunk(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
+    """Row f3's continued chunk: a 1024-token chunk of an attention layer (config-4 layer
+    shape: 16/2 heads, D 256, q/k RMSNorm, IMRoPE, gate, f16 cache) continuing an 8192-token
+    sequence, against a fresh 1024-token prompt.  Timed as device steps (pi_attn_layer_forward_dev,
+    HIP events) and through the host-slice seam (wall clock, copies included); plus the
+    paged prefill kernel alone on the config-2 heads (gather included)."""
+    from oracle import oracle as orc  # only for the CPU leg
+    rng = np.random.default_rng(0x5EED0C4)
+    f32 = np.float32
+    hq, hkv, d, hist, n = 16, 2, 256, 8192, 1024
+    qn_w = rng.uniform(0.5, 1.5, d).astype(f32)
+    kn_w = rng.uniform(0.5, 1.5, d).astype(f32)
+    kw = dict(q_norm_w=qn_w, k_norm_w=kn_w, rope_dim=64, rope_base=1e7, sections=[11, 11, 10, 0])
+    lay = rt.AttnLayer(dev, hist + n + 16, hq, hkv, d, torch.float16, **kw)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED0C5)
+    rnd = lambda *shape: torch.randn(shape, generator=g, device="cuda")  # noqa: E731
+    hq_, hk_, hv_ = rnd(hist, hq, d), rnd(hist, hkv, d), rnd(hist, hkv, d)
+    cq, ck, cv, cg = rnd(n, hq, d), rnd(n, hkv, d), rnd(n, hkv, d), rnd(n, hq, d)
+    out = torch.empty((n, hq, d), device="cuda")
+    res = {}
+
+    def dev_time(prefix):  # GPU time of one chunk step after a prefix of `prefix` tokens
+        ts = []
+        for rep in range(warmup + steps):
+            lay.reset()
+            if prefix:
+                lay.forward_dev(hq_[:prefix].clone(), hk_[:prefix].clone(), hv_[:prefix])
+            q, k = cq.clone(), ck.clone()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            lay.forward_dev(q, k, cv, gate=cg, out=out)
+            b.record()
+            torch.cuda.synchronize()
+            if rep >= warmup:
+                ts.append(a.elapsed_time(b))
+        return float(np.median(ts))
+    fresh_ms = dev_time(0)
+    chunk_ms = dev_time(hist)
+    flops_chunk = 4.0 * hq * d * n * (hist + (n + 1) / 2)
+    flops_fresh = 4.0 * hq * d * n * (n + 1) / 2
+    res["f3_attn_layer_prompt_1024_c4_device"] = {
+        "ms_per_call": fresh_ms, "tokens_per_s": n / fresh_ms * 1e3,
+        "attn_TFLOP_s": flops_fresh / fresh_ms / 1e9}
+    res["f3_attn_layer_chunk_1024_over_8192_c4_device"] = {
+        "ms_per_call": chunk_ms, "tokens_per_s": n / chunk_ms * 1e3,
+        "attn_TFLOP_s": flops_chunk / chunk_ms / 1e9, "vs_fresh_prompt": chunk_ms / fresh_ms,
+        "flops_vs_fresh_prompt": flops_chunk / flops_fresh}
+    # through the host-slice seam (copies of the slices both ways, synchronous)
+    hh = [x.cpu().numpy() for x in (hq_, hk_, hv_)]
+    ch = [x.cpu().numpy() for x in (cq, ck, cv, cg)]
+    walls = {}
+    for name, prefix in (("fresh", 0), ("chunk", hist)):
+        ts = []
+        for rep in range(4):
+            lay.reset()
+            if prefix:
+                lay.forward(hh[0].copy(), hh[1].copy(), hh[2])
+            q, k = ch[0].copy(), ch[1].copy()
+            t0 = time.perf_counter()
+            lay.forward(q, k, ch[2], gate=ch[3])
+            if rep >= 1:
+                ts.append(time.perf_counter() - t0)
+        walls[name] = float(np.median(ts)) * 1e3
+    res["f3_attn_layer_chunk_1024_over_8192_c4"] = {
+        "ms_per_call": walls["chunk"], "tokens_per_s": n / walls["chunk"] * 1e3,
+        "fresh_prompt_ms_per_call": walls["fresh"], "vs_fresh_prompt": walls["chunk"] / walls["fresh"]}
+    if cpu_s > 0:
+        # the reference's per-token loop for the first tokens of the chunk over the 8192 history
+        freqs = orc.compute_imrope_freqs(1e7, 64, [11, 11, 10, 0])
+        okw = dict(q_norm_w=qn_w, k_norm_w=kn_w, rope_dim=64, rope_base=1e7, freqs=freqs)
+        # the history's cache: K normalised and rotated at 0 .. 8191 (no attention needed)
+        _, kc = orc.attn_prepare(None, hh[1], hq, hkv, d, k_norm_w=kn_w, rope_dim=64,
+                                 rope_base=1e7, freqs=freqs, pos0=0)
+        vc = hh[2]
+        m, t = 0, 0.0
+        with OneCore():
+            while m < n and t < cpu_s:
+                t0 = time.perf_counter()
+                _, kc, vc = orc.attn_layer_tokens(ch[0][m:m + 4], ch[1][m:m + 4], ch[2][m:m + 4],
+                                                  gate=ch[3][m:m + 4], key_cache=kc, value_cache=vc,
+                                                  prev_seq_len=hist + m, **okw)
+                t += time.perf_counter() - t0
+                m += 4
+        cpu = _cpu(m / t, "tokens/s", f"or_attn_layer_tokens for the first {m} tokens of the "
+                   f"chunk over the {hist}-token history, 4 per call", round(t, 3))
+        res["f3_attn_layer_chunk_1024_over_8192_c4"]["cpu_baseline"] = cpu
+        res["f3_attn_layer_chunk_1024_over_8192_c4_device"]["cpu_baseline"] = cpu
+        res["f3_attn_layer_prompt_1024_c4_device"]["cpu_baseline"] = dict(
+            cpu, sample="the same CPU figure (tokens of a chunk after 8192 cached); a fresh "
+                        "prompt's first tokens attend fewer keys")
+    lay.close()
+
+    # the paged prefill kernel alone: config-2 heads, 1024 queries over 8192 + 1024 keys
+    hq, hkv, d = 32, 8, 128
+    pages = (hist + n) // 16
+    pool = rt.KvPool(dev, pages + 8, hkv, d, torch.float16)
+    row = torch.from_numpy(np.random.default_rng(1).permutation(pages + 8)[:pages].astype(np.int32)).cuda()
+    k = rnd(hist + n, hkv, d)
+    v = rnd(hist + n, hkv, d)
+    pool.append(k[None], v[None], row[None].contiguous(), torch.zeros(1, dtype=torch.int32, device="cuda"))
+    q16 = rnd(n, hq, d).half()
+    o = torch.empty((n, hq, d), device="cuda")
+    P = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    args = (dev.h, P(q16), pool.p, P(row), pages, hist, n, hq, 0, 1.0 / math.sqrt(d), P(o), None)
+    r = timer.run(_lib_fn(dev, dev.lib.pi_attn_prefill_paged, args), steps, warmup)
+    fl = 4.0 * hq * d * n * (hist + (n + 1) / 2)
+    tf = fl / (r["ms_avg"] * 1e-3) / 1e12
+    res["c2_prefill_paged_1024_over_8192"] = {"TFLOP_s": tf, "mfma_frac": tf / MFMA_F16_PEAK_TFLOPS,
+                                              "ms_per_step": r["ms_avg"], "flops_per_launch": fl}
+    if cpu_s > 0:
+        kf = k.cpu().numpy().astype(np.float16).astype(np.float32)
+        vf = v.cpu().numpy().astype(np.float16).astype(np.float32)
+        qf = q16.float().cpu().numpy()
+        oh = o.cpu().numpy()
+        t, fl_done, i, err = 0.0, 0.0, n - 1, 0.0
+        with OneCore():
+            while i >= 0 and t < cpu_s:
+                t0 = time.perf_counter()
+                ref = orc.attn_decode(qf[i], kf[:hist + i + 1], vf[:hist + i + 1])
+                t += time.perf_counter() - t0
+                fl_done += 4.0 * hq * d * (hist + i + 1)
+                err = max(err, _row_rel(oh[i], ref))
+                i -= 97
+        res["c2_prefill_paged_1024_over_8192"]["cpu_baseline"] = _cpu(
+            fl_done / t / 1e12, "TFLOP/s", f"or_attn_decode on rows {n - 1}, {n - 98}, ... of the "
+            f"chunk over their {hist}+ keys", round(t, 3), parity_max_row_rel_err=round(err, 6))
+    pool.close()
+    return res
+
+
 def bench_copy(torch, timer, steps, warmup, nbytes=1 << 30):
     """A plain device copy of known size: the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters, and the practical HBM ceiling."""
@@ -920,6 +1051,8 @@ def _single(torch, rt, dev, timer, a):
         return bench_copy(torch, timer, st, wu)
     if w == "rows_f":
         return bench_rows_f(torch, rt, dev, timer, st, wu)
+    if w == "chunk":
+        return bench_chunk(torch, rt, dev, timer, st, wu)
     return bench_gdn_decode(torch, rt, dev, timer, st, wu)
 
 
@@ -947,7 +1080,7 @@ def main():
     # CPU baseline budget (seconds of single-core oracle work) per workload
     cs = a.cpu_seconds
     share = {"c2": 0.25, "c2_32k": 0.04, "c3": 0.15, "c4": 0.1, "c1": 0.03, "gdn_dec": 0.04,
-             "gdn_pre": 0.1, "tq": 0.07, "rows_f": 0.22}
+             "gdn_pre": 0.1, "tq": 0.07, "rows_f": 0.2, "chunk": 0.04}
     budget = {k: v * cs for k, v in share.items()}
     t_all0 = time.perf_counter()
 
@@ -1031,6 +1164,8 @@ def main():
                                                      a.steps, a.warmup, cpu_s=budget["tq"])
         wl.update(bench_rows_f(torch, rt, dev, timer, a.steps, a.warmup,
                                cpu_s=budget["rows_f"]))
+        wl.update(bench_chunk(torch, rt, dev, timer, min(a.steps, 10), min(a.warmup, 3),
+                              cpu_s=budget["chunk"]))
         line["workloads"] = {k: _rounded(v) for k, v in wl.items()}
         line["prefill"] = _rounded(line["prefill"])
     line["bench_wall_s"] = round(time.perf_counter() - t_all0, 2)

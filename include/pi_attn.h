@@ -166,6 +166,20 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
                     int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale, float* d_out,
                     void* stream);
 
+/* Causal prefill of a chunk that continues a sequence, over its paged cache
+ * (src/model/mod.rs:668 token loop over :1140-1190 with prev_seq_len =
+ * start_pos): query row i sits at position start_pos + i and attends keys
+ * 0 .. start_pos + i, read from the f16 pool through the sequence's page-table
+ * row d_page_table[max_pages] (the chunk's own K/V appended first, as the
+ * reference appends before it attends).  d_q [n_tok][n_q_heads][D] f16 (normed,
+ * rotated), d_out [n_tok][n_q_heads][D] f32; f16 pool with D = 128 or 256.  The
+ * pages are gathered into contiguous f16 rows in the handle's workspace, then
+ * the flash prefill runs with its queries offset by start_pos. */
+int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
+                          const int32_t* d_page_table, int32_t max_pages, int32_t start_pos,
+                          int32_t n_tok, int32_t n_q_heads, int32_t gqa_mode, float scale,
+                          float* d_out, void* stream);
+
 /* ---- gated DeltaNet ----------------------------------------------------------
  * Gates (src/model/mod.rs:796-839): beta = sigmoid(beta_raw),
  * g = ssm_a * softplus(a_raw + dt_bias) (identity above 10).
@@ -260,6 +274,14 @@ void pi_attn_layer_destroy(pi_attn_layer layer);
  * nothing.  Synchronous. */
 int pi_attn_layer_forward(pi_handle h, pi_attn_layer layer, float* h_q, float* h_k,
                           const float* h_v, const float* h_gate, int32_t n_tokens, float* h_out);
+/* pi_attn_layer_forward with device pointers (same layouts), enqueued on `stream` without
+ * host copies or waits: the layer's sequence length advances when the call returns.  A
+ * prompt or a continued chunk of an f16 cache at head_dim 128 / 256 runs the flash prefill
+ * (a continued chunk over its pages, as pi_attn_prefill_paged); other shapes run one decode
+ * row per token.  Calls on one layer must be ordered on one stream. */
+int pi_attn_layer_forward_dev(pi_handle h, pi_attn_layer layer, float* d_q, float* d_k,
+                              const float* d_v, const float* d_gate, int32_t n_tokens,
+                              float* d_out, void* stream);
 /* LayerCache::reset (src/model/mod.rs:1854-1856): the sequence restarts at position 0. */
 void pi_attn_layer_reset(pi_attn_layer layer);
 int32_t pi_attn_layer_seq_len(pi_attn_layer layer);
@@ -283,6 +305,11 @@ void pi_gdn_layer_destroy(pi_gdn_layer layer);
 int pi_gdn_layer_forward(pi_handle h, pi_gdn_layer layer, const float* h_qkv, const float* h_z,
                          const float* h_beta_raw, const float* h_a_raw, int32_t n_tokens,
                          float* h_out);
+/* pi_gdn_layer_forward with device pointers (same layouts), enqueued on `stream` without
+ * host copies or waits.  Calls on one layer must be ordered on one stream. */
+int pi_gdn_layer_forward_dev(pi_handle h, pi_gdn_layer layer, const float* d_qkv,
+                             const float* d_z, const float* d_beta_raw, const float* d_a_raw,
+                             int32_t n_tokens, float* d_out, void* stream);
 /* The GDN part of InferenceContext::reset (src/model/mod.rs:1867-1869): both states to zero. */
 int pi_gdn_layer_reset(pi_handle h, pi_gdn_layer layer);
 

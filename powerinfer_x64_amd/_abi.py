@@ -42,6 +42,8 @@ SIGNATURES = {
                                       _vp, _vp]),
     "pi_attn_prefill": (_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                _i32, _f32, _vp, _vp]),
+    "pi_attn_prefill_paged": (_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _vp,
+                                     _vp]),
     "pi_gdn_gates": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "pi_gdn_conv1d": (_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "pi_gdn_rmsnorm_gated": (_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _vp]),
@@ -61,12 +63,14 @@ SIGNATURES = {
                                     _f32, _vp, _i32, ctypes.POINTER(_vp)]),
     "pi_attn_layer_destroy": (None, [_vp]),
     "pi_attn_layer_forward": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
+    "pi_attn_layer_forward_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp]),
     "pi_attn_layer_reset": (None, [_vp]),
     "pi_attn_layer_seq_len": (_i32, [_vp]),
     "pi_gdn_layer_create": (_int, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _f32,
                                    ctypes.POINTER(_vp)]),
     "pi_gdn_layer_destroy": (None, [_vp]),
     "pi_gdn_layer_forward": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
+    "pi_gdn_layer_forward_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp]),
     "pi_gdn_layer_reset": (_int, [_vp, _vp]),
     "pi_tq_generate": (_int, [_i32, ctypes.c_uint64, _vp, _vp]),
     "pi_tq_pool_create": (_int, [_vp, _i32, _i32, _i32, _i32, ctypes.POINTER(_vp)]),

@@ -28,6 +28,8 @@ struct pi_handle_s {
     size_t h2d_floats = 0;
     float* tq_qv = nullptr;        // TurboQuant virtual queries [batch][Hq][256]
     size_t tq_qv_floats = 0;
+    char* pf_buf = nullptr;        // paged prefill: the sequence's K / V gathered to f16 rows
+    size_t pf_bytes = 0;
     // Ordering of the workspaces above across caller streams: ws_event marks
     // the last workspace use, issued on ws_stream.
     hipEvent_t ws_event = nullptr;
@@ -54,8 +56,10 @@ struct pi_attn_layer_s {
     float* d_kn = nullptr;
     int32_t* d_pt = nullptr;        // kLayerRows identical rows of the identity page table
     int32_t* d_ctx = nullptr;       // per-row context lengths, then the start position
-    float* d_buf = nullptr;         // staging: q, k, v, gate, out, f16 q / k / v
+    float* d_buf = nullptr;         // host-slice staging: q, gate, out, k, v (f32)
     size_t buf_floats = 0;
+    char* d_half = nullptr;         // f16 q, then f16 K / V rows for the flash prefill
+    size_t half_bytes = 0;
     int32_t seq_len = 0;
 };
 
@@ -69,7 +73,7 @@ struct pi_gdn_layer_s {
     float* d_norm = nullptr;    // [dv]
     float* d_conv_state = nullptr;  // [d_conv - 1][conv_dim]
     float* d_state = nullptr;       // [hv][dk][dv]
-    float* d_buf = nullptr;         // staging
+    float* d_buf = nullptr;         // staging: activation, q, k, v, beta, g (+ host-slice I/O)
     size_t buf_floats = 0;
 };
 
@@ -277,6 +281,7 @@ void pi_destroy(pi_handle h) {
     (void)hipFree(h->gws.buf);
     (void)hipFree(h->h2d_scratch);
     (void)hipFree(h->tq_qv);
+    (void)hipFree(h->pf_buf);
     if (h->ws_event) (void)hipEventDestroy(h->ws_event);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
@@ -569,10 +574,49 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
         return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: n_q_heads %d not a multiple of n_kv_heads %d", n_q_heads, n_kv_heads);
     if (batch == 0 || seq_len == 0) return PI_OK;
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_prefill");
-    PI_HIP(h, pi::launch_prefill(d_q, d_k, d_v, dtype, batch, seq_len, n_q_heads, n_kv_heads,
-                                 head_dim, causal ? 1 : 0, gqa_mode, scale, d_out, pick(h, stream)),
+    PI_HIP(h, pi::launch_prefill(d_q, d_k, d_v, dtype, batch, seq_len, seq_len, 0, n_q_heads,
+                                 n_kv_heads, head_dim, causal ? 1 : 0, gqa_mode, scale, d_out,
+                                 pick(h, stream)),
            "pi_attn_prefill");
     return PI_OK;
+}
+
+int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
+                          const int32_t* d_page_table, int32_t max_pages, int32_t start_pos,
+                          int32_t n_tok, int32_t n_q_heads, int32_t gqa_mode, float scale,
+                          float* d_out, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!d_q || !pool || !d_page_table || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: null argument");
+    const pi::KvGeom& g = pool->g;
+    if (start_pos < 0 || n_tok < 0 || max_pages <= 0 || n_q_heads <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: start_pos=%d n_tok=%d max_pages=%d n_q_heads=%d",
+                    start_pos, n_tok, max_pages, n_q_heads);
+    if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: gqa_mode %d", gqa_mode);
+    if (g.dtype != PI_F16 || (g.head_dim != 128 && g.head_dim != 256))
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill_paged: f16 pool with head_dim 128 or 256 (dtype %d, head_dim %d)",
+                    g.dtype, g.head_dim);
+    if (n_q_heads % g.n_kv_heads != 0)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill_paged: n_q_heads %d not a multiple of n_kv_heads %d",
+                    n_q_heads, g.n_kv_heads);
+    const long long n_keys = (long long)start_pos + n_tok;
+    if (n_keys > (long long)max_pages * pi::kPageTokens)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: %lld keys exceed the %d-page row", n_keys, max_pages);
+    if (n_tok == 0) return PI_OK;
+    hipStream_t s = pick(h, stream);
+    PI_HIP(h, hipSetDevice(h->device), "pi_attn_prefill_paged");
+    int rc;
+    if ((rc = ws_begin(h, s, "pi_attn_prefill_paged"))) return rc;
+    const size_t rows = (size_t)n_keys * g.n_kv_heads * g.head_dim;  // f16 elements of K (and of V)
+    if ((rc = grow(h, &h->pf_buf, &h->pf_bytes, 4 * rows, s, "pi_attn_prefill_paged workspace", false))) return rc;
+    char* gk = h->pf_buf;
+    char* gv = h->pf_buf + 2 * rows;
+    PI_HIP(h, pi::launch_kv_gather(g, d_page_table, (int32_t)n_keys, gk, gv, s), "pi_attn_prefill_paged");
+    PI_HIP(h, pi::launch_prefill(d_q, gk, gv, PI_F16, 1, n_tok, (int32_t)n_keys, start_pos, n_q_heads,
+                                 g.n_kv_heads, g.head_dim, 1, gqa_mode, scale, d_out, s),
+           "pi_attn_prefill_paged");
+    return ws_end(h, s, "pi_attn_prefill_paged");
 }
 
 // ---- gated DeltaNet ------------------------------------------------------------------
@@ -942,6 +986,7 @@ void pi_attn_layer_destroy(pi_attn_layer L) {
     (void)hipFree(L->d_qn);
     (void)hipFree(L->d_kn);
     (void)hipFree(L->d_buf);
+    (void)hipFree(L->d_half);
     delete L;
 }
 
@@ -951,6 +996,65 @@ void pi_attn_layer_reset(pi_attn_layer L) {
 
 int32_t pi_attn_layer_seq_len(pi_attn_layer L) { return L ? L->seq_len : 0; }
 
+// The attention step of forward for n tokens whose q, k, v (and gate) are on the
+// device: norm + RoPE + append at positions seq_len .., then attention for every
+// token over the keys up to its own.  An f16 cache at head_dim 128 / 256 runs
+// the flash prefill for n > 1 (a fresh prompt over its own rows; a continued
+// chunk over the sequence's pages gathered to f16 rows); anything else runs one
+// decode row per token.  Positions and row lengths are written on the device,
+// so the step enqueues work on `s` and never waits for it.
+static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, const float* dv,
+                           const float* dg, int32_t n, float* dout, hipStream_t s) {
+    const int prev = L->seq_len;
+    if ((long long)prev + n > (long long)L->max_pages * pi::kPageTokens)
+        return fail(h, PI_ERR_OUT_OF_MEMORY, "attention layer: %d + %d tokens exceed the layer cache of %d",
+                    prev, n, L->max_pages * pi::kPageTokens);
+    void* sv = reinterpret_cast<void*>(s);
+    const int D = L->dim;
+    const size_t nq = (size_t)n * L->n_heads * D;
+    int rc;
+    int32_t* d_start = L->d_ctx + kLayerRows;
+    PI_HIP(h, pi::launch_fill_iota(d_start, 1, prev, s), "attention layer");
+    if ((rc = pi_attn_prologue(h, dq, dk, dv, L->d_qn, L->d_kn, L->eps, L->rope_dim, L->rope_base,
+                               L->has_sections ? L->sections : nullptr, L->pool, L->d_pt,
+                               L->max_pages, d_start, 1, n, L->n_heads, sv)))
+        return rc;
+    const float scale = 1.0f / std::sqrt((float)D);
+    if (n > 1 && (D == 128 || D == 256) && L->kv_dtype == PI_F16) {
+        // causal flash attention: f16 q rows, then K / V rows of positions 0 .. prev + n - 1
+        const size_t kv_rows = (size_t)(prev + n) * L->n_kv * D;
+        if ((rc = grow(h, &L->d_half, &L->half_bytes, 2 * nq + 4 * kv_rows, s, "attention layer staging", false)))
+            return rc;
+        char* hq16 = L->d_half;
+        char* hk16 = hq16 + 2 * nq;
+        char* hv16 = hk16 + 2 * kv_rows;
+        PI_HIP(h, pi::launch_to_half(dq, hq16, nq, s), "attention layer");
+        if (prev == 0) {  // a fresh prompt: its own rotated rows (the pool holds the same f16 values)
+            PI_HIP(h, pi::launch_to_half(dk, hk16, kv_rows, s), "attention layer");
+            PI_HIP(h, pi::launch_to_half(dv, hv16, kv_rows, s), "attention layer");
+        } else {          // a continued chunk: the whole sequence out of its pages
+            PI_HIP(h, pi::launch_kv_gather(L->pool->g, L->d_pt, prev + n, hk16, hv16, s), "attention layer");
+        }
+        PI_HIP(h, pi::launch_prefill(hq16, hk16, hv16, PI_F16, 1, n, prev + n, prev, L->n_heads, L->n_kv,
+                                     D, 1, L->gqa_mode, scale, dout, s),
+               "attention layer");
+        if (dg) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
+    } else {
+        // one decode row per token over the paged cache: row i sees prev + i + 1 keys
+        for (int r0 = 0; r0 < n; r0 += kLayerRows) {
+            const int rows = std::min(kLayerRows, n - r0);
+            PI_HIP(h, pi::launch_fill_iota(L->d_ctx, rows, prev + r0 + 1, s), "attention layer");
+            const size_t off = (size_t)r0 * L->n_heads * D;
+            if ((rc = pi_attn_decode(h, dq + off, L->pool, L->d_pt, L->max_pages, L->d_ctx, rows,
+                                     L->n_heads, L->gqa_mode, scale, dg ? dg + off : nullptr,
+                                     dout + off, sv)))
+                return rc;
+        }
+    }
+    L->seq_len = prev + n;
+    return PI_OK;
+}
+
 int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, const float* h_v,
                           const float* h_gate, int32_t n_tokens, float* h_out) {
     PI_CHECK_HANDLE(h);
@@ -958,66 +1062,38 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward: null argument");
     if (n_tokens < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward: n_tokens=%d", n_tokens);
     if (n_tokens == 0) return PI_OK;
-    const int prev = L->seq_len;
-    if ((long long)prev + n_tokens > (long long)L->max_pages * pi::kPageTokens)
+    if ((long long)L->seq_len + n_tokens > (long long)L->max_pages * pi::kPageTokens)
         return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_attn_layer_forward: %d + %d tokens exceed the layer cache of %d",
-                    prev, n_tokens, L->max_pages * pi::kPageTokens);
+                    L->seq_len, n_tokens, L->max_pages * pi::kPageTokens);
     hipStream_t s = h->stream;
-    void* sv = reinterpret_cast<void*>(s);
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_layer_forward");
     const int D = L->dim;
     const size_t nq = (size_t)n_tokens * L->n_heads * D, nk = (size_t)n_tokens * L->n_kv * D;
-    const size_t need = 3 * nq + 2 * nk + (nq + 2 * nk + 1) / 2;  // q, gate, out, k, v, f16 copies
-    int rc = grow(h, &L->d_buf, &L->buf_floats, need, s, "pi_attn_layer_forward staging", false);
+    int rc = grow(h, &L->d_buf, &L->buf_floats, 3 * nq + 2 * nk, s, "pi_attn_layer_forward staging", false);
     if (rc) return rc;
     float *dq = L->d_buf, *dg = dq + nq, *dout = dg + nq, *dk = dout + nq, *dv = dk + nk;
-    void* hq16 = dv + nk;
-    void* hk16 = reinterpret_cast<char*>(hq16) + nq * 2;
-    void* hv16 = reinterpret_cast<char*>(hk16) + nk * 2;
     if ((rc = copy_sync(h, dq, h_q, nq * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
     if ((rc = copy_sync(h, dk, h_k, nk * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
     if ((rc = copy_sync(h, dv, h_v, nk * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
     if (h_gate && (rc = copy_sync(h, dg, h_gate, nq * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
-    // norm + RoPE + append at positions prev .. prev + n_tokens - 1
-    int32_t* d_start = L->d_ctx + kLayerRows;
-    PI_HIP(h, hipMemcpyAsync(d_start, &prev, sizeof(int32_t), hipMemcpyHostToDevice, s), "pi_attn_layer_forward");
-    if ((rc = pi_attn_prologue(h, dq, dk, dv, L->d_qn, L->d_kn, L->eps, L->rope_dim, L->rope_base,
-                               L->has_sections ? L->sections : nullptr, L->pool, L->d_pt,
-                               L->max_pages, d_start, 1, n_tokens, L->n_heads, sv)))
-        return rc;
-    const float scale = 1.0f / std::sqrt((float)D);
-    if (prev == 0 && n_tokens > 1 && (D == 128 || D == 256) && L->kv_dtype == PI_F16) {
-        // a fresh prompt: causal flash attention over the rotated rows (f16 inputs)
-        PI_HIP(h, pi::launch_to_half(dq, hq16, nq, s), "pi_attn_layer_forward");
-        PI_HIP(h, pi::launch_to_half(dk, hk16, nk, s), "pi_attn_layer_forward");
-        PI_HIP(h, pi::launch_to_half(dv, hv16, nk, s), "pi_attn_layer_forward");
-        if ((rc = pi_attn_prefill(h, hq16, hk16, hv16, PI_F16, 1, n_tokens, L->n_heads, L->n_kv, D,
-                                  1, L->gqa_mode, scale, dout, sv)))
-            return rc;
-        if (h_gate) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "pi_attn_layer_forward");
-    } else {
-        // one decode row per token over the paged cache: row i sees prev + i + 1 keys
-        std::vector<int32_t> ctx(kLayerRows);
-        for (int r0 = 0; r0 < n_tokens; r0 += kLayerRows) {
-            const int rows = std::min(kLayerRows, n_tokens - r0);
-            for (int i = 0; i < rows; ++i) ctx[i] = prev + r0 + i + 1;
-            PI_HIP(h, hipMemcpyAsync(L->d_ctx, ctx.data(), rows * sizeof(int32_t), hipMemcpyHostToDevice, s),
-                   "pi_attn_layer_forward");
-            const size_t off = (size_t)r0 * L->n_heads * D;
-            if ((rc = pi_attn_decode(h, dq + off, L->pool, L->d_pt, L->max_pages, L->d_ctx, rows,
-                                     L->n_heads, L->gqa_mode, scale, h_gate ? dg + off : nullptr,
-                                     dout + off, sv)))
-                return rc;
-            // the host row of context lengths is reused by the next chunk
-            PI_HIP(h, hipStreamSynchronize(s), "pi_attn_layer_forward");
-        }
-    }
+    if ((rc = attn_layer_step(h, L, dq, dk, dv, h_gate ? dg : nullptr, n_tokens, dout, s))) return rc;
     if ((rc = copy_sync(h, h_out, dout, nq * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
     if ((rc = copy_sync(h, h_q, dq, nq * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
     if ((rc = copy_sync(h, h_k, dk, nk * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
     PI_HIP(h, hipStreamSynchronize(s), "pi_attn_layer_forward");
-    L->seq_len = prev + n_tokens;
     return PI_OK;
+}
+
+int pi_attn_layer_forward_dev(pi_handle h, pi_attn_layer L, float* d_q, float* d_k,
+                              const float* d_v, const float* d_gate, int32_t n_tokens,
+                              float* d_out, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!L || !d_q || !d_k || !d_v || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward_dev: null argument");
+    if (n_tokens < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward_dev: n_tokens=%d", n_tokens);
+    if (n_tokens == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_attn_layer_forward_dev");
+    return attn_layer_step(h, L, d_q, d_k, d_v, d_gate, n_tokens, d_out, pick(h, stream));
 }
 
 // ---- gated-DeltaNet layer state -------------------------------------------------------
@@ -1090,6 +1166,36 @@ int pi_gdn_layer_reset(pi_handle h, pi_gdn_layer L) {
     return PI_OK;
 }
 
+// The GDN step of forward for n tokens on the device (src/model/mod.rs:750-932):
+// conv1d + SiLU with the rolling state, the q / k / v split, the gates, the
+// delta rule (chunked for n > 1) and RMSNormGated x SiLU(z).  Enqueued on `s`.
+static int gdn_layer_step(pi_handle h, pi_gdn_layer L, const float* dx, const float* dz,
+                          const float* dbr, const float* dar, int32_t n_tokens, float* dout,
+                          hipStream_t s) {
+    void* sv = reinterpret_cast<void*>(s);
+    const size_t n = (size_t)n_tokens, C = L->conv_dim, kd = (size_t)L->hk * L->dk;
+    const size_t vd = (size_t)L->hv * L->dv, nh = (size_t)L->hv;
+    // activation, q, k, v, beta, g
+    const size_t need = n * C + 2 * n * kd + n * vd + 2 * n * nh;
+    int rc = grow(h, &L->d_buf, &L->buf_floats, need, s, "gdn layer staging", false);
+    if (rc) return rc;
+    float *act = L->d_buf, *dq = act + n * C, *dk = dq + n * kd, *dv = dk + n * kd;
+    float *db = dv + n * vd, *dg = db + n * nh;
+    if ((rc = pi_gdn_conv1d(h, dx, L->d_conv_state, L->d_w, act, 1, n_tokens, (int32_t)C, L->d_conv, sv)))
+        return rc;
+    PI_HIP(h, hipMemcpy2DAsync(dq, kd * 4, act, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
+    PI_HIP(h, hipMemcpy2DAsync(dk, kd * 4, act + kd, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
+    PI_HIP(h, hipMemcpy2DAsync(dv, vd * 4, act + 2 * kd, C * 4, vd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
+    if ((rc = pi_gdn_gates(h, dbr, dar, L->d_ssm_a, L->d_dt, db, dg, n_tokens, L->hv, sv))) return rc;
+    if (n_tokens > 1)
+        rc = pi_gdn_prefill(h, dq, dk, dv, db, dg, L->d_state, dout, n_tokens, L->hk, L->hv, L->dk,
+                            L->dv, 64, sv);
+    else
+        rc = pi_gdn_decode(h, dq, dk, dv, db, dg, L->d_state, dout, 1, L->hk, L->hv, L->dk, L->dv, sv);
+    if (rc) return rc;
+    return pi_gdn_rmsnorm_gated(h, dout, dz, L->d_norm, n_tokens, L->hv, L->dv, L->eps, sv);
+}
+
 int pi_gdn_layer_forward(pi_handle h, pi_gdn_layer L, const float* h_qkv, const float* h_z,
                          const float* h_beta_raw, const float* h_a_raw, int32_t n_tokens,
                          float* h_out) {
@@ -1099,38 +1205,35 @@ int pi_gdn_layer_forward(pi_handle h, pi_gdn_layer L, const float* h_qkv, const 
     if (n_tokens < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_layer_forward: n_tokens=%d", n_tokens);
     if (n_tokens == 0) return PI_OK;
     hipStream_t s = h->stream;
-    void* sv = reinterpret_cast<void*>(s);
     PI_HIP(h, hipSetDevice(h->device), "pi_gdn_layer_forward");
-    const size_t n = (size_t)n_tokens, C = L->conv_dim, kd = (size_t)L->hk * L->dk;
+    const size_t n = (size_t)n_tokens, C = L->conv_dim;
     const size_t vd = (size_t)L->hv * L->dv, nh = (size_t)L->hv;
-    // qkv, activation, q, k, v, z, beta_raw, a_raw, beta, g, out
-    const size_t need = 2 * n * C + 2 * n * kd + 3 * n * vd + 4 * n * nh;
-    int rc = grow(h, &L->d_buf, &L->buf_floats, need, s, "pi_gdn_layer_forward staging", false);
+    // host-slice I/O: qkv, z, beta_raw, a_raw, out
+    const size_t need = n * C + 2 * n * vd + 2 * n * nh;
+    int rc = grow(h, &h->h2d_scratch, &h->h2d_floats, need, s, "pi_gdn_layer_forward staging", false);
     if (rc) return rc;
-    float *dx = L->d_buf, *act = dx + n * C, *dq = act + n * C, *dk = dq + n * kd, *dv = dk + n * kd;
-    float *dz = dv + n * vd, *dbr = dz + n * vd, *dar = dbr + n * nh, *db = dar + n * nh;
-    float *dg = db + n * nh, *dout = dg + n * nh;
+    float *dx = h->h2d_scratch, *dz = dx + n * C, *dbr = dz + n * vd, *dar = dbr + n * nh;
+    float* dout = dar + n * nh;
     if ((rc = copy_sync(h, dx, h_qkv, n * C * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
     if ((rc = copy_sync(h, dz, h_z, n * vd * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
     if ((rc = copy_sync(h, dbr, h_beta_raw, n * nh * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
     if ((rc = copy_sync(h, dar, h_a_raw, n * nh * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
-    // conv1d + SiLU with the rolling state (:750-776), then the q / k / v split (:779-781)
-    if ((rc = pi_gdn_conv1d(h, dx, L->d_conv_state, L->d_w, act, 1, n_tokens, (int32_t)C, L->d_conv, sv)))
-        return rc;
-    PI_HIP(h, hipMemcpy2DAsync(dq, kd * 4, act, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "pi_gdn_layer_forward");
-    PI_HIP(h, hipMemcpy2DAsync(dk, kd * 4, act + kd, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "pi_gdn_layer_forward");
-    PI_HIP(h, hipMemcpy2DAsync(dv, vd * 4, act + 2 * kd, C * 4, vd * 4, n, hipMemcpyDeviceToDevice, s), "pi_gdn_layer_forward");
-    if ((rc = pi_gdn_gates(h, dbr, dar, L->d_ssm_a, L->d_dt, db, dg, n_tokens, L->hv, sv))) return rc;
-    if (n_tokens > 1)
-        rc = pi_gdn_prefill(h, dq, dk, dv, db, dg, L->d_state, dout, n_tokens, L->hk, L->hv, L->dk,
-                            L->dv, 64, sv);
-    else
-        rc = pi_gdn_decode(h, dq, dk, dv, db, dg, L->d_state, dout, 1, L->hk, L->hv, L->dk, L->dv, sv);
-    if (rc) return rc;
-    if ((rc = pi_gdn_rmsnorm_gated(h, dout, dz, L->d_norm, n_tokens, L->hv, L->dv, L->eps, sv))) return rc;
+    if ((rc = gdn_layer_step(h, L, dx, dz, dbr, dar, n_tokens, dout, s))) return rc;
     if ((rc = copy_sync(h, h_out, dout, n * vd * 4, hipMemcpyDeviceToHost, "pi_gdn_layer_forward"))) return rc;
     PI_HIP(h, hipStreamSynchronize(s), "pi_gdn_layer_forward");
     return PI_OK;
+}
+
+int pi_gdn_layer_forward_dev(pi_handle h, pi_gdn_layer L, const float* d_qkv, const float* d_z,
+                             const float* d_beta_raw, const float* d_a_raw, int32_t n_tokens,
+                             float* d_out, void* stream) {
+    PI_CHECK_HANDLE(h);
+    if (!L || !d_qkv || !d_z || !d_beta_raw || !d_a_raw || !d_out)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_layer_forward_dev: null argument");
+    if (n_tokens < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_layer_forward_dev: n_tokens=%d", n_tokens);
+    if (n_tokens == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), "pi_gdn_layer_forward_dev");
+    return gdn_layer_step(h, L, d_qkv, d_z, d_beta_raw, d_a_raw, n_tokens, d_out, pick(h, stream));
 }
 
 // ---- TurboQuant compressed KV ------------------------------------------------------

@@ -111,6 +111,7 @@ hipError_t launch_head_rmsnorm(float* x, const float* w, int32_t n_rows, int32_t
 hipError_t launch_softmax(float* x, int32_t n, hipStream_t s);
 hipError_t launch_to_half(const float* x, void* y, size_t n, hipStream_t s);
 hipError_t launch_apply_gate(float* out, const float* gate, size_t n, hipStream_t s);
+hipError_t launch_fill_iota(int32_t* dst, int32_t n, int32_t first, hipStream_t s);
 hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
                                 const float* k_norm_w, float eps, const RopeFreqs& freqs,
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,
@@ -118,10 +119,18 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
                                 const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
                                 int32_t n_q_heads, hipStream_t s);
 
+// Causal (or full) flash attention of seq_len query rows per sequence over
+// n_keys keys; query row i sits at key position q_off + i (a fresh prompt:
+// n_keys = seq_len, q_off = 0).  q / out [batch][seq_len][Hq][D],
+// k / v [batch][n_keys][Hkv][D].
 hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
-                          int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
-                          int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale,
-                          float* out, hipStream_t s);
+                          int32_t batch, int32_t seq_len, int32_t n_keys, int32_t q_off,
+                          int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t causal,
+                          int32_t gqa_mode, float scale, float* out, hipStream_t s);
+// The f16 pool's K and V of positions 0 .. n_tok-1 of one sequence (page-table
+// row `page_table`) gathered into contiguous f16 [n_tok][Hkv][D] rows.
+hipError_t launch_kv_gather(const KvGeom& g, const int32_t* page_table, int32_t n_tok,
+                            void* k_out, void* v_out, hipStream_t s);
 
 hipError_t launch_gdn_gates(const float* beta_raw, const float* a_raw, const float* ssm_a,
                             const float* dt_bias, float* beta, float* g, int32_t n_tok,

@@ -54,7 +54,10 @@ struct PrefillArgs {
     const void* k;
     const void* v;
     float* out;
-    int S, hq, hkv, group, causal, gqa_mode;
+    int S;      // query rows per sequence
+    int Sk;     // keys per sequence (K / V rows)
+    int q_off;  // position of query row 0 among the keys (causal: row i sees keys <= q_off + i)
+    int hq, hkv, group, causal, gqa_mode;
     float qk_scale;  // scale * log2(e)
 };
 
@@ -125,18 +128,20 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hs = wave % HPW, rt = wave / HPW;
     const int b = blockIdx.z;
-    const int S = a.S;
+    const int S = a.S, Sk = a.Sk, q_off = a.q_off;
     const int qb = gridDim.y - 1 - blockIdx.y;  // heaviest (latest) query blocks first
     const int per_kv = a.group / HPW;           // workgroups per KV head
     const int kvh = blockIdx.x / per_kv;
     const int head = head_of(kvh, (blockIdx.x % per_kv) * HPW + hs, a.hkv, a.group, a.gqa_mode);
     const int p0 = qb * WROWS + rt * ROWS;
-    const int wg_keys = a.causal ? min(S, qb * WROWS + WROWS) : S;
+    const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
     const int n_tiles = (wg_keys + BN - 1) / BN;
-    const int w_keys = a.causal ? min(S, p0 + ROWS) : S;
+    const int w_keys = a.causal ? min(Sk, q_off + p0 + ROWS) : Sk;
     const int w_tiles = p0 < S ? (w_keys + BN - 1) / BN : 0;  // tiles this wavefront attends
-    const bool last_masked = w_tiles > 0 && ((a.causal && (w_tiles - 1) * BN + BN - 1 > p0) ||
-                                             w_tiles * BN > S);
+    // Tiles from t_mask on hold a key past the wavefront's first row (causal)
+    // or past the keys; they go through the mask.  Without an offset that is
+    // at most the last tile; with one, the last two.
+    const int t_mask = min(a.causal ? (q_off + p0 + 1) / BN : Sk / BN, Sk / BN);
 
     const int r = lane & 31;   // query column of this lane
     const int hh = lane >> 5;  // 8-wide k slice of the MFMA operands
@@ -161,14 +166,14 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     float m_run = -1e30f, l_run = 0.f;
 
     const size_t tok_stride = (size_t)a.hkv * D;
-    const T* kbase = reinterpret_cast<const T*>(a.k) + ((size_t)b * S * a.hkv + kvh) * D;
-    const T* vbase = reinterpret_cast<const T*>(a.v) + ((size_t)b * S * a.hkv + kvh) * D;
+    const T* kbase = reinterpret_cast<const T*>(a.k) + ((size_t)b * Sk * a.hkv + kvh) * D;
+    const T* vbase = reinterpret_cast<const T*>(a.v) + ((size_t)b * Sk * a.hkv + kvh) * D;
 
     // Direct global -> LDS loads (16 bytes per lane, lane i lands at base +
     // 16 i).  K: load i of a tile covers chunks 64 i .. 64 i + 63 of the padded
     // tile (row = chunk / 17; chunk 16 of a row is padding and reloads chunk
     // 0).  V: load i covers rows 4 i .. 4 i + 3.  Rows past the prompt reload
-    // row S-1 (finite values; their scores are masked to -inf, P = 0).
+    // row Sk-1 (finite values; their scores are masked to -inf, P = 0).
     typedef __attribute__((address_space(3))) void lds_void;
     // The load is issued from inline assembly so that the compiler does not
     // add vmcnt waits before LDS reads (it cannot tell the buffers apart);
@@ -224,7 +229,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     auto issue_unit = [&](int u) {
         const int buf = u % NB;
         const int k0 = u * BN;
-        if (k0 + BN <= S) {
+        if (k0 + BN <= Sk) {
             const T* kb = kbase + (size_t)k0 * tok_stride;
 #pragma unroll
             for (int j = 0; j < KJ; ++j) {
@@ -236,7 +241,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
             for (int j = 0; j < KJ; ++j) {
                 const int i = wave + NW * j;
                 if (i < K_INSTR) {
-                    const int key = min(k0 + k_row[j], S - 1);
+                    const int key = min(k0 + k_row[j], Sk - 1);
                     const T* src = kbase + (size_t)key * tok_stride +
                                    (k_off[j] - (size_t)k_row[j] * tok_stride * sizeof(T)) / sizeof(T);
                     dma16(src, (lds_void*)&sk[buf][512 * i]);
@@ -246,13 +251,13 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         if (u >= 1) {
             const int v0 = k0 - BN;
             const T* vb = vbase + (size_t)v0 * tok_stride;
-            if (v0 + BN <= S) {
+            if (v0 + BN <= Sk) {
 #pragma unroll
                 for (int j = 0; j < VJ; ++j) dma16s(vb, v_off[j], (lds_void*)&sv[buf][512 * (VJ * wave + j)]);
             } else {
 #pragma unroll
                 for (int j = 0; j < VJ; ++j) {
-                    const int key = min(v0 + v_row[j], S - 1);
+                    const int key = min(v0 + v_row[j], Sk - 1);
                     const T* src = vbase + (size_t)key * tok_stride +
                                    (v_off[j] - (size_t)v_row[j] * tok_stride * sizeof(T)) / sizeof(T);
                     dma16(src, (lds_void*)&sv[buf][512 * (VJ * wave + j)]);
@@ -347,7 +352,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int key = k0 + 32 * tt + 8 * (e >> 2) + 4 * hh + (e & 3);
-                    if (key >= S || (a.causal && key > qpos)) s[tt][e] = -INFINITY;
+                    if (key >= Sk || (a.causal && key > q_off + qpos)) s[tt][e] = -INFINITY;
                 }
         }
         float mx = fmaxf(max16(s[0]), max16(s[1]));
@@ -419,7 +424,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         if (wave < NW / 2) {
             for (int t = 0; t <= n_tiles; ++t) {
                 mfma_phase(t);
-                if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
+                if (t < w_tiles) phase_softmax(t, t >= t_mask);
                 if (t + 3 <= n_tiles) issue_unit(t + 3);
                 if (t < n_tiles) {
                     wait_unit(ahead_of(t + 1));
@@ -428,7 +433,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
             }
         } else {
             for (int t = 0; t <= n_tiles; ++t) {
-                if (t >= 1 && t - 1 < w_tiles) phase_softmax(t - 1, t - 1 == w_tiles - 1 && last_masked);
+                if (t >= 1 && t - 1 < w_tiles) phase_softmax(t - 1, t - 1 >= t_mask);
                 if (t + 3 <= n_tiles) issue_unit(t + 3);
                 mfma_phase(t);
                 if (t < n_tiles) {
@@ -445,7 +450,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         for (int t = 0; t <= n_tiles; ++t) {
             if (t >= 1 && t + 1 <= n_tiles) issue_unit(t + 1);
             mfma_phase(t);
-            if (t < w_tiles) phase_softmax(t, t == w_tiles - 1 && last_masked);
+            if (t < w_tiles) phase_softmax(t, t >= t_mask);
             if (t < n_tiles) {
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
                 barrier();
@@ -497,16 +502,19 @@ void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int ba
 }  // namespace
 
 hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
-                          int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
-                          int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale,
-                          float* out, hipStream_t s) {
+                          int32_t batch, int32_t seq_len, int32_t n_keys, int32_t q_off,
+                          int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t causal,
+                          int32_t gqa_mode, float scale, float* out, hipStream_t s) {
     if (head_dim != 128 && head_dim != 256) return hipErrorInvalidValue;
+    if (q_off < 0 || n_keys < 1 || (causal && q_off + seq_len > n_keys)) return hipErrorInvalidValue;
     PrefillArgs a;
     a.q = q;
     a.k = k;
     a.v = v;
     a.out = out;
     a.S = seq_len;
+    a.Sk = n_keys;
+    a.q_off = q_off;
     a.hq = n_q_heads;
     a.hkv = n_kv_heads;
     a.group = n_q_heads / n_kv_heads;

@@ -3,6 +3,7 @@
 //
 //   kv_append   : LayerCache append (src/model/mod.rs:1140-1146) into the paged pool
 //   kv_read     : pool -> reference layout [T][n_kv][D] f32
+//   kv_gather   : one sequence's f16 pages -> contiguous f16 K / V rows (paged prefill)
 //   rope        : ops::apply_rope / apply_rope_with_freqs (src/ops.rs:35-67,130-157)
 //                 as driven by src/model/mod.rs:1072-1138
 //   head_rmsnorm: ops::rms_norm per head (src/ops.rs:13-27; src/model/mod.rs:1035-1070)
@@ -77,6 +78,43 @@ __global__ __launch_bounds__(256) void kv_read_kernel(KvGeom g, const int32_t* _
         }
         ko[idx] = kv;
         vo[idx] = vv;
+    }
+}
+
+// One workgroup per (page, KV head) of a sequence: its 16 tokens of K and V
+// out of the f16 pool into contiguous [token][Hkv][D] f16 rows, the layout the
+// prefill kernel streams.  A K block is already 16-byte chunks of 8 dims per
+// token ([D/8][16][8]); a V block is dim-major ([D][16]) and is transposed in
+// LDS.  Tokens at or past n_tok are not written; a page id outside the pool
+// gives zero rows.
+template <int D>
+__global__ __launch_bounds__(256) void kv_gather_kernel(KvGeom g, const int32_t* __restrict__ pt,
+                                                        int n_tok, f16* __restrict__ k_out,
+                                                        f16* __restrict__ v_out) {
+    constexpr int NCH = D / 8 * kPageTokens;  // 16-byte chunks of one block
+    __shared__ __attribute__((aligned(16))) f16 sv[D * kPageTokens];
+    const int lp = blockIdx.x, h = blockIdx.y, H = g.n_kv_heads;
+    const int page = pt[lp];
+    const bool ok = page >= 0 && page < g.n_pages;
+    const size_t blk = ((size_t)(ok ? page : 0) * H + h) * kPageTokens * D;
+    const f16x8* kb = reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(g.k) + blk);
+    const f16x8* vb = reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(g.v) + blk);
+    for (int i = threadIdx.x; i < NCH; i += 256) {
+        *reinterpret_cast<f16x8*>(&sv[8 * i]) = ok ? vb[i] : f16x8{};
+        const int c = i / kPageTokens, tok = i % kPageTokens;  // chunk i = dims 8c.., token tok
+        const int pos = lp * kPageTokens + tok;
+        if (pos < n_tok)
+            *reinterpret_cast<f16x8*>(k_out + ((size_t)pos * H + h) * D + 8 * c) = ok ? kb[i] : f16x8{};
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < NCH; i += 256) {
+        const int tok = i / (D / 8), c = i % (D / 8);  // output chunk: token tok, dims 8c..
+        const int pos = lp * kPageTokens + tok;
+        if (pos >= n_tok) continue;
+        f16x8 x;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = sv[(8 * c + e) * kPageTokens + tok];
+        *reinterpret_cast<f16x8*>(v_out + ((size_t)pos * H + h) * D + 8 * c) = x;
     }
 }
 
@@ -298,6 +336,21 @@ hipError_t launch_kv_read(const KvGeom& g, const int32_t* page_table, int32_t ma
     return hipGetLastError();
 }
 
+hipError_t launch_kv_gather(const KvGeom& g, const int32_t* page_table, int32_t n_tok,
+                            void* k_out, void* v_out, hipStream_t s) {
+    if (g.dtype != 1 || n_tok <= 0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n_tok + kPageTokens - 1) / kPageTokens), (unsigned)g.n_kv_heads);
+    f16* ko = static_cast<f16*>(k_out);
+    f16* vo = static_cast<f16*>(v_out);
+    switch (g.head_dim) {
+        case 64: hipLaunchKernelGGL(kv_gather_kernel<64>, grid, dim3(256), 0, s, g, page_table, n_tok, ko, vo); break;
+        case 128: hipLaunchKernelGGL(kv_gather_kernel<128>, grid, dim3(256), 0, s, g, page_table, n_tok, ko, vo); break;
+        case 256: hipLaunchKernelGGL(kv_gather_kernel<256>, grid, dim3(256), 0, s, g, page_table, n_tok, ko, vo); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
                                 const float* k_norm_w, float eps, const RopeFreqs& freqs,
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,
@@ -329,6 +382,14 @@ hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, in
     return hipGetLastError();
 }
 
+// dst[i] = first + i for i < n (device-side positions and context lengths, so a
+// layer step issues no host copies).
+__global__ __launch_bounds__(256) void fill_iota_kernel(int32_t* __restrict__ dst, int n,
+                                                        int first) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = first + i;
+}
+
 __global__ __launch_bounds__(256) void to_half_kernel(const float* __restrict__ x,
                                                       f16* __restrict__ y, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -352,6 +413,12 @@ static unsigned grid_1d(size_t n) {
 hipError_t launch_to_half(const float* x, void* y, size_t n, hipStream_t s) {
     hipLaunchKernelGGL(to_half_kernel, dim3(grid_1d(n)), dim3(256), 0, s, x,
                        reinterpret_cast<f16*>(y), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_iota(int32_t* dst, int32_t n, int32_t first, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_iota_kernel, dim3((n + 255) / 256), dim3(256), 0, s, dst, n, first);
     return hipGetLastError();
 }
 

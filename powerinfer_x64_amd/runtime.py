@@ -223,6 +223,24 @@ class AttnLayer:
                                                           vp(g), n, vp(out)))
         return out
 
+    def forward_dev(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    gate: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+        """The same step on device tensors (f32, q [n, Hq, D], k / v [n, Hkv, D]; q and k
+        normalised / rotated in place), enqueued on torch's current stream."""
+        d = self.dev
+        n = q.shape[0]
+        _need(q, "q", torch.float32, (n, self.n_heads, self.head_dim), d.torch_device)
+        for name, t in (("k", k), ("v", v)):
+            _need(t, name, torch.float32, (n, self.n_kv_heads, self.head_dim), d.torch_device)
+        if gate is not None:
+            _need(gate, "gate", torch.float32, q.shape, d.torch_device)
+        if out is None:
+            out = torch.empty_like(q)
+        _need(out, "out", torch.float32, q.shape, d.torch_device)
+        d.check(d.lib.pi_attn_layer_forward_dev(d.h, self.p, _vp(q), _vp(k), _vp(v), _vp(gate), n,
+                                                _vp(out), d.stream()))
+        return out
+
 
 class GdnLayer:
     """Gated-DeltaNet layer of one sequence, on the device: the rolling conv state and the
@@ -276,6 +294,21 @@ class GdnLayer:
         vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
         self.dev.check(self.dev.lib.pi_gdn_layer_forward(self.dev.h, self.p, vp(qkv), vp(z),
                                                          vp(beta_raw), vp(a_raw), n, vp(out)))
+        return out
+
+    def forward_dev(self, qkv: torch.Tensor, z: torch.Tensor, beta_raw: torch.Tensor,
+                    a_raw: torch.Tensor, out: Optional[torch.Tensor] = None):
+        """The same step on device f32 tensors, enqueued on torch's current stream."""
+        d = self.dev
+        n = qkv.shape[0]
+        for name, t, shp in (("qkv", qkv, (n, self.conv_dim)), ("z", z, (n, self.hv, self.dv)),
+                             ("beta_raw", beta_raw, (n, self.hv)), ("a_raw", a_raw, (n, self.hv))):
+            _need(t, name, torch.float32, shp, d.torch_device)
+        if out is None:
+            out = torch.empty((n, self.hv, self.dv), dtype=torch.float32, device=qkv.device)
+        _need(out, "out", torch.float32, (n, self.hv, self.dv), d.torch_device)
+        d.check(d.lib.pi_gdn_layer_forward_dev(d.h, self.p, _vp(qkv), _vp(z), _vp(beta_raw),
+                                               _vp(a_raw), n, _vp(out), d.stream()))
         return out
 
 
@@ -449,6 +482,28 @@ def attn_prefill(dev: Device, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     dev.check(dev.lib.pi_attn_prefill(dev.h, _vp(q), _vp(k), _vp(v), _DTYPE_CODE[q.dtype], bsz,
                                       s, hq, hkv, dh, 1 if causal else 0, gqa_mode, float(scale),
                                       _vp(out), dev.stream()))
+    return out
+
+
+def attn_prefill_paged(dev: Device, q: torch.Tensor, pool: KvPool, page_row: torch.Tensor,
+                       start_pos: int, gqa_mode: int = MODULO, scale: Optional[float] = None,
+                       out: Optional[torch.Tensor] = None):
+    """A chunk continuing a sequence: q [n, Hq, D] f16 at positions start_pos .. start_pos + n - 1
+    over the sequence's pages (page_row: int32 [max_pages]; the chunk's K/V appended first)
+    -> out [n, Hq, D] f32."""
+    _need(q, "q", torch.float16, dev=dev.torch_device)
+    n, hq, dh = q.shape
+    if dh != pool.head_dim:
+        raise InvalidArg(f"q head_dim {dh} != pool head_dim {pool.head_dim}")
+    _need(page_row, "page_row", torch.int32, dev=dev.torch_device)
+    if out is None:
+        out = torch.empty((n, hq, dh), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32, (n, hq, dh), dev.torch_device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(dh)
+    dev.check(dev.lib.pi_attn_prefill_paged(dev.h, _vp(q), pool.p, _vp(page_row), page_row.numel(),
+                                            int(start_pos), n, hq, gqa_mode, float(scale), _vp(out),
+                                            dev.stream()))
     return out
 
 

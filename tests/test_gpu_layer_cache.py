@@ -3,8 +3,9 @@ slices the way InferenceContext::forward holds them (src/model/mod.rs:668-1219),
 oracle's per-token restatement (or_attn_layer_tokens) of the same calls.
 
 A sequence is driven through a prompt, single decode tokens and a continued multi-token chunk
-(the three paths of the forward: causal prefill, one decode row, decode rows over the cached
-history).  Tolerances as for the other attention tests: max-abs <= 2e-3 with an f32 cache,
+(the paths of the forward: causal prefill of a prompt, one decode row per token, and a
+continued chunk -- the flash prefill over the sequence's pages for an f16 cache, decode rows
+over the cached history for an f32 one).  Tolerances as for the other attention tests: max-abs <= 2e-3 with an f32 cache,
 per-row relative <= 1e-2 with an f16 cache; q and k come back normalised and rotated as in the
 reference (<= 1e-5).
 """
