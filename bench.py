@@ -52,7 +52,7 @@ def _args():
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--workload", default=None,
                    choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "tq", "copy",
-                            "rows_f", "chunk"],
+                            "rows_f", "chunk", "tq_c4"],
                    help="time one workload only and print its figures (for sweeps)")
     return p.parse_args()
 
@@ -183,11 +183,11 @@ def bench_decode(torch, rt, dev, timer, lens, hq, hkv, d, theta, seed, steps, wa
     return res, (pool, tpt, ctx, q, out, gate)
 
 
-def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup, cpu_s=0.0):
-    """TurboQuant compressed-KV decode (pi_tq_attn_decode) over the config 2 shape: the
-    cache is appended through pi_tq_append (K, V ~ N(0,1) generated on the GPU); the timed
-    call includes the per-query precompute and the merge."""
-    d = 128
+def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup, cpu_s=0.0,
+                    d=128, gated=False):
+    """TurboQuant compressed-KV decode (pi_tq_attn_decode) over a paged cache appended through
+    pi_tq_append (K, V ~ N(0,1) generated on the GPU); the timed call includes the per-query
+    precompute and the merge (and the sigmoid gate when `gated`)."""
     rng = np.random.default_rng(seed)
     n_pages_seq = [(int(x) + PAGE - 1) // PAGE for x in lens]
     total = sum(n_pages_seq)
@@ -197,7 +197,7 @@ def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup, c
     for i, n in enumerate(n_pages_seq):
         pt[i, :n] = perm[off:off + n]
         off += n
-    pool = rt.TqPool(dev, total, hkv)
+    pool = rt.TqPool(dev, total, hkv, head_dim=d)
     tpt = torch.from_numpy(pt).cuda()
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -213,9 +213,11 @@ def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup, c
     q = torch.randn((len(lens), hq, d), generator=g, device="cuda")
     ctx = torch.tensor([int(x) for x in lens], dtype=torch.int32, device="cuda")
     out = torch.empty_like(q)
+    gate = torch.randn(q.shape, generator=g, device="cuda") if gated else None
     lib = dev.lib
     args = (dev.h, ctypes.c_void_p(q.data_ptr()), pool.p, ctypes.c_void_p(tpt.data_ptr()),
-            tpt.shape[1], ctypes.c_void_p(ctx.data_ptr()), len(lens), hq, 0, None,
+            tpt.shape[1], ctypes.c_void_p(ctx.data_ptr()), len(lens), hq, 0,
+            None if gate is None else ctypes.c_void_p(gate.data_ptr()),
             ctypes.c_void_p(out.data_ptr()), None)
 
     def fn():
@@ -226,15 +228,16 @@ def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup, c
     tokens = sum(int(x) for x in lens)
     cpu = None
     if cpu_s > 0:
-        cpu = cpu_tq_decode(torch, pool, tpt, q, out, lens, hq, hkv, cpu_s)
-    # per token and KV head: 64-byte key record + f32 norm + 128 f16 values
-    algo = (tokens * hkv * (64 + 4 + d * 2) + 2 * len(lens) * hq * d * 4
+        cpu = cpu_tq_decode(torch, pool, tpt, q, out, lens, hq, hkv, cpu_s, d, gate)
+    # per token and KV head: d/2-byte key record + f32 norm + d f16 values
+    rec = d // 2 + 4 + d * 2
+    algo = (tokens * hkv * rec + (3 if gated else 2) * len(lens) * hq * d * 4
             + total * 4 + len(lens) * 4 + 2 * hkv * d * d * 4)
     gbs = algo / (t["ms_avg"] * 1e-3) / 1e9
     f16_equiv = tokens * hkv * d * 2 * 2
-    res = {"GB_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "ms_per_step": t["ms_avg"],
+    res = {"head_dim": d, "GB_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "ms_per_step": t["ms_avg"],
            "ms_median": t["ms_median"], "bytes_per_launch": algo, "tokens": tokens,
-           "kv_bytes_vs_f16_pool": round(tokens * hkv * (68 + d * 2) / f16_equiv, 4),
+           "kv_bytes_vs_f16_pool": round(tokens * hkv * rec / f16_equiv, 4),
            "append_tokens_per_s": tokens / append_s}
     if cpu is not None:
         res["cpu_baseline"] = cpu
@@ -242,14 +245,15 @@ def bench_tq_decode(torch, rt, dev, timer, lens, hq, hkv, seed, steps, warmup, c
     return res
 
 
-def cpu_tq_decode(torch, pool, tpt, q, out, lens, hq, hkv, budget_s):
+def cpu_tq_decode(torch, pool, tpt, q, out, lens, hq, hkv, budget_s, d=128, gate=None):
     """or_tq_cache_attend (the compressed-cache attention of src/turboquant/mod.rs:489-535 with
     the precomputed query) per query head, over the stored records read back from the pool,
-    sequence by sequence until the budget is spent."""
+    sequence by sequence until the budget is spent (then the gate, :1192-1196)."""
     from oracle import oracle as orc
     torch.cuda.synchronize()
     qh, oh = q.cpu().numpy(), out.cpu().numpy()
-    mats = [orc.tq_matrices(128, 0xCAFEBABE + h) for h in range(hkv)]
+    gh = None if gate is None else gate.cpu().numpy()
+    mats = [orc.tq_matrices(d, 0xCAFEBABE + h) for h in range(hkv)]
     t = 0.0
     nbytes = toks = done = 0
     err = 0.0
@@ -261,8 +265,10 @@ def cpu_tq_decode(torch, pool, tpt, q, out, lens, hq, hkv, budget_s):
             t0 = time.perf_counter()
             ref = np.stack([orc.tq_cache_attend(qh[i, h], kh, nh, vh, *mats[h % hkv], h % hkv)
                             for h in range(hq)])
+            if gh is not None:
+                ref = orc.apply_gate(ref, gh[i])
             t += time.perf_counter() - t0
-            nbytes += L * hkv * (64 + 4 + 128 * 2) + 2 * hq * 128 * 4
+            nbytes += L * hkv * (d // 2 + 4 + d * 2) + 2 * hq * d * 4
             toks += L
             done += 1
             err = max(err, _row_rel(oh[i], ref))
@@ -271,7 +277,7 @@ def cpu_tq_decode(torch, pool, tpt, q, out, lens, hq, hkv, budget_s):
     return _cpu(nbytes / t / 1e9, "GB/s",
                 f"or_tq_cache_attend per query head on {done} of {len(lens)} sequences ({toks} "
                 f"tokens) of stored records read back from the pool; bytes counted as the GPU "
-                f"entry's (324 B per token and KV head)", round(t, 3),
+                f"entry's ({d // 2 + 4 + d * 2} B per token and KV head)", round(t, 3),
                 parity_max_row_rel_err=round(err, 6))
 
 
@@ -1047,6 +1053,9 @@ def _single(torch, rt, dev, timer, a):
         rng = np.random.default_rng(0x5EED0001)
         lens = [int(x) for x in rng.integers(1024, 32769, size=32)]
         return bench_tq_decode(torch, rt, dev, timer, lens, 32, 8, 0x5EED0004, st, wu)
+    if w == "tq_c4":
+        return bench_tq_decode(torch, rt, dev, timer, [65536] * 8, 16, 2, 0x5EED0014, st, wu,
+                               d=256, gated=True)
     if w == "copy":
         return bench_copy(torch, timer, st, wu)
     if w == "rows_f":
@@ -1161,7 +1170,13 @@ def main():
         torch.cuda.empty_cache()
         # TurboQuant compressed-KV decode on the config 2 shape (3-bit + QJL keys, f16 values)
         wl["c2_turboquant_decode"] = bench_tq_decode(torch, rt, dev, timer, lens, 32, 8, 0x5EED0004,
-                                                     a.steps, a.warmup, cpu_s=budget["tq"])
+                                                     a.steps, a.warmup, cpu_s=budget["tq"] / 2)
+        torch.cuda.empty_cache()
+        # TurboQuant on config 4's attention layer shape: 16/2 heads, D 256, gated, 8 x 65536
+        wl["c4_turboquant_decode_64k"] = bench_tq_decode(torch, rt, dev, timer, [65536] * 8, 16, 2,
+                                                         0x5EED0014, a.steps, a.warmup,
+                                                         cpu_s=budget["tq"] / 2, d=256, gated=True)
+        torch.cuda.empty_cache()
         wl.update(bench_rows_f(torch, rt, dev, timer, a.steps, a.warmup,
                                cpu_s=budget["rows_f"]))
         wl.update(bench_chunk(torch, rt, dev, timer, min(a.steps, 10), min(a.warmup, 3),

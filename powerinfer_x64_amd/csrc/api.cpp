@@ -1254,14 +1254,14 @@ int pi_tq_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t
         return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_pool_create: page_tokens must be 16 (got %d)", page_tokens);
     if (n_pages <= 0 || n_kv_heads <= 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_tq_pool_create: n_pages=%d n_kv_heads=%d", n_pages, n_kv_heads);
-    if (head_dim != 128)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_pool_create: head_dim %d (128)", head_dim);
-    const int D = 128;
+    if (head_dim != 128 && head_dim != 256)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_pool_create: head_dim %d (128 or 256)", head_dim);
+    const int D = head_dim;
     const size_t nblk = (size_t)n_pages * n_kv_heads;
-    const size_t kbytes = nblk * pi::kPageTokens * (pi::kTqKeyBytes + 4);
+    const size_t kbytes = nblk * pi::kPageTokens * (pi::tq_key_bytes(D) + 4);
     const size_t vbytes = nblk * pi::kPageTokens * D * 2;
     const size_t mbytes = (size_t)n_kv_heads * D * D * sizeof(float);
-    // per-head matrices, transposed for the kernels (TurboQuant::new(3, 128, 128,
+    // per-head matrices, transposed for the kernels (TurboQuant::new(3, D, D,
     // 0xCAFE_BABE + h), src/turboquant/mod.rs:430-437)
     std::vector<float> rot((size_t)D * D), qjl((size_t)D * D);
     std::vector<float> rt((size_t)n_kv_heads * D * D), gt((size_t)n_kv_heads * D * D);

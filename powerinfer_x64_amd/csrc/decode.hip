@@ -178,18 +178,19 @@ struct Tile<float, D> {
     }
 };
 
-// TurboQuant pool (src/turboquant/mod.rs:408-566): per (page, KV head) a K
-// block of 16 packed keys (64 B each: 3-bit Lloyd-Max codes of the rotated,
-// sqrt(d)-scaled unit key, LSB first, then 128 QJL sign bits) followed by the
-// 16 f32 key norms, and a V block [128 dims][16 tokens] of f16 values.  The
-// query row is the 256-wide "virtual query" [R.q / sqrt(d) | c * G.R.q / d]
-// (tq_query_kernel), so a key's score is norm * <virtual key, virtual query>
-// with the virtual key [centroid(code_i) | +-1 sign_i].  The dot runs on
-// v_mfma_f32_16x16x32_f16: the k index of MFMA block kb, lane group g,
-// element e is dim 32g + 8kb + e (kb < 4) or sign 32g + 8(kb-4) + e, so a
-// lane decodes only the 32 codes (3 dwords) and 32 signs (1 dword) of its
-// quarter of the key.  The centroid half of the query is split into f16
-// hi + lo parts; centroids are f16 (relative rounding <= 1.9e-4).
+// TurboQuant pool (src/turboquant/mod.rs:408-566), head_dim D = 128 or 256:
+// per (page, KV head) a K block of 16 packed keys (D/2 bytes each: 3-bit
+// Lloyd-Max codes of the rotated, sqrt(D)-scaled unit key, LSB first, then D
+// QJL sign bits) followed by the 16 f32 key norms, and a V block [D dims][16
+// tokens] of f16 values.  The query row is the 2D-wide "virtual query"
+// [R.q / sqrt(D) | c * G.R.q / sqrt(D)] (tq_query_kernel), so a key's score is
+// norm * <virtual key, virtual query> with the virtual key [centroid(code_i) |
+// +-1 sign_i].  The dot runs on v_mfma_f32_16x16x32_f16: the k index of MFMA
+// block kb, lane group g, element e is dim (D/4) g + 8 kb + e (kb < D/32) or
+// sign (D/4) g + 8 (kb - D/32) + e, so a lane decodes only the D/4 codes
+// (3D/128 dwords) and D/4 signs (D/128 dwords) of its quarter of the key.  The
+// centroid half of the query is split into f16 hi + lo parts; centroids are
+// f16 (relative rounding <= 1.9e-4).
 struct TqKey {};
 constexpr uint64_t kTqMagF16 =       // f16 bits of 0.2451, 0.756, 1.344, 2.152
     0x33D8ull | (0x3A0Cull << 16) | (0x3D60ull << 32) | (0x404Eull << 48);
@@ -224,30 +225,33 @@ __device__ __forceinline__ void tq_lut_build() {
     }
 }
 
-template <>
-struct Tile<TqKey, 128> {
-    static constexpr int D = 128;
+template <int D>
+struct Tile<TqKey, D> {
     static constexpr int NV = D / 16;
-    static constexpr size_t KBLK = (size_t)kPageTokens * (kTqKeyBytes + 4);
+    static constexpr int NQ = D / 32;        // MFMA k-blocks of each half (centroids, signs)
+    static constexpr int CW = 3 * D / 128;   // code dwords of a lane's quarter
+    static constexpr int SW = D / 128;       // sign dwords of a lane's quarter
+    static constexpr int KB = tq_key_bytes(D);
+    static constexpr size_t KBLK = (size_t)kPageTokens * (KB + 4);
     static constexpr size_t VBLK = (size_t)kPageTokens * D * 2;
     static constexpr int QD = 2 * D;
-    uint32_t code[3];  // 3-bit codes of dims 32g .. 32g+31 of token lane%16
-    uint32_t sign;     // QJL signs 32g .. 32g+31 of token lane%16
-    f32x4 norm;        // norms of tokens 4g .. 4g+3 (the rows of this lane's scores)
+    uint32_t code[CW];  // 3-bit codes of dims (D/4) g .. +D/4 of token lane%16
+    uint32_t sign[SW];  // QJL signs of the same dims
+    f32x4 norm;         // norms of tokens 4g .. 4g+3 (the rows of this lane's scores)
     f16x4 v[NV];
     struct Q {
-        f16x8 hi[8];
-        f16x8 lo[4];
+        f16x8 hi[2 * NQ];
+        f16x8 lo[NQ];
     };
 
     __device__ __forceinline__ void load(const char* kbp, const char* vbp, int lane) {
         const int tok = lane & 15, grp = lane >> 4;
-        const uint32_t* rec = reinterpret_cast<const uint32_t*>(kbp + tok * kTqKeyBytes);
-        code[0] = rec[3 * grp];
-        code[1] = rec[3 * grp + 1];
-        code[2] = rec[3 * grp + 2];
-        sign = rec[12 + grp];
-        norm = *reinterpret_cast<const f32x4*>(kbp + kPageTokens * kTqKeyBytes + 16 * grp);
+        const uint32_t* rec = reinterpret_cast<const uint32_t*>(kbp + tok * KB);
+#pragma unroll
+        for (int w = 0; w < CW; ++w) code[w] = rec[CW * grp + w];
+#pragma unroll
+        for (int w = 0; w < SW; ++w) sign[w] = rec[4 * CW + SW * grp + w];
+        norm = *reinterpret_cast<const f32x4*>(kbp + kPageTokens * KB + 16 * grp);
         const f16* vb = reinterpret_cast<const f16*>(vbp);
 #pragma unroll
         for (int t = 0; t < NV; ++t)
@@ -255,8 +259,8 @@ struct Tile<TqKey, 128> {
     }
     static __device__ __forceinline__ void load_q(Q& q, const float* qrow, float qs, int grp) {
 #pragma unroll
-        for (int kb = 0; kb < 8; ++kb) {
-            const float* src = qrow + (kb < 4 ? 32 * grp + 8 * kb : D + 32 * grp + 8 * (kb - 4));
+        for (int kb = 0; kb < 2 * NQ; ++kb) {
+            const float* src = qrow + (kb < NQ ? (D / 4) * grp + 8 * kb : D + (D / 4) * grp + 8 * (kb - NQ));
             const f32x4 a = *reinterpret_cast<const f32x4*>(src);
             const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
@@ -264,7 +268,7 @@ struct Tile<TqKey, 128> {
                 const float x = (i < 4 ? a[i] : b[i - 4]) * qs;
                 const f16 h = to_f16(x);
                 q.hi[kb][i] = h;
-                if (kb < 4) q.lo[kb][i] = to_f16(x - (float)h);
+                if (kb < NQ) q.lo[kb][i] = to_f16(x - (float)h);
             }
         }
     }
@@ -280,7 +284,7 @@ struct Tile<TqKey, 128> {
         const TqLut& L = tq_lut();
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+        for (int kb = 0; kb < NQ; ++kb) {
             u32x4 w;
 #pragma unroll
             for (int p = 0; p < 4; ++p) w[p] = L.pair[pair_of(4 * kb + p)];
@@ -289,9 +293,9 @@ struct Tile<TqKey, 128> {
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, q.lo[kb], s, 0, 0, 0);
         }
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const f16x8 sf = L.sign[(sign >> (8 * kb)) & 255u];
-            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, q.hi[4 + kb], s, 0, 0, 0);
+        for (int kb = 0; kb < NQ; ++kb) {
+            const f16x8 sf = L.sign[(sign[kb >> 2] >> (8 * (kb & 3))) & 255u];
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(sf, q.hi[NQ + kb], s, 0, 0, 0);
         }
         return s * norm;
     }
@@ -654,7 +658,7 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
         cus = 256;
     int per_cu = 1;
     const bool hp = g.dtype == 1;
-    if (g.dtype == kTqDtype) per_cu = wgs_per_cu<TqKey, 128>();
+    if (g.dtype == kTqDtype) per_cu = g.head_dim == 256 ? wgs_per_cu<TqKey, 256>() : wgs_per_cu<TqKey, 128>();
     else switch (g.head_dim) {
         case 64: per_cu = hp ? wgs_per_cu<f16, 64>() : wgs_per_cu<float, 64>(); break;
         case 128: per_cu = hp ? wgs_per_cu<f16, 128>() : wgs_per_cu<float, 128>(); break;
@@ -707,8 +711,11 @@ size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan) {
 
 hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,
                          const DecodePlan& plan, hipStream_t s) {
-    if (g.dtype == kTqDtype)
-        return g.head_dim == 128 ? launch_t<TqKey, 128>(g, p, ws, plan, s) : hipErrorInvalidValue;
+    if (g.dtype == kTqDtype) {
+        if (g.head_dim == 128) return launch_t<TqKey, 128>(g, p, ws, plan, s);
+        if (g.head_dim == 256) return launch_t<TqKey, 256>(g, p, ws, plan, s);
+        return hipErrorInvalidValue;
+    }
     const bool hp = g.dtype == 1;
     switch (g.head_dim) {
         case 64: return hp ? launch_t<f16, 64>(g, p, ws, plan, s) : launch_t<float, 64>(g, p, ws, plan, s);

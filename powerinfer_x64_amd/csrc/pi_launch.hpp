@@ -11,8 +11,9 @@ namespace pi {
 constexpr int kPageTokens = 16;  // tokens per KV page
 constexpr int kItemPages = 16;   // max pages per decode work item (the balancing unit)
 constexpr int kMaxBatch = 4096;  // sequences per decode launch (LDS prefix scan)
-constexpr int kTqDtype = 3;      // KvGeom::dtype of a TurboQuant pool (head_dim 128)
-constexpr int kTqKeyBytes = 64;  // packed TurboQuant key: 3 x 128 code bits + 128 sign bits
+constexpr int kTqDtype = 3;      // KvGeom::dtype of a TurboQuant pool (head_dim 128 or 256)
+// Bytes of one packed TurboQuant key of head_dim d: 3 d code bits + d QJL sign bits.
+constexpr int tq_key_bytes(int d) { return d / 2; }
 
 // KV pool geometry: one K and one V block of kPageTokens x head_dim elements
 // per (page, kv head).  K block layout: [head_dim/E][16 tokens][E] with
@@ -30,15 +31,15 @@ struct KvGeom {
     int32_t elem_bytes;
 };
 
-// TurboQuant compressed pool (head_dim 128): g.k holds per (page, KV head)
-// 16 packed keys of kTqKeyBytes then their 16 f32 norms, g.v the f16 V block
-// [128][16]; rt / gt are the per-head rotation and QJL matrices, transposed
-// ([h][j][i] = M[h][i][j]) so that lane i reads row i coalesced.
+// TurboQuant compressed pool (head_dim d = 128 or 256): g.k holds per (page,
+// KV head) 16 packed keys of tq_key_bytes(d) then their 16 f32 norms, g.v the
+// f16 V block [d][16]; rt / gt are the per-head rotation and QJL matrices,
+// transposed ([h][j][i] = M[h][i][j]) so that lane i reads row i coalesced.
 struct TqPool {
     KvGeom g;
     float* rt;
     float* gt;
-    float scale;  // sqrt(128) in f32: the quantizer's per-coordinate scale
+    float scale;  // sqrt(d) in f32: the quantizer's per-coordinate scale
     float corr;   // residual_norm * qjl_scale of the 3-bit estimator
 };
 

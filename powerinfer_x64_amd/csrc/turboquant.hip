@@ -4,9 +4,9 @@
 // tile (decode.hip).
 //
 // Replaces CompressedKVCache (src/turboquant/mod.rs:408-566) with head_dim
-// 128: keys are L2-normalised, rotated by the head's orthogonal matrix R,
-// scaled by sqrt(128), coded with the 3-bit Lloyd-Max codebook, and the
-// residual's projections on the QJL matrix G keep their signs
+// D = 128 or 256: keys are L2-normalised, rotated by the head's orthogonal
+// matrix R, scaled by sqrt(D), coded with the 3-bit Lloyd-Max codebook, and
+// the residual's D projections on the QJL matrix G keep their signs
 // (quantize_vector, :128-187); values are stored as f16 (:481-483).
 //
 // tq_append_kernel reproduces quantize_vector bit for bit: every sum is the
@@ -15,14 +15,12 @@
 // rounded, the nearest
 // centroid takes the first strict minimum, and a QJL bit is set for a
 // projection >= 0.  One wavefront per (sequence, token, KV
-// head); lane i owns rotated coordinates i and i + 64.
+// head); lane i owns rotated coordinates i + 64 j, j < D / 64.
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
 namespace pi {
 namespace {
-
-constexpr int TD = 128;  // head_dim of the TurboQuant pool
 
 __constant__ float kCentroids3[8] = {-2.1520f, -1.3440f, -0.7560f, -0.2451f,
                                      0.2451f,  0.7560f,  1.3440f,  2.1520f};
@@ -61,14 +59,18 @@ __device__ __forceinline__ int nearest_centroid(float x) {
     return best;
 }
 
+template <int D>
 __global__ __launch_bounds__(256) void tq_append_kernel(TqPool t, const float* __restrict__ k,
                                                         const float* __restrict__ v,
                                                         const int32_t* __restrict__ page_table,
                                                         int max_pages,
                                                         const int32_t* __restrict__ start_pos,
                                                         int n_seq, int n_tok) {
-    __shared__ float s_x[4][TD];
-    __shared__ uint32_t s_bits[4][12];
+    constexpr int NJ = D / 64;          // coordinates per lane
+    constexpr int CW = 3 * D / 32;      // record dwords of the 3-bit codes
+    constexpr int KB = tq_key_bytes(D);
+    __shared__ float s_x[4][D];
+    __shared__ uint32_t s_bits[4][CW];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int n_kv = t.g.n_kv_heads;
     const long long item = (long long)blockIdx.x * 4 + w;
@@ -77,57 +79,67 @@ __global__ __launch_bounds__(256) void tq_append_kernel(TqPool t, const float* _
     const int kvh = (int)(it % n_kv);
     const int tok = (int)((it / n_kv) % n_tok);
     const int seq = (int)(it / ((long long)n_kv * n_tok));
-    const size_t row = (((size_t)seq * n_tok + tok) * n_kv + kvh) * TD;
+    const size_t row = (((size_t)seq * n_tok + tok) * n_kv + kvh) * D;
 
     // L2 norm: sequential f32 sum of squares (:466-468)
-    s_x[w][lane] = k[row + lane];
-    s_x[w][lane + 64] = k[row + lane + 64];
-    if (lane < 12) s_bits[w][lane] = 0u;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) s_x[w][lane + 64 * j] = k[row + lane + 64 * j];
+    if (lane < CW) s_bits[w][lane] = 0u;
     __syncthreads();
     float ss = 0.f;
-    for (int j = 0; j < TD; ++j) ss = __fadd_rn(ss, __fmul_rn(s_x[w][j], s_x[w][j]));
+    for (int j = 0; j < D; ++j) ss = __fadd_rn(ss, __fmul_rn(s_x[w][j], s_x[w][j]));
     const float norm = sqrt_rn(ss);
     const float inv = norm > 1e-12f ? __fdiv_rn(1.0f, norm) : 0.0f;
-    const float x0 = __fmul_rn(s_x[w][lane], inv), x1 = __fmul_rn(s_x[w][lane + 64], inv);
-    __syncthreads();
-    s_x[w][lane] = x0;
-    s_x[w][lane + 64] = x1;
-    __syncthreads();
-
-    // rotation rows lane, lane + 64, then the sqrt(d) scale (:131-146)
-    const float* rt = t.rt + (size_t)kvh * TD * TD;
-    float r0 = 0.f, r1 = 0.f;
-    for (int j = 0; j < TD; ++j) {
-        const float xj = s_x[w][j];
-        r0 = __fadd_rn(r0, __fmul_rn(rt[j * TD + lane], xj));
-        r1 = __fadd_rn(r1, __fmul_rn(rt[j * TD + lane + 64], xj));
-    }
-    r0 = __fmul_rn(r0, t.scale);
-    r1 = __fmul_rn(r1, t.scale);
-    const int c0 = nearest_centroid(r0), c1 = nearest_centroid(r1);
-    __syncthreads();
-    s_x[w][lane] = __fsub_rn(r0, kCentroids3[c0]);  // residual (:170-173)
-    s_x[w][lane + 64] = __fsub_rn(r1, kCentroids3[c1]);
-    // codes: coordinate i occupies bits 3i .. 3i+2 of the record
+    float x[NJ];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int i = lane + 64 * h;
-        const uint32_t c = (uint32_t)(h ? c1 : c0);
+    for (int j = 0; j < NJ; ++j) x[j] = __fmul_rn(s_x[w][lane + 64 * j], inv);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) s_x[w][lane + 64 * j] = x[j];
+    __syncthreads();
+
+    // rotation rows lane + 64 j, then the sqrt(d) scale (:131-146)
+    const float* rt = t.rt + (size_t)kvh * D * D;
+    float r[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) r[j] = 0.f;
+    for (int i = 0; i < D; ++i) {
+        const float xi = s_x[w][i];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) r[j] = __fadd_rn(r[j], __fmul_rn(rt[i * D + lane + 64 * j], xi));
+    }
+    int c[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        r[j] = __fmul_rn(r[j], t.scale);
+        c[j] = nearest_centroid(r[j]);
+    }
+    __syncthreads();
+    // residual (:170-173); codes: coordinate i occupies bits 3i .. 3i+2 of the record
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int i = lane + 64 * j;
+        s_x[w][i] = __fsub_rn(r[j], kCentroids3[c[j]]);
+        const uint32_t cv = (uint32_t)c[j];
         const int bit = 3 * i, wd = bit >> 5, off = bit & 31;
-        atomicOr(&s_bits[w][wd], c << off);
-        if (off > 29) atomicOr(&s_bits[w][wd + 1], c >> (32 - off));
+        atomicOr(&s_bits[w][wd], cv << off);
+        if (off > 29) atomicOr(&s_bits[w][wd + 1], cv >> (32 - off));
     }
     __syncthreads();
 
-    // QJL signs of G . residual (:176-184)
-    const float* gt = t.gt + (size_t)kvh * TD * TD;
-    float p0 = 0.f, p1 = 0.f;
-    for (int j = 0; j < TD; ++j) {
-        const float rj = s_x[w][j];
-        p0 = __fadd_rn(p0, __fmul_rn(gt[j * TD + lane], rj));
-        p1 = __fadd_rn(p1, __fmul_rn(gt[j * TD + lane + 64], rj));
+    // QJL signs of G . residual (:176-184), one ballot per 64 projections
+    const float* gt = t.gt + (size_t)kvh * D * D;
+    float pr[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) pr[j] = 0.f;
+    for (int i = 0; i < D; ++i) {
+        const float ri = s_x[w][i];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) pr[j] = __fadd_rn(pr[j], __fmul_rn(gt[i * D + lane + 64 * j], ri));
     }
-    const uint64_t m0 = __ballot(p0 >= 0.0f), m1 = __ballot(p1 >= 0.0f);
+    uint64_t m[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) m[j] = __ballot(pr[j] >= 0.0f);
     if (!on) return;
 
     const int pos = start_pos[seq] + tok;
@@ -136,46 +148,50 @@ __global__ __launch_bounds__(256) void tq_append_kernel(TqPool t, const float* _
     if (page < 0 || page >= t.g.n_pages) return;
     const int slot = pos % kPageTokens;
     const size_t blk = (size_t)page * n_kv + kvh;
-    char* kb = reinterpret_cast<char*>(t.g.k) + blk * (kPageTokens * (kTqKeyBytes + 4));
-    uint32_t* rec = reinterpret_cast<uint32_t*>(kb + slot * kTqKeyBytes);
-    if (lane < 12) rec[lane] = s_bits[w][lane];
-    if (lane == 12) rec[12] = (uint32_t)m0;
-    if (lane == 13) rec[13] = (uint32_t)(m0 >> 32);
-    if (lane == 14) rec[14] = (uint32_t)m1;
-    if (lane == 15) rec[15] = (uint32_t)(m1 >> 32);
-    if (lane == 16) reinterpret_cast<float*>(kb + kPageTokens * kTqKeyBytes)[slot] = norm;
+    char* kb = reinterpret_cast<char*>(t.g.k) + blk * (kPageTokens * (KB + 4));
+    uint32_t* rec = reinterpret_cast<uint32_t*>(kb + slot * KB);
+    if (lane < CW) rec[lane] = s_bits[w][lane];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        if (lane == CW + 2 * j) rec[CW + 2 * j] = (uint32_t)m[j];
+        if (lane == CW + 2 * j + 1) rec[CW + 2 * j + 1] = (uint32_t)(m[j] >> 32);
+    }
+    if (lane == 63) reinterpret_cast<float*>(kb + kPageTokens * KB)[slot] = norm;
     // values as f16 (round to nearest even), V block [dim][16 tokens]
-    f16* vb = reinterpret_cast<f16*>(t.g.v) + blk * (kPageTokens * TD);
-    vb[lane * kPageTokens + slot] = to_f16(v[row + lane]);
-    vb[(lane + 64) * kPageTokens + slot] = to_f16(v[row + lane + 64]);
+    f16* vb = reinterpret_cast<f16*>(t.g.v) + blk * (kPageTokens * D);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+        vb[(lane + 64 * j) * kPageTokens + slot] = to_f16(v[row + lane + 64 * j]);
 }
 
 // Stored records of tokens start .. start+n_tok-1 of one sequence: keys
-// [n_tok][Hkv][64] bytes, norms [n_tok][Hkv], values [n_tok][Hkv][128] f16.
+// [n_tok][Hkv][D/2] bytes, norms [n_tok][Hkv], values [n_tok][Hkv][D] f16.
+template <int D>
 __global__ __launch_bounds__(256) void tq_read_kernel(TqPool t, const int32_t* __restrict__ page_table,
                                                       int max_pages, int seq, int start, int n_tok,
                                                       uint8_t* __restrict__ keys_out,
                                                       float* __restrict__ norms_out,
                                                       uint16_t* __restrict__ v_out) {
+    constexpr int KB = tq_key_bytes(D);
     const int n_kv = t.g.n_kv_heads;
-    const long long total = (long long)n_tok * n_kv * TD;
+    const long long total = (long long)n_tok * n_kv * D;
     for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (long long)gridDim.x * blockDim.x) {
-        const int d = (int)(e % TD);
-        const int kvh = (int)((e / TD) % n_kv);
-        const int i = (int)(e / ((long long)TD * n_kv));
+        const int d = (int)(e % D);
+        const int kvh = (int)((e / D) % n_kv);
+        const int i = (int)(e / ((long long)D * n_kv));
         const int pos = start + i;
         if (pos / kPageTokens >= max_pages) continue;
         const int page = page_table[(size_t)seq * max_pages + pos / kPageTokens];
         if (page < 0 || page >= t.g.n_pages) continue;
         const int slot = pos % kPageTokens;
         const size_t blk = (size_t)page * n_kv + kvh;
-        const char* kb = reinterpret_cast<const char*>(t.g.k) + blk * (kPageTokens * (kTqKeyBytes + 4));
-        const uint16_t* vb = reinterpret_cast<const uint16_t*>(t.g.v) + blk * (kPageTokens * TD);
+        const char* kb = reinterpret_cast<const char*>(t.g.k) + blk * (kPageTokens * (KB + 4));
+        const uint16_t* vb = reinterpret_cast<const uint16_t*>(t.g.v) + blk * (kPageTokens * D);
         const size_t o = (size_t)i * n_kv + kvh;
-        v_out[o * TD + d] = vb[d * kPageTokens + slot];
-        if (d < kTqKeyBytes) keys_out[o * kTqKeyBytes + d] = (uint8_t)kb[slot * kTqKeyBytes + d];
-        if (d == 0) norms_out[o] = reinterpret_cast<const float*>(kb + kPageTokens * kTqKeyBytes)[slot];
+        v_out[o * D + d] = vb[d * kPageTokens + slot];
+        if (d < KB) keys_out[o * KB + d] = (uint8_t)kb[slot * KB + d];
+        if (d == 0) norms_out[o] = reinterpret_cast<const float*>(kb + kPageTokens * KB)[slot];
     }
 }
 
@@ -185,76 +201,97 @@ __global__ __launch_bounds__(256) void tq_read_kernel(TqPool t, const int32_t* _
 //
 // One workgroup of 256 threads per (sequence, KV head, chunk of up to
 // kQueryHeads query heads of that KV head): every matrix element read from
-// L2 serves all heads of the chunk.  Thread (half, i) owns output column i
-// and sums rows j of its half (the matrices are stored transposed, so a row
-// step reads 512 contiguous bytes per wavefront); the two halves meet in
-// LDS.  The queries sit in LDS as [row][head], one 16-byte read per row.
+// L2 serves all heads of the chunk.  Thread (half, i) owns output columns
+// i + 128 c (c < D / 128) and sums rows j of its half (the matrices are stored
+// transposed, so a row step reads 512 contiguous bytes per wavefront); the two
+// halves meet in LDS.  The queries sit in LDS as [row][head], one 16-byte read
+// per row.
 constexpr int kQueryHeads = 4;
 
+template <int D>
 __global__ __launch_bounds__(256) void tq_query_kernel(TqPool t, const float* __restrict__ q,
                                                        float* __restrict__ qv, int n_q_heads,
                                                        int gqa_mode) {
-    __shared__ float4 s_x[TD];                    // query (pass 1) or R.q (pass 2), [row][head]
-    __shared__ float s_part[2][kQueryHeads][TD];  // per-half partial sums
+    constexpr int NC = D / 128;                  // output columns per thread
+    __shared__ float4 s_x[D];                    // query (pass 1) or R.q (pass 2), [row][head]
+    __shared__ float s_part[2][kQueryHeads][D];  // per-half partial sums
     const int n_kv = t.g.n_kv_heads;
     const int group = n_q_heads / n_kv;
     const int n_chunks = (group + kQueryHeads - 1) / kQueryHeads;
     const int kvh = blockIdx.x / n_chunks, c0 = (blockIdx.x % n_chunks) * kQueryHeads;
     const int nh = min(kQueryHeads, group - c0);
-    const int b = blockIdx.y, tid = threadIdx.x, half = tid >> 7, i = tid & (TD - 1);
+    const int b = blockIdx.y, tid = threadIdx.x, half = tid >> 7, i = tid & 127;
     auto head_of = [&](int k) { return gqa_mode == 0 ? kvh + (c0 + k) * n_kv : kvh * group + c0 + k; };
 
-    // stage the chunk's queries: thread (half, i) loads heads 2*half, 2*half + 1 of row i
+    // stage the chunk's queries: thread (half, i) loads heads 2*half, 2*half + 1 of rows i + 128 c
     float* sx = reinterpret_cast<float*>(s_x);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-        const int k = 2 * half + kk;
-        sx[i * kQueryHeads + k] = k < nh ? q[((size_t)b * n_q_heads + head_of(k)) * TD + i] : 0.f;
-    }
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int k = 2 * half + kk, row = i + 128 * c;
+            sx[row * kQueryHeads + k] = k < nh ? q[((size_t)b * n_q_heads + head_of(k)) * D + row] : 0.f;
+        }
     __syncthreads();
 
     const float inv = 1.0f / t.scale;
-    float r_own[2] = {0.f, 0.f};  // R.q of (head 2*half + kk, column i), kept for the output
+    float r_own[NC][2];  // R.q of (head 2*half + kk, column i + 128 c), kept for the output
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
-        const float* mt = (pass == 0 ? t.rt : t.gt) + (size_t)kvh * TD * TD + (size_t)half * (TD / 2) * TD + i;
-        const float4* xs = s_x + half * (TD / 2);
-        float acc[kQueryHeads] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 16
-        for (int j = 0; j < TD / 2; ++j) {
-            const float m = mt[(size_t)j * TD];
+        const float* mt = (pass == 0 ? t.rt : t.gt) + (size_t)kvh * D * D + (size_t)half * (D / 2) * D + i;
+        const float4* xs = s_x + half * (D / 2);
+        float acc[NC][kQueryHeads];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int k = 0; k < kQueryHeads; ++k) acc[c][k] = 0.f;
+#pragma unroll 8
+        for (int j = 0; j < D / 2; ++j) {
             const float4 x = xs[j];
-            acc[0] = fmaf(m, x.x, acc[0]);
-            acc[1] = fmaf(m, x.y, acc[1]);
-            acc[2] = fmaf(m, x.z, acc[2]);
-            acc[3] = fmaf(m, x.w, acc[3]);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float m = mt[(size_t)j * D + 128 * c];
+                acc[c][0] = fmaf(m, x.x, acc[c][0]);
+                acc[c][1] = fmaf(m, x.y, acc[c][1]);
+                acc[c][2] = fmaf(m, x.z, acc[c][2]);
+                acc[c][3] = fmaf(m, x.w, acc[c][3]);
+            }
         }
 #pragma unroll
-        for (int k = 0; k < kQueryHeads; ++k) s_part[half][k][i] = acc[k];
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int k = 0; k < kQueryHeads; ++k) s_part[half][k][i + 128 * c] = acc[c][k];
         __syncthreads();
-        // thread (half, i) finishes heads 2*half, 2*half + 1 of column i
-        float out[2];
+        // thread (half, i) finishes heads 2*half, 2*half + 1 of its columns
+        float out[NC][2];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const int k = 2 * half + kk;
-            out[kk] = s_part[0][k][i] + s_part[1][k][i];
-        }
-        if (pass == 0) {
+        for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-                r_own[kk] = out[kk];
-                sx[i * kQueryHeads + 2 * half + kk] = out[kk];  // every read of pass 0 ended at the barrier
+                const int k = 2 * half + kk, col = i + 128 * c;
+                out[c][kk] = s_part[0][k][col] + s_part[1][k][col];
             }
+        if (pass == 0) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    r_own[c][kk] = out[c][kk];
+                    // every read of pass 0 ended at the barrier above
+                    sx[(i + 128 * c) * kQueryHeads + 2 * half + kk] = out[c][kk];
+                }
             __syncthreads();
         } else {
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int k = 2 * half + kk;
-                if (k >= nh) continue;
-                float* row = qv + ((size_t)b * n_q_heads + head_of(k)) * 2 * TD;
-                row[i] = r_own[kk] * inv;
-                row[TD + i] = t.corr * (out[kk] * inv);
-            }
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int k = 2 * half + kk, col = i + 128 * c;
+                    if (k >= nh) continue;
+                    float* row = qv + ((size_t)b * n_q_heads + head_of(k)) * 2 * D;
+                    row[col] = r_own[c][kk] * inv;
+                    row[D + col] = t.corr * (out[c][kk] * inv);
+                }
         }
     }
 }
@@ -267,20 +304,33 @@ hipError_t launch_tq_append(const TqPool& t, const float* k, const float* v,
     const long long items = (long long)n_seq * n_tok * t.g.n_kv_heads;
     if (items <= 0) return hipSuccess;
     if ((items + 3) / 4 > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(tq_append_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, t, k,
-                       v, page_table, max_pages, start_pos, n_seq, n_tok);
+    const dim3 grid((unsigned)((items + 3) / 4));
+    if (t.g.head_dim == 128)
+        hipLaunchKernelGGL(tq_append_kernel<128>, grid, dim3(256), 0, s, t, k, v, page_table, max_pages,
+                           start_pos, n_seq, n_tok);
+    else if (t.g.head_dim == 256)
+        hipLaunchKernelGGL(tq_append_kernel<256>, grid, dim3(256), 0, s, t, k, v, page_table, max_pages,
+                           start_pos, n_seq, n_tok);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 hipError_t launch_tq_read(const TqPool& t, const int32_t* page_table, int32_t max_pages,
                           int32_t seq, int32_t start, int32_t n_tok, uint8_t* keys_out,
                           float* norms_out, uint16_t* v_out, hipStream_t s) {
-    const long long total = (long long)n_tok * t.g.n_kv_heads * TD;
+    const long long total = (long long)n_tok * t.g.n_kv_heads * t.g.head_dim;
     if (total <= 0) return hipSuccess;
     long long blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(tq_read_kernel, dim3((unsigned)blocks), dim3(256), 0, s, t, page_table,
-                       max_pages, seq, start, n_tok, keys_out, norms_out, v_out);
+    if (t.g.head_dim == 128)
+        hipLaunchKernelGGL(tq_read_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, s, t, page_table,
+                           max_pages, seq, start, n_tok, keys_out, norms_out, v_out);
+    else if (t.g.head_dim == 256)
+        hipLaunchKernelGGL(tq_read_kernel<256>, dim3((unsigned)blocks), dim3(256), 0, s, t, page_table,
+                           max_pages, seq, start, n_tok, keys_out, norms_out, v_out);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
@@ -289,8 +339,13 @@ hipError_t launch_tq_query(const TqPool& t, const float* q, float* qv, int32_t b
     if (batch <= 0) return hipSuccess;
     const int group = n_q_heads / t.g.n_kv_heads;
     const int n_chunks = (group + kQueryHeads - 1) / kQueryHeads;
-    hipLaunchKernelGGL(tq_query_kernel, dim3(t.g.n_kv_heads * n_chunks, batch), dim3(256), 0, s, t,
-                       q, qv, n_q_heads, gqa_mode);
+    const dim3 grid(t.g.n_kv_heads * n_chunks, batch);
+    if (t.g.head_dim == 128)
+        hipLaunchKernelGGL(tq_query_kernel<128>, grid, dim3(256), 0, s, t, q, qv, n_q_heads, gqa_mode);
+    else if (t.g.head_dim == 256)
+        hipLaunchKernelGGL(tq_query_kernel<256>, grid, dim3(256), 0, s, t, q, qv, n_q_heads, gqa_mode);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

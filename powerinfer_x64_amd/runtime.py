@@ -314,14 +314,14 @@ class GdnLayer:
 
 class TqPool:
     """TurboQuant compressed KV cache (CompressedKVCache, src/turboquant/mod.rs:408-566) in
-    16-token pages: 64-byte 3-bit + QJL key records with f32 norms, f16 values; head_dim 128."""
-
-    KEY_BYTES = 64
+    16-token pages: head_dim/2-byte 3-bit + QJL key records with f32 norms, f16 values;
+    head_dim 128 or 256."""
 
     def __init__(self, dev: Device, n_pages: int, n_kv_heads: int, head_dim: int = 128,
                  page_tokens: int = PAGE_TOKENS):
         self.dev = dev
         self.n_pages, self.n_kv_heads, self.head_dim = n_pages, n_kv_heads, head_dim
+        self.KEY_BYTES = head_dim // 2
         p = ctypes.c_void_p()
         dev.check(dev.lib.pi_tq_pool_create(dev.h, n_pages, page_tokens, n_kv_heads, head_dim,
                                             ctypes.byref(p)))
@@ -344,7 +344,7 @@ class TqPool:
 
     def append(self, k: torch.Tensor, v: torch.Tensor, page_table: torch.Tensor,
                start_pos: torch.Tensor):
-        """k, v: [n_seq, n_tok, n_kv_heads, 128] f32."""
+        """k, v: [n_seq, n_tok, n_kv_heads, head_dim] f32."""
         d = self.dev
         if k.dim() != 4 or k.shape[2:] != (self.n_kv_heads, self.head_dim):
             raise InvalidArg(f"k: shape {tuple(k.shape)}")
@@ -359,7 +359,8 @@ class TqPool:
                                    page_table.shape[1], _vp(start_pos), n_seq, n_tok, d.stream()))
 
     def read(self, page_table: torch.Tensor, seq: int, start: int, n_tok: int):
-        """(keys [n_tok, Hkv, 64] uint8, norms [n_tok, Hkv] f32, values [n_tok, Hkv, 128] f16)."""
+        """(keys [n_tok, Hkv, head_dim/2] uint8, norms [n_tok, Hkv] f32, values [n_tok, Hkv,
+        head_dim] f16)."""
         d = self.dev
         _need(page_table, "page_table", torch.int32, dev=d.torch_device)
         ko = torch.empty((n_tok, self.n_kv_heads, self.KEY_BYTES), dtype=torch.uint8,
@@ -387,7 +388,7 @@ def tq_generate(dim: int, seed: int):
 def tq_attn_decode(dev: Device, q: torch.Tensor, pool: TqPool, page_table: torch.Tensor,
                    ctx_len: torch.Tensor, gqa_mode: int = MODULO,
                    gate: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
-    """q [B, Hq, 128] f32 -> out [B, Hq, 128] f32 over each sequence's compressed cache."""
+    """q [B, Hq, D] f32 -> out [B, Hq, D] f32 over each sequence's compressed cache."""
     _need(q, "q", torch.float32, dev=dev.torch_device)
     b, hq, dh = q.shape
     if dh != pool.head_dim:

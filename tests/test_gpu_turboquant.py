@@ -2,8 +2,9 @@
 (src/turboquant/mod.rs:408-566 and the compressed branch of the decode
 attention, src/model/mod.rs:1161-1166).
 
-Append: the stored 64-byte key records, norms and f16 values must equal the
-restated quantize_vector / append byte for byte.  Decode: per head row
+Append: the stored key records (head_dim/2 bytes: 64 at D 128, 128 at D 256),
+norms and f16 values must equal the restated quantize_vector / append byte for
+byte.  Decode: per head row
 ||out - ref||_2 / ||ref||_2 <= 1e-2 (the north star's bound for an f16 KV
 cache); the GPU dot uses f16 centroids (relative rounding <= 1.9e-4) and
 keeps the weights below 1e-7 that the reference's value sum skips.
@@ -14,23 +15,23 @@ import torch
 
 from oracle import oracle as o
 from powerinfer_x64_amd import runtime as rt
-from tests.gpu_util import device, row_rel_err, to_dev
+from tests.gpu_util import device, parallel_map, row_rel_err, to_dev
 
 pytestmark = pytest.mark.gpu
 D = 128
 
 
-def _matrices(n_kv):
-    Rs, Gs = zip(*[o.tq_matrices(D, 0xCAFEBABE + h) for h in range(n_kv)])
+def _matrices(n_kv, d=D):
+    Rs, Gs = zip(*[o.tq_matrices(d, 0xCAFEBABE + h) for h in range(n_kv)])
     return np.stack(Rs), np.stack(Gs)
 
 
 class TqCase:
     """Sequences of lengths `lens` appended in chunks into a permuted page table."""
 
-    def __init__(self, rng, lens, hkv, extra_pages=2, key_scale=None):
+    def __init__(self, rng, lens, hkv, extra_pages=2, key_scale=None, d=D):
         self.lens = [int(x) for x in lens]
-        self.hkv = hkv
+        self.hkv, self.d = hkv, d
         b = len(self.lens)
         self.max_pages = max(1, max((x + 15) // 16 for x in self.lens))
         n_used = sum((x + 15) // 16 for x in self.lens)
@@ -42,15 +43,15 @@ class TqCase:
             np_i = (L + 15) // 16
             self.pt[i, :np_i] = perm[c:c + np_i]
             c += np_i
-        self.k = [rng.standard_normal((L, hkv, D)).astype(np.float32) for L in self.lens]
+        self.k = [rng.standard_normal((L, hkv, d)).astype(np.float32) for L in self.lens]
         if key_scale is not None:
             self.k = [x * key_scale(rng, x.shape) for x in self.k]
             self.k = [x.astype(np.float32) for x in self.k]
-        self.v = [rng.standard_normal((L, hkv, D)).astype(np.float32) for L in self.lens]
-        self.R, self.G = _matrices(hkv)
+        self.v = [rng.standard_normal((L, hkv, d)).astype(np.float32) for L in self.lens]
+        self.R, self.G = _matrices(hkv, d)
 
     def build(self, dev, chunk=None):
-        self.pool = rt.TqPool(dev, self.n_pages, self.hkv)
+        self.pool = rt.TqPool(dev, self.n_pages, self.hkv, head_dim=self.d)
         self.pt_d = to_dev(self.pt)
         for i, L in enumerate(self.lens):
             step = chunk or max(L, 1)
@@ -64,7 +65,7 @@ class TqCase:
 
     def oracle_cache(self, i):
         L = self.lens[i]
-        packed = np.zeros((L, self.hkv, 64), np.uint8)
+        packed = np.zeros((L, self.hkv, self.d // 2), np.uint8)
         norms = np.zeros((L, self.hkv), np.float32)
         for t in range(L):
             packed[t], norms[t] = o.tq_cache_append_keys(self.k[i][t], self.R, self.G)
@@ -74,7 +75,7 @@ class TqCase:
         packed, norms, vals = self.oracle_cache(i)
         hq = q.shape[0]
         group = hq // self.hkv
-        out = np.zeros((hq, D), np.float32)
+        out = np.zeros((hq, self.d), np.float32)
         for h in range(hq):
             kvh = h % self.hkv if gqa_mode == 0 else h // group
             if self.lens[i]:
@@ -158,10 +159,47 @@ def test_decode_gate_empty_context_and_long_sequence():
 
 def test_bad_arguments_raise():
     dev = device()
-    with pytest.raises(rt.Unsupported):
-        rt.TqPool(dev, 4, 2, head_dim=64)
+    for d in (64, 192, 512):
+        with pytest.raises(rt.Unsupported):
+            rt.TqPool(dev, 4, 2, head_dim=d)
     pool = rt.TqPool(dev, 4, 2)
     q = torch.zeros((1, 3, D), dtype=torch.float32, device="cuda")
     with pytest.raises(rt.Unsupported):  # 3 q heads over 2 kv heads
         rt.tq_attn_decode(dev, q, pool, to_dev(np.zeros((1, 4), np.int32)),
                           to_dev(np.array([1], np.int32)))
+
+
+def test_append_records_bit_exact_d256():
+    """head_dim 256 (config 4's attention layers): 128-byte records, chunked appends,
+    magnitudes 1e-3 .. 1e3 and a zero key."""
+    dev = device()
+    rng = np.random.default_rng(0x70C4)
+
+    def scale(r, shape):
+        return 10.0 ** r.uniform(-3, 3, size=shape[:2] + (1,))
+    case = TqCase(rng, [1, 16, 37, 130], 2, key_scale=scale, d=256)
+    case.k[2][3, 0, :] = 0.0
+    case.build(dev, chunk=11)
+    for i in range(len(case.lens)):
+        _check_records(case, i)
+
+
+@pytest.mark.parametrize("gqa_mode", [0, 1])
+def test_decode_c4_shape_d256_gate(gqa_mode):
+    """Config-4 heads over a TurboQuant cache: 16 q / 2 kv heads, D 256, sigmoid gate, ragged
+    contexts up to 4097 (the score scale is 1/sqrt(256))."""
+    dev = device()
+    rng = np.random.default_rng(0x70C5 + gqa_mode)
+    lens = [4097, 1, 700, 64]
+    hq, hkv = 16, 2
+    case = TqCase(rng, lens, hkv, d=256)
+    case.build(dev)
+    q = rng.standard_normal((len(lens), hq, 256)).astype(np.float32) * 2
+    gate = rng.standard_normal((len(lens), hq, 256)).astype(np.float32)
+    out = rt.tq_attn_decode(dev, to_dev(q), case.pool, case.pt_d, to_dev(np.array(lens, np.int32)),
+                            gqa_mode=gqa_mode, gate=to_dev(gate)).cpu().numpy()
+    refs = parallel_map(lambda i: case.oracle_out(i, q[i], gqa_mode, gate[i]), range(len(lens)))
+    for i in range(len(lens)):
+        err = row_rel_err(out[i], refs[i])
+        print(f"\nD 256 seq {i} (L={lens[i]}): rel err {err:.3e}")
+        assert err <= 1e-2, f"seq {i} (L={lens[i]}): rel err {err}"

@@ -22,6 +22,56 @@ def test_splitmix64_published_vector():
                                         16408922859458223821]
 
 
+def _box_muller_f64(seed, n, trig=np.cos):
+    """The reference's Gaussian (src/turboquant/mod.rs:733-746) recomputed in float64 numpy
+    from SplitMix64 outputs (pinned above by the published vector): u = (x >> 11) / 2^53,
+    g = sqrt(-2 ln max(u1, 1e-10)) * cos(2 pi u2), rounded to f32."""
+    xs = np.array(o.splitmix64(seed, 2 * n), dtype=np.uint64)
+    u = (xs >> np.uint64(11)).astype(np.float64) / 2.0 ** 53
+    r = np.sqrt(-2.0 * np.log(np.maximum(u[0::2], 1e-10)))
+    return (r * trig(2.0 * np.pi * u[1::2])).astype(np.float32)
+
+
+def _ulps(a, b):
+    ia, ib = (np.asarray(x, np.float32).view(np.int32).astype(np.int64) for x in (a, b))
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("seed", [0xCAFEBABE, 0xCAFEBABE ^ 0xDEADBEEF, 1])
+def test_box_muller_gaussians_match_float64_restatement(seed):
+    """The oracle's f32 Gaussians equal an independent float64 evaluation of r cos(theta) to
+    1 f32 ulp (the two libm's may round the f64 log / cos differently in the last bit); a
+    sin-for-cos slip, the swapped uniforms or a dropped factor 2 in the radius does not."""
+    n = 4096
+    got = o.splitmix64_gaussians(seed, n)
+    assert _ulps(got, _box_muller_f64(seed, n)).max() <= 1
+    assert _ulps(got, _box_muller_f64(seed, n, np.sin)).max() > 1000
+    xs = np.array(o.splitmix64(seed, 2 * n), dtype=np.uint64)
+    u = (xs >> np.uint64(11)).astype(np.float64) / 2.0 ** 53
+    swapped = (np.sqrt(-2.0 * np.log(np.maximum(u[1::2], 1e-10))) *
+               np.cos(2.0 * np.pi * u[0::2])).astype(np.float32)
+    assert _ulps(got, swapped).max() > 1000
+    no_two = (np.sqrt(-np.log(np.maximum(u[0::2], 1e-10))) *
+              np.cos(2.0 * np.pi * u[1::2])).astype(np.float32)
+    assert _ulps(got, no_two).max() > 1000
+
+
+@pytest.mark.parametrize("dim", [128, 256])
+def test_product_matrices_from_float64_gaussians(dim):
+    """The product's host generator (pi_tq_generate): the QJL matrix is the Gaussians of
+    seed ^ 0xDEADBEEF row by row, and the rotation's first column is the first column of the
+    seed's Gaussian matrix, normalised (Gram-Schmidt's first step), both from the float64
+    restatement."""
+    from powerinfer_x64_amd import runtime as rt
+    seed = 0xCAFEBABE + 1
+    R, G = rt.tq_generate(dim, seed)
+    g = _box_muller_f64(seed ^ 0xDEADBEEF, dim * dim).reshape(dim, dim)
+    assert _ulps(G, g).max() <= 1
+    a = _box_muller_f64(seed, dim * dim).reshape(dim, dim).astype(np.float64)
+    col = a[:, 0] / np.linalg.norm(a[:, 0])
+    assert np.abs(R[:, 0] - col).max() < 1e-6
+
+
 def test_box_muller_gaussians_are_standard_normal():
     x = o.splitmix64_gaussians(0xCAFEBABE, 200000).astype(np.float64)
     assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01

@@ -13,7 +13,7 @@ from powerinfer_x64_amd import runtime as rt
 
 
 @pytest.mark.parametrize("dim,seed", [(128, 0xCAFEBABE), (128, 0xCAFEBABE + 7), (16, 123),
-                                      (64, 456)])
+                                      (64, 456), (256, 0xCAFEBABE + 1)])
 def test_generate_matches_oracle_bitwise(dim, seed):
     R, G = rt.tq_generate(dim, seed)
     R2, G2 = o.tq_matrices(dim, seed)
