@@ -278,6 +278,7 @@ void pi_destroy(pi_handle h) {
     if (h->ws_used) (void)hipEventSynchronize(h->ws_event);
     (void)hipFree(h->dws.partial_o);
     (void)hipFree(h->dws.partial_ml);
+    (void)hipFree(h->dws.seg_runs);
     (void)hipFree(h->gws.buf);
     (void)hipFree(h->h2d_scratch);
     (void)hipFree(h->tq_qv);
@@ -474,6 +475,14 @@ static int decode_check(pi_handle h, const char* fn, const pi::KvGeom& g, const 
         return fail(h, PI_ERR_UNSUPPORTED, "%s: batch %d > %d", fn, batch, pi::kMaxBatch);
     if ((long long)batch * g.n_kv_heads * ((max_pages + pi::kItemPages - 1) / pi::kItemPages) > (1LL << 30))
         return fail(h, PI_ERR_UNSUPPORTED, "%s: batch x kv heads x pages too large", fn);
+    // q rows are read and out rows written in 16-byte groups
+    if (((uintptr_t)d_q | (uintptr_t)d_out) & 15)
+        return fail(h, PI_ERR_INVALID_ARG, "%s: d_q and d_out must be 16-byte aligned", fn);
+    return PI_OK;
+}
+
+static int gate_check(pi_handle h, const char* fn, const float* d_gate) {
+    if ((uintptr_t)d_gate & 15) return fail(h, PI_ERR_INVALID_ARG, "%s: d_gate must be 16-byte aligned", fn);
     return PI_OK;
 }
 
@@ -505,6 +514,7 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
     const pi::KvGeom& g = pool->g;
     int rc = decode_check(h, "pi_attn_decode", g, d_q, d_page_table, d_ctx_len, d_out, max_pages,
                           batch, n_q_heads, gqa_mode);
+    if (!rc) rc = gate_check(h, "pi_attn_decode", d_gate);
     if (rc) return rc;
     if (batch == 0) return PI_OK;
     hipStream_t s = pick(h, stream);
@@ -515,6 +525,8 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
     const size_t need_ml = need_o / g.head_dim * 2;
     if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_attn_decode workspace", false))) return rc;
     if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_attn_decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->dws.seg_runs, &h->dws.capacity_runs, pi::decode_ws_ints_runs(g, plan), s,
+                   "pi_attn_decode workspace", false))) return rc;
     const pi::DecodeParams p = decode_params(d_q, d_page_table, max_pages, d_ctx_len, batch, n_q_heads,
                                              gqa_mode, scale, d_gate, d_out, plan);
     PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), "pi_attn_decode");
@@ -531,25 +543,31 @@ int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
     const pi::KvGeom& g = pool->g;
     int rc = decode_check(h, "pi_attn_decode_noalloc", g, d_q, d_page_table, d_ctx_len, d_out,
                           max_pages, batch, n_q_heads, gqa_mode);
+    if (!rc) rc = gate_check(h, "pi_attn_decode_noalloc", d_gate);
     if (rc) return rc;
     if (batch == 0) return PI_OK;
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode_noalloc");
     const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
-    // partial o, then (m, l) at the next 256-byte boundary, all inside the scratch
+    // partial o, then (m, l), then the segments' run table, each at a 256-byte boundary
+    // inside the scratch
     const size_t need_o = pi::decode_ws_floats_o(g, plan);
     const size_t off_ml = (need_o + 63) / 64 * 64;
     const size_t need_ml = need_o / g.head_dim * 2;
-    if (off_ml + need_ml > pi::kDecodeScratchFloats)
+    const size_t off_runs = (off_ml + need_ml + 63) / 64 * 64;
+    const size_t need_runs = pi::decode_ws_ints_runs(g, plan);
+    if (off_runs + need_runs > pi::kDecodeScratchFloats)
         return fail(h, PI_ERR_UNSUPPORTED,
                     "pi_attn_decode_noalloc: %zu scratch floats needed (batch %d x %d kv heads + %d "
                     "workgroups, %d q heads per kv head, head_dim %d) > the fixed %zu",
-                    off_ml + need_ml, batch, g.n_kv_heads, plan.grid, plan.group, g.head_dim,
+                    off_runs + need_runs, batch, g.n_kv_heads, plan.grid, plan.group, g.head_dim,
                     pi::kDecodeScratchFloats);
     pi::DecodeWorkspace ws;
     ws.partial_o = h->scratch;
     ws.partial_ml = h->scratch + off_ml;
+    ws.seg_runs = reinterpret_cast<int32_t*>(h->scratch + off_runs);
     ws.capacity_o = need_o;
     ws.capacity_ml = need_ml;
+    ws.capacity_runs = need_runs;
     const pi::DecodeParams p = decode_params(d_q, d_page_table, max_pages, d_ctx_len, batch, n_q_heads,
                                              gqa_mode, scale, d_gate, d_out, plan);
     PI_HIP(h, pi::launch_decode(g, p, ws, plan, pick(h, stream)), "pi_attn_decode_noalloc");
@@ -1358,6 +1376,7 @@ int pi_tq_attn_decode(pi_handle h, const float* d_q, pi_tq_pool pool, const int3
     const pi::KvGeom& g = pool->t.g;
     int rc = decode_check(h, "pi_tq_attn_decode", g, d_q, d_page_table, d_ctx_len, d_out, max_pages,
                           batch, n_q_heads, gqa_mode);
+    if (!rc) rc = gate_check(h, "pi_tq_attn_decode", d_gate);
     if (rc) return rc;
     if (batch == 0) return PI_OK;
     hipStream_t s = pick(h, stream);
@@ -1369,6 +1388,8 @@ int pi_tq_attn_decode(pi_handle h, const float* d_q, pi_tq_pool pool, const int3
     const size_t need_qv = (size_t)batch * n_q_heads * 2 * g.head_dim;
     if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_tq_attn_decode workspace", false))) return rc;
     if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_tq_attn_decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->dws.seg_runs, &h->dws.capacity_runs, pi::decode_ws_ints_runs(g, plan), s,
+                   "pi_tq_attn_decode workspace", false))) return rc;
     if ((rc = grow(h, &h->tq_qv, &h->tq_qv_floats, need_qv, s, "pi_tq_attn_decode workspace", false))) return rc;
     PI_HIP(h, pi::launch_tq_query(pool->t, d_q, h->tq_qv, batch, n_q_heads, gqa_mode, s),
            "pi_tq_attn_decode");

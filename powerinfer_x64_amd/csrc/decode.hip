@@ -441,6 +441,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
         const int kvh = run.kvh, seg0 = run.seg0, run_end = run.run_end, L = run.len;
         const int pg0 = run.pg0, pg1 = run.pg1;
         const bool whole = run.whole;
+        if (cur == seg0 && tid == 0) {  // the segment's run table, for the merge kernel
+            int wg1;
+            const int n_runs = sched::merge_runs(s_cum, n_kv, chunk, b, kvh, &wg1);
+            const size_t seg = (size_t)b * n_kv + kvh;
+            ws.seg_runs[2 * seg] = wg1;
+            ws.seg_runs[2 * seg + 1] = n_runs;
+        }
 
         const int head = head_of(kvh, col_on ? col : 0, n_kv, group, p.gqa_mode);
         typename T::Q q;
@@ -546,42 +553,40 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
 }
 
 // Combines the run partials of every (sequence, KV head) segment that spans
-// more than one workgroup range; zero-length sequences get zeros.  Runs of a
-// segment [I, I+n) start at I and at every multiple of `chunk` inside it.
-// Grid (ceil(G*D / 256), n_kv, batch): one thread per output element.
+// more than one workgroup range; zero-length sequences get zeros.  The
+// segment's run table (workgroup of run 1, number of runs) was written by
+// the decode workgroup that started it.  Grid (ceil(G*D / 256), n_kv, batch):
+// a workgroup owns 256 output values of one segment (64 16-byte groups); its
+// 4 wavefronts first form the run weights of the block's columns, then sum
+// every 4th run each and meet in LDS.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, DecodeWorkspace ws,
-                                                           int n_kv, int D, int group,
-                                                           int n_wg) {
-    __shared__ int s_cum[kMaxBatch + 1];
-    __shared__ int s_red[4];
-    __shared__ float s_w[4][kMaxRuns];  // per column (<= 4 per 256 elements) and run
+                                                           int n_kv, int D, int group) {
+    __shared__ float s_w[4][kMaxRuns];  // per column (<= 4 per 256 values) and run
     __shared__ int s_slot[kMaxRuns];
     __shared__ float s_inv[4];
+    __shared__ __attribute__((aligned(16))) f32x4 s_acc[4][64];
     const int kvh = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x;
-    const int per_kv = scan_items(p, s_cum, s_red);
-    const int chunk = (n_kv * per_kv + n_wg - 1) / n_wg;
-    const int nb = s_cum[b + 1] - s_cum[b];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int GD = group * D;
     const int e0 = blockIdx.x * 256;
-    const int idx = e0 + tid;
-    if (nb == 0) {  // empty context: softmax over nothing leaves zeros (src/ops.rs:161)
+    const size_t seg = (size_t)b * n_kv + kvh;
+    if (sched::seq_tokens(p.ctx_len[b], p.max_pages) == 0) {
+        // empty context: softmax over nothing leaves zeros (src/ops.rs:161)
+        const int idx = e0 + tid;
         if (idx < GD) {
             const int c = idx / D, d = idx - c * D;
             p.out[((size_t)b * p.n_q_heads + head_of(kvh, c, n_kv, group, p.gqa_mode)) * D + d] = 0.f;
         }
         return;
     }
-    int wg1;
-    const int n_runs = sched::merge_runs(s_cum, n_kv, chunk, b, kvh, &wg1);
-    if (n_runs == 1) return;  // one run: written directly by decode_kernel
-    for (int r = tid; r < n_runs && r < kMaxRuns; r += 256)
+    const int wg1 = ws.seg_runs[2 * seg], n_runs = ws.seg_runs[2 * seg + 1];
+    if (n_runs <= 1) return;  // one run: written directly by decode_kernel
+    for (int r = tid; r < n_runs; r += 256)
         s_slot[r] = (int)sched::run_slot(r == 0, b, kvh, n_kv, p.batch, wg1 + r - 1);
     __syncthreads();
     const int c_lo = e0 / D, c_hi = min(group - 1, (e0 + 255) / D);
-    const int lane = tid & 63, wave = tid >> 6;
     const float* pml = ws.partial_ml;
-    if (wave <= c_hi - c_lo) {  // one wavefront per column
+    if (wave <= c_hi - c_lo) {  // one wavefront per column of this block
         const int c = c_lo + wave;
         float M = -1e30f;
         for (int r = lane; r < n_runs; r += 64) M = fmaxf(M, pml[((size_t)s_slot[r] * group + c) * 2]);
@@ -599,26 +604,42 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
         if (lane == 0) s_inv[wave] = lsum > 0.f ? 1.0f / lsum : 0.f;
     }
     __syncthreads();
-    if (idx >= GD) return;
-    const int c = idx / D, d = idx - c * D;
-    const float* w = s_w[c - c_lo];
-    float o0 = 0.f, o1 = 0.f;
-    int r = 0;
-    for (; r + 2 <= n_runs; r += 2) {
-        o0 += w[r] * ws.partial_o[(size_t)s_slot[r] * GD + idx];
-        o1 += w[r + 1] * ws.partial_o[(size_t)s_slot[r + 1] * GD + idx];
+    // thread (wave, lane): values e0 + 4 lane .. +3, runs wave, wave + 4, ...
+    const int e = e0 + 4 * lane;
+    const bool on = e < GD;  // GD is a multiple of 4 (D >= 64)
+    const int cw = (on ? e / D : c_lo) - c_lo;
+    const float* w = s_w[cw];
+    const float* po = ws.partial_o + (on ? e : 0);
+    auto part = [&](int r) { return *reinterpret_cast<const f32x4*>(po + (size_t)s_slot[r] * GD); };
+    f32x4 a[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int r = wave;
+    for (; r + 12 < n_runs; r += 16) {  // four independent loads in flight
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] += w[r + 4 * j] * part(r + 4 * j);
     }
-    if (r < n_runs) o0 += w[r] * ws.partial_o[(size_t)s_slot[r] * GD + idx];
+    for (; r < n_runs; r += 4) a[0] += w[r] * part(r);
+    s_acc[wave][lane] = (a[0] + a[1]) + (a[2] + a[3]);
+    __syncthreads();
+    if (wave != 0 || !on) return;
+    const f32x4 acc = (s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]);
+    const float inv = s_inv[cw];
+    const int c = e / D, d = e - c * D;
     const int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
     const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
-    float res = (o0 + o1) * s_inv[c - c_lo];
-    if (p.gate) res *= sigmoidf_(p.gate[oi]);
-    p.out[oi] = res;
+    f32x4 res = acc * inv;
+    if (p.gate) {
+        const f32x4 gt = *reinterpret_cast<const f32x4*>(p.gate + oi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) res[i] *= sigmoidf_(gt[i]);
+    }
+    *reinterpret_cast<f32x4*>(p.out + oi) = res;
 }
 
 template <typename KT, int D>
 constexpr int np_of() {
-    return std::is_same<KT, TqKey>::value ? 1 : (sizeof(KT) == 2 && D <= 128) ? 2 : 1;
+    return std::is_same<KT, TqKey>::value ? 1 : sizeof(KT) == 2 ? 2 : 1;
 }
 
 template <typename KT, int D>
@@ -643,7 +664,7 @@ hipError_t launch_t(const KvGeom& g, const DecodeParams& p, const DecodeWorkspac
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(decode_merge_kernel, dim3((group * D + 255) / 256, g.n_kv_heads, p.batch),
-                       dim3(256), 0, s, p, ws, g.n_kv_heads, D, group, plan.grid);
+                       dim3(256), 0, s, p, ws, g.n_kv_heads, D, group);
     return hipGetLastError();
 }
 
@@ -680,6 +701,7 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
     plan.item_pages = ip;
     // one partial slot per segment and one per workgroup (run_slot)
     plan.n_slots = (long long)batch * g.n_kv_heads + plan.grid;
+    plan.batch = batch;
     plan.group = n_q_heads / g.n_kv_heads;
     return plan;
 }
@@ -707,6 +729,10 @@ hipError_t decode_scratch(int device, float** ptr) {
 
 size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan) {
     return (size_t)plan.n_slots * plan.group * g.head_dim;
+}
+
+size_t decode_ws_ints_runs(const KvGeom& g, const DecodePlan& plan) {
+    return (size_t)2 * plan.batch * g.n_kv_heads;
 }
 
 hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,

@@ -46,8 +46,11 @@ struct TqPool {
 struct DecodeWorkspace {
     float* partial_o;     // [slot][G][D]: slot = segment (b * Hkv + kvh) or batch * Hkv + workgroup
     float* partial_ml;    // [slot][G][2]  (running max, sum) in log2 units
+    int32_t* seg_runs;    // [segment][2]: (workgroup of run 1, number of runs), set by the
+                          // workgroup that starts the segment
     size_t capacity_o;    // floats
     size_t capacity_ml;   // floats
+    size_t capacity_runs; // int32 entries
 };
 
 struct DecodeParams {
@@ -66,6 +69,7 @@ struct DecodeParams {
 
 struct DecodePlan {
     int32_t grid;        // persistent workgroups (CUs x resident workgroups per CU)
+    int32_t batch;
     long long n_slots;   // partial slots: batch * n_kv_heads + grid
     int32_t group;       // q heads per kv head
     int32_t item_pages;  // pages per work item
@@ -80,6 +84,8 @@ hipError_t decode_scratch(int device, float** ptr);
 DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
                        int device);
 size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan);
+// int32 entries of the per-segment run table (2 per (sequence, KV head)).
+size_t decode_ws_ints_runs(const KvGeom& g, const DecodePlan& plan);
 hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,
                          const DecodePlan& plan, hipStream_t s);
 

@@ -57,6 +57,8 @@ bool walk(const Case& c) {
     std::vector<int> page_seen((size_t)batch * n_kv * mp, 0);
     std::map<long long, std::pair<int, int>> slot_owner;  // slot -> (b, kvh)
     std::vector<char> whole((size_t)batch * n_kv, 0);
+    // run table (workgroup of run 1, number of runs) written by the segment's first run
+    std::vector<std::pair<int, int>> table((size_t)batch * n_kv, {-1, -1});
     for (int w = 0; w < c.grid && n_items > 0; ++w) {
         int cur = w * chunk;
         const int end = imin(n_items, cur + chunk);
@@ -71,6 +73,13 @@ bool walk(const Case& c) {
             CHECK(r.len >= 0 && r.len <= kPage * mp, "%s: len=%d", c.name, r.len);
             CHECK(r.pg0 >= 0 && r.pg0 <= r.pg1 && r.pg1 <= mp, "%s: pages [%d, %d) of %d", c.name, r.pg0, r.pg1, mp);
             for (int i = cur; i < r.run_end; ++i) item_seen[i]++;
+            if (cur == r.seg0) {
+                auto& t = table[(size_t)r.b * n_kv + r.kvh];
+                CHECK(t.second == -1, "%s: run table of (b %d, kvh %d) written twice", c.name, r.b, r.kvh);
+                int wg1;
+                const int n_runs = merge_runs(s_cum.data(), n_kv, chunk, r.b, r.kvh, &wg1);
+                t = {wg1, n_runs};
+            }
             for (int sub = r.pg0; sub < r.pg1; sub += kSubPages) {
                 for (int wave = 0; wave < kWaves; ++wave) {
                     int first, n_my;
@@ -114,8 +123,9 @@ bool walk(const Case& c) {
     for (int b = 0; b < batch && n_items > 0; ++b) {
         if (s_cum[b + 1] == s_cum[b]) continue;
         for (int kvh = 0; kvh < n_kv; ++kvh) {
-            int wg1;
-            const int n_runs = merge_runs(s_cum.data(), n_kv, chunk, b, kvh, &wg1);
+            const auto t = table[(size_t)b * n_kv + kvh];
+            CHECK(t.second != -1, "%s: run table of (b %d, kvh %d) never written", c.name, b, kvh);
+            const int wg1 = t.first, n_runs = t.second;
             CHECK(n_runs >= 1 && n_runs <= c.grid + 1 && n_runs <= 1024, "%s: %d runs", c.name, n_runs);
             if (n_runs == 1) {
                 CHECK(whole[(size_t)b * n_kv + kvh], "%s: (b %d, kvh %d) one run but not whole", c.name, b, kvh);
