@@ -130,7 +130,10 @@ int pi_attn_prologue(pi_handle h, float* d_q, float* d_k, const float* d_v,
  * (normed, rotated); out [batch][n_q_heads][D] f32.  scale multiplies q.k
  * (1/sqrt(D) in the reference).  d_gate (nullable) [batch][n_q_heads][D]:
  * out *= sigmoid(gate) (src/model/mod.rs:1192-1196).  Split-K flash decoding,
- * one launch; n_q_heads/n_kv_heads <= 16.  Device tables are read, not
+ * one launch.  Any head counts with the modulo map (a KV head's query heads
+ * ride in the MFMA columns, up to 16 per pass); the grouped map needs n_q_heads
+ * a multiple of n_kv_heads.  d_q, d_out and d_gate are 16-byte aligned (the
+ * kernels move them in 16-byte groups).  Device tables are read, not
  * trusted: d_ctx_len[b] is clamped to [0, 16 * max_pages], and a page id
  * outside [0, n_pages) holds no tokens (its keys are masked; a sequence with
  * no unmasked key gets zeros, as an empty context does). */
@@ -160,7 +163,8 @@ int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
  * reference's per-token loop computes (src/model/mod.rs:668,1140-1190).
  * d_q [batch][seq_len][n_q_heads][D], d_k/d_v [batch][seq_len][n_kv_heads][D]
  * in dtype (PI_BF16 or PI_F16); d_out [batch][seq_len][n_q_heads][D] f32.
- * MFMA flash attention with fp32 softmax/accumulation; D = 128 or 256. */
+ * MFMA flash attention with fp32 softmax/accumulation; D = 128 or 256.  Head
+ * counts as pi_attn_decode. */
 int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d_v, int32_t dtype,
                     int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
                     int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale, float* d_out,

@@ -466,15 +466,15 @@ static int decode_check(pi_handle h, const char* fn, const pi::KvGeom& g, const 
         return fail(h, PI_ERR_INVALID_ARG, "%s: batch=%d max_pages=%d n_q_heads=%d", fn, batch, max_pages, n_q_heads);
     if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
         return fail(h, PI_ERR_INVALID_ARG, "%s: gqa_mode %d", fn, gqa_mode);
-    if (n_q_heads % g.n_kv_heads != 0)
-        return fail(h, PI_ERR_UNSUPPORTED, "%s: n_q_heads %d not a multiple of n_kv_heads %d", fn, n_q_heads, g.n_kv_heads);
-    const int group = n_q_heads / g.n_kv_heads;
-    if (group > 16 || group * g.head_dim > 2048)
-        return fail(h, PI_ERR_UNSUPPORTED, "%s: %d q heads per kv head at head_dim %d", fn, group, g.head_dim);
+    // the modulo map (src/model/mod.rs:1155) takes any head counts; the grouped one needs a multiple
+    if (gqa_mode == PI_GQA_GROUPED && n_q_heads % g.n_kv_heads != 0)
+        return fail(h, PI_ERR_INVALID_ARG, "%s: grouped head map with n_q_heads %d not a multiple of n_kv_heads %d",
+                    fn, n_q_heads, g.n_kv_heads);
     if (batch > pi::kMaxBatch)
         return fail(h, PI_ERR_UNSUPPORTED, "%s: batch %d > %d", fn, batch, pi::kMaxBatch);
-    if ((long long)batch * g.n_kv_heads * ((max_pages + pi::kItemPages - 1) / pi::kItemPages) > (1LL << 30))
-        return fail(h, PI_ERR_UNSUPPORTED, "%s: batch x kv heads x pages too large", fn);
+    const long long blocks = ((long long)n_q_heads + g.n_kv_heads - 1) / g.n_kv_heads;  // >= column blocks
+    if ((long long)batch * g.n_kv_heads * blocks * ((max_pages + pi::kItemPages - 1) / pi::kItemPages) > (1LL << 30))
+        return fail(h, PI_ERR_UNSUPPORTED, "%s: batch x heads x pages too large", fn);
     // q rows are read and out rows written in 16-byte groups
     if (((uintptr_t)d_q | (uintptr_t)d_out) & 15)
         return fail(h, PI_ERR_INVALID_ARG, "%s: d_q and d_out must be 16-byte aligned", fn);
@@ -502,6 +502,9 @@ static pi::DecodeParams decode_params(const float* d_q, const int32_t* d_page_ta
     p.gqa_mode = gqa_mode;
     p.scale = scale;
     p.item_pages = plan.item_pages;
+    p.group = plan.group;
+    p.cols = plan.cols;
+    p.n_cb = plan.n_cb;
     return p;
 }
 
@@ -520,7 +523,7 @@ int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode");
     if ((rc = ws_begin(h, s, "pi_attn_decode"))) return rc;
-    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
+    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, gqa_mode, h->device);
     const size_t need_o = pi::decode_ws_floats_o(g, plan);
     const size_t need_ml = need_o / g.head_dim * 2;
     if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_attn_decode workspace", false))) return rc;
@@ -547,7 +550,7 @@ int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
     if (rc) return rc;
     if (batch == 0) return PI_OK;
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode_noalloc");
-    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
+    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, gqa_mode, h->device);
     // partial o, then (m, l), then the segments' run table, each at a 256-byte boundary
     // inside the scratch
     const size_t need_o = pi::decode_ws_floats_o(g, plan);
@@ -588,8 +591,9 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
         return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: dtype %d (bf16 or f16)", dtype);
     if (head_dim != 128 && head_dim != 256)
         return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: head_dim %d (128 or 256)", head_dim);
-    if (n_q_heads % n_kv_heads != 0)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: n_q_heads %d not a multiple of n_kv_heads %d", n_q_heads, n_kv_heads);
+    if (gqa_mode == PI_GQA_GROUPED && n_q_heads % n_kv_heads != 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill: grouped head map with n_q_heads %d not a multiple of n_kv_heads %d",
+                    n_q_heads, n_kv_heads);
     if (batch == 0 || seq_len == 0) return PI_OK;
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_prefill");
     PI_HIP(h, pi::launch_prefill(d_q, d_k, d_v, dtype, batch, seq_len, seq_len, 0, n_q_heads,
@@ -615,8 +619,8 @@ int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
     if (g.dtype != PI_F16 || (g.head_dim != 128 && g.head_dim != 256))
         return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill_paged: f16 pool with head_dim 128 or 256 (dtype %d, head_dim %d)",
                     g.dtype, g.head_dim);
-    if (n_q_heads % g.n_kv_heads != 0)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill_paged: n_q_heads %d not a multiple of n_kv_heads %d",
+    if (gqa_mode == PI_GQA_GROUPED && n_q_heads % g.n_kv_heads != 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: grouped head map with n_q_heads %d not a multiple of n_kv_heads %d",
                     n_q_heads, g.n_kv_heads);
     const long long n_keys = (long long)start_pos + n_tok;
     if (n_keys > (long long)max_pages * pi::kPageTokens)
@@ -949,11 +953,14 @@ int pi_attn_layer_create(pi_handle h, int32_t max_tokens, int32_t n_heads, int32
     PI_CHECK_HANDLE(h);
     if (!out) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: out is null");
     *out = nullptr;
-    if (max_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0)
+    if (max_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: max_tokens=%d n_heads=%d n_kv_heads=%d",
                     max_tokens, n_heads, n_kv_heads);
     if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: gqa_mode %d", gqa_mode);
+    if (gqa_mode == PI_GQA_GROUPED && n_heads % n_kv_heads != 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: grouped head map with n_heads %d not a multiple of n_kv_heads %d",
+                    n_heads, n_kv_heads);
     pi_attn_layer L = new (std::nothrow) pi_attn_layer_s();
     if (!L) return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_attn_layer_create: host allocation");
     L->owner = h;
@@ -1382,7 +1389,7 @@ int pi_tq_attn_decode(pi_handle h, const float* d_q, pi_tq_pool pool, const int3
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_tq_attn_decode");
     if ((rc = ws_begin(h, s, "pi_tq_attn_decode"))) return rc;
-    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, h->device);
+    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, gqa_mode, h->device);
     const size_t need_o = pi::decode_ws_floats_o(g, plan);
     const size_t need_ml = need_o / g.head_dim * 2;
     const size_t need_qv = (size_t)batch * n_q_heads * 2 * g.head_dim;

@@ -317,6 +317,15 @@ __device__ __forceinline__ int head_of(int kvh, int col, int n_kv, int group, in
     return mode == 0 ? kvh + col * n_kv : kvh * group + col;
 }
 
+// Query head of column c of segment `sidx` (KV head sidx / n_cb, column block
+// sidx % n_cb), or -1 when the column holds no head.
+__device__ __forceinline__ int seg_head(const DecodeParams& p, int sidx, int c, int n_kv) {
+    const int kvh = sidx / p.n_cb, cg = (sidx % p.n_cb) * p.cols + c;
+    if (c >= p.cols || cg >= p.group) return -1;
+    const int h = head_of(kvh, cg, n_kv, p.group, p.gqa_mode);
+    return h < p.n_q_heads ? h : -1;
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // Softmax/PV state of one wavefront: O^T accumulators (lane = head column
@@ -407,7 +416,7 @@ __device__ __forceinline__ int scan_items(const DecodeParams& p, int* s_cum, int
 // otherwise it writes a partial into the slot of its first item.
 template <typename KT, int D, int NP>
 __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams p,
-                                                          DecodeWorkspace ws, int group) {
+                                                          DecodeWorkspace ws) {
     using T = Tile<KT, D>;
     __shared__ int s_cum[kMaxBatch + 1];
     __shared__ int s_red[4];
@@ -416,10 +425,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
     __shared__ __attribute__((aligned(16))) float s_o[kWaves][kMaxGD];
 
     const int n_kv = g.n_kv_heads;
+    const int n_seg = n_kv * p.n_cb;  // segments per sequence: (KV head, column block)
     const int tid = threadIdx.x;
     T::prepare();  // tile tables in LDS; the scan below has barriers
     const int per_kv = scan_items(p, s_cum, s_red);
-    const int n_items = n_kv * per_kv;
+    const int n_items = n_seg * per_kv;
     const int chunk = (n_items + gridDim.x - 1) / gridDim.x;
     int cur = blockIdx.x * chunk;
     const int end = min(n_items, cur + chunk);
@@ -428,30 +438,31 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
-    const bool col_on = col < group;
-    const int GD = group * D;
+    const int GD = p.cols * D;
     const char* kpool = reinterpret_cast<const char*>(g.k);
     const char* vpool = reinterpret_cast<const char*>(g.v);
 
-    int b = sched::find_seq(s_cum, p.batch, n_kv, cur);
+    int b = sched::find_seq(s_cum, p.batch, n_seg, cur);
     while (cur < end) {
-        const sched::Run run = sched::run_at(s_cum, p.ctx_len, p.max_pages, n_kv, p.item_pages, b,
+        const sched::Run run = sched::run_at(s_cum, p.ctx_len, p.max_pages, n_seg, p.item_pages, b,
                                              cur, end);
         b = run.b;
-        const int kvh = run.kvh, seg0 = run.seg0, run_end = run.run_end, L = run.len;
+        const int sidx = run.kvh, kvh = sidx / p.n_cb;  // segment within the sequence, its KV head
+        const int seg0 = run.seg0, run_end = run.run_end, L = run.len;
         const int pg0 = run.pg0, pg1 = run.pg1;
         const bool whole = run.whole;
         if (cur == seg0 && tid == 0) {  // the segment's run table, for the merge kernel
             int wg1;
-            const int n_runs = sched::merge_runs(s_cum, n_kv, chunk, b, kvh, &wg1);
-            const size_t seg = (size_t)b * n_kv + kvh;
+            const int n_runs = sched::merge_runs(s_cum, n_seg, chunk, b, sidx, &wg1);
+            const size_t seg = (size_t)b * n_seg + sidx;
             ws.seg_runs[2 * seg] = wg1;
             ws.seg_runs[2 * seg + 1] = n_runs;
         }
 
-        const int head = head_of(kvh, col_on ? col : 0, n_kv, group, p.gqa_mode);
+        const int head = seg_head(p, sidx, col, n_kv);
+        const bool col_on = head >= 0;
         typename T::Q q;
-        T::load_q(q, p.q + ((size_t)b * p.n_q_heads + head) * T::QD,
+        T::load_q(q, p.q + ((size_t)b * p.n_q_heads + (col_on ? head : 0)) * T::QD,
                   col_on ? p.scale * kLog2e : 0.f, grp);
         Acc<D> acc;
 #pragma unroll
@@ -508,7 +519,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
         acc.l = wave_sum_xor(acc.l, 32);
 
         // ---- merge the 4 wavefronts in LDS ----
-        if (col_on) {
+        // (a column with no head ran a zero query: finite values, never written out)
+        if (col < p.cols) {
 #pragma unroll
             for (int t = 0; t < D / 16; ++t)
                 *reinterpret_cast<f32x4*>(&s_o[wave][col * D + 16 * t + 4 * grp]) = acc.o[t];
@@ -518,9 +530,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
             }
         }
         __syncthreads();
-        const size_t slot = (size_t)sched::run_slot(cur == seg0, b, kvh, n_kv, p.batch, blockIdx.x);
+        const size_t slot = (size_t)sched::run_slot(cur == seg0, b, sidx, n_seg, p.batch, blockIdx.x);
         float* po = ws.partial_o + slot * GD;
-        float* pml = ws.partial_ml + slot * group * 2;
+        float* pml = ws.partial_ml + slot * p.cols * 2;
         for (int idx = tid; idx < GD; idx += kThreads) {
             const int c = idx / D, d = idx - c * D;
             float M = s_m[0][c];
@@ -534,7 +546,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
                 lsum += f * s_l[w][c];
             }
             if (whole) {
-                const int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
+                const int h = seg_head(p, sidx, c, n_kv);
+                if (h < 0) continue;
                 const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
                 float r = lsum > 0.f ? o / lsum : 0.f;  // every key masked: zeros
                 if (p.gate) r *= sigmoidf_(p.gate[oi]);
@@ -552,49 +565,51 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
     }
 }
 
-// Combines the run partials of every (sequence, KV head) segment that spans
-// more than one workgroup range; zero-length sequences get zeros.  The
-// segment's run table (workgroup of run 1, number of runs) was written by
-// the decode workgroup that started it.  Grid (ceil(G*D / 256), n_kv, batch):
+// Combines the run partials of every (sequence, KV head, column block) segment
+// that spans more than one workgroup range; zero-length sequences get zeros.
+// The segment's run table (workgroup of run 1, number of runs) was written by
+// the decode workgroup that started it.  Grid (ceil(cols*D / 256), segments
+// per sequence, batch):
 // a workgroup owns 256 output values of one segment (64 16-byte groups); its
 // 4 wavefronts first form the run weights of the block's columns, then sum
 // every 4th run each and meet in LDS.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, DecodeWorkspace ws,
-                                                           int n_kv, int D, int group) {
+                                                           int n_kv, int D) {
     __shared__ float s_w[4][kMaxRuns];  // per column (<= 4 per 256 values) and run
     __shared__ int s_slot[kMaxRuns];
     __shared__ float s_inv[4];
     __shared__ __attribute__((aligned(16))) f32x4 s_acc[4][64];
-    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int sidx = blockIdx.y, b = blockIdx.z, n_seg = gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int GD = group * D;
+    const int cols = p.cols, GD = cols * D;
     const int e0 = blockIdx.x * 256;
-    const size_t seg = (size_t)b * n_kv + kvh;
+    const size_t seg = (size_t)b * n_seg + sidx;
     if (sched::seq_tokens(p.ctx_len[b], p.max_pages) == 0) {
         // empty context: softmax over nothing leaves zeros (src/ops.rs:161)
         const int idx = e0 + tid;
         if (idx < GD) {
             const int c = idx / D, d = idx - c * D;
-            p.out[((size_t)b * p.n_q_heads + head_of(kvh, c, n_kv, group, p.gqa_mode)) * D + d] = 0.f;
+            const int h = seg_head(p, sidx, c, n_kv);
+            if (h >= 0) p.out[((size_t)b * p.n_q_heads + h) * D + d] = 0.f;
         }
         return;
     }
     const int wg1 = ws.seg_runs[2 * seg], n_runs = ws.seg_runs[2 * seg + 1];
     if (n_runs <= 1) return;  // one run: written directly by decode_kernel
     for (int r = tid; r < n_runs; r += 256)
-        s_slot[r] = (int)sched::run_slot(r == 0, b, kvh, n_kv, p.batch, wg1 + r - 1);
+        s_slot[r] = (int)sched::run_slot(r == 0, b, sidx, n_seg, p.batch, wg1 + r - 1);
     __syncthreads();
-    const int c_lo = e0 / D, c_hi = min(group - 1, (e0 + 255) / D);
+    const int c_lo = e0 / D, c_hi = min(cols - 1, (e0 + 255) / D);
     const float* pml = ws.partial_ml;
     if (wave <= c_hi - c_lo) {  // one wavefront per column of this block
         const int c = c_lo + wave;
         float M = -1e30f;
-        for (int r = lane; r < n_runs; r += 64) M = fmaxf(M, pml[((size_t)s_slot[r] * group + c) * 2]);
+        for (int r = lane; r < n_runs; r += 64) M = fmaxf(M, pml[((size_t)s_slot[r] * cols + c) * 2]);
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) M = wave_max_xor(M, m);
         float lsum = 0.f;
         for (int r = lane; r < n_runs; r += 64) {
-            const size_t mi = ((size_t)s_slot[r] * group + c) * 2;
+            const size_t mi = ((size_t)s_slot[r] * cols + c) * 2;
             const float w = fast_exp2(pml[mi] - M);
             s_w[wave][r] = w;
             lsum += w * pml[mi + 1];
@@ -626,7 +641,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     const f32x4 acc = (s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]);
     const float inv = s_inv[cw];
     const int c = e / D, d = e - c * D;
-    const int h = head_of(kvh, c, n_kv, group, p.gqa_mode);
+    const int h = seg_head(p, sidx, c, n_kv);
+    if (h < 0) return;
     const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
     f32x4 res = acc * inv;
     if (p.gate) {
@@ -658,21 +674,27 @@ int wgs_per_cu() {
 template <typename KT, int D>
 hipError_t launch_t(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,
                     const DecodePlan& plan, hipStream_t s) {
-    const int group = p.n_q_heads / g.n_kv_heads;
     hipLaunchKernelGGL((decode_kernel<KT, D, np_of<KT, D>()>), dim3(plan.grid), dim3(kThreads), 0,
-                       s, g, p, ws, group);
+                       s, g, p, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3((group * D + 255) / 256, g.n_kv_heads, p.batch),
-                       dim3(256), 0, s, p, ws, g.n_kv_heads, D, group);
+    hipLaunchKernelGGL(decode_merge_kernel, dim3((p.cols * D + 255) / 256, g.n_kv_heads * p.n_cb, p.batch),
+                       dim3(256), 0, s, p, ws, g.n_kv_heads, D);
     return hipGetLastError();
 }
 
 }  // namespace
 
 DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
-                       int device) {
+                       int32_t gqa_mode, int device) {
     DecodePlan plan;
+    // head blocking: the modulo map (h % Hkv) gives KV head k the heads k, k + Hkv, ... below
+    // Hq, at most ceil(Hq / Hkv); a segment takes up to 16 of them and cols * D <= 2048 floats
+    plan.group = gqa_mode == 0 ? (n_q_heads + g.n_kv_heads - 1) / g.n_kv_heads : n_q_heads / g.n_kv_heads;
+    const int max_cols = std::min(16, kMaxGD / g.head_dim);
+    plan.n_cb = (plan.group + max_cols - 1) / max_cols;
+    plan.cols = (plan.group + plan.n_cb - 1) / plan.n_cb;  // even blocks
+    const int n_seg = g.n_kv_heads * plan.n_cb;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
         cus <= 0)
@@ -695,14 +717,13 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
     // Item size: kItemPages pages, halved while the launch's upper bound of
     // items would not give every workgroup two items (small batches and short
     // contexts then still spread over the whole chip).
-    const long long max_seg_pages = (long long)batch * g.n_kv_heads * max_pages;
+    const long long max_seg_pages = (long long)batch * n_seg * max_pages;
     int ip = kItemPages;
     while (ip > 1 && max_seg_pages / ip < 2LL * plan.grid) ip >>= 1;
     plan.item_pages = ip;
     // one partial slot per segment and one per workgroup (run_slot)
-    plan.n_slots = (long long)batch * g.n_kv_heads + plan.grid;
+    plan.n_slots = (long long)batch * n_seg + plan.grid;
     plan.batch = batch;
-    plan.group = n_q_heads / g.n_kv_heads;
     return plan;
 }
 
@@ -728,11 +749,11 @@ hipError_t decode_scratch(int device, float** ptr) {
 }
 
 size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan) {
-    return (size_t)plan.n_slots * plan.group * g.head_dim;
+    return (size_t)plan.n_slots * plan.cols * g.head_dim;
 }
 
 size_t decode_ws_ints_runs(const KvGeom& g, const DecodePlan& plan) {
-    return (size_t)2 * plan.batch * g.n_kv_heads;
+    return (size_t)2 * plan.batch * g.n_kv_heads * plan.n_cb;
 }
 
 hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWorkspace& ws,

@@ -65,13 +65,22 @@ struct DecodeParams {
     int32_t gqa_mode;
     float scale;
     int32_t item_pages;  // pages per work item (power of 2, <= kItemPages), set by decode_plan
+    // Query heads of a KV head ride in the MFMA columns, `cols` (<= 16, cols * D <= 2048) to
+    // a segment; a KV head with more splits into n_cb column blocks, each its own segment.
+    // group: query heads per KV head for the head map (modulo: ceil(n_q_heads / n_kv_heads),
+    // columns whose head would be >= n_q_heads are off).  Set by decode_plan.
+    int32_t group;
+    int32_t cols;
+    int32_t n_cb;
 };
 
 struct DecodePlan {
     int32_t grid;        // persistent workgroups (CUs x resident workgroups per CU)
     int32_t batch;
-    long long n_slots;   // partial slots: batch * n_kv_heads + grid
-    int32_t group;       // q heads per kv head
+    long long n_slots;   // partial slots: batch * segments per sequence + grid
+    int32_t group;       // query heads per KV head of the head map
+    int32_t cols;        // query heads per segment
+    int32_t n_cb;        // segments (column blocks) per KV head
     int32_t item_pages;  // pages per work item
 };
 // Floats of the per-GPU fixed scratch behind pi_attn_decode_noalloc (16 MiB).
@@ -80,9 +89,9 @@ constexpr size_t kDecodeScratchFloats = (size_t)4 << 20;
 // once per device with hipGetSymbolAddress.
 hipError_t decode_scratch(int device, float** ptr);
 
-// Grid size and workspace bound of a decode launch on `device`.
+// Grid size, head blocking and workspace bound of a decode launch on `device`.
 DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
-                       int device);
+                       int32_t gqa_mode, int device);
 size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan);
 // int32 entries of the per-segment run table (2 per (sequence, KV head)).
 size_t decode_ws_ints_runs(const KvGeom& g, const DecodePlan& plan);

@@ -133,6 +133,9 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     const int per_kv = a.group / HPW;           // workgroups per KV head
     const int kvh = blockIdx.x / per_kv;
     const int head = head_of(kvh, (blockIdx.x % per_kv) * HPW + hs, a.hkv, a.group, a.gqa_mode);
+    // modulo map with n_q_heads not a multiple of n_kv_heads: HPW is 1, so a
+    // workgroup whose head does not exist leaves as a whole, before any barrier
+    if (head >= a.hq) return;
     const int p0 = qb * WROWS + rt * ROWS;
     const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
     const int n_tiles = (wg_keys + BN - 1) / BN;
@@ -517,11 +520,14 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     a.q_off = q_off;
     a.hq = n_q_heads;
     a.hkv = n_kv_heads;
-    a.group = n_q_heads / n_kv_heads;
+    const bool multiple = n_q_heads % n_kv_heads == 0;
+    if (!multiple && gqa_mode != 0) return hipErrorInvalidValue;
+    // query heads per KV head (modulo map: up to ceil(Hq / Hkv), the last ones may not exist)
+    a.group = (n_q_heads + n_kv_heads - 1) / n_kv_heads;
     a.causal = causal;
     a.gqa_mode = gqa_mode;
     a.qk_scale = scale * kLog2e;
-    const int hpw = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
+    const int hpw = !multiple ? 1 : a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
     const bool bf = dtype == 2;
     if (head_dim == 128) launch_d<128>(a, hpw, n_kv_heads, seq_len, batch, bf, s);
     else launch_d<256>(a, hpw, n_kv_heads, seq_len, batch, bf, s);

@@ -216,12 +216,14 @@ __global__ __launch_bounds__(256) void tq_query_kernel(TqPool t, const float* __
     __shared__ float4 s_x[D];                    // query (pass 1) or R.q (pass 2), [row][head]
     __shared__ float s_part[2][kQueryHeads][D];  // per-half partial sums
     const int n_kv = t.g.n_kv_heads;
-    const int group = n_q_heads / n_kv;
+    // heads of KV head kvh: kvh + j * n_kv below n_q_heads (modulo map), or a block of `group`
+    const int group = gqa_mode == 0 ? (n_q_heads + n_kv - 1) / n_kv : n_q_heads / n_kv;
     const int n_chunks = (group + kQueryHeads - 1) / kQueryHeads;
     const int kvh = blockIdx.x / n_chunks, c0 = (blockIdx.x % n_chunks) * kQueryHeads;
-    const int nh = min(kQueryHeads, group - c0);
     const int b = blockIdx.y, tid = threadIdx.x, half = tid >> 7, i = tid & 127;
     auto head_of = [&](int k) { return gqa_mode == 0 ? kvh + (c0 + k) * n_kv : kvh * group + c0 + k; };
+    int nh = 0;  // heads of this chunk that exist
+    while (nh < kQueryHeads && c0 + nh < group && head_of(nh) < n_q_heads) ++nh;
 
     // stage the chunk's queries: thread (half, i) loads heads 2*half, 2*half + 1 of rows i + 128 c
     float* sx = reinterpret_cast<float*>(s_x);
@@ -337,7 +339,8 @@ hipError_t launch_tq_read(const TqPool& t, const int32_t* page_table, int32_t ma
 hipError_t launch_tq_query(const TqPool& t, const float* q, float* qv, int32_t batch,
                            int32_t n_q_heads, int32_t gqa_mode, hipStream_t s) {
     if (batch <= 0) return hipSuccess;
-    const int group = n_q_heads / t.g.n_kv_heads;
+    const int n_kv = t.g.n_kv_heads;
+    const int group = gqa_mode == 0 ? (n_q_heads + n_kv - 1) / n_kv : n_q_heads / n_kv;
     const int n_chunks = (group + kQueryHeads - 1) / kQueryHeads;
     const dim3 grid(t.g.n_kv_heads * n_chunks, batch);
     if (t.g.head_dim == 128)

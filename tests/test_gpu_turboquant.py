@@ -164,9 +164,9 @@ def test_bad_arguments_raise():
             rt.TqPool(dev, 4, 2, head_dim=d)
     pool = rt.TqPool(dev, 4, 2)
     q = torch.zeros((1, 3, D), dtype=torch.float32, device="cuda")
-    with pytest.raises(rt.Unsupported):  # 3 q heads over 2 kv heads
+    with pytest.raises(rt.InvalidArg):  # 3 q heads over 2 kv heads: only the modulo map
         rt.tq_attn_decode(dev, q, pool, to_dev(np.zeros((1, 4), np.int32)),
-                          to_dev(np.array([1], np.int32)))
+                          to_dev(np.array([1], np.int32)), gqa_mode=1)
 
 
 def test_append_records_bit_exact_d256():
