@@ -225,17 +225,19 @@ def attn_layer_tokens(q, k, v, gate=None, q_norm_w=None, k_norm_w=None, eps=1e-6
 
 
 def attn_prepare(q, k, n_heads, n_kv_heads, head_dim, q_norm_w=None, k_norm_w=None, eps=1e-6,
-                 rope_dim=None, rope_base=10000.0, freqs=None, pos0=0):
+                 rope_dim=None, rope_base=10000.0, freqs=None, pos0=0, q_head_dim=None):
     """Q/K norm + RoPE driver for n consecutive tokens (no attention); returns copies.
 
-    q [n, Hq, D] or None, k [n, Hkv, D] or None; token i at position pos0 + i."""
+    q [n, Hq, Dq] or None (Dq = q_head_dim, default head_dim), k [n, Hkv, D] or None;
+    token i at position pos0 + i."""
     qq = None if q is None else np.array(q, dtype=np.float32, copy=True)
     kk = None if k is None else np.array(k, dtype=np.float32, copy=True)
     n = (qq if qq is not None else kk).shape[0]
     qn = _f32(q_norm_w) if q_norm_w is not None else None
     kn = _f32(k_norm_w) if k_norm_w is not None else None
     f = _f32(freqs) if freqs is not None else None
-    lib().or_attn_prepare(_p(qq), _p(kk), n, n_heads, n_kv_heads, head_dim, head_dim, _p(qn),
+    lib().or_attn_prepare(_p(qq), _p(kk), n, n_heads, n_kv_heads,
+                          head_dim if q_head_dim is None else q_head_dim, head_dim, _p(qn),
                           _p(kn), float(eps), rope_dim if rope_dim else head_dim,
                           float(rope_base), _p(f), 0 if f is None else f.size, pos0)
     return qq, kk

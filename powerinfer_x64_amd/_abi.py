@@ -61,6 +61,8 @@ SIGNATURES = {
                                        _i32]),
     "pi_attn_layer_create": (_int, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _f32, _i32,
                                     _f32, _vp, _i32, ctypes.POINTER(_vp)]),
+    "pi_attn_layer_create_dims": (_int, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
+                                         _f32, _i32, _f32, _vp, _i32, ctypes.POINTER(_vp)]),
     "pi_attn_layer_destroy": (None, [_vp]),
     "pi_attn_layer_forward": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
     "pi_attn_layer_forward_dev": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp]),

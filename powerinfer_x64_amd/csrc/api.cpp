@@ -48,6 +48,7 @@ struct pi_attn_layer_s {
     pi_handle owner;
     pi_kv_pool pool = nullptr;      // max_pages pages, page i at physical page i
     int32_t max_pages = 0, n_heads = 0, n_kv = 0, dim = 0, kv_dtype = 0;
+    int32_t q_dim = 0, v_dim = 0;   // query / value head widths (dim: the key head width)
     int32_t rope_dim = 0, gqa_mode = 0;
     float eps = 0.f, rope_base = 0.f;
     int32_t sections[4] = {0, 0, 0, 0};
@@ -312,8 +313,6 @@ int pi_kv_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t
         return fail(h, PI_ERR_UNSUPPORTED, "pi_kv_pool_create: head_dim %d (64/128/256)", head_dim);
     if (dtype != PI_F32 && dtype != PI_F16)
         return fail(h, PI_ERR_UNSUPPORTED, "pi_kv_pool_create: pool dtype %d (f32 or f16)", dtype);
-    if (dtype == PI_F32 && head_dim == 256)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_kv_pool_create: f32 pool with head_dim 256");
     const int eb = dtype == PI_F32 ? 4 : 2;
     const size_t bytes = (size_t)n_pages * n_kv_heads * pi::kPageTokens * head_dim * eb;
     PI_HIP(h, hipSetDevice(h->device), "pi_kv_pool_create");
@@ -751,15 +750,15 @@ int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const flo
     PI_CHECK_HANDLE(h);
     if (!h_out || !h_q || (seq_len && (!h_k_cache || !h_v_cache)))
         return fail(h, PI_ERR_INVALID_ARG, "attention_head: null slice");
-    if (head_dim == 0 || head_dim > 128)
-        return fail(h, PI_ERR_UNSUPPORTED, "attention_head: head_dim %zu (1..128 on the device)", head_dim);
+    if (head_dim == 0 || head_dim > 256)
+        return fail(h, PI_ERR_UNSUPPORTED, "attention_head: head_dim %zu (1..256 on the device)", head_dim);
     if (seq_len > (size_t)1 << 24) return fail(h, PI_ERR_UNSUPPORTED, "attention_head: seq_len %zu", seq_len);
     PI_HIP(h, hipSetDevice(h->device), "attention_head");
     hipStream_t s = h->stream;
-    // Rows are zero-padded to a kernel head size (64 or 128): zero q and key
+    // Rows are zero-padded to a kernel head size (64, 128 or 256): zero q and key
     // dims leave every dot product unchanged, the scale stays 1/sqrt(head_dim),
     // and the padded output dims are dropped.
-    const size_t pd = head_dim <= 64 ? 64 : 128;
+    const size_t pd = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
     // One f32 sequence, one head: a pool with ceil(seq_len/16) pages and the identity table.
     const int n_pages = (int)((seq_len + 15) / 16) + 1;
     pi_kv_pool pool = nullptr;
@@ -950,9 +949,25 @@ int pi_attn_layer_create(pi_handle h, int32_t max_tokens, int32_t n_heads, int32
                          int32_t head_dim, int32_t kv_dtype, const float* h_q_norm_w,
                          const float* h_k_norm_w, float eps, int32_t rope_dim, float rope_base,
                          const int32_t* h_sections, int32_t gqa_mode, pi_attn_layer* out) {
+    return pi_attn_layer_create_dims(h, max_tokens, n_heads, n_kv_heads, head_dim, head_dim,
+                                     head_dim, kv_dtype, h_q_norm_w, h_k_norm_w, eps, rope_dim,
+                                     rope_base, h_sections, gqa_mode, out);
+}
+
+int pi_attn_layer_create_dims(pi_handle h, int32_t max_tokens, int32_t n_heads,
+                              int32_t n_kv_heads, int32_t q_head_dim, int32_t head_dim,
+                              int32_t v_head_dim, int32_t kv_dtype, const float* h_q_norm_w,
+                              const float* h_k_norm_w, float eps, int32_t rope_dim,
+                              float rope_base, const int32_t* h_sections, int32_t gqa_mode,
+                              pi_attn_layer* out) {
     PI_CHECK_HANDLE(h);
     if (!out) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: out is null");
     *out = nullptr;
+    // src/model/mod.rs:976-982,1043-1190: attention reads the first head_dim dims of each
+    // query head, so the query head is at least that wide; any value width
+    if (q_head_dim < head_dim || v_head_dim <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: q_head_dim=%d head_dim=%d v_head_dim=%d",
+                    q_head_dim, head_dim, v_head_dim);
     if (max_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: max_tokens=%d n_heads=%d n_kv_heads=%d",
                     max_tokens, n_heads, n_kv_heads);
@@ -968,6 +983,8 @@ int pi_attn_layer_create(pi_handle h, int32_t max_tokens, int32_t n_heads, int32
     L->n_heads = n_heads;
     L->n_kv = n_kv_heads;
     L->dim = head_dim;
+    L->q_dim = q_head_dim;
+    L->v_dim = v_head_dim;
     L->kv_dtype = kv_dtype;
     L->rope_dim = rope_dim;
     L->gqa_mode = gqa_mode;
@@ -1080,6 +1097,30 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     return PI_OK;
 }
 
+// Copies `rows` rows of `width` floats between buffers of row pitches `dp` / `sp` floats.
+static int copy_rows(pi_handle h, void* dst, size_t dp, const void* src, size_t sp, size_t width,
+                     size_t rows, hipMemcpyKind kind, hipStream_t s, const char* what) {
+    if (!rows || !width) return PI_OK;
+    PI_HIP(h, hipMemcpy2DAsync(dst, dp * 4, src, sp * 4, width * 4, rows, kind, s), what);
+    return PI_OK;
+}
+
+// The layer's inputs in the step's packed form, [n][H][head_dim] rows (src/model/mod.rs:
+// 1043-1190): the first head_dim dims of each query head; V cut or zero-padded to head_dim
+// (output dims at or past the value width stay zero, as the reference's head_out); the gate
+// as the flat prefix of n_heads * head_dim values of each token's n_heads * q_head_dim
+// (the reference multiplies attn_out[i] by sigmoid(output_gate[i]), :1192-1196).
+static int pack_layer_inputs(pi_handle h, pi_attn_layer L, const float* q, const float* v,
+                             const float* g, int32_t n, float* dq, float* dv, float* dg,
+                             hipMemcpyKind kind, hipStream_t s, const char* what) {
+    const size_t D = L->dim, Hq = L->n_heads, Hkv = L->n_kv;
+    int rc = copy_rows(h, dq, D, q, L->q_dim, D, (size_t)n * Hq, kind, s, what);
+    if (!rc && L->v_dim < (int)D) PI_HIP(h, pi::launch_fill_zero(dv, (size_t)n * Hkv * D, s), what);
+    if (!rc) rc = copy_rows(h, dv, D, v, L->v_dim, std::min<size_t>(D, L->v_dim), (size_t)n * Hkv, kind, s, what);
+    if (!rc && g) rc = copy_rows(h, dg, Hq * D, g, Hq * L->q_dim, Hq * D, n, kind, s, what);
+    return rc;
+}
+
 int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, const float* h_v,
                           const float* h_gate, int32_t n_tokens, float* h_out) {
     PI_CHECK_HANDLE(h);
@@ -1097,15 +1138,15 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
     int rc = grow(h, &L->d_buf, &L->buf_floats, 3 * nq + 2 * nk, s, "pi_attn_layer_forward staging", false);
     if (rc) return rc;
     float *dq = L->d_buf, *dg = dq + nq, *dout = dg + nq, *dk = dout + nq, *dv = dk + nk;
-    if ((rc = copy_sync(h, dq, h_q, nq * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
-    if ((rc = copy_sync(h, dk, h_k, nk * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
-    if ((rc = copy_sync(h, dv, h_v, nk * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
-    if (h_gate && (rc = copy_sync(h, dg, h_gate, nq * 4, hipMemcpyHostToDevice, "pi_attn_layer_forward"))) return rc;
+    const char* what = "pi_attn_layer_forward";
+    if ((rc = pack_layer_inputs(h, L, h_q, h_v, h_gate, n_tokens, dq, dv, dg, hipMemcpyHostToDevice, s, what))) return rc;
+    if ((rc = copy_sync(h, dk, h_k, nk * 4, hipMemcpyHostToDevice, what))) return rc;
     if ((rc = attn_layer_step(h, L, dq, dk, dv, h_gate ? dg : nullptr, n_tokens, dout, s))) return rc;
-    if ((rc = copy_sync(h, h_out, dout, nq * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
-    if ((rc = copy_sync(h, h_q, dq, nq * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
-    if ((rc = copy_sync(h, h_k, dk, nk * 4, hipMemcpyDeviceToHost, "pi_attn_layer_forward"))) return rc;
-    PI_HIP(h, hipStreamSynchronize(s), "pi_attn_layer_forward");
+    if ((rc = copy_sync(h, h_out, dout, nq * 4, hipMemcpyDeviceToHost, what))) return rc;
+    // q and k come back normalised and rotated (only the first head_dim dims of a query head)
+    if ((rc = copy_rows(h, h_q, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads, hipMemcpyDeviceToHost, s, what))) return rc;
+    if ((rc = copy_sync(h, h_k, dk, nk * 4, hipMemcpyDeviceToHost, what))) return rc;
+    PI_HIP(h, hipStreamSynchronize(s), what);
     return PI_OK;
 }
 
@@ -1117,8 +1158,19 @@ int pi_attn_layer_forward_dev(pi_handle h, pi_attn_layer L, float* d_q, float* d
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward_dev: null argument");
     if (n_tokens < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward_dev: n_tokens=%d", n_tokens);
     if (n_tokens == 0) return PI_OK;
-    PI_HIP(h, hipSetDevice(h->device), "pi_attn_layer_forward_dev");
-    return attn_layer_step(h, L, d_q, d_k, d_v, d_gate, n_tokens, d_out, pick(h, stream));
+    const char* what = "pi_attn_layer_forward_dev";
+    PI_HIP(h, hipSetDevice(h->device), what);
+    hipStream_t s = pick(h, stream);
+    if (L->q_dim == L->dim && L->v_dim == L->dim)  // already in the step's packed form
+        return attn_layer_step(h, L, d_q, d_k, d_v, d_gate, n_tokens, d_out, s);
+    const int D = L->dim;
+    const size_t nq = (size_t)n_tokens * L->n_heads * D, nk = (size_t)n_tokens * L->n_kv * D;
+    int rc = grow(h, &L->d_buf, &L->buf_floats, 2 * nq + nk, s, "pi_attn_layer_forward_dev staging", false);
+    if (rc) return rc;
+    float *dq = L->d_buf, *dg = dq + nq, *dv = dg + nq;
+    if ((rc = pack_layer_inputs(h, L, d_q, d_v, d_gate, n_tokens, dq, dv, dg, hipMemcpyDeviceToDevice, s, what))) return rc;
+    if ((rc = attn_layer_step(h, L, dq, d_k, dv, d_gate ? dg : nullptr, n_tokens, d_out, s))) return rc;
+    return copy_rows(h, d_q, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads, hipMemcpyDeviceToDevice, s, what);
 }
 
 // ---- gated-DeltaNet layer state -------------------------------------------------------

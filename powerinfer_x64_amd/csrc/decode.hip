@@ -705,7 +705,7 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
     else switch (g.head_dim) {
         case 64: per_cu = hp ? wgs_per_cu<f16, 64>() : wgs_per_cu<float, 64>(); break;
         case 128: per_cu = hp ? wgs_per_cu<f16, 128>() : wgs_per_cu<float, 128>(); break;
-        default: per_cu = wgs_per_cu<f16, 256>(); break;
+        default: per_cu = hp ? wgs_per_cu<f16, 256>() : wgs_per_cu<float, 256>(); break;
     }
     // A segment splits into at most grid + 1 runs; the merge kernel stages
     // kMaxRuns of them in LDS, so the grid stays below that.
@@ -767,7 +767,7 @@ hipError_t launch_decode(const KvGeom& g, const DecodeParams& p, const DecodeWor
     switch (g.head_dim) {
         case 64: return hp ? launch_t<f16, 64>(g, p, ws, plan, s) : launch_t<float, 64>(g, p, ws, plan, s);
         case 128: return hp ? launch_t<f16, 128>(g, p, ws, plan, s) : launch_t<float, 128>(g, p, ws, plan, s);
-        case 256: return hp ? launch_t<f16, 256>(g, p, ws, plan, s) : hipErrorInvalidValue;
+        case 256: return hp ? launch_t<f16, 256>(g, p, ws, plan, s) : launch_t<float, 256>(g, p, ws, plan, s);
         default: return hipErrorInvalidValue;
     }
 }

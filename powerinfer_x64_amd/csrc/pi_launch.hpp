@@ -128,6 +128,7 @@ hipError_t launch_softmax(float* x, int32_t n, hipStream_t s);
 hipError_t launch_to_half(const float* x, void* y, size_t n, hipStream_t s);
 hipError_t launch_apply_gate(float* out, const float* gate, size_t n, hipStream_t s);
 hipError_t launch_fill_iota(int32_t* dst, int32_t n, int32_t first, hipStream_t s);
+hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t s);
 hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
                                 const float* k_norm_w, float eps, const RopeFreqs& freqs,
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,

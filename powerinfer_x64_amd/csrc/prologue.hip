@@ -382,6 +382,13 @@ hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, in
     return hipGetLastError();
 }
 
+// Zeros written by a kernel (a memset node must not sit in a captured graph).
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ dst, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = 0.f;
+}
+
 // dst[i] = first + i for i < n (device-side positions and context lengths, so a
 // layer step issues no host copies).
 __global__ __launch_bounds__(256) void fill_iota_kernel(int32_t* __restrict__ dst, int n,
@@ -413,6 +420,12 @@ static unsigned grid_1d(size_t n) {
 hipError_t launch_to_half(const float* x, void* y, size_t n, hipStream_t s) {
     hipLaunchKernelGGL(to_half_kernel, dim3(grid_1d(n)), dim3(256), 0, s, x,
                        reinterpret_cast<f16*>(y), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_1d(n)), dim3(256), 0, s, dst, n);
     return hipGetLastError();
 }
 

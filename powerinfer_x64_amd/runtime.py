@@ -167,9 +167,14 @@ class AttnLayer:
     def __init__(self, dev: Device, max_tokens: int, n_heads: int, n_kv_heads: int,
                  head_dim: int, kv_dtype: torch.dtype = torch.float16, q_norm_w=None,
                  k_norm_w=None, eps: float = 1e-6, rope_dim: int = None,
-                 rope_base: float = 1e6, sections=None, gqa_mode: int = MODULO):
+                 rope_base: float = 1e6, sections=None, gqa_mode: int = MODULO,
+                 q_head_dim: int = None, v_head_dim: int = None):
+        """head_dim is the key head width; q_head_dim (>= head_dim) and v_head_dim default to
+        it (src/model/mod.rs:976-982: the three may differ)."""
         self.dev = dev
         self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
+        self.q_head_dim = head_dim if q_head_dim is None else q_head_dim
+        self.v_head_dim = head_dim if v_head_dim is None else v_head_dim
         qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, np.float32).reshape(-1)
         kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, np.float32).reshape(-1)
         for name, w in (("q_norm_w", qn), ("k_norm_w", kn)):
@@ -177,8 +182,9 @@ class AttnLayer:
                 raise InvalidArg(f"{name}: expected {head_dim} values, got {w.size}")
         sec = None if sections is None else (ctypes.c_int32 * 4)(*[int(x) for x in sections])
         p = ctypes.c_void_p()
-        dev.check(dev.lib.pi_attn_layer_create(
-            dev.h, max_tokens, n_heads, n_kv_heads, head_dim, _DTYPE_CODE.get(kv_dtype, -1),
+        dev.check(dev.lib.pi_attn_layer_create_dims(
+            dev.h, max_tokens, n_heads, n_kv_heads, self.q_head_dim, head_dim, self.v_head_dim,
+            _DTYPE_CODE.get(kv_dtype, -1),
             None if qn is None else qn.ctypes.data_as(ctypes.c_void_p),
             None if kn is None else kn.ctypes.data_as(ctypes.c_void_p), float(eps),
             head_dim if rope_dim is None else rope_dim, float(rope_base), sec, gqa_mode,
@@ -204,20 +210,21 @@ class AttnLayer:
         self.dev.lib.pi_attn_layer_reset(self.p)
 
     def forward(self, q: np.ndarray, k: np.ndarray, v: np.ndarray, gate=None):
-        """q [n, Hq, D], k, v [n, Hkv, D] float32 (q, k normalised / rotated in place);
-        returns out [n, Hq, D]."""
+        """q [n, Hq, Dq], k [n, Hkv, D], v [n, Hkv, Dv] float32 (q, k normalised / rotated in
+        place); gate like q; returns out [n, Hq, D]."""
         n = q.shape[0]
-        for name, a, h in (("q", q, self.n_heads), ("k", k, self.n_kv_heads),
-                           ("v", v, self.n_kv_heads)):
+        for name, a, h, d in (("q", q, self.n_heads, self.q_head_dim),
+                              ("k", k, self.n_kv_heads, self.head_dim),
+                              ("v", v, self.n_kv_heads, self.v_head_dim)):
             if (not isinstance(a, np.ndarray) or a.dtype != np.float32 or
-                    not a.flags.c_contiguous or a.shape != (n, h, self.head_dim)):
-                raise InvalidArg(f"{name}: expected C-contiguous float32 [{n}, {h}, {self.head_dim}]")
+                    not a.flags.c_contiguous or a.shape != (n, h, d)):
+                raise InvalidArg(f"{name}: expected C-contiguous float32 [{n}, {h}, {d}]")
         g = None
         if gate is not None:
             g = np.ascontiguousarray(gate, np.float32)
             if g.shape != q.shape:
                 raise InvalidArg(f"gate: shape {g.shape}")
-        out = np.empty_like(q)
+        out = np.empty((n, self.n_heads, self.head_dim), np.float32)
         vp = lambda a: None if a is None else a.ctypes.data_as(ctypes.c_void_p)
         self.dev.check(self.dev.lib.pi_attn_layer_forward(self.dev.h, self.p, vp(q), vp(k), vp(v),
                                                           vp(g), n, vp(out)))
@@ -225,18 +232,20 @@ class AttnLayer:
 
     def forward_dev(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     gate: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
-        """The same step on device tensors (f32, q [n, Hq, D], k / v [n, Hkv, D]; q and k
-        normalised / rotated in place), enqueued on torch's current stream."""
+        """The same step on device tensors (f32, q / gate [n, Hq, Dq], k [n, Hkv, D],
+        v [n, Hkv, Dv]; q and k normalised / rotated in place), enqueued on torch's current
+        stream; returns out [n, Hq, D]."""
         d = self.dev
         n = q.shape[0]
-        _need(q, "q", torch.float32, (n, self.n_heads, self.head_dim), d.torch_device)
-        for name, t in (("k", k), ("v", v)):
-            _need(t, name, torch.float32, (n, self.n_kv_heads, self.head_dim), d.torch_device)
+        _need(q, "q", torch.float32, (n, self.n_heads, self.q_head_dim), d.torch_device)
+        _need(k, "k", torch.float32, (n, self.n_kv_heads, self.head_dim), d.torch_device)
+        _need(v, "v", torch.float32, (n, self.n_kv_heads, self.v_head_dim), d.torch_device)
         if gate is not None:
             _need(gate, "gate", torch.float32, q.shape, d.torch_device)
+        shp = (n, self.n_heads, self.head_dim)
         if out is None:
-            out = torch.empty_like(q)
-        _need(out, "out", torch.float32, q.shape, d.torch_device)
+            out = torch.empty(shp, dtype=torch.float32, device=q.device)
+        _need(out, "out", torch.float32, shp, d.torch_device)
         d.check(d.lib.pi_attn_layer_forward_dev(d.h, self.p, _vp(q), _vp(k), _vp(v), _vp(gate), n,
                                                 _vp(out), d.stream()))
         return out

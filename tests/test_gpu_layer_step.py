@@ -19,11 +19,12 @@ def _pool(rt, dev, n_seq, max_tokens, hkv, d, dtype, rng):
     return rt.KvPool(dev, n_seq * pages, hkv, d, dtype=dtype), to_dev(pt)
 
 
-@pytest.mark.parametrize("shape", ["c2", "c4", "c2_prompt", "c4_prompt"])
+@pytest.mark.parametrize("shape", ["c2", "c4", "c2_prompt", "c4_prompt", "c4_f32"])
 def test_prologue_matches_oracle(shape):
     """Three sequences, 5 tokens each at different offsets; *_prompt: one 1100-token
     prompt (a launch of >= 1024 tokens shares one cos / sin table per token), with NORM
-    RoPE (c2) or Q/K RMSNorm and IMRoPE at D 256 (c4)."""
+    RoPE (c2) or Q/K RMSNorm and IMRoPE at D 256 (c4); the c2 shapes and c4_f32 append to an
+    f32 pool, the other c4 shapes to an f16 one."""
     from powerinfer_x64_amd import runtime as rt
     dev = device()
     rng = np.random.default_rng(50)
@@ -42,7 +43,7 @@ def test_prologue_matches_oracle(shape):
     qn = rng.uniform(0.5, 1.5, d).astype(np.float32) if norm else None
     kn = rng.uniform(0.5, 1.5, d).astype(np.float32) if norm else None
     freqs = orc.compute_imrope_freqs(base, rd, sec) if sec else None
-    pool_dtype = torch.float32 if d <= 128 else torch.float16  # f32 pools hold D <= 128
+    pool_dtype = torch.float16 if shape in ("c4", "c4_prompt") else torch.float32
     pool, pt = _pool(rt, dev, n_seq, int(starts.max()) + n_tok, hkv, d, pool_dtype, rng)
     tq, tk = to_dev(q), to_dev(k)
     rt.attn_prologue(dev, tq, tk, to_dev(v), pool, pt, to_dev(starts),

@@ -281,6 +281,48 @@ def test_attn_layer_qk_norm_imrope_gate_f64(orc):
     np.testing.assert_allclose(kc[prev:], kr, atol=5e-5)
 
 
+@pytest.mark.parametrize("dq,dk,dv", [(48, 32, 32), (32, 32, 20), (40, 32, 44)])
+def test_attn_layer_distinct_head_widths_f64(orc, dq, dk, dv):
+    """Query, key and value heads of different widths (src/model/mod.rs:976-982, 1035-1196):
+    the Q norm and RoPE touch the first dk dims of a query head and attention reads only
+    those; output dims at or past dv stay zero and value dims past dk are not read; the gate
+    is the flat prefix of hq * dk values of each token's hq * dq."""
+    rng = np.random.default_rng(dq * 1000 + dv)
+    n, hq, hkv, eps = 5, 4, 2, 1e-6
+    q = rng.standard_normal((n, hq, dq)).astype(np.float32)
+    k = rng.standard_normal((n, hkv, dk)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, dv)).astype(np.float32)
+    gate = rng.standard_normal((n, hq, dq)).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, dk).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, dk).astype(np.float32)
+    out, kc, vc = orc.attn_layer_tokens(q, k, v, gate=gate, q_norm_w=qn, k_norm_w=kn, eps=eps,
+                                        rope_base=1e4)
+    assert out.shape == (n, hq, dk) and vc.shape == (n, hkv, dv)
+    qr = ref64.rms_norm(q[:, :, :dk], qn, eps)
+    kr = ref64.rms_norm(k, kn, eps)
+    qr = np.stack([ref64.rope_adjacent(qr[i], i, dk, 1e4) for i in range(n)])
+    kr = np.stack([ref64.rope_adjacent(kr[i], i, dk, 1e4) for i in range(n)])
+    m = min(dk, dv)
+    exp = np.zeros((n, hq, dk))
+    for i in range(n):
+        exp[i, :, :m] = ref64.attention(qr[i], kr[:i + 1], v[:i + 1, :, :m], lambda h: h % hkv)
+    g = gate.reshape(n, hq * dq)[:, :hq * dk].reshape(n, hq, dk).astype(np.float64)
+    exp = exp / (1 + np.exp(-g))
+    np.testing.assert_allclose(out, exp, atol=2e-5)
+    assert not out[:, :, m:].any()
+    np.testing.assert_allclose(kc, kr, atol=2e-5)
+    # the Q dims past dk are neither normalised, rotated nor read
+    qq, _ = orc.attn_prepare(q, None, hq, hkv, dk, q_norm_w=qn, eps=eps, rope_base=1e4,
+                             q_head_dim=dq)
+    np.testing.assert_allclose(qq[:, :, :dk], qr, atol=2e-5)
+    np.testing.assert_array_equal(qq[:, :, dk:], q[:, :, dk:])
+    q2 = q.copy()
+    q2[:, :, dk:] = rng.standard_normal(q2[:, :, dk:].shape)
+    out2, _, _ = orc.attn_layer_tokens(q2, k, v, gate=gate, q_norm_w=qn, k_norm_w=kn, eps=eps,
+                                       rope_base=1e4)
+    np.testing.assert_array_equal(out, out2)
+
+
 # ---- src/model/mod.rs gated-DeltaNet ---------------------------------------
 
 def test_gdn_gates_closed_form(orc):
