@@ -694,8 +694,10 @@ static int gdn_shape_check(pi_handle h, const char* fn, int32_t n_k_heads, int32
                            int32_t k_hd, int32_t v_hd) {
     if (n_k_heads <= 0 || n_v_heads <= 0)
         return fail(h, PI_ERR_INVALID_ARG, "%s: n_k_heads=%d n_v_heads=%d", fn, n_k_heads, n_v_heads);
-    if (k_hd != 128 || v_hd != 128)
-        return fail(h, PI_ERR_UNSUPPORTED, "%s: k_hd=%d v_hd=%d (128)", fn, k_hd, v_hd);
+    if (k_hd <= 0 || v_hd <= 0)
+        return fail(h, PI_ERR_INVALID_ARG, "%s: k_hd=%d v_hd=%d", fn, k_hd, v_hd);
+    if (k_hd > pi::kGdnMaxKhd)
+        return fail(h, PI_ERR_UNSUPPORTED, "%s: k_hd=%d (at most %d)", fn, k_hd, pi::kGdnMaxKhd);
     return PI_OK;
 }
 
@@ -712,7 +714,7 @@ int pi_gdn_decode(pi_handle h, const float* d_q, const float* d_k, const float* 
     if (batch == 0) return PI_OK;
     PI_HIP(h, hipSetDevice(h->device), "pi_gdn_decode");
     PI_HIP(h, pi::launch_gdn_decode(d_q, d_k, d_v, d_beta, d_g, d_state, d_out, batch, n_k_heads,
-                                    n_v_heads, pick(h, stream)),
+                                    n_v_heads, k_hd, v_hd, pick(h, stream)),
            "pi_gdn_decode");
     return PI_OK;
 }
@@ -727,10 +729,17 @@ int pi_gdn_prefill(pi_handle h, const float* d_q, const float* d_k, const float*
     if (n_tok < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_prefill: n_tok=%d", n_tok);
     int rc = gdn_shape_check(h, "pi_gdn_prefill", n_k_heads, n_v_heads, k_hd, v_hd);
     if (rc) return rc;
-    if (chunk != 64) return fail(h, PI_ERR_UNSUPPORTED, "pi_gdn_prefill: chunk %d (64)", chunk);
+    if (chunk != 64 && chunk != 1)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_gdn_prefill: chunk %d (64, or 1: token by token)", chunk);
     if (n_tok == 0) return PI_OK;
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_gdn_prefill");
+    if (chunk == 1 || k_hd != 128 || v_hd != 128) {  // the per-token recurrence, any widths
+        PI_HIP(h, pi::launch_gdn_recur(d_q, d_k, d_v, d_beta, d_g, d_state, d_out, 1, n_tok, n_k_heads,
+                                       n_v_heads, k_hd, v_hd, s),
+               "pi_gdn_prefill");
+        return PI_OK;
+    }
     if ((rc = ws_begin(h, s, "pi_gdn_prefill"))) return rc;
     const size_t need = pi::gdn_prefill_ws_floats(n_tok, n_k_heads, n_v_heads, chunk);
     if (need) {
@@ -931,7 +940,8 @@ int pi_ssm_gated_delta_step(pi_handle h, float* h_out, float* h_state, const flo
     if ((rc = copy_sync(h, dv, h_v, nv * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
     if ((rc = copy_sync(h, db, h_beta, nh * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
     if ((rc = copy_sync(h, dg, h_g, nh * 4, hipMemcpyHostToDevice, "gated_delta_step"))) return rc;
-    PI_HIP(h, pi::launch_gdn_decode(dq, dk, dv, db, dg, ds, dout, 1, n_k_heads, n_v_heads, h->stream),
+    PI_HIP(h, pi::launch_gdn_decode(dq, dk, dv, db, dg, ds, dout, 1, n_k_heads, n_v_heads, k_hd,
+                                    v_hd, h->stream),
            "gated_delta_step");
     if ((rc = copy_sync(h, h_state, ds, ns * 4, hipMemcpyDeviceToHost, "gated_delta_step"))) return rc;
     if ((rc = copy_sync(h, h_out, dout, nv * 4, hipMemcpyDeviceToHost, "gated_delta_step"))) return rc;

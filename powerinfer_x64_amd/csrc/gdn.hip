@@ -293,6 +293,107 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// Any head widths (k_hd <= 256, any v_hd): the per-token recurrence of
+// src/model/mod.rs:841-916 itself, token after token.  A wavefront owns 8
+// state columns of one (sequence, V head): lane (r = lane / 8, c = lane % 8)
+// holds rows r + 8 i (i < NR) of column c0 + c in registers, so every column
+// sum (the norms, S^T k, S^T q) is a 3-step shuffle over the 8 row groups and
+// no wavefront waits for another.  The next token's q, k, v, beta and g are
+// loaded while the current one computes.  `stride` is the token pitch of the
+// q / k / v / beta / g rows: n_tok consecutive tokens of one sequence
+// (prefill), or one token of each of `batch` sequences (decode, n_tok = 1).
+// ---------------------------------------------------------------------------
+template <int NR>
+__global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict__ q,
+                                                        const float* __restrict__ k,
+                                                        const float* __restrict__ v,
+                                                        const float* __restrict__ beta,
+                                                        const float* __restrict__ g,
+                                                        float* __restrict__ state,
+                                                        float* __restrict__ out, int n_tok,
+                                                        int hk, int hv, int dk, int dv) {
+    const int lane = threadIdx.x & 63;
+    const int c0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 8;
+    if (c0 >= dv) return;  // a whole wavefront past the last column
+    const int vh = blockIdx.y, b = blockIdx.z, kh = vh % hk;
+    const int r = lane >> 3, col = c0 + (lane & 7);
+    const bool con = col < dv;
+    // token t of this (sequence, V head): rows of q / k at ((b + t) * hk + kh) * dk, ...
+    const size_t sh = (size_t)b * hv + vh;
+    float* S = state + sh * dk * dv + (con ? col : 0);
+    float s[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int row = r + 8 * i;
+        s[i] = (con && row < dk) ? S[(size_t)row * dv] : 0.f;
+    }
+    const float qs = 1.0f / sqrtf((float)dk);
+    float qn[NR], kn[NR], vx = 0.f, bt = 0.f, gx = 0.f;
+    auto fetch = [&](int t) {
+        const size_t tok = (size_t)b + t;  // sequence b's token t (one of the two is 0)
+        const float* qr = q + (tok * hk + kh) * dk;
+        const float* kr = k + (tok * hk + kh) * dk;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int row = r + 8 * i;
+            qn[i] = row < dk ? qr[row] : 0.f;
+            kn[i] = row < dk ? kr[row] : 0.f;
+        }
+        vx = con ? v[(tok * hv + vh) * dv + col] : 0.f;
+        bt = beta[tok * hv + vh];
+        gx = g[tok * hv + vh];
+    };
+    fetch(0);
+    for (int t = 0; t < n_tok; ++t) {
+        float qc[NR], kc[NR];
+        float sq = 0.f, sk = 0.f;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            qc[i] = qn[i];
+            kc[i] = kn[i];
+            sq += qc[i] * qc[i];
+            sk += kc[i] * kc[i];
+        }
+        const float vc = vx, bc = bt, decay = expf(gx);
+        if (t + 1 < n_tok) fetch(t + 1);
+#pragma unroll
+        for (int m = 8; m <= 32; m <<= 1) {
+            sq = wave_sum_xor(sq, m);
+            sk = wave_sum_xor(sk, m);
+        }
+        // L2 norms with max(|x|, 1e-12), q also / sqrt(k_hd) (src/model/mod.rs:855-875)
+        const float nq = fmaxf(sqrtf(sq), 1e-12f), nk = fmaxf(sqrtf(sk), 1e-12f);
+        // S *= exp(g); kv_mem = S^T k (:883-898)
+        float kv = 0.f;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            kc[i] = kc[i] / nk;
+            qc[i] = qc[i] / nq * qs;
+            s[i] *= decay;
+            kv += s[i] * kc[i];
+        }
+#pragma unroll
+        for (int m = 8; m <= 32; m <<= 1) kv = wave_sum_xor(kv, m);
+        // delta = (v - kv_mem) beta; S += k delta^T; o = S^T q (:899-916)
+        const float delta = (vc - kv) * bc;
+        float o = 0.f;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            s[i] += kc[i] * delta;
+            o += s[i] * qc[i];
+        }
+#pragma unroll
+        for (int m = 8; m <= 32; m <<= 1) o = wave_sum_xor(o, m);
+        if (r == 0 && con) out[(((size_t)b + t) * hv + vh) * dv + col] = o;
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int row = r + 8 * i;
+        if (con && row < dk) S[(size_t)row * dv] = s[i];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Chunked prefill.  For a chunk of C = 64 tokens of one V head, with q/k
 // normalised, gamma_i = exp(lg_i), lg = inclusive cumsum of g over the chunk
 // and S the state entering the chunk, the per-token recurrence above equals
@@ -933,9 +1034,32 @@ hipError_t launch_gdn_rmsnorm_gated(float* o, const float* z, const float* w, in
     return hipGetLastError();
 }
 
+hipError_t launch_gdn_recur(const float* q, const float* k, const float* v, const float* beta,
+                            const float* g, float* state, float* out, int32_t batch, int32_t n_tok,
+                            int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd, int32_t v_hd,
+                            hipStream_t s) {
+    if (k_hd <= 0 || k_hd > kGdnMaxKhd || v_hd <= 0 || (batch > 1 && n_tok != 1))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((v_hd + 31) / 32), (unsigned)n_v_heads, (unsigned)batch);
+    const int nr = (k_hd + 7) / 8;
+#define PI_GDN_RECUR(N)                                                                           \
+    hipLaunchKernelGGL(gdn_recur_kernel<N>, grid, dim3(256), 0, s, q, k, v, beta, g, state, out, \
+                       n_tok, n_k_heads, n_v_heads, k_hd, v_hd)
+    if (nr <= 4) PI_GDN_RECUR(4);
+    else if (nr <= 8) PI_GDN_RECUR(8);
+    else if (nr <= 16) PI_GDN_RECUR(16);
+    else PI_GDN_RECUR(32);
+#undef PI_GDN_RECUR
+    return hipGetLastError();
+}
+
 hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, const float* beta,
                              const float* g, float* state, float* out, int32_t batch,
-                             int32_t n_k_heads, int32_t n_v_heads, hipStream_t s) {
+                             int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd, int32_t v_hd,
+                             hipStream_t s) {
+    if (k_hd != DK || v_hd != DV)
+        return launch_gdn_recur(q, k, v, beta, g, state, out, batch, 1, n_k_heads, n_v_heads, k_hd,
+                                v_hd, s);
     hipLaunchKernelGGL(gdn_decode_kernel, dim3(DV / DCOLS, n_v_heads, batch), dim3(256), 0, s, q, k,
                        v, beta, g, state, out, n_k_heads, n_v_heads);
     return hipGetLastError();

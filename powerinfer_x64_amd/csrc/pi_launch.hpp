@@ -157,9 +157,19 @@ hipError_t launch_gdn_conv1d(const float* x, float* state, const float* w, float
                              hipStream_t s);
 hipError_t launch_gdn_rmsnorm_gated(float* o, const float* z, const float* w, int32_t n_rows,
                                     int32_t n_v_heads, int32_t v_hd, float eps, hipStream_t s);
+// Largest key head width of the gated-DeltaNet kernels; k_hd = v_hd = 128
+// run the tuned decode / chunked kernels, other widths the per-token kernel.
+constexpr int kGdnMaxKhd = 256;
 hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, const float* beta,
                              const float* g, float* state, float* out, int32_t batch,
-                             int32_t n_k_heads, int32_t n_v_heads, hipStream_t s);
+                             int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd, int32_t v_hd,
+                             hipStream_t s);
+// The per-token recurrence for any k_hd <= kGdnMaxKhd and v_hd: `batch`
+// sequences of one token each, or one sequence of n_tok tokens.
+hipError_t launch_gdn_recur(const float* q, const float* k, const float* v, const float* beta,
+                            const float* g, float* state, float* out, int32_t batch, int32_t n_tok,
+                            int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd, int32_t v_hd,
+                            hipStream_t s);
 
 struct GdnWorkspace {
     float* buf;

@@ -68,7 +68,9 @@ def _inputs(rng, n, hk, hv, dk, dv):
 @pytest.mark.parametrize("hk,hv,d", [(16, 32, 128), (2, 4, 128)])
 def test_gdn_layer_prompt_decode_chunk_reset(hk, hv, d):
     """A 200-token prompt, 3 decode tokens, a 65-token continued chunk, then reset
-    and a fresh 1-token start and 40-token prompt: each call's output to 2e-3."""
+    and a fresh 1-token start and 40-token prompt.  Each output element within the
+    recurrence's 2e-3 bound carried through RMSNormGated (_OracleLayer.forward), and each
+    (token, V head) row within 1e-2 relative."""
     from powerinfer_x64_amd import runtime as rt
     dev = device()
     rng = np.random.default_rng(90 + hk)
