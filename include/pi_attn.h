@@ -260,6 +260,18 @@ int pi_ssm_gated_delta_step(pi_handle h, float* h_out, float* h_state, const flo
                             const float* h_k, const float* h_v, const float* h_beta,
                             const float* h_g, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
                             int32_t v_hd);
+/* ssm::ssm_forward (src/ssm/mod.rs:40-157): one token of the Mamba-2-style
+ * selective scan on host slices, computed on the device.  x, dt_bias [d_inner];
+ * ssm_a, state [d_state * d_inner] (state in/out); alpha [d_inner * d_inner];
+ * conv1d, beta and out_w are taken at the lengths passed, and as in the
+ * reference the conv taps apply only when conv1d_len = d_inner * d_conv, the
+ * input-dependent B only when beta_len = d_state * d_inner, the output
+ * projection only when out_len = d_inner * d_inner.  y [d_inner]. */
+int pi_ssm_forward(pi_handle h, float* h_y, const float* h_x, const float* h_conv1d,
+                   size_t conv1d_len, const float* h_ssm_a, const float* h_dt_bias,
+                   const float* h_alpha, const float* h_beta, size_t beta_len,
+                   const float* h_out_w, size_t out_len, float* h_state, size_t d_inner,
+                   size_t d_state, size_t d_conv);
 
 /* ---- Attention layer cache (the seam in InferenceContext::forward) -------------------
  * LayerCache (src/model/mod.rs:73-106) of one attention layer for one sequence, held on the

@@ -6,7 +6,7 @@
 // #[test]s) reads the same:
 //   powerinfer::ops  -- src/ops.rs: rms_norm, apply_rope, compute_imrope_freqs,
 //                       apply_rope_with_freqs, softmax, attention_head
-//   powerinfer::ssm  -- src/ssm/mod.rs: create_ssm_state, plus the gated-delta
+//   powerinfer::ssm  -- src/ssm/mod.rs: ssm_forward, create_ssm_state, plus the gated-delta
 //                       step of src/model/mod.rs:841-916
 //   powerinfer::rocm -- the offload seam of src/cuda/mod.rs:373-537:
 //                       Device::init() -> std::optional (None = CPU path) and
@@ -115,6 +115,25 @@ public:
         return result(pi_ssm_gated_delta_step(h_, out.data(), state.data(), q.data(), k.data(),
                                               v.data(), beta.data(), g.data(), (int32_t)n_k_heads,
                                               (int32_t)n_v_heads, (int32_t)k_hd, (int32_t)v_hd));
+    }
+
+    std::optional<Result> try_ssm_forward(std::span<float> y, std::span<const float> x,
+                                          std::span<const float> ssm_conv1d,
+                                          std::span<const float> ssm_a,
+                                          std::span<const float> ssm_dt_bias,
+                                          std::span<const float> ssm_alpha,
+                                          std::span<const float> ssm_beta,
+                                          std::span<const float> ssm_out, std::span<float> state,
+                                          size_t d_inner, size_t d_state, size_t d_conv) const {
+        // the reference's debug_assert_eq!s (src/ssm/mod.rs:53-54) and the slices it indexes
+        if (x.size() != d_inner || y.size() != d_inner || state.size() != d_state * d_inner ||
+            ssm_a.size() != d_state * d_inner || ssm_dt_bias.size() != d_inner ||
+            ssm_alpha.size() != d_inner * d_inner)
+            return Result{PI_ERR_INVALID_ARG, "ssm_forward: slice sizes do not match d_inner / d_state"};
+        return result(pi_ssm_forward(h_, y.data(), x.data(), ssm_conv1d.data(), ssm_conv1d.size(),
+                                     ssm_a.data(), ssm_dt_bias.data(), ssm_alpha.data(),
+                                     ssm_beta.data(), ssm_beta.size(), ssm_out.data(),
+                                     ssm_out.size(), state.data(), d_inner, d_state, d_conv));
     }
 
 private:
@@ -299,6 +318,24 @@ inline void attention_head(std::span<float> out, std::span<const float> q,
 }  // namespace ops
 
 namespace ssm {
+
+// src/ssm/mod.rs:40-52: ssm_forward, one token of the Mamba-2-style selective
+// scan (the reference keeps it beside the gated-DeltaNet path and does not call
+// it from forward), computed on the device; returns y [d_inner], updates state.
+inline std::vector<float> ssm_forward(std::span<const float> x, std::span<const float> ssm_conv1d,
+                                      std::span<const float> ssm_a,
+                                      std::span<const float> ssm_dt_bias,
+                                      std::span<const float> ssm_alpha,
+                                      std::span<const float> ssm_beta,
+                                      std::span<const float> ssm_out, std::span<float> state,
+                                      size_t d_inner, size_t d_state, size_t d_conv) {
+    std::vector<float> y(d_inner);
+    auto& d = rocm::current();
+    const Result r = *d.try_ssm_forward(y, x, ssm_conv1d, ssm_a, ssm_dt_bias, ssm_alpha, ssm_beta,
+                                        ssm_out, state, d_inner, d_state, d_conv);
+    if (!r.ok()) throw BackendError(r.status, r.message);
+    return y;
+}
 
 // src/ssm/mod.rs:164-166: a zeroed [d_state * d_inner] state.  For a Qwen3.5
 // gated-DeltaNet layer d_state * d_inner = n_v_heads * k_hd * v_hd, laid out

@@ -398,6 +398,66 @@ void or_conv1d_silu(float* x, float* hist, const float* w, size_t conv_dim, size
     }
 }
 
+void or_ssm_forward(float* y, const float* x, const float* conv1d, size_t conv1d_len,
+                    const float* ssm_a, const float* dt_bias, const float* alpha,
+                    const float* beta, size_t beta_len, const float* out_w, size_t out_len,
+                    float* state, size_t d_inner, size_t d_state, size_t d_conv) {
+    float* conv_out = (float*)calloc(d_inner ? d_inner : 1, sizeof(float));
+    float* dt = (float*)calloc(d_inner ? d_inner : 1, sizeof(float));
+    float* b_vals = (float*)calloc(d_state ? d_state : 1, sizeof(float));
+    /* Step 1 (:63-74): every tap multiplies the current input, or pass-through. */
+    if (conv1d_len == d_inner * d_conv) {
+        for (size_t i = 0; i < d_inner; ++i) {
+            float sum = 0.0f;
+            for (size_t k = 0; k < d_conv; ++k) sum += x[i] * conv1d[i * d_conv + k];
+            conv_out[i] = sum;
+        }
+    } else {
+        memcpy(conv_out, x, d_inner * sizeof(float));
+    }
+    /* dt (:85-99): softplus with cut-offs at +-20. */
+    for (size_t i = 0; i < d_inner; ++i) {
+        float sum = dt_bias[i];
+        for (size_t j = 0; j < d_inner; ++j) sum += conv_out[j] * alpha[i * d_inner + j];
+        dt[i] = sum > 20.0f ? sum : (sum < -20.0f ? 0.0f : logf(1.0f + expf(sum)));
+    }
+    /* B (:102-110) */
+    int has_b = beta_len == d_state * d_inner && d_state > 0;
+    if (has_b)
+        for (size_t s = 0; s < d_state; ++s) {
+            float sum = 0.0f;
+            for (size_t j = 0; j < d_inner; ++j) sum += conv_out[j] * beta[s * d_inner + j];
+            b_vals[s] = sum;
+        }
+    /* discretise and scan (:113-128) */
+    for (size_t s = 0; s < d_state; ++s)
+        for (size_t i = 0; i < d_inner; ++i) {
+            size_t idx = s * d_inner + i;
+            float b_val = has_b ? b_vals[s] : conv_out[i];
+            float a_discrete = expf(-dt[i] * expf(ssm_a[idx]));
+            float b_discrete = dt[i] * b_val;
+            state[idx] = a_discrete * state[idx] + b_discrete * conv_out[i];
+        }
+    /* output (:131-155) */
+    for (size_t i = 0; i < d_inner; ++i) y[i] = 0.0f;
+    if (out_len == d_inner * d_inner) {
+        for (size_t i = 0; i < d_inner; ++i) {
+            float sum = 0.0f;
+            for (size_t s = 0; s < d_state; ++s) sum += state[s * d_inner + i];
+            for (size_t j = 0; j < d_inner; ++j) y[j] += sum * out_w[j * d_inner + i];
+        }
+    } else {
+        for (size_t i = 0; i < d_inner; ++i) {
+            float sum = 0.0f;
+            for (size_t s = 0; s < d_state; ++s) sum += state[s * d_inner + i];
+            y[i] = sum;
+        }
+    }
+    free(conv_out);
+    free(dt);
+    free(b_vals);
+}
+
 /* ---- TurboQuant compressed KV (src/turboquant/mod.rs) ---------------------------------- */
 
 /* Lloyd-Max centroids for N(0,1) by bit width 1..4 (src/turboquant/mod.rs:27-40). */

@@ -109,6 +109,15 @@ void or_gdn_tokens(float* out, float* state, const float* q_raw, const float* k_
 void or_rmsnorm_gated(float* o, const float* z, const float* w, size_t n_v_heads, size_t v_hd,
                       float eps);
 
+/* src/ssm/mod.rs:40-157 -- ssm_forward, one token of the Mamba-2-style scan.
+ * x, dt_bias: [d_inner]; ssm_a, state: [d_state * d_inner] (state in/out);
+ * alpha: [d_inner * d_inner]; conv1d / beta / out_w at the given lengths select
+ * the reference's branches.  y: [d_inner]. */
+void or_ssm_forward(float* y, const float* x, const float* conv1d, size_t conv1d_len,
+                    const float* ssm_a, const float* dt_bias, const float* alpha,
+                    const float* beta, size_t beta_len, const float* out_w, size_t out_len,
+                    float* state, size_t d_inner, size_t d_state, size_t d_conv);
+
 /* src/model/mod.rs:750-776 -- depthwise causal conv1d + SiLU for one token.
  * hist: [d_conv-1][conv_dim] previous inputs, oldest first (zeros at start);
  * x: [conv_dim] new input, overwritten with the activation; hist is shifted. */

@@ -63,6 +63,8 @@ def lib():
                                      _sz, _sz, _sz]),
             "or_rmsnorm_gated": (None, [_f32p, _f32p, _f32p, _sz, _sz, ctypes.c_float]),
             "or_conv1d_silu": (None, [_f32p, _f32p, _f32p, _sz, _sz]),
+            "or_ssm_forward": (None, [_f32p, _f32p, _f32p, _sz, _f32p, _f32p, _f32p, _f32p, _sz,
+                                      _f32p, _sz, _f32p, _sz, _sz, _sz]),
             "or_splitmix64_next": (ctypes.c_uint64, [_u64p]),
             "or_splitmix64_gaussian": (ctypes.c_float, [_u64p]),
             "or_tq_orthogonal": (None, [_f32p, _sz, ctypes.c_uint64]),
@@ -275,6 +277,19 @@ def rmsnorm_gated(o, z, w, eps):
     rows = o.size // (hv * dv)
     lib().or_rmsnorm_gated(_p(o), _p(zz), _p(ww), rows * hv, dv, float(eps))
     return o
+
+
+def ssm_forward(x, conv1d, ssm_a, dt_bias, alpha, beta, out_w, state, d_inner, d_state, d_conv):
+    """ssm::ssm_forward (src/ssm/mod.rs:40-157); returns (y, new state).  conv1d / beta /
+    out_w are used at their own lengths, as the reference's branches test them."""
+    x, ssm_a, dt_bias, alpha = (_f32(a) for a in (x, ssm_a, dt_bias, alpha))
+    conv1d, beta, out_w = (_f32(a) for a in (conv1d, beta, out_w))
+    st = np.array(state, dtype=np.float32, copy=True).reshape(-1)
+    y = np.zeros(d_inner, np.float32)
+    lib().or_ssm_forward(_p(y), _p(x), _p(conv1d), conv1d.size, _p(ssm_a), _p(dt_bias),
+                         _p(alpha), _p(beta), beta.size, _p(out_w), out_w.size, _p(st), d_inner,
+                         d_state, d_conv)
+    return y, st
 
 
 def conv1d_silu(x, hist, w, d_conv):

@@ -59,6 +59,8 @@ SIGNATURES = {
     "pi_compute_imrope_freqs": (_int, [_f32, _sz, _vp, _vp]),
     "pi_ssm_gated_delta_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
                                        _i32]),
+    "pi_ssm_forward": (_int, [_vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp,
+                              _sz, _sz, _sz]),
     "pi_attn_layer_create": (_int, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _f32, _i32,
                                     _f32, _vp, _i32, ctypes.POINTER(_vp)]),
     "pi_attn_layer_create_dims": (_int, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp,

@@ -949,6 +949,67 @@ int pi_ssm_gated_delta_step(pi_handle h, float* h_out, float* h_state, const flo
     return PI_OK;
 }
 
+int pi_ssm_forward(pi_handle h, float* h_y, const float* h_x, const float* h_conv1d,
+                   size_t conv1d_len, const float* h_ssm_a, const float* h_dt_bias,
+                   const float* h_alpha, const float* h_beta, size_t beta_len,
+                   const float* h_out_w, size_t out_len, float* h_state, size_t d_inner,
+                   size_t d_state, size_t d_conv) {
+    PI_CHECK_HANDLE(h);
+    const char* fn = "ssm_forward";
+    if (!h_y || !h_x || !h_ssm_a || !h_dt_bias || !h_alpha || !h_state ||
+        (conv1d_len && !h_conv1d) || (beta_len && !h_beta) || (out_len && !h_out_w))
+        return fail(h, PI_ERR_INVALID_ARG, "%s: null slice", fn);
+    if (d_inner == 0 || d_inner > (1u << 16) || d_state > (1u << 16) || d_conv > (1u << 16))
+        return fail(h, PI_ERR_INVALID_ARG, "%s: d_inner=%zu d_state=%zu d_conv=%zu", fn, d_inner,
+                    d_state, d_conv);
+    // src/ssm/mod.rs:63,101,131 pick the branches by slice length
+    const bool has_conv = conv1d_len == d_inner * d_conv;
+    const bool has_b = d_state > 0 && beta_len == d_state * d_inner;
+    const bool has_out = out_len == d_inner * d_inner;
+    const size_t ns = d_state * d_inner, na = d_inner * d_inner;
+    const size_t nc = has_conv ? conv1d_len : 0, nb = has_b ? beta_len : 0, no = has_out ? out_len : 0;
+    PI_HIP(h, hipSetDevice(h->device), fn);
+    // inputs: x, conv, a, dt_bias, alpha, beta, out_w, state; outputs y; scratch 3 d_inner + d_state
+    const size_t need = d_inner + nc + ns + d_inner + na + nb + no + ns + d_inner + 3 * d_inner + d_state;
+    float* d;
+    int rc = stage_in(h, need, &d);
+    if (rc) return rc;
+    pi::SsmArgs a{};
+    float* p = d;
+    auto take = [&](size_t n) { float* r = p; p += n; return r; };
+    float *dx = take(d_inner), *dw = take(nc), *da = take(ns), *ddt = take(d_inner),
+          *dal = take(na), *dbe = take(nb), *dow = take(no), *dst = take(ns), *dy = take(d_inner);
+    a.conv_out = take(d_inner);
+    a.dt = take(d_inner);
+    a.colsum = take(d_inner);
+    a.bv = take(d_state);
+    const struct { float* dst; const float* src; size_t n; } ins[] = {
+        {dx, h_x, d_inner}, {dw, h_conv1d, nc}, {da, h_ssm_a, ns}, {ddt, h_dt_bias, d_inner},
+        {dal, h_alpha, na}, {dbe, h_beta, nb}, {dow, h_out_w, no}, {dst, h_state, ns}};
+    for (const auto& c : ins)
+        if ((rc = copy_sync(h, c.dst, c.src, c.n * 4, hipMemcpyHostToDevice, fn))) return rc;
+    a.x = dx;
+    a.conv_w = dw;
+    a.a = da;
+    a.dt_bias = ddt;
+    a.alpha = dal;
+    a.beta = dbe;
+    a.out_w = dow;
+    a.state = dst;
+    a.y = dy;
+    a.d_inner = (int32_t)d_inner;
+    a.d_state = (int32_t)d_state;
+    a.d_conv = (int32_t)d_conv;
+    a.has_conv = has_conv;
+    a.has_b = has_b;
+    a.has_out = has_out;
+    PI_HIP(h, pi::launch_ssm_forward(a, h->stream), fn);
+    if ((rc = copy_sync(h, h_y, dy, d_inner * 4, hipMemcpyDeviceToHost, fn))) return rc;
+    if ((rc = copy_sync(h, h_state, dst, ns * 4, hipMemcpyDeviceToHost, fn))) return rc;
+    PI_HIP(h, hipStreamSynchronize(h->stream), fn);
+    return PI_OK;
+}
+
 // ---- attention layer cache ------------------------------------------------------------
 
 namespace {

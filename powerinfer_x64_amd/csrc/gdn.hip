@@ -394,6 +394,99 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// ssm::ssm_forward (src/ssm/mod.rs:40-157): the Mamba-2-style selective scan of
+// one token, which the reference keeps beside the gated-DeltaNet path.  Four
+// launches: the conv taps (or the pass-through), one wavefront per row of the
+// dt (alpha) and B (beta) projections, one thread per state column for the
+// discretised update and its column sum, one wavefront per row of the output
+// projection.  Which branches apply follows the reference's slice-length tests
+// (has_conv, has_b, has_out), decided on the host.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ssm_conv_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ w, int has_conv,
+                                                       float* __restrict__ conv_out, int d_inner,
+                                                       int d_conv) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= d_inner) return;
+    if (has_conv) {  // :63-70, every tap on the current input
+        float sum = 0.f;
+        for (int t = 0; t < d_conv; ++t) sum += x[i] * w[(size_t)i * d_conv + t];
+        conv_out[i] = sum;
+    } else {  // :71-74
+        conv_out[i] = x[i];
+    }
+}
+
+// rows [0, d_inner): dt_i = softplus(dt_bias_i + alpha_i . conv_out) with the
+// reference's +-20 cut-offs (:85-99); rows [d_inner, d_inner + d_state) when
+// has_b: B_s = beta_s . conv_out (:102-110).
+__global__ __launch_bounds__(256) void ssm_proj_kernel(const float* __restrict__ conv_out,
+                                                       const float* __restrict__ alpha,
+                                                       const float* __restrict__ dt_bias,
+                                                       const float* __restrict__ beta,
+                                                       float* __restrict__ dt, float* __restrict__ bv,
+                                                       int n_rows, int d_inner) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n_rows) return;
+    const float* wr = row < d_inner ? alpha + (size_t)row * d_inner : beta + (size_t)(row - d_inner) * d_inner;
+    float sum = 0.f;
+    for (int j = lane; j < d_inner; j += 64) sum += conv_out[j] * wr[j];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sum = wave_sum_xor(sum, m);
+    if (lane != 0) return;
+    if (row < d_inner) {
+        const float z = dt_bias[row] + sum;
+        dt[row] = z > 20.0f ? z : z < -20.0f ? 0.0f : logf(1.0f + expf(z));
+    } else {
+        bv[row - d_inner] = sum;
+    }
+}
+
+// state[s][i] = exp(-dt_i exp(A[s][i])) state[s][i] + (dt_i B) conv_out_i with
+// B = B_s (has_b) or conv_out_i (:113-128); colsum_i = sum_s state[s][i].
+__global__ __launch_bounds__(256) void ssm_scan_kernel(const float* __restrict__ conv_out,
+                                                       const float* __restrict__ a,
+                                                       const float* __restrict__ dt,
+                                                       const float* __restrict__ bv, int has_b,
+                                                       float* __restrict__ state,
+                                                       float* __restrict__ colsum, int d_inner,
+                                                       int d_state) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= d_inner) return;
+    const float dti = dt[i], ci = conv_out[i];
+    float sum = 0.f;
+    for (int st = 0; st < d_state; ++st) {
+        const size_t idx = (size_t)st * d_inner + i;
+        const float a_d = expf(-dti * expf(a[idx]));
+        const float b_d = dti * (has_b ? bv[st] : ci);
+        const float x = a_d * state[idx] + b_d * ci;
+        state[idx] = x;
+        sum += x;
+    }
+    colsum[i] = sum;
+}
+
+// has_out: y_j = sum_i colsum_i out[j][i] (:131-145); else y_i = colsum_i (:146-155).
+__global__ __launch_bounds__(256) void ssm_out_kernel(const float* __restrict__ colsum,
+                                                      const float* __restrict__ w, int has_out,
+                                                      float* __restrict__ y, int d_inner) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= d_inner) return;
+    if (!has_out) {
+        if (lane == 0) y[row] = colsum[row];
+        return;
+    }
+    const float* wr = w + (size_t)row * d_inner;
+    float sum = 0.f;
+    for (int i = lane; i < d_inner; i += 64) sum += colsum[i] * wr[i];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sum = wave_sum_xor(sum, m);
+    if (lane == 0) y[row] = sum;
+}
+
+// ---------------------------------------------------------------------------
 // Chunked prefill.  For a chunk of C = 64 tokens of one V head, with q/k
 // normalised, gamma_i = exp(lg_i), lg = inclusive cumsum of g over the chunk
 // and S the state entering the chunk, the per-token recurrence above equals
@@ -1062,6 +1155,21 @@ hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, con
                                 v_hd, s);
     hipLaunchKernelGGL(gdn_decode_kernel, dim3(DV / DCOLS, n_v_heads, batch), dim3(256), 0, s, q, k,
                        v, beta, g, state, out, n_k_heads, n_v_heads);
+    return hipGetLastError();
+}
+
+hipError_t launch_ssm_forward(const SsmArgs& a, hipStream_t s) {
+    if (a.d_inner <= 0 || a.d_state < 0 || a.d_conv < 0) return hipErrorInvalidValue;
+    const unsigned g1 = (unsigned)((a.d_inner + 255) / 256);
+    hipLaunchKernelGGL(ssm_conv_kernel, dim3(g1), dim3(256), 0, s, a.x, a.conv_w, a.has_conv,
+                       a.conv_out, a.d_inner, a.d_conv);
+    const int n_rows = a.d_inner + (a.has_b ? a.d_state : 0);
+    hipLaunchKernelGGL(ssm_proj_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0, s,
+                       a.conv_out, a.alpha, a.dt_bias, a.beta, a.dt, a.bv, n_rows, a.d_inner);
+    hipLaunchKernelGGL(ssm_scan_kernel, dim3(g1), dim3(256), 0, s, a.conv_out, a.a, a.dt, a.bv,
+                       a.has_b, a.state, a.colsum, a.d_inner, a.d_state);
+    hipLaunchKernelGGL(ssm_out_kernel, dim3((unsigned)((a.d_inner + 3) / 4)), dim3(256), 0, s,
+                       a.colsum, a.out_w, a.has_out, a.y, a.d_inner);
     return hipGetLastError();
 }
 

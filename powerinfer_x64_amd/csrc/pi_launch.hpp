@@ -171,6 +171,16 @@ hipError_t launch_gdn_recur(const float* q, const float* k, const float* v, cons
                             int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd, int32_t v_hd,
                             hipStream_t s);
 
+// ssm::ssm_forward of one token (src/ssm/mod.rs:40-157) on device buffers;
+// has_* are the reference's slice-length tests, decided by the caller.
+struct SsmArgs {
+    const float *x, *conv_w, *a, *dt_bias, *alpha, *beta, *out_w;
+    float *state, *y;
+    float *conv_out, *dt, *bv, *colsum;  // scratch: d_inner, d_inner, d_state, d_inner floats
+    int32_t d_inner, d_state, d_conv, has_conv, has_b, has_out;
+};
+hipError_t launch_ssm_forward(const SsmArgs& a, hipStream_t s);
+
 struct GdnWorkspace {
     float* buf;
     size_t capacity;  // floats

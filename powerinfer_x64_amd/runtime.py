@@ -570,6 +570,29 @@ def gdn_prefill(dev: Device, q, k, v, beta, g, state, out=None, chunk: int = 64)
     return out
 
 
+def ssm_forward(dev: Device, x, ssm_conv1d, ssm_a, ssm_dt_bias, ssm_alpha, ssm_beta, ssm_out,
+                state: np.ndarray, d_inner: int, d_state: int, d_conv: int) -> np.ndarray:
+    """ssm::ssm_forward (src/ssm/mod.rs:40-157) on host slices, computed on the GPU: returns
+    y [d_inner] and updates `state` (float32 [d_state * d_inner], C-contiguous) in place.
+    ssm_conv1d, ssm_beta and ssm_out pick the reference's branches by their lengths."""
+    f = lambda a: np.ascontiguousarray(np.asarray(a, np.float32).reshape(-1))  # noqa: E731
+    x, w, a, bias, alpha, beta, out_w = (f(v) for v in (x, ssm_conv1d, ssm_a, ssm_dt_bias,
+                                                        ssm_alpha, ssm_beta, ssm_out))
+    if (not isinstance(state, np.ndarray) or state.dtype != np.float32 or
+            not state.flags.c_contiguous or state.size != d_state * d_inner):
+        raise InvalidArg(f"state: expected C-contiguous float32 of {d_state * d_inner} values")
+    for name, arr, n in (("x", x, d_inner), ("ssm_dt_bias", bias, d_inner),
+                         ("ssm_a", a, d_state * d_inner), ("ssm_alpha", alpha, d_inner * d_inner)):
+        if arr.size != n:
+            raise InvalidArg(f"{name}: expected {n} values, got {arr.size}")
+    y = np.empty(d_inner, np.float32)
+    vp = lambda arr: arr.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    dev.check(dev.lib.pi_ssm_forward(dev.h, vp(y), vp(x), vp(w), w.size, vp(a), vp(bias),
+                                     vp(alpha), vp(beta), beta.size, vp(out_w), out_w.size,
+                                     vp(state), d_inner, d_state, d_conv))
+    return y
+
+
 def attention_head(dev: Device, q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
                    seq_len: int, head_dim: int) -> np.ndarray:
     """ops::attention_head (src/ops.rs:213-247) on host slices, computed on the GPU."""

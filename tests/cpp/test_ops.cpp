@@ -174,6 +174,38 @@ static void test_gated_delta_zero_state() {
     }
 }
 
+// src/ssm/mod.rs:176-231, the reference's ssm_forward tests, on the device.
+static void test_ssm_forward() {
+    {
+        const size_t d_inner = 4, d_state = 2, d_conv = 4;
+        const std::vector<float> x = {1, 2, 3, 4}, conv(d_inner * d_conv, 0.1f),
+                                 a(d_state * d_inner, -0.5f), dt_bias(d_inner, 0.0f),
+                                 alpha(d_inner * d_inner, 0.1f), beta(d_state * d_inner, 0.1f),
+                                 out(d_inner * d_inner, 0.1f);
+        auto state = ssm::create_ssm_state(d_state, d_inner);
+        const auto y = ssm::ssm_forward(x, conv, a, dt_bias, alpha, beta, out, state, d_inner,
+                                        d_state, d_conv);
+        CHECK(y.size() == d_inner);
+        for (float v : y) CHECK(std::isfinite(v));
+        bool moved = false;
+        for (float s : state) moved |= s != 0.0f;
+        CHECK(moved);
+    }
+    {
+        const size_t d_inner = 8, d_state = 4, d_conv = 4;
+        const std::vector<float> x(d_inner, 1.0f), conv(d_inner * d_conv, 0.2f),
+                                 a(d_state * d_inner, -1.0f), dt_bias(d_inner, 0.5f),
+                                 alpha(d_inner * d_inner, 0.1f), beta(d_state * d_inner, 0.1f),
+                                 out(d_inner * d_inner, 0.05f), x2(d_inner, 2.0f);
+        auto state = ssm::create_ssm_state(d_state, d_inner);
+        const auto y1 = ssm::ssm_forward(x, conv, a, dt_bias, alpha, beta, out, state, d_inner,
+                                         d_state, d_conv);
+        const auto y2 = ssm::ssm_forward(x2, conv, a, dt_bias, alpha, beta, out, state, d_inner,
+                                         d_state, d_conv);
+        CHECK(y1 != y2);
+    }
+}
+
 // Size mismatches raise InvalidArgument, as the reference's debug_assert_eq! would panic.
 static void test_size_checks() {
     float x[4] = {1, 2, 3, 4}, w[3] = {1, 1, 1}, out[4];
@@ -201,6 +233,7 @@ int main() {
     run("smoke::attention_head", test_smoke_attention);
     run("ops::compute_imrope_freqs + apply_rope_with_freqs", test_imrope_freqs);
     run("ssm::gated_delta_step zero state", test_gated_delta_zero_state);
+    run("ssm::ssm_forward", test_ssm_forward);
     run("size checks", test_size_checks);
     std::printf("%d failed\n", g_failed);
     return g_failed ? 1 : 0;

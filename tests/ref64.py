@@ -87,3 +87,24 @@ def gdn_chunk_wy(q, k, v, beta, g, S0):
     O = np.exp(lg)[:, None] * (q @ S0) + (M * (q @ k.T)) @ delta
     S = np.exp(lg[-1]) * S0 + k.T @ (np.exp(lg[-1] - lg)[:, None] * delta)
     return O, S
+
+
+def ssm_forward(x, conv1d, a, dt_bias, alpha, beta, out_w, state, d_inner, d_state, d_conv):
+    """Mamba-2-style selective scan of one token in float64 matrix form: conv taps as a
+    row-sum scale, dt = softplus(bias + alpha u) (0 below -20, identity above 20),
+    S = exp(-dt * exp(A)) * S + dt B u, y = W^T-free projection of the column sums."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(conv1d, np.float64)
+    u = x * w.reshape(d_inner, d_conv).sum(axis=1) if w.size == d_inner * d_conv else x.copy()
+    z = np.asarray(dt_bias, np.float64) + np.asarray(alpha, np.float64).reshape(d_inner, d_inner) @ u
+    dt = np.where(z > 20, z, np.where(z < -20, 0.0, np.log1p(np.exp(np.minimum(z, 20)))))
+    b = np.asarray(beta, np.float64)
+    bvals = (b.reshape(d_state, d_inner) @ u)[:, None] if (d_state and b.size == d_state * d_inner) \
+        else u[None, :]
+    S = np.asarray(state, np.float64).reshape(d_state, d_inner)
+    A = np.asarray(a, np.float64).reshape(d_state, d_inner)
+    S = np.exp(-dt[None, :] * np.exp(A)) * S + dt[None, :] * bvals * u[None, :]
+    col = S.sum(axis=0)
+    o = np.asarray(out_w, np.float64)
+    y = o.reshape(d_inner, d_inner) @ col if o.size == d_inner * d_inner else col
+    return y, S.reshape(-1)

@@ -18,7 +18,7 @@ def test_reference_op_tests_on_gpu():
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "FAIL" not in r.stdout
-    assert r.stdout.count("PASS") == 8
+    assert r.stdout.count("PASS") == 9
 
 
 def test_device_layer_cache_cpp():

@@ -406,6 +406,63 @@ def test_gdn_mistake_readout_before_update_detected(orc):
     np.testing.assert_allclose(out[0, 0], s1[0].T.astype(np.float64) @ qp[0], atol=1e-6)
 
 
+# ---- src/ssm/mod.rs ssm_forward ------------------------------------------------
+
+def test_ssm_forward_reference_tests(orc):
+    """The reference's own tests (src/ssm/mod.rs:176-231): finite outputs, the state moves
+    off zero, and a second input gives a different output from the carried state."""
+    d_inner, d_state, d_conv = 4, 2, 4
+    y, st = orc.ssm_forward([1, 2, 3, 4], [0.1] * 16, [-0.5] * 8, [0.0] * 4, [0.1] * 16,
+                            [0.1] * 8, [0.1] * 16, np.zeros(8), d_inner, d_state, d_conv)
+    assert y.shape == (4,) and np.isfinite(y).all() and (st != 0).any()
+    d_inner, d_state = 8, 4
+    args = ([0.2] * 32, [-1.0] * 32, [0.5] * 8, [0.1] * 64, [0.1] * 32, [0.05] * 64)
+    y1, st = orc.ssm_forward([1.0] * 8, *args, np.zeros(32), d_inner, d_state, d_conv)
+    y2, _ = orc.ssm_forward([2.0] * 8, *args, st, d_inner, d_state, d_conv)
+    assert not np.array_equal(y1, y2)
+
+
+@pytest.mark.parametrize("branches", ["all", "no_conv", "no_b", "no_out", "none"])
+def test_ssm_forward_f64(orc, branches):
+    """Random inputs through each slice-length branch against the float64 matrix form."""
+    rng = np.random.default_rng(len(branches))
+    d_inner, d_state, d_conv = 24, 5, 4
+    x = rng.standard_normal(d_inner)
+    conv = rng.standard_normal(d_inner * d_conv) * 0.5
+    a = rng.standard_normal(d_state * d_inner) * 0.5
+    bias = rng.standard_normal(d_inner)
+    alpha = rng.standard_normal(d_inner * d_inner) * 0.3
+    beta = rng.standard_normal(d_state * d_inner) * 0.3
+    out_w = rng.standard_normal(d_inner * d_inner) * 0.3
+    st0 = rng.standard_normal(d_state * d_inner)
+    if branches in ("no_conv", "none"):
+        conv = conv[:-1]
+    if branches in ("no_b", "none"):
+        beta = beta[:d_inner]
+    if branches in ("no_out", "none"):
+        out_w = out_w[:5]
+    x, conv, a, bias, alpha, beta, out_w, st0 = (np.asarray(v, np.float32) for v in
+                                                 (x, conv, a, bias, alpha, beta, out_w, st0))
+    y, st = orc.ssm_forward(x, conv, a, bias, alpha, beta, out_w, st0, d_inner, d_state, d_conv)
+    ey, est = ref64.ssm_forward(x, conv, a, bias, alpha, beta, out_w, st0, d_inner, d_state, d_conv)
+    np.testing.assert_allclose(st, est, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(y, ey, rtol=1e-4, atol=1e-4 * np.abs(ey).max())
+
+
+def test_ssm_forward_closed_form(orc):
+    """alpha = 0, A = 0, no conv taps, no B, no output projection: dt = softplus(bias) (0 under
+    -20, bias over 20), S' = exp(-dt) S + dt x^2, y = column sums."""
+    d_inner, d_state = 4, 2
+    x = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    bias = np.array([0.3, -25.0, 25.0, -1.0], np.float32)
+    st0 = np.array([1, 2, 3, 4, -1, 0.5, 0.25, 2], np.float32)
+    y, st = orc.ssm_forward(x, [], np.zeros(8), bias, np.zeros(16), [], [], st0, d_inner, d_state, 3)
+    dt = np.array([np.log1p(np.exp(0.3)), 0.0, 25.0, np.log1p(np.exp(-1.0))])
+    S = np.exp(-dt) * st0.reshape(2, 4).astype(np.float64) + dt * x.astype(np.float64) ** 2
+    np.testing.assert_allclose(st, S.reshape(-1), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(y, S.sum(axis=0), rtol=1e-6, atol=1e-6)
+
+
 def test_rmsnorm_gated_closed_form(orc):
     rng = np.random.default_rng(18)
     o = rng.standard_normal((4, 128)).astype(np.float32)
