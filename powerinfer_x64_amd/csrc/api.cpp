@@ -615,8 +615,8 @@ int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
                     start_pos, n_tok, max_pages, n_q_heads);
     if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: gqa_mode %d", gqa_mode);
-    if (g.dtype != PI_F16 || (g.head_dim != 128 && g.head_dim != 256))
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill_paged: f16 pool with head_dim 128 or 256 (dtype %d, head_dim %d)",
+    if (g.dtype == PI_F16 ? (g.head_dim != 128 && g.head_dim != 256) : g.dtype != PI_F32)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill_paged: pool dtype %d head_dim %d (f16 at 128 / 256, or f32)",
                     g.dtype, g.head_dim);
     if (gqa_mode == PI_GQA_GROUPED && n_q_heads % g.n_kv_heads != 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: grouped head map with n_q_heads %d not a multiple of n_kv_heads %d",
@@ -627,6 +627,12 @@ int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
     if (n_tok == 0) return PI_OK;
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_prefill_paged");
+    if (g.dtype == PI_F32) {  // straight from the pages, no workspace
+        PI_HIP(h, pi::launch_prefill_f32(g, static_cast<const float*>(d_q), d_page_table, max_pages,
+                                         start_pos, n_tok, n_q_heads, gqa_mode, scale, d_out, s),
+               "pi_attn_prefill_paged");
+        return PI_OK;
+    }
     int rc;
     if ((rc = ws_begin(h, s, "pi_attn_prefill_paged"))) return rc;
     const size_t rows = (size_t)n_keys * g.n_kv_heads * g.head_dim;  // f16 elements of K (and of V)
@@ -1150,6 +1156,12 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
         }
         PI_HIP(h, pi::launch_prefill(hq16, hk16, hv16, PI_F16, 1, n, prev + n, prev, L->n_heads, L->n_kv,
                                      D, 1, L->gqa_mode, scale, dout, s),
+               "attention layer");
+        if (dg) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
+    } else if (n > 1 && L->kv_dtype == PI_F32) {
+        // causal attention straight from the f32 pages, at f32 accuracy
+        PI_HIP(h, pi::launch_prefill_f32(L->pool->g, dq, L->d_pt, L->max_pages, prev, n, L->n_heads,
+                                         L->gqa_mode, scale, dout, s),
                "attention layer");
         if (dg) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
     } else {

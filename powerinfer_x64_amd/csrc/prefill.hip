@@ -475,6 +475,203 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         }
 }
 
+// ---------------------------------------------------------------------------
+// prefill_f32_kernel: causal attention of a chunk of queries (f32 rows) over an
+// f32 KV pool, read through the sequence's page table (src/model/mod.rs:668
+// token loop over :1140-1190 with an f32 cache).  Products keep f32 accuracy
+// on the bf16 MFMA by splitting each f32 operand into bf16 hi + lo parts
+// (x = hi + lo to 16 significant bits, the exponent range of f32) and summing
+// hi.hi + hi.lo + lo.hi: three v_mfma_f32_16x16x32_bf16 per block.
+//
+// A workgroup of 4 wavefronts covers 64 query rows of one query head; wave w
+// owns rows 16 w .. 16 w + 15.  Per 32-key tile (two pool pages):
+//   S^T[32 key x 16 q] = K . Q^T   (lane: query column c = lane % 16, keys 4 g + r)
+//   O^T[D x 16 q]     += V^T . P^T (P^T's contraction order matches the lane's keys)
+// K is staged in LDS as [key][dim] hi / lo rows, V as [dim][key] (the pool's V
+// block is already dim-major); the next tile's raw f32 pages are loaded into
+// registers while the current tile computes.
+// ---------------------------------------------------------------------------
+struct PrefillF32Args {
+    const float* q;         // [n_tok][hq][D], normalised and rotated
+    const float* kpool;     // f32 pool K blocks [page][hkv][D/4][16][4]
+    const float* vpool;     // f32 pool V blocks [page][hkv][D][16]
+    const int32_t* pt;      // the sequence's page-table row
+    float* out;             // [n_tok][hq][D]
+    int n_tok, q_off, max_pages, n_pages, hq, hkv, group, gqa_mode;
+    float qk_scale;         // scale * log2(e)
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillF32Args a) {
+    constexpr int TK = 32;          // keys per tile (two pages)
+    constexpr int KST = D + 8;      // K row stride (bf16)
+    constexpr int VST = TK + 4;     // V^T row stride (bf16)
+    constexpr int NF = 2 * TK * D / 4 / 256;  // float4 loads per thread per tile (K and V)
+    constexpr int NKS = D / 32;     // 32-dim steps of Q.K
+    constexpr int NDB = D / 16;     // 16-dim blocks of O^T
+    __shared__ __attribute__((aligned(16))) bf16 skh[TK * KST], skl[TK * KST];
+    __shared__ __attribute__((aligned(16))) bf16 svh[D * VST], svl[D * VST];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int qb = gridDim.x - 1 - blockIdx.x;  // heaviest (latest) query blocks first
+    const int head = blockIdx.y;
+    const int kvh = a.gqa_mode == 0 ? head % a.hkv : head / a.group;
+    const int L = a.q_off + a.n_tok;            // keys of the sequence after this chunk
+    const int p0 = qb * 64 + 16 * wave;         // this wave's first query row
+    const int wg_keys = min(L, a.q_off + qb * 64 + 64);
+    const int n_tiles = (wg_keys + TK - 1) / TK;
+    const int w_keys = min(L, a.q_off + p0 + 16);
+    const int w_tiles = p0 < a.n_tok ? (w_keys + TK - 1) / TK : 0;
+    const int qpos = p0 + c;
+
+    // Q^T operand (B of K.Q^T): lane holds q[qpos][32 ks + 8 g .. +7] as hi / lo
+    bf16x8 qh[NKS], ql[NKS];
+    {
+        const bool ok = qpos < a.n_tok;
+        const float* qr = a.q + ((size_t)(ok ? qpos : 0) * a.hq + head) * D;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            f32x4 x0 = *reinterpret_cast<const f32x4*>(qr + 32 * ks + 8 * g);
+            f32x4 x1 = *reinterpret_cast<const f32x4*>(qr + 32 * ks + 8 * g + 4);
+            if (!ok) x0 = x1 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = j < 4 ? x0[j] : x1[j - 4];
+                const bf16 h = to_bf16(x);
+                qh[ks][j] = h;
+                ql[ks][j] = to_bf16(x - (float)h);
+            }
+        }
+    }
+    f32x4 o[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -1e30f, l_run = 0.f;
+
+    // Tile loads: float4 i of a tile (i = tid + 256 j) is K (i < 8 D) or V, of
+    // page i / (4 D) % 2; within a page block both are a linear copy.
+    f32x4 pre[NF];
+    const size_t blk = (size_t)16 * D;  // floats of one (page, KV head) block
+    auto load_tile = [&](int t) {
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            const int i = tid + 256 * j;
+            const bool isv = i >= 8 * D;
+            const int ii = isv ? i - 8 * D : i;
+            const int half = ii / (4 * D), ci = ii % (4 * D);
+            const int lp = 2 * t + half;
+            const int pid = lp < a.max_pages ? a.pt[lp] : -1;
+            const bool ok = lp * 16 < L && pid >= 0 && pid < a.n_pages;
+            const float* base = (isv ? a.vpool : a.kpool) + ((size_t)(ok ? pid : 0) * a.hkv + kvh) * blk;
+            pre[j] = ok ? *reinterpret_cast<const f32x4*>(base + 4 * ci) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    auto stage_tile = [&]() {
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            const int i = tid + 256 * j;
+            const bool isv = i >= 8 * D;
+            const int ii = isv ? i - 8 * D : i;
+            const int half = ii / (4 * D), ci = ii % (4 * D);
+            bf16x4 h, l;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[e] = to_bf16(pre[j][e]);
+                l[e] = to_bf16(pre[j][e] - (float)h[e]);
+            }
+            if (!isv) {  // K block [D/4][16][4]: dims 4 (ci / 16) .. +3 of token ci % 16
+                const int off = (16 * half + ci % 16) * KST + 4 * (ci / 16);
+                *reinterpret_cast<bf16x4*>(skh + off) = h;
+                *reinterpret_cast<bf16x4*>(skl + off) = l;
+            } else {     // V block [D][16]: tokens 4 (ci % 4) .. +3 of dim ci / 4
+                const int off = (ci / 4) * VST + 16 * half + 4 * (ci % 4);
+                *reinterpret_cast<bf16x4*>(svh + off) = h;
+                *reinterpret_cast<bf16x4*>(svl + off) = l;
+            }
+        }
+    };
+    auto mma = [](bf16x8 x, bf16x8 y, f32x4 acc) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, acc, 0, 0, 0);
+    };
+    const float cs = a.qk_scale;
+    load_tile(0);
+    for (int t = 0; t < n_tiles; ++t) {
+        __syncthreads();  // the previous tile's LDS reads are done
+        stage_tile();
+        if (t + 1 < n_tiles) load_tile(t + 1);
+        __syncthreads();
+        if (t >= w_tiles) continue;
+        // S^T for keys 16 kb + 4 g + r
+        f32x4 st[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const int off = (16 * kb + c) * KST + 32 * ks + 8 * g;
+                const bf16x8 kh = *reinterpret_cast<const bf16x8*>(skh + off);
+                const bf16x8 kl = *reinterpret_cast<const bf16x8*>(skl + off);
+                acc = mma(kh, qh[ks], acc);
+                acc = mma(kh, ql[ks], acc);
+                acc = mma(kl, qh[ks], acc);
+            }
+            st[kb] = acc;
+        }
+        const int k0 = t * TK;
+        if (k0 + TK > a.q_off + p0 || k0 + TK > L) {  // the tile reaches past a row's last key
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * kb + 4 * g + r;
+                    if (key >= L || key > a.q_off + qpos) st[kb][r] = -INFINITY;
+                }
+        }
+        float mx = fmaxf(fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3])),
+                         fmaxf(fmaxf(st[1][0], st[1][1]), fmaxf(st[1][2], st[1][3])));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx * cs);
+        const float alpha = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < NDB; ++i) o[i] *= alpha;
+        // P^T operand: contraction slot 8 g + j is key 16 (j / 4) + 4 g + j % 4
+        bf16x8 ph, pl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float p = fast_exp2(__builtin_fmaf(st[j >> 2][j & 3], cs, -m_new));
+            l_run += p;
+            const bf16 h = to_bf16(p);
+            ph[j] = h;
+            pl[j] = to_bf16(p - (float)h);
+        }
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            const int off = (16 * db + c) * VST + 4 * g;
+            const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(svh + off);
+            const bf16x4 h1 = *reinterpret_cast<const bf16x4*>(svh + off + 16);
+            const bf16x4 l0 = *reinterpret_cast<const bf16x4*>(svl + off);
+            const bf16x4 l1 = *reinterpret_cast<const bf16x4*>(svl + off + 16);
+            const bf16x8 vh = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+            const bf16x8 vl = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+            o[db] = mma(vh, ph, o[db]);
+            o[db] = mma(vh, pl, o[db]);
+            o[db] = mma(vl, ph, o[db]);
+        }
+    }
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (qpos >= a.n_tok) return;
+    const float inv = 1.0f / l_run;
+    float* orow = a.out + ((size_t)qpos * a.hq + head) * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+        *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db] * inv;
+}
+
 }  // namespace
 
 namespace {
@@ -503,6 +700,37 @@ void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int ba
     }
 }
 }  // namespace
+
+hipError_t launch_prefill_f32(const KvGeom& g, const float* q, const int32_t* page_table,
+                              int32_t max_pages, int32_t q_off, int32_t n_tok, int32_t n_q_heads,
+                              int32_t gqa_mode, float scale, float* out, hipStream_t s) {
+    if (g.dtype != 0 || q_off < 0 || n_tok < 1 || max_pages < 1) return hipErrorInvalidValue;
+    const bool multiple = n_q_heads % g.n_kv_heads == 0;
+    if (!multiple && gqa_mode != 0) return hipErrorInvalidValue;
+    PrefillF32Args a;
+    a.q = q;
+    a.kpool = reinterpret_cast<const float*>(g.k);
+    a.vpool = reinterpret_cast<const float*>(g.v);
+    a.pt = page_table;
+    a.out = out;
+    a.n_tok = n_tok;
+    a.q_off = q_off;
+    a.max_pages = max_pages;
+    a.n_pages = g.n_pages;
+    a.hq = n_q_heads;
+    a.hkv = g.n_kv_heads;
+    a.group = (n_q_heads + g.n_kv_heads - 1) / g.n_kv_heads;
+    a.gqa_mode = gqa_mode;
+    a.qk_scale = scale * kLog2e;
+    const dim3 grid((unsigned)((n_tok + 63) / 64), (unsigned)n_q_heads);
+    switch (g.head_dim) {
+        case 64: hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(256), 0, s, a); break;
+        case 256: hipLaunchKernelGGL(prefill_f32_kernel<256>, grid, dim3(256), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
                           int32_t batch, int32_t seq_len, int32_t n_keys, int32_t q_off,

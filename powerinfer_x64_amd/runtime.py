@@ -498,10 +498,10 @@ def attn_prefill(dev: Device, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 def attn_prefill_paged(dev: Device, q: torch.Tensor, pool: KvPool, page_row: torch.Tensor,
                        start_pos: int, gqa_mode: int = MODULO, scale: Optional[float] = None,
                        out: Optional[torch.Tensor] = None):
-    """A chunk continuing a sequence: q [n, Hq, D] f16 at positions start_pos .. start_pos + n - 1
+    """A chunk continuing a sequence: q [n, Hq, D] at positions start_pos .. start_pos + n - 1
     over the sequence's pages (page_row: int32 [max_pages]; the chunk's K/V appended first)
-    -> out [n, Hq, D] f32."""
-    _need(q, "q", torch.float16, dev=dev.torch_device)
+    -> out [n, Hq, D] f32.  q is f16 for an f16 pool, f32 for an f32 pool."""
+    _need(q, "q", pool.dtype, dev=dev.torch_device)
     n, hq, dh = q.shape
     if dh != pool.head_dim:
         raise InvalidArg(f"q head_dim {dh} != pool head_dim {pool.head_dim}")

@@ -7,7 +7,8 @@ P is or_attn_decode over keys 0 .. P + i.  Keys are drawn raw, normalised / rota
 positions and appended to a pool with permuted pages on the GPU; the oracle prepares the
 same raw rows (or_attn_prepare) and reads them rounded to f16 as the pool stores them; the
 chunk's queries are rotated at P .. and rounded to f16 (the kernel's input).  Tolerance:
-1e-2 relative per (token, head) row (f16 class); argmax of synthetic logits exact.
+1e-2 relative per (token, head) row (f16 class); argmax of synthetic logits exact.  With an
+f32 pool nothing is rounded and the bound is max-abs 2e-3 (f32 class).
 """
 import numpy as np
 import pytest
@@ -38,25 +39,27 @@ class Chunk:
         self.qn = rng.uniform(0.5, 1.5, d).astype(np.float32) if norm else None
         self.kn = rng.uniform(0.5, 1.5, d).astype(np.float32) if norm else None
 
-    def prepared(self):
-        """Rotated q (f16-rounded) and K (f16-rounded), V (f16-rounded), as f32."""
+    def prepared(self, f32=False):
+        """Rotated q and K, and V, rounded to f16 (f16 pool) or not (f32 pool), as f32."""
         kw = dict(eps=1e-6, rope_dim=self.rope_dim, rope_base=self.theta, freqs=self.freqs)
         _, kr = orc.attn_prepare(None, self.k, self.hq, self.hkv, self.d, k_norm_w=self.kn,
                                  pos0=0, **kw)
         qr, _ = orc.attn_prepare(self.q, None, self.hq, self.hkv, self.d, q_norm_w=self.qn,
                                  pos0=self.prev, **kw)
+        if f32:
+            return qr, kr, self.v
         r = lambda a: a.astype(np.float16).astype(np.float32)  # noqa: E731
         return r(qr), r(kr), r(self.v)
 
-    def oracle(self, rows):
-        q, k, v = self.prepared()
+    def oracle(self, rows, f32=False):
+        q, k, v = self.prepared(f32)
         p = self.prev
         return np.stack(parallel_map(lambda i: orc.attn_decode(q[i], k[:p + i + 1], v[:p + i + 1]),
                                      list(rows)))
 
-    def gpu(self, dev, gqa_mode=0):
+    def gpu(self, dev, gqa_mode=0, pool_dtype=torch.float16):
         from powerinfer_x64_amd import runtime as rt
-        pool = rt.KvPool(dev, self.n_pages, self.hkv, self.d, dtype=torch.float16)
+        pool = rt.KvPool(dev, self.n_pages, self.hkv, self.d, dtype=pool_dtype)
         row = to_dev(self.row)
         q, k, v = to_dev(self.q), to_dev(self.k), to_dev(self.v)
         # the prologue's steps: norm, RoPE at the positions, append
@@ -70,8 +73,8 @@ class Chunk:
                 self.rope_dim, self.theta, self.sections)
         pool.append(k[None].contiguous(), v[None].contiguous(), row[None].contiguous(),
                     torch.zeros(1, dtype=torch.int32, device="cuda"))
-        out = rt.attn_prefill_paged(dev, q.half().contiguous(), pool, row, self.prev,
-                                    gqa_mode=gqa_mode)
+        qin = q.half().contiguous() if pool_dtype == torch.float16 else q
+        out = rt.attn_prefill_paged(dev, qin, pool, row, self.prev, gqa_mode=gqa_mode)
         torch.cuda.synchronize()
         self.pool, self.row_dev, self.q16 = pool, row, q.half().contiguous()
         return out.cpu().numpy()
@@ -83,6 +86,52 @@ def _check(out, ref, what):
     print(f"\n{what}: worst row rel err {err:.3e}, argmax mismatches {mism}/{n} ({ties} ties)")
     assert err <= 1e-2, f"{what}: rel err {err}"
     assert mism == 0, f"{what}: {mism} argmax mismatches"
+
+
+def _check_f32(out, ref, what):
+    err = float(np.abs(out - ref).max())
+    n, mism, ties = argmax_agreement(out, ref)
+    print(f"\n{what}: max-abs {err:.3e}, argmax mismatches {mism}/{n} ({ties} ties)")
+    assert err <= 2e-3, f"{what}: max-abs {err}"
+    assert mism == 0, f"{what}: {mism} argmax mismatches"
+
+
+@pytest.mark.parametrize("prev,n,hq,hkv,d", [(0, 300, 32, 32, 128), (700, 150, 32, 8, 128),
+                                             (33, 129, 10, 4, 64), (1000, 65, 16, 2, 256),
+                                             (4095, 1, 8, 8, 128), (17, 2, 4, 1, 64)])
+def test_paged_prefill_f32_pool(prev, n, hq, hkv, d):
+    """An f32 pool: a fresh prompt (prev 0, config-1 heads), continued chunks at tile and
+    non-tile offsets, modulo heads that are not a multiple, D 64 / 128 / 256."""
+    dev = device()
+    c = Chunk(np.random.default_rng(prev * 7 + n + d), prev, n, hq, hkv, d)
+    out = c.gpu(dev, pool_dtype=torch.float32)
+    _check_f32(out, c.oracle(range(n), f32=True), f"f32 prev {prev} + {n} D {d}")
+
+
+def test_paged_prefill_f32_grouped_d256_norm():
+    """f32 pool, 16/2 heads, D 256, q/k norm and IMRoPE, grouped head map."""
+    dev = device()
+    c = Chunk(np.random.default_rng(0xF32), 300, 100, 16, 2, 256, theta=1e7, rope_dim=64,
+              sections=[11, 11, 10, 0], norm=True)
+    out = c.gpu(dev, gqa_mode=1, pool_dtype=torch.float32)
+    q, k, v = c.prepared(f32=True)
+    perm = [(h % 8) * 2 + h // 8 for h in range(16)]
+
+    def row(i):
+        qq = np.empty_like(q[i])
+        qq[perm] = q[i]
+        return orc.attn_decode(qq, k[:c.prev + i + 1], v[:c.prev + i + 1])[perm]
+    _check_f32(out, np.stack(parallel_map(row, range(c.n))), "f32 D 256 grouped")
+
+
+def test_paged_prefill_f32_1024_over_8k_history():
+    """A 1024-token chunk over an 8192-token history with an f32 pool (config-1 heads at
+    config-2's GQA): sampled rows across the chunk."""
+    dev = device()
+    c = Chunk(np.random.default_rng(0xF8192), 8192, 1024, 32, 8, 128)
+    out = c.gpu(dev, pool_dtype=torch.float32)
+    rows = [0, 1, 31, 32, 63, 64, 1000, 1023] + list(np.random.default_rng(4).integers(0, 1024, 16))
+    _check_f32(out[rows], c.oracle(rows, f32=True), "f32 1024 over 8192")
 
 
 @pytest.mark.parametrize("prev,n", [(700, 300), (64, 64), (1000, 2), (4095, 1), (33, 129)])
@@ -150,8 +199,11 @@ def test_paged_prefill_rejects_bad_shapes():
     with pytest.raises(rt.InvalidArg):  # 120 + 10 keys > 8 pages of 16
         rt.attn_prefill_paged(dev, q, pool, row, 120)
     pool32 = rt.KvPool(dev, 8, 2, 128, dtype=torch.float32)
-    with pytest.raises(rt.Unsupported):
+    with pytest.raises(rt.InvalidArg):  # an f32 pool takes f32 queries
         rt.attn_prefill_paged(dev, q, pool32, row, 0)
+    pool64 = rt.KvPool(dev, 8, 2, 64, dtype=torch.float16)
+    with pytest.raises(rt.Unsupported):  # the f16 flash prefill runs D 128 / 256
+        rt.attn_prefill_paged(dev, q[:, :, :64].contiguous(), pool64, row, 0)
 
 
 def test_layer_forward_dev_equals_host_slices():
