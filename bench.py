@@ -39,6 +39,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+MFMA_F32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA
 PAGE = 16
 
 
@@ -994,6 +995,25 @@ def bench_chunk(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
         res["c2_prefill_paged_1024_over_8192"]["cpu_baseline"] = _cpu(
             fl_done / t / 1e12, "TFLOP/s", f"or_attn_decode on rows {n - 1}, {n - 98}, ... of the "
             f"chunk over their {hist}+ keys", round(t, 3), parity_max_row_rel_err=round(err, 6))
+    pool.close()
+
+    # the f32-cache prefill straight from the pages: config-1 heads (32/32, D 128, f32 cache),
+    # 1024 queries over 8192 + 1024 keys, f32-accurate products (bf16 hi / lo splits)
+    hq, hkv = 32, 32
+    pool = rt.KvPool(dev, pages + 8, hkv, d, torch.float32)
+    k = rnd(hist + n, hkv, d)
+    v = rnd(hist + n, hkv, d)
+    pool.append(k[None], v[None], row[None].contiguous(), torch.zeros(1, dtype=torch.int32, device="cuda"))
+    q32 = rnd(n, hq, d)
+    o = torch.empty((n, hq, d), device="cuda")
+    args = (dev.h, P(q32), pool.p, P(row), pages, hist, n, hq, 0, 1.0 / math.sqrt(d), P(o), None)
+    r = timer.run(_lib_fn(dev, dev.lib.pi_attn_prefill_paged, args), steps, warmup)
+    fl = 4.0 * hq * d * n * (hist + (n + 1) / 2)
+    tf = fl / (r["ms_avg"] * 1e-3) / 1e12
+    res["c1_prefill_paged_f32_1024_over_8192"] = {
+        "TFLOP_s": tf, "mfma_frac_bf16_peak": tf / MFMA_F16_PEAK_TFLOPS,
+        "vs_f32_mfma_peak": tf / MFMA_F32_PEAK_TFLOPS, "ms_per_step": r["ms_avg"],
+        "flops_per_launch": fl}
     pool.close()
     return res
 

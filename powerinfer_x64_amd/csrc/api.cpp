@@ -780,7 +780,8 @@ int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const flo
     int rc = pi_kv_pool_create(h, n_pages, 16, 1, (int)pd, PI_F32, &pool);
     if (rc) return rc;
     const size_t kv = seq_len * pd;
-    const size_t need = 2 * kv + 2 * pd + (size_t)n_pages + 2;
+    const size_t raw = pd == head_dim ? 0 : seq_len * head_dim;  // unpadded rows, copied whole
+    const size_t need = 2 * kv + 2 * pd + (size_t)n_pages + 2 + 2 * raw;
     rc = grow(h, &h->h2d_scratch, &h->h2d_floats, need, s, "attention_head staging", false);
     if (rc) {
         pi_kv_pool_destroy(pool);
@@ -792,6 +793,8 @@ int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const flo
     float* dout = dq + pd;
     int32_t* dpt = reinterpret_cast<int32_t*>(dout + pd);
     int32_t* dmeta = dpt + n_pages;  // [start_pos=0, ctx_len]
+    float* rk = reinterpret_cast<float*>(dmeta + 2);
+    float* rv = rk + raw;
     int32_t* hpt = new (std::nothrow) int32_t[n_pages + 2];
     if (!hpt) {
         pi_kv_pool_destroy(pool);
@@ -802,8 +805,15 @@ int pi_ops_attention_head(pi_handle h, float* h_out, const float* h_q, const flo
     hpt[n_pages + 1] = (int32_t)seq_len;
     const size_t rb = head_dim * 4, pb = pd * 4;
     hipError_t e = hipMemsetAsync(dk, 0, (2 * kv + pd) * 4, s);
-    if (e == hipSuccess && kv) e = hipMemcpy2DAsync(dk, pb, h_k_cache, rb, rb, seq_len, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess && kv) e = hipMemcpy2DAsync(dv, pb, h_v_cache, rb, rb, seq_len, hipMemcpyHostToDevice, s);
+    if (kv && !raw) {
+        if (e == hipSuccess) e = hipMemcpyAsync(dk, h_k_cache, kv * 4, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipMemcpyAsync(dv, h_v_cache, kv * 4, hipMemcpyHostToDevice, s);
+    } else if (kv) {  // one host copy per cache, then rows padded on the device
+        if (e == hipSuccess) e = hipMemcpyAsync(rk, h_k_cache, raw * 4, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipMemcpyAsync(rv, h_v_cache, raw * 4, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipMemcpy2DAsync(dk, pb, rk, rb, rb, seq_len, hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess) e = hipMemcpy2DAsync(dv, pb, rv, rb, rb, seq_len, hipMemcpyDeviceToDevice, s);
+    }
     if (e == hipSuccess) e = hipMemcpyAsync(dq, h_q, rb, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(dpt, hpt, (n_pages + 2) * 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -1218,16 +1228,41 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_layer_forward");
     const int D = L->dim;
     const size_t nq = (size_t)n_tokens * L->n_heads * D, nk = (size_t)n_tokens * L->n_kv * D;
-    int rc = grow(h, &L->d_buf, &L->buf_floats, 3 * nq + 2 * nk, s, "pi_attn_layer_forward staging", false);
+    // distinct widths: the host slices arrive whole (one copy each) in a raw region and
+    // are packed on the device (2D copies from pageable memory would go row by row)
+    const bool packed = L->q_dim == D && L->v_dim == D;
+    const size_t rq = packed ? 0 : (size_t)n_tokens * L->n_heads * L->q_dim;
+    const size_t rv = packed ? 0 : (size_t)n_tokens * L->n_kv * L->v_dim;
+    int rc = grow(h, &L->d_buf, &L->buf_floats, 3 * nq + 2 * nk + 2 * rq + rv, s,
+                  "pi_attn_layer_forward staging", false);
     if (rc) return rc;
     float *dq = L->d_buf, *dg = dq + nq, *dout = dg + nq, *dk = dout + nq, *dv = dk + nk;
+    float *raw_q = dv + nk, *raw_g = raw_q + rq, *raw_v = raw_g + rq;
     const char* what = "pi_attn_layer_forward";
-    if ((rc = pack_layer_inputs(h, L, h_q, h_v, h_gate, n_tokens, dq, dv, dg, hipMemcpyHostToDevice, s, what))) return rc;
+    if (packed) {
+        if ((rc = copy_sync(h, dq, h_q, nq * 4, hipMemcpyHostToDevice, what))) return rc;
+        if ((rc = copy_sync(h, dv, h_v, nk * 4, hipMemcpyHostToDevice, what))) return rc;
+        if (h_gate && (rc = copy_sync(h, dg, h_gate, nq * 4, hipMemcpyHostToDevice, what))) return rc;
+    } else {
+        if ((rc = copy_sync(h, raw_q, h_q, rq * 4, hipMemcpyHostToDevice, what))) return rc;
+        if ((rc = copy_sync(h, raw_v, h_v, rv * 4, hipMemcpyHostToDevice, what))) return rc;
+        if (h_gate && (rc = copy_sync(h, raw_g, h_gate, rq * 4, hipMemcpyHostToDevice, what))) return rc;
+        if ((rc = pack_layer_inputs(h, L, raw_q, raw_v, h_gate ? raw_g : nullptr, n_tokens, dq, dv, dg,
+                                    hipMemcpyDeviceToDevice, s, what)))
+            return rc;
+    }
     if ((rc = copy_sync(h, dk, h_k, nk * 4, hipMemcpyHostToDevice, what))) return rc;
     if ((rc = attn_layer_step(h, L, dq, dk, dv, h_gate ? dg : nullptr, n_tokens, dout, s))) return rc;
     if ((rc = copy_sync(h, h_out, dout, nq * 4, hipMemcpyDeviceToHost, what))) return rc;
     // q and k come back normalised and rotated (only the first head_dim dims of a query head)
-    if ((rc = copy_rows(h, h_q, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads, hipMemcpyDeviceToHost, s, what))) return rc;
+    if (packed) {
+        if ((rc = copy_sync(h, h_q, dq, nq * 4, hipMemcpyDeviceToHost, what))) return rc;
+    } else {
+        if ((rc = copy_rows(h, raw_q, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads,
+                            hipMemcpyDeviceToDevice, s, what)))
+            return rc;
+        if ((rc = copy_sync(h, h_q, raw_q, rq * 4, hipMemcpyDeviceToHost, what))) return rc;
+    }
     if ((rc = copy_sync(h, h_k, dk, nk * 4, hipMemcpyDeviceToHost, what))) return rc;
     PI_HIP(h, hipStreamSynchronize(s), what);
     return PI_OK;
