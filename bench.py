@@ -140,15 +140,19 @@ def _paged_decode_setup(torch, rt, dev, lens, hq, hkv, d, theta, seed, sections=
     return pool, tpt, ctx, q, algo
 
 
-def _decode_fn(dev, pool, tpt, ctx, q, out, gate=None):
+def _decode_fn(dev, pool, tpt, ctx, q, out, gate=None, torch=None):
+    """One pi_attn_decode call; with `torch`, on torch's current stream (as a graph capture
+    needs), else on the handle's stream."""
     lib = dev.lib
-    args = (dev.h, ctypes.c_void_p(q.data_ptr()), pool.p, ctypes.c_void_p(tpt.data_ptr()),
+    args = [dev.h, ctypes.c_void_p(q.data_ptr()), pool.p, ctypes.c_void_p(tpt.data_ptr()),
             tpt.shape[1], ctypes.c_void_p(ctx.data_ptr()), q.shape[0], q.shape[1], 0,
             1.0 / math.sqrt(q.shape[2]),
             None if gate is None else ctypes.c_void_p(gate.data_ptr()),
-            ctypes.c_void_p(out.data_ptr()), None)
+            ctypes.c_void_p(out.data_ptr()), None]
 
     def fn():
+        if torch is not None:
+            args[-1] = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         rc = lib.pi_attn_decode(*args)
         if rc:
             raise RuntimeError(lib.pi_last_error(dev.h).decode())
@@ -158,6 +162,7 @@ def _decode_fn(dev, pool, tpt, ctx, q, out, gate=None):
 def bench_decode(torch, rt, dev, timer, lens, hq, hkv, d, theta, seed, steps, warmup,
                  cpu_s=0.0, **kw):
     gate_on = kw.pop("gate", False)
+    graph = kw.pop("graph", False)
     pool, tpt, ctx, q, algo = _paged_decode_setup(torch, rt, dev, lens, hq, hkv, d, theta, seed,
                                                   **kw)
     out = torch.empty_like(q)
@@ -169,6 +174,12 @@ def bench_decode(torch, rt, dev, timer, lens, hq, hkv, d, theta, seed, steps, wa
     res = {"GB_s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "ms_per_step": t["ms_avg"],
            "ms_median": t["ms_median"], "bytes_per_launch": algo,
            "tokens": int(sum(int(x) for x in lens))}
+    if graph:
+        # the same call (decode + merge kernels) replayed from a captured graph of 64 calls:
+        # what a serving loop that launches its layers from graphs pays per step
+        us = graph_us_per_call(torch, _decode_fn(dev, pool, tpt, ctx, q, out, gate, torch=torch))
+        res.update({"us_per_step_graph": us, "GB_s_graph": algo / us / 1e3,
+                    "hbm_frac_graph": algo / us / 1e3 / HBM_PEAK_GBS})
     if cpu_s > 0:
         torch.cuda.synchronize()
         qh, oh = q.cpu().numpy(), out.cpu().numpy()
@@ -1064,7 +1075,7 @@ def _single(torch, rt, dev, timer, a):
                             gate=True)[0]
     if w == "c1":
         return bench_decode(torch, rt, dev, timer, [513], 32, 32, 128, 1e4, 0x5EED0000, st, wu,
-                            pool_dtype=torch.float32)[0]
+                            pool_dtype=torch.float32, graph=True)[0]
     if w == "c3":
         return bench_prefill(torch, rt, dev, timer, 4096, 32, 8, 128, 1e6, 0x5EED0002, st, wu)
     if w == "gdn_prefill":
@@ -1176,7 +1187,8 @@ def main():
         torch.cuda.empty_cache()
         wl["c4_gated_decode_64k"] = r4
         r1, st = bench_decode(torch, rt, dev, timer, [513], 32, 32, 128, 1e4, 0x5EED0000,
-                              a.steps, a.warmup, pool_dtype=torch.float32, cpu_s=budget["c1"])
+                              a.steps, a.warmup, pool_dtype=torch.float32, cpu_s=budget["c1"],
+                              graph=True)
         del st
         wl["c1_mha_decode_513"] = r1
         wl["c5_gdn_decode_step"] = bench_gdn_decode(torch, rt, dev, timer, a.steps, a.warmup,

@@ -584,7 +584,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     const int cols = p.cols, GD = cols * D;
     const int e0 = blockIdx.x * 256;
     const size_t seg = (size_t)b * n_seg + sidx;
-    if (sched::seq_tokens(p.ctx_len[b], p.max_pages) == 0) {
+    // The context length and the run table load together: a merge is a short chain of
+    // dependent memory round trips, so every load that can is issued beside another.
+    const int ctx = p.ctx_len[b];
+    const int wg1 = ws.seg_runs[2 * seg], n_runs_raw = ws.seg_runs[2 * seg + 1];
+    if (sched::seq_tokens(ctx, p.max_pages) == 0) {
         // empty context: softmax over nothing leaves zeros (src/ops.rs:161)
         const int idx = e0 + tid;
         if (idx < GD) {
@@ -594,42 +598,61 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
         }
         return;
     }
-    const int wg1 = ws.seg_runs[2 * seg], n_runs = ws.seg_runs[2 * seg + 1];
+    const int n_runs = n_runs_raw;
     if (n_runs <= 1) return;  // one run: written directly by decode_kernel
     for (int r = tid; r < n_runs; r += 256)
         s_slot[r] = (int)sched::run_slot(r == 0, b, sidx, n_seg, p.batch, wg1 + r - 1);
     __syncthreads();
     const int c_lo = e0 / D, c_hi = min(cols - 1, (e0 + 255) / D);
-    const float* pml = ws.partial_ml;
+    // thread (wave, lane): values e0 + 4 lane .. +3 of runs wave, wave + 4, ...; the first
+    // kPre of those runs are loaded now, beside the (max, sum) pairs, before any weight is known
+    constexpr int kPre = 4;
+    const int e = e0 + 4 * lane;
+    const bool on = e < GD;  // GD is a multiple of 4 (D >= 64)
+    const float* po = ws.partial_o + (on ? e : 0);
+    auto part = [&](int r) { return *reinterpret_cast<const f32x4*>(po + (size_t)s_slot[r] * GD); };
+    f32x4 pre[kPre];
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const int r = wave + 4 * j;
+        pre[j] = r < n_runs ? part(r) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2* pml = reinterpret_cast<const f2*>(ws.partial_ml);
     if (wave <= c_hi - c_lo) {  // one wavefront per column of this block
         const int c = c_lo + wave;
-        float M = -1e30f;
-        for (int r = lane; r < n_runs; r += 64) M = fmaxf(M, pml[((size_t)s_slot[r] * cols + c) * 2]);
+        // (running max, sum) of runs lane, lane + 64, ... : the first in registers
+        const f2 ml0 = lane < n_runs ? pml[(size_t)s_slot[lane] * cols + c] : f2{-1e30f, 0.f};
+        float M = ml0[0];
+        for (int r = lane + 64; r < n_runs; r += 64) M = fmaxf(M, pml[(size_t)s_slot[r] * cols + c][0]);
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) M = wave_max_xor(M, m);
         float lsum = 0.f;
-        for (int r = lane; r < n_runs; r += 64) {
-            const size_t mi = ((size_t)s_slot[r] * cols + c) * 2;
-            const float w = fast_exp2(pml[mi] - M);
+        if (lane < n_runs) {
+            const float w = fast_exp2(ml0[0] - M);
+            s_w[wave][lane] = w;
+            lsum = w * ml0[1];
+        }
+        for (int r = lane + 64; r < n_runs; r += 64) {
+            const f2 ml = pml[(size_t)s_slot[r] * cols + c];
+            const float w = fast_exp2(ml[0] - M);
             s_w[wave][r] = w;
-            lsum += w * pml[mi + 1];
+            lsum += w * ml[1];
         }
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
         if (lane == 0) s_inv[wave] = lsum > 0.f ? 1.0f / lsum : 0.f;
     }
     __syncthreads();
-    // thread (wave, lane): values e0 + 4 lane .. +3, runs wave, wave + 4, ...
-    const int e = e0 + 4 * lane;
-    const bool on = e < GD;  // GD is a multiple of 4 (D >= 64)
     const int cw = (on ? e / D : c_lo) - c_lo;
     const float* w = s_w[cw];
-    const float* po = ws.partial_o + (on ? e : 0);
-    auto part = [&](int r) { return *reinterpret_cast<const f32x4*>(po + (size_t)s_slot[r] * GD); };
     f32x4 a[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) a[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    int r = wave;
+    for (int j = 0; j < kPre; ++j) {
+        const int r = wave + 4 * j;
+        a[j] = r < n_runs ? w[r] * pre[j] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    int r = wave + 4 * kPre;
     for (; r + 12 < n_runs; r += 16) {  // four independent loads in flight
 #pragma unroll
         for (int j = 0; j < 4; ++j) a[j] += w[r + 4 * j] * part(r + 4 * j);
