@@ -20,6 +20,8 @@
 // read per ~4 clocks (256 B/clk for 16-byte reads).  So each wavefront
 // alternates a pure MFMA phase and a pure VALU (softmax) phase, and the two
 // wavefronts of a SIMD run in opposite phases.
+#include <cstdlib>
+
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -59,6 +61,10 @@ struct PrefillArgs {
     int q_off;  // position of query row 0 among the keys (causal: row i sees keys <= q_off + i)
     int hq, hkv, group, causal, gqa_mode;
     float qk_scale;  // scale * log2(e)
+    // causal balance: workgroup y takes query blocks nqb-1-y and y in turn, so
+    // every workgroup walks nqb + 1 key tiles and one wave of workgroups fills
+    // the chip evenly (else: one block each, heaviest first)
+    int paired;
 };
 
 __device__ __forceinline__ int head_of(int kvh, int c, int hkv, int group, int mode) {
@@ -123,19 +129,40 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     __shared__ __attribute__((aligned(1024))) T sk[NB][BN * KS];
     __shared__ __attribute__((aligned(1024))) T sv[NB][BN * D];
 
-    const int tid = threadIdx.x;
+    {  // a head that does not exist (modulo map with n_q_heads not a multiple of n_kv_heads:
+       // HPW is 1) makes the whole workgroup leave, before any barrier
+        const int per_kv = a.group / HPW;
+        const int hs0 = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) % HPW;
+        if (head_of((int)blockIdx.x / per_kv, ((int)blockIdx.x % per_kv) * HPW + hs0, a.hkv,
+                    a.group, a.gqa_mode) >= a.hq)
+            return;
+    }
+    const int nqb = (a.S + WROWS - 1) / WROWS;
+    const int by = blockIdx.y;
+    const int n_blocks = a.paired && by != nqb - 1 - by ? 2 : 1;
+    for (int blk = 0; blk < n_blocks; ++blk) {
+    // heaviest (latest) query blocks first; a paired workgroup then takes block y
+    int qb = blk == 0 ? (a.paired ? nqb - 1 - by : (int)gridDim.y - 1 - by) : by;
+    if (blk > 0) {
+        // every wave is past its last LDS read of the previous block before the
+        // new block's loads land in the unit buffers
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    }
+    // Everything below is derived afresh for each block from values the compiler
+    // cannot carry over (opaque copies), so nothing stays live across blocks.
+    int tid = threadIdx.x, bxx = blockIdx.x;
+    asm volatile("" : "+v"(tid));
+    asm volatile("" : "+s"(bxx), "+s"(qb));
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hs = wave % HPW, rt = wave / HPW;
     const int b = blockIdx.z;
     const int S = a.S, Sk = a.Sk, q_off = a.q_off;
-    const int qb = gridDim.y - 1 - blockIdx.y;  // heaviest (latest) query blocks first
     const int per_kv = a.group / HPW;           // workgroups per KV head
-    const int kvh = blockIdx.x / per_kv;
-    const int head = head_of(kvh, (blockIdx.x % per_kv) * HPW + hs, a.hkv, a.group, a.gqa_mode);
-    // modulo map with n_q_heads not a multiple of n_kv_heads: HPW is 1, so a
-    // workgroup whose head does not exist leaves as a whole, before any barrier
-    if (head >= a.hq) return;
+    const int kvh = bxx / per_kv;
+    const int head = head_of(kvh, (bxx % per_kv) * HPW + hs, a.hkv, a.group, a.gqa_mode);
     const int p0 = qb * WROWS + rt * ROWS;
     const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
     const int n_tiles = (wg_keys + BN - 1) / BN;
@@ -462,17 +489,19 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     }
 
     l_run = wave_sum_xor(l_run, 32);
-    if (qpos >= S) return;
-    const float inv = 1.0f / l_run;
-    float* orow = a.out + (((size_t)b * S + qpos) * a.hq + head) * D;
+    if (qpos < S) {
+        const float inv = 1.0f / l_run;
+        float* orow = a.out + (((size_t)b * S + qpos) * a.hq + head) * D;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f32x4 t = {o[dt][4 * i] * inv, o[dt][4 * i + 1] * inv, o[dt][4 * i + 2] * inv,
-                       o[dt][4 * i + 3] * inv};
-            *reinterpret_cast<f32x4*>(orow + 32 * dt + 8 * i + 4 * hh) = t;
-        }
+            for (int i = 0; i < 4; ++i) {
+                f32x4 t = {o[dt][4 * i] * inv, o[dt][4 * i + 1] * inv, o[dt][4 * i + 2] * inv,
+                           o[dt][4 * i + 3] * inv};
+                *reinterpret_cast<f32x4*>(orow + 32 * dt + 8 * i + 4 * hh) = t;
+            }
+    }
+    }  // query blocks of this workgroup
 }
 
 // ---------------------------------------------------------------------------
@@ -683,7 +712,8 @@ void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int ba
     // kernel so the heaviest blocks go first); with x = KV head and
     // round-robin dispatch over the 8 XCDs, a KV head's K/V stays in one L2.
     const int rows = ROWS * NW / hpw;
-    const dim3 grid(n_kv_heads * (a.group / hpw), (seq_len + rows - 1) / rows, batch);
+    const int nqb = (seq_len + rows - 1) / rows;
+    const dim3 grid(n_kv_heads * (a.group / hpw), a.paired ? (nqb + 1) / 2 : nqb, batch);
     const dim3 block(64 * NW);
     switch (hpw) {
         case 4:
@@ -757,6 +787,26 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     a.qk_scale = scale * kLog2e;
     const int hpw = !multiple ? 1 : a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
     const bool bf = dtype == 2;
+    // Pair the query blocks (equal work per workgroup) when the pairs alone fill every CU
+    // once or more; a shorter prompt keeps one block per workgroup for the parallelism.
+    // PI_PREFILL_PAIRED=0 / 1 forces either schedule.
+    {
+        const int nw = head_dim == 128 ? PrefillCfg<128>::NW : PrefillCfg<256>::NW;
+        const int rows = ROWS * nw / hpw;
+        const long long pairs = (long long)n_kv_heads * (a.group / hpw) * batch *
+                                (((seq_len + rows - 1) / rows + 1) / 2);
+        static int n_cu = -1;
+        if (n_cu < 0) {
+            int dev = 0, v = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+                v = 0;
+            n_cu = v;
+        }
+        a.paired = causal && n_cu > 0 && pairs >= n_cu;
+        static const char* env = std::getenv("PI_PREFILL_PAIRED");
+        if (env && causal) a.paired = env[0] == '1';
+    }
     if (head_dim == 128) launch_d<128>(a, hpw, n_kv_heads, seq_len, batch, bf, s);
     else launch_d<256>(a, hpw, n_kv_heads, seq_len, batch, bf, s);
     return hipGetLastError();
