@@ -30,6 +30,8 @@ struct pi_handle_s {
     size_t tq_qv_floats = 0;
     char* pf_buf = nullptr;        // paged prefill: the sequence's K / V gathered to f16 rows
     size_t pf_bytes = 0;
+    float* pfs_buf = nullptr;      // prefill key-split partials
+    size_t pfs_floats = 0;
     // Ordering of the workspaces above across caller streams: ws_event marks
     // the last workspace use, issued on ws_stream.
     hipEvent_t ws_event = nullptr;
@@ -284,6 +286,7 @@ void pi_destroy(pi_handle h) {
     (void)hipFree(h->h2d_scratch);
     (void)hipFree(h->tq_qv);
     (void)hipFree(h->pf_buf);
+    (void)hipFree(h->pfs_buf);
     if (h->ws_event) (void)hipEventDestroy(h->ws_event);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
@@ -595,11 +598,16 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
                     n_q_heads, n_kv_heads);
     if (batch == 0 || seq_len == 0) return PI_OK;
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_prefill");
+    hipStream_t s = pick(h, stream);
+    int rc;
+    if ((rc = ws_begin(h, s, "pi_attn_prefill"))) return rc;
+    const size_t need = pi::prefill_ws_floats(batch, seq_len, n_q_heads, n_kv_heads, head_dim, causal ? 1 : 0);
+    if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "pi_attn_prefill workspace", false))) return rc;
     PI_HIP(h, pi::launch_prefill(d_q, d_k, d_v, dtype, batch, seq_len, seq_len, 0, n_q_heads,
                                  n_kv_heads, head_dim, causal ? 1 : 0, gqa_mode, scale, d_out,
-                                 pick(h, stream)),
+                                 h->pfs_buf, h->pfs_floats, s),
            "pi_attn_prefill");
-    return PI_OK;
+    return ws_end(h, s, "pi_attn_prefill");
 }
 
 int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
@@ -640,8 +648,12 @@ int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
     char* gk = h->pf_buf;
     char* gv = h->pf_buf + 2 * rows;
     PI_HIP(h, pi::launch_kv_gather(g, d_page_table, (int32_t)n_keys, gk, gv, s), "pi_attn_prefill_paged");
+    const size_t need = pi::prefill_ws_floats(1, n_tok, n_q_heads, g.n_kv_heads, g.head_dim, 1);
+    if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "pi_attn_prefill_paged workspace", false)))
+        return rc;
     PI_HIP(h, pi::launch_prefill(d_q, gk, gv, PI_F16, 1, n_tok, (int32_t)n_keys, start_pos, n_q_heads,
-                                 g.n_kv_heads, g.head_dim, 1, gqa_mode, scale, d_out, s),
+                                 g.n_kv_heads, g.head_dim, 1, gqa_mode, scale, d_out, h->pfs_buf,
+                                 h->pfs_floats, s),
            "pi_attn_prefill_paged");
     return ws_end(h, s, "pi_attn_prefill_paged");
 }
@@ -1164,9 +1176,14 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
         } else {          // a continued chunk: the whole sequence out of its pages
             PI_HIP(h, pi::launch_kv_gather(L->pool->g, L->d_pt, prev + n, hk16, hv16, s), "attention layer");
         }
+        if ((rc = ws_begin(h, s, "attention layer"))) return rc;
+        const size_t need = pi::prefill_ws_floats(1, n, L->n_heads, L->n_kv, D, 1);
+        if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "attention layer workspace", false)))
+            return rc;
         PI_HIP(h, pi::launch_prefill(hq16, hk16, hv16, PI_F16, 1, n, prev + n, prev, L->n_heads, L->n_kv,
-                                     D, 1, L->gqa_mode, scale, dout, s),
+                                     D, 1, L->gqa_mode, scale, dout, h->pfs_buf, h->pfs_floats, s),
                "attention layer");
+        if ((rc = ws_end(h, s, "attention layer"))) return rc;
         if (dg) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
     } else if (n > 1 && L->kv_dtype == PI_F32) {
         // causal attention straight from the f32 pages, at f32 accuracy

@@ -140,10 +140,15 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
 // n_keys keys; query row i sits at key position q_off + i (a fresh prompt:
 // n_keys = seq_len, q_off = 0).  q / out [batch][seq_len][Hq][D],
 // k / v [batch][n_keys][Hkv][D].
+// ws: the key-split partials of a launch with fewer workgroups than CUs (floats from
+// prefill_ws_floats; 0 = no split).  With ws null or short the launch runs unsplit.
+size_t prefill_ws_floats(int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
+                         int32_t head_dim, int32_t causal);
 hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
                           int32_t batch, int32_t seq_len, int32_t n_keys, int32_t q_off,
                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t causal,
-                          int32_t gqa_mode, float scale, float* out, hipStream_t s);
+                          int32_t gqa_mode, float scale, float* out, float* ws, size_t ws_floats,
+                          hipStream_t s);
 // Causal attention of n_tok f32 query rows [n_tok][Hq][D] at positions q_off ..
 // q_off + n_tok - 1 over an f32 pool (D = 64 / 128 / 256), keys read through the
 // sequence's page-table row; products at f32 accuracy (bf16 hi + lo splits).

@@ -65,6 +65,12 @@ struct PrefillArgs {
     // every workgroup walks nqb + 1 key tiles and one wave of workgroups fills
     // the chip evenly (else: one block each, heaviest first)
     int paired;
+    // key split (a launch with fewer workgroups than CUs): blockIdx.z = batch * ksplit +
+    // split; split k of a workgroup's n key tiles takes tiles [k p, (k+1) p), p = ceil(n /
+    // ksplit), and leaves its unnormalised O and (max, sum) for prefill_merge_kernel
+    int ksplit;
+    float* part_o;   // [ksplit][B][S][Hq][D]
+    float* part_ml;  // [ksplit][B][S][Hq][2]
 };
 
 __device__ __forceinline__ int head_of(int kvh, int c, int hkv, int group, int mode) {
@@ -158,7 +164,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hs = wave % HPW, rt = wave / HPW;
-    const int b = blockIdx.z;
+    const int b = (int)blockIdx.z / a.ksplit, ksp = (int)blockIdx.z % a.ksplit;
     const int S = a.S, Sk = a.Sk, q_off = a.q_off;
     const int per_kv = a.group / HPW;           // workgroups per KV head
     const int kvh = bxx / per_kv;
@@ -166,6 +172,10 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     const int p0 = qb * WROWS + rt * ROWS;
     const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
     const int n_tiles = (wg_keys + BN - 1) / BN;
+    // this workgroup's key tiles: [tb, tb + nloc); step t below works on tile tb + t
+    const int kper = (n_tiles + a.ksplit - 1) / a.ksplit;
+    const int tb = min(n_tiles, ksp * kper);
+    const int nloc = min(n_tiles, tb + kper) - tb;
     const int w_keys = a.causal ? min(Sk, q_off + p0 + ROWS) : Sk;
     const int w_tiles = p0 < S ? (w_keys + BN - 1) / BN : 0;  // tiles this wavefront attends
     // Tiles from t_mask on hold a key past the wavefront's first row (causal)
@@ -258,7 +268,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     }
     auto issue_unit = [&](int u) {
         const int buf = u % NB;
-        const int k0 = u * BN;
+        const int k0 = (tb + u) * BN;
         if (k0 + BN <= Sk) {
             const T* kb = kbase + (size_t)k0 * tok_stride;
 #pragma unroll
@@ -413,14 +423,14 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     };
 
     issue_unit(0);
-    if (n_tiles >= 1) issue_unit(1);
+    if (nloc >= 1) issue_unit(1);
     __builtin_amdgcn_s_waitcnt(0);  // all counters (Q loads, units 0 and 1)
     barrier();
     // The MFMA phase runs at a raised wave priority so that its MFMA and LDS
     // issues win over the other wave's softmax VALU stream on the same SIMD.
     auto mfma_phase = [&](int t) {
-        const bool pv = t >= 1 && t - 1 < w_tiles;
-        const bool qk = t < w_tiles;
+        const bool pv = t >= 1 && tb + t - 1 < w_tiles;
+        const bool qk = t < nloc && tb + t < w_tiles;
         __builtin_amdgcn_s_setprio(2);
         if (pv) run_pv(t % NB);
         if (qk) run_qk(t % NB);
@@ -442,7 +452,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
                 __builtin_amdgcn_s_waitcnt(0x0F70);
             }
         };
-        auto ahead_of = [&](int u) { return min(2, max(0, n_tiles - u)); };
+        auto ahead_of = [&](int u) { return min(2, max(0, nloc - u)); };
         // One barrier per tile step t = 0 .. n_tiles.  Lead waves (0-3): the
         // MFMA phase of tile t, then the softmax of tile t; lag waves (4-7): the
         // softmax of tile t-1, then the MFMA phase of tile t; so the two
@@ -450,23 +460,23 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         // issues its loads of unit t+3 in step t (the buffer's previous unit,
         // t-1, was last read in step t-1) and waits for unit t+1 before the
         // barrier.
-        if (2 <= n_tiles) issue_unit(2);
+        if (2 <= nloc) issue_unit(2);
         if (wave < NW / 2) {
-            for (int t = 0; t <= n_tiles; ++t) {
+            for (int t = 0; t <= nloc; ++t) {
                 mfma_phase(t);
-                if (t < w_tiles) phase_softmax(t, t >= t_mask);
-                if (t + 3 <= n_tiles) issue_unit(t + 3);
-                if (t < n_tiles) {
+                if (t < nloc && tb + t < w_tiles) phase_softmax(tb + t, tb + t >= t_mask);
+                if (t + 3 <= nloc) issue_unit(t + 3);
+                if (t < nloc) {
                     wait_unit(ahead_of(t + 1));
                     barrier();
                 }
             }
         } else {
-            for (int t = 0; t <= n_tiles; ++t) {
-                if (t >= 1 && t - 1 < w_tiles) phase_softmax(t - 1, t - 1 >= t_mask);
-                if (t + 3 <= n_tiles) issue_unit(t + 3);
+            for (int t = 0; t <= nloc; ++t) {
+                if (t >= 1 && tb + t - 1 < w_tiles) phase_softmax(tb + t - 1, tb + t - 1 >= t_mask);
+                if (t + 3 <= nloc) issue_unit(t + 3);
                 mfma_phase(t);
-                if (t < n_tiles) {
+                if (t < nloc) {
                     wait_unit(ahead_of(t + 1));
                     barrier();
                 }
@@ -477,11 +487,11 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         // its loads of unit t+1 (the buffer's previous unit, t-1, was last read
         // in step t-1), runs the MFMA phase and the softmax of tile t, and
         // waits for unit t+1 before the barrier.
-        for (int t = 0; t <= n_tiles; ++t) {
-            if (t >= 1 && t + 1 <= n_tiles) issue_unit(t + 1);
+        for (int t = 0; t <= nloc; ++t) {
+            if (t >= 1 && t + 1 <= nloc) issue_unit(t + 1);
             mfma_phase(t);
-            if (t < w_tiles) phase_softmax(t, t >= t_mask);
-            if (t < n_tiles) {
+            if (t < nloc && tb + t < w_tiles) phase_softmax(tb + t, tb + t >= t_mask);
+            if (t < nloc) {
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
                 barrier();
             }
@@ -489,7 +499,23 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     }
 
     l_run = wave_sum_xor(l_run, 32);
-    if (qpos < S) {
+    if (a.ksplit > 1) {  // unnormalised partial of this key split
+        if (qpos < S) {
+            const size_t row = (((size_t)ksp * (gridDim.z / a.ksplit) + b) * S + qpos) * a.hq + head;
+            float* po = a.part_o + row * D;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f32x4 t = {o[dt][4 * i], o[dt][4 * i + 1], o[dt][4 * i + 2], o[dt][4 * i + 3]};
+                    *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * i + 4 * hh) = t;
+                }
+            if (hh == 0) {
+                a.part_ml[2 * row] = m_run;
+                a.part_ml[2 * row + 1] = l_run;
+            }
+        }
+    } else if (qpos < S) {
         const float inv = 1.0f / l_run;
         float* orow = a.out + (((size_t)b * S + qpos) * a.hq + head) * D;
 #pragma unroll
@@ -701,6 +727,32 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillF32Args a) {
         *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db] * inv;
 }
 
+// The key splits of a prefill launch combined per (batch, query row, head): the
+// log-sum-exp merge of the splits' (max, sum) in log2 units and their O.  One
+// wavefront per row, D / 64 values per lane.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
+                                                            const float* __restrict__ part_ml,
+                                                            float* __restrict__ out, long long rows,
+                                                            int ksplit) {
+    constexpr int V = D / 64;
+    typedef float fv __attribute__((ext_vector_type(V)));
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    float M = -1e30f;
+    for (int k = 0; k < ksplit; ++k) M = fmaxf(M, part_ml[2 * (k * rows + row)]);
+    float L = 0.f;
+    fv acc = {};
+    for (int k = 0; k < ksplit; ++k) {
+        const long long r = k * rows + row;
+        const float w = fast_exp2(part_ml[2 * r] - M);
+        L += w * part_ml[2 * r + 1];
+        acc += w * *reinterpret_cast<const fv*>(part_o + r * D + V * lane);
+    }
+    *reinterpret_cast<fv*>(out + row * D + V * lane) = acc * (1.0f / L);
+}
+
 }  // namespace
 
 namespace {
@@ -713,7 +765,7 @@ void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int ba
     // round-robin dispatch over the 8 XCDs, a KV head's K/V stays in one L2.
     const int rows = ROWS * NW / hpw;
     const int nqb = (seq_len + rows - 1) / rows;
-    const dim3 grid(n_kv_heads * (a.group / hpw), a.paired ? (nqb + 1) / 2 : nqb, batch);
+    const dim3 grid(n_kv_heads * (a.group / hpw), a.paired ? (nqb + 1) / 2 : nqb, batch * a.ksplit);
     const dim3 block(64 * NW);
     switch (hpw) {
         case 4:
@@ -762,10 +814,64 @@ hipError_t launch_prefill_f32(const KvGeom& g, const float* q, const int32_t* pa
     return hipGetLastError();
 }
 
+namespace {
+int cu_count() {
+    static int n_cu = -1;
+    if (n_cu < 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            v = 0;
+        n_cu = v;
+    }
+    return n_cu;
+}
+
+struct PrefillSched {
+    int hpw, paired, ksplit;
+};
+
+// The schedule of a launch.  Causal launches whose pairs of query blocks fill every CU
+// once or more pair them (equal work per workgroup).  Otherwise, a launch with fewer
+// workgroups than CUs splits each workgroup's keys over up to 4 workgroups (more CUs
+// busy, one merge launch after).  PI_PREFILL_PAIRED=0 / 1 and PI_PREFILL_KSPLIT=n
+// force either choice.
+PrefillSched prefill_sched(int batch, int seq_len, int n_q_heads, int n_kv_heads, int head_dim,
+                           int causal) {
+    PrefillSched sc;
+    const bool multiple = n_q_heads % n_kv_heads == 0;
+    const int group = (n_q_heads + n_kv_heads - 1) / n_kv_heads;
+    sc.hpw = !multiple ? 1 : group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
+    const int nw = head_dim == 128 ? PrefillCfg<128>::NW : PrefillCfg<256>::NW;
+    const int rows = ROWS * nw / sc.hpw;
+    const long long wgs = (long long)n_kv_heads * (group / sc.hpw) * batch * ((seq_len + rows - 1) / rows);
+    const long long pairs = (long long)n_kv_heads * (group / sc.hpw) * batch *
+                            (((seq_len + rows - 1) / rows + 1) / 2);
+    const int n_cu = cu_count();
+    sc.paired = causal && n_cu > 0 && pairs >= n_cu;
+    static const char* env_p = std::getenv("PI_PREFILL_PAIRED");
+    if (env_p && causal) sc.paired = env_p[0] == '1';
+    sc.ksplit = 1;
+    if (!sc.paired && n_cu > 0 && wgs < n_cu) sc.ksplit = (int)std::min<long long>(4, n_cu / wgs);
+    static const char* env_k = std::getenv("PI_PREFILL_KSPLIT");
+    if (env_k && !sc.paired) sc.ksplit = std::max(1, std::min(4, std::atoi(env_k)));
+    return sc;
+}
+}  // namespace
+
+size_t prefill_ws_floats(int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
+                         int32_t head_dim, int32_t causal) {
+    if (batch <= 0 || seq_len <= 0 || n_q_heads <= 0 || n_kv_heads <= 0) return 0;
+    const PrefillSched sc = prefill_sched(batch, seq_len, n_q_heads, n_kv_heads, head_dim, causal);
+    if (sc.ksplit <= 1) return 0;
+    return (size_t)sc.ksplit * batch * seq_len * n_q_heads * (head_dim + 2);
+}
+
 hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t dtype,
                           int32_t batch, int32_t seq_len, int32_t n_keys, int32_t q_off,
                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t causal,
-                          int32_t gqa_mode, float scale, float* out, hipStream_t s) {
+                          int32_t gqa_mode, float scale, float* out, float* ws, size_t ws_floats,
+                          hipStream_t s) {
     if (head_dim != 128 && head_dim != 256) return hipErrorInvalidValue;
     if (q_off < 0 || n_keys < 1 || (causal && q_off + seq_len > n_keys)) return hipErrorInvalidValue;
     PrefillArgs a;
@@ -785,30 +891,28 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     a.causal = causal;
     a.gqa_mode = gqa_mode;
     a.qk_scale = scale * kLog2e;
-    const int hpw = !multiple ? 1 : a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
     const bool bf = dtype == 2;
-    // Pair the query blocks (equal work per workgroup) when the pairs alone fill every CU
-    // once or more; a shorter prompt keeps one block per workgroup for the parallelism.
-    // PI_PREFILL_PAIRED=0 / 1 forces either schedule.
-    {
-        const int nw = head_dim == 128 ? PrefillCfg<128>::NW : PrefillCfg<256>::NW;
-        const int rows = ROWS * nw / hpw;
-        const long long pairs = (long long)n_kv_heads * (a.group / hpw) * batch *
-                                (((seq_len + rows - 1) / rows + 1) / 2);
-        static int n_cu = -1;
-        if (n_cu < 0) {
-            int dev = 0, v = 0;
-            if (hipGetDevice(&dev) != hipSuccess ||
-                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-                v = 0;
-            n_cu = v;
-        }
-        a.paired = causal && n_cu > 0 && pairs >= n_cu;
-        static const char* env = std::getenv("PI_PREFILL_PAIRED");
-        if (env && causal) a.paired = env[0] == '1';
+    const PrefillSched sc = prefill_sched(batch, seq_len, n_q_heads, n_kv_heads, head_dim, causal);
+    a.paired = sc.paired;
+    a.ksplit = 1;
+    a.part_o = a.part_ml = nullptr;
+    const size_t rows = (size_t)batch * seq_len * n_q_heads;
+    if (sc.ksplit > 1 && ws && ws_floats >= (size_t)sc.ksplit * rows * (head_dim + 2)) {
+        a.ksplit = sc.ksplit;
+        a.part_o = ws;
+        a.part_ml = ws + (size_t)sc.ksplit * rows * head_dim;
     }
-    if (head_dim == 128) launch_d<128>(a, hpw, n_kv_heads, seq_len, batch, bf, s);
-    else launch_d<256>(a, hpw, n_kv_heads, seq_len, batch, bf, s);
+    if (head_dim == 128) launch_d<128>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
+    else launch_d<256>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.ksplit == 1) return e;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (head_dim == 128)
+        hipLaunchKernelGGL(prefill_merge_kernel<128>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out,
+                           (long long)rows, a.ksplit);
+    else
+        hipLaunchKernelGGL(prefill_merge_kernel<256>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out,
+                           (long long)rows, a.ksplit);
     return hipGetLastError();
 }
 
