@@ -522,8 +522,12 @@ def bench_gdn_decode(torch, rt, dev, timer, steps, warmup, cpu_s=0.0, batch=1, g
             fn()
         us = graph_us_per_call(torch, fn_cur)
         args[-1] = None
+        # the per-launch floor of a graph on this box: torch's fill of one element, replayed the same way
+        one = torch.empty(1, device="cuda")
+        floor_us = graph_us_per_call(torch, lambda: one.fill_(1.0))
         res.update({"us_per_step_graph": us, "GB_s_graph": algo / us / 1e3,
-                    "hbm_frac_graph": algo / us / 1e3 / HBM_PEAK_GBS})
+                    "hbm_frac_graph": algo / us / 1e3 / HBM_PEAK_GBS,
+                    "graph_launch_floor_us": floor_us})
     if cpu_s > 0:
         # the timed calls advanced the state: one GPU step from zero for the parity figure
         state.zero_()
