@@ -53,7 +53,7 @@ def _args():
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--workload", default=None,
                    choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "tq", "copy",
-                            "rows_f", "chunk", "tq_c4"],
+                            "rows_f", "chunk", "tq_c4", "c4_prefill"],
                    help="time one workload only and print its figures (for sweeps)")
     return p.parse_args()
 
@@ -1052,14 +1052,15 @@ def _traffic(summary, kernels):
     p = os.path.join(ROOT, "profiles", f"{summary}.txt")
     if not os.path.exists(p):
         return None
+    # table rows: kernel, workgroups, FETCH_KiB, WRITE_KiB, read_B(cal), write_B(cal)[, algo, ratio]
     total, seen, in_table = 0, set(), False
     for line in open(p):
         f = line.split()
-        if f[:3] == ["kernel", "FETCH_KiB", "WRITE_KiB"]:
+        if f[:4] == ["kernel", "wgs", "FETCH_KiB", "WRITE_KiB"]:
             in_table = True
             continue
-        if in_table and len(f) == 5 and f[0] in kernels:
-            total += int(float(f[3])) + int(float(f[4]))
+        if in_table and len(f) >= 6 and f[0] in kernels and f[0] not in seen:
+            total += int(float(f[4])) + int(float(f[5]))
             seen.add(f[0])
     return total if seen == set(kernels) else None
 
@@ -1082,6 +1083,8 @@ def _single(torch, rt, dev, timer, a):
                             pool_dtype=torch.float32, graph=True)[0]
     if w == "c3":
         return bench_prefill(torch, rt, dev, timer, 4096, 32, 8, 128, 1e6, 0x5EED0002, st, wu)
+    if w == "c4_prefill":  # a 4096-token prompt of the config-4 layer (16/2 heads, D 256)
+        return bench_prefill(torch, rt, dev, timer, 4096, 16, 2, 256, 1e7, 0x5EED0007, st, wu)
     if w == "gdn_prefill":
         return bench_gdn_prefill(torch, rt, dev, timer, st, wu)
     if w == "tq":
