@@ -94,6 +94,6 @@ def test_pool_rejects_bad_shapes():
         rt.KvPool(dev, 4, 2, 128, page_tokens=32)
     pool = rt.KvPool(dev, 4, 3, 128)
     q = torch.zeros((1, 4, 128), device="cuda")
-    with pytest.raises(rt.Unsupported):  # 4 q heads over 3 kv heads
+    with pytest.raises(rt.InvalidArg):  # 4 q heads over 3 kv heads: the grouped map needs a multiple
         rt.attn_decode(dev, q, pool, torch.zeros((1, 1), dtype=torch.int32, device="cuda"),
-                       torch.ones(1, dtype=torch.int32, device="cuda"))
+                       torch.ones(1, dtype=torch.int32, device="cuda"), gqa_mode=1)
