@@ -323,18 +323,20 @@ int pi_kv_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t
     if (!p) return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_kv_pool_create: host allocation");
     p->owner = h;
     p->bytes = 2 * bytes;
-    p->g = pi::KvGeom{nullptr, nullptr, n_pages, n_kv_heads, head_dim, dtype, eb};
-    hipError_t e = hipMalloc(&p->g.k, bytes);
-    if (e == hipSuccess) e = hipMalloc(&p->g.v, bytes);
+    // K and V blocks interleaved per (page, KV head): a segment's page is one 2 x 16 x D run
+    const size_t blk = (size_t)pi::kPageTokens * head_dim * eb;
+    p->g = pi::KvGeom{nullptr, nullptr, n_pages, n_kv_heads, head_dim, dtype, eb, 2 * blk, 2 * blk};
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, 2 * bytes);
     // Zero once so slack slots of partially filled pages hold finite values.
-    if (e == hipSuccess) e = hipMemset(p->g.k, 0, bytes);
-    if (e == hipSuccess) e = hipMemset(p->g.v, 0, bytes);
+    if (e == hipSuccess) e = hipMemset(base, 0, 2 * bytes);
     if (e != hipSuccess) {
-        (void)hipFree(p->g.k);
-        (void)hipFree(p->g.v);
+        (void)hipFree(base);
         delete p;
         return hip_fail(h, e, "pi_kv_pool_create");
     }
+    p->g.k = base;
+    p->g.v = static_cast<char*>(base) + blk;
     *out = p;
     return PI_OK;
 }
@@ -343,8 +345,7 @@ void pi_kv_pool_destroy(pi_kv_pool pool) {
     if (!pool) return;
     (void)hipSetDevice(pool->owner->device);
     (void)hipDeviceSynchronize();
-    (void)hipFree(pool->g.k);
-    (void)hipFree(pool->g.v);
+    (void)hipFree(pool->g.k);  // one allocation: v is inside it
     delete pool;
 }
 
@@ -1491,7 +1492,10 @@ int pi_tq_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t
     p->owner = h;
     p->bytes = kbytes + vbytes + 2 * mbytes;
     pi::TqPool& t = p->t;
-    t.g = pi::KvGeom{nullptr, nullptr, n_pages, n_kv_heads, D, pi::kTqDtype, 0};
+    // separate K (packed records + norms) and V (f16) arrays
+    t.g = pi::KvGeom{nullptr, nullptr, n_pages, n_kv_heads, D, pi::kTqDtype, 0,
+                     (size_t)pi::kPageTokens * (pi::tq_key_bytes(D) + 4),
+                     (size_t)pi::kPageTokens * D * 2};
     t.rt = t.gt = nullptr;
     t.scale = std::sqrt((float)D);
     // residual_norm * qjl_scale of the 3-bit estimator (src/turboquant/mod.rs:297-316)

@@ -67,8 +67,6 @@ template <int D>
 struct Tile<f16, D> {
     static constexpr int NK = D / 32;  // K loads (16 B) per lane per page
     static constexpr int NV = D / 16;  // V loads (8 B) per lane per page
-    static constexpr size_t KBLK = (size_t)kPageTokens * D * 2;  // bytes per (page, KV head)
-    static constexpr size_t VBLK = KBLK;
     static constexpr int QD = D;  // floats per query row
     static __device__ __forceinline__ void prepare() {}
     f16x8 k[NK];
@@ -126,8 +124,6 @@ template <int D>
 struct Tile<float, D> {
     static constexpr int NK = D / 16;
     static constexpr int NV = D / 16;
-    static constexpr size_t KBLK = (size_t)kPageTokens * D * 4;  // bytes per (page, KV head)
-    static constexpr size_t VBLK = KBLK;
     static constexpr int QD = D;
     static __device__ __forceinline__ void prepare() {}
     f32x4 k[NK];
@@ -232,8 +228,6 @@ struct Tile<TqKey, D> {
     static constexpr int CW = 3 * D / 128;   // code dwords of a lane's quarter
     static constexpr int SW = D / 128;       // sign dwords of a lane's quarter
     static constexpr int KB = tq_key_bytes(D);
-    static constexpr size_t KBLK = (size_t)kPageTokens * (KB + 4);
-    static constexpr size_t VBLK = (size_t)kPageTokens * D * 2;
     static constexpr int QD = 2 * D;
     uint32_t code[CW];  // 3-bit codes of dims (D/4) g .. +D/4 of token lane%16
     uint32_t sign[SW];  // QJL signs of the same dims
@@ -488,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
                     const int j = NP * i + u;
                     const int pid = j < n_my ? __builtin_amdgcn_readlane(pid_v, j) : first_pid;
                     const size_t blk = (size_t)pid * n_kv + kvh;
-                    dst[u].load(kpool + blk * T::KBLK, vpool + blk * T::VBLK, lane);
+                    dst[u].load(kpool + blk * g.kstride, vpool + blk * g.vstride, lane);
                 }
             };
             auto valid_of = [&](int* valid, int i) {

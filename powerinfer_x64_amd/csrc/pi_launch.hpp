@@ -20,7 +20,10 @@ constexpr int tq_key_bytes(int d) { return d / 2; }
 // E = 16 bytes / element size (16-byte chunks, chunk-major), V block layout:
 // [head_dim][16 tokens] (dim-major).  Both match the MFMA operand order the
 // decode kernel loads with one linear 16-byte (K) or 8/16-byte (V) access
-// per lane.
+// per lane.  Block (page, kv head) i = page * n_kv_heads + kv head starts at
+// k + i * kstride and v + i * vstride bytes.  The f16 / f32 pool interleaves
+// them: K block, then V block, per (page, kv head), so one segment's page is
+// one contiguous run of 2 x 16 x D elements (v = k + one block, strides = two).
 struct KvGeom {
     void* k;            // device base of K blocks
     void* v;            // device base of V blocks
@@ -29,6 +32,8 @@ struct KvGeom {
     int32_t head_dim;
     int32_t dtype;      // PI_F32 / PI_F16
     int32_t elem_bytes;
+    size_t kstride;     // bytes from one K block to the next
+    size_t vstride;     // bytes from one V block to the next
 };
 
 // TurboQuant compressed pool (head_dim d = 128 or 256): g.k holds per (page,

@@ -548,8 +548,9 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
 // ---------------------------------------------------------------------------
 struct PrefillF32Args {
     const float* q;         // [n_tok][hq][D], normalised and rotated
-    const float* kpool;     // f32 pool K blocks [page][hkv][D/4][16][4]
-    const float* vpool;     // f32 pool V blocks [page][hkv][D][16]
+    const float* kpool;     // f32 pool K blocks [D/4][16][4] of (page, kv head) i at kpool + i kstride
+    const float* vpool;     // f32 pool V blocks [D][16] at vpool + i vstride
+    size_t kstride, vstride;  // bytes
     const int32_t* pt;      // the sequence's page-table row
     float* out;             // [n_tok][hq][D]
     int n_tok, q_off, max_pages, n_pages, hq, hkv, group, gqa_mode;
@@ -607,7 +608,6 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillF32Args a) {
     // Tile loads: float4 i of a tile (i = tid + 256 j) is K (i < 8 D) or V, of
     // page i / (4 D) % 2; within a page block both are a linear copy.
     f32x4 pre[NF];
-    const size_t blk = (size_t)16 * D;  // floats of one (page, KV head) block
     auto load_tile = [&](int t) {
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
@@ -618,7 +618,10 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillF32Args a) {
             const int lp = 2 * t + half;
             const int pid = lp < a.max_pages ? a.pt[lp] : -1;
             const bool ok = lp * 16 < L && pid >= 0 && pid < a.n_pages;
-            const float* base = (isv ? a.vpool : a.kpool) + ((size_t)(ok ? pid : 0) * a.hkv + kvh) * blk;
+            const size_t bi = (size_t)(ok ? pid : 0) * a.hkv + kvh;
+            const float* base = reinterpret_cast<const float*>(
+                isv ? reinterpret_cast<const char*>(a.vpool) + bi * a.vstride
+                    : reinterpret_cast<const char*>(a.kpool) + bi * a.kstride);
             pre[j] = ok ? *reinterpret_cast<const f32x4*>(base + 4 * ci) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
     };
@@ -793,6 +796,8 @@ hipError_t launch_prefill_f32(const KvGeom& g, const float* q, const int32_t* pa
     a.q = q;
     a.kpool = reinterpret_cast<const float*>(g.k);
     a.vpool = reinterpret_cast<const float*>(g.v);
+    a.kstride = g.kstride;
+    a.vstride = g.vstride;
     a.pt = page_table;
     a.out = out;
     a.n_tok = n_tok;

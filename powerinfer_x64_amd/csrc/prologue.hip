@@ -44,9 +44,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvGeom g, const ST* __re
         const int page = pt[(size_t)s * max_pages + lp];
         if (page < 0 || page >= g.n_pages) continue;
         const int tok = pos % kPageTokens;
-        const size_t blk = ((size_t)page * H + h) * kPageTokens * D;
-        PT* kp = reinterpret_cast<PT*>(g.k) + blk;
-        PT* vp = reinterpret_cast<PT*>(g.v) + blk;
+        const size_t blk = (size_t)page * H + h;
+        PT* kp = reinterpret_cast<PT*>(static_cast<char*>(g.k) + blk * g.kstride);
+        PT* vp = reinterpret_cast<PT*>(static_cast<char*>(g.v) + blk * g.vstride);
         kp[k_index<PT>(tok, d)] = from_f32<PT>(to_f32(k[idx]));
         vp[v_index(tok, d)] = from_f32<PT>(to_f32(v[idx]));
     }
@@ -71,9 +71,9 @@ __global__ __launch_bounds__(256) void kv_read_kernel(KvGeom g, const int32_t* _
             const int page = pt[(size_t)seq * max_pages + lp];
             if (page >= 0 && page < g.n_pages) {
                 const int tok = pos % kPageTokens;
-                const size_t blk = ((size_t)page * H + h) * kPageTokens * D;
-                kv = to_f32(reinterpret_cast<const PT*>(g.k)[blk + k_index<PT>(tok, d)]);
-                vv = to_f32(reinterpret_cast<const PT*>(g.v)[blk + v_index(tok, d)]);
+                const size_t blk = (size_t)page * H + h;
+                kv = to_f32(reinterpret_cast<const PT*>(static_cast<const char*>(g.k) + blk * g.kstride)[k_index<PT>(tok, d)]);
+                vv = to_f32(reinterpret_cast<const PT*>(static_cast<const char*>(g.v) + blk * g.vstride)[v_index(tok, d)]);
             }
         }
         ko[idx] = kv;
@@ -96,9 +96,9 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(KvGeom g, const int32_t*
     const int lp = blockIdx.x, h = blockIdx.y, H = g.n_kv_heads;
     const int page = pt[lp];
     const bool ok = page >= 0 && page < g.n_pages;
-    const size_t blk = ((size_t)(ok ? page : 0) * H + h) * kPageTokens * D;
-    const f16x8* kb = reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(g.k) + blk);
-    const f16x8* vb = reinterpret_cast<const f16x8*>(reinterpret_cast<const f16*>(g.v) + blk);
+    const size_t blk = (size_t)(ok ? page : 0) * H + h;
+    const f16x8* kb = reinterpret_cast<const f16x8*>(static_cast<const char*>(g.k) + blk * g.kstride);
+    const f16x8* vb = reinterpret_cast<const f16x8*>(static_cast<const char*>(g.v) + blk * g.vstride);
     for (int i = threadIdx.x; i < NCH; i += 256) {
         *reinterpret_cast<f16x8*>(&sv[8 * i]) = ok ? vb[i] : f16x8{};
         const int c = i / kPageTokens, tok = i % kPageTokens;  // chunk i = dims 8c.., token tok
@@ -272,9 +272,9 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
             const int page = pt[(size_t)sq * max_pages + lp];
             if (page >= 0 && page < g.n_pages) {
                 const int tok = pos % kPageTokens;
-                const size_t blk = ((size_t)page * hkv + kvh) * kPageTokens * D;
-                PT* kp = reinterpret_cast<PT*>(g.k) + blk;
-                PT* vp = reinterpret_cast<PT*>(g.v) + blk;
+                const size_t blk = (size_t)page * hkv + kvh;
+                PT* kp = reinterpret_cast<PT*>(static_cast<char*>(g.k) + blk * g.kstride);
+                PT* vp = reinterpret_cast<PT*>(static_cast<char*>(g.v) + blk * g.vstride);
                 const float* vr = v + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
                 for (int d = lane; d < D; d += 64) {
                     kp[k_index<PT>(tok, d)] = from_f32<PT>(r[d]);
