@@ -94,13 +94,22 @@ __device__ __forceinline__ int head_of(int kvh, int c, int hkv, int group, int m
 // prompt-end mask; the mask is one wave-uniform branch around a straight-line
 // select block.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float max16(const f32x16& s) {
-    const float a = fmaxf(fmaxf(s[0], s[1]), s[2]);
-    const float b = fmaxf(fmaxf(s[3], s[4]), s[5]);
-    const float c = fmaxf(fmaxf(s[6], s[7]), s[8]);
-    const float d = fmaxf(fmaxf(s[9], s[10]), s[11]);
-    const float e = fmaxf(fmaxf(s[12], s[13]), s[14]);
-    return fmaxf(fmaxf(fmaxf(a, b), fmaxf(c, d)), fmaxf(e, s[15]));
+// Three-way max as one v_max3_f32.  fmaxf would first quiet a signalling NaN in every
+// operand (an extra v_max per score); scores come from MFMA accumulators or -inf masks,
+// never a signalling NaN, so the plain instruction gives the same result.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float max32(const f32x16& s, const f32x16& t) {
+    const float a = vmax3(s[0], s[1], s[2]), b = vmax3(s[3], s[4], s[5]);
+    const float c = vmax3(s[6], s[7], s[8]), d = vmax3(s[9], s[10], s[11]);
+    const float e = vmax3(s[12], s[13], s[14]), f = vmax3(s[15], t[0], t[1]);
+    const float g = vmax3(t[2], t[3], t[4]), h = vmax3(t[5], t[6], t[7]);
+    const float i = vmax3(t[8], t[9], t[10]), j = vmax3(t[11], t[12], t[13]);
+    const float k = vmax3(a, b, c), l = vmax3(d, e, f), m = vmax3(g, h, i);
+    return vmax3(vmax3(k, l, m), j, vmax3(t[14], t[15], j));
 }
 
 // Head dims 128 and 256.  D = 128: 8 wavefronts (two per SIMD, in opposite
@@ -395,7 +404,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
                     if (key >= Sk || (a.causal && key > q_off + qpos)) s[tt][e] = -INFINITY;
                 }
         }
-        float mx = fmaxf(max16(s[0]), max16(s[1]));
+        float mx = max32(s[0], s[1]);
         if (__any(mx * c > m_run + kLazy)) {
             mx = wave_max_xor(mx, 32);
             const float m_new = fmaxf(m_run, mx * c);
