@@ -32,6 +32,8 @@ struct pi_handle_s {
     size_t pf_bytes = 0;
     float* pfs_buf = nullptr;      // prefill key-split partials
     size_t pfs_floats = 0;
+    float* pin = nullptr;          // pinned host staging of the small host-slice layer calls
+    size_t pin_floats = 0;
     // Ordering of the workspaces above across caller streams: ws_event marks
     // the last workspace use, issued on ws_stream.
     hipEvent_t ws_event = nullptr;
@@ -58,7 +60,7 @@ struct pi_attn_layer_s {
     float* d_qn = nullptr;          // per-head RMSNorm weights (null: no norm)
     float* d_kn = nullptr;
     int32_t* d_pt = nullptr;        // kLayerRows identical rows of the identity page table
-    int32_t* d_ctx = nullptr;       // per-row context lengths, then the start position
+    int32_t* d_ctx = nullptr;       // the start position, then per-row context lengths (kLayerRows + 1)
     float* d_buf = nullptr;         // host-slice staging: q, gate, out, k, v (f32)
     size_t buf_floats = 0;
     char* d_half = nullptr;         // f16 q, then f16 K / V rows for the flash prefill
@@ -287,6 +289,7 @@ void pi_destroy(pi_handle h) {
     (void)hipFree(h->tq_qv);
     (void)hipFree(h->pf_buf);
     (void)hipFree(h->pfs_buf);
+    if (h->pin) (void)hipHostFree(h->pin);
     if (h->ws_event) (void)hipEventDestroy(h->ws_event);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
@@ -1155,8 +1158,10 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     const int D = L->dim;
     const size_t nq = (size_t)n * L->n_heads * D;
     int rc;
-    int32_t* d_start = L->d_ctx + kLayerRows;
-    PI_HIP(h, pi::launch_fill_iota(d_start, 1, prev, s), "attention layer");
+    // one launch writes [prev, prev + 1, ...]: the prologue's start position, then the context
+    // lengths of the first decode rows (d_ctx holds kLayerRows + 1 entries)
+    int32_t* d_start = L->d_ctx;
+    PI_HIP(h, pi::launch_fill_iota(d_start, std::min(n, kLayerRows) + 1, prev, s), "attention layer");
     if ((rc = pi_attn_prologue(h, dq, dk, dv, L->d_qn, L->d_kn, L->eps, L->rope_dim, L->rope_base,
                                L->has_sections ? L->sections : nullptr, L->pool, L->d_pt,
                                L->max_pages, d_start, 1, n, L->n_heads, sv)))
@@ -1196,9 +1201,9 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
         // one decode row per token over the paged cache: row i sees prev + i + 1 keys
         for (int r0 = 0; r0 < n; r0 += kLayerRows) {
             const int rows = std::min(kLayerRows, n - r0);
-            PI_HIP(h, pi::launch_fill_iota(L->d_ctx, rows, prev + r0 + 1, s), "attention layer");
+            if (r0 > 0) PI_HIP(h, pi::launch_fill_iota(L->d_ctx + 1, rows, prev + r0 + 1, s), "attention layer");
             const size_t off = (size_t)r0 * L->n_heads * D;
-            if ((rc = pi_attn_decode(h, dq + off, L->pool, L->d_pt, L->max_pages, L->d_ctx, rows,
+            if ((rc = pi_attn_decode(h, dq + off, L->pool, L->d_pt, L->max_pages, L->d_ctx + 1, rows,
                                      L->n_heads, L->gqa_mode, scale, dg ? dg + off : nullptr,
                                      dout + off, sv)))
                 return rc;
@@ -1232,6 +1237,27 @@ static int pack_layer_inputs(pi_handle h, pi_attn_layer L, const float* q, const
     return rc;
 }
 
+// A small host-slice call (a decode token) stages its slices through one pinned host
+// buffer: one host-to-device and one device-to-host copy per call instead of one per
+// slice.  Larger calls copy each slice directly (their time is the bytes, not the copies).
+constexpr size_t kPinnedMaxFloats = (size_t)1 << 20;  // 4 MiB each way
+
+static bool pinned_staging(pi_handle h, size_t floats) {
+    if (floats > kPinnedMaxFloats) return false;
+    if (floats <= h->pin_floats) return true;
+    if (h->pin) (void)hipHostFree(h->pin);  // the previous call has synchronised
+    h->pin = nullptr;
+    h->pin_floats = 0;
+    const size_t n = kPinnedMaxFloats;
+    if (hipHostMalloc(reinterpret_cast<void**>(&h->pin), n * sizeof(float), hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        h->pin = nullptr;
+        return false;
+    }
+    h->pin_floats = n;
+    return true;
+}
+
 int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, const float* h_v,
                           const float* h_gate, int32_t n_tokens, float* h_out) {
     PI_CHECK_HANDLE(h);
@@ -1243,44 +1269,62 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
         return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_attn_layer_forward: %d + %d tokens exceed the layer cache of %d",
                     L->seq_len, n_tokens, L->max_pages * pi::kPageTokens);
     hipStream_t s = h->stream;
-    PI_HIP(h, hipSetDevice(h->device), "pi_attn_layer_forward");
+    const char* what = "pi_attn_layer_forward";
+    PI_HIP(h, hipSetDevice(h->device), what);
     const int D = L->dim;
     const size_t nq = (size_t)n_tokens * L->n_heads * D, nk = (size_t)n_tokens * L->n_kv * D;
-    // distinct widths: the host slices arrive whole (one copy each) in a raw region and
-    // are packed on the device (2D copies from pageable memory would go row by row)
+    // Slices as the caller holds them: q and gate [n][Hq][q_dim], v [n][Hkv][v_dim].  With
+    // distinct widths they arrive whole in "io" regions and are packed on the device (2D
+    // copies from pageable memory would go row by row).
     const bool packed = L->q_dim == D && L->v_dim == D;
-    const size_t rq = packed ? 0 : (size_t)n_tokens * L->n_heads * L->q_dim;
-    const size_t rv = packed ? 0 : (size_t)n_tokens * L->n_kv * L->v_dim;
-    int rc = grow(h, &L->d_buf, &L->buf_floats, 3 * nq + 2 * nk + 2 * rq + rv, s,
-                  "pi_attn_layer_forward staging", false);
+    const size_t qin = (size_t)n_tokens * L->n_heads * L->q_dim;
+    const size_t vin = (size_t)n_tokens * L->n_kv * L->v_dim;
+    const size_t gin = h_gate ? qin : 0;
+    // device staging: [out | q io | k | v io | gate io] (+ packed q, v, gate for distinct widths),
+    // so the inputs (q, k, v, gate) and the outputs (out, q, k) are each one contiguous run
+    const size_t need = nq + qin + nk + vin + qin + (packed ? 0 : 2 * nq + nk);
+    int rc = grow(h, &L->d_buf, &L->buf_floats, need, s, "pi_attn_layer_forward staging", false);
     if (rc) return rc;
-    float *dq = L->d_buf, *dg = dq + nq, *dout = dg + nq, *dk = dout + nq, *dv = dk + nk;
-    float *raw_q = dv + nk, *raw_g = raw_q + rq, *raw_v = raw_g + rq;
-    const char* what = "pi_attn_layer_forward";
-    if (packed) {
-        if ((rc = copy_sync(h, dq, h_q, nq * 4, hipMemcpyHostToDevice, what))) return rc;
-        if ((rc = copy_sync(h, dv, h_v, nk * 4, hipMemcpyHostToDevice, what))) return rc;
-        if (h_gate && (rc = copy_sync(h, dg, h_gate, nq * 4, hipMemcpyHostToDevice, what))) return rc;
-    } else {
-        if ((rc = copy_sync(h, raw_q, h_q, rq * 4, hipMemcpyHostToDevice, what))) return rc;
-        if ((rc = copy_sync(h, raw_v, h_v, rv * 4, hipMemcpyHostToDevice, what))) return rc;
-        if (h_gate && (rc = copy_sync(h, raw_g, h_gate, rq * 4, hipMemcpyHostToDevice, what))) return rc;
-        if ((rc = pack_layer_inputs(h, L, raw_q, raw_v, h_gate ? raw_g : nullptr, n_tokens, dq, dv, dg,
-                                    hipMemcpyDeviceToDevice, s, what)))
-            return rc;
+    float *dout = L->d_buf, *qio = dout + nq, *dk = qio + qin, *vio = dk + nk, *gio = vio + vin;
+    float *dq = qio, *dv = vio, *dg = gio;
+    if (!packed) {
+        dq = gio + qin;
+        dv = dq + nq;
+        dg = dv + nk;
     }
-    if ((rc = copy_sync(h, dk, h_k, nk * 4, hipMemcpyHostToDevice, what))) return rc;
+    const size_t in_f = qin + nk + vin + gin, out_f = nq + qin + nk;
+    const bool pin = pinned_staging(h, std::max(in_f, out_f));
+    if (pin) {
+        float* p = h->pin;
+        std::memcpy(p, h_q, qin * 4);
+        std::memcpy(p + qin, h_k, nk * 4);
+        std::memcpy(p + qin + nk, h_v, vin * 4);
+        if (h_gate) std::memcpy(p + qin + nk + vin, h_gate, gin * 4);
+        if ((rc = copy_sync(h, qio, p, in_f * 4, hipMemcpyHostToDevice, what))) return rc;
+    } else {
+        if ((rc = copy_sync(h, qio, h_q, qin * 4, hipMemcpyHostToDevice, what))) return rc;
+        if ((rc = copy_sync(h, dk, h_k, nk * 4, hipMemcpyHostToDevice, what))) return rc;
+        if ((rc = copy_sync(h, vio, h_v, vin * 4, hipMemcpyHostToDevice, what))) return rc;
+        if (h_gate && (rc = copy_sync(h, gio, h_gate, gin * 4, hipMemcpyHostToDevice, what))) return rc;
+    }
+    if (!packed && (rc = pack_layer_inputs(h, L, qio, vio, h_gate ? gio : nullptr, n_tokens, dq, dv, dg,
+                                           hipMemcpyDeviceToDevice, s, what)))
+        return rc;
     if ((rc = attn_layer_step(h, L, dq, dk, dv, h_gate ? dg : nullptr, n_tokens, dout, s))) return rc;
-    if ((rc = copy_sync(h, h_out, dout, nq * 4, hipMemcpyDeviceToHost, what))) return rc;
-    // q and k come back normalised and rotated (only the first head_dim dims of a query head)
-    if (packed) {
-        if ((rc = copy_sync(h, h_q, dq, nq * 4, hipMemcpyDeviceToHost, what))) return rc;
-    } else {
-        if ((rc = copy_rows(h, raw_q, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads,
-                            hipMemcpyDeviceToDevice, s, what)))
-            return rc;
-        if ((rc = copy_sync(h, h_q, raw_q, rq * 4, hipMemcpyDeviceToHost, what))) return rc;
+    // q and k go back normalised and rotated (only the first head_dim dims of a query head)
+    if (!packed && (rc = copy_rows(h, qio, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads,
+                                   hipMemcpyDeviceToDevice, s, what)))
+        return rc;
+    if (pin) {
+        if ((rc = copy_sync(h, h->pin, dout, out_f * 4, hipMemcpyDeviceToHost, what))) return rc;
+        PI_HIP(h, hipStreamSynchronize(s), what);
+        std::memcpy(h_out, h->pin, nq * 4);
+        std::memcpy(h_q, h->pin + nq, qin * 4);
+        std::memcpy(h_k, h->pin + nq + qin, nk * 4);
+        return PI_OK;
     }
+    if ((rc = copy_sync(h, h_out, dout, nq * 4, hipMemcpyDeviceToHost, what))) return rc;
+    if ((rc = copy_sync(h, h_q, qio, qin * 4, hipMemcpyDeviceToHost, what))) return rc;
     if ((rc = copy_sync(h, h_k, dk, nk * 4, hipMemcpyDeviceToHost, what))) return rc;
     PI_HIP(h, hipStreamSynchronize(s), what);
     return PI_OK;
@@ -1396,9 +1440,15 @@ static int gdn_layer_step(pi_handle h, pi_gdn_layer L, const float* dx, const fl
     float *db = dv + n * vd, *dg = db + n * nh;
     if ((rc = pi_gdn_conv1d(h, dx, L->d_conv_state, L->d_w, act, 1, n_tokens, (int32_t)C, L->d_conv, sv)))
         return rc;
-    PI_HIP(h, hipMemcpy2DAsync(dq, kd * 4, act, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
-    PI_HIP(h, hipMemcpy2DAsync(dk, kd * 4, act + kd, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
-    PI_HIP(h, hipMemcpy2DAsync(dv, vd * 4, act + 2 * kd, C * 4, vd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
+    if (n == 1) {  // one token's row already holds q, k and v back to back
+        dq = act;
+        dk = act + kd;
+        dv = act + 2 * kd;
+    } else {
+        PI_HIP(h, hipMemcpy2DAsync(dq, kd * 4, act, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
+        PI_HIP(h, hipMemcpy2DAsync(dk, kd * 4, act + kd, C * 4, kd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
+        PI_HIP(h, hipMemcpy2DAsync(dv, vd * 4, act + 2 * kd, C * 4, vd * 4, n, hipMemcpyDeviceToDevice, s), "gdn layer");
+    }
     if ((rc = pi_gdn_gates(h, dbr, dar, L->d_ssm_a, L->d_dt, db, dg, n_tokens, L->hv, sv))) return rc;
     if (n_tokens > 1)
         rc = pi_gdn_prefill(h, dq, dk, dv, db, dg, L->d_state, dout, n_tokens, L->hk, L->hv, L->dk,
@@ -1427,11 +1477,27 @@ int pi_gdn_layer_forward(pi_handle h, pi_gdn_layer L, const float* h_qkv, const 
     if (rc) return rc;
     float *dx = h->h2d_scratch, *dz = dx + n * C, *dbr = dz + n * vd, *dar = dbr + n * nh;
     float* dout = dar + n * nh;
-    if ((rc = copy_sync(h, dx, h_qkv, n * C * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
-    if ((rc = copy_sync(h, dz, h_z, n * vd * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
-    if ((rc = copy_sync(h, dbr, h_beta_raw, n * nh * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
-    if ((rc = copy_sync(h, dar, h_a_raw, n * nh * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+    const size_t in_f = n * C + n * vd + 2 * n * nh;
+    const bool pin = pinned_staging(h, in_f);  // the four inputs as one copy (small calls)
+    if (pin) {
+        std::memcpy(h->pin, h_qkv, n * C * 4);
+        std::memcpy(h->pin + n * C, h_z, n * vd * 4);
+        std::memcpy(h->pin + n * C + n * vd, h_beta_raw, n * nh * 4);
+        std::memcpy(h->pin + n * C + n * vd + n * nh, h_a_raw, n * nh * 4);
+        if ((rc = copy_sync(h, dx, h->pin, in_f * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+    } else {
+        if ((rc = copy_sync(h, dx, h_qkv, n * C * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+        if ((rc = copy_sync(h, dz, h_z, n * vd * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+        if ((rc = copy_sync(h, dbr, h_beta_raw, n * nh * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+        if ((rc = copy_sync(h, dar, h_a_raw, n * nh * 4, hipMemcpyHostToDevice, "pi_gdn_layer_forward"))) return rc;
+    }
     if ((rc = gdn_layer_step(h, L, dx, dz, dbr, dar, n_tokens, dout, s))) return rc;
+    if (pin && n * vd <= h->pin_floats) {
+        if ((rc = copy_sync(h, h->pin, dout, n * vd * 4, hipMemcpyDeviceToHost, "pi_gdn_layer_forward"))) return rc;
+        PI_HIP(h, hipStreamSynchronize(s), "pi_gdn_layer_forward");
+        std::memcpy(h_out, h->pin, n * vd * 4);
+        return PI_OK;
+    }
     if ((rc = copy_sync(h, h_out, dout, n * vd * 4, hipMemcpyDeviceToHost, "pi_gdn_layer_forward"))) return rc;
     PI_HIP(h, hipStreamSynchronize(s), "pi_gdn_layer_forward");
     return PI_OK;
