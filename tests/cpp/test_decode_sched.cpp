@@ -44,7 +44,8 @@ struct Case {
 };
 
 // Mirrors decode_kernel / decode_merge_kernel (decode.hip) step for step,
-// with the kernels' own schedule functions.
+// with the kernels' own schedule functions.  merge_runs must give exactly the
+// number of runs that write a partial (none is left out of the merge).
 bool walk(const Case& c) {
     const int batch = (int)c.ctx.size(), n_kv = c.n_kv, mp = c.max_pages, ip = c.item_pages;
     std::vector<int> s_cum(batch + 1, 0);
@@ -57,6 +58,8 @@ bool walk(const Case& c) {
     std::vector<int> page_seen((size_t)batch * n_kv * mp, 0);
     std::map<long long, std::pair<int, int>> slot_owner;  // slot -> (b, kvh)
     std::vector<char> whole((size_t)batch * n_kv, 0);
+    // runs that wrote a partial, per segment: the merge must fold every one of them
+    std::vector<int> n_partial((size_t)batch * n_kv, 0);
     // run table (workgroup of run 1, number of runs) written by the segment's first run
     std::vector<std::pair<int, int>> table((size_t)batch * n_kv, {-1, -1});
     for (int w = 0; w < c.grid && n_items > 0; ++w) {
@@ -106,6 +109,7 @@ bool walk(const Case& c) {
             } else {
                 CHECK(!slot_owner.count(slot), "%s: slot %lld written twice", c.name, slot);
                 slot_owner[slot] = {r.b, r.kvh};
+                n_partial[(size_t)r.b * n_kv + r.kvh]++;
             }
             cur = r.run_end;
         }
@@ -131,6 +135,8 @@ bool walk(const Case& c) {
                 CHECK(whole[(size_t)b * n_kv + kvh], "%s: (b %d, kvh %d) one run but not whole", c.name, b, kvh);
                 continue;
             }
+            CHECK(n_partial[(size_t)b * n_kv + kvh] == n_runs, "%s: (b %d, kvh %d) %d partial runs, table says %d",
+                  c.name, b, kvh, n_partial[(size_t)b * n_kv + kvh], n_runs);
             for (int r = 0; r < n_runs; ++r) {
                 const long long slot = run_slot(r == 0, b, kvh, n_kv, batch, wg1 + r - 1);
                 auto it = slot_owner.find(slot);
