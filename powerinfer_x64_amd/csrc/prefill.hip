@@ -4,7 +4,10 @@
 // per prompt token (src/model/mod.rs:668 token loop, :1140-1190 append-then-
 // attend), i.e. row i attends keys 0..i.
 //
-// One kernel, prefill_fa_kernel (below): a workgroup of 8 wavefronts covers
+// Head dim 128 runs prefill_fa_kernel (below), head dim 256 prefill_fa256_kernel
+// (16 query rows per wavefront, the same two-phase schedule).
+//
+// prefill_fa_kernel: a workgroup of 8 wavefronts covers
 // HPW query heads that share one KV head and 256/HPW query positions; each
 // wavefront owns 32 query rows of one head and computes, per 64-key tile,
 //   S^T[64 key x 32 q] = K . Q^T          (16 x v_mfma_f32_32x32x16)
@@ -540,6 +543,385 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
 }
 
 // ---------------------------------------------------------------------------
+// prefill_fa256_kernel: head dim 256 with two wavefronts per SIMD.  At 32 query
+// rows a wavefront's O and Q^T alone take 192 registers, so prefill_fa_kernel
+// runs D = 256 with one wavefront per SIMD, whose MFMA and softmax phases then
+// cannot overlap.  Here a wavefront owns 16 query rows on
+// v_mfma_f32_16x16x32 (O^T 64 registers, Q^T 32), so the workgroup has 8
+// wavefronts (two per SIMD, in opposite phases as in prefill_fa_kernel) and
+// covers the same 128 query rows per head set.  Per 64-key tile and wavefront:
+//   S^T[64 key x 16 q] = K . Q^T    (4 key blocks x 8 dim steps = 32 MFMAs)
+//   O^T[256 x 16 q]   += V^T . P^T  (16 dim blocks x 2 key steps = 32 MFMAs)
+// A lane holds query column lane % 16 and keys 16 kb + 4 (lane / 16) + r of
+// each key block kb, so the P^T operand of key step j is the lane's own P of
+// blocks 2j and 2j+1 (contraction slot 8 g + i is key 32 j + 4 g + i, slot
+// 8 g + 4 + i key 32 j + 16 + 4 g + i), and the row max / sum need two
+// cross-lane steps.  Units (K of tile u, V of tile u - 1) live in two LDS
+// buffers: K rows padded to 528 bytes as in prefill_fa_kernel, V rows of 512
+// bytes whose 16-byte chunks sit at chunk ^ 2 (row % 8), so the 16 rows one
+// transposing read touches fall on 8 distinct bank groups.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Mfma16;
+template <>
+struct Mfma16<bf16> {
+    static __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Mfma16<f16> {
+    static __device__ __forceinline__ f32x4 mma(f16x8 a, f16x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+__device__ __forceinline__ float max16(const f32x4* s) {
+    const float a = vmax3(s[0][0], s[0][1], s[0][2]), b = vmax3(s[0][3], s[1][0], s[1][1]);
+    const float c = vmax3(s[1][2], s[1][3], s[2][0]), d = vmax3(s[2][1], s[2][2], s[2][3]);
+    const float e = vmax3(s[3][0], s[3][1], s[3][2]);
+    return vmax3(vmax3(a, b, c), vmax3(d, e, s[3][3]), a);
+}
+
+template <typename T, int HPW>
+__global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
+    typedef typename Mfma<T>::v8 v8;
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    constexpr int D = 256, NW = 8, R = 16;  // head dim, wavefronts, query rows per wavefront
+    constexpr int RT = NW / HPW;            // row tiles per workgroup
+    constexpr int WROWS = R * RT;           // query rows per workgroup (128 / HPW)
+    constexpr int NB = 2;                   // unit buffers
+    constexpr int NDB = D / 16;             // 16-dim blocks of O^T
+    constexpr int KS = D + 8;               // K row stride (elements): 16 bytes of padding
+    constexpr int KCH = KS / 8;             // 33 16-byte chunks per K row
+    constexpr int K_INSTR = BN * KCH / 64;  // 33 direct loads of 1 KB per K tile
+    constexpr int KJ = (K_INSTR + NW - 1) / NW;
+    constexpr int V_INSTR = BN * D * 2 / 1024;  // 32 per V tile
+    constexpr int VJ = V_INSTR / NW;
+    constexpr int VRPI = 1024 / (2 * D);  // V rows per load (2)
+    constexpr int VCPR = D / 8;           // 16-byte chunks per V row (32)
+    static_assert(WROWS * HPW == 128, "the launch geometry assumes 128 rows per head set");
+    __shared__ __attribute__((aligned(1024))) T sk[NB][BN * KS];
+    __shared__ __attribute__((aligned(1024))) T sv[NB][BN * D];
+
+    {  // a head that does not exist (modulo map, HPW 1) makes the whole workgroup leave
+        const int per_kv = a.group / HPW;
+        const int hs0 = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) % HPW;
+        if (head_of((int)blockIdx.x / per_kv, ((int)blockIdx.x % per_kv) * HPW + hs0, a.hkv,
+                    a.group, a.gqa_mode) >= a.hq)
+            return;
+    }
+    const int nqb = (a.S + WROWS - 1) / WROWS;
+    const int by = blockIdx.y;
+    const int n_blocks = a.paired && by != nqb - 1 - by ? 2 : 1;
+    for (int blk = 0; blk < n_blocks; ++blk) {
+    int qb = blk == 0 ? (a.paired ? nqb - 1 - by : (int)gridDim.y - 1 - by) : by;
+    if (blk > 0) {  // the previous block's LDS reads are done before new loads land
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    }
+    int tid = threadIdx.x, bxx = blockIdx.x;
+    asm volatile("" : "+v"(tid));
+    asm volatile("" : "+s"(bxx), "+s"(qb));
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hs = wave % HPW, rt = wave / HPW;
+    const int b = (int)blockIdx.z / a.ksplit, ksp = (int)blockIdx.z % a.ksplit;
+    const int S = a.S, Sk = a.Sk, q_off = a.q_off;
+    const int per_kv = a.group / HPW;
+    const int kvh = bxx / per_kv;
+    const int head = head_of(kvh, (bxx % per_kv) * HPW + hs, a.hkv, a.group, a.gqa_mode);
+    const int p0 = qb * WROWS + rt * R;
+    const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
+    const int n_tiles = (wg_keys + BN - 1) / BN;
+    const int kper = (n_tiles + a.ksplit - 1) / a.ksplit;
+    const int tb = min(n_tiles, ksp * kper);
+    const int nloc = min(n_tiles, tb + kper) - tb;
+    const int w_keys = a.causal ? min(Sk, q_off + p0 + R) : Sk;
+    const int w_tiles = p0 < S ? (w_keys + BN - 1) / BN : 0;
+    const int t_mask = min(a.causal ? (q_off + p0 + 1) / BN : Sk / BN, Sk / BN);
+
+    const int ln = lane & 15;  // query column of this lane
+    const int g = lane >> 4;   // 8-wide contraction slice of the operands
+    const int qpos = p0 + ln;
+
+    // Q^T operand: lane holds q[qpos][32 ks + 8 g .. +7]
+    v8 qr[D / 32];
+    {
+        const T* qg = reinterpret_cast<const T*>(a.q);
+        const bool ok = qpos < S;
+        const T* qrow = qg + (((size_t)b * S + (ok ? qpos : 0)) * a.hq + head) * D;
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            v8 t = *reinterpret_cast<const v8*>(qrow + 32 * ks + 8 * g);
+            if (!ok) t = v8{};
+            qr[ks] = t;
+        }
+    }
+    f32x4 o[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -1e30f, l_run = 0.f;
+
+    const size_t tok_stride = (size_t)a.hkv * D;
+    const T* kbase = reinterpret_cast<const T*>(a.k) + ((size_t)b * Sk * a.hkv + kvh) * D;
+    const T* vbase = reinterpret_cast<const T*>(a.v) + ((size_t)b * Sk * a.hkv + kvh) * D;
+
+    typedef __attribute__((address_space(3))) void lds_void;
+    // direct global -> LDS loads from inline assembly (no compiler waits before LDS
+    // reads; M0 saved and restored); base and LDS address pinned to scalar registers
+    auto dma16 = [](const void* src, lds_void* dst) {
+        const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)dst);
+        unsigned saved;
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\t"
+                     "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+    };
+    auto dma16s = [](const void* base, unsigned voff, lds_void* dst) {
+        const uintptr_t bp = (uintptr_t)base;
+        const unsigned blo = __builtin_amdgcn_readfirstlane((unsigned)bp);
+        const unsigned bhi = __builtin_amdgcn_readfirstlane((unsigned)(bp >> 32));
+        base = (const void*)(((uintptr_t)bhi << 32) | blo);
+        const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)dst);
+        unsigned saved;
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+                     "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(voff), "s"(base), "s"(lds) : "memory");
+    };
+    int k_row[KJ], v_row[VJ];
+    unsigned k_off[KJ], v_off[VJ];
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+        const int i = wave + NW * j;
+        const int L = 64 * (i < K_INSTR ? i : 0) + lane;
+        const int row = L / KCH, ch = L - row * KCH;
+        k_row[j] = row;
+        k_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * (ch < KCH - 1 ? ch : 0)) * sizeof(T));
+    }
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+        const int i = VJ * wave + j;
+        const int row = VRPI * i + lane / VCPR;
+        const int cc = (lane % VCPR) ^ (2 * (row & 7));
+        v_row[j] = row;
+        v_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * cc) * sizeof(T));
+    }
+    auto issue_unit = [&](int u) {
+        const int buf = u % NB;
+        const int k0 = (tb + u) * BN;
+        if (k0 + BN <= Sk) {
+            const T* kb = kbase + (size_t)k0 * tok_stride;
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) {
+                const int i = wave + NW * j;
+                if (i < K_INSTR) dma16s(kb, k_off[j], (lds_void*)&sk[buf][512 * i]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) {
+                const int i = wave + NW * j;
+                if (i < K_INSTR) {
+                    const int key = min(k0 + k_row[j], Sk - 1);
+                    const T* src = kbase + (size_t)key * tok_stride +
+                                   (k_off[j] - (size_t)k_row[j] * tok_stride * sizeof(T)) / sizeof(T);
+                    dma16(src, (lds_void*)&sk[buf][512 * i]);
+                }
+            }
+        }
+        if (u >= 1) {
+            const int v0 = k0 - BN;
+            const T* vb = vbase + (size_t)v0 * tok_stride;
+            if (v0 + BN <= Sk) {
+#pragma unroll
+                for (int j = 0; j < VJ; ++j) dma16s(vb, v_off[j], (lds_void*)&sv[buf][512 * (VJ * wave + j)]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < VJ; ++j) {
+                    const int key = min(v0 + v_row[j], Sk - 1);
+                    const T* src = vbase + (size_t)key * tok_stride +
+                                   (v_off[j] - (size_t)v_row[j] * tok_stride * sizeof(T)) / sizeof(T);
+                    dma16(src, (lds_void*)&sv[buf][512 * (VJ * wave + j)]);
+                }
+            }
+        }
+    };
+    auto barrier = [&]() {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    const float c = a.qk_scale;
+    typedef __attribute__((address_space(3))) const T* lds_ptr;
+    typedef __attribute__((address_space(3))) const v8* lds_v8;
+    typedef __attribute__((address_space(3))) s4* lds_s4;
+    // K operand of key block kb, dim step ks: row 16 kb + ln, elements 32 ks + 8 g .. +7
+    const lds_ptr k_lane = (lds_ptr)&sk[0][ln * KS + 8 * g];
+    // MFMA i of a QK phase: key block i % 4, dim step i / 4 (four independent accumulators)
+    auto kfrag = [&](lds_ptr kt, int i) {
+        return *reinterpret_cast<lds_v8>(kt + (i & 3) * 16 * KS + (i >> 2) * 32);
+    };
+    // V^T operand of dim block db, key step j by two transposing reads: in the
+    // 16-lane group g, lane j' points at key row 32 j + 4 g + j' / 4 (+ 16 for the
+    // second read), dims 16 db + 4 (j' % 4) .. +3; lane i then holds 4 keys of dim
+    // 16 db + i.  Rows 32 j + 4 g + j'/4 and that + 16 share row % 8.
+    const int vrow = 4 * g + (ln >> 2);
+    const int vsw = 2 * (vrow & 7);
+    auto vfrag = [&](int buf, int i) {  // MFMA i of a PV phase: dim block i % 16, key step i / 16
+        const int db = i % NDB, j = i / NDB;
+        const int ch = (2 * db + ((ln & 3) >> 1)) ^ vsw;
+        const lds_ptr base = (lds_ptr)&sv[buf][0] + (32 * j + vrow) * D + 8 * ch + 4 * (ln & 1);
+        const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)base);
+        const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(base + 16 * D));
+        typedef typename Mfma<T>::v4 v4;
+        const v4 l4 = __builtin_bit_cast(v4, lo), h4 = __builtin_bit_cast(v4, hi);
+        return v8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+    };
+    constexpr int PF = 4;
+
+    f32x4 s[4];
+    v8 pb[2];  // P^T operand of the tile whose PV is pending
+    auto run_pv = [&](int buf) {
+        constexpr int NM = 2 * NDB;  // 32 MFMAs: 16 dim blocks x 2 key steps
+        v8 vf[PF];
+#pragma unroll
+        for (int i = 0; i < PF; ++i) vf[i] = vfrag(buf, i);
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            const v8 va = vf[i % PF];
+            if (i + PF < NM) vf[i % PF] = vfrag(buf, i + PF);
+            o[i % NDB] = Mfma16<T>::mma(va, pb[i / NDB], o[i % NDB]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
+#pragma unroll
+        for (int i = 0; i < NM - PF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+    };
+    auto run_qk = [&](int buf) {
+        constexpr int NM = 4 * (D / 32);  // 32 MFMAs: 4 key blocks x 8 dim steps
+        const lds_ptr kt = k_lane + buf * (BN * KS);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        v8 kf[PF];
+#pragma unroll
+        for (int i = 0; i < PF; ++i) kf[i] = kfrag(kt, i);
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            const v8 ka = kf[i % PF];
+            if (i + PF < NM) kf[i % PF] = kfrag(kt, i + PF);
+            s[i & 3] = Mfma16<T>::mma(ka, qr[i >> 2], s[i & 3]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+        for (int i = 0; i < NM - PF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+    };
+    auto phase_softmax = [&](int t, bool masked) {
+        const int k0 = t * BN;
+        if (masked) {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * kb + 4 * g + r;
+                    if (key >= Sk || (a.causal && key > q_off + qpos)) s[kb][r] = -INFINITY;
+                }
+        }
+        float mx = max16(s);
+        if (__any(mx * c > m_run + kLazy)) {
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m_run, mx * c);
+            const float alpha = fast_exp2(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < NDB; ++i) o[i] *= alpha;
+            m_run = m_new;
+        }
+        float ls[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float p[8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p[r] = fast_exp2(__builtin_fmaf(s[2 * j][r], c, -m_run));
+                p[4 + r] = fast_exp2(__builtin_fmaf(s[2 * j + 1][r], c, -m_run));
+            }
+#pragma unroll
+            for (int r = 0; r < 8; ++r) pb[j][r] = (T)p[r];
+            ls[j] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        }
+        l_run += ls[0] + ls[1];
+    };
+    auto mfma_phase = [&](int t) {
+        const bool pv = t >= 1 && tb + t - 1 < w_tiles;
+        const bool qk = t < nloc && tb + t < w_tiles;
+        __builtin_amdgcn_s_setprio(2);
+        if (pv) run_pv(t % NB);
+        if (qk) run_qk(t % NB);
+        __builtin_amdgcn_s_setprio(0);
+    };
+
+    issue_unit(0);
+    __builtin_amdgcn_s_waitcnt(0);  // all counters (Q loads, unit 0)
+    barrier();
+    // One barrier per tile step t = 0 .. nloc.  Lead waves (0-3): the MFMA phase of
+    // tile t, then its softmax; lag waves (4-7): the softmax of tile t-1, then the
+    // MFMA phase of tile t.  Each wave issues its loads of unit t+1 after its
+    // softmax (the buffer's previous unit, t-1, was last read in step t-1) and waits
+    // for them before the barrier.
+    if (wave < NW / 2) {
+        for (int t = 0; t <= nloc; ++t) {
+            mfma_phase(t);
+            if (t < nloc && tb + t < w_tiles) phase_softmax(tb + t, tb + t >= t_mask);
+            if (t + 1 <= nloc) issue_unit(t + 1);
+            if (t < nloc) {
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+                barrier();
+            }
+        }
+    } else {
+        for (int t = 0; t <= nloc; ++t) {
+            if (t >= 1 && tb + t - 1 < w_tiles) phase_softmax(tb + t - 1, tb + t - 1 >= t_mask);
+            if (t + 1 <= nloc) issue_unit(t + 1);
+            mfma_phase(t);
+            if (t < nloc) {
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+                barrier();
+            }
+        }
+    }
+
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (a.ksplit > 1) {  // unnormalised partial of this key split
+        if (qpos < S) {
+            const size_t row = (((size_t)ksp * (gridDim.z / a.ksplit) + b) * S + qpos) * a.hq + head;
+            float* po = a.part_o + row * D;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) *reinterpret_cast<f32x4*>(po + 16 * db + 4 * g) = o[db];
+            if (g == 0) {
+                a.part_ml[2 * row] = m_run;
+                a.part_ml[2 * row + 1] = l_run;
+            }
+        }
+    } else if (qpos < S) {
+        const float inv = 1.0f / l_run;
+        float* orow = a.out + (((size_t)b * S + qpos) * a.hq + head) * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db] * inv;
+    }
+    }  // query blocks of this workgroup
+}
+
+// ---------------------------------------------------------------------------
 // prefill_f32_kernel: causal attention of a chunk of queries (f32 rows) over an
 // f32 KV pool, read through the sequence's page table (src/model/mod.rs:668
 // token loop over :1140-1190 with an f32 cache).  Products keep f32 accuracy
@@ -768,6 +1150,16 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
 }  // namespace
 
 namespace {
+// Head dim 256 runs prefill_fa256_kernel (two wavefronts per SIMD); PI_PREFILL_FA256=0
+// selects the one-wavefront-per-SIMD prefill_fa_kernel<., ., 256> instead.
+bool use_fa256() {
+    static const bool on = [] {
+        const char* e = std::getenv("PI_PREFILL_FA256");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 template <int D>
 void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int batch, bool bf,
               hipStream_t s) {
@@ -779,6 +1171,25 @@ void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int ba
     const int nqb = (seq_len + rows - 1) / rows;
     const dim3 grid(n_kv_heads * (a.group / hpw), a.paired ? (nqb + 1) / 2 : nqb, batch * a.ksplit);
     const dim3 block(64 * NW);
+    if constexpr (D == 256) {
+        if (use_fa256()) {  // same grid: 128 / hpw query rows per workgroup either way
+            const dim3 block8(512);
+            switch (hpw) {
+                case 4:
+                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 4>), grid, block8, 0, s, a);
+                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 4>), grid, block8, 0, s, a);
+                    break;
+                case 2:
+                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 2>), grid, block8, 0, s, a);
+                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 2>), grid, block8, 0, s, a);
+                    break;
+                default:
+                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 1>), grid, block8, 0, s, a);
+                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 1>), grid, block8, 0, s, a);
+            }
+            return;
+        }
+    }
     switch (hpw) {
         case 4:
             if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 4, D>), grid, block, 0, s, a);

@@ -134,6 +134,32 @@ def test_prefill_head_dim_256(s, dtype):
     assert mism == 0
 
 
+def test_prefill_head_dim_256_4096_sampled_rows():
+    """The config-4 layer shape at S 4096 (16/2 heads, D 256): the launch pairs a heavy and a
+    light query block per workgroup; rows sampled across the prompt, every block edge."""
+    rng = np.random.default_rng(0x5EED0007)
+    tq, tk, tv = _inputs(rng, 4096, 16, 2, 256, theta=1e7)
+    out = _run(tq, tk, tv)
+    rows = [0, 1, 15, 16, 17, 31, 32, 63, 64, 127, 128, 2047, 2048, 2049, 4064, 4094, 4095]
+    rows += list(np.random.default_rng(6).integers(0, 4096, 15))
+    ref = _oracle_rows(tq, tk, tv, rows)
+    assert row_rel_err(out[rows], ref) <= 1e-2
+    n, mism, ties = argmax_agreement(out[rows], ref)
+    assert mism == 0
+    assert np.isfinite(out).all()
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 2), (3, 3), (5, 2)])
+def test_prefill_head_dim_256_groupings(hq, hkv):
+    """D 256 with two query heads per KV head (2-head workgroups), one (1-head workgroups) and
+    a modulo map whose head count is not a multiple of the KV heads."""
+    rng = np.random.default_rng(hq * 11 + hkv)
+    tq, tk, tv = _inputs(rng, 180, hq, hkv, 256)
+    out = _run(tq, tk, tv)
+    ref = _oracle_rows(tq, tk, tv, range(180))
+    assert row_rel_err(out, ref) <= 1e-2
+
+
 def test_prefill_head_dim_256_noncausal_grouped_vs_f64():
     rng = np.random.default_rng(23)
     tq, tk, tv = _inputs(rng, 150, 8, 2, 256)
