@@ -557,9 +557,12 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
 // blocks 2j and 2j+1 (contraction slot 8 g + i is key 32 j + 4 g + i, slot
 // 8 g + 4 + i key 32 j + 16 + 4 g + i), and the row max / sum need two
 // cross-lane steps.  Units (K of tile u, V of tile u - 1) live in two LDS
-// buffers: K rows padded to 528 bytes as in prefill_fa_kernel, V rows of 512
-// bytes whose 16-byte chunks sit at chunk ^ 2 (row % 8), so the 16 rows one
-// transposing read touches fall on 8 distinct bank groups.
+// buffers: K rows padded to 544 bytes (two rows apart differ by 2 16-byte
+// chunks of banks, so the K reads, 16 rows x 4 chunks per instruction, have no
+// bank conflicts; the 528-byte rows of prefill_fa_kernel lost 0.2 of the LDS
+// cycles to conflicts here), V rows of 512 bytes whose 16-byte chunks sit at
+// chunk ^ 2 (row % 8), so the 16 rows one transposing read touches fall on 8
+// distinct bank groups.
 // ---------------------------------------------------------------------------
 template <typename T>
 struct Mfma16;
@@ -592,9 +595,9 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
     constexpr int WROWS = R * RT;           // query rows per workgroup (128 / HPW)
     constexpr int NB = 2;                   // unit buffers
     constexpr int NDB = D / 16;             // 16-dim blocks of O^T
-    constexpr int KS = D + 8;               // K row stride (elements): 16 bytes of padding
-    constexpr int KCH = KS / 8;             // 33 16-byte chunks per K row
-    constexpr int K_INSTR = BN * KCH / 64;  // 33 direct loads of 1 KB per K tile
+    constexpr int KS = D + 16;              // K row stride (elements): 32 bytes of padding
+    constexpr int KCH = KS / 8;             // 34 16-byte chunks per K row
+    constexpr int K_INSTR = BN * KCH / 64;  // 34 direct loads of 1 KB per K tile
     constexpr int KJ = (K_INSTR + NW - 1) / NW;
     constexpr int V_INSTR = BN * D * 2 / 1024;  // 32 per V tile
     constexpr int VJ = V_INSTR / NW;
@@ -697,7 +700,8 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
         const int L = 64 * (i < K_INSTR ? i : 0) + lane;
         const int row = L / KCH, ch = L - row * KCH;
         k_row[j] = row;
-        k_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * (ch < KCH - 1 ? ch : 0)) * sizeof(T));
+        // the two pad chunks of a row reload its chunks 0 and 1
+        k_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * (ch < D / 8 ? ch : ch - D / 8)) * sizeof(T));
     }
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
