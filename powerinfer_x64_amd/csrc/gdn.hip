@@ -504,7 +504,9 @@ constexpr int GC = 64;          // chunk length
 constexpr int KS_ = DK + 4;     // LDS row stride of [64][128] tiles
 constexpr int TS_ = GC + 4;     // LDS row stride of [64][64] / [16][64] tiles
 constexpr int SCOLS = 16;       // state columns per scan workgroup
-constexpr int KH_ = DK + 8;     // f16 row stride of [rows][128] f16 tiles (272 B)
+// f16 row stride of [rows][128] f16 tiles (288 B): two rows apart differ by two 16-byte
+// chunks of LDS banks, so the 16-row x 4-chunk MFMA operand reads are conflict-free
+constexpr int KH_ = DK + 16;
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -552,7 +554,7 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
     __shared__ __attribute__((aligned(16))) float sqk[GC * TS_];  // Q K^T (lower tiles)
     __shared__ float slg[2][GC], sb[2][GC];
     // phase A: the normalised k / q rows as f16 hi + lo parts (row stride KH_
-    // halves, 272 bytes: conflict-free 16-byte reads down 16 rows)
+    // halves, 288 bytes: conflict-free 16-byte reads down 16 rows)
     f16* skh = reinterpret_cast<f16*>(s_big);
     f16* skl = skh + GC * KH_;
     f16* sqh = skl + GC * KH_;
@@ -795,7 +797,7 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
 // wait (Q side in phase 2, K side in phase 3); K^T comes from transposing
 // reads of the k tile.  The small per-chunk loads are unmasked (clamped), so
 // no compiler-inserted wait lands inside a phase.
-constexpr int KT_ = GC + 8;  // f16 row stride of the [16][64] R^T, Delta^T tiles (144 B)
+constexpr int KT_ = GC + 16;  // f16 row stride of the [16][64] R^T, Delta^T tiles (160 B, as KH_)
 
 __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__ q,
                                                        const float* __restrict__ k,

@@ -955,8 +955,10 @@ struct PrefillF32Args {
 template <int D>
 __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillF32Args a) {
     constexpr int TK = 32;          // keys per tile (two pages)
-    constexpr int KST = D + 8;      // K row stride (bf16)
-    constexpr int VST = TK + 4;     // V^T row stride (bf16)
+    // Row strides (bf16) chosen so that the 16-row x 4-chunk operand reads and the staging
+    // writes fall on distinct LDS banks: K rows of D + 16, V^T rows of 40 (80 bytes).
+    constexpr int KST = D + 16;     // K row stride (bf16)
+    constexpr int VST = TK + 8;     // V^T row stride (bf16)
     constexpr int NF = 2 * TK * D / 4 / 256;  // float4 loads per thread per tile (K and V)
     constexpr int NKS = D / 32;     // 32-dim steps of Q.K
     constexpr int NDB = D / 16;     // 16-dim blocks of O^T
