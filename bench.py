@@ -9,8 +9,8 @@ batch with K/V already resident in HBM.  `value` is algorithmic bytes (K and V
 of every cached token once, q, out, page-table entries) per second.
 
 Also reported (same line, "prefill"/"workloads"): config 3 causal prefill
-TFLOP/s, the all-32k variant of config 2, config 4 gated decode, config 1,
-and the gated-DeltaNet decode step.  Inputs are synthetic N(0,1) generated on
+TFLOP/s, the config-4 layer's prefill at head dim 256, the all-32k variant of
+config 2, config 4 gated decode, config 1, and the gated-DeltaNet decode step.  Inputs are synthetic N(0,1) generated on
 the GPU from fixed seeds; RoPE is applied by the library's own kernel.
 
 Timing: after `warmup` calls and a synchronize, one HIP event pair on the
@@ -1127,7 +1127,7 @@ def main():
     # CPU baseline budget (seconds of single-core oracle work) per workload
     cs = a.cpu_seconds
     share = {"c2": 0.25, "c2_32k": 0.04, "c3": 0.15, "c4": 0.1, "c1": 0.03, "gdn_dec": 0.04,
-             "gdn_pre": 0.1, "tq": 0.07, "rows_f": 0.2, "chunk": 0.04}
+             "gdn_pre": 0.1, "tq": 0.07, "rows_f": 0.2, "chunk": 0.04, "c4_pre": 0.05}
     budget = {k: v * cs for k, v in share.items()}
     t_all0 = time.perf_counter()
 
@@ -1187,6 +1187,11 @@ def main():
                            "ms_per_step": round(pf["ms_per_step"], 4),
                            "tokens_per_s": round(pf["tokens_per_s"], 1),
                            "cpu_baseline": pf["cpu_baseline"]}
+        # the config-4 attention layer's prompt: causal prefill at head dim 256, S 4096, 16/2 heads
+        wl["c4_layer_prefill_4096_d256"] = bench_prefill(torch, rt, dev, timer, 4096, 16, 2, 256, 1e7,
+                                                         0x5EED0007, a.steps, a.warmup,
+                                                         cpu_s=budget["c4_pre"])
+        torch.cuda.empty_cache()
         r4, st = bench_decode(torch, rt, dev, timer, [65536] * 8, 16, 2, 256, 1e7, 0x5EED0003,
                               a.steps, a.warmup, sections=[11, 11, 10, 0], rope_dim=64,
                               qk_norm=True, gate=True, cpu_s=budget["c4"])
