@@ -10,6 +10,8 @@
 //   softmax     : ops::softmax on one row (src/ops.rs:160-180)
 //   attn_prologue: the three above fused for a whole layer step
 //                 (src/model/mod.rs:1035-1146): norm, RoPE, append
+#include <cstdlib>
+
 #include "pi_device.hpp"
 #include "pi_launch.hpp"
 
@@ -286,6 +288,162 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     }
 }
 
+// The same prologue with each head row in registers: lane l holds the EPL =
+// D / 64 consecutive values EPL l .. +EPL-1, loaded and stored as one vector,
+// so a row needs no LDS staging and no wave barriers.  The RMS norm reduces
+// across the wavefront; NORM pairs (2i, 2i+1) lie in one lane (EPL >= 2) or
+// in lanes l, l ^ 1 (EPL = 1); NeoX pairs (i, i + n_pairs) in lanes l and
+// l +- n_pairs / EPL, which needs n_pairs to be a multiple of EPL (the launch
+// falls back to attn_prologue_kernel otherwise).
+template <int N>
+__device__ __forceinline__ void load_vec(float* d, const float* s) {
+    if constexpr (N == 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(s);
+        d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+    } else if constexpr (N == 2) {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const f32x2 v = *reinterpret_cast<const f32x2*>(s);
+        d[0] = v[0]; d[1] = v[1];
+    } else {
+        d[0] = s[0];
+    }
+}
+template <int N>
+__device__ __forceinline__ void store_vec(float* d, const float* s) {
+    if constexpr (N == 4) {
+        *reinterpret_cast<f32x4*>(d) = f32x4{s[0], s[1], s[2], s[3]};
+    } else if constexpr (N == 2) {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<f32x2*>(d) = f32x2{s[0], s[1]};
+    } else {
+        d[0] = s[0];
+    }
+}
+
+template <typename PT, int EPL>
+__global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
+    float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ qn, const float* __restrict__ kn, float eps, RopeFreqs f,
+    int n_pairs, int neox, KvGeom g, const int32_t* __restrict__ pt, int max_pages,
+    const int32_t* __restrict__ start_pos, int n_seq, int n_tok, int hq) {
+    constexpr int D = 64 * EPL;
+    __shared__ float cs_s[2][128];  // cos, sin of pair i at this token's position
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int hkv = g.n_kv_heads, heads = hq + hkv;
+    const bool table = gridDim.y == 1;  // uniform per launch
+    // A prompt launch keeps each run of 16 consecutive tokens (a page of K and V when
+    // the prompt starts on a page) on one XCD: workgroups are dispatched round-robin
+    // over the 8 XCDs, and workgroup 8 (16 g + i) + x takes token 128 g + 16 x + i, so
+    // the partial-line writes of the page's 2-byte K / V values merge in that XCD's L2
+    // instead of reaching HBM from eight caches.
+    int u = blockIdx.x;
+    if (table && u < (int)(gridDim.x / 128) * 128) {
+        const int x = u & 7, m = u >> 3;
+        u = (m >> 4) * 128 + x * 16 + (m & 15);
+    }
+    const int t = u % n_tok, sq = u / n_tok;
+    const int pos = start_pos[sq] + t;
+    if (table) {
+        for (int i = threadIdx.x; i < n_pairs; i += 256) {
+            const float theta = (float)pos * f.f[i];
+            cs_s[0][i] = cosf(theta);
+            cs_s[1][i] = sinf(theta);
+        }
+        __syncthreads();
+    }
+    auto cos_sin = [&](int i, float* c, float* sn) {
+        if (table) {
+            *c = cs_s[0][i];
+            *sn = cs_s[1][i];
+        } else {
+            const float theta = (float)pos * f.f[i];
+            *c = cosf(theta);
+            *sn = sinf(theta);
+        }
+    };
+    const int e0 = EPL * lane;  // this lane's first element of a row
+    const int per = (heads + gridDim.y - 1) / gridDim.y;
+    const int h1 = min(heads, (int)(blockIdx.y + 1) * per);
+    for (int head = blockIdx.y * per + wv; head < h1; head += 4) {
+        const bool is_q = head < hq;
+        const int kvh = head - hq;
+        float* x = is_q ? q + (((size_t)sq * n_tok + t) * hq + head) * D
+                        : k + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
+        const float* nw = is_q ? qn : kn;
+        float xv[EPL];
+        load_vec<EPL>(xv, x + e0);
+        if (nw) {  // ops::rms_norm (src/ops.rs:13-27) per head
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
+            const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+            float wv_[EPL];
+            load_vec<EPL>(wv_, nw + e0);
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * wv_[j];
+        }
+        // ops::apply_rope / apply_rope_with_freqs: pair i is (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
+        if (neox) {
+            const int off = n_pairs / EPL;  // lanes between the two elements of a pair
+            const int src = lane < off ? lane + off : lane - off;
+            float pv[EPL];
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) pv[j] = __shfl(xv[j], src < 64 ? src : lane, 64);
+            if (lane < 2 * off) {
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) {
+                    const bool first = lane < off;
+                    const int i = first ? e0 + j : e0 + j - n_pairs;
+                    float c, sn;
+                    cos_sin(i, &c, &sn);
+                    xv[j] = first ? xv[j] * c - pv[j] * sn : pv[j] * sn + xv[j] * c;
+                }
+            }
+        } else if constexpr (EPL >= 2) {
+#pragma unroll
+            for (int j = 0; j < EPL; j += 2) {
+                const int i = (e0 + j) >> 1;
+                if (i < n_pairs) {
+                    float c, sn;
+                    cos_sin(i, &c, &sn);
+                    const float x0 = xv[j], x1 = xv[j + 1];
+                    xv[j] = x0 * c - x1 * sn;
+                    xv[j + 1] = x0 * sn + x1 * c;
+                }
+            }
+        } else {
+            const float pv0 = __shfl_xor(xv[0], 1, 64);
+            const int i = e0 >> 1;
+            if (i < n_pairs) {
+                float c, sn;
+                cos_sin(i, &c, &sn);
+                xv[0] = (lane & 1) ? pv0 * sn + xv[0] * c : xv[0] * c - pv0 * sn;
+            }
+        }
+        store_vec<EPL>(x + e0, xv);
+        // append-then-attend (src/model/mod.rs:1140-1146): K (normed, rotated) and V at pos
+        const int lp = pos / kPageTokens;
+        if (!is_q && pos >= 0 && lp < max_pages) {
+            const int page = pt[(size_t)sq * max_pages + lp];
+            if (page >= 0 && page < g.n_pages) {
+                const int tok = pos % kPageTokens;
+                const size_t blk = (size_t)page * hkv + kvh;
+                PT* kp = reinterpret_cast<PT*>(static_cast<char*>(g.k) + blk * g.kstride);
+                PT* vp = reinterpret_cast<PT*>(static_cast<char*>(g.v) + blk * g.vstride);
+                float vr[EPL];
+                load_vec<EPL>(vr, v + (((size_t)sq * n_tok + t) * hkv + kvh) * D + e0);
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) {
+                    kp[k_index<PT>(tok, e0 + j)] = from_f32<PT>(xv[j]);
+                    vp[v_index(tok, e0 + j)] = from_f32<PT>(vr[j]);
+                }
+            }
+        }
+    }
+}
+
 int grid_for(size_t total) {
     size_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
@@ -351,6 +509,17 @@ hipError_t launch_kv_gather(const KvGeom& g, const int32_t* page_table, int32_t 
     return hipGetLastError();
 }
 
+namespace {
+// PI_PROLOGUE_VEC=0 keeps every launch on the LDS-staged attn_prologue_kernel.
+bool use_vec_prologue() {
+    static const bool on = [] {
+        const char* e = std::getenv("PI_PROLOGUE_VEC");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+}  // namespace
+
 hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
                                 const float* k_norm_w, float eps, const RopeFreqs& freqs,
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,
@@ -362,6 +531,26 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
     if (toks > 0x7fffffffLL || n_pairs > 128) return hipErrorInvalidValue;
     const int heads = n_q_heads + g.n_kv_heads;
     const dim3 grid((unsigned)toks, toks >= 1024 ? 1u : (unsigned)((heads + 3) / 4));
+    const int epl = g.head_dim / 64;
+    // vector accesses of EPL floats need rows aligned to EPL * 4 bytes
+    const uintptr_t amask = (uintptr_t)(4 * (epl > 0 ? epl : 1) - 1);
+    const bool aligned = (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)q_norm_w |
+                           (uintptr_t)k_norm_w) & amask) == 0;
+    if ((g.head_dim == 64 || g.head_dim == 128 || g.head_dim == 256) && (!neox || n_pairs % epl == 0) &&
+        2 * n_pairs <= g.head_dim && aligned && use_vec_prologue()) {
+#define PI_PROLOGUE_VEC(PT, E)                                                                     \
+    hipLaunchKernelGGL((attn_prologue_vec_kernel<PT, E>), grid, dim3(256), 0, s, q, k, v, q_norm_w, \
+                       k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages, start_pos,    \
+                       n_seq, n_tok, n_q_heads)
+        const bool hp = g.dtype == 1;
+        switch (epl) {
+            case 1: if (hp) PI_PROLOGUE_VEC(f16, 1); else PI_PROLOGUE_VEC(float, 1); break;
+            case 2: if (hp) PI_PROLOGUE_VEC(f16, 2); else PI_PROLOGUE_VEC(float, 2); break;
+            default: if (hp) PI_PROLOGUE_VEC(f16, 4); else PI_PROLOGUE_VEC(float, 4); break;
+        }
+#undef PI_PROLOGUE_VEC
+        return hipGetLastError();
+    }
     if (g.dtype == 1)
         hipLaunchKernelGGL(attn_prologue_kernel<f16>, grid, dim3(256), 0, s, q, k, v, q_norm_w,
                            k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages,
