@@ -1167,6 +1167,9 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
                                L->max_pages, d_start, 1, n, L->n_heads, sv)))
         return rc;
     const float scale = 1.0f / std::sqrt((float)D);
+    // the prefill kernels apply a 16-byte-aligned gate where they write the output; another
+    // gate takes a launch of its own after them
+    const float* dg_fused = dg && !((uintptr_t)dg & 15) ? dg : nullptr;
     if (n > 1 && (D == 128 || D == 256) && L->kv_dtype == PI_F16) {
         // causal flash attention: f16 q rows, then K / V rows of positions 0 .. prev + n - 1
         const size_t kv_rows = (size_t)(prev + n) * L->n_kv * D;
@@ -1187,16 +1190,17 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
         if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "attention layer workspace", false)))
             return rc;
         PI_HIP(h, pi::launch_prefill(hq16, hk16, hv16, PI_F16, 1, n, prev + n, prev, L->n_heads, L->n_kv,
-                                     D, 1, L->gqa_mode, scale, dout, h->pfs_buf, h->pfs_floats, s),
+                                     D, 1, L->gqa_mode, scale, dout, h->pfs_buf, h->pfs_floats, s,
+                                     dg_fused),
                "attention layer");
         if ((rc = ws_end(h, s, "attention layer"))) return rc;
-        if (dg) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
+        if (dg && !dg_fused) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
     } else if (n > 1 && L->kv_dtype == PI_F32) {
         // causal attention straight from the f32 pages, at f32 accuracy
         PI_HIP(h, pi::launch_prefill_f32(L->pool->g, dq, L->d_pt, L->max_pages, prev, n, L->n_heads,
-                                         L->gqa_mode, scale, dout, s),
+                                         L->gqa_mode, scale, dout, s, dg_fused),
                "attention layer");
-        if (dg) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
+        if (dg && !dg_fused) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
     } else {
         // one decode row per token over the paged cache: row i sees prev + i + 1 keys
         for (int r0 = 0; r0 < n; r0 += kLayerRows) {

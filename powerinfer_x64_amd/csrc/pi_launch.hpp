@@ -153,13 +153,14 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
                           int32_t batch, int32_t seq_len, int32_t n_keys, int32_t q_off,
                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t causal,
                           int32_t gqa_mode, float scale, float* out, float* ws, size_t ws_floats,
-                          hipStream_t s);
+                          hipStream_t s, const float* gate = nullptr);
 // Causal attention of n_tok f32 query rows [n_tok][Hq][D] at positions q_off ..
 // q_off + n_tok - 1 over an f32 pool (D = 64 / 128 / 256), keys read through the
 // sequence's page-table row; products at f32 accuracy (bf16 hi + lo splits).
 hipError_t launch_prefill_f32(const KvGeom& g, const float* q, const int32_t* page_table,
                               int32_t max_pages, int32_t q_off, int32_t n_tok, int32_t n_q_heads,
-                              int32_t gqa_mode, float scale, float* out, hipStream_t s);
+                              int32_t gqa_mode, float scale, float* out, hipStream_t s,
+                              const float* gate = nullptr);
 // The f16 pool's K and V of positions 0 .. n_tok-1 of one sequence (page-table
 // row `page_table`) gathered into contiguous f16 [n_tok][Hkv][D] rows.
 hipError_t launch_kv_gather(const KvGeom& g, const int32_t* page_table, int32_t n_tok,

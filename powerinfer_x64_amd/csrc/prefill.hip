@@ -74,7 +74,12 @@ struct PrefillArgs {
     int ksplit;
     float* part_o;   // [ksplit][B][S][Hq][D]
     float* part_ml;  // [ksplit][B][S][Hq][2]
+    // optional output gate [B][S][Hq][D]: out *= 1 / (1 + exp(-gate)) (src/model/mod.rs:1192-1196),
+    // applied where the normalised output is written (the epilogue, or the merge of key splits)
+    const float* gate;
 };
+
+__device__ __forceinline__ float gate_sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
 
 __device__ __forceinline__ int head_of(int kvh, int c, int hkv, int group, int mode) {
     return mode == 0 ? kvh + c * hkv : kvh * group + c;
@@ -529,13 +534,19 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         }
     } else if (qpos < S) {
         const float inv = 1.0f / l_run;
-        float* orow = a.out + (((size_t)b * S + qpos) * a.hq + head) * D;
+        const size_t ro = (((size_t)b * S + qpos) * a.hq + head) * D;
+        float* orow = a.out + ro;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 f32x4 t = {o[dt][4 * i] * inv, o[dt][4 * i + 1] * inv, o[dt][4 * i + 2] * inv,
                            o[dt][4 * i + 3] * inv};
+                if (a.gate) {
+                    const f32x4 gt = *reinterpret_cast<const f32x4*>(a.gate + ro + 32 * dt + 8 * i + 4 * hh);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) t[e] *= gate_sigmoid(gt[e]);
+                }
                 *reinterpret_cast<f32x4*>(orow + 32 * dt + 8 * i + 4 * hh) = t;
             }
     }
@@ -918,9 +929,18 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
         }
     } else if (qpos < S) {
         const float inv = 1.0f / l_run;
-        float* orow = a.out + (((size_t)b * S + qpos) * a.hq + head) * D;
+        const size_t ro = (((size_t)b * S + qpos) * a.hq + head) * D;
+        float* orow = a.out + ro;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db] * inv;
+        for (int db = 0; db < NDB; ++db) {
+            f32x4 t = o[db] * inv;
+            if (a.gate) {
+                const f32x4 gt = *reinterpret_cast<const f32x4*>(a.gate + ro + 16 * db + 4 * g);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[e] *= gate_sigmoid(gt[e]);
+            }
+            *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = t;
+        }
     }
     }  // query blocks of this workgroup
 }
@@ -948,6 +968,7 @@ struct PrefillF32Args {
     size_t kstride, vstride;  // bytes
     const int32_t* pt;      // the sequence's page-table row
     float* out;             // [n_tok][hq][D]
+    const float* gate;      // optional [n_tok][hq][D]: out *= sigmoid(gate)
     int n_tok, q_off, max_pages, n_pages, hq, hkv, group, gqa_mode;
     float qk_scale;         // scale * log2(e)
 };
@@ -1121,10 +1142,18 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillF32Args a) {
     l_run += __shfl_xor(l_run, 32, 64);
     if (qpos >= a.n_tok) return;
     const float inv = 1.0f / l_run;
-    float* orow = a.out + ((size_t)qpos * a.hq + head) * D;
+    const size_t ro = ((size_t)qpos * a.hq + head) * D;
+    float* orow = a.out + ro;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
-        *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = o[db] * inv;
+    for (int db = 0; db < NDB; ++db) {
+        f32x4 t = o[db] * inv;
+        if (a.gate) {
+            const f32x4 gt = *reinterpret_cast<const f32x4*>(a.gate + ro + 16 * db + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[e] *= gate_sigmoid(gt[e]);
+        }
+        *reinterpret_cast<f32x4*>(orow + 16 * db + 4 * g) = t;
+    }
 }
 
 // The key splits of a prefill launch combined per (batch, query row, head): the
@@ -1134,7 +1163,7 @@ template <int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
                                                             const float* __restrict__ part_ml,
                                                             float* __restrict__ out, long long rows,
-                                                            int ksplit) {
+                                                            int ksplit, const float* __restrict__ gate) {
     constexpr int V = D / 64;
     typedef float fv __attribute__((ext_vector_type(V)));
     const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -1150,7 +1179,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
         L += w * part_ml[2 * r + 1];
         acc += w * *reinterpret_cast<const fv*>(part_o + r * D + V * lane);
     }
-    *reinterpret_cast<fv*>(out + row * D + V * lane) = acc * (1.0f / L);
+    acc *= 1.0f / L;
+    if (gate) {
+        const fv gt = *reinterpret_cast<const fv*>(gate + row * D + V * lane);
+#pragma unroll
+        for (int e = 0; e < V; ++e) acc[e] *= gate_sigmoid(gt[e]);
+    }
+    *reinterpret_cast<fv*>(out + row * D + V * lane) = acc;
 }
 
 }  // namespace
@@ -1214,7 +1249,8 @@ void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int ba
 
 hipError_t launch_prefill_f32(const KvGeom& g, const float* q, const int32_t* page_table,
                               int32_t max_pages, int32_t q_off, int32_t n_tok, int32_t n_q_heads,
-                              int32_t gqa_mode, float scale, float* out, hipStream_t s) {
+                              int32_t gqa_mode, float scale, float* out, hipStream_t s,
+                              const float* gate) {
     if (g.dtype != 0 || q_off < 0 || n_tok < 1 || max_pages < 1) return hipErrorInvalidValue;
     const bool multiple = n_q_heads % g.n_kv_heads == 0;
     if (!multiple && gqa_mode != 0) return hipErrorInvalidValue;
@@ -1226,6 +1262,7 @@ hipError_t launch_prefill_f32(const KvGeom& g, const float* q, const int32_t* pa
     a.vstride = g.vstride;
     a.pt = page_table;
     a.out = out;
+    a.gate = gate;
     a.n_tok = n_tok;
     a.q_off = q_off;
     a.max_pages = max_pages;
@@ -1302,7 +1339,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
                           int32_t batch, int32_t seq_len, int32_t n_keys, int32_t q_off,
                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t causal,
                           int32_t gqa_mode, float scale, float* out, float* ws, size_t ws_floats,
-                          hipStream_t s) {
+                          hipStream_t s, const float* gate) {
     if (head_dim != 128 && head_dim != 256) return hipErrorInvalidValue;
     if (q_off < 0 || n_keys < 1 || (causal && q_off + seq_len > n_keys)) return hipErrorInvalidValue;
     PrefillArgs a;
@@ -1327,6 +1364,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     a.paired = sc.paired;
     a.ksplit = 1;
     a.part_o = a.part_ml = nullptr;
+    a.gate = gate;
     const size_t rows = (size_t)batch * seq_len * n_q_heads;
     if (sc.ksplit > 1 && ws && ws_floats >= (size_t)sc.ksplit * rows * (head_dim + 2)) {
         a.ksplit = sc.ksplit;
@@ -1340,10 +1378,10 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     const dim3 grid((unsigned)((rows + 3) / 4));
     if (head_dim == 128)
         hipLaunchKernelGGL(prefill_merge_kernel<128>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out,
-                           (long long)rows, a.ksplit);
+                           (long long)rows, a.ksplit, gate);
     else
         hipLaunchKernelGGL(prefill_merge_kernel<256>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out,
-                           (long long)rows, a.ksplit);
+                           (long long)rows, a.ksplit, gate);
     return hipGetLastError();
 }
 

@@ -110,6 +110,28 @@ def test_layer_f32_cache_prompt_over_256_rows():
            np.random.default_rng(0x1A6), 32, 32, 128)
 
 
+def test_layer_f32_cache_gated_prompt_and_chunk():
+    """The sigmoid gate on an f32 cache's prefill (applied in the f32-cache kernel's epilogue):
+    a 150-token prompt, one decode token, then a 40-token chunk (8/2 heads, D 128)."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    layer = rt.AttnLayer(dev, 256, 8, 2, 128, torch.float32, rope_base=1e4)
+    _drive(layer, [150, 1, 40], dict(rope_base=1e4), _abs(2e-3),
+           np.random.default_rng(0x1A7), 8, 2, 128, gate=True)
+
+
+@pytest.mark.parametrize("hq,hkv,d,chunks", [(16, 2, 256, [1100, 64]), (32, 8, 128, [700, 48])])
+def test_layer_f16_cache_gated_prompt_and_key_split(hq, hkv, d, chunks):
+    """The gate of an f16 cache's flash prefill in both places it is applied: a long prompt
+    whose launch fills the chip (the gate in the prefill epilogue) and a short chunk over it
+    (a small launch whose key splits are merged, the merge applying the gate)."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    layer = rt.AttnLayer(dev, sum(chunks) + 16, hq, hkv, d, torch.float16, rope_base=1e6)
+    _drive(layer, chunks, dict(rope_base=1e6), _rel(1e-2),
+           np.random.default_rng(0x1A8 + d), hq, hkv, d, gate=True)
+
+
 def test_layer_rejects_short_norm_weights():
     """Norm weights must hold head_dim values: a shorter array is refused before anything
     reads it."""
