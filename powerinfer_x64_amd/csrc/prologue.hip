@@ -109,14 +109,25 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(KvGeom g, const int32_t*
             *reinterpret_cast<f16x8*>(k_out + ((size_t)pos * H + h) * D + 8 * c) = ok ? kb[i] : f16x8{};
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < NCH; i += 256) {
-        const int tok = i / (D / 8), c = i % (D / 8);  // output chunk: token tok, dims 8c..
-        const int pos = lp * kPageTokens + tok;
-        if (pos >= n_tok) continue;
+    // V rows out of the [D][16] block by transposing LDS reads: in the 16-lane group of
+    // dim chunk c, lane j points at dim 8c + 4e + j/4, tokens 4 (j % 4) .. +3 (e = 0, 1);
+    // lane i then holds dims 8c + 4e .. +3 of token i, and writes 16 bytes of its row.
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef f16 f16x4_ __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4* lds_s4;
+    const int j = threadIdx.x & 15, grp = threadIdx.x >> 4;  // 16 groups of 16 lanes
+    for (int c = grp; c < D / 8; c += 16) {
         f16x8 x;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sv[(8 * c + e) * kPageTokens + tok];
-        *reinterpret_cast<f16x8*>(v_out + ((size_t)pos * H + h) * D + 8 * c) = x;
+        for (int e = 0; e < 2; ++e) {
+            const f16* src = &sv[(8 * c + 4 * e + (j >> 2)) * kPageTokens + 4 * (j & 3)];
+            const s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)src);
+            const f16x4_ y = __builtin_bit_cast(f16x4_, r);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) x[4 * e + q] = y[q];
+        }
+        const int pos = lp * kPageTokens + j;
+        if (pos < n_tok) *reinterpret_cast<f16x8*>(v_out + ((size_t)pos * H + h) * D + 8 * c) = x;
     }
 }
 
