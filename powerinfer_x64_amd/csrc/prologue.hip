@@ -54,6 +54,68 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvGeom g, const ST* __re
     }
 }
 
+// Append by page block: workgroup (x, h) writes the slots that sequence x / ppn
+// appends into its (x % ppn)-th page touched (ppn = pages one call can touch:
+// ceil(n_tok / 16) + 1), K head h, as whole 16-byte chunks of the block where the
+// chunk's tokens all belong to the call, so each block is written by one
+// workgroup in full lines (the element-per-thread form spread a page's 2-byte
+// writes over every XCD's L2, and HBM took twice the bytes).  Slots outside the
+// call, positions past the table, and page ids outside the pool are left alone.
+template <typename ST, typename PT>
+__global__ __launch_bounds__(256) void kv_append_page_kernel(KvGeom g, const ST* __restrict__ k,
+                                                             const ST* __restrict__ v,
+                                                             const int32_t* __restrict__ pt,
+                                                             int max_pages,
+                                                             const int32_t* __restrict__ start_pos,
+                                                             int n_tok, int ppn) {
+    constexpr int E = 16 / (int)sizeof(PT);  // pool values per 16-byte chunk
+    typedef PT pv __attribute__((ext_vector_type(E)));
+    const int D = g.head_dim, H = g.n_kv_heads;
+    const int sq = blockIdx.x / ppn, j = blockIdx.x % ppn, h = blockIdx.y;
+    const long long start = start_pos[sq];
+    const long long first = start > 0 ? start : 0;        // positions below 0 are dropped
+    const long long lpl = first / kPageTokens + j;         // page of the sequence's table
+    if (lpl >= max_pages) return;
+    const int lp = (int)lpl;
+    const long long t0 = first > lpl * kPageTokens ? first : lpl * kPageTokens;
+    const long long t1 = start + n_tok < (lpl + 1) * kPageTokens ? start + n_tok : (lpl + 1) * kPageTokens;
+    if (t0 >= t1) return;
+    const int page = pt[(size_t)sq * max_pages + lp];
+    if (page < 0 || page >= g.n_pages) return;
+    const size_t blk = (size_t)page * H + h;
+    PT* kp = reinterpret_cast<PT*>(static_cast<char*>(g.k) + blk * g.kstride);
+    PT* vp = reinterpret_cast<PT*>(static_cast<char*>(g.v) + blk * g.vstride);
+    const int s0 = (int)(t0 - lpl * kPageTokens), s1 = (int)(t1 - lpl * kPageTokens);  // slots [s0, s1)
+    auto src = [&](const ST* base, int slot, int d) {  // the call's value of slot, dim d
+        const int t = (int)(lpl * kPageTokens + slot - start);
+        return to_f32(base[(((size_t)sq * n_tok + t) * H + h) * D + d]);
+    };
+    // K block [D / E][16][E]: chunk c = (dims E (c / 16) .., slot c % 16)
+    for (int c = threadIdx.x; c < D / E * kPageTokens; c += 256) {
+        const int slot = c % kPageTokens, d0 = E * (c / kPageTokens);
+        if (slot < s0 || slot >= s1) continue;
+        pv x;
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = from_f32<PT>(src(k, slot, d0 + e));
+        *reinterpret_cast<pv*>(kp + (size_t)E * c) = x;
+    }
+    // V block [D][16]: chunk c = (dim c / (16 / E), slots E (c % (16 / E)) ..)
+    constexpr int CPR = kPageTokens / E;  // chunks per dim row
+    for (int c = threadIdx.x; c < D * CPR; c += 256) {
+        const int d = c / CPR, sl0 = E * (c % CPR);
+        if (sl0 + E <= s0 || sl0 >= s1) continue;
+        if (sl0 >= s0 && sl0 + E <= s1) {
+            pv x;
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[e] = from_f32<PT>(src(v, sl0 + e, d));
+            *reinterpret_cast<pv*>(vp + (size_t)E * c) = x;
+        } else {  // a chunk the call covers in part: its own slots only
+            for (int e = 0; e < E; ++e)
+                if (sl0 + e >= s0 && sl0 + e < s1) vp[(size_t)E * c + e] = from_f32<PT>(src(v, sl0 + e, d));
+        }
+    }
+}
+
 template <typename PT>
 __global__ __launch_bounds__(256) void kv_read_kernel(KvGeom g, const int32_t* __restrict__ pt,
                                                       int max_pages, int seq, int start,
@@ -469,6 +531,17 @@ hipError_t append_src(const KvGeom& g, const void* k, const void* v, const int32
     const size_t total = (size_t)n_seq * n_tok * g.n_kv_heads * g.head_dim;
     const ST* ks = reinterpret_cast<const ST*>(k);
     const ST* vs = reinterpret_cast<const ST*>(v);
+    const long long ppn = (n_tok + kPageTokens - 1) / kPageTokens + 1;  // pages one sequence can touch
+    if ((long long)n_seq * ppn <= 0x7fffffffLL && g.n_kv_heads <= 65535) {
+        const dim3 grid((unsigned)(n_seq * ppn), (unsigned)g.n_kv_heads);
+        if (g.dtype == 1)
+            hipLaunchKernelGGL((kv_append_page_kernel<ST, f16>), grid, dim3(256), 0, s, g, ks, vs, pt,
+                               max_pages, sp, n_tok, (int)ppn);
+        else
+            hipLaunchKernelGGL((kv_append_page_kernel<ST, float>), grid, dim3(256), 0, s, g, ks, vs, pt,
+                               max_pages, sp, n_tok, (int)ppn);
+        return hipGetLastError();
+    }
     if (g.dtype == 1)
         hipLaunchKernelGGL((kv_append_kernel<ST, f16>), dim3(grid_for(total)), dim3(256), 0, s, g,
                            ks, vs, pt, max_pages, sp, n_seq, n_tok);

@@ -85,6 +85,55 @@ def test_kv_append_read_roundtrip(pool_dtype, src):
         np.testing.assert_array_equal(vo.cpu().numpy(), ev)
 
 
+@pytest.mark.parametrize("pool_dtype,d", [(torch.float16, 256), (torch.float16, 64),
+                                         (torch.float32, 128)])
+def test_kv_append_page_edges(pool_dtype, d):
+    """Appends that start and end inside pages, at different positions per sequence, with a
+    negative start (the positions below 0 are dropped) and rows past the table: every slot the
+    call owns holds its value, every other slot keeps what it held."""
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(7 + d)
+    hkv, n_pages, mp = 2, 30, 6
+    pool = rt.KvPool(dev, n_pages, hkv, d, dtype=pool_dtype)
+    table = rng.permutation(n_pages)[:2 * mp].reshape(2, mp).astype(np.int32)
+    pt = to_dev(table)
+    cap = 16 * mp
+    ek = np.zeros((2, cap, hkv, d), np.float32)
+    ev = np.zeros((2, cap, hkv, d), np.float32)
+
+    def append(starts, n):
+        k = rng.standard_normal((2, n, hkv, d)).astype(np.float32)
+        v = rng.standard_normal((2, n, hkv, d)).astype(np.float32)
+        pool.append(to_dev(k), to_dev(v), pt, to_dev(np.array(starts, np.int32)))
+        for s_ in range(2):
+            for t in range(n):
+                p = starts[s_] + t
+                if 0 <= p < cap:
+                    ek[s_, p] = k[s_, t]
+                    ev[s_, p] = v[s_, t]
+
+    append([0, 0], 50)      # a prompt ending inside page 3
+    append([50, 37], 7)     # continues seq 0; overwrites slots 37.. of seq 1 inside a page
+    append([-3, 57], 5)     # seq 0: positions 0 and 1 only
+    append([60, 93], 9)     # seq 1 runs past its 96-slot table: positions >= 96 dropped
+    for s_ in range(2):
+        ko, vo = pool.read(pt, s_, 0, cap)
+        torch.cuda.synchronize()
+        want_k = torch.from_numpy(ek[s_]).to(pool_dtype).float().numpy()
+        want_v = torch.from_numpy(ev[s_]).to(pool_dtype).float().numpy()
+        written = np.zeros(cap, bool)
+        if s_ == 0:
+            written[:57] = True
+            written[60:69] = True
+        else:
+            written[:50] = True
+            written[57:62] = True
+            written[93:96] = True
+        np.testing.assert_array_equal(ko.cpu().numpy()[written], want_k[written])
+        np.testing.assert_array_equal(vo.cpu().numpy()[written], want_v[written])
+
+
 def test_pool_rejects_bad_shapes():
     rt = _rt()
     dev = device()
