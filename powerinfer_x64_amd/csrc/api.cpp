@@ -1547,7 +1547,11 @@ int pi_tq_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t
     // per-head matrices, transposed for the kernels (TurboQuant::new(3, D, D,
     // 0xCAFE_BABE + h), src/turboquant/mod.rs:430-437)
     std::vector<float> rot((size_t)D * D), qjl((size_t)D * D);
-    std::vector<float> rt((size_t)n_kv_heads * D * D), gt((size_t)n_kv_heads * D * D);
+    // and G.R (double sums, rounded once), which turns a query into its virtual
+    // query in one product
+    std::vector<float> rt((size_t)n_kv_heads * D * D), gt((size_t)n_kv_heads * D * D),
+        grt((size_t)n_kv_heads * D * D);
+    std::vector<double> gr_row(D);
     for (int kh = 0; kh < n_kv_heads; ++kh) {
         tq_matrices(D, 0xCAFEBABEULL + (uint64_t)kh, rot.data(), qjl.data());
         for (int i = 0; i < D; ++i)
@@ -1555,18 +1559,27 @@ int pi_tq_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t
                 rt[((size_t)kh * D + j) * D + i] = rot[(size_t)i * D + j];
                 gt[((size_t)kh * D + j) * D + i] = qjl[(size_t)i * D + j];
             }
+        for (int i = 0; i < D; ++i) {
+            std::fill(gr_row.begin(), gr_row.end(), 0.0);
+            for (int k = 0; k < D; ++k) {
+                const double gik = qjl[(size_t)i * D + k];
+                const float* rk = &rot[(size_t)k * D];
+                for (int j = 0; j < D; ++j) gr_row[j] += gik * rk[j];
+            }
+            for (int j = 0; j < D; ++j) grt[((size_t)kh * D + j) * D + i] = (float)gr_row[j];
+        }
     }
     PI_HIP(h, hipSetDevice(h->device), "pi_tq_pool_create");
     pi_tq_pool p = new (std::nothrow) pi_tq_pool_s();
     if (!p) return fail(h, PI_ERR_OUT_OF_MEMORY, "pi_tq_pool_create: host allocation");
     p->owner = h;
-    p->bytes = kbytes + vbytes + 2 * mbytes;
+    p->bytes = kbytes + vbytes + 3 * mbytes;
     pi::TqPool& t = p->t;
     // separate K (packed records + norms) and V (f16) arrays
     t.g = pi::KvGeom{nullptr, nullptr, n_pages, n_kv_heads, D, pi::kTqDtype, 0,
                      (size_t)pi::kPageTokens * (pi::tq_key_bytes(D) + 4),
                      (size_t)pi::kPageTokens * D * 2};
-    t.rt = t.gt = nullptr;
+    t.rt = t.gt = t.grt = nullptr;
     t.scale = std::sqrt((float)D);
     // residual_norm * qjl_scale of the 3-bit estimator (src/turboquant/mod.rs:297-316)
     t.corr = std::sqrt(0.043f * (1.0f / t.scale)) * std::sqrt(3.14159274f / (2.0f * (float)D));
@@ -1574,15 +1587,18 @@ int pi_tq_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t
     if (e == hipSuccess) e = hipMalloc(&t.g.v, vbytes);
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&t.rt), mbytes);
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&t.gt), mbytes);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&t.grt), mbytes);
     if (e == hipSuccess) e = hipMemset(t.g.k, 0, kbytes);
     if (e == hipSuccess) e = hipMemset(t.g.v, 0, vbytes);
     if (e == hipSuccess) e = hipMemcpy(t.rt, rt.data(), mbytes, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(t.gt, gt.data(), mbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(t.grt, grt.data(), mbytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void)hipFree(t.g.k);
         (void)hipFree(t.g.v);
         (void)hipFree(t.rt);
         (void)hipFree(t.gt);
+        (void)hipFree(t.grt);
         delete p;
         return hip_fail(h, e, "pi_tq_pool_create");
     }
@@ -1598,6 +1614,7 @@ void pi_tq_pool_destroy(pi_tq_pool pool) {
     (void)hipFree(pool->t.g.v);
     (void)hipFree(pool->t.rt);
     (void)hipFree(pool->t.gt);
+    (void)hipFree(pool->t.grt);
     delete pool;
 }
 

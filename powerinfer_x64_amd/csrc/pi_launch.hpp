@@ -44,6 +44,7 @@ struct TqPool {
     KvGeom g;
     float* rt;
     float* gt;
+    float* grt;   // (G.R) transposed per head, for the one-pass virtual query (nullable)
     float scale;  // sqrt(d) in f32: the quantizer's per-coordinate scale
     float corr;   // residual_norm * qjl_scale of the 3-bit estimator
 };

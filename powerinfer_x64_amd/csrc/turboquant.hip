@@ -298,6 +298,77 @@ __global__ __launch_bounds__(256) void tq_query_kernel(TqPool t, const float* __
     }
 }
 
+// One-pass form of the same product: with GR = G.R precomputed per KV head
+// (TqPool::grt, transposed), the virtual query is [R; GR].q, so its 2 d rows
+// split over workgroups with no dependency between them.  A workgroup owns 64
+// of those rows for every query head of one (sequence, KV head); lane l of
+// each wavefront owns row 64 blockIdx.x + l and wavefront w sums the quarter
+// j = w d / 4 .. of the columns (one coalesced 256-byte read of the transposed
+// matrix per column), for up to kQuery2Heads heads whose query values are LDS
+// broadcasts; the quarters meet in LDS.  NH (4, 8 or 16) bounds the heads per
+// KV head; missing heads are zero queries, so the loops have no branches.
+constexpr int kQuery2Heads = 16;
+
+template <int D, int NH>
+__global__ __launch_bounds__(256) void tq_query2_kernel(TqPool t, const float* __restrict__ q,
+                                                        float* __restrict__ qv, int n_q_heads,
+                                                        int gqa_mode) {
+    __shared__ __attribute__((aligned(16))) float s_q[NH][D];
+    __shared__ float s_part[4][NH][64];
+    const int n_kv = t.g.n_kv_heads;
+    const int group = gqa_mode == 0 ? (n_q_heads + n_kv - 1) / n_kv : n_q_heads / n_kv;
+    const int kvh = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    auto head_of = [&](int k) { return gqa_mode == 0 ? kvh + k * n_kv : kvh * group + k; };
+    int nh = 0;  // heads of this KV head that exist (group <= NH, checked by the launcher)
+    while (nh < group && head_of(nh) < n_q_heads) ++nh;
+    const int row = 64 * blockIdx.x + lane;  // of the 2 D outputs; a block never straddles D
+    const float* mt = (row < D ? t.rt + (size_t)kvh * D * D + row : t.grt + (size_t)kvh * D * D + (row - D));
+    // the wavefront's D / 4 matrix values are all requested first, beside the
+    // query loads: one memory round trip (the matrices are rarely still in the
+    // caches after the decode kernel has streamed the pool)
+    const int j0 = wave * (D / 4);
+    float m[D / 4];
+#pragma unroll
+    for (int e = 0; e < D / 4; ++e) m[e] = mt[(size_t)(j0 + e) * D];
+    constexpr int QL = NH * D / 256;  // query values per thread
+    float qx[QL];
+#pragma unroll
+    for (int i = 0; i < QL; ++i) {
+        const int idx = tid + 256 * i, k = idx / D, j = idx - k * D;
+        qx[i] = k < nh ? q[((size_t)b * n_q_heads + head_of(k)) * D + j] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < QL; ++i) {
+        const int idx = tid + 256 * i;
+        s_q[idx / D][idx % D] = qx[i];
+    }
+    __syncthreads();
+    float acc[NH];
+#pragma unroll
+    for (int k = 0; k < NH; ++k) acc[k] = 0.f;
+#pragma unroll
+    for (int e = 0; e < D / 4; e += 4) {
+#pragma unroll
+        for (int k = 0; k < NH; ++k) {
+            const float4 x = *reinterpret_cast<const float4*>(&s_q[k][j0 + e]);
+            acc[k] = fmaf(m[e], x.x, acc[k]);
+            acc[k] = fmaf(m[e + 1], x.y, acc[k]);
+            acc[k] = fmaf(m[e + 2], x.z, acc[k]);
+            acc[k] = fmaf(m[e + 3], x.w, acc[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NH; ++k) s_part[wave][k][lane] = acc[k];
+    __syncthreads();
+    const float inv = 1.0f / t.scale;
+    for (int k = wave; k < nh; k += 4) {
+        const float x = (s_part[0][k][lane] + s_part[1][k][lane]) + (s_part[2][k][lane] + s_part[3][k][lane]);
+        float* dst = qv + ((size_t)b * n_q_heads + head_of(k)) * 2 * D;
+        dst[row] = row < D ? x * inv : t.corr * (x * inv);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_tq_append(const TqPool& t, const float* k, const float* v,
@@ -341,6 +412,25 @@ hipError_t launch_tq_query(const TqPool& t, const float* q, float* qv, int32_t b
     if (batch <= 0) return hipSuccess;
     const int n_kv = t.g.n_kv_heads;
     const int group = gqa_mode == 0 ? (n_q_heads + n_kv - 1) / n_kv : n_q_heads / n_kv;
+    if (t.grt && group <= kQuery2Heads && group > 0) {
+        const dim3 grid2((unsigned)(2 * t.g.head_dim / 64), (unsigned)n_kv, (unsigned)batch);
+#define PI_TQ_Q2(DD, NN) \
+    hipLaunchKernelGGL((tq_query2_kernel<DD, NN>), grid2, dim3(256), 0, s, t, q, qv, n_q_heads, gqa_mode)
+        const int nh = group <= 4 ? 4 : group <= 8 ? 8 : 16;
+        if (t.g.head_dim == 128) {
+            if (nh == 4) PI_TQ_Q2(128, 4);
+            else if (nh == 8) PI_TQ_Q2(128, 8);
+            else PI_TQ_Q2(128, 16);
+        } else if (t.g.head_dim == 256) {
+            if (nh == 4) PI_TQ_Q2(256, 4);
+            else if (nh == 8) PI_TQ_Q2(256, 8);
+            else PI_TQ_Q2(256, 16);
+        } else {
+            return hipErrorInvalidValue;
+        }
+#undef PI_TQ_Q2
+        return hipGetLastError();
+    }
     const int n_chunks = (group + kQueryHeads - 1) / kQueryHeads;
     const dim3 grid(t.g.n_kv_heads * n_chunks, batch);
     if (t.g.head_dim == 128)
