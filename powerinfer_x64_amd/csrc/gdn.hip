@@ -202,9 +202,11 @@ __global__ __launch_bounds__(256) void gdn_rmsnorm_gated_kernel(float* __restric
 // 128 x 32 tile of the state, 16 KB, whose rows are 128-byte lines.  Thread t
 // holds rows t/8 + 32 i (i < 4), columns 4 (t % 8) .. +3, as four 16-byte
 // loads issued before anything else, so the step costs one memory round trip.
-// Every wavefront computes the q / k norms itself with shuffles (no barrier);
-// the two column sums (S^T k, then S^T q after the update) reduce over a
-// wavefront's rows with shuffles and over the 4 wavefronts in LDS.
+// Every wavefront computes the q / k norms and k.q itself with shuffles.  The
+// readout after the update is o = S'^T q = (gamma S)^T q + delta (k.q), so both
+// column sums ((gamma S)^T k and (gamma S)^T q) come from the state as loaded,
+// in one reduction: over a wavefront's rows with shuffles and over the 4
+// wavefronts in LDS, behind one barrier.
 constexpr int DCOLS = 32;  // state columns per decode workgroup
 
 __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict__ q,
@@ -215,7 +217,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict
                                                          float* __restrict__ state,
                                                          float* __restrict__ out, int hk,
                                                          int hv) {
-    __shared__ __attribute__((aligned(16))) float s_part[2][4][DCOLS];
+    __shared__ __attribute__((aligned(16))) float s_part[4][2 * DCOLS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c0 = blockIdx.x * DCOLS;
     const int vh = blockIdx.y, b = blockIdx.z;
@@ -234,61 +236,63 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict
     const float q0 = qr[lane], q1 = qr[lane + 64], k0 = kr[lane], k1 = kr[lane + 64];
     const f32x4 vv = *reinterpret_cast<const f32x4*>(v + sh * DV + c0 + 4 * cg);
     const float decay = expf(g[sh]), bt = beta[sh];
-    float sq = q0 * q0 + q1 * q1, sk = k0 * k0 + k1 * k1;
+    float sq = q0 * q0 + q1 * q1, sk = k0 * k0 + k1 * k1, skq = k0 * q0 + k1 * q1;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) {
         sq = wave_sum_xor(sq, m);
         sk = wave_sum_xor(sk, m);
+        skq = wave_sum_xor(skq, m);
     }
-    const float nq = fmaxf(sqrtf(sq), 1e-12f), nk = fmaxf(sqrtf(sk), 1e-12f);
-    const float qs = 1.0f / sqrtf((float)DK);
+    const float inq = 1.0f / fmaxf(sqrtf(sq), 1e-12f) * (1.0f / sqrtf((float)DK));
+    const float ink = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
+    const float kq = skq * ink * inq;  // (normalised k) . (normalised, scaled q)
     // this thread's rows rr, rr + 32 (first halves) and rr + 64, rr + 96 (second)
     float kn[4], qn[4];
-    kn[0] = __shfl(k0, rr, 64) / nk;
-    kn[1] = __shfl(k0, rr + 32, 64) / nk;
-    kn[2] = __shfl(k1, rr, 64) / nk;
-    kn[3] = __shfl(k1, rr + 32, 64) / nk;
-    qn[0] = __shfl(q0, rr, 64) / nq * qs;
-    qn[1] = __shfl(q0, rr + 32, 64) / nq * qs;
-    qn[2] = __shfl(q1, rr, 64) / nq * qs;
-    qn[3] = __shfl(q1, rr + 32, 64) / nq * qs;
+    kn[0] = __shfl(k0, rr, 64) * ink;
+    kn[1] = __shfl(k0, rr + 32, 64) * ink;
+    kn[2] = __shfl(k1, rr, 64) * ink;
+    kn[3] = __shfl(k1, rr + 32, 64) * ink;
+    qn[0] = __shfl(q0, rr, 64) * inq;
+    qn[1] = __shfl(q0, rr + 32, 64) * inq;
+    qn[2] = __shfl(q1, rr, 64) * inq;
+    qn[3] = __shfl(q1, rr + 32, 64) * inq;
 
-    // S *= exp(g); kv_mem = S^T k (src/model/mod.rs:883-898)
-    f32x4 kv = {0.f, 0.f, 0.f, 0.f};
+    // S *= exp(g); kv_mem = S^T k and S^T q of the decayed state (src/model/mod.rs:883-898)
+    f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = kv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         s[i] *= decay;
         kv += s[i] * kn[i];
+        qv += s[i] * qn[i];
     }
 #pragma unroll
     for (int m = 8; m <= 32; m <<= 1)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) kv[c] = wave_sum_xor(kv[c], m);
-    if (lane < 8) *reinterpret_cast<f32x4*>(&s_part[0][wave][4 * lane]) = kv;
+        for (int c = 0; c < 4; ++c) {
+            kv[c] = wave_sum_xor(kv[c], m);
+            qv[c] = wave_sum_xor(qv[c], m);
+        }
+    if (lane < 8) {
+        *reinterpret_cast<f32x4*>(&s_part[wave][4 * lane]) = kv;
+        *reinterpret_cast<f32x4*>(&s_part[wave][DCOLS + 4 * lane]) = qv;
+    }
     __syncthreads();
-    f32x4 kv_mem = *reinterpret_cast<const f32x4*>(&s_part[0][0][4 * cg]);
+    f32x4 kv_mem = *reinterpret_cast<const f32x4*>(&s_part[0][4 * cg]);
 #pragma unroll
-    for (int w = 1; w < 4; ++w) kv_mem += *reinterpret_cast<const f32x4*>(&s_part[0][w][4 * cg]);
-    // delta = (v - kv_mem) beta; S += k delta^T; o = S^T q (:899-916)
+    for (int w = 1; w < 4; ++w) kv_mem += *reinterpret_cast<const f32x4*>(&s_part[w][4 * cg]);
+    // delta = (v - kv_mem) beta; S += k delta^T (:899-916)
     const f32x4 delta = (vv - kv_mem) * bt;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         s[i] += kn[i] * delta;
-        o += s[i] * qn[i];
         *reinterpret_cast<f32x4*>(S + (size_t)(rr + 32 * i) * DV) = s[i];
     }
-#pragma unroll
-    for (int m = 8; m <= 32; m <<= 1)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o[c] = wave_sum_xor(o[c], m);
-    if (lane < 8) *reinterpret_cast<f32x4*>(&s_part[1][wave][4 * lane]) = o;
-    __syncthreads();
+    // o = S'^T q = (decayed S)^T q + delta (k.q)
     if (tid < 8) {
-        f32x4 acc = *reinterpret_cast<const f32x4*>(&s_part[1][0][4 * tid]);
+        f32x4 acc = *reinterpret_cast<const f32x4*>(&s_part[0][DCOLS + 4 * tid]);
 #pragma unroll
-        for (int w = 1; w < 4; ++w) acc += *reinterpret_cast<const f32x4*>(&s_part[1][w][4 * tid]);
-        *reinterpret_cast<f32x4*>(out + sh * DV + c0 + 4 * tid) = acc;
+        for (int w = 1; w < 4; ++w) acc += *reinterpret_cast<const f32x4*>(&s_part[w][DCOLS + 4 * tid]);
+        *reinterpret_cast<f32x4*>(out + sh * DV + c0 + 4 * tid) = acc + delta * kq;
     }
 }
 
