@@ -841,6 +841,16 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
                          lambda: gl.forward(x1, z1, b1, a1))
     res["f3_gdn_layer_prompt_1024_c5"] = pr
     res["f3_gdn_layer_decode_token_c5"] = dc
+    # the same one-token step on device tensors (pi_gdn_layer_forward_dev), HIP events
+    dev_t = lambda a: torch.from_numpy(a).to("cuda")  # noqa: E731
+    xd, zd, bd, ad = dev_t(x1), dev_t(z1), dev_t(b1), dev_t(a1)
+    od = torch.empty((1, hv, dv), dtype=torch.float32, device="cuda")
+    gl.reset()
+    gl.forward_dev(dev_t(xa), dev_t(za), dev_t(ba), dev_t(aa))  # a prompt's state and conv rows
+    r = timer.run(lambda: gl.forward_dev(xd, zd, bd, ad, out=od), 200, 20)
+    res["f3_gdn_layer_decode_token_c5_device"] = {
+        "us_per_token": r["ms_avg"] * 1e3, "us_median": r["ms_median"] * 1e3,
+        "tokens_per_s": 1e3 / r["ms_avg"]}
     gl.close()
     if leg_s > 0:
         kd, vd = hk * dk, hv * dv

@@ -77,6 +77,7 @@ struct pi_gdn_layer_s {
     float* d_dt = nullptr;      // [hv]
     float* d_norm = nullptr;    // [dv]
     float* d_conv_state = nullptr;  // [d_conv - 1][conv_dim]
+    float* d_conv_alt = nullptr;    // the one-launch step's second conv state (swapped each step)
     float* d_state = nullptr;       // [hv][dk][dv]
     float* d_buf = nullptr;         // staging: activation, q, k, v, beta, g (+ host-slice I/O)
     size_t buf_floats = 0;
@@ -1359,6 +1360,12 @@ int pi_attn_layer_forward_dev(pi_handle h, pi_attn_layer L, float* d_q, float* d
 
 // ---- gated-DeltaNet layer state -------------------------------------------------------
 
+// A layer with k_hd = v_hd = 128 and d_conv 4 runs a one-token step as one
+// launch (gdn_step_kernel), alternating two conv-state buffers.
+static bool gdn_one_launch_step(const pi_gdn_layer_s* L) {
+    return L->dk == 128 && L->dv == 128 && L->d_conv == 4;
+}
+
 int pi_gdn_layer_create(pi_handle h, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,
                         int32_t v_hd, int32_t d_conv, const float* h_conv_w, const float* h_ssm_a,
                         const float* h_dt_bias, const float* h_norm_w, float eps,
@@ -1391,6 +1398,7 @@ int pi_gdn_layer_create(pi_handle h, int32_t n_k_heads, int32_t n_v_heads, int32
     alloc(&L->d_dt, n_v_heads);
     alloc(&L->d_norm, v_hd);
     alloc(&L->d_conv_state, cs);
+    if (gdn_one_launch_step(L)) alloc(&L->d_conv_alt, cs);
     alloc(&L->d_state, sn);
     if (e == hipSuccess) e = hipMemcpy(L->d_w, h_conv_w, wn * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(L->d_ssm_a, h_ssm_a, n_v_heads * 4, hipMemcpyHostToDevice);
@@ -1411,7 +1419,8 @@ void pi_gdn_layer_destroy(pi_gdn_layer L) {
     if (!L) return;
     (void)hipSetDevice(L->owner->device);
     (void)hipDeviceSynchronize();
-    for (float* p : {L->d_w, L->d_ssm_a, L->d_dt, L->d_norm, L->d_conv_state, L->d_state, L->d_buf})
+    for (float* p : {L->d_w, L->d_ssm_a, L->d_dt, L->d_norm, L->d_conv_state, L->d_conv_alt, L->d_state,
+                     L->d_buf})
         (void)hipFree(p);
     delete L;
 }
@@ -1434,6 +1443,14 @@ static int gdn_layer_step(pi_handle h, pi_gdn_layer L, const float* dx, const fl
                           const float* dbr, const float* dar, int32_t n_tokens, float* dout,
                           hipStream_t s) {
     void* sv = reinterpret_cast<void*>(s);
+    if (n_tokens == 1 && L->d_conv_alt && !(((uintptr_t)dz | (uintptr_t)dout) & 15)) {
+        PI_HIP(h, pi::launch_gdn_step(dx, L->d_conv_state, L->d_conv_alt, L->d_w, dz, dbr, dar,
+                                      L->d_ssm_a, L->d_dt, L->d_norm, L->eps, L->d_state, dout,
+                                      L->hk, L->hv, s),
+               "gdn layer step");
+        std::swap(L->d_conv_state, L->d_conv_alt);  // later launches on this stream see the new state
+        return PI_OK;
+    }
     const size_t n = (size_t)n_tokens, C = L->conv_dim, kd = (size_t)L->hk * L->dk;
     const size_t vd = (size_t)L->hv * L->dv, nh = (size_t)L->hv;
     // activation, q, k, v, beta, g

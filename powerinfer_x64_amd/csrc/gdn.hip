@@ -296,6 +296,136 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(const float* __restrict
     }
 }
 
+// One GDN layer step of a single token (src/model/mod.rs:750-932 at n = 1) in
+// one launch: conv1d + SiLU (d_conv 4) with the rolling state, the gates, the
+// q / k L2 norms, the delta rule and RMSNormGated x SiLU(z), which otherwise
+// take five launches.  One workgroup of 512 threads per V head vh (K head
+// kh = vh % hk):
+//  - it convolves the 128 q and 128 k channels of kh and the 128 v channels
+//    of vh itself (a K head's q / k channels are convolved once per V head
+//    tiled onto it: 384 channels of 4 taps, a few cycles);
+//  - the conv state is read from cs_in and its one-token shift written to
+//    cs_out (the layer alternates two buffers), each workgroup copying a
+//    1 / hv share of the channels, so no workgroup reads what another writes;
+//  - thread t holds state rows t / 32 + 16 i (i < 8), columns 4 (t % 32) ..
+//    + 3, loaded before anything else; both column sums ((g S)^T k and
+//    (g S)^T q) reduce together over the rows (o = (g S)^T q + delta (k.q),
+//    as in gdn_decode_kernel), then wavefront 0 applies RMSNormGated to the
+//    head's 128 outputs.
+// The arithmetic of each step follows gdn_conv1d_k4_kernel, gdn_gates_kernel,
+// gdn_decode_kernel and gdn_rmsnorm_gated_kernel.
+__global__ __launch_bounds__(512) void gdn_step_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ cs_in,
+                                                       float* __restrict__ cs_out,
+                                                       const float* __restrict__ w,
+                                                       const float* __restrict__ z,
+                                                       const float* __restrict__ beta_raw,
+                                                       const float* __restrict__ a_raw,
+                                                       const float* __restrict__ ssm_a,
+                                                       const float* __restrict__ dt_bias,
+                                                       const float* __restrict__ norm_w, float eps,
+                                                       float* __restrict__ state,
+                                                       float* __restrict__ out, int hk, int hv) {
+    __shared__ float s_q[DK], s_k[DK], s_v[DV];
+    __shared__ __attribute__((aligned(16))) float s_red[8][2 * DV];  // per wavefront: S^T k | S^T q
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int vh = blockIdx.x, kh = vh % hk;
+    const int C = 2 * hk * DK + hv * DV;
+    const int cg = tid & 31, rr = tid >> 5;
+    float* S = state + (size_t)vh * DK * DV + 4 * cg;
+    f32x4 s[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = *reinterpret_cast<const f32x4*>(S + (size_t)(rr + 16 * i) * DV);
+
+    // conv1d + SiLU: X_ext = [cs_in rows 0..2 (oldest first); x], taps w[c][0..3]
+    auto conv = [&](int c) {
+        const f32x4 wc = *reinterpret_cast<const f32x4*>(w + (size_t)c * 4);
+        float val = 0.f;
+        val += wc[0] * cs_in[c];
+        val += wc[1] * cs_in[C + c];
+        val += wc[2] * cs_in[2 * C + c];
+        val += wc[3] * x[c];
+        return val / (1.0f + expf(-val));
+    };
+    if (tid < DK) s_q[tid] = conv(kh * DK + tid);
+    else if (tid < 2 * DK) s_k[tid - DK] = conv(hk * DK + kh * DK + tid - DK);
+    else if (tid < 2 * DK + DV) s_v[tid - 2 * DK] = conv(2 * hk * DK + vh * DV + tid - 2 * DK);
+    {  // the new conv state: rows 1, 2 of the old one and this token, for a share of the channels
+        const int c_lo = (int)((long long)vh * C / hv), c_hi = (int)((long long)(vh + 1) * C / hv);
+        for (int c = c_lo + tid; c < c_hi; c += 512) {
+            cs_out[c] = cs_in[C + c];
+            cs_out[C + c] = cs_in[2 * C + c];
+            cs_out[2 * C + c] = x[c];
+        }
+    }
+    // gates (src/model/mod.rs:806-839)
+    const float bt = 1.0f / (1.0f + expf(-beta_raw[vh]));
+    const float sp_in = a_raw[vh] + dt_bias[vh];
+    const float sp = sp_in > 10.0f ? sp_in : logf(1.0f + expf(sp_in));
+    const float decay = expf(ssm_a[vh] * sp);
+    __syncthreads();
+
+    // L2 norms (max(|x|, 1e-12); q also / sqrt(Dk)) and k.q, in every wavefront
+    const float q0 = s_q[lane], q1 = s_q[lane + 64], k0 = s_k[lane], k1 = s_k[lane + 64];
+    float sq = q0 * q0 + q1 * q1, sk = k0 * k0 + k1 * k1, skq = k0 * q0 + k1 * q1;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        sq = wave_sum_xor(sq, m);
+        sk = wave_sum_xor(sk, m);
+        skq = wave_sum_xor(skq, m);
+    }
+    const float inq = 1.0f / fmaxf(sqrtf(sq), 1e-12f) * (1.0f / sqrtf((float)DK));
+    const float ink = 1.0f / fmaxf(sqrtf(sk), 1e-12f);
+    const float kq = skq * ink * inq;
+    float kn[8];
+    f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = kv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        kn[i] = s_k[rr + 16 * i] * ink;
+        const float qn = s_q[rr + 16 * i] * inq;
+        s[i] *= decay;
+        kv += s[i] * kn[i];
+        qv += s[i] * qn;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {  // rows rr and rr + 1 of a wavefront: lanes l, l + 32
+        kv[c] += __shfl_xor(kv[c], 32, 64);
+        qv[c] += __shfl_xor(qv[c], 32, 64);
+    }
+    if (lane < 32) {
+        *reinterpret_cast<f32x4*>(&s_red[wave][4 * cg]) = kv;
+        *reinterpret_cast<f32x4*>(&s_red[wave][DV + 4 * cg]) = qv;
+    }
+    __syncthreads();
+    f32x4 kv_mem = *reinterpret_cast<const f32x4*>(&s_red[0][4 * cg]);
+#pragma unroll
+    for (int wv = 1; wv < 8; ++wv) kv_mem += *reinterpret_cast<const f32x4*>(&s_red[wv][4 * cg]);
+    const f32x4 vv = *reinterpret_cast<const f32x4*>(&s_v[4 * cg]);
+    const f32x4 delta = (vv - kv_mem) * bt;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        s[i] += kn[i] * delta;
+        *reinterpret_cast<f32x4*>(S + (size_t)(rr + 16 * i) * DV) = s[i];
+    }
+    if (wave == 0 && lane < 32) {
+        // o = (decayed S)^T q + delta (k.q); then RMSNormGated over the head's 128 values
+        f32x4 o = *reinterpret_cast<const f32x4*>(&s_red[0][DV + 4 * cg]);
+#pragma unroll
+        for (int wv = 1; wv < 8; ++wv) o += *reinterpret_cast<const f32x4*>(&s_red[wv][DV + 4 * cg]);
+        o += delta * kq;
+        float ss = o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3];
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float sc = 1.0f / sqrtf(ss / (float)DV + eps);
+        const f32x4 zv = *reinterpret_cast<const f32x4*>(z + (size_t)vh * DV + 4 * cg);
+        const f32x4 nw = *reinterpret_cast<const f32x4*>(norm_w + 4 * cg);
+        f32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = (o[e] * sc * nw[e]) * (zv[e] / (1.0f + expf(-zv[e])));
+        *reinterpret_cast<f32x4*>(out + (size_t)vh * DV + 4 * cg) = r;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Any head widths (k_hd <= 256, any v_hd): the per-token recurrence of
 // src/model/mod.rs:841-916 itself, token after token.  A wavefront owns 8
@@ -1149,6 +1279,20 @@ hipError_t launch_gdn_recur(const float* q, const float* k, const float* v, cons
     else if (nr <= 16) PI_GDN_RECUR(16);
     else PI_GDN_RECUR(32);
 #undef PI_GDN_RECUR
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_step(const float* x, const float* cs_in, float* cs_out, const float* w,
+                           const float* z, const float* beta_raw, const float* a_raw,
+                           const float* ssm_a, const float* dt_bias, const float* norm_w, float eps,
+                           float* state, float* out, int32_t n_k_heads, int32_t n_v_heads,
+                           hipStream_t s) {
+    if (n_k_heads <= 0 || n_v_heads <= 0) return hipErrorInvalidValue;
+    // f32x4 accesses: conv taps (4 per channel), z / norm / out rows of 128
+    if (((uintptr_t)w | (uintptr_t)z | (uintptr_t)norm_w | (uintptr_t)out | (uintptr_t)state) & 15)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gdn_step_kernel, dim3(n_v_heads), dim3(512), 0, s, x, cs_in, cs_out, w, z,
+                       beta_raw, a_raw, ssm_a, dt_bias, norm_w, eps, state, out, n_k_heads, n_v_heads);
     return hipGetLastError();
 }
 

@@ -175,6 +175,14 @@ hipError_t launch_gdn_conv1d(const float* x, float* state, const float* w, float
                              hipStream_t s);
 hipError_t launch_gdn_rmsnorm_gated(float* o, const float* z, const float* w, int32_t n_rows,
                                     int32_t n_v_heads, int32_t v_hd, float eps, hipStream_t s);
+// One GDN layer step of one token, k_hd = v_hd = 128, d_conv 4: conv1d + SiLU
+// (state cs_in -> cs_out, [3][conv_dim] each), gates, delta rule and
+// RMSNormGated x SiLU(z) into out [n_v_heads][128], in one launch.
+hipError_t launch_gdn_step(const float* x, const float* cs_in, float* cs_out, const float* w,
+                           const float* z, const float* beta_raw, const float* a_raw,
+                           const float* ssm_a, const float* dt_bias, const float* norm_w, float eps,
+                           float* state, float* out, int32_t n_k_heads, int32_t n_v_heads,
+                           hipStream_t s);
 // Largest key head width of the gated-DeltaNet kernels; k_hd = v_hd = 128
 // run the tuned decode / chunked kernels, other widths the per-token kernel.
 constexpr int kGdnMaxKhd = 256;
