@@ -133,3 +133,24 @@ def test_gdn_layer_rejects_bad_shapes():
         layer.forward(qkv, z[:2].copy(), br, ar)
     assert layer.forward(qkv[:0].copy(), z[:0].copy(), br[:0].copy(), ar[:0].copy()).shape == (0, hv, d)
     layer.close()
+
+
+def test_gdn_layer_forward_dev_equals_host_slices():
+    """pi_gdn_layer_forward_dev on device tensors gives pi_gdn_layer_forward's bits over a
+    prompt, an odd and an even run of one-token steps (the one-launch step alternates two
+    conv-state buffers) and continued chunks, so the two seams share every kernel and state."""
+    import torch
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    rng = np.random.default_rng(97)
+    hk, hv, d = 2, 4, 128
+    w = _weights(rng, hk, hv, d, d, 4)
+    host, devl = rt.GdnLayer(dev, hk, hv, d, d, *w), rt.GdnLayer(dev, hk, hv, d, d, *w)
+    to_dev = lambda a: torch.from_numpy(a).to("cuda")  # noqa: E731
+    for n in (33, 1, 1, 1, 7, 1, 1, 12):
+        x = _inputs(rng, n, hk, hv, d, d)
+        want = host.forward(*x)
+        got = devl.forward_dev(*(to_dev(a) for a in x)).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), n
+    host.close()
+    devl.close()
