@@ -333,36 +333,56 @@ __global__ __launch_bounds__(512) void gdn_step_kernel(const float* __restrict__
     const int C = 2 * hk * DK + hv * DV;
     const int cg = tid & 31, rr = tid >> 5;
     float* S = state + (size_t)vh * DK * DV + 4 * cg;
+    // The conv inputs of this thread's channel are requested first and the state
+    // tile after them, so the conv (which everything else waits for) does not
+    // queue behind the tile's 64 KB.  X_ext = [cs_in rows 0..2 (oldest first); x],
+    // taps w[c][0..3]; thread t < 384 convolves q (t < 128) or k of kh, or v of vh.
+    const int cc = tid < DK ? kh * DK + tid
+                 : tid < 2 * DK ? hk * DK + kh * DK + tid - DK
+                 : 2 * hk * DK + vh * DV + min(tid - 2 * DK, DV - 1);
+    const f32x4 wc = *reinterpret_cast<const f32x4*>(w + (size_t)cc * 4);
+    const float x0 = cs_in[cc], x1 = cs_in[C + cc], x2 = cs_in[2 * C + cc], x3 = x[cc];
+    // the new conv state for this workgroup's share of the channels (C / hv <= 512 of
+    // them at the model's shapes; larger shares loop below) and the gate inputs
+    const int c_lo = (int)((long long)vh * C / hv), c_hi = (int)((long long)(vh + 1) * C / hv);
+    const int c1 = c_lo + tid;
+    float n0 = 0.f, n1 = 0.f, n2 = 0.f;
+    if (c1 < c_hi) {
+        n0 = cs_in[C + c1];
+        n1 = cs_in[2 * C + c1];
+        n2 = x[c1];
+    }
+    const float braw = beta_raw[vh], araw = a_raw[vh], dtb = dt_bias[vh], sa = ssm_a[vh];
     f32x4 s[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) s[i] = *reinterpret_cast<const f32x4*>(S + (size_t)(rr + 16 * i) * DV);
-
-    // conv1d + SiLU: X_ext = [cs_in rows 0..2 (oldest first); x], taps w[c][0..3]
-    auto conv = [&](int c) {
-        const f32x4 wc = *reinterpret_cast<const f32x4*>(w + (size_t)c * 4);
+    {
         float val = 0.f;
-        val += wc[0] * cs_in[c];
-        val += wc[1] * cs_in[C + c];
-        val += wc[2] * cs_in[2 * C + c];
-        val += wc[3] * x[c];
-        return val / (1.0f + expf(-val));
-    };
-    if (tid < DK) s_q[tid] = conv(kh * DK + tid);
-    else if (tid < 2 * DK) s_k[tid - DK] = conv(hk * DK + kh * DK + tid - DK);
-    else if (tid < 2 * DK + DV) s_v[tid - 2 * DK] = conv(2 * hk * DK + vh * DV + tid - 2 * DK);
-    {  // the new conv state: rows 1, 2 of the old one and this token, for a share of the channels
-        const int c_lo = (int)((long long)vh * C / hv), c_hi = (int)((long long)(vh + 1) * C / hv);
-        for (int c = c_lo + tid; c < c_hi; c += 512) {
-            cs_out[c] = cs_in[C + c];
-            cs_out[C + c] = cs_in[2 * C + c];
-            cs_out[2 * C + c] = x[c];
-        }
+        val += wc[0] * x0;
+        val += wc[1] * x1;
+        val += wc[2] * x2;
+        val += wc[3] * x3;
+        const float act = val / (1.0f + expf(-val));
+        if (tid < DK) s_q[tid] = act;
+        else if (tid < 2 * DK) s_k[tid - DK] = act;
+        else if (tid < 2 * DK + DV) s_v[tid - 2 * DK] = act;
+    }
+    // the new conv state: rows 1, 2 of the old one and this token
+    if (c1 < c_hi) {
+        cs_out[c1] = n0;
+        cs_out[C + c1] = n1;
+        cs_out[2 * C + c1] = n2;
+    }
+    for (int c = c1 + 512; c < c_hi; c += 512) {
+        cs_out[c] = cs_in[C + c];
+        cs_out[C + c] = cs_in[2 * C + c];
+        cs_out[2 * C + c] = x[c];
     }
     // gates (src/model/mod.rs:806-839)
-    const float bt = 1.0f / (1.0f + expf(-beta_raw[vh]));
-    const float sp_in = a_raw[vh] + dt_bias[vh];
+    const float bt = 1.0f / (1.0f + expf(-braw));
+    const float sp_in = araw + dtb;
     const float sp = sp_in > 10.0f ? sp_in : logf(1.0f + expf(sp_in));
-    const float decay = expf(ssm_a[vh] * sp);
+    const float decay = expf(sa * sp);
     __syncthreads();
 
     // L2 norms (max(|x|, 1e-12); q also / sqrt(Dk)) and k.q, in every wavefront
