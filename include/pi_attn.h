@@ -344,7 +344,9 @@ int pi_gdn_layer_forward(pi_handle h, pi_gdn_layer layer, const float* h_qkv, co
                          const float* h_beta_raw, const float* h_a_raw, int32_t n_tokens,
                          float* h_out);
 /* pi_gdn_layer_forward with device pointers (same layouts), enqueued on `stream` without
- * host copies or waits.  Calls on one layer must be ordered on one stream. */
+ * host copies or waits.  Calls on one layer must be ordered on one stream.  With k_hd = v_hd
+ * = 128 and d_conv 4, a one-token call is one kernel launch (16-byte aligned d_z and d_out;
+ * otherwise the general path runs). */
 int pi_gdn_layer_forward_dev(pi_handle h, pi_gdn_layer layer, const float* d_qkv,
                              const float* d_z, const float* d_beta_raw, const float* d_a_raw,
                              int32_t n_tokens, float* d_out, void* stream);
@@ -362,7 +364,9 @@ typedef struct pi_tq_pool_s* pi_tq_pool;
  * dim, seed) (:76-103: Gram-Schmidt of a SplitMix64 / Box-Muller Gaussian matrix, and a
  * Gaussian matrix of seed ^ 0xDEADBEEF).  Errors through pi_last_error(NULL). */
 int pi_tq_generate(int32_t dim, uint64_t seed, float* h_rotation, float* h_qjl);
-/* CompressedKVCache::new (:430-447) over a paged pool: n_pages pages of 16 tokens. */
+/* CompressedKVCache::new (:430-447) over a paged pool: n_pages pages of 16 tokens.  Besides
+ * the rotation R and QJL matrix G of each KV head, the pool keeps G.R (computed on the host at
+ * creation), so a query's virtual query is one product; pi_tq_pool_bytes counts all three. */
 int pi_tq_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t n_kv_heads,
                       int32_t head_dim, pi_tq_pool* out);
 void pi_tq_pool_destroy(pi_tq_pool pool);
