@@ -567,16 +567,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(KvGeom g, DecodeParams
 // a workgroup owns 256 output values of one segment (64 16-byte groups); its
 // 4 wavefronts first form the run weights of the block's columns, then sum
 // every 4th run each and meet in LDS.
+template <int V>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, DecodeWorkspace ws,
                                                            int n_kv, int D) {
+    // V values per thread (4, or 1 for launches with few workgroups): 64 V per workgroup
+    typedef typename std::conditional<V == 4, f32x4, float>::type VT;
     __shared__ float s_w[4][kMaxRuns];  // per column (<= 4 per 256 values) and run
     __shared__ int s_slot[kMaxRuns];
     __shared__ float s_inv[4];
-    __shared__ __attribute__((aligned(16))) f32x4 s_acc[4][64];
+    __shared__ __attribute__((aligned(16))) VT s_acc[4][64];
     const int sidx = blockIdx.y, b = blockIdx.z, n_seg = gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cols = p.cols, GD = cols * D;
-    const int e0 = blockIdx.x * 256;
+    const int e0 = blockIdx.x * 64 * V;
     const size_t seg = (size_t)b * n_seg + sidx;
     // The context length and the run table load together: a merge is a short chain of
     // dependent memory round trips, so every load that can is issued beside another.
@@ -585,7 +588,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     if (sched::seq_tokens(ctx, p.max_pages) == 0) {
         // empty context: softmax over nothing leaves zeros (src/ops.rs:161)
         const int idx = e0 + tid;
-        if (idx < GD) {
+        if (tid < 64 * V && idx < GD) {
             const int c = idx / D, d = idx - c * D;
             const int h = seg_head(p, sidx, c, n_kv);
             if (h >= 0) p.out[((size_t)b * p.n_q_heads + h) * D + d] = 0.f;
@@ -597,19 +600,20 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     for (int r = tid; r < n_runs; r += 256)
         s_slot[r] = (int)sched::run_slot(r == 0, b, sidx, n_seg, p.batch, wg1 + r - 1);
     __syncthreads();
-    const int c_lo = e0 / D, c_hi = min(cols - 1, (e0 + 255) / D);
+    const int c_lo = e0 / D, c_hi = min(cols - 1, (e0 + 64 * V - 1) / D);
     // thread (wave, lane): values e0 + 4 lane .. +3 of runs wave, wave + 4, ...; the first
     // kPre of those runs are loaded now, beside the (max, sum) pairs, before any weight is known
     constexpr int kPre = 4;
-    const int e = e0 + 4 * lane;
+    const int e = e0 + V * lane;
     const bool on = e < GD;  // GD is a multiple of 4 (D >= 64)
     const float* po = ws.partial_o + (on ? e : 0);
-    auto part = [&](int r) { return *reinterpret_cast<const f32x4*>(po + (size_t)s_slot[r] * GD); };
-    f32x4 pre[kPre];
+    auto part = [&](int r) { return *reinterpret_cast<const VT*>(po + (size_t)s_slot[r] * GD); };
+    const VT zero = VT{};
+    VT pre[kPre];
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
         const int r = wave + 4 * j;
-        pre[j] = r < n_runs ? part(r) : f32x4{0.f, 0.f, 0.f, 0.f};
+        pre[j] = r < n_runs ? part(r) : zero;
     }
     typedef float f2 __attribute__((ext_vector_type(2)));
     const f2* pml = reinterpret_cast<const f2*>(ws.partial_ml);
@@ -640,11 +644,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     __syncthreads();
     const int cw = (on ? e / D : c_lo) - c_lo;
     const float* w = s_w[cw];
-    f32x4 a[4];
+    VT a[4];
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
         const int r = wave + 4 * j;
-        a[j] = r < n_runs ? w[r] * pre[j] : f32x4{0.f, 0.f, 0.f, 0.f};
+        a[j] = r < n_runs ? w[r] * pre[j] : zero;
     }
     int r = wave + 4 * kPre;
     for (; r + 12 < n_runs; r += 16) {  // four independent loads in flight
@@ -655,19 +659,21 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     s_acc[wave][lane] = (a[0] + a[1]) + (a[2] + a[3]);
     __syncthreads();
     if (wave != 0 || !on) return;
-    const f32x4 acc = (s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]);
+    const VT acc = (s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]);
     const float inv = s_inv[cw];
     const int c = e / D, d = e - c * D;
     const int h = seg_head(p, sidx, c, n_kv);
     if (h < 0) return;
     const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
-    f32x4 res = acc * inv;
+    VT res = acc * inv;
     if (p.gate) {
-        const f32x4 gt = *reinterpret_cast<const f32x4*>(p.gate + oi);
+        const VT gt = *reinterpret_cast<const VT*>(p.gate + oi);
+        float* rp = reinterpret_cast<float*>(&res);
+        const float* gp = reinterpret_cast<const float*>(&gt);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) res[i] *= sigmoidf_(gt[i]);
+        for (int i = 0; i < V; ++i) rp[i] *= sigmoidf_(gp[i]);
     }
-    *reinterpret_cast<f32x4*>(p.out + oi) = res;
+    *reinterpret_cast<VT*>(p.out + oi) = res;
 }
 
 template <typename KT, int D>
@@ -695,8 +701,15 @@ hipError_t launch_t(const KvGeom& g, const DecodeParams& p, const DecodeWorkspac
                        s, g, p, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3((p.cols * D + 255) / 256, g.n_kv_heads * p.n_cb, p.batch),
-                       dim3(256), 0, s, p, ws, g.n_kv_heads, D);
+    // 256 values per merge workgroup, or 64 when that leaves fewer than 128 workgroups
+    // (one long sequence: each segment's many runs then spread over four times the CUs)
+    const long long wg4 = (long long)((p.cols * D + 255) / 256) * g.n_kv_heads * p.n_cb * p.batch;
+    if (wg4 >= 128)
+        hipLaunchKernelGGL(decode_merge_kernel<4>, dim3((p.cols * D + 255) / 256, g.n_kv_heads * p.n_cb, p.batch),
+                           dim3(256), 0, s, p, ws, g.n_kv_heads, D);
+    else
+        hipLaunchKernelGGL(decode_merge_kernel<1>, dim3((p.cols * D + 63) / 64, g.n_kv_heads * p.n_cb, p.batch),
+                           dim3(256), 0, s, p, ws, g.n_kv_heads, D);
     return hipGetLastError();
 }
 
