@@ -120,10 +120,11 @@ def test_append_in_chunks_and_edge_keys():
         _check_records(case, i)
 
 
-@pytest.mark.parametrize("hq,hkv", [(8, 2), (12, 2), (3, 3)])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (12, 2), (3, 3), (32, 2), (42, 2)])
 @pytest.mark.parametrize("gqa_mode", [0, 1])
 def test_decode_matches_oracle_ragged(gqa_mode, hq, hkv):
-    """Groups of 4, 6 (a full and a partial chunk of the query precompute) and 1."""
+    """Groups of 4, 6, 1 and 16 (the one-pass query precompute's head bounds 4, 8 and 16) and
+    21 (above its bound: the two-pass precompute, full chunks of 4 heads and a partial one)."""
     dev = device()
     rng = np.random.default_rng(0x70C2 + gqa_mode + 16 * hq)
     lens = [1, 16, 200, 1000, 37]
