@@ -1194,12 +1194,12 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             *reinterpret_cast<f16x4*>(sdph + ln * KT_ + 16 * rb + 4 * g4) = ph;
             *reinterpret_cast<f16x4*>(sdpl + ln * KT_ + 16 * rb + 4 * g4) = pl;
             // chunk n+1's tiles go to the other buffer (last read in chunk
-            // n-1): the K side issues 3 of its 8 loads here, where it
+            // n-1): the K side issues 5 of its 8 loads here, where it
             // finishes phase 2 before the Q side, and the rest in phase 3
-            if (n + 1 < n_chunks) issue(n + 1, 0, 3);
+            if (n + 1 < n_chunks) issue(n + 1, 0, 5);
         }
         __syncthreads();
-        if (kside && n + 1 < n_chunks) issue(n + 1, 3, 8);
+        if (kside && n + 1 < n_chunks) issue(n + 1, 5, 8);
         // phase 3a: O = gamma QS + M Delta (waves 4-7)
         if (!kside) {
             const f32x4 o = mm_split_sw(sm_[cb], sm_[cb] + GC * GC, sdth, sdtl, 16 * rb, (rb >> 1) + 1);
