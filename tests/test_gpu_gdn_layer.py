@@ -65,7 +65,7 @@ def _inputs(rng, n, hk, hv, dk, dv):
             rng.standard_normal((n, hv)).astype(np.float32))
 
 
-@pytest.mark.parametrize("hk,hv,d", [(16, 32, 128), (2, 4, 128)])
+@pytest.mark.parametrize("hk,hv,d", [(16, 32, 128), (2, 4, 128), (3, 6, 128), (4, 4, 128)])
 def test_gdn_layer_prompt_decode_chunk_reset(hk, hv, d):
     """A 200-token prompt, 3 decode tokens, a 65-token continued chunk, then reset
     and a fresh 1-token start and 40-token prompt.  Each output element within the
