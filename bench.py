@@ -890,6 +890,8 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
         res["f3_gdn_layer_decode_token_c5"]["cpu_baseline"] = _cpu(
             m / sec_, "tokens/s", f"the oracle's GDN layer chain for one token, {m} calls",
             round(sec_, 3), us_per_token=round(sec_ / m * 1e6, 2))
+        res["f3_gdn_layer_decode_token_c5_device"]["cpu_baseline"] = dict(
+            res["f3_gdn_layer_decode_token_c5"]["cpu_baseline"])
     return res
 
 
