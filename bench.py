@@ -789,6 +789,20 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
     res["f3_attn_layer_prompt_1024_c4"] = pr
     res["f3_attn_layer_decode_token_c4"] = dc
     lay.close()
+    # the decode token on device tensors (pi_attn_layer_forward_dev: prologue, decode over the
+    # prompt's pages and the gate), HIP events over 200 tokens after the 1024-token prompt
+    n_tok_dev = 2 * 200 + 20  # timer.run: warm-up, the timed pass and the per-call pass
+    lay = rt.AttnLayer(dev, prompt + n_tok_dev + 16, hq, hkv, d, torch.float16, q_norm_w=qn_w,
+                       k_norm_w=kn_w, rope_dim=64, rope_base=1e7, sections=[11, 11, 10, 0])
+    dev_t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda")  # noqa: E731
+    lay.forward_dev(dev_t(raw[0]), dev_t(raw[1]), dev_t(raw[2]), gate=dev_t(raw[3]))
+    qd, kd1, vd1, gd1 = (dev_t(x) for x in raw[4:])
+    od = torch.empty((1, hq, d), dtype=torch.float32, device="cuda")
+    r = timer.run(lambda: lay.forward_dev(qd, kd1, vd1, gate=gd1, out=od), 200, 20)
+    res["f3_attn_layer_decode_token_c4_device"] = {
+        "us_per_token": r["ms_avg"] * 1e3, "us_median": r["ms_median"] * 1e3,
+        "tokens_per_s": 1e3 / r["ms_avg"]}
+    lay.close()
     if leg_s > 0:
         freqs = orc.compute_imrope_freqs(1e7, 64, [11, 11, 10, 0])
         kw = dict(q_norm_w=qn_w, k_norm_w=kn_w, rope_dim=64, rope_base=1e7, freqs=freqs)
@@ -827,6 +841,8 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
         res["f3_attn_layer_decode_token_c4"]["cpu_baseline"] = _cpu(
             m / sec_, "tokens/s", f"or_attn_layer_tokens for one token after {n} cached, {m} "
             f"calls", round(sec_, 3), us_per_token=round(sec_ / m * 1e6, 2))
+        res["f3_attn_layer_decode_token_c4_device"]["cpu_baseline"] = dict(
+            res["f3_attn_layer_decode_token_c4"]["cpu_baseline"])
 
     conv_w = (rng.standard_normal((conv_dim, d_conv)) * 0.5).astype(f32)
     ssm_a = -np.exp(rng.standard_normal(hv)).astype(f32)
