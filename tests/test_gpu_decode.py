@@ -197,3 +197,33 @@ def test_decode_large_batch_scan():
             np.testing.assert_array_equal(out[i], 0)
         else:
             assert row_rel_err(out[i], case.oracle_out(i, kv_round=np.float16)) <= 1e-2
+
+
+@pytest.mark.parametrize("pool_dtype,d,hq,hkv,length", [
+    (torch.float32, 128, 8, 2, 1024),   # 4 heads a segment (cols * D = 512), 64 pages
+    (torch.float32, 64, 4, 1, 1000),
+    (torch.float16, 64, 16, 2, 17),     # 8 heads a segment at D 64
+    (torch.float16, 128, 4, 4, 1),
+    (torch.float16, 128, 32, 8, 700),
+    (torch.float32, 128, 32, 32, 0),    # no tokens: zeros (written by the merge)
+])
+def test_one_sequence_short_contexts(pool_dtype, d, hq, hkv, length):
+    """One sequence of at most 64 pages (a decode token stream): the split schedule spreads a
+    few pages per workgroup and the merge folds them; every output row against the oracle
+    (f32: max-abs 2e-3; f16: 1e-2 rel); the output starts as NaN."""
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    rng = np.random.default_rng(0x5EED0900 + d + hq + length)
+    case = PagedCase(rng, [length], hq, hkv, d, theta=1e6)
+    case.gpu_build(dev, pool_dtype)
+    q = case.gpu_q(dev)
+    out = torch.full_like(q, float("nan"))
+    rt.attn_decode(dev, q, case.pool, case.pt, to_dev(np.array([length], np.int32)), out=out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    if pool_dtype == torch.float32:
+        ref = case.oracle_out(0)
+        err = np.abs(got[0] - ref).max()
+        assert err <= 2e-3, f"max-abs {err}"
+    else:
+        _check_f16(case, got)
