@@ -1192,13 +1192,10 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
 
 namespace {
 // Head dim 256 runs prefill_fa256_kernel (two wavefronts per SIMD); PI_PREFILL_FA256=0
-// selects the one-wavefront-per-SIMD prefill_fa_kernel<., ., 256> instead.
+// selects the one-wavefront-per-SIMD prefill_fa_kernel<., ., 256> instead (read per call).
 bool use_fa256() {
-    static const bool on = [] {
-        const char* e = std::getenv("PI_PREFILL_FA256");
-        return !(e && e[0] == '0');
-    }();
-    return on;
+    const char* e = std::getenv("PI_PREFILL_FA256");
+    return !(e && e[0] == '0');
 }
 
 template <int D>

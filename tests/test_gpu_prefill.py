@@ -134,6 +134,21 @@ def test_prefill_head_dim_256(s, dtype):
     assert mism == 0
 
 
+@pytest.mark.parametrize("s,hq,hkv,dtype", [(70, 16, 2, torch.bfloat16), (300, 16, 2, torch.float16),
+                                             (180, 4, 2, torch.bfloat16), (129, 2, 2, torch.float16)])
+def test_prefill_head_dim_256_one_wave_per_simd_kernel(monkeypatch, s, hq, hkv, dtype):
+    """The alternative D 256 kernel (PI_PREFILL_FA256=0: one wavefront per SIMD, two unit
+    buffers): every row against the oracle's per-row decode, 1e-2 relative per row."""
+    monkeypatch.setenv("PI_PREFILL_FA256", "0")
+    rng = np.random.default_rng(260 + s + hq)
+    tq, tk, tv = _inputs(rng, s, hq, hkv, 256, dtype=dtype)
+    out = _run(tq, tk, tv)
+    ref = _oracle_rows(tq, tk, tv, range(s))
+    assert row_rel_err(out, ref) <= 1e-2
+    n, mism, ties = argmax_agreement(out, ref)
+    assert mism == 0
+
+
 def test_prefill_head_dim_256_4096_sampled_rows():
     """The config-4 layer shape at S 4096 (16/2 heads, D 256): the launch pairs a heavy and a
     light query block per workgroup; rows sampled across the prompt, every block edge."""
