@@ -1314,11 +1314,11 @@ PrefillSched prefill_sched(int batch, int seq_len, int n_q_heads, int n_kv_heads
                             (((seq_len + rows - 1) / rows + 1) / 2);
     const int n_cu = cu_count();
     sc.paired = causal && n_cu > 0 && pairs >= n_cu;
-    static const char* env_p = std::getenv("PI_PREFILL_PAIRED");
+    const char* env_p = std::getenv("PI_PREFILL_PAIRED");  // read per call, as is PI_PREFILL_KSPLIT
     if (env_p && causal) sc.paired = env_p[0] == '1';
     sc.ksplit = 1;
     if (!sc.paired && n_cu > 0 && wgs < n_cu) sc.ksplit = (int)std::min<long long>(4, n_cu / wgs);
-    static const char* env_k = std::getenv("PI_PREFILL_KSPLIT");
+    const char* env_k = std::getenv("PI_PREFILL_KSPLIT");
     if (env_k && !sc.paired) sc.ksplit = std::max(1, std::min(4, std::atoi(env_k)));
     return sc;
 }

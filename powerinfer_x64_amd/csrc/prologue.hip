@@ -594,13 +594,10 @@ hipError_t launch_kv_gather(const KvGeom& g, const int32_t* page_table, int32_t 
 }
 
 namespace {
-// PI_PROLOGUE_VEC=0 keeps every launch on the LDS-staged attn_prologue_kernel.
+// PI_PROLOGUE_VEC=0 keeps every launch on the LDS-staged attn_prologue_kernel (read per call).
 bool use_vec_prologue() {
-    static const bool on = [] {
-        const char* e = std::getenv("PI_PROLOGUE_VEC");
-        return !(e && e[0] == '0');
-    }();
-    return on;
+    const char* e = std::getenv("PI_PROLOGUE_VEC");
+    return !(e && e[0] == '0');
 }
 }  // namespace
 

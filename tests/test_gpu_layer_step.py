@@ -67,6 +67,13 @@ def test_prologue_matches_oracle(shape):
             assert np.array_equal(vc.cpu().numpy(), v[s].astype(np.float16).astype(np.float32))
 
 
+@pytest.mark.parametrize("shape", ["c2", "c4", "c4_prompt", "c4_f32"])
+def test_prologue_lds_staged_kernel(monkeypatch, shape):
+    """PI_PROLOGUE_VEC=0 (read per call): the LDS-staged prologue kernel on the same
+    shapes and checks as the register-resident one."""
+    monkeypatch.setenv("PI_PROLOGUE_VEC", "0")
+    test_prologue_matches_oracle(shape)
+
 @pytest.mark.parametrize("case", ["c1_f32", "c4_f16"])
 def test_layer_prefill_then_decode_steps(case):
     """A 48-token prompt through the prologue, then 6 decode steps (prologue

@@ -182,3 +182,22 @@ def test_prefill_head_dim_256_noncausal_grouped_vs_f64():
     out = _run(tq, tk, tv, causal=False, gqa_mode=1)
     ref = np.stack([ref64.attention(qf[i], kf, vf, lambda h: h // 4) for i in range(150)])
     assert row_rel_err(out, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("paired,ksplit,s,hq,hkv", [("1", None, 300, 32, 8), ("1", None, 129, 4, 2),
+                                                    ("0", "1", 700, 32, 8), ("0", "2", 300, 8, 2),
+                                                    ("0", "3", 129, 4, 4), ("0", "4", 520, 32, 8)])
+def test_prefill_forced_schedules(monkeypatch, paired, ksplit, s, hq, hkv):
+    """PI_PREFILL_PAIRED / PI_PREFILL_KSPLIT (read per call) force the paired query-block
+    schedule, or a given key split, on shapes the launch would schedule otherwise: every row
+    against the oracle's per-row decode, 1e-2 relative per row, argmax exact."""
+    monkeypatch.setenv("PI_PREFILL_PAIRED", paired)
+    if ksplit is not None:
+        monkeypatch.setenv("PI_PREFILL_KSPLIT", ksplit)
+    rng = np.random.default_rng(380 + s + hq)
+    tq, tk, tv = _inputs(rng, s, hq, hkv, 128)
+    out = _run(tq, tk, tv)
+    ref = _oracle_rows(tq, tk, tv, range(s))
+    assert row_rel_err(out, ref) <= 1e-2
+    n, mism, ties = argmax_agreement(out, ref)
+    assert mism == 0
