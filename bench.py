@@ -1189,7 +1189,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(c2["GB_s"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(c2["hbm_frac"], 4),
                      "traffic": _traffic("decode_kernel_c2",
-                                         ["decode_kernel<f16,128,2>", "decode_merge_kernel"])},
+                                         ["decode_kernel<f16,128,2>", "decode_merge_kernel<4>"])},
         "cpu_baseline": {**{k: (round(v, 4) if isinstance(v, float) else v)
                             for k, v in cpu.items()}, **cpu_info(),
                          "pinned": "os.sched_setaffinity to one core for the oracle calls"},

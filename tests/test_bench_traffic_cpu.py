@@ -1,0 +1,24 @@
+"""The bench line's roofline.traffic comes from the committed rocprofv3 FETCH_SIZE /
+WRITE_SIZE table of the C2 decode (profiles/decode_kernel_c2.txt); the kernel names the
+bench looks up must be the ones that table lists, or the field silently becomes null."""
+import importlib.util
+import os
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _bench():
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(ROOT, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_c2_traffic_table_has_the_benched_kernels():
+    b = _bench()
+    t = b._traffic("decode_kernel_c2", ["decode_kernel<f16,128,2>", "decode_merge_kernel<4>"])
+    assert t is not None
+    # the C2 launch's algorithmic bytes are 2.28 GB; counter traffic sits within 10 % above them
+    assert 2.2e9 <= t <= 2.6e9, t
+    src = open(os.path.join(ROOT, "bench.py")).read()
+    assert '"decode_merge_kernel<4>"' in src
