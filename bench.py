@@ -1057,6 +1057,23 @@ def bench_chunk(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
         "TFLOP_s": tf, "mfma_frac_bf16_peak": tf / MFMA_F16_PEAK_TFLOPS,
         "vs_f32_mfma_peak": tf / MFMA_F32_PEAK_TFLOPS, "ms_per_step": r["ms_avg"],
         "flops_per_launch": fl}
+    if cpu_s > 0:
+        kf, vf, qf, oh = k.cpu().numpy(), v.cpu().numpy(), q32.cpu().numpy(), o.cpu().numpy()
+        t, fl_done, i, err, rows = 0.0, 0.0, n - 1, 0.0, 0
+        with OneCore():
+            while i >= 0 and t < cpu_s:
+                t0 = time.perf_counter()
+                ref = orc.attn_decode(qf[i], kf[:hist + i + 1], vf[:hist + i + 1])
+                t += time.perf_counter() - t0
+                fl_done += 4.0 * hq * d * (hist + i + 1)
+                e = float(np.abs(oh[i].astype(np.float64) - ref).max())
+                err = e if not e <= err else err  # a NaN row stays NaN
+                rows += 1
+                i -= 97
+        res["c1_prefill_paged_f32_1024_over_8192"]["cpu_baseline"] = _cpu(
+            fl_done / t / 1e12, "TFLOP/s", f"or_attn_decode on {rows} rows ({n - 1}, {n - 98}, ...) "
+            f"of the f32 chunk over their {hist}+ keys", round(t, 3),
+            parity_max_abs_err=float(f"{err:.3e}"), gpu_out_finite=bool(np.isfinite(oh).all()))
     pool.close()
     return res
 
@@ -1131,8 +1148,13 @@ def _single(torch, rt, dev, timer, a):
     return bench_gdn_decode(torch, rt, dev, timer, st, wu)
 
 
+def _round_num(v):
+    # 4 decimals, but 3 significant digits below 0.01 so small errors do not print as 0
+    return round(v, 4) if v == 0 or abs(v) >= 1e-2 or v != v else float(f"{v:.3g}")
+
+
 def _rounded(d):
-    return {k: (round(v, 4) if isinstance(v, float) else _rounded(v) if isinstance(v, dict) else v)
+    return {k: (_round_num(v) if isinstance(v, float) else _rounded(v) if isinstance(v, dict) else v)
             for k, v in d.items()}
 
 

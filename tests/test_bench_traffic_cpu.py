@@ -22,3 +22,9 @@ def test_c2_traffic_table_has_the_benched_kernels():
     assert 2.2e9 <= t <= 2.6e9, t
     src = open(os.path.join(ROOT, "bench.py")).read()
     assert '"decode_merge_kernel<4>"' in src
+
+
+def test_rounding_keeps_small_errors():
+    b = _bench()
+    r = b._rounded({"a": 3.948807e-07, "b": 5782.0412, "c": 0.0, "d": {"e": 0.00424411}})
+    assert r["a"] == 3.95e-07 and r["b"] == 5782.0412 and r["c"] == 0.0 and r["d"]["e"] == 0.00424
