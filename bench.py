@@ -624,6 +624,11 @@ def _fp(a, offset=0):
     return ctypes.cast(ctypes.c_void_p(a.ctypes.data + 4 * offset), ctypes.POINTER(ctypes.c_float))
 
 
+def _nan_max(a, b):
+    """max(a, b), except that a NaN on either side gives NaN (and stays NaN after)."""
+    return float("nan") if (a != a or b != b) else max(a, b)
+
+
 def _cpu_repeat(fn, budget_s):
     """Calls fn() until budget_s seconds of it (at least once); returns (seconds, calls)."""
     t, n = 0.0, 0
@@ -1067,7 +1072,7 @@ def bench_chunk(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
                 t += time.perf_counter() - t0
                 fl_done += 4.0 * hq * d * (hist + i + 1)
                 e = float(np.abs(oh[i].astype(np.float64) - ref).max())
-                err = e if not e <= err else err  # a NaN row stays NaN
+                err = _nan_max(err, e)
                 rows += 1
                 i -= 97
         res["c1_prefill_paged_f32_1024_over_8192"]["cpu_baseline"] = _cpu(

@@ -11,10 +11,14 @@
  *     and a caller without a handle takes the CPU path (None);
  *   - status classes follow BackendError (src/runtime/mod.rs:6-18);
  *   - pointers named d_* are device pointers (HBM), h_* are host pointers;
- *   - `stream` is a hipStream_t; NULL is HIP's default (null) stream.  Calls
- *     are asynchronous on that stream except the h_* "sync" wrappers, which
- *     run on the handle's own stream and synchronise before returning, like
- *     GpuDevice::matvec (src/cuda/mod.rs:244-330);
+ *   - `stream` is a hipStream_t; NULL is HIP's default (null) stream, as for
+ *     every HIP API, not the handle's stream.  The null stream is the legacy
+ *     one: work on it waits for, and holds back, work on every blocking stream
+ *     of the device, so a caller that wants its calls isolated from other
+ *     streams passes a non-blocking stream of its own.  Calls are
+ *     asynchronous on that stream except the h_* "sync" wrappers, which run on
+ *     the handle's own (non-blocking) stream and synchronise before
+ *     returning, like GpuDevice::matvec (src/cuda/mod.rs:244-330);
  *   - one handle per host thread; the library takes no locks.  A handle's
  *     workspaces (decode partials, GDN prefill buffers) may serve calls on
  *     different streams: a call on another stream than the previous
@@ -350,7 +354,11 @@ int pi_gdn_layer_forward(pi_handle h, pi_gdn_layer layer, const float* h_qkv, co
 int pi_gdn_layer_forward_dev(pi_handle h, pi_gdn_layer layer, const float* d_qkv,
                              const float* d_z, const float* d_beta_raw, const float* d_a_raw,
                              int32_t n_tokens, float* d_out, void* stream);
-/* The GDN part of InferenceContext::reset (src/model/mod.rs:1867-1869): both states to zero. */
+/* The GDN part of InferenceContext::reset (src/model/mod.rs:1867-1869): both states to zero.
+ * It first waits for all work queued on the device (so forward_dev steps still pending on any
+ * stream, a caller's non-blocking stream included, finish before the states are cleared),
+ * then zeroes the conv state (both buffers of the one-launch step) and the recurrent state,
+ * and returns when they are zero.  Synchronous. */
 int pi_gdn_layer_reset(pi_handle h, pi_gdn_layer layer);
 
 /* ---- TurboQuant compressed KV (src/turboquant/mod.rs:408-566) -------------------------

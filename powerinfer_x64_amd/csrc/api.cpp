@@ -1159,6 +1159,9 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     const int D = L->dim;
     const size_t nq = (size_t)n * L->n_heads * D;
     int rc;
+    // the callers stage anything else; checked here too, before the first launch
+    if (((uintptr_t)dq | (uintptr_t)dout | (uintptr_t)dg) & 15)
+        return fail(h, PI_ERR_INVALID_ARG, "attention layer: q, gate and out rows must be 16-byte aligned");
     // one launch writes [prev, prev + 1, ...]: the prologue's start position, then the context
     // lengths of the first decode rows (d_ctx holds kLayerRows + 1 entries)
     int32_t* d_start = L->d_ctx;
@@ -1286,14 +1289,18 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
     const size_t vin = (size_t)n_tokens * L->n_kv * L->v_dim;
     const size_t gin = h_gate ? qin : 0;
     // device staging: [out | q io | k | v io | gate io] (+ packed q, v, gate for distinct widths),
-    // so the inputs (q, k, v, gate) and the outputs (out, q, k) are each one contiguous run
-    const size_t need = nq + qin + nk + vin + qin + (packed ? 0 : 2 * nq + nk);
+    // so the inputs (q, k, v, gate) and the outputs (out, q, k) are each one contiguous run.
+    // Every region the kernels address starts on a 16-byte boundary: with distinct widths
+    // the io regions' lengths need not be multiples of 4 floats, so the packed regions
+    // after them start at the next 16-byte boundary.
+    const size_t pk0 = (nq + qin + nk + vin + qin + 3) & ~(size_t)3;
+    const size_t need = packed ? pk0 : pk0 + 2 * nq + nk;
     int rc = grow(h, &L->d_buf, &L->buf_floats, need, s, "pi_attn_layer_forward staging", false);
     if (rc) return rc;
     float *dout = L->d_buf, *qio = dout + nq, *dk = qio + qin, *vio = dk + nk, *gio = vio + vin;
     float *dq = qio, *dv = vio, *dg = gio;
     if (!packed) {
-        dq = gio + qin;
+        dq = L->d_buf + pk0;
         dv = dq + nq;
         dg = dv + nk;
     }
@@ -1344,17 +1351,26 @@ int pi_attn_layer_forward_dev(pi_handle h, pi_attn_layer L, float* d_q, float* d
     if (n_tokens < 0) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_forward_dev: n_tokens=%d", n_tokens);
     if (n_tokens == 0) return PI_OK;
     const char* what = "pi_attn_layer_forward_dev";
+    if ((long long)L->seq_len + n_tokens > (long long)L->max_pages * pi::kPageTokens)
+        return fail(h, PI_ERR_OUT_OF_MEMORY, "%s: %d + %d tokens exceed the layer cache of %d", what,
+                    L->seq_len, n_tokens, L->max_pages * pi::kPageTokens);
     PI_HIP(h, hipSetDevice(h->device), what);
     hipStream_t s = pick(h, stream);
-    if (L->q_dim == L->dim && L->v_dim == L->dim)  // already in the step's packed form
+    // The step's kernels move q, the gate and out in 16-byte groups.  Rows already in the
+    // step's packed form at such addresses go straight in; otherwise they are staged in the
+    // layer's buffer (decided before anything is launched, so a call never fails half done).
+    const bool packed = L->q_dim == L->dim && L->v_dim == L->dim;
+    const bool out_ok = !((uintptr_t)d_out & 15);
+    if (packed && out_ok && !(((uintptr_t)d_q | (uintptr_t)d_gate) & 15))
         return attn_layer_step(h, L, d_q, d_k, d_v, d_gate, n_tokens, d_out, s);
     const int D = L->dim;
     const size_t nq = (size_t)n_tokens * L->n_heads * D, nk = (size_t)n_tokens * L->n_kv * D;
-    int rc = grow(h, &L->d_buf, &L->buf_floats, 2 * nq + nk, s, "pi_attn_layer_forward_dev staging", false);
+    int rc = grow(h, &L->d_buf, &L->buf_floats, 3 * nq + nk, s, "pi_attn_layer_forward_dev staging", false);
     if (rc) return rc;
-    float *dq = L->d_buf, *dg = dq + nq, *dv = dg + nq;
+    float *dq = L->d_buf, *dg = dq + nq, *dv = dg + nq, *ds = dv + nk;
     if ((rc = pack_layer_inputs(h, L, d_q, d_v, d_gate, n_tokens, dq, dv, dg, hipMemcpyDeviceToDevice, s, what))) return rc;
-    if ((rc = attn_layer_step(h, L, dq, d_k, dv, d_gate ? dg : nullptr, n_tokens, d_out, s))) return rc;
+    if ((rc = attn_layer_step(h, L, dq, d_k, dv, d_gate ? dg : nullptr, n_tokens, out_ok ? d_out : ds, s))) return rc;
+    if (!out_ok) PI_HIP(h, hipMemcpyAsync(d_out, ds, nq * 4, hipMemcpyDeviceToDevice, s), what);
     return copy_rows(h, d_q, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads, hipMemcpyDeviceToDevice, s, what);
 }
 
@@ -1429,10 +1445,15 @@ int pi_gdn_layer_reset(pi_handle h, pi_gdn_layer L) {
     PI_CHECK_HANDLE(h);
     if (!L) return fail(h, PI_ERR_INVALID_ARG, "pi_gdn_layer_reset: null layer");
     PI_HIP(h, hipSetDevice(h->device), "pi_gdn_layer_reset");
-    PI_HIP(h, hipStreamSynchronize(h->stream), "pi_gdn_layer_reset");
+    // forward_dev may have left steps on any stream (a caller's non-blocking stream
+    // included) that still read and write these states: wait for all of the device's
+    // work, then zero on the handle's stream and wait for that too
+    PI_HIP(h, hipDeviceSynchronize(), "pi_gdn_layer_reset");
     const size_t cs = (size_t)(L->d_conv - 1) * L->conv_dim;
-    if (cs) PI_HIP(h, hipMemset(L->d_conv_state, 0, cs * 4), "pi_gdn_layer_reset");
-    PI_HIP(h, hipMemset(L->d_state, 0, (size_t)L->hv * L->dk * L->dv * 4), "pi_gdn_layer_reset");
+    if (cs) PI_HIP(h, hipMemsetAsync(L->d_conv_state, 0, cs * 4, h->stream), "pi_gdn_layer_reset");
+    if (cs && L->d_conv_alt) PI_HIP(h, hipMemsetAsync(L->d_conv_alt, 0, cs * 4, h->stream), "pi_gdn_layer_reset");
+    PI_HIP(h, hipMemsetAsync(L->d_state, 0, (size_t)L->hv * L->dk * L->dv * 4, h->stream), "pi_gdn_layer_reset");
+    PI_HIP(h, hipStreamSynchronize(h->stream), "pi_gdn_layer_reset");
     return PI_OK;
 }
 

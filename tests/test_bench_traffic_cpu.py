@@ -28,3 +28,17 @@ def test_rounding_keeps_small_errors():
     b = _bench()
     r = b._rounded({"a": 3.948807e-07, "b": 5782.0412, "c": 0.0, "d": {"e": 0.00424411}})
     assert r["a"] == 3.95e-07 and r["b"] == 5782.0412 and r["c"] == 0.0 and r["d"]["e"] == 0.00424
+
+
+def test_nan_max_keeps_a_nan():
+    b = _bench()
+    nan = float("nan")
+    err = 0.0
+    for e in [1e-4, nan, 3e-4, 2e-4]:  # a NaN row in the middle of the sample
+        err = b._nan_max(err, e)
+    assert err != err
+    err = 0.0
+    for e in [1e-4, 3e-4, 2e-4]:
+        err = b._nan_max(err, e)
+    assert err == 3e-4
+    assert b._nan_max(nan, 1.0) != b._nan_max(nan, 1.0)

@@ -154,3 +154,31 @@ def test_gdn_layer_forward_dev_equals_host_slices():
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), n
     host.close()
     devl.close()
+
+
+def test_gdn_layer_reset_orders_after_side_stream_steps():
+    """Steps enqueued on a non-blocking torch side stream, then pi_gdn_layer_reset with no
+    synchronisation in between: the reset waits for those steps before it zeroes the conv
+    state (both of the one-token step's alternating buffers) and the recurrent state, so the
+    steps that follow give a fresh layer's bits."""
+    import torch
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    rng = np.random.default_rng(99)
+    hk, hv, d = 2, 4, 128
+    w = _weights(rng, hk, hv, d, d, 4)
+    used, fresh = rt.GdnLayer(dev, hk, hv, d, d, *w), rt.GdnLayer(dev, hk, hv, d, d, *w)
+    side = torch.cuda.Stream()
+    before = [_inputs(rng, n, hk, hv, d, d) for n in (300, 1, 1, 1)]
+    after = [_inputs(rng, n, hk, hv, d, d) for n in (1, 1, 20, 1)]
+    with torch.cuda.stream(side):
+        for x in before:
+            used.forward_dev(*(torch.from_numpy(a).to("cuda", non_blocking=False) for a in x))
+        used.reset()
+        got = [used.forward_dev(*(torch.from_numpy(a).to("cuda") for a in x)) for x in after]
+    side.synchronize()
+    for x, g in zip(after, got):
+        want = fresh.forward(*x)
+        assert np.array_equal(g.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    used.close()
+    fresh.close()

@@ -162,3 +162,40 @@ def test_layer_reset_and_full_cache():
     assert layer.seq_len == 0
     b = layer.forward(q.copy(), k.copy(), v)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.float16, 128), (torch.float16, 64), (torch.float32, 128)])
+def test_layer_forward_dev_misaligned_rows(dtype, d):
+    """q, the gate and out at 4-byte offsets (views into larger buffers) give the bits of the
+    same calls on 16-byte-aligned tensors, over a prompt, decode tokens and a chunk: the
+    layer stages such rows itself, so nothing fails after the prologue has already
+    rotated q and k and appended to the cache."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    hq, hkv = 4, 2
+    rng = np.random.default_rng(0x1AA + d)
+    a = rt.AttnLayer(dev, 256, hq, hkv, d, dtype, rope_base=1e6)
+    b = rt.AttnLayer(dev, 256, hq, hkv, d, dtype, rope_base=1e6)
+
+    def shifted(x):  # the same values one float past a 16-byte boundary
+        buf = torch.empty(x.numel() + 4, dtype=x.dtype, device=x.device)
+        view = buf[1:1 + x.numel()].view(x.shape)
+        view.copy_(x)
+        return view
+
+    for n in (40, 1, 1, 20):
+        q = torch.from_numpy(rng.standard_normal((n, hq, d)).astype(np.float32)).cuda()
+        k = torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float32)).cuda()
+        v = torch.from_numpy(rng.standard_normal((n, hkv, d)).astype(np.float32)).cuda()
+        g = torch.from_numpy(rng.standard_normal((n, hq, d)).astype(np.float32)).cuda()
+        qa, ka = q.clone(), k.clone()
+        want = a.forward_dev(qa, ka, v, gate=g)
+        qb, kb, gb = shifted(q), k.clone(), shifted(g)
+        ob = shifted(torch.zeros((n, hq, d), dtype=torch.float32, device=q.device))
+        assert qb.data_ptr() % 16 == 4 and gb.data_ptr() % 16 == 4 and ob.data_ptr() % 16 == 4
+        got = b.forward_dev(qb, kb, v, gate=gb, out=ob)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32)), n
+        assert torch.equal(qb.view(torch.int32), qa.view(torch.int32)), n
+        assert torch.equal(kb.view(torch.int32), ka.view(torch.int32)), n
+        assert a.seq_len == b.seq_len
