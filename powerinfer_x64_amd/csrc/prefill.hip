@@ -33,7 +33,14 @@ namespace {
 
 constexpr int BN = 64;         // keys per block
 constexpr int ROWS = 32;       // query rows per wavefront
-constexpr float kLazy = 8.0f;  // log2 headroom before the running max moves
+// The running max of a row moves only when a lane's exps of a tile against it sum past
+// kSumCap = 2^13 (an overflow to inf or a NaN counts too): the tile's max is then taken and
+// the tile redone against it.  With at most 32 exps per lane, a sum within the cap means
+// no score exceeded the max by more than 13 (log2 units), so every P value stays below
+// 2^13, far inside the f32 / bf16 range; a sum past it means one exceeded it by more than 8
+// (or 9 at 16 exps per lane).  Most tiles take no max at all; the first tile of a row always
+// moves it (from -1e30).
+constexpr float kSumCap = 8192.0f;
 
 template <typename T>
 struct Mfma;
@@ -412,31 +419,37 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
                     if (key >= Sk || (a.causal && key > q_off + qpos)) s[tt][e] = -INFINITY;
                 }
         }
-        float mx = max32(s[0], s[1]);
-        if (__any(mx * c > m_run + kLazy)) {
-            mx = wave_max_xor(mx, 32);
+        // exps against the current running max; their sum also tells whether a score
+        // outgrew it (see kSumCap), and only then is the max taken and the tile redone
+        auto exps = [&]() {
+            float ls[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int tt = ks >> 1, i0 = 2 * (ks & 1);
+                float p[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    p[j] = fast_exp2(__builtin_fmaf(s[tt][4 * i0 + j], c, -m_run));
+                    p[4 + j] = fast_exp2(__builtin_fmaf(s[tt][4 * (i0 + 1) + j], c, -m_run));
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pb[ks][j] = (T)p[j];
+                ls[ks] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            }
+            return (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        };
+        float lt = exps();
+        if (__any(!(lt <= kSumCap))) {
+            const float mx = wave_max_xor(max32(s[0], s[1]), 32);
             const float m_new = fmaxf(m_run, mx * c);
             const float alpha = fast_exp2(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
             for (int i = 0; i < D / 32; ++i) o[i] *= alpha;
             m_run = m_new;
+            lt = exps();
         }
-        float ls[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int tt = ks >> 1, i0 = 2 * (ks & 1);
-            float p[8];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                p[j] = fast_exp2(__builtin_fmaf(s[tt][4 * i0 + j], c, -m_run));
-                p[4 + j] = fast_exp2(__builtin_fmaf(s[tt][4 * (i0 + 1) + j], c, -m_run));
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) pb[ks][j] = (T)p[j];
-            ls[ks] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-        }
-        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        l_run += lt;
     };
 
     issue_unit(0);
@@ -849,8 +862,27 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
                     if (key >= Sk || (a.causal && key > q_off + qpos)) s[kb][r] = -INFINITY;
                 }
         }
-        float mx = max16(s);
-        if (__any(mx * c > m_run + kLazy)) {
+        // exps against the current running max; the max only when their sum says a
+        // score outgrew it (see kSumCap)
+        auto exps = [&]() {
+            float ls[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float p[8];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    p[r] = fast_exp2(__builtin_fmaf(s[2 * j][r], c, -m_run));
+                    p[4 + r] = fast_exp2(__builtin_fmaf(s[2 * j + 1][r], c, -m_run));
+                }
+#pragma unroll
+                for (int r = 0; r < 8; ++r) pb[j][r] = (T)p[r];
+                ls[j] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            }
+            return ls[0] + ls[1];
+        };
+        float lt = exps();
+        if (__any(!(lt <= kSumCap))) {
+            float mx = max16(s);
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float m_new = fmaxf(m_run, mx * c);
@@ -859,21 +891,9 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < NDB; ++i) o[i] *= alpha;
             m_run = m_new;
+            lt = exps();
         }
-        float ls[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float p[8];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                p[r] = fast_exp2(__builtin_fmaf(s[2 * j][r], c, -m_run));
-                p[4 + r] = fast_exp2(__builtin_fmaf(s[2 * j + 1][r], c, -m_run));
-            }
-#pragma unroll
-            for (int r = 0; r < 8; ++r) pb[j][r] = (T)p[r];
-            ls[j] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-        }
-        l_run += ls[0] + ls[1];
+        l_run += lt;
     };
     auto mfma_phase = [&](int t) {
         const bool pv = t >= 1 && tb + t - 1 < w_tiles;

@@ -201,3 +201,25 @@ def test_prefill_forced_schedules(monkeypatch, paired, ksplit, s, hq, hkv):
     assert row_rel_err(out, ref) <= 1e-2
     n, mism, ties = argmax_agreement(out, ref)
     assert mism == 0
+
+
+@pytest.mark.parametrize("s,hq,hkv,d", [(513, 32, 8, 128), (300, 16, 2, 256)])
+def test_prefill_running_max_moves_in_late_tiles(s, hq, hkv, d):
+    """Keys whose scale grows along the prompt, plus a few spike keys: the scores of later
+    tiles exceed a row's running max by up to dozens of log2 units, tile after tile, so the
+    kernels' rare path (max, rescale of O and the row sum, exps redone against the new max)
+    runs in the middle of rows, not only on their first tile.  Every row against the oracle."""
+    rng = np.random.default_rng(0x1A70 + d)
+    q = rng.standard_normal((s, hq, d)).astype(np.float32)
+    k = rng.standard_normal((s, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((s, hkv, d)).astype(np.float32)
+    k *= (1.0 + np.arange(s, dtype=np.float32) / 32.0)[:, None, None]
+    for t in (97, 200, 260):  # spike keys: aligned with their row's query
+        if t < s:
+            k[t, 0] = 6.0 * q[t, 0]
+    qr, kr = orc.attn_prepare(q, k, hq, hkv, d, rope_base=1e6, pos0=0)
+    tq, tk, tv = (torch.from_numpy(x).to(torch.bfloat16) for x in (qr, kr, v))
+    out = _run(tq, tk, tv)
+    ref = _oracle_rows(tq, tk, tv, range(s))
+    assert np.isfinite(out).all()
+    assert row_rel_err(out, ref) <= 1e-2
