@@ -6,8 +6,10 @@ order/symmetry, orthogonality, reconstruction MSE, QJL dot accuracy, packing
 round trips, compressed sizes, cache compression ratio).  Properties: the
 QJL estimator is unbiased, the precomputed-query path equals the direct one,
 and a float64 numpy evaluation of the cache attention from the unpacked
-fields agrees with the f32 restatement.  A planted sign slip in the QJL
-correction is caught.
+fields agrees with the f32 restatement.  The codebooks equal float64 Lloyd-Max
+iteration for N(0,1), and every code and QJL sign of the quantizer equals a
+float64 evaluation of its steps.  Planted slips (a sign slip in the QJL
+correction, a dropped sqrt(d) scale) are caught.
 """
 import numpy as np
 import pytest
@@ -244,3 +246,86 @@ def test_cache_compression_ratio():
     T, n_kv, dim = 10, 2, 16
     mem = T * n_kv * (o.tq_compressed_bytes(3, dim, dim) + 4 + 2 * dim)
     assert T * n_kv * dim * 4 * 2 / mem > 2.0
+
+
+def _lloyd_max_gaussian(levels, iters=3000):
+    """Lloyd-Max quantizer of N(0,1) with `levels` levels in float64 (Max 1960): boundaries
+    at the midpoints of adjacent centroids, each centroid the conditional mean of its cell,
+    E[X | a < X < b] = (phi(a) - phi(b)) / (Phi(b) - Phi(a))."""
+    from scipy.stats import norm
+    c = np.linspace(-2.0, 2.0, levels)
+    for _ in range(iters):
+        b = np.concatenate(([-np.inf], (c[1:] + c[:-1]) / 2, [np.inf]))
+        c = (norm.pdf(b[:-1]) - norm.pdf(b[1:])) / (norm.cdf(b[1:]) - norm.cdf(b[:-1]))
+    return c
+
+
+@pytest.mark.parametrize("bits", [1, 3, 4])
+def test_centroids_are_the_gaussian_lloyd_max_levels(bits):
+    """The 1-, 3- and 4-bit codebooks of src/turboquant/mod.rs:27-41 are Max's optimal
+    quantizers of N(0,1), printed to 4 decimals: the oracle's tables equal float64 Lloyd
+    iteration to that rounding.  (The reference's 2-bit table, +-0.4950 / +-1.4996, is not
+    Max's +-0.4528 / +-1.5104; the oracle keeps the reference's values, and no path here
+    quantizes at 2 bits.)"""
+    got = o.tq_centroids(bits).astype(np.float64)
+    assert np.abs(got - _lloyd_max_gaussian(1 << bits)).max() <= 6e-4
+
+
+def test_two_bit_table_is_the_references_not_maxs():
+    got = o.tq_centroids(2).astype(np.float64)
+    assert np.allclose(got, [-1.4996, -0.4950, 0.4950, 1.4996], atol=1e-6)
+    assert np.abs(got - _lloyd_max_gaussian(4)).max() > 0.04
+
+
+def _quantize_f64(x, R, G, sqrt_d=True):
+    """quantize_vector (src/turboquant/mod.rs:128-187) evaluated in float64: rotate, scale by
+    sqrt(d) (sqrt_d=False plants the dropped-scale slip), nearest centroid with the first
+    strict minimum winning, residual, QJL signs G.r >= 0.  Also returns, per coordinate and per
+    sign, whether f32 rounding could flip the decision (within 1e-4 of a cell boundary, or a
+    projection within 1e-3 of zero); those are left out of the comparison."""
+    d = x.size
+    c = o.tq_centroids(3).astype(np.float64)
+    rot = R.astype(np.float64) @ x.astype(np.float64)
+    if sqrt_d:
+        rot *= np.sqrt(d)
+    dist = np.abs(rot[:, None] - c[None, :])
+    idx = np.argmin(dist, axis=1)  # the first of equal minima, as `dist < best_dist` keeps
+    bounds = (c[1:] + c[:-1]) / 2
+    amb_idx = np.abs(rot[:, None] - bounds[None, :]).min(axis=1) < 1e-4
+    res = rot - c[idx]
+    proj = G.astype(np.float64) @ res
+    return idx.astype(np.uint8), (proj >= 0).astype(np.uint8), amb_idx, np.abs(proj) < 1e-3
+
+
+@pytest.mark.parametrize("dim", [16, 128])
+@pytest.mark.parametrize("seed", [0xCAFEBABE, 0xCAFEBABF, 7])
+def test_quantizer_codes_match_float64_brute_force(dim, seed):
+    """Every 3-bit code and QJL sign of or_tq_quantize equals the float64 evaluation of the
+    reference's steps (away from the f32 rounding ties), and whole records are byte-identical
+    to the float64 fields packed; the same check rejects a quantizer that drops the sqrt(d)
+    scale before the nearest-centroid search, which a reconstruction-MSE bound accepts."""
+    R, G = o.tq_matrices(dim, seed)
+    rng = np.random.default_rng(seed & 0xFFFF)
+    n_vec, n_amb, exact, slip_diff, slip_mse = 40, 0, 0, 0, []
+    for _ in range(n_vec):
+        x = rng.standard_normal(dim).astype(np.float32)
+        x /= np.linalg.norm(x)
+        pk = o.tq_quantize(x, R, G, 3, dim)
+        idx_o, sg_o = o.tq_unpack(pk, dim, 3, dim)
+        idx, sg, amb_i, amb_s = _quantize_f64(x, R, G)
+        assert np.array_equal(idx_o[~amb_i], idx[~amb_i])
+        assert np.array_equal(sg_o[~amb_s], sg[~amb_s])
+        n_amb += int(amb_i.sum() + amb_s.sum())
+        if not amb_i.any() and not amb_s.any():
+            assert np.array_equal(pk, o.tq_pack(idx, 3, sg))
+            exact += 1
+        # planted slip: no sqrt(d) scale
+        idx_b, _, _, _ = _quantize_f64(x, R, G, sqrt_d=False)
+        slip_diff += int((idx_b != idx_o).sum())
+        rec = o.tq_dequantize(o.tq_pack(idx_b, 3, np.zeros(dim, np.uint8)), R, 3)
+        slip_mse.append(float(((rec - x) ** 2).mean()))
+    assert n_amb <= 0.02 * n_vec * 2 * dim
+    assert exact >= n_vec * 3 // 4
+    assert slip_diff >= 0.3 * n_vec * dim
+    if dim == 16:  # the slipped codes still pass the reconstruction bound of :792-834
+        assert np.mean(slip_mse) < 0.2
