@@ -515,32 +515,42 @@ static pi::DecodeParams decode_params(const float* d_q, const int32_t* d_page_ta
     return p;
 }
 
+// The decode launch on the handle's workspace.  max_tokens bounds every sequence's length
+// (0: the table row's 16 * max_pages); the layer seam passes its exact length, so the work
+// items are sized for the tokens the sequence holds, not for its whole cache.
+static int attn_decode_ws(pi_handle h, const char* fn, const float* d_q, pi_kv_pool pool,
+                          const int32_t* d_page_table, int32_t max_pages, const int32_t* d_ctx_len,
+                          int32_t batch, int32_t n_q_heads, int32_t gqa_mode, float scale,
+                          const float* d_gate, float* d_out, hipStream_t s, int32_t max_tokens) {
+    const pi::KvGeom& g = pool->g;
+    int rc = decode_check(h, fn, g, d_q, d_page_table, d_ctx_len, d_out, max_pages, batch,
+                          n_q_heads, gqa_mode);
+    if (!rc) rc = gate_check(h, fn, d_gate);
+    if (rc) return rc;
+    if (batch == 0) return PI_OK;
+    PI_HIP(h, hipSetDevice(h->device), fn);
+    if ((rc = ws_begin(h, s, fn))) return rc;
+    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, gqa_mode, h->device, max_tokens);
+    const size_t need_o = pi::decode_ws_floats_o(g, plan);
+    const size_t need_ml = need_o / g.head_dim * 2;
+    if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "decode workspace", false))) return rc;
+    if ((rc = grow(h, &h->dws.seg_runs, &h->dws.capacity_runs, pi::decode_ws_ints_runs(g, plan), s,
+                   "decode workspace", false))) return rc;
+    const pi::DecodeParams p = decode_params(d_q, d_page_table, max_pages, d_ctx_len, batch, n_q_heads,
+                                             gqa_mode, scale, d_gate, d_out, plan);
+    PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), fn);
+    return ws_end(h, s, fn);
+}
+
 int pi_attn_decode(pi_handle h, const float* d_q, pi_kv_pool pool, const int32_t* d_page_table,
                    int32_t max_pages, const int32_t* d_ctx_len, int32_t batch, int32_t n_q_heads,
                    int32_t gqa_mode, float scale, const float* d_gate, float* d_out,
                    void* stream) {
     PI_CHECK_HANDLE(h);
     if (!pool) return fail(h, PI_ERR_INVALID_ARG, "pi_attn_decode: null argument");
-    const pi::KvGeom& g = pool->g;
-    int rc = decode_check(h, "pi_attn_decode", g, d_q, d_page_table, d_ctx_len, d_out, max_pages,
-                          batch, n_q_heads, gqa_mode);
-    if (!rc) rc = gate_check(h, "pi_attn_decode", d_gate);
-    if (rc) return rc;
-    if (batch == 0) return PI_OK;
-    hipStream_t s = pick(h, stream);
-    PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode");
-    if ((rc = ws_begin(h, s, "pi_attn_decode"))) return rc;
-    const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, gqa_mode, h->device);
-    const size_t need_o = pi::decode_ws_floats_o(g, plan);
-    const size_t need_ml = need_o / g.head_dim * 2;
-    if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_attn_decode workspace", false))) return rc;
-    if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_attn_decode workspace", false))) return rc;
-    if ((rc = grow(h, &h->dws.seg_runs, &h->dws.capacity_runs, pi::decode_ws_ints_runs(g, plan), s,
-                   "pi_attn_decode workspace", false))) return rc;
-    const pi::DecodeParams p = decode_params(d_q, d_page_table, max_pages, d_ctx_len, batch, n_q_heads,
-                                             gqa_mode, scale, d_gate, d_out, plan);
-    PI_HIP(h, pi::launch_decode(g, p, h->dws, plan, s), "pi_attn_decode");
-    return ws_end(h, s, "pi_attn_decode");
+    return attn_decode_ws(h, "pi_attn_decode", d_q, pool, d_page_table, max_pages, d_ctx_len, batch,
+                          n_q_heads, gqa_mode, scale, d_gate, d_out, pick(h, stream), 0);
 }
 
 int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
@@ -558,6 +568,7 @@ int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
     if (batch == 0) return PI_OK;
     PI_HIP(h, hipSetDevice(h->device), "pi_attn_decode_noalloc");
     const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, gqa_mode, h->device);
+    const size_t limit = pi::kDecodeScratchFloats;
     // partial o, then (m, l), then the segments' run table, each at a 256-byte boundary
     // inside the scratch
     const size_t need_o = pi::decode_ws_floats_o(g, plan);
@@ -565,12 +576,12 @@ int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
     const size_t need_ml = need_o / g.head_dim * 2;
     const size_t off_runs = (off_ml + need_ml + 63) / 64 * 64;
     const size_t need_runs = pi::decode_ws_ints_runs(g, plan);
-    if (off_runs + need_runs > pi::kDecodeScratchFloats)
+    if (off_runs + need_runs > limit)
         return fail(h, PI_ERR_UNSUPPORTED,
                     "pi_attn_decode_noalloc: %zu scratch floats needed (batch %d x %d kv heads + %d "
                     "workgroups, %d q heads per kv head, head_dim %d) > the fixed %zu",
                     off_runs + need_runs, batch, g.n_kv_heads, plan.grid, plan.group, g.head_dim,
-                    pi::kDecodeScratchFloats);
+                    limit);
     pi::DecodeWorkspace ws;
     ws.partial_o = h->scratch;
     ws.partial_ml = h->scratch + off_ml;
@@ -1162,14 +1173,25 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     // the callers stage anything else; checked here too, before the first launch
     if (((uintptr_t)dq | (uintptr_t)dout | (uintptr_t)dg) & 15)
         return fail(h, PI_ERR_INVALID_ARG, "attention layer: q, gate and out rows must be 16-byte aligned");
-    // one launch writes [prev, prev + 1, ...]: the prologue's start position, then the context
-    // lengths of the first decode rows (d_ctx holds kLayerRows + 1 entries)
-    int32_t* d_start = L->d_ctx;
-    PI_HIP(h, pi::launch_fill_iota(d_start, std::min(n, kLayerRows) + 1, prev, s), "attention layer");
-    if ((rc = pi_attn_prologue(h, dq, dk, dv, L->d_qn, L->d_kn, L->eps, L->rope_dim, L->rope_base,
-                               L->has_sections ? L->sections : nullptr, L->pool, L->d_pt,
-                               L->max_pages, d_start, 1, n, L->n_heads, sv)))
-        return rc;
+    // The prologue (norm, RoPE, append at positions prev ..) takes its start position as a
+    // scalar and writes the context lengths of the decode rows of the step (row i: prev + i +
+    // 1 keys) into d_ctx, so no launch of its own fills them.
+    const bool rows = !((n > 1 && (D == 128 || D == 256) && L->kv_dtype == PI_F16) ||
+                        (n > 1 && L->kv_dtype == PI_F32));
+    {
+        const pi::KvGeom& g = L->pool->g;
+        const int rd = L->rope_dim <= 0 ? D : std::min(L->rope_dim, D);
+        if (rd / 2 > 128) return fail(h, PI_ERR_UNSUPPORTED, "attention layer: rope_dim %d", rd);
+        pi::RopeFreqs f;
+        std::memset(&f, 0, sizeof f);
+        if (L->has_sections) imrope_freqs(L->rope_base, rd, f.f);
+        else norm_rope_freqs(L->rope_base, rd, f.f);
+        PI_HIP(h, pi::launch_attn_prologue(dq, dk, dv, L->d_qn, L->d_kn, L->eps, f, rd / 2,
+                                           L->has_sections ? 1 : 0, g, L->d_pt, L->max_pages, nullptr,
+                                           1, n, L->n_heads, s, prev, L->d_ctx,
+                                           rows ? std::min(n, kLayerRows) : 0),
+               "attention layer");
+    }
     const float scale = 1.0f / std::sqrt((float)D);
     // the prefill kernels apply a 16-byte-aligned gate where they write the output; another
     // gate takes a launch of its own after them
@@ -1206,14 +1228,15 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
                "attention layer");
         if (dg && !dg_fused) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
     } else {
-        // one decode row per token over the paged cache: row i sees prev + i + 1 keys
+        // one decode row per token over the paged cache: row i sees prev + i + 1 keys (the
+        // prologue wrote the first kLayerRows lengths)
         for (int r0 = 0; r0 < n; r0 += kLayerRows) {
-            const int rows = std::min(kLayerRows, n - r0);
-            if (r0 > 0) PI_HIP(h, pi::launch_fill_iota(L->d_ctx + 1, rows, prev + r0 + 1, s), "attention layer");
+            const int nr = std::min(kLayerRows, n - r0);
+            if (r0 > 0) PI_HIP(h, pi::launch_fill_iota(L->d_ctx, nr, prev + r0 + 1, s), "attention layer");
             const size_t off = (size_t)r0 * L->n_heads * D;
-            if ((rc = pi_attn_decode(h, dq + off, L->pool, L->d_pt, L->max_pages, L->d_ctx + 1, rows,
-                                     L->n_heads, L->gqa_mode, scale, dg ? dg + off : nullptr,
-                                     dout + off, sv)))
+            if ((rc = attn_decode_ws(h, "attention layer", dq + off, L->pool, L->d_pt, L->max_pages, L->d_ctx,
+                                     nr, L->n_heads, L->gqa_mode, scale, dg ? dg + off : nullptr,
+                                     dout + off, s, prev + r0 + nr)))
                 return rc;
         }
     }

@@ -716,7 +716,7 @@ hipError_t launch_t(const KvGeom& g, const DecodeParams& p, const DecodeWorkspac
 }  // namespace
 
 DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
-                       int32_t gqa_mode, int device) {
+                       int32_t gqa_mode, int device, int32_t max_tokens) {
     DecodePlan plan;
     // head blocking: the modulo map (h % Hkv) gives KV head k the heads k, k + Hkv, ... below
     // Hq, at most ceil(Hq / Hkv); a segment takes up to 16 of them and cols * D <= 2048 floats
@@ -746,8 +746,12 @@ DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_
     }
     // Item size: kItemPages pages, halved while the launch's upper bound of
     // items would not give every workgroup two items (small batches and short
-    // contexts then still spread over the whole chip).
-    const long long max_seg_pages = (long long)batch * n_seg * max_pages;
+    // contexts then still spread over the whole chip).  The bound is the caller's
+    // max_tokens per sequence when it gives one, else the table row.
+    const long long seq_pages =
+        max_tokens > 0 ? std::min<long long>(max_pages, ((long long)max_tokens + kPageTokens - 1) / kPageTokens)
+                       : max_pages;
+    const long long max_seg_pages = (long long)batch * n_seg * seq_pages;
     int ip = kItemPages;
     while (ip > 1 && max_seg_pages / ip < 2LL * plan.grid) ip >>= 1;
     plan.item_pages = ip;

@@ -95,9 +95,10 @@ constexpr size_t kDecodeScratchFloats = (size_t)4 << 20;
 // once per device with hipGetSymbolAddress.
 hipError_t decode_scratch(int device, float** ptr);
 
-// Grid size, head blocking and workspace bound of a decode launch on `device`.
+// Grid size, head blocking and workspace bound of a decode launch on `device`.  max_tokens
+// bounds the tokens any sequence holds (<= 0: 16 * max_pages); it sizes the work items.
 DecodePlan decode_plan(const KvGeom& g, int32_t batch, int32_t max_pages, int32_t n_q_heads,
-                       int32_t gqa_mode, int device);
+                       int32_t gqa_mode, int device, int32_t max_tokens = 0);
 size_t decode_ws_floats_o(const KvGeom& g, const DecodePlan& plan);
 // int32 entries of the per-segment run table (2 per (sequence, KV head)).
 size_t decode_ws_ints_runs(const KvGeom& g, const DecodePlan& plan);
@@ -140,7 +141,8 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,
                                 const int32_t* page_table, int32_t max_pages,
                                 const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
-                                int32_t n_q_heads, hipStream_t s);
+                                int32_t n_q_heads, hipStream_t s, int32_t start_scalar = 0,
+                                int32_t* ctx_out = nullptr, int32_t n_ctx = 0);
 
 // Causal (or full) flash attention of seq_len query rows per sequence over
 // n_keys keys; query row i sits at key position q_off + i (a fresh prompt:

@@ -267,6 +267,23 @@ __global__ __launch_bounds__(1024) void softmax_row_kernel(float* __restrict__ x
     for (int i = tid; i < n; i += 1024) x[i] *= inv;
 }
 
+// Start positions of a prologue launch: one per sequence on the device, or (dev null) the
+// scalar first position of a one-sequence launch.  A launch may also write the context
+// lengths of the decode rows that follow it, ctx_out[i] = scalar + 1 + i for i < n_ctx
+// (row i attends the keys up to its own position), so the layer step needs no launch of
+// its own for them.
+struct PrologueStart {
+    const int32_t* dev;
+    int32_t scalar;
+    int32_t* ctx_out;
+    int32_t n_ctx;
+    __device__ __forceinline__ int of(int sq) const { return dev ? dev[sq] : scalar; }
+    __device__ __forceinline__ void write_ctx() const {
+        if (ctx_out && blockIdx.x == 0 && blockIdx.y == 0)
+            for (int i = threadIdx.x; i < n_ctx; i += blockDim.x) ctx_out[i] = scalar + 1 + i;
+    }
+};
+
 // Fused decode / prefill prologue of a full-attention layer
 // (src/model/mod.rs:1035-1146): for token t of sequence s at position
 // start_pos[s] + t, every q head and k head is RMS-normed (optional weights)
@@ -284,13 +301,14 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ qn, const float* __restrict__ kn, float eps, RopeFreqs f,
     int n_pairs, int neox, KvGeom g, const int32_t* __restrict__ pt, int max_pages,
-    const int32_t* __restrict__ start_pos, int n_seq, int n_tok, int hq) {
+    PrologueStart start_pos, int n_seq, int n_tok, int hq) {
     __shared__ float row_s[4][256];
     __shared__ float cs_s[2][128];  // cos, sin of pair i at this token's position
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int D = g.head_dim, hkv = g.n_kv_heads, heads = hq + hkv;
     const int t = blockIdx.x % n_tok, sq = blockIdx.x / n_tok;
-    const int pos = start_pos[sq] + t;
+    const int pos = start_pos.of(sq) + t;
+    start_pos.write_ctx();
     const bool table = gridDim.y == 1;  // uniform per launch
     if (table) {
         for (int i = threadIdx.x; i < n_pairs; i += 256) {
@@ -398,7 +416,7 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
     float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ qn, const float* __restrict__ kn, float eps, RopeFreqs f,
     int n_pairs, int neox, KvGeom g, const int32_t* __restrict__ pt, int max_pages,
-    const int32_t* __restrict__ start_pos, int n_seq, int n_tok, int hq) {
+    PrologueStart start_pos, int n_seq, int n_tok, int hq) {
     constexpr int D = 64 * EPL;
     __shared__ float cs_s[2][128];  // cos, sin of pair i at this token's position
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -415,7 +433,8 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
         u = (m >> 4) * 128 + x * 16 + (m & 15);
     }
     const int t = u % n_tok, sq = u / n_tok;
-    const int pos = start_pos[sq] + t;
+    const int pos = start_pos.of(sq) + t;
+    start_pos.write_ctx();
     if (table) {
         for (int i = threadIdx.x; i < n_pairs; i += 256) {
             const float theta = (float)pos * f.f[i];
@@ -606,7 +625,10 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,
                                 const int32_t* page_table, int32_t max_pages,
                                 const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
-                                int32_t n_q_heads, hipStream_t s) {
+                                int32_t n_q_heads, hipStream_t s, int32_t start_scalar,
+                                int32_t* ctx_out, int32_t n_ctx) {
+    if (!start_pos && n_seq != 1) return hipErrorInvalidValue;
+    const PrologueStart sp{start_pos, start_scalar, ctx_out, ctx_out ? n_ctx : 0};
     const long long toks = (long long)n_seq * n_tok;
     if (toks <= 0) return hipSuccess;
     if (toks > 0x7fffffffLL || n_pairs > 128) return hipErrorInvalidValue;
@@ -621,7 +643,7 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
         2 * n_pairs <= g.head_dim && aligned && use_vec_prologue()) {
 #define PI_PROLOGUE_VEC(PT, E)                                                                     \
     hipLaunchKernelGGL((attn_prologue_vec_kernel<PT, E>), grid, dim3(256), 0, s, q, k, v, q_norm_w, \
-                       k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages, start_pos,    \
+                       k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages, sp,           \
                        n_seq, n_tok, n_q_heads)
         const bool hp = g.dtype == 1;
         switch (epl) {
@@ -635,11 +657,11 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
     if (g.dtype == 1)
         hipLaunchKernelGGL(attn_prologue_kernel<f16>, grid, dim3(256), 0, s, q, k, v, q_norm_w,
                            k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages,
-                           start_pos, n_seq, n_tok, n_q_heads);
+                           sp, n_seq, n_tok, n_q_heads);
     else
         hipLaunchKernelGGL(attn_prologue_kernel<float>, grid, dim3(256), 0, s, q, k, v, q_norm_w,
                            k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages,
-                           start_pos, n_seq, n_tok, n_q_heads);
+                           sp, n_seq, n_tok, n_q_heads);
     return hipGetLastError();
 }
 
