@@ -181,10 +181,12 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
  * row d_page_table[max_pages] (the chunk's own K/V appended first, as the
  * reference appends before it attends).  d_q [n_tok][n_q_heads][D] in the
  * pool's dtype (normed, rotated), d_out [n_tok][n_q_heads][D] f32.  f16 pool
- * (D = 128 or 256): the pages are gathered into contiguous f16 rows in the
- * handle's workspace, then the flash prefill runs with its queries offset by
- * start_pos.  f32 pool (D = 64, 128 or 256): a kernel reads the pages directly
- * and keeps f32 accuracy (bf16 hi + lo operand splits on the MFMA). */
+ * at D = 64 or 128: the flash prefill reads K/V straight from the pages (no
+ * copy of the history); at D = 256 the pages are gathered into contiguous f16
+ * rows in the handle's workspace first.  f32 pool (D = 64, 128 or 256): a
+ * kernel reads the pages directly and keeps f32 accuracy (bf16 hi + lo operand
+ * splits on the MFMA).  A page id outside [0, n_pages) holds no tokens: its
+ * keys are left out of the softmax, as in pi_attn_decode. */
 int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
                           const int32_t* d_page_table, int32_t max_pages, int32_t start_pos,
                           int32_t n_tok, int32_t n_q_heads, int32_t gqa_mode, float scale,
@@ -317,10 +319,10 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer layer, float* h_q, float* h
                           const float* h_v, const float* h_gate, int32_t n_tokens, float* h_out);
 /* pi_attn_layer_forward with device pointers (same layouts), enqueued on `stream` without
  * host copies or waits: the layer's sequence length advances when the call returns.  A
- * prompt or a continued chunk of an f16 cache at head_dim 128 / 256 runs the flash prefill
- * (a continued chunk over its pages, as pi_attn_prefill_paged), of an f32 cache the f32
- * prefill over its pages; an f16 cache at head_dim 64 runs one decode row per token.  Calls
- * on one layer must be ordered on one stream. */
+ * prompt or a continued chunk (more than one token) runs the flash prefill over the layer's
+ * pages, as pi_attn_prefill_paged (f16 cache: straight from the pages at head_dim 64 / 128;
+ * f32 cache: the f32 prefill); a single token runs the decode.  Calls on one layer must be
+ * ordered on one stream. */
 int pi_attn_layer_forward_dev(pi_handle h, pi_attn_layer layer, float* d_q, float* d_k,
                               const float* d_v, const float* d_gate, int32_t n_tokens,
                               float* d_out, void* stream);

@@ -639,9 +639,8 @@ int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
                     start_pos, n_tok, max_pages, n_q_heads);
     if (gqa_mode != PI_GQA_MODULO && gqa_mode != PI_GQA_GROUPED)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: gqa_mode %d", gqa_mode);
-    if (g.dtype == PI_F16 ? (g.head_dim != 128 && g.head_dim != 256) : g.dtype != PI_F32)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill_paged: pool dtype %d head_dim %d (f16 at 128 / 256, or f32)",
-                    g.dtype, g.head_dim);
+    if (g.dtype != PI_F16 && g.dtype != PI_F32)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill_paged: pool dtype %d (f16 or f32)", g.dtype);
     if (gqa_mode == PI_GQA_GROUPED && n_q_heads % g.n_kv_heads != 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill_paged: grouped head map with n_q_heads %d not a multiple of n_kv_heads %d",
                     n_q_heads, g.n_kv_heads);
@@ -659,6 +658,16 @@ int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
     }
     int rc;
     if ((rc = ws_begin(h, s, "pi_attn_prefill_paged"))) return rc;
+    if (g.head_dim != 256) {  // straight from the f16 pages
+        const size_t need = pi::prefill_ws_floats(1, n_tok, n_q_heads, g.n_kv_heads, g.head_dim, 1);
+        if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "pi_attn_prefill_paged workspace", false)))
+            return rc;
+        PI_HIP(h, pi::launch_prefill_pool(g, d_q, 0, d_page_table, start_pos, n_tok, n_q_heads, gqa_mode,
+                                          scale, d_out, h->pfs_buf, h->pfs_floats, s),
+               "pi_attn_prefill_paged");
+        return ws_end(h, s, "pi_attn_prefill_paged");
+    }
+    // head dim 256: the pages gathered to contiguous f16 rows, then the contiguous prefill
     const size_t rows = (size_t)n_keys * g.n_kv_heads * g.head_dim;  // f16 elements of K (and of V)
     if ((rc = grow(h, &h->pf_buf, &h->pf_bytes, 4 * rows, s, "pi_attn_prefill_paged workspace", false))) return rc;
     char* gk = h->pf_buf;
@@ -1176,8 +1185,7 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     // The prologue (norm, RoPE, append at positions prev ..) takes its start position as a
     // scalar and writes the context lengths of the decode rows of the step (row i: prev + i +
     // 1 keys) into d_ctx, so no launch of its own fills them.
-    const bool rows = !((n > 1 && (D == 128 || D == 256) && L->kv_dtype == PI_F16) ||
-                        (n > 1 && L->kv_dtype == PI_F32));
+    const bool rows = !(n > 1 && (L->kv_dtype == PI_F16 || L->kv_dtype == PI_F32));
     {
         const pi::KvGeom& g = L->pool->g;
         const int rd = L->rope_dim <= 0 ? D : std::min(L->rope_dim, D);
@@ -1196,7 +1204,19 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     // the prefill kernels apply a 16-byte-aligned gate where they write the output; another
     // gate takes a launch of its own after them
     const float* dg_fused = dg && !((uintptr_t)dg & 15) ? dg : nullptr;
-    if (n > 1 && (D == 128 || D == 256) && L->kv_dtype == PI_F16) {
+    if (n > 1 && (D == 64 || D == 128) && L->kv_dtype == PI_F16) {
+        // causal flash attention over the sequence's pages (the chunk's own K / V appended by
+        // the prologue), q read in f32
+        if ((rc = ws_begin(h, s, "attention layer"))) return rc;
+        const size_t need = pi::prefill_ws_floats(1, n, L->n_heads, L->n_kv, D, 1);
+        if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "attention layer workspace", false)))
+            return rc;
+        PI_HIP(h, pi::launch_prefill_pool(L->pool->g, dq, 1, L->d_pt, prev, n, L->n_heads, L->gqa_mode,
+                                          scale, dout, h->pfs_buf, h->pfs_floats, s, dg_fused),
+               "attention layer");
+        if ((rc = ws_end(h, s, "attention layer"))) return rc;
+        if (dg && !dg_fused) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
+    } else if (n > 1 && D == 256 && L->kv_dtype == PI_F16) {
         // causal flash attention: f16 q rows, then K / V rows of positions 0 .. prev + n - 1
         const size_t kv_rows = (size_t)(prev + n) * L->n_kv * D;
         if ((rc = grow(h, &L->d_half, &L->half_bytes, 2 * nq + 4 * kv_rows, s, "attention layer staging", false)))

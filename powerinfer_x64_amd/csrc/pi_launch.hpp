@@ -160,6 +160,14 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
 // Causal attention of n_tok f32 query rows [n_tok][Hq][D] at positions q_off ..
 // q_off + n_tok - 1 over an f32 pool (D = 64 / 128 / 256), keys read through the
 // sequence's page-table row; products at f32 accuracy (bf16 hi + lo splits).
+// Causal prefill of n_tok query rows at positions q_off .. of one sequence, its keys 0 ..
+// q_off + n_tok - 1 read straight from the f16 pool's pages (head_dim 64 or 128) through
+// the sequence's page-table row; q [n_tok][n_q_heads][D] in f32 (q_f32) or f16.  ws: the
+// key-split partials (prefill_ws_floats(1, n_tok, ...)).
+hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, const int32_t* page_table,
+                               int32_t q_off, int32_t n_tok, int32_t n_q_heads, int32_t gqa_mode,
+                               float scale, float* out, float* ws, size_t ws_floats, hipStream_t s,
+                               const float* gate = nullptr);
 hipError_t launch_prefill_f32(const KvGeom& g, const float* q, const int32_t* page_table,
                               int32_t max_pages, int32_t q_off, int32_t n_tok, int32_t n_q_heads,
                               int32_t gqa_mode, float scale, float* out, hipStream_t s,

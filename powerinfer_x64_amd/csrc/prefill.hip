@@ -84,6 +84,15 @@ struct PrefillArgs {
     // optional output gate [B][S][Hq][D]: out *= 1 / (1 + exp(-gate)) (src/model/mod.rs:1192-1196),
     // applied where the normalised output is written (the epilogue, or the merge of key splits)
     const float* gate;
+    // Paged source (prefill_fa_kernel<., ., ., true>, one sequence): K / V out of the pool's
+    // page blocks through the page-table row pt (kpool / vpool + (page * hkv + kv head) *
+    // kstride / vstride bytes), and q in f32 when q_f32 (else in T).
+    const int32_t* pt;
+    const char* kpool;
+    const char* vpool;
+    size_t kstride, vstride;
+    int n_pages;
+    int q_f32;
 };
 
 __device__ __forceinline__ float gate_sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
@@ -133,10 +142,11 @@ __device__ __forceinline__ float max32(const f32x16& s, const f32x16& t) {
 // up to 512 registers each) and two unit buffers; each wavefront runs its MFMA
 // and softmax phases back to back.
 template <int D> struct PrefillCfg;
+template <> struct PrefillCfg<64> { static constexpr int NW = 8, NB = 4; };
 template <> struct PrefillCfg<128> { static constexpr int NW = 8, NB = 4; };
 template <> struct PrefillCfg<256> { static constexpr int NW = 4, NB = 2; };
 
-template <typename T, int HPW, int D>
+template <typename T, int HPW, int D, bool PG>
 __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(PrefillArgs a) {
     typedef typename Mfma<T>::v8 v8;
     typedef typename Mfma<T>::v4 v4;
@@ -148,14 +158,19 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     constexpr int NDT = D / 32;       // 32-dim tiles of O^T
     constexpr int KS = D + 8;         // K [key][dim] row stride (elements): 16 bytes of padding
     constexpr int KCH = KS / 8;       // 16-byte chunks per K row (17 or 33)
-    constexpr int K_INSTR = BN * KCH / 64;  // direct loads of 1 KB per K tile (17 or 33)
+    // direct loads of 1 KB per K tile: 17 or 33 padded rows; paged, D / 8 (one per 16-byte chunk)
+    constexpr int K_INSTR = PG ? D / 8 : BN * KCH / 64;
     constexpr int KJ = (K_INSTR + NW - 1) / NW;  // K loads per wavefront
     constexpr int V_INSTR = BN * D * 2 / 1024;  // direct loads of 1 KB per V tile (16 or 32)
     constexpr int VJ = V_INSTR / NW;  // V loads per wavefront
     constexpr int VRPI = 1024 / (2 * D);  // V rows per load (4 or 2)
     constexpr int VCPR = D / 8;       // 16-byte chunks per V row (16 or 32)
-    // buffer u % NB holds K of tile u ([key][dim], padded rows) and V of tile
-    // u - 1 ([key][dim], 2D-byte rows, chunk c of row r at c ^ 4*(r % 4))
+    // buffer u % NB holds K of tile u and V of tile u - 1.  Contiguous source: K [key][dim] with
+    // padded rows, V [key][dim] with 2D-byte rows, chunk c of row r at c ^ 4*(r % 4).  Paged
+    // source, page-major like the pool's blocks: K [4 pages][D/8][16 keys][8] with key pi(s)
+    // in slot s (pi swaps bits 2 and 3), V [4 pages][D][16 keys] with the 8-key halves of
+    // dim d's 32-byte row swapped when bit 2 ^ bit 3 of d is set (16 consecutive dims then
+    // cover every bank once).
     __shared__ __attribute__((aligned(1024))) T sk[NB][BN * KS];
     __shared__ __attribute__((aligned(1024))) T sv[NB][BN * D];
 
@@ -213,7 +228,19 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
 
     // Q^T operand: lane holds q[qpos][16*kk + 8*hh .. +7]
     v8 qr[D / 16];
-    {
+    if (PG && a.q_f32) {  // f32 query rows, rounded to T here (RNE)
+        const float* qg = reinterpret_cast<const float*>(a.q);
+        const bool ok = qpos < S;
+        const float* qrow = qg + (((size_t)b * S + (ok ? qpos : 0)) * a.hq + head) * D;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(qrow + 16 * kk + 8 * hh);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(qrow + 16 * kk + 8 * hh + 4);
+            v8 t = {(T)lo[0], (T)lo[1], (T)lo[2], (T)lo[3], (T)hi[0], (T)hi[1], (T)hi[2], (T)hi[3]};
+            if (!ok) t = v8{};
+            qr[kk] = t;
+        }
+    } else {
         const T* qg = reinterpret_cast<const T*>(a.q);
         const bool ok = qpos < S;
         const T* qrow = qg + (((size_t)b * S + (ok ? qpos : 0)) * a.hq + head) * D;
@@ -290,7 +317,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         v_row[j] = row;
         v_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * cc) * sizeof(T));
     }
-    auto issue_unit = [&](int u) {
+    auto issue_unit_c = [&](int u) {
         const int buf = u % NB;
         const int k0 = (tb + u) * BN;
         if (k0 + BN <= Sk) {
@@ -329,6 +356,113 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
             }
         }
     };
+    // Paged source.  The page ids of a tile's four 16-key pages (pages past the sequence's
+    // last key repeat its last page; the keys there are masked) are scalar loads: a vector
+    // load would share vmcnt with the direct loads in flight (its wait would drain them all).  A page id outside [0, n_pages) holds
+    // no tokens: page 0 is read in its place and its keys are masked (bit j of the unit's bad
+    // mask), as the decode does.  Load i of a unit moves 1 KB of one page, i / NDT: K chunks
+    // 4 (i % NDT) .. +3, V dims 32 (i % NDT) .. +31.  With i = wave + NW j and NW a multiple
+    // of NDT, a wave's loads keep one 1 KB slice (i % NDT) of pages wave / NDT + (NW / NDT) j:
+    // the base is one scalar per load and the lane offsets are fixed.
+    typedef int i32x4_ __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(4))) const int32_t* const_i32p;
+    typedef __attribute__((address_space(4))) const i32x4_* const_i32x4p;
+    const int last_pg = (Sk - 1) >> 4;
+    const int pj0 = wave / NDT, pq = wave % NDT;
+    // a page's blocks of all KV heads span under 4 GB (checked by the launcher)
+    const unsigned page_bytes_k = (unsigned)(a.hkv * a.kstride), page_bytes_v = (unsigned)(a.hkv * a.vstride);
+    const char* kq_pg = a.kpool + (size_t)kvh * a.kstride + 1024 * pq;
+    const char* vq_pg = a.vpool + (size_t)kvh * a.vstride + 1024 * pq;
+    // K: lane l is key slot l % 16 (holding key pi(l % 16), pi swapping bits 2 and 3) of
+    // chunk 4 (i % NDT) + l / 16.  V: lane l is the 8-key half (l % 2) ^ g(d) of dim
+    // d = 32 (i % NDT) + l / 2, g(d) = bit 2 ^ bit 3 of d.
+    const int ks_ = lane & 15;
+    const unsigned k_lo = (unsigned)((lane >> 4) * 256 + 16 * ((ks_ & 3) | ((ks_ & 4) << 1) | ((ks_ & 8) >> 1)));
+    const int vd_ = lane >> 1;
+    const unsigned v_lo = (unsigned)(vd_ * 32 + 16 * ((lane & 1) ^ (((vd_ >> 2) ^ (vd_ >> 3)) & 1)));
+    // Paged, 8 wavefronts: the lead wave w (0-3) issues the loads of waves w and w + 4 (its
+    // lag partner's share) after its softmax, when its lag partner runs its MFMA phase; the
+    // lag waves then issue none and their path through a step (softmax, MFMA phase) is free
+    // of load issue, which stalls on the direct-load path's latency.
+    constexpr int LPD = (PG && NW == 8) ? 2 : 1;  // load passes of a loading wave
+    const bool loader = wave < NW / LPD;
+    // this wave's page ids for the K tile of the unit issued last (the next unit's V tile)
+    unsigned koff_prev[LPD][KJ] = {};
+    auto load_ids = [&](int u) {
+        i32x4_ r = {};
+        if constexpr (PG) {
+            const int p0_ = (tb + u) * (BN >> 4);
+            if (p0_ + 3 <= last_pg) {
+                r = *(const_i32x4p)((const_i32p)a.pt + __builtin_amdgcn_readfirstlane(p0_));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    r[j] = ((const_i32p)a.pt)[__builtin_amdgcn_readfirstlane(min(p0_ + j, last_pg))];
+            }
+        }
+        return r;
+    };
+    // Whether every page id of this workgroup's tiles lies in the pool, checked once before
+    // any direct load (so its vector loads' wait drains nothing): then no unit needs a
+    // bad-page mask and only the loading waves read page ids.
+    bool ids_ok = true;
+    if constexpr (PG) {
+        const int pe = min((tb + nloc) * (BN >> 4), last_pg + 1);
+        bool bad_l = false;
+        for (int pp = tb * (BN >> 4) + lane; pp < pe; pp += 64)
+            bad_l |= (unsigned)a.pt[pp] >= (unsigned)a.n_pages;
+        ids_ok = !__any(bad_l);
+    }
+    // the loading waves read the next unit's ids at the start of an issue, so the scalar
+    // load's latency passes while this unit's direct loads issue
+    i32x4_ ids_next = loader ? load_ids(0) : i32x4_{};
+    unsigned bad_units = 0;   // 4 bits per unit buffer: the K tile's pages outside the pool
+    auto issue_unit_p = [&](int u) {
+        const int buf = u % NB;
+        i32x4_ r;
+        if (loader) {
+            r = ids_next;
+            ids_next = load_ids(u + 1);
+        } else {
+            if (ids_ok) return;
+            r = load_ids(u);
+        }
+        if (!ids_ok) {
+            unsigned bad = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bad |= (unsigned)((unsigned)r[j] >= (unsigned)a.n_pages) << j;
+            bad_units = (bad_units & ~(15u << (4 * buf))) | (bad << (4 * buf));
+        }
+        if (!loader) return;
+#pragma unroll
+        for (int ps = 0; ps < LPD; ++ps) {
+            const int wv = wave + ps * (NW / LPD);  // the wave whose share this is
+            unsigned koff[KJ];
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) {
+                const int pj = wv / NDT + (NW / NDT) * j;
+                const int x = pj == 0 ? r[0] : pj == 1 ? r[1] : pj == 2 ? r[2] : r[3];
+                koff[j] = (unsigned)x < (unsigned)a.n_pages ? (unsigned)x : 0u;
+                const int i = wv + NW * j;
+                if (i < K_INSTR)
+                    dma16s(kq_pg + (size_t)koff[j] * page_bytes_k, k_lo, (lds_void*)&sk[buf][512 * i]);
+            }
+            if (u >= 1) {
+#pragma unroll
+                for (int j = 0; j < KJ; ++j) {
+                    const int i = wv + NW * j;
+                    if (i < K_INSTR)
+                        dma16s(vq_pg + (size_t)koff_prev[ps][j] * page_bytes_v, v_lo, (lds_void*)&sv[buf][512 * i]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) koff_prev[ps][j] = koff[j];
+        }
+    };
+    auto issue_unit = [&](int u) {
+        if constexpr (PG) issue_unit_p(u);
+        else issue_unit_c(u);
+    };
     // barrier without the compiler's fence: LDS visibility is handled by the
     // explicit waits; the empty asm keeps memory accesses on their side
     auto barrier = [&]() {
@@ -341,9 +475,15 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     typedef __attribute__((address_space(3))) const T* lds_ptr;
     typedef __attribute__((address_space(3))) const v8* lds_v8;
     typedef __attribute__((address_space(3))) s4* lds_s4;
-    const lds_ptr k_lane = (lds_ptr)&sk[0][r * KS + 8 * hh];
+    // Paged source: the K operand's row r reads key r with bits 2 and 3 swapped (key slot
+    // r % 16 of page r / 16 holds it), so slot e of a lane's P^T operand (built from the S^T
+    // accumulator, rows 8 j + 4 hh + e % 4) is key 8 hh + e of its 16-key step: the V^T
+    // operand is then 8 consecutive keys of one dim, one 16-byte read of the page's V rows.
+    const lds_ptr k_lane = PG ? (lds_ptr)&sk[0][(r >> 4) * 16 * D + hh * 128 + (r & 15) * 8]
+                              : (lds_ptr)&sk[0][r * KS + 8 * hh];
     auto kfrag = [&](lds_ptr kt, int i) {  // i = 2*kk + tt
-        return *reinterpret_cast<lds_v8>(kt + (i & 1) * 32 * KS + (i >> 1) * 16);
+        if constexpr (PG) return *reinterpret_cast<lds_v8>(kt + (i & 1) * 32 * D + (i >> 1) * 256);
+        else return *reinterpret_cast<lds_v8>(kt + (i & 1) * 32 * KS + (i >> 1) * 16);
     };
     // V^T operand by two transposing reads: in each 16-lane group, lane j
     // points at key row kb + j/4, dims db + 4 (j % 4) .. +3; lane i then holds
@@ -355,13 +495,20 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
         voff[dt] = vrow * D + 32 * (dt ^ ((jg >> 2) & 3)) + 8 * vq + 4 * (jg & 1);
+    // paged: lane i of dim tile dt reads dim 32 dt + i, keys 16 ks + 8 hh .. +7 (page ks)
+    const int vdl = lane & 31;
+    const lds_ptr v_lane_pg = (lds_ptr)&sv[0][vdl * 16 + 8 * (hh ^ (((vdl >> 2) ^ (vdl >> 3)) & 1))];
     auto vfrag = [&](int buf, int i) {  // i = NDT*ks + dt: keys 16 ks + {4hh..+3, 8+4hh..+3}
         const int dt = i % NDT, ks = i / NDT;
-        const lds_ptr base = (lds_ptr)&sv[buf][0] + voff[dt] + (16 * ks) * D;
-        const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)base);
-        const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(base + 8 * D));
-        const v4 l4 = __builtin_bit_cast(v4, lo), h4 = __builtin_bit_cast(v4, hi);
-        return v8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+        if constexpr (PG) {
+            return *reinterpret_cast<lds_v8>(v_lane_pg + buf * (BN * D) + ks * 16 * D + dt * 512);
+        } else {
+            const lds_ptr base = (lds_ptr)&sv[buf][0] + voff[dt] + (16 * ks) * D;
+            const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)base);
+            const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(base + 8 * D));
+            const v4 l4 = __builtin_bit_cast(v4, lo), h4 = __builtin_bit_cast(v4, hi);
+            return v8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+        }
     };
     constexpr int PF = 4;
 
@@ -408,15 +555,18 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         }
         __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
     };
-    auto phase_softmax = [&](int t, bool masked) {
+    auto phase_softmax = [&](int t, bool masked, unsigned bad) {
         const int k0 = t * BN;
         if (masked) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const int key = k0 + 32 * tt + 8 * (e >> 2) + 4 * hh + (e & 3);
-                    if (key >= Sk || (a.causal && key > q_off + qpos)) s[tt][e] = -INFINITY;
+                    const int kr = PG ? 16 * (e >> 3) + 8 * hh + 4 * ((e >> 2) & 1) + (e & 3)
+                                      : 8 * (e >> 2) + 4 * hh + (e & 3);
+                    const int key = k0 + 32 * tt + kr;
+                    if (key >= Sk || (a.causal && key > q_off + qpos) || ((bad >> ((32 * tt + kr) >> 4)) & 1))
+                        s[tt][e] = -INFINITY;
                 }
         }
         // exps against the current running max; their sum also tells whether a score
@@ -467,21 +617,29 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         __builtin_amdgcn_s_setprio(0);
     };
     if constexpr (NW == 8) {
-        const int nl = (wave == 0 ? 3 : 2) + 2;  // this wave's loads per unit (K + V)
+        // this wave's loads per unit (K + V): 5 for wave 0 and 4 for the others with the
+        // padded contiguous K tile (17 loads); from the pool D / 16 for a lead wave and none
+        // for a lag wave
+        constexpr int NLP = LPD * ((K_INSTR / NW) + VJ);
+        const int nl = PG ? NLP : (wave == 0 ? 3 : 2) + 2;
         // Wait until this wave's loads of unit u are complete while its loads of
         // the next `ahead` units (0, 1 or 2) may still be in flight.
         // vmcnt(n) on gfx9: bits 3:0 and 15:14; expcnt 6:4 = 7; lgkmcnt 11:8 = 15
+#define PI_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
         auto wait_unit = [&](int ahead) {
             if (ahead == 2) {
-                if (nl == 5) __builtin_amdgcn_s_waitcnt(0x0F7A);
-                else __builtin_amdgcn_s_waitcnt(0x0F78);
+                if (PG) PI_VMCNT(2 * NLP);
+                else if (nl == 5) PI_VMCNT(10);
+                else PI_VMCNT(8);
             } else if (ahead == 1) {
-                if (nl == 5) __builtin_amdgcn_s_waitcnt(0x0F75);
-                else __builtin_amdgcn_s_waitcnt(0x0F74);
+                if (PG) PI_VMCNT(NLP);
+                else if (nl == 5) PI_VMCNT(5);
+                else PI_VMCNT(4);
             } else {
-                __builtin_amdgcn_s_waitcnt(0x0F70);
+                PI_VMCNT(0);
             }
         };
+#undef PI_VMCNT
         auto ahead_of = [&](int u) { return min(2, max(0, nloc - u)); };
         // One barrier per tile step t = 0 .. n_tiles.  Lead waves (0-3): the
         // MFMA phase of tile t, then the softmax of tile t; lag waves (4-7): the
@@ -494,7 +652,10 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         if (wave < NW / 2) {
             for (int t = 0; t <= nloc; ++t) {
                 mfma_phase(t);
-                if (t < nloc && tb + t < w_tiles) phase_softmax(tb + t, tb + t >= t_mask);
+                if (t < nloc && tb + t < w_tiles) {
+                    const unsigned bd = (bad_units >> (4 * (t % NB))) & 15;
+                    phase_softmax(tb + t, tb + t >= t_mask || bd, bd);
+                }
                 if (t + 3 <= nloc) issue_unit(t + 3);
                 if (t < nloc) {
                     wait_unit(ahead_of(t + 1));
@@ -503,7 +664,10 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
             }
         } else {
             for (int t = 0; t <= nloc; ++t) {
-                if (t >= 1 && tb + t - 1 < w_tiles) phase_softmax(tb + t - 1, tb + t - 1 >= t_mask);
+                if (t >= 1 && tb + t - 1 < w_tiles) {
+                    const unsigned bd = (bad_units >> (4 * ((t - 1) % NB))) & 15;
+                    phase_softmax(tb + t - 1, tb + t - 1 >= t_mask || bd, bd);
+                }
                 if (t + 3 <= nloc) issue_unit(t + 3);
                 mfma_phase(t);
                 if (t < nloc) {
@@ -520,7 +684,10 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
         for (int t = 0; t <= nloc; ++t) {
             if (t >= 1 && t + 1 <= nloc) issue_unit(t + 1);
             mfma_phase(t);
-            if (t < nloc && tb + t < w_tiles) phase_softmax(tb + t, tb + t >= t_mask);
+            if (t < nloc && tb + t < w_tiles) {
+                const unsigned bd = (bad_units >> (4 * (t % NB))) & 15;
+                phase_softmax(tb + t, tb + t >= t_mask || bd, bd);
+            }
             if (t < nloc) {
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
                 barrier();
@@ -1250,16 +1417,16 @@ void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int ba
     }
     switch (hpw) {
         case 4:
-            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 4, D>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 4, D>), grid, block, 0, s, a);
+            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 4, D, false>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 4, D, false>), grid, block, 0, s, a);
             break;
         case 2:
-            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 2, D>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 2, D>), grid, block, 0, s, a);
+            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 2, D, false>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 2, D, false>), grid, block, 0, s, a);
             break;
         default:
-            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 1, D>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 1, D>), grid, block, 0, s, a);
+            if (bf) hipLaunchKernelGGL((prefill_fa_kernel<bf16, 1, D, false>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((prefill_fa_kernel<f16, 1, D, false>), grid, block, 0, s, a);
     }
 }
 }  // namespace
@@ -1327,7 +1494,7 @@ PrefillSched prefill_sched(int batch, int seq_len, int n_q_heads, int n_kv_heads
     const bool multiple = n_q_heads % n_kv_heads == 0;
     const int group = (n_q_heads + n_kv_heads - 1) / n_kv_heads;
     sc.hpw = !multiple ? 1 : group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
-    const int nw = head_dim == 128 ? PrefillCfg<128>::NW : PrefillCfg<256>::NW;
+    const int nw = head_dim == 256 ? PrefillCfg<256>::NW : PrefillCfg<128>::NW;
     const int rows = ROWS * nw / sc.hpw;
     const long long wgs = (long long)n_kv_heads * (group / sc.hpw) * batch * ((seq_len + rows - 1) / rows);
     const long long pairs = (long long)n_kv_heads * (group / sc.hpw) * batch *
@@ -1398,6 +1565,71 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
                            (long long)rows, a.ksplit, gate);
     else
         hipLaunchKernelGGL(prefill_merge_kernel<256>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out,
+                           (long long)rows, a.ksplit, gate);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, const int32_t* page_table,
+                               int32_t q_off, int32_t n_tok, int32_t n_q_heads, int32_t gqa_mode,
+                               float scale, float* out, float* ws, size_t ws_floats, hipStream_t s,
+                               const float* gate) {
+    const int D = g.head_dim;
+    if (g.dtype != 1 || (D != 64 && D != 128) || q_off < 0 || n_tok < 1) return hipErrorInvalidValue;
+    if ((uint64_t)g.n_kv_heads * std::max(g.kstride, g.vstride) >= (1ull << 32)) return hipErrorInvalidValue;
+    const bool multiple = n_q_heads % g.n_kv_heads == 0;
+    if (!multiple && gqa_mode != 0) return hipErrorInvalidValue;
+    PrefillArgs a;
+    a.q = q;
+    a.k = a.v = nullptr;
+    a.out = out;
+    a.S = n_tok;
+    a.Sk = q_off + n_tok;
+    a.q_off = q_off;
+    a.hq = n_q_heads;
+    a.hkv = g.n_kv_heads;
+    a.group = (n_q_heads + g.n_kv_heads - 1) / g.n_kv_heads;
+    a.causal = 1;
+    a.gqa_mode = gqa_mode;
+    a.qk_scale = scale * kLog2e;
+    a.gate = gate;
+    a.pt = page_table;
+    a.kpool = static_cast<const char*>(g.k);
+    a.vpool = static_cast<const char*>(g.v);
+    a.kstride = g.kstride;
+    a.vstride = g.vstride;
+    a.n_pages = g.n_pages;
+    a.q_f32 = q_f32;
+    const PrefillSched sc = prefill_sched(1, n_tok, n_q_heads, g.n_kv_heads, D, 1);
+    a.paired = sc.paired;
+    a.ksplit = 1;
+    a.part_o = a.part_ml = nullptr;
+    const size_t rows = (size_t)n_tok * n_q_heads;
+    if (sc.ksplit > 1 && ws && ws_floats >= (size_t)sc.ksplit * rows * (D + 2)) {
+        a.ksplit = sc.ksplit;
+        a.part_o = ws;
+        a.part_ml = ws + (size_t)sc.ksplit * rows * D;
+    }
+    constexpr int NW = PrefillCfg<128>::NW;
+    const int wrows = ROWS * NW / sc.hpw;
+    const int nqb = (n_tok + wrows - 1) / wrows;
+    const dim3 grid(g.n_kv_heads * (a.group / sc.hpw), a.paired ? (nqb + 1) / 2 : nqb, a.ksplit);
+    const dim3 block(64 * NW);
+#define PI_PAGED(DD)                                                                                 \
+    switch (sc.hpw) {                                                                                \
+        case 4: hipLaunchKernelGGL((prefill_fa_kernel<f16, 4, DD, true>), grid, block, 0, s, a); break; \
+        case 2: hipLaunchKernelGGL((prefill_fa_kernel<f16, 2, DD, true>), grid, block, 0, s, a); break; \
+        default: hipLaunchKernelGGL((prefill_fa_kernel<f16, 1, DD, true>), grid, block, 0, s, a);      \
+    }
+    if (D == 128) { PI_PAGED(128) } else { PI_PAGED(64) }
+#undef PI_PAGED
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.ksplit == 1) return e;
+    const dim3 mgrid((unsigned)((rows + 3) / 4));
+    if (D == 128)
+        hipLaunchKernelGGL(prefill_merge_kernel<128>, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, out,
+                           (long long)rows, a.ksplit, gate);
+    else
+        hipLaunchKernelGGL(prefill_merge_kernel<64>, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, out,
                            (long long)rows, a.ksplit, gate);
     return hipGetLastError();
 }

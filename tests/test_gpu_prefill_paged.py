@@ -167,7 +167,8 @@ def test_paged_prefill_c4_shape_d256(gqa_mode):
 
 
 def test_paged_prefill_start_zero_equals_contiguous_prefill():
-    """start_pos 0: the same f16 rows as pi_attn_prefill's, so the outputs agree bit for bit."""
+    """start_pos 0: the same f16 rows as pi_attn_prefill's.  The paged kernel takes a key step's
+    16 keys in another slot order inside its MFMAs, so the two agree to f32 rounding."""
     from powerinfer_x64_amd import runtime as rt
     dev = device()
     c = Chunk(np.random.default_rng(5), 0, 333, 32, 8, 128)
@@ -177,7 +178,8 @@ def test_paged_prefill_start_zero_equals_contiguous_prefill():
     ref = rt.attn_prefill(dev, c.q16[None], k16.half()[None].contiguous(),
                           torch.from_numpy(c.v).cuda().half()[None].contiguous())
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(out, ref[0].cpu().numpy())
+    ref = ref[0].cpu().numpy()
+    assert row_rel_err(out, ref) <= 1e-5
 
 
 def test_paged_prefill_1024_over_8k_history():
@@ -202,8 +204,63 @@ def test_paged_prefill_rejects_bad_shapes():
     with pytest.raises(rt.InvalidArg):  # an f32 pool takes f32 queries
         rt.attn_prefill_paged(dev, q, pool32, row, 0)
     pool64 = rt.KvPool(dev, 8, 2, 64, dtype=torch.float16)
-    with pytest.raises(rt.Unsupported):  # the f16 flash prefill runs D 128 / 256
-        rt.attn_prefill_paged(dev, q[:, :, :64].contiguous(), pool64, row, 0)
+    with pytest.raises(rt.InvalidArg):  # q rows must match the pool's head_dim
+        rt.attn_prefill_paged(dev, q, pool64, row, 0)
+
+
+@pytest.mark.parametrize("prev,n,hq,hkv", [(0, 200, 8, 8), (300, 129, 16, 4), (1000, 1, 4, 2),
+                                           (17, 64, 12, 4)])
+def test_paged_prefill_f16_head_dim_64(prev, n, hq, hkv):
+    """An f16 pool at head dim 64 (the flash prefill straight from the pages): a fresh prompt,
+    continued chunks at tile and non-tile offsets, a single row, modulo heads."""
+    dev = device()
+    c = Chunk(np.random.default_rng(prev * 13 + n + 64), prev, n, hq, hkv, 64)
+    out = c.gpu(dev)
+    _check(out, c.oracle(range(n)), f"D 64 prev {prev} + {n}")
+
+
+def test_paged_prefill_page_ids_outside_the_pool_hold_no_tokens():
+    """Page-table entries outside [0, n_pages) hold no tokens, as for the decode: their keys
+    are masked (a row whose every key is masked gets zeros).  Two pages of the history, one
+    inside a tile and one at a tile's start, are made invalid; the oracle drops their keys."""
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    c = Chunk(np.random.default_rng(0xBAD), 200, 100, 8, 2, 128)
+    c.gpu(dev)  # pool filled through the real row
+    bad = [2, 4]  # pages 2 (keys 32..47) and 4 (keys 64..79)
+    row = c.row.copy()
+    row[2], row[4] = -1, c.n_pages + 3
+    out = rt.attn_prefill_paged(dev, c.q16, c.pool, to_dev(row), c.prev)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    q, k, v = c.prepared()
+    keep = np.ones(c.prev + c.n, bool)
+    for pg in bad:
+        keep[16 * pg:16 * pg + 16] = False
+
+    def ref_row(i):
+        m = keep[:c.prev + i + 1]
+        return orc.attn_decode(q[i], k[:c.prev + i + 1][m], v[:c.prev + i + 1][m])
+    _check(out, np.stack(parallel_map(ref_row, range(c.n))), "pages outside the pool")
+
+
+@pytest.mark.parametrize("paired,ksplit", [("1", None), (None, "2"), (None, "3"), (None, "4")])
+@pytest.mark.parametrize("prev,n,hq,hkv,d", [(700, 150, 32, 8, 128), (1000, 129, 16, 2, 256),
+                                             (300, 129, 16, 4, 64)])
+def test_paged_prefill_forced_schedules(monkeypatch, paired, ksplit, prev, n, hq, hkv, d):
+    """The paired schedule and key splits 2-4 forced on continued chunks (start_pos > 0, so the
+    last two tiles of a wavefront take the mask), for the paged kernel at D 64 / 128 and the
+    gathered D 256 one, against the oracle."""
+    if paired:
+        monkeypatch.setenv("PI_PREFILL_PAIRED", paired)
+    else:
+        monkeypatch.setenv("PI_PREFILL_PAIRED", "0")
+        monkeypatch.setenv("PI_PREFILL_KSPLIT", ksplit)
+    dev = device()
+    c = Chunk(np.random.default_rng(prev + n + d + (int(ksplit) if ksplit else 9)), prev, n, hq, hkv, d,
+              theta=1e6)
+    out = c.gpu(dev)
+    _check(out, c.oracle(range(n)), f"forced paired={paired} ksplit={ksplit} D {d}")
 
 
 def test_layer_forward_dev_equals_host_slices():
