@@ -946,6 +946,10 @@ def bench_chunk(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
                 lay.forward_dev(hq_[:prefix].clone(), hk_[:prefix].clone(), hv_[:prefix])
             q, k = cq.clone(), ck.clone()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            # ~50 us of GPU spin ahead of the start event: the host has enqueued the step's
+            # launches before the GPU reaches it, as when layers run back to back, so the
+            # figure is the step's device time, not the host's launch latency
+            torch.cuda._sleep(100_000)
             a.record()
             lay.forward_dev(q, k, cv, gate=cg, out=out)
             b.record()

@@ -28,8 +28,6 @@ struct pi_handle_s {
     size_t h2d_floats = 0;
     float* tq_qv = nullptr;        // TurboQuant virtual queries [batch][Hq][256]
     size_t tq_qv_floats = 0;
-    char* pf_buf = nullptr;        // paged prefill: the sequence's K / V gathered to f16 rows
-    size_t pf_bytes = 0;
     float* pfs_buf = nullptr;      // prefill key-split partials
     size_t pfs_floats = 0;
     float* pin = nullptr;          // pinned host staging of the small host-slice layer calls
@@ -63,8 +61,6 @@ struct pi_attn_layer_s {
     int32_t* d_ctx = nullptr;       // the start position, then per-row context lengths (kLayerRows + 1)
     float* d_buf = nullptr;         // host-slice staging: q, gate, out, k, v (f32)
     size_t buf_floats = 0;
-    char* d_half = nullptr;         // f16 q, then f16 K / V rows for the flash prefill
-    size_t half_bytes = 0;
     int32_t seq_len = 0;
 };
 
@@ -288,7 +284,6 @@ void pi_destroy(pi_handle h) {
     (void)hipFree(h->gws.buf);
     (void)hipFree(h->h2d_scratch);
     (void)hipFree(h->tq_qv);
-    (void)hipFree(h->pf_buf);
     (void)hipFree(h->pfs_buf);
     if (h->pin) (void)hipHostFree(h->pin);
     if (h->ws_event) (void)hipEventDestroy(h->ws_event);
@@ -658,27 +653,12 @@ int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
     }
     int rc;
     if ((rc = ws_begin(h, s, "pi_attn_prefill_paged"))) return rc;
-    if (g.head_dim != 256) {  // straight from the f16 pages
-        const size_t need = pi::prefill_ws_floats(1, n_tok, n_q_heads, g.n_kv_heads, g.head_dim, 1);
-        if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "pi_attn_prefill_paged workspace", false)))
-            return rc;
-        PI_HIP(h, pi::launch_prefill_pool(g, d_q, 0, d_page_table, start_pos, n_tok, n_q_heads, gqa_mode,
-                                          scale, d_out, h->pfs_buf, h->pfs_floats, s),
-               "pi_attn_prefill_paged");
-        return ws_end(h, s, "pi_attn_prefill_paged");
-    }
-    // head dim 256: the pages gathered to contiguous f16 rows, then the contiguous prefill
-    const size_t rows = (size_t)n_keys * g.n_kv_heads * g.head_dim;  // f16 elements of K (and of V)
-    if ((rc = grow(h, &h->pf_buf, &h->pf_bytes, 4 * rows, s, "pi_attn_prefill_paged workspace", false))) return rc;
-    char* gk = h->pf_buf;
-    char* gv = h->pf_buf + 2 * rows;
-    PI_HIP(h, pi::launch_kv_gather(g, d_page_table, (int32_t)n_keys, gk, gv, s), "pi_attn_prefill_paged");
+    // straight from the f16 pages
     const size_t need = pi::prefill_ws_floats(1, n_tok, n_q_heads, g.n_kv_heads, g.head_dim, 1);
     if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "pi_attn_prefill_paged workspace", false)))
         return rc;
-    PI_HIP(h, pi::launch_prefill(d_q, gk, gv, PI_F16, 1, n_tok, (int32_t)n_keys, start_pos, n_q_heads,
-                                 g.n_kv_heads, g.head_dim, 1, gqa_mode, scale, d_out, h->pfs_buf,
-                                 h->pfs_floats, s),
+    PI_HIP(h, pi::launch_prefill_pool(g, d_q, 0, d_page_table, start_pos, n_tok, n_q_heads, gqa_mode,
+                                      scale, d_out, h->pfs_buf, h->pfs_floats, s),
            "pi_attn_prefill_paged");
     return ws_end(h, s, "pi_attn_prefill_paged");
 }
@@ -1152,7 +1132,6 @@ void pi_attn_layer_destroy(pi_attn_layer L) {
     (void)hipFree(L->d_qn);
     (void)hipFree(L->d_kn);
     (void)hipFree(L->d_buf);
-    (void)hipFree(L->d_half);
     delete L;
 }
 
@@ -1204,7 +1183,7 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     // the prefill kernels apply a 16-byte-aligned gate where they write the output; another
     // gate takes a launch of its own after them
     const float* dg_fused = dg && !((uintptr_t)dg & 15) ? dg : nullptr;
-    if (n > 1 && (D == 64 || D == 128) && L->kv_dtype == PI_F16) {
+    if (n > 1 && L->kv_dtype == PI_F16) {
         // causal flash attention over the sequence's pages (the chunk's own K / V appended by
         // the prologue), q read in f32
         if ((rc = ws_begin(h, s, "attention layer"))) return rc;
@@ -1213,31 +1192,6 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
             return rc;
         PI_HIP(h, pi::launch_prefill_pool(L->pool->g, dq, 1, L->d_pt, prev, n, L->n_heads, L->gqa_mode,
                                           scale, dout, h->pfs_buf, h->pfs_floats, s, dg_fused),
-               "attention layer");
-        if ((rc = ws_end(h, s, "attention layer"))) return rc;
-        if (dg && !dg_fused) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");
-    } else if (n > 1 && D == 256 && L->kv_dtype == PI_F16) {
-        // causal flash attention: f16 q rows, then K / V rows of positions 0 .. prev + n - 1
-        const size_t kv_rows = (size_t)(prev + n) * L->n_kv * D;
-        if ((rc = grow(h, &L->d_half, &L->half_bytes, 2 * nq + 4 * kv_rows, s, "attention layer staging", false)))
-            return rc;
-        char* hq16 = L->d_half;
-        char* hk16 = hq16 + 2 * nq;
-        char* hv16 = hk16 + 2 * kv_rows;
-        PI_HIP(h, pi::launch_to_half(dq, hq16, nq, s), "attention layer");
-        if (prev == 0) {  // a fresh prompt: its own rotated rows (the pool holds the same f16 values)
-            PI_HIP(h, pi::launch_to_half(dk, hk16, kv_rows, s), "attention layer");
-            PI_HIP(h, pi::launch_to_half(dv, hv16, kv_rows, s), "attention layer");
-        } else {          // a continued chunk: the whole sequence out of its pages
-            PI_HIP(h, pi::launch_kv_gather(L->pool->g, L->d_pt, prev + n, hk16, hv16, s), "attention layer");
-        }
-        if ((rc = ws_begin(h, s, "attention layer"))) return rc;
-        const size_t need = pi::prefill_ws_floats(1, n, L->n_heads, L->n_kv, D, 1);
-        if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "attention layer workspace", false)))
-            return rc;
-        PI_HIP(h, pi::launch_prefill(hq16, hk16, hv16, PI_F16, 1, n, prev + n, prev, L->n_heads, L->n_kv,
-                                     D, 1, L->gqa_mode, scale, dout, h->pfs_buf, h->pfs_floats, s,
-                                     dg_fused),
                "attention layer");
         if ((rc = ws_end(h, s, "attention layer"))) return rc;
         if (dg && !dg_fused) PI_HIP(h, pi::launch_apply_gate(dout, dg, nq, s), "attention layer");

@@ -132,7 +132,6 @@ hipError_t launch_rope(float* q, float* k, const int32_t* pos, int32_t n_tok, in
 hipError_t launch_head_rmsnorm(float* x, const float* w, int32_t n_rows, int32_t dim,
                                int32_t row_stride, float eps, hipStream_t s);
 hipError_t launch_softmax(float* x, int32_t n, hipStream_t s);
-hipError_t launch_to_half(const float* x, void* y, size_t n, hipStream_t s);
 hipError_t launch_apply_gate(float* out, const float* gate, size_t n, hipStream_t s);
 hipError_t launch_fill_iota(int32_t* dst, int32_t n, int32_t first, hipStream_t s);
 hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t s);
@@ -161,7 +160,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
 // q_off + n_tok - 1 over an f32 pool (D = 64 / 128 / 256), keys read through the
 // sequence's page-table row; products at f32 accuracy (bf16 hi + lo splits).
 // Causal prefill of n_tok query rows at positions q_off .. of one sequence, its keys 0 ..
-// q_off + n_tok - 1 read straight from the f16 pool's pages (head_dim 64 or 128) through
+// q_off + n_tok - 1 read straight from the f16 pool's pages (head_dim 64, 128 or 256) through
 // the sequence's page-table row; q [n_tok][n_q_heads][D] in f32 (q_f32) or f16.  ws: the
 // key-split partials (prefill_ws_floats(1, n_tok, ...)).
 hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, const int32_t* page_table,
@@ -172,10 +171,6 @@ hipError_t launch_prefill_f32(const KvGeom& g, const float* q, const int32_t* pa
                               int32_t max_pages, int32_t q_off, int32_t n_tok, int32_t n_q_heads,
                               int32_t gqa_mode, float scale, float* out, hipStream_t s,
                               const float* gate = nullptr);
-// The f16 pool's K and V of positions 0 .. n_tok-1 of one sequence (page-table
-// row `page_table`) gathered into contiguous f16 [n_tok][Hkv][D] rows.
-hipError_t launch_kv_gather(const KvGeom& g, const int32_t* page_table, int32_t n_tok,
-                            void* k_out, void* v_out, hipStream_t s);
 
 hipError_t launch_gdn_gates(const float* beta_raw, const float* a_raw, const float* ssm_a,
                             const float* dt_bias, float* beta, float* g, int32_t n_tok,

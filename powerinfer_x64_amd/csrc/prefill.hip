@@ -77,8 +77,11 @@ struct PrefillArgs {
     int paired;
     // key split (a launch with fewer workgroups than CUs): blockIdx.z = batch * ksplit +
     // split; split k of a workgroup's n key tiles takes tiles [k p, (k+1) p), p = ceil(n /
-    // ksplit), and leaves its unnormalised O and (max, sum) for prefill_merge_kernel
+    // ksplit), and leaves its unnormalised O and (max, sum) for prefill_merge_kernel.  A
+    // query block of at most kthr tiles is not split: split 0 takes all its tiles and
+    // writes the output, the other splits skip it.
     int ksplit;
+    int kthr;
     float* part_o;   // [ksplit][B][S][Hq][D]
     float* part_ml;  // [ksplit][B][S][Hq][2]
     // optional output gate [B][S][Hq][D]: out *= 1 / (1 + exp(-gate)) (src/model/mod.rs:1192-1196),
@@ -212,7 +215,9 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
     const int n_tiles = (wg_keys + BN - 1) / BN;
     // this workgroup's key tiles: [tb, tb + nloc); step t below works on tile tb + t
-    const int kper = (n_tiles + a.ksplit - 1) / a.ksplit;
+    const bool split = a.ksplit > 1 && n_tiles > a.kthr;
+    if (!split && ksp > 0) continue;  // split 0 runs the whole block (uniform per workgroup)
+    const int kper = split ? (n_tiles + a.ksplit - 1) / a.ksplit : n_tiles;
     const int tb = min(n_tiles, ksp * kper);
     const int nloc = min(n_tiles, tb + kper) - tb;
     const int w_keys = a.causal ? min(Sk, q_off + p0 + ROWS) : Sk;
@@ -696,7 +701,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     }
 
     l_run = wave_sum_xor(l_run, 32);
-    if (a.ksplit > 1) {  // unnormalised partial of this key split
+    if (split) {  // unnormalised partial of this key split
         if (qpos < S) {
             const size_t row = (((size_t)ksp * (gridDim.z / a.ksplit) + b) * S + qpos) * a.hq + head;
             float* po = a.part_o + row * D;
@@ -777,7 +782,7 @@ __device__ __forceinline__ float max16(const f32x4* s) {
     return vmax3(vmax3(a, b, c), vmax3(d, e, s[3][3]), a);
 }
 
-template <typename T, int HPW>
+template <typename T, int HPW, bool PG>
 __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
     typedef typename Mfma<T>::v8 v8;
     typedef short s4 __attribute__((ext_vector_type(4)));
@@ -829,7 +834,9 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
     const int p0 = qb * WROWS + rt * R;
     const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
     const int n_tiles = (wg_keys + BN - 1) / BN;
-    const int kper = (n_tiles + a.ksplit - 1) / a.ksplit;
+    const bool split = a.ksplit > 1 && n_tiles > a.kthr;
+    if (!split && ksp > 0) continue;  // split 0 runs the whole block (uniform per workgroup)
+    const int kper = split ? (n_tiles + a.ksplit - 1) / a.ksplit : n_tiles;
     const int tb = min(n_tiles, ksp * kper);
     const int nloc = min(n_tiles, tb + kper) - tb;
     const int w_keys = a.causal ? min(Sk, q_off + p0 + R) : Sk;
@@ -842,7 +849,19 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
 
     // Q^T operand: lane holds q[qpos][32 ks + 8 g .. +7]
     v8 qr[D / 32];
-    {
+    if (PG && a.q_f32) {  // f32 query rows, rounded to T here (RNE)
+        const float* qg = reinterpret_cast<const float*>(a.q);
+        const bool ok = qpos < S;
+        const float* qrow = qg + (((size_t)b * S + (ok ? qpos : 0)) * a.hq + head) * D;
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(qrow + 32 * ks + 8 * g);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(qrow + 32 * ks + 8 * g + 4);
+            v8 t = {(T)lo[0], (T)lo[1], (T)lo[2], (T)lo[3], (T)hi[0], (T)hi[1], (T)hi[2], (T)hi[3]};
+            if (!ok) t = v8{};
+            qr[ks] = t;
+        }
+    } else {
         const T* qg = reinterpret_cast<const T*>(a.q);
         const bool ok = qpos < S;
         const T* qrow = qg + (((size_t)b * S + (ok ? qpos : 0)) * a.hq + head) * D;
@@ -902,7 +921,7 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
         v_row[j] = row;
         v_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * cc) * sizeof(T));
     }
-    auto issue_unit = [&](int u) {
+    auto issue_unit_c = [&](int u) {
         const int buf = u % NB;
         const int k0 = (tb + u) * BN;
         if (k0 + BN <= Sk) {
@@ -941,6 +960,78 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
             }
         }
     };
+    // Paged source, page-major unit buffers as in prefill_fa_kernel: K [4 pages][32 chunks]
+    // [16 key slots][8] with key k of an odd page in slot k ^ 4, V [4 pages][256 dims][16
+    // keys] with dim d's 8-key halves swapped when bit 2 ^ bit 3 of d is set.  Load i moves
+    // 1 KB of page i / 8: K chunks 4 (i % 8) .. +3, V dims 32 (i % 8) .. +31; wave w issues
+    // slice w of every page (i = w + 8 j, page j).  Page ids as in prefill_fa_kernel: scalar
+    // loads, the next unit's read at the start of an issue; a page id outside the pool holds
+    // no tokens (page 0 read, keys masked).
+    typedef int i32x4_ __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(4))) const int32_t* const_i32p;
+    typedef __attribute__((address_space(4))) const i32x4_* const_i32x4p;
+    const int last_pg = (Sk - 1) >> 4;
+    const unsigned page_bytes_k = (unsigned)(a.hkv * a.kstride), page_bytes_v = (unsigned)(a.hkv * a.vstride);
+    const char* kq_pg = a.kpool + (size_t)kvh * a.kstride + 1024 * wave;
+    const char* vq_pg = a.vpool + (size_t)kvh * a.vstride + 1024 * wave;
+    const int ks_ = lane & 15, vd_ = lane >> 1;
+    const unsigned k_lo0 = (unsigned)((lane >> 4) * 256 + 16 * ks_);
+    const unsigned k_lo1 = (unsigned)((lane >> 4) * 256 + 16 * (ks_ ^ 4));
+    const unsigned v_lo = (unsigned)(vd_ * 32 + 16 * ((lane & 1) ^ (((vd_ >> 2) ^ (vd_ >> 3)) & 1)));
+    unsigned koff_prev[4] = {};
+    auto load_ids = [&](int u) {
+        i32x4_ r = {};
+        if constexpr (PG) {
+            const int p0_ = (tb + u) * (BN >> 4);
+            if (p0_ + 3 <= last_pg) {
+                r = *(const_i32x4p)((const_i32p)a.pt + __builtin_amdgcn_readfirstlane(p0_));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    r[j] = ((const_i32p)a.pt)[__builtin_amdgcn_readfirstlane(min(p0_ + j, last_pg))];
+            }
+        }
+        return r;
+    };
+    bool ids_ok = true;  // every page id of the workgroup's tiles in the pool (checked once)
+    if constexpr (PG) {
+        const int pe = min((tb + nloc) * (BN >> 4), last_pg + 1);
+        bool bad_l = false;
+        for (int pp = tb * (BN >> 4) + lane; pp < pe; pp += 64)
+            bad_l |= (unsigned)a.pt[pp] >= (unsigned)a.n_pages;
+        ids_ok = !__any(bad_l);
+    }
+    i32x4_ ids_next = load_ids(0);
+    unsigned bad_units = 0;  // 4 bits per unit buffer: the K tile's pages outside the pool
+    auto issue_unit_p = [&](int u) {
+        const int buf = u % NB;
+        const i32x4_ r = ids_next;
+        ids_next = load_ids(u + 1);
+        if (!ids_ok) {
+            unsigned bad = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bad |= (unsigned)((unsigned)r[j] >= (unsigned)a.n_pages) << j;
+            bad_units = (bad_units & ~(15u << (4 * buf))) | (bad << (4 * buf));
+        }
+        unsigned koff[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            koff[j] = (unsigned)r[j] < (unsigned)a.n_pages ? (unsigned)r[j] : 0u;
+            dma16s(kq_pg + (size_t)koff[j] * page_bytes_k, (j & 1) ? k_lo1 : k_lo0,
+                   (lds_void*)&sk[buf][512 * (wave + NW * j)]);
+        }
+        if (u >= 1) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                dma16s(vq_pg + (size_t)koff_prev[j] * page_bytes_v, v_lo, (lds_void*)&sv[buf][512 * (wave + NW * j)]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) koff_prev[j] = koff[j];
+    };
+    auto issue_unit = [&](int u) {
+        if constexpr (PG) issue_unit_p(u);
+        else issue_unit_c(u);
+    };
     auto barrier = [&]() {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -951,11 +1042,26 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
     typedef __attribute__((address_space(3))) const T* lds_ptr;
     typedef __attribute__((address_space(3))) const v8* lds_v8;
     typedef __attribute__((address_space(3))) s4* lds_s4;
+    // Paged: row rho of key block kb reads key 32 (kb / 2) + 8 (rho / 4) + 4 (kb % 2) +
+    // rho % 4, so that the P^T slots 8 g .. 8 g + 7 of key step j (accumulator rows 4 g + r
+    // of blocks 2 j, 2 j + 1) are the 8 consecutive keys 32 j + 8 g .. +7: the V^T operand
+    // is one 16-byte read of a page's dim row.  Lane offsets (elements) for kb % 2 = 0, 1:
+    const int kpar = ln >> 3;  // page parity of this lane's K rows
+    const int kpg_base = kpar * 4096 + g * 128 + (8 * ((ln >> 2) & 1) + (ln & 3)) * 8;
+    const lds_ptr k_lane_p0 = (lds_ptr)&sk[0][kpg_base + 32 * kpar];
+    const lds_ptr k_lane_p1 = (lds_ptr)&sk[0][kpg_base + 32 * (kpar ^ 1)];
+    const int vgsw = ((ln >> 2) ^ (ln >> 3)) & 1;
+    const lds_ptr v_lane_pg = (lds_ptr)&sv[0][(g >> 1) * 4096 + ln * 16 + 8 * ((g & 1) ^ vgsw)];
     // K operand of key block kb, dim step ks: row 16 kb + ln, elements 32 ks + 8 g .. +7
     const lds_ptr k_lane = (lds_ptr)&sk[0][ln * KS + 8 * g];
     // MFMA i of a QK phase: key block i % 4, dim step i / 4 (four independent accumulators)
     auto kfrag = [&](lds_ptr kt, int i) {
         return *reinterpret_cast<lds_v8>(kt + (i & 3) * 16 * KS + (i >> 2) * 32);
+    };
+    auto kfrag_p = [&](int buf, int i) {  // paged: key block i % 4, dim step i / 4
+        const int kb = i & 3, ks = i >> 2;
+        const lds_ptr kl = (kb & 1) ? k_lane_p1 : k_lane_p0;
+        return *reinterpret_cast<lds_v8>(kl + buf * (BN * KS) + (kb >> 1) * 8192 + ks * 512);
     };
     // V^T operand of dim block db, key step j by two transposing reads: in the
     // 16-lane group g, lane j' points at key row 32 j + 4 g + j' / 4 (+ 16 for the
@@ -965,6 +1071,7 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
     const int vsw = 2 * (vrow & 7);
     auto vfrag = [&](int buf, int i) {  // MFMA i of a PV phase: dim block i % 16, key step i / 16
         const int db = i % NDB, j = i / NDB;
+        if constexpr (PG) return *reinterpret_cast<lds_v8>(v_lane_pg + buf * (BN * D) + j * 8192 + db * 256);
         const int ch = (2 * db + ((ln & 3) >> 1)) ^ vsw;
         const lds_ptr base = (lds_ptr)&sv[buf][0] + (32 * j + vrow) * D + 8 * ch + 4 * (ln & 1);
         const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)base);
@@ -1001,13 +1108,17 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
         const lds_ptr kt = k_lane + buf * (BN * KS);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto kf_at = [&](int i) {
+            if constexpr (PG) return kfrag_p(buf, i);
+            else return kfrag(kt, i);
+        };
         v8 kf[PF];
 #pragma unroll
-        for (int i = 0; i < PF; ++i) kf[i] = kfrag(kt, i);
+        for (int i = 0; i < PF; ++i) kf[i] = kf_at(i);
 #pragma unroll
         for (int i = 0; i < NM; ++i) {
             const v8 ka = kf[i % PF];
-            if (i + PF < NM) kf[i % PF] = kfrag(kt, i + PF);
+            if (i + PF < NM) kf[i % PF] = kf_at(i + PF);
             s[i & 3] = Mfma16<T>::mma(ka, qr[i >> 2], s[i & 3]);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
@@ -1018,15 +1129,17 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
         }
         __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
     };
-    auto phase_softmax = [&](int t, bool masked) {
+    auto phase_softmax = [&](int t, bool masked, unsigned bad) {
         const int k0 = t * BN;
         if (masked) {
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int key = k0 + 16 * kb + 4 * g + r;
-                    if (key >= Sk || (a.causal && key > q_off + qpos)) s[kb][r] = -INFINITY;
+                    const int kr = PG ? 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + r : 16 * kb + 4 * g + r;
+                    const int key = k0 + kr;
+                    if (key >= Sk || (a.causal && key > q_off + qpos) || ((bad >> (kr >> 4)) & 1))
+                        s[kb][r] = -INFINITY;
                 }
         }
         // exps against the current running max; the max only when their sum says a
@@ -1082,7 +1195,10 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
     if (wave < NW / 2) {
         for (int t = 0; t <= nloc; ++t) {
             mfma_phase(t);
-            if (t < nloc && tb + t < w_tiles) phase_softmax(tb + t, tb + t >= t_mask);
+            if (t < nloc && tb + t < w_tiles) {
+                const unsigned bd = (bad_units >> (4 * (t % NB))) & 15;
+                phase_softmax(tb + t, tb + t >= t_mask || bd, bd);
+            }
             if (t + 1 <= nloc) issue_unit(t + 1);
             if (t < nloc) {
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -1091,7 +1207,10 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
         }
     } else {
         for (int t = 0; t <= nloc; ++t) {
-            if (t >= 1 && tb + t - 1 < w_tiles) phase_softmax(tb + t - 1, tb + t - 1 >= t_mask);
+            if (t >= 1 && tb + t - 1 < w_tiles) {
+                const unsigned bd = (bad_units >> (4 * ((t - 1) % NB))) & 15;
+                phase_softmax(tb + t - 1, tb + t - 1 >= t_mask || bd, bd);
+            }
             if (t + 1 <= nloc) issue_unit(t + 1);
             mfma_phase(t);
             if (t < nloc) {
@@ -1103,7 +1222,7 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
 
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
-    if (a.ksplit > 1) {  // unnormalised partial of this key split
+    if (split) {  // unnormalised partial of this key split
         if (qpos < S) {
             const size_t row = (((size_t)ksp * (gridDim.z / a.ksplit) + b) * S + qpos) * a.hq + head;
             float* po = a.part_o + row * D;
@@ -1346,15 +1465,18 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillF32Args a) {
 // The key splits of a prefill launch combined per (batch, query row, head): the
 // log-sum-exp merge of the splits' (max, sum) in log2 units and their O.  One
 // wavefront per row, D / 64 values per lane.
+// Rows of query positions below q0 (blocks that were not split) are already written; the
+// launch starts at row `first`.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
                                                             const float* __restrict__ part_ml,
                                                             float* __restrict__ out, long long rows,
-                                                            int ksplit, const float* __restrict__ gate) {
+                                                            int ksplit, const float* __restrict__ gate,
+                                                            long long first, int S, int hq, int q0) {
     constexpr int V = D / 64;
     typedef float fv __attribute__((ext_vector_type(V)));
-    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    const long long row = first + (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows || (row / hq) % S < q0) return;
     const int lane = threadIdx.x & 63;
     float M = -1e30f;
     for (int k = 0; k < ksplit; ++k) M = fmaxf(M, part_ml[2 * (k * rows + row)]);
@@ -1401,16 +1523,16 @@ void launch_d(const PrefillArgs& a, int hpw, int n_kv_heads, int seq_len, int ba
             const dim3 block8(512);
             switch (hpw) {
                 case 4:
-                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 4>), grid, block8, 0, s, a);
-                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 4>), grid, block8, 0, s, a);
+                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 4, false>), grid, block8, 0, s, a);
+                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 4, false>), grid, block8, 0, s, a);
                     break;
                 case 2:
-                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 2>), grid, block8, 0, s, a);
-                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 2>), grid, block8, 0, s, a);
+                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 2, false>), grid, block8, 0, s, a);
+                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 2, false>), grid, block8, 0, s, a);
                     break;
                 default:
-                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 1>), grid, block8, 0, s, a);
-                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 1>), grid, block8, 0, s, a);
+                    if (bf) hipLaunchKernelGGL((prefill_fa256_kernel<bf16, 1, false>), grid, block8, 0, s, a);
+                    else hipLaunchKernelGGL((prefill_fa256_kernel<f16, 1, false>), grid, block8, 0, s, a);
             }
             return;
         }
@@ -1509,6 +1631,38 @@ PrefillSched prefill_sched(int batch, int seq_len, int n_q_heads, int n_kv_heads
     if (env_k && !sc.paired) sc.ksplit = std::max(1, std::min(4, std::atoi(env_k)));
     return sc;
 }
+
+// The selective key split of a launch with a.ksplit > 1 and wrows query rows per block:
+// blocks of at most kthr = ceil(most tiles / ksplit) tiles run whole (no more work than a
+// split piece of the longest block), the longer ones are split.  Sets a.kthr; returns the
+// first query row of a split block (S when none is: nothing to merge).
+int split_plan(PrefillArgs& a, int wrows) {
+    const int nqb = (a.S + wrows - 1) / wrows;
+    auto tiles = [&](int qb) {
+        const int keys = a.causal ? std::min(a.Sk, a.q_off + qb * wrows + wrows) : a.Sk;
+        return (keys + BN - 1) / BN;
+    };
+    a.kthr = (tiles(nqb - 1) + a.ksplit - 1) / a.ksplit;
+    for (int qb = 0; qb < nqb; ++qb)
+        if (tiles(qb) > a.kthr) return qb * wrows;
+    return a.S;
+}
+
+// The merge of the split blocks' rows (batch, query row >= q0, head) into out.
+hipError_t launch_merge(int D, const PrefillArgs& a, int batch, int q0, float* out, hipStream_t s) {
+    if (q0 >= a.S) return hipSuccess;
+    const long long rows = (long long)batch * a.S * a.hq;
+    const long long first = batch == 1 ? (long long)q0 * a.hq : 0;
+    const dim3 grid((unsigned)((rows - first + 3) / 4));
+#define PI_MERGE(DD)                                                                               \
+    hipLaunchKernelGGL(prefill_merge_kernel<DD>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out, rows, \
+                       a.ksplit, a.gate, first, a.S, a.hq, q0)
+    if (D == 256) PI_MERGE(256);
+    else if (D == 128) PI_MERGE(128);
+    else PI_MERGE(64);
+#undef PI_MERGE
+    return hipGetLastError();
+}
 }  // namespace
 
 size_t prefill_ws_floats(int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
@@ -1547,26 +1701,22 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     const PrefillSched sc = prefill_sched(batch, seq_len, n_q_heads, n_kv_heads, head_dim, causal);
     a.paired = sc.paired;
     a.ksplit = 1;
+    a.kthr = 0;
     a.part_o = a.part_ml = nullptr;
     a.gate = gate;
     const size_t rows = (size_t)batch * seq_len * n_q_heads;
+    int q0 = seq_len;
     if (sc.ksplit > 1 && ws && ws_floats >= (size_t)sc.ksplit * rows * (head_dim + 2)) {
         a.ksplit = sc.ksplit;
         a.part_o = ws;
         a.part_ml = ws + (size_t)sc.ksplit * rows * head_dim;
+        q0 = split_plan(a, ROWS * (head_dim == 256 ? PrefillCfg<256>::NW : PrefillCfg<128>::NW) / sc.hpw);
     }
     if (head_dim == 128) launch_d<128>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
     else launch_d<256>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.ksplit == 1) return e;
-    const dim3 grid((unsigned)((rows + 3) / 4));
-    if (head_dim == 128)
-        hipLaunchKernelGGL(prefill_merge_kernel<128>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out,
-                           (long long)rows, a.ksplit, gate);
-    else
-        hipLaunchKernelGGL(prefill_merge_kernel<256>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out,
-                           (long long)rows, a.ksplit, gate);
-    return hipGetLastError();
+    return launch_merge(head_dim, a, batch, q0, out, s);
 }
 
 hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, const int32_t* page_table,
@@ -1574,7 +1724,7 @@ hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, co
                                float scale, float* out, float* ws, size_t ws_floats, hipStream_t s,
                                const float* gate) {
     const int D = g.head_dim;
-    if (g.dtype != 1 || (D != 64 && D != 128) || q_off < 0 || n_tok < 1) return hipErrorInvalidValue;
+    if (g.dtype != 1 || (D != 64 && D != 128 && D != 256) || q_off < 0 || n_tok < 1) return hipErrorInvalidValue;
     if ((uint64_t)g.n_kv_heads * std::max(g.kstride, g.vstride) >= (1ull << 32)) return hipErrorInvalidValue;
     const bool multiple = n_q_heads % g.n_kv_heads == 0;
     if (!multiple && gqa_mode != 0) return hipErrorInvalidValue;
@@ -1602,36 +1752,42 @@ hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, co
     const PrefillSched sc = prefill_sched(1, n_tok, n_q_heads, g.n_kv_heads, D, 1);
     a.paired = sc.paired;
     a.ksplit = 1;
+    a.kthr = 0;
     a.part_o = a.part_ml = nullptr;
     const size_t rows = (size_t)n_tok * n_q_heads;
+    // 256 / hpw query rows per workgroup (128 / hpw at D = 256), 8 wavefronts either way
+    const int wrows = ROWS * (D == 256 ? PrefillCfg<256>::NW : PrefillCfg<128>::NW) / sc.hpw;
+    int q0 = n_tok;
     if (sc.ksplit > 1 && ws && ws_floats >= (size_t)sc.ksplit * rows * (D + 2)) {
         a.ksplit = sc.ksplit;
         a.part_o = ws;
         a.part_ml = ws + (size_t)sc.ksplit * rows * D;
+        q0 = split_plan(a, wrows);
     }
-    constexpr int NW = PrefillCfg<128>::NW;
-    const int wrows = ROWS * NW / sc.hpw;
     const int nqb = (n_tok + wrows - 1) / wrows;
     const dim3 grid(g.n_kv_heads * (a.group / sc.hpw), a.paired ? (nqb + 1) / 2 : nqb, a.ksplit);
-    const dim3 block(64 * NW);
+    const dim3 block(512);
 #define PI_PAGED(DD)                                                                                 \
     switch (sc.hpw) {                                                                                \
         case 4: hipLaunchKernelGGL((prefill_fa_kernel<f16, 4, DD, true>), grid, block, 0, s, a); break; \
         case 2: hipLaunchKernelGGL((prefill_fa_kernel<f16, 2, DD, true>), grid, block, 0, s, a); break; \
         default: hipLaunchKernelGGL((prefill_fa_kernel<f16, 1, DD, true>), grid, block, 0, s, a);      \
     }
-    if (D == 128) { PI_PAGED(128) } else { PI_PAGED(64) }
+    if (D == 256) {
+        switch (sc.hpw) {
+            case 4: hipLaunchKernelGGL((prefill_fa256_kernel<f16, 4, true>), grid, block, 0, s, a); break;
+            case 2: hipLaunchKernelGGL((prefill_fa256_kernel<f16, 2, true>), grid, block, 0, s, a); break;
+            default: hipLaunchKernelGGL((prefill_fa256_kernel<f16, 1, true>), grid, block, 0, s, a);
+        }
+    } else if (D == 128) {
+        PI_PAGED(128)
+    } else {
+        PI_PAGED(64)
+    }
 #undef PI_PAGED
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.ksplit == 1) return e;
-    const dim3 mgrid((unsigned)((rows + 3) / 4));
-    if (D == 128)
-        hipLaunchKernelGGL(prefill_merge_kernel<128>, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, out,
-                           (long long)rows, a.ksplit, gate);
-    else
-        hipLaunchKernelGGL(prefill_merge_kernel<64>, mgrid, dim3(256), 0, s, a.part_o, a.part_ml, out,
-                           (long long)rows, a.ksplit, gate);
-    return hipGetLastError();
+    return launch_merge(D, a, 1, q0, out, s);
 }
 
 }  // namespace pi

@@ -3,7 +3,6 @@
 //
 //   kv_append   : LayerCache append (src/model/mod.rs:1140-1146) into the paged pool
 //   kv_read     : pool -> reference layout [T][n_kv][D] f32
-//   kv_gather   : one sequence's f16 pages -> contiguous f16 K / V rows (paged prefill)
 //   rope        : ops::apply_rope / apply_rope_with_freqs (src/ops.rs:35-67,130-157)
 //                 as driven by src/model/mod.rs:1072-1138
 //   head_rmsnorm: ops::rms_norm per head (src/ops.rs:13-27; src/model/mod.rs:1035-1070)
@@ -142,54 +141,6 @@ __global__ __launch_bounds__(256) void kv_read_kernel(KvGeom g, const int32_t* _
         }
         ko[idx] = kv;
         vo[idx] = vv;
-    }
-}
-
-// One workgroup per (page, KV head) of a sequence: its 16 tokens of K and V
-// out of the f16 pool into contiguous [token][Hkv][D] f16 rows, the layout the
-// prefill kernel streams.  A K block is already 16-byte chunks of 8 dims per
-// token ([D/8][16][8]); a V block is dim-major ([D][16]) and is transposed in
-// LDS.  Tokens at or past n_tok are not written; a page id outside the pool
-// gives zero rows.
-template <int D>
-__global__ __launch_bounds__(256) void kv_gather_kernel(KvGeom g, const int32_t* __restrict__ pt,
-                                                        int n_tok, f16* __restrict__ k_out,
-                                                        f16* __restrict__ v_out) {
-    constexpr int NCH = D / 8 * kPageTokens;  // 16-byte chunks of one block
-    __shared__ __attribute__((aligned(16))) f16 sv[D * kPageTokens];
-    const int lp = blockIdx.x, h = blockIdx.y, H = g.n_kv_heads;
-    const int page = pt[lp];
-    const bool ok = page >= 0 && page < g.n_pages;
-    const size_t blk = (size_t)(ok ? page : 0) * H + h;
-    const f16x8* kb = reinterpret_cast<const f16x8*>(static_cast<const char*>(g.k) + blk * g.kstride);
-    const f16x8* vb = reinterpret_cast<const f16x8*>(static_cast<const char*>(g.v) + blk * g.vstride);
-    for (int i = threadIdx.x; i < NCH; i += 256) {
-        *reinterpret_cast<f16x8*>(&sv[8 * i]) = ok ? vb[i] : f16x8{};
-        const int c = i / kPageTokens, tok = i % kPageTokens;  // chunk i = dims 8c.., token tok
-        const int pos = lp * kPageTokens + tok;
-        if (pos < n_tok)
-            *reinterpret_cast<f16x8*>(k_out + ((size_t)pos * H + h) * D + 8 * c) = ok ? kb[i] : f16x8{};
-    }
-    __syncthreads();
-    // V rows out of the [D][16] block by transposing LDS reads: in the 16-lane group of
-    // dim chunk c, lane j points at dim 8c + 4e + j/4, tokens 4 (j % 4) .. +3 (e = 0, 1);
-    // lane i then holds dims 8c + 4e .. +3 of token i, and writes 16 bytes of its row.
-    typedef short s4 __attribute__((ext_vector_type(4)));
-    typedef f16 f16x4_ __attribute__((ext_vector_type(4)));
-    typedef __attribute__((address_space(3))) s4* lds_s4;
-    const int j = threadIdx.x & 15, grp = threadIdx.x >> 4;  // 16 groups of 16 lanes
-    for (int c = grp; c < D / 8; c += 16) {
-        f16x8 x;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const f16* src = &sv[(8 * c + 4 * e + (j >> 2)) * kPageTokens + 4 * (j & 3)];
-            const s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)src);
-            const f16x4_ y = __builtin_bit_cast(f16x4_, r);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) x[4 * e + q] = y[q];
-        }
-        const int pos = lp * kPageTokens + j;
-        if (pos < n_tok) *reinterpret_cast<f16x8*>(v_out + ((size_t)pos * H + h) * D + 8 * c) = x;
     }
 }
 
@@ -421,7 +372,7 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
     __shared__ float cs_s[2][128];  // cos, sin of pair i at this token's position
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int hkv = g.n_kv_heads, heads = hq + hkv;
-    const bool table = gridDim.y == 1;  // uniform per launch
+    const bool table = gridDim.y == 1;  // uniform per launch: the token remap below
     // A prompt launch keeps each run of 16 consecutive tokens (a page of K and V when
     // the prompt starts on a page) on one XCD: workgroups are dispatched round-robin
     // over the 8 XCDs, and workgroup 8 (16 g + i) + x takes token 128 g + 16 x + i, so
@@ -435,101 +386,113 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
     const int t = u % n_tok, sq = u / n_tok;
     const int pos = start_pos.of(sq) + t;
     start_pos.write_ctx();
-    if (table) {
-        for (int i = threadIdx.x; i < n_pairs; i += 256) {
-            const float theta = (float)pos * f.f[i];
-            cs_s[0][i] = cosf(theta);
-            cs_s[1][i] = sinf(theta);
-        }
-        __syncthreads();
+    // cos / sin of the workgroup's token position, once per pair (every thread of the
+    // workgroup works on that token)
+    for (int i = threadIdx.x; i < n_pairs; i += 256) {
+        const float theta = (float)pos * f.f[i];
+        cs_s[0][i] = cosf(theta);
+        cs_s[1][i] = sinf(theta);
     }
+    __syncthreads();
     auto cos_sin = [&](int i, float* c, float* sn) {
-        if (table) {
-            *c = cs_s[0][i];
-            *sn = cs_s[1][i];
-        } else {
-            const float theta = (float)pos * f.f[i];
-            *c = cosf(theta);
-            *sn = sinf(theta);
-        }
+        *c = cs_s[0][i];
+        *sn = cs_s[1][i];
     };
     const int e0 = EPL * lane;  // this lane's first element of a row
     const int per = (heads + gridDim.y - 1) / gridDim.y;
     const int h1 = min(heads, (int)(blockIdx.y + 1) * per);
-    for (int head = blockIdx.y * per + wv; head < h1; head += 4) {
-        const bool is_q = head < hq;
-        const int kvh = head - hq;
-        float* x = is_q ? q + (((size_t)sq * n_tok + t) * hq + head) * D
-                        : k + (((size_t)sq * n_tok + t) * hkv + kvh) * D;
-        const float* nw = is_q ? qn : kn;
-        float xv[EPL];
-        load_vec<EPL>(xv, x + e0);
-        if (nw) {  // ops::rms_norm (src/ops.rs:13-27) per head
-            float ss = 0.f;
+    auto row_of = [&](int head) {
+        return head < hq ? q + (((size_t)sq * n_tok + t) * hq + head) * D
+                         : k + (((size_t)sq * n_tok + t) * hkv + (head - hq)) * D;
+    };
+    // A wavefront's heads are head0, head0 + 4, ...: the rows of up to MH of them (and the V
+    // rows of its K heads) are loaded before any is processed, so their loads overlap.
+    constexpr int MH = 6;
+    for (int head0 = blockIdx.y * per + wv; head0 < h1; head0 += 4 * MH) {
+        float xs[MH][EPL], vs[MH][EPL];
 #pragma unroll
-            for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
-            const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-            float wv_[EPL];
-            load_vec<EPL>(wv_, nw + e0);
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * wv_[j];
-        }
-        // ops::apply_rope / apply_rope_with_freqs: pair i is (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
-        if (neox) {
-            const int off = n_pairs / EPL;  // lanes between the two elements of a pair
-            const int src = lane < off ? lane + off : lane - off;
-            float pv[EPL];
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) pv[j] = __shfl(xv[j], src < 64 ? src : lane, 64);
-            if (lane < 2 * off) {
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) {
-                    const bool first = lane < off;
-                    const int i = first ? e0 + j : e0 + j - n_pairs;
-                    float c, sn;
-                    cos_sin(i, &c, &sn);
-                    xv[j] = first ? xv[j] * c - pv[j] * sn : pv[j] * sn + xv[j] * c;
-                }
+        for (int m = 0; m < MH; ++m) {
+            const int head = head0 + 4 * m;
+            if (head < h1) {
+                load_vec<EPL>(xs[m], row_of(head) + e0);
+                if (head >= hq) load_vec<EPL>(vs[m], v + (((size_t)sq * n_tok + t) * hkv + (head - hq)) * D + e0);
             }
-        } else if constexpr (EPL >= 2) {
+        }
 #pragma unroll
-            for (int j = 0; j < EPL; j += 2) {
-                const int i = (e0 + j) >> 1;
+        for (int m = 0; m < MH; ++m) {
+            const int head = head0 + 4 * m;
+            if (head >= h1) break;
+            const bool is_q = head < hq;
+            const int kvh = head - hq;
+            float* x = row_of(head);
+            const float* nw = is_q ? qn : kn;
+            float* xv = xs[m];
+            if (nw) {  // ops::rms_norm (src/ops.rs:13-27) per head
+                float ss = 0.f;
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
+#pragma unroll
+                for (int sh = 32; sh >= 1; sh >>= 1) ss = wave_sum_xor(ss, sh);
+                const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+                float wv_[EPL];
+                load_vec<EPL>(wv_, nw + e0);
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * wv_[j];
+            }
+            // ops::apply_rope / apply_rope_with_freqs: pair i is (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
+            if (neox) {
+                const int off = n_pairs / EPL;  // lanes between the two elements of a pair
+                const int src = lane < off ? lane + off : lane - off;
+                float pv[EPL];
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) pv[j] = __shfl(xv[j], src < 64 ? src : lane, 64);
+                if (lane < 2 * off) {
+#pragma unroll
+                    for (int j = 0; j < EPL; ++j) {
+                        const bool first = lane < off;
+                        const int i = first ? e0 + j : e0 + j - n_pairs;
+                        float c, sn;
+                        cos_sin(i, &c, &sn);
+                        xv[j] = first ? xv[j] * c - pv[j] * sn : pv[j] * sn + xv[j] * c;
+                    }
+                }
+            } else if constexpr (EPL >= 2) {
+#pragma unroll
+                for (int j = 0; j < EPL; j += 2) {
+                    const int i = (e0 + j) >> 1;
+                    if (i < n_pairs) {
+                        float c, sn;
+                        cos_sin(i, &c, &sn);
+                        const float x0 = xv[j], x1 = xv[j + 1];
+                        xv[j] = x0 * c - x1 * sn;
+                        xv[j + 1] = x0 * sn + x1 * c;
+                    }
+                }
+            } else {
+                const float pv0 = __shfl_xor(xv[0], 1, 64);
+                const int i = e0 >> 1;
                 if (i < n_pairs) {
                     float c, sn;
                     cos_sin(i, &c, &sn);
-                    const float x0 = xv[j], x1 = xv[j + 1];
-                    xv[j] = x0 * c - x1 * sn;
-                    xv[j + 1] = x0 * sn + x1 * c;
+                    xv[0] = (lane & 1) ? pv0 * sn + xv[0] * c : xv[0] * c - pv0 * sn;
                 }
             }
-        } else {
-            const float pv0 = __shfl_xor(xv[0], 1, 64);
-            const int i = e0 >> 1;
-            if (i < n_pairs) {
-                float c, sn;
-                cos_sin(i, &c, &sn);
-                xv[0] = (lane & 1) ? pv0 * sn + xv[0] * c : xv[0] * c - pv0 * sn;
-            }
-        }
-        store_vec<EPL>(x + e0, xv);
-        // append-then-attend (src/model/mod.rs:1140-1146): K (normed, rotated) and V at pos
-        const int lp = pos / kPageTokens;
-        if (!is_q && pos >= 0 && lp < max_pages) {
-            const int page = pt[(size_t)sq * max_pages + lp];
-            if (page >= 0 && page < g.n_pages) {
-                const int tok = pos % kPageTokens;
-                const size_t blk = (size_t)page * hkv + kvh;
-                PT* kp = reinterpret_cast<PT*>(static_cast<char*>(g.k) + blk * g.kstride);
-                PT* vp = reinterpret_cast<PT*>(static_cast<char*>(g.v) + blk * g.vstride);
-                float vr[EPL];
-                load_vec<EPL>(vr, v + (((size_t)sq * n_tok + t) * hkv + kvh) * D + e0);
+            store_vec<EPL>(x + e0, xv);
+            // append-then-attend (src/model/mod.rs:1140-1146): K (normed, rotated) and V at pos
+            const int lp = pos / kPageTokens;
+            if (!is_q && pos >= 0 && lp < max_pages) {
+                const int page = pt[(size_t)sq * max_pages + lp];
+                if (page >= 0 && page < g.n_pages) {
+                    const int tok = pos % kPageTokens;
+                    const size_t blk = (size_t)page * hkv + kvh;
+                    PT* kp = reinterpret_cast<PT*>(static_cast<char*>(g.k) + blk * g.kstride);
+                    PT* vp = reinterpret_cast<PT*>(static_cast<char*>(g.v) + blk * g.vstride);
+                    const float* vr = vs[m];
 #pragma unroll
-                for (int j = 0; j < EPL; ++j) {
-                    kp[k_index<PT>(tok, e0 + j)] = from_f32<PT>(xv[j]);
-                    vp[v_index(tok, e0 + j)] = from_f32<PT>(vr[j]);
+                    for (int j = 0; j < EPL; ++j) {
+                        kp[k_index<PT>(tok, e0 + j)] = from_f32<PT>(xv[j]);
+                        vp[v_index(tok, e0 + j)] = from_f32<PT>(vr[j]);
+                    }
                 }
             }
         }
@@ -594,21 +557,6 @@ hipError_t launch_kv_read(const KvGeom& g, const int32_t* page_table, int32_t ma
     else
         hipLaunchKernelGGL((kv_read_kernel<float>), dim3(grid_for(total)), dim3(256), 0, s, g,
                            page_table, max_pages, seq, start, n_tok, k_out, v_out);
-    return hipGetLastError();
-}
-
-hipError_t launch_kv_gather(const KvGeom& g, const int32_t* page_table, int32_t n_tok,
-                            void* k_out, void* v_out, hipStream_t s) {
-    if (g.dtype != 1 || n_tok <= 0) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((n_tok + kPageTokens - 1) / kPageTokens), (unsigned)g.n_kv_heads);
-    f16* ko = static_cast<f16*>(k_out);
-    f16* vo = static_cast<f16*>(v_out);
-    switch (g.head_dim) {
-        case 64: hipLaunchKernelGGL(kv_gather_kernel<64>, grid, dim3(256), 0, s, g, page_table, n_tok, ko, vo); break;
-        case 128: hipLaunchKernelGGL(kv_gather_kernel<128>, grid, dim3(256), 0, s, g, page_table, n_tok, ko, vo); break;
-        case 256: hipLaunchKernelGGL(kv_gather_kernel<256>, grid, dim3(256), 0, s, g, page_table, n_tok, ko, vo); break;
-        default: return hipErrorInvalidValue;
-    }
     return hipGetLastError();
 }
 
@@ -689,13 +637,6 @@ __global__ __launch_bounds__(256) void fill_iota_kernel(int32_t* __restrict__ ds
     if (i < n) dst[i] = first + i;
 }
 
-__global__ __launch_bounds__(256) void to_half_kernel(const float* __restrict__ x,
-                                                      f16* __restrict__ y, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x)
-        y[i] = to_f16(x[i]);
-}
-
 // out *= sigmoid(gate) (src/model/mod.rs:1192-1196)
 __global__ __launch_bounds__(256) void apply_gate_kernel(float* __restrict__ out,
                                                          const float* __restrict__ gate, size_t n) {
@@ -707,12 +648,6 @@ __global__ __launch_bounds__(256) void apply_gate_kernel(float* __restrict__ out
 static unsigned grid_1d(size_t n) {
     const size_t b = (n + 255) / 256;
     return (unsigned)(b > 65536 ? 65536 : (b == 0 ? 1 : b));
-}
-
-hipError_t launch_to_half(const float* x, void* y, size_t n, hipStream_t s) {
-    hipLaunchKernelGGL(to_half_kernel, dim3(grid_1d(n)), dim3(256), 0, s, x,
-                       reinterpret_cast<f16*>(y), n);
-    return hipGetLastError();
 }
 
 hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t s) {

@@ -219,13 +219,25 @@ def test_paged_prefill_f16_head_dim_64(prev, n, hq, hkv):
     _check(out, c.oracle(range(n)), f"D 64 prev {prev} + {n}")
 
 
-def test_paged_prefill_page_ids_outside_the_pool_hold_no_tokens():
+@pytest.mark.parametrize("prev,n,hq,hkv", [(0, 300, 16, 2), (17, 64, 16, 2), (1000, 1, 8, 2),
+                                           (50, 129, 12, 4)])
+def test_paged_prefill_f16_head_dim_256(prev, n, hq, hkv):
+    """An f16 pool at head dim 256 (the two-wavefront-per-SIMD flash prefill straight from the
+    pages): a fresh prompt, chunks at non-tile offsets, a single row, modulo heads."""
+    dev = device()
+    c = Chunk(np.random.default_rng(prev * 7 + n + 256), prev, n, hq, hkv, 256)
+    out = c.gpu(dev)
+    _check(out, c.oracle(range(n)), f"D 256 prev {prev} + {n}")
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_paged_prefill_page_ids_outside_the_pool_hold_no_tokens(d):
     """Page-table entries outside [0, n_pages) hold no tokens, as for the decode: their keys
     are masked (a row whose every key is masked gets zeros).  Two pages of the history, one
     inside a tile and one at a tile's start, are made invalid; the oracle drops their keys."""
     from powerinfer_x64_amd import runtime as rt
     dev = device()
-    c = Chunk(np.random.default_rng(0xBAD), 200, 100, 8, 2, 128)
+    c = Chunk(np.random.default_rng(0xBAD + d), 200, 100, 8, 2, d)
     c.gpu(dev)  # pool filled through the real row
     bad = [2, 4]  # pages 2 (keys 32..47) and 4 (keys 64..79)
     row = c.row.copy()
