@@ -51,6 +51,9 @@ def _args():
     p.add_argument("--cpu-seconds", type=float, default=20.0,
                    help="budget of the single-core CPU baseline sample")
     p.add_argument("--only-headline", action="store_true")
+    p.add_argument("--no-graph-replays", action="store_true",
+                   help="leave out the layer-token figures replayed from HIP graphs (thousands of "
+                        "dispatches: slow under a per-dispatch counter profiler)")
     p.add_argument("--workload", default=None,
                    choices=["c1", "c2", "c2_32k", "c3", "c4", "gdn", "gdn_prefill", "tq", "copy",
                             "rows_f", "chunk", "tq_c4", "c4_prefill"],
@@ -367,9 +370,11 @@ def cpu_decode(qh, load, lens, hkv, d, elem_bytes, budget_s, out_gpu, gate=None,
             err = max(err, _row_rel(out_gpu[i], ref))
             if t >= budget_s:
                 break
-    note = (f"; the {len(kept)} sequence(s) were repeated from host memory, so their "
-            f"{sum(k.nbytes + v.nbytes for k, v in kept.values()) / 1e6:.1f} MB can stay in the "
-            f"CPU caches" if calls > len(seen) else "")
+    rep_mb = sum(k.nbytes + v.nbytes for k, v in kept.values()) / 1e6
+    note = ""
+    if calls > len(seen):  # a repeat re-reads its K/V; only a few MB can stay in a CCD's L3
+        where = "can stay in the CPU caches" if rep_mb <= 16 else "is re-read from DRAM on each repeat"
+        note = f"; the {len(kept)} sequence(s) were repeated from host memory ({rep_mb:.1f} MB, which {where})"
     return _cpu(nbytes / t / 1e9, "GB/s",
                 f"or_attn_decode{' + or_apply_gate' if gate is not None else ''} on {len(seen)} "
                 f"of {len(lens)} sequences ({calls} calls, {tokens} tokens) read back from the "
@@ -646,7 +651,7 @@ def _cpu_hbm(name, sec, units, unit_bytes, sample, **extra):
                 us_per_unit=round(sec / units * 1e6, 3), **extra)
 
 
-def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
+def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0, graphs=True):
     """The steps either side of the path: the fused attention prologue (row f1:
     per-head RMSNorm, RoPE, paged append in one launch) and the GDN conv1d and
     RMSNormGated (row f2), at a prompt shape (HBM-bound) and a decode step; and row
@@ -796,17 +801,24 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
     lay.close()
     # the decode token on device tensors (pi_attn_layer_forward_dev: prologue, decode over the
     # prompt's pages and the gate), HIP events over 200 tokens after the 1024-token prompt
-    n_tok_dev = 2 * 200 + 20  # timer.run: warm-up, the timed pass and the per-call pass
+    # timer.run (warm-up, the timed pass, the per-call pass), then one call and a capture of 64
+    n_tok_dev = 2 * 200 + 20 + 65
     lay = rt.AttnLayer(dev, prompt + n_tok_dev + 16, hq, hkv, d, torch.float16, q_norm_w=qn_w,
                        k_norm_w=kn_w, rope_dim=64, rope_base=1e7, sections=[11, 11, 10, 0])
     dev_t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda")  # noqa: E731
     lay.forward_dev(dev_t(raw[0]), dev_t(raw[1]), dev_t(raw[2]), gate=dev_t(raw[3]))
     qd, kd1, vd1, gd1 = (dev_t(x) for x in raw[4:])
     od = torch.empty((1, hq, d), dtype=torch.float32, device="cuda")
-    r = timer.run(lambda: lay.forward_dev(qd, kd1, vd1, gate=gd1, out=od), 200, 20)
+    tok = lambda: lay.forward_dev(qd, kd1, vd1, gate=gd1, out=od)  # noqa: E731
+    r = timer.run(tok, 200, 20)
+    # back to back from Python the host's per-call cost sets the pace; 64 tokens captured in
+    # one HIP graph and replayed give the device time per token (each replay recomputes the
+    # captured positions)
     res["f3_attn_layer_decode_token_c4_device"] = {
         "us_per_token": r["ms_avg"] * 1e3, "us_median": r["ms_median"] * 1e3,
         "tokens_per_s": 1e3 / r["ms_avg"]}
+    if graphs:
+        res["f3_attn_layer_decode_token_c4_device"]["us_per_token_graph"] = graph_us_per_call(torch, tok)
     lay.close()
     if leg_s > 0:
         freqs = orc.compute_imrope_freqs(1e7, 64, [11, 11, 10, 0])
@@ -868,10 +880,13 @@ def bench_rows_f(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
     od = torch.empty((1, hv, dv), dtype=torch.float32, device="cuda")
     gl.reset()
     gl.forward_dev(dev_t(xa), dev_t(za), dev_t(ba), dev_t(aa))  # a prompt's state and conv rows
-    r = timer.run(lambda: gl.forward_dev(xd, zd, bd, ad, out=od), 200, 20)
+    gtok = lambda: gl.forward_dev(xd, zd, bd, ad, out=od)  # noqa: E731
+    r = timer.run(gtok, 200, 20)
     res["f3_gdn_layer_decode_token_c5_device"] = {
         "us_per_token": r["ms_avg"] * 1e3, "us_median": r["ms_median"] * 1e3,
         "tokens_per_s": 1e3 / r["ms_avg"]}
+    if graphs:
+        res["f3_gdn_layer_decode_token_c5_device"]["us_per_token_graph"] = graph_us_per_call(torch, gtok)
     gl.close()
     if leg_s > 0:
         kd, vd = hk * dk, hv * dv
@@ -988,29 +1003,56 @@ def bench_chunk(torch, rt, dev, timer, steps, warmup, cpu_s=0.0):
         "ms_per_call": walls["chunk"], "tokens_per_s": n / walls["chunk"] * 1e3,
         "fresh_prompt_ms_per_call": walls["fresh"], "vs_fresh_prompt": walls["chunk"] / walls["fresh"]}
     if cpu_s > 0:
-        # the reference's per-token loop for the first tokens of the chunk over the 8192 history
+        # the reference's per-token loop (the oracle's C entry on caches allocated once, so no
+        # call copies a cache), 4 tokens per call for the first tokens of the chunk over the
+        # 8192 history
+        c_lib = orc.lib()
         freqs = orc.compute_imrope_freqs(1e7, 64, [11, 11, 10, 0])
-        okw = dict(q_norm_w=qn_w, k_norm_w=kn_w, rope_dim=64, rope_base=1e7, freqs=freqs)
+        fr = np.ascontiguousarray(freqs, np.float32)
         # the history's cache: K normalised and rotated at 0 .. 8191 (no attention needed)
         _, kc = orc.attn_prepare(None, hh[1], hq, hkv, d, k_norm_w=kn_w, rope_dim=64,
                                  rope_base=1e7, freqs=freqs, pos0=0)
-        vc = hh[2]
+        kcap = np.zeros((hist + n, hkv, d), f32)
+        vcap = np.zeros((hist + n, hkv, d), f32)
+        kcap[:hist], vcap[:hist] = kc, hh[2]
+
+        def tokens(i0, m_, prev, kc_, vc_):
+            qx = np.array(ch[0][i0:i0 + m_], f32)  # normalised / rotated in place
+            kx = np.array(ch[1][i0:i0 + m_], f32)
+            o = np.empty((m_, hq, d), f32)
+            c_lib.or_attn_layer_tokens(_fp(o), _fp(qx), _fp(np.ascontiguousarray(ch[3][i0:i0 + m_])),
+                                       _fp(kx), _fp(np.ascontiguousarray(ch[2][i0:i0 + m_])), m_,
+                                       hq, hkv, d, d, d, _fp(qn_w), _fp(kn_w), 1e-6, 64, 1e7,
+                                       _fp(fr), fr.size, _fp(kc_), _fp(vc_), prev)
         m, t = 0, 0.0
         with OneCore():
             while m < n and t < cpu_s:
                 t0 = time.perf_counter()
-                _, kc, vc = orc.attn_layer_tokens(ch[0][m:m + 4], ch[1][m:m + 4], ch[2][m:m + 4],
-                                                  gate=ch[3][m:m + 4], key_cache=kc, value_cache=vc,
-                                                  prev_seq_len=hist + m, **okw)
+                tokens(m, 4, hist + m, kcap, vcap)
                 t += time.perf_counter() - t0
                 m += 4
         cpu = _cpu(m / t, "tokens/s", f"or_attn_layer_tokens for the first {m} tokens of the "
                    f"chunk over the {hist}-token history, 4 per call", round(t, 3))
         res["f3_attn_layer_chunk_1024_over_8192_c4"]["cpu_baseline"] = cpu
         res["f3_attn_layer_chunk_1024_over_8192_c4_device"]["cpu_baseline"] = cpu
-        res["f3_attn_layer_prompt_1024_c4_device"]["cpu_baseline"] = dict(
-            cpu, sample="the same CPU figure (tokens of a chunk after 8192 cached); a fresh "
-                        "prompt's first tokens attend fewer keys")
+        # the fresh prompt: tokens at positions spread evenly over it, each attending its own
+        # prefix (the prompt's keys normalised and rotated once, as the cache holds them)
+        _, kp = orc.attn_prepare(None, ch[1], hq, hkv, d, k_norm_w=kn_w, rope_dim=64,
+                                 rope_base=1e7, freqs=freqs, pos0=0)
+        kpc, vpc = np.ascontiguousarray(kp, f32), np.array(ch[2], f32)
+        stride = 37
+        m, t, i = 0, 0.0, 0
+        with OneCore():
+            while i < n and t < cpu_s:
+                t0 = time.perf_counter()
+                tokens(i, 1, i, kpc, vpc)
+                t += time.perf_counter() - t0
+                m += 1
+                i += stride
+        res["f3_attn_layer_prompt_1024_c4_device"]["cpu_baseline"] = _cpu(
+            m / t, "tokens/s", f"or_attn_layer_tokens for {m} tokens of a fresh {n}-token prompt "
+            f"(positions 0, {stride}, {2 * stride}, ...: each attends its own prefix), one per "
+            f"call", round(t, 3))
     lay.close()
 
     # the paged prefill kernel alone: config-2 heads, 1024 queries over 8192 + 1024 keys
@@ -1151,7 +1193,7 @@ def _single(torch, rt, dev, timer, a):
     if w == "copy":
         return bench_copy(torch, timer, st, wu)
     if w == "rows_f":
-        return bench_rows_f(torch, rt, dev, timer, st, wu)
+        return bench_rows_f(torch, rt, dev, timer, st, wu, graphs=not a.no_graph_replays)
     if w == "chunk":
         return bench_chunk(torch, rt, dev, timer, st, wu)
     return bench_gdn_decode(torch, rt, dev, timer, st, wu)
@@ -1281,7 +1323,7 @@ def main():
                                                          cpu_s=budget["tq"] / 2, d=256, gated=True)
         torch.cuda.empty_cache()
         wl.update(bench_rows_f(torch, rt, dev, timer, a.steps, a.warmup,
-                               cpu_s=budget["rows_f"]))
+                               cpu_s=budget["rows_f"], graphs=not a.no_graph_replays))
         wl.update(bench_chunk(torch, rt, dev, timer, min(a.steps, 10), min(a.warmup, 3),
                               cpu_s=budget["chunk"]))
         line["workloads"] = {k: _rounded(v) for k, v in wl.items()}
