@@ -181,12 +181,12 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
  * row d_page_table[max_pages] (the chunk's own K/V appended first, as the
  * reference appends before it attends).  d_q [n_tok][n_q_heads][D] in the
  * pool's dtype (normed, rotated), d_out [n_tok][n_q_heads][D] f32.  f16 pool
- * at D = 64 or 128: the flash prefill reads K/V straight from the pages (no
- * copy of the history); at D = 256 the pages are gathered into contiguous f16
- * rows in the handle's workspace first.  f32 pool (D = 64, 128 or 256): a
- * kernel reads the pages directly and keeps f32 accuracy (bf16 hi + lo operand
- * splits on the MFMA).  A page id outside [0, n_pages) holds no tokens: its
- * keys are left out of the softmax, as in pi_attn_decode. */
+ * (D = 64, 128 or 256): the flash prefill reads K/V straight from the pages
+ * (no copy of the history; the handle's workspace holds only the key splits'
+ * partials of the chunk's rows).  f32 pool (D = 64, 128 or 256): a kernel
+ * reads the pages directly and keeps f32 accuracy (bf16 hi + lo operand splits
+ * on the MFMA).  A page id outside [0, n_pages) holds no tokens: its keys are
+ * left out of the softmax, as in pi_attn_decode. */
 int pi_attn_prefill_paged(pi_handle h, const void* d_q, pi_kv_pool pool,
                           const int32_t* d_page_table, int32_t max_pages, int32_t start_pos,
                           int32_t n_tok, int32_t n_q_heads, int32_t gqa_mode, float scale,
