@@ -132,6 +132,25 @@ def test_layer_f16_cache_gated_prompt_and_key_split(hq, hkv, d, chunks):
            np.random.default_rng(0x1A8 + d), hq, hkv, d, gate=True)
 
 
+@pytest.mark.parametrize("paired,ksplit", [("1", None), (None, "2"), (None, "3"), (None, "4")])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 2, 256), (32, 8, 128), (8, 2, 64)])
+def test_layer_f16_cache_gated_forced_schedules(monkeypatch, paired, ksplit, hq, hkv, d):
+    """A gated prompt and a gated continued chunk of an f16 cache under each forced schedule: the
+    paired blocks, and 2-4 key splits, where blocks longer than a split piece merge their splits
+    (the merge applies the gate) and the shorter ones run whole (the epilogue applies it)."""
+    if paired:
+        monkeypatch.setenv("PI_PREFILL_PAIRED", paired)
+    else:
+        monkeypatch.setenv("PI_PREFILL_PAIRED", "0")
+        monkeypatch.setenv("PI_PREFILL_KSPLIT", ksplit)
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    chunks = [300, 130]
+    layer = rt.AttnLayer(dev, sum(chunks) + 16, hq, hkv, d, torch.float16, rope_base=1e6)
+    _drive(layer, chunks, dict(rope_base=1e6), _rel(1e-2),
+           np.random.default_rng(0x1B0 + d + (int(ksplit) if ksplit else 7)), hq, hkv, d, gate=True)
+
+
 def test_layer_rejects_short_norm_weights():
     """Norm weights must hold head_dim values: a shorter array is refused before anything
     reads it."""
