@@ -285,8 +285,11 @@ int pi_ssm_forward(pi_handle h, float* h_y, const float* h_x, const float* h_con
  * LayerCache (src/model/mod.rs:73-106) of one attention layer for one sequence, held on the
  * device: a paged pool of max_tokens tokens, the per-head Q/K RMSNorm weights (NULL when the
  * layer has none, src/model/mod.rs:1035-1070), the RoPE mode (NORM when h_sections is NULL,
- * else the sectioned NeoX rotation, :1072-1138) and the KV dtype (PI_F32 or PI_F16, head_dim
- * 64, 128 or 256). */
+ * else the sectioned NeoX rotation, :1072-1138) and the KV dtype (PI_F32 or PI_F16).
+ * head_dim is 1..256: a width other than 64, 128 or 256 runs zero-padded to the next of them
+ * (the pool's rows and the step's kernels at that width; zero dims change no q.k, the output
+ * is cut back to head_dim, and the Q/K RMSNorm, RoPE and the 1/sqrt(head_dim) scale use
+ * head_dim itself). */
 typedef struct pi_attn_layer_s* pi_attn_layer;
 int pi_attn_layer_create(pi_handle h, int32_t max_tokens, int32_t n_heads, int32_t n_kv_heads,
                          int32_t head_dim, int32_t kv_dtype, const float* h_q_norm_w,
@@ -294,8 +297,8 @@ int pi_attn_layer_create(pi_handle h, int32_t max_tokens, int32_t n_heads, int32
                          const int32_t* h_sections, int32_t gqa_mode, pi_attn_layer* out);
 /* The same layer with the reference's separate head widths (src/model/mod.rs:976-982,
  * 1043-1190): query heads of q_head_dim >= head_dim values of which attention, the Q norm and
- * RoPE use the first head_dim (the rest pass through untouched); key heads of head_dim (the
- * pool's, 64 / 128 / 256); value heads of v_head_dim, of which the first min(head_dim,
+ * RoPE use the first head_dim (the rest pass through untouched); key heads of head_dim
+ * (1..256); value heads of v_head_dim, of which the first min(head_dim,
  * v_head_dim) reach the output.  forward then takes q and gate [n][n_heads][q_head_dim], k
  * [n][n_kv_heads][head_dim], v [n][n_kv_heads][v_head_dim] and writes out
  * [n][n_heads][head_dim] (dims at or past v_head_dim zero); the gate multiplies the flat

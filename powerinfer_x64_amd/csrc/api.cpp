@@ -51,6 +51,7 @@ struct pi_attn_layer_s {
     pi_kv_pool pool = nullptr;      // max_pages pages, page i at physical page i
     int32_t max_pages = 0, n_heads = 0, n_kv = 0, dim = 0, kv_dtype = 0;
     int32_t q_dim = 0, v_dim = 0;   // query / value head widths (dim: the key head width)
+    int32_t pdim = 0;               // the step's row width: the smallest of 64 / 128 / 256 >= dim
     int32_t rope_dim = 0, gqa_mode = 0;
     float eps = 0.f, rope_base = 0.f;
     int32_t sections[4] = {0, 0, 0, 0};
@@ -1072,6 +1073,8 @@ int pi_attn_layer_create_dims(pi_handle h, int32_t max_tokens, int32_t n_heads,
     if (q_head_dim < head_dim || v_head_dim <= 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: q_head_dim=%d head_dim=%d v_head_dim=%d",
                     q_head_dim, head_dim, v_head_dim);
+    if (head_dim <= 0 || head_dim > 256)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_layer_create: head_dim %d (1..256)", head_dim);
     if (max_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_layer_create: max_tokens=%d n_heads=%d n_kv_heads=%d",
                     max_tokens, n_heads, n_kv_heads);
@@ -1087,6 +1090,9 @@ int pi_attn_layer_create_dims(pi_handle h, int32_t max_tokens, int32_t n_heads,
     L->n_heads = n_heads;
     L->n_kv = n_kv_heads;
     L->dim = head_dim;
+    // a head narrower than a kernel width runs zero-padded to the next one: zero dims add
+    // nothing to q.k and give zero output dims, and the scale and the norm keep head_dim
+    L->pdim = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
     L->q_dim = q_head_dim;
     L->v_dim = v_head_dim;
     L->kv_dtype = kv_dtype;
@@ -1102,16 +1108,20 @@ int pi_attn_layer_create_dims(pi_handle h, int32_t max_tokens, int32_t n_heads,
         pi_attn_layer_destroy(L);
         return rc;
     };
-    int rc = pi_kv_pool_create(h, L->max_pages, pi::kPageTokens, n_kv_heads, head_dim, kv_dtype, &L->pool);
+    int rc = pi_kv_pool_create(h, L->max_pages, pi::kPageTokens, n_kv_heads, L->pdim, kv_dtype, &L->pool);
     if (rc) return undo(rc);
     hipError_t e = hipSuccess;
     const size_t pt = (size_t)kLayerRows * L->max_pages;
+    const size_t wb = (size_t)L->pdim * sizeof(float);
     e = hipMalloc(reinterpret_cast<void**>(&L->d_pt), pt * sizeof(int32_t));
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&L->d_ctx), (kLayerRows + 1) * sizeof(int32_t));
-    if (e == hipSuccess && h_q_norm_w) e = hipMalloc(reinterpret_cast<void**>(&L->d_qn), head_dim * sizeof(float));
-    if (e == hipSuccess && h_k_norm_w) e = hipMalloc(reinterpret_cast<void**>(&L->d_kn), head_dim * sizeof(float));
-    if (e == hipSuccess && L->d_qn) e = hipMemcpy(L->d_qn, h_q_norm_w, head_dim * sizeof(float), hipMemcpyHostToDevice);
-    if (e == hipSuccess && L->d_kn) e = hipMemcpy(L->d_kn, h_k_norm_w, head_dim * sizeof(float), hipMemcpyHostToDevice);
+    // norm weights zero past head_dim, so the padding dims stay zero after the norm
+    for (auto [dst, src] : {std::pair<float**, const float*>{&L->d_qn, h_q_norm_w}, {&L->d_kn, h_k_norm_w}}) {
+        if (e != hipSuccess || !src) continue;
+        e = hipMalloc(reinterpret_cast<void**>(dst), wb);
+        if (e == hipSuccess) e = hipMemset(*dst, 0, wb);
+        if (e == hipSuccess) e = hipMemcpy(*dst, src, head_dim * sizeof(float), hipMemcpyHostToDevice);
+    }
     if (e == hipSuccess) {
         std::vector<int32_t> rows(pt);
         for (size_t i = 0; i < pt; ++i) rows[i] = (int32_t)(i % L->max_pages);
@@ -1142,12 +1152,12 @@ void pi_attn_layer_reset(pi_attn_layer L) {
 int32_t pi_attn_layer_seq_len(pi_attn_layer L) { return L ? L->seq_len : 0; }
 
 // The attention step of forward for n tokens whose q, k, v (and gate) are on the
-// device: norm + RoPE + append at positions seq_len .., then attention for every
-// token over the keys up to its own.  An f16 cache at head_dim 128 / 256 runs
-// the flash prefill for n > 1 (a fresh prompt over its own rows; a continued
-// chunk over the sequence's pages gathered to f16 rows); anything else runs one
-// decode row per token.  Positions and row lengths are written on the device,
-// so the step enqueues work on `s` and never waits for it.
+// device, in rows of pdim floats (zero past head_dim): norm + RoPE + append at
+// positions seq_len .., then attention for every token over the keys up to its own.
+// For n > 1 an f16 cache runs the flash prefill and an f32 cache the f32 prefill,
+// both reading K / V straight from the layer's pages; a single token runs one decode
+// row.  Positions and row lengths are written on the device, so the step enqueues
+// work on `s` and never waits for it.
 static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, const float* dv,
                            const float* dg, int32_t n, float* dout, hipStream_t s) {
     const int prev = L->seq_len;
@@ -1155,7 +1165,7 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
         return fail(h, PI_ERR_OUT_OF_MEMORY, "attention layer: %d + %d tokens exceed the layer cache of %d",
                     prev, n, L->max_pages * pi::kPageTokens);
     void* sv = reinterpret_cast<void*>(s);
-    const int D = L->dim;
+    const int D = L->pdim;  // row width; the head's own width is L->dim
     const size_t nq = (size_t)n * L->n_heads * D;
     int rc;
     // the callers stage anything else; checked here too, before the first launch
@@ -1167,7 +1177,7 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     const bool rows = !(n > 1 && (L->kv_dtype == PI_F16 || L->kv_dtype == PI_F32));
     {
         const pi::KvGeom& g = L->pool->g;
-        const int rd = L->rope_dim <= 0 ? D : std::min(L->rope_dim, D);
+        const int rd = L->rope_dim <= 0 ? L->dim : std::min(L->rope_dim, L->dim);
         if (rd / 2 > 128) return fail(h, PI_ERR_UNSUPPORTED, "attention layer: rope_dim %d", rd);
         pi::RopeFreqs f;
         std::memset(&f, 0, sizeof f);
@@ -1176,10 +1186,10 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
         PI_HIP(h, pi::launch_attn_prologue(dq, dk, dv, L->d_qn, L->d_kn, L->eps, f, rd / 2,
                                            L->has_sections ? 1 : 0, g, L->d_pt, L->max_pages, nullptr,
                                            1, n, L->n_heads, s, prev, L->d_ctx,
-                                           rows ? std::min(n, kLayerRows) : 0),
+                                           rows ? std::min(n, kLayerRows) : 0, L->dim),
                "attention layer");
     }
-    const float scale = 1.0f / std::sqrt((float)D);
+    const float scale = 1.0f / std::sqrt((float)L->dim);
     // the prefill kernels apply a 16-byte-aligned gate where they write the output; another
     // gate takes a launch of its own after them
     const float* dg_fused = dg && !((uintptr_t)dg & 15) ? dg : nullptr;
@@ -1218,28 +1228,38 @@ static int attn_layer_step(pi_handle h, pi_attn_layer L, float* dq, float* dk, c
     return PI_OK;
 }
 
-// Copies `rows` rows of `width` floats between buffers of row pitches `dp` / `sp` floats.
-static int copy_rows(pi_handle h, void* dst, size_t dp, const void* src, size_t sp, size_t width,
-                     size_t rows, hipMemcpyKind kind, hipStream_t s, const char* what) {
-    if (!rows || !width) return PI_OK;
-    PI_HIP(h, hipMemcpy2DAsync(dst, dp * 4, src, sp * 4, width * 4, rows, kind, s), what);
-    return PI_OK;
-}
-
-// The layer's inputs in the step's packed form, [n][H][head_dim] rows (src/model/mod.rs:
+// The layer's inputs in the step's packed form, [n][H][pdim] rows (src/model/mod.rs:
 // 1043-1190): the first head_dim dims of each query head; V cut or zero-padded to head_dim
 // (output dims at or past the value width stay zero, as the reference's head_out); the gate
 // as the flat prefix of n_heads * head_dim values of each token's n_heads * q_head_dim
-// (the reference multiplies attn_out[i] by sigmoid(output_gate[i]), :1192-1196).
-static int pack_layer_inputs(pi_handle h, pi_attn_layer L, const float* q, const float* v,
-                             const float* g, int32_t n, float* dq, float* dv, float* dg,
-                             hipMemcpyKind kind, hipStream_t s, const char* what) {
-    const size_t D = L->dim, Hq = L->n_heads, Hkv = L->n_kv;
-    int rc = copy_rows(h, dq, D, q, L->q_dim, D, (size_t)n * Hq, kind, s, what);
-    if (!rc && L->v_dim < (int)D) PI_HIP(h, pi::launch_fill_zero(dv, (size_t)n * Hkv * D, s), what);
-    if (!rc) rc = copy_rows(h, dv, D, v, L->v_dim, std::min<size_t>(D, L->v_dim), (size_t)n * Hkv, kind, s, what);
-    if (!rc && g) rc = copy_rows(h, dg, Hq * D, g, Hq * L->q_dim, Hq * D, n, kind, s, what);
-    return rc;
+// (the reference multiplies attn_out[i] by sigmoid(output_gate[i]), :1192-1196), head h's
+// dims the values h * head_dim ..  Every row is zero past head_dim out to pdim.  k (at
+// head_dim wide rows) is packed only when dk is given (pdim > head_dim).
+static int pack_layer_inputs(pi_handle h, pi_attn_layer L, const float* q, const float* k,
+                             const float* v, const float* g, int32_t n, float* dq, float* dk,
+                             float* dv, float* dg, hipStream_t s, const char* what) {
+    const size_t D = L->dim, W = L->pdim, Hq = L->n_heads, Hkv = L->n_kv, qd = L->q_dim, vd = L->v_dim;
+    const int d = (int)D, w = (int)W;
+    PI_HIP(h, pi::launch_pack_rows(dq, q, n, (int)Hq, d, w, Hq * qd, qd, Hq * W, W, s), what);
+    if (dk) PI_HIP(h, pi::launch_pack_rows(dk, k, n, (int)Hkv, d, w, Hkv * D, D, Hkv * W, W, s), what);
+    PI_HIP(h, pi::launch_pack_rows(dv, v, n, (int)Hkv, (int)std::min(D, vd), w, Hkv * vd, vd, Hkv * W, W, s),
+           what);
+    if (g) PI_HIP(h, pi::launch_pack_rows(dg, g, n, (int)Hq, d, w, Hq * qd, D, Hq * W, W, s), what);
+    return PI_OK;
+}
+
+// The step's outputs back to the caller's widths: q's first head_dim dims of each query
+// head (normalised and rotated; the rest of a q_head_dim row untouched), and, where the
+// step ran on wider rows (dk / dout given), k and out cut to head_dim.
+static int unpack_layer_outputs(pi_handle h, pi_attn_layer L, int32_t n, const float* dq, float* q,
+                                const float* dk, float* k, const float* dout, float* out,
+                                hipStream_t s, const char* what) {
+    const size_t D = L->dim, W = L->pdim, Hq = L->n_heads, Hkv = L->n_kv, qd = L->q_dim;
+    const int d = (int)D;
+    PI_HIP(h, pi::launch_pack_rows(q, dq, n, (int)Hq, d, d, Hq * W, W, Hq * qd, qd, s), what);
+    if (dk) PI_HIP(h, pi::launch_pack_rows(k, dk, n, (int)Hkv, d, d, Hkv * W, W, Hkv * D, D, s), what);
+    if (dout) PI_HIP(h, pi::launch_pack_rows(out, dout, n, (int)Hq, d, d, Hq * W, W, Hq * D, D, s), what);
+    return PI_OK;
 }
 
 // A small host-slice call (a decode token) stages its slices through one pinned host
@@ -1276,30 +1296,38 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
     hipStream_t s = h->stream;
     const char* what = "pi_attn_layer_forward";
     PI_HIP(h, hipSetDevice(h->device), what);
-    const int D = L->dim;
+    const int D = L->dim, W = L->pdim;
     const size_t nq = (size_t)n_tokens * L->n_heads * D, nk = (size_t)n_tokens * L->n_kv * D;
-    // Slices as the caller holds them: q and gate [n][Hq][q_dim], v [n][Hkv][v_dim].  With
-    // distinct widths they arrive whole in "io" regions and are packed on the device (2D
-    // copies from pageable memory would go row by row).
-    const bool packed = L->q_dim == D && L->v_dim == D;
+    const size_t nqw = (size_t)n_tokens * L->n_heads * W, nkw = (size_t)n_tokens * L->n_kv * W;
+    // Slices as the caller holds them: q and gate [n][Hq][q_dim], v [n][Hkv][v_dim], k and
+    // out [n][H][head_dim].  With distinct widths, or a head_dim the step runs padded to
+    // pdim, they arrive whole in "io" regions and are packed on the device (2D copies from
+    // pageable memory would go row by row).
+    const bool packed = L->q_dim == D && L->v_dim == D && W == D;
+    const bool wide = W != D;
     const size_t qin = (size_t)n_tokens * L->n_heads * L->q_dim;
     const size_t vin = (size_t)n_tokens * L->n_kv * L->v_dim;
     const size_t gin = h_gate ? qin : 0;
-    // device staging: [out | q io | k | v io | gate io] (+ packed q, v, gate for distinct widths),
-    // so the inputs (q, k, v, gate) and the outputs (out, q, k) are each one contiguous run.
-    // Every region the kernels address starts on a 16-byte boundary: with distinct widths
-    // the io regions' lengths need not be multiples of 4 floats, so the packed regions
-    // after them start at the next 16-byte boundary.
+    // device staging: [out | q io | k | v io | gate io] (+ packed q, v, gate, and k and out
+    // at pdim wide rows, when not packed), so the inputs (q, k, v, gate) and the outputs
+    // (out, q, k) are each one contiguous run.  Every region the kernels address starts on
+    // a 16-byte boundary: with distinct widths the io regions' lengths need not be
+    // multiples of 4 floats, so the packed regions after them start at the next 16-byte
+    // boundary (the packed regions are whole pdim rows).
     const size_t pk0 = (nq + qin + nk + vin + qin + 3) & ~(size_t)3;
-    const size_t need = packed ? pk0 : pk0 + 2 * nq + nk;
+    const size_t need = packed ? pk0 : pk0 + 2 * nqw + nkw + (wide ? nkw + nqw : 0);
     int rc = grow(h, &L->d_buf, &L->buf_floats, need, s, "pi_attn_layer_forward staging", false);
     if (rc) return rc;
     float *dout = L->d_buf, *qio = dout + nq, *dk = qio + qin, *vio = dk + nk, *gio = vio + vin;
-    float *dq = qio, *dv = vio, *dg = gio;
+    float *dq = qio, *dv = vio, *dg = gio, *dkw = dk, *doutw = dout;
     if (!packed) {
         dq = L->d_buf + pk0;
-        dv = dq + nq;
-        dg = dv + nk;
+        dv = dq + nqw;
+        dg = dv + nkw;
+        if (wide) {
+            dkw = dg + nqw;
+            doutw = dkw + nkw;
+        }
     }
     const size_t in_f = qin + nk + vin + gin, out_f = nq + qin + nk;
     const bool pin = pinned_staging(h, std::max(in_f, out_f));
@@ -1316,13 +1344,13 @@ int pi_attn_layer_forward(pi_handle h, pi_attn_layer L, float* h_q, float* h_k, 
         if ((rc = copy_sync(h, vio, h_v, vin * 4, hipMemcpyHostToDevice, what))) return rc;
         if (h_gate && (rc = copy_sync(h, gio, h_gate, gin * 4, hipMemcpyHostToDevice, what))) return rc;
     }
-    if (!packed && (rc = pack_layer_inputs(h, L, qio, vio, h_gate ? gio : nullptr, n_tokens, dq, dv, dg,
-                                           hipMemcpyDeviceToDevice, s, what)))
+    if (!packed && (rc = pack_layer_inputs(h, L, qio, dk, vio, h_gate ? gio : nullptr, n_tokens, dq,
+                                           wide ? dkw : nullptr, dv, dg, s, what)))
         return rc;
-    if ((rc = attn_layer_step(h, L, dq, dk, dv, h_gate ? dg : nullptr, n_tokens, dout, s))) return rc;
+    if ((rc = attn_layer_step(h, L, dq, dkw, dv, h_gate ? dg : nullptr, n_tokens, doutw, s))) return rc;
     // q and k go back normalised and rotated (only the first head_dim dims of a query head)
-    if (!packed && (rc = copy_rows(h, qio, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads,
-                                   hipMemcpyDeviceToDevice, s, what)))
+    if (!packed && (rc = unpack_layer_outputs(h, L, n_tokens, dq, qio, wide ? dkw : nullptr, dk,
+                                              wide ? doutw : nullptr, dout, s, what)))
         return rc;
     if (pin) {
         if ((rc = copy_sync(h, h->pin, dout, out_f * 4, hipMemcpyDeviceToHost, what))) return rc;
@@ -1356,19 +1384,25 @@ int pi_attn_layer_forward_dev(pi_handle h, pi_attn_layer L, float* d_q, float* d
     // The step's kernels move q, the gate and out in 16-byte groups.  Rows already in the
     // step's packed form at such addresses go straight in; otherwise they are staged in the
     // layer's buffer (decided before anything is launched, so a call never fails half done).
-    const bool packed = L->q_dim == L->dim && L->v_dim == L->dim;
+    const bool wide = L->pdim != L->dim;
+    const bool packed = L->q_dim == L->dim && L->v_dim == L->dim && !wide;
     const bool out_ok = !((uintptr_t)d_out & 15);
     if (packed && out_ok && !(((uintptr_t)d_q | (uintptr_t)d_gate) & 15))
         return attn_layer_step(h, L, d_q, d_k, d_v, d_gate, n_tokens, d_out, s);
-    const int D = L->dim;
-    const size_t nq = (size_t)n_tokens * L->n_heads * D, nk = (size_t)n_tokens * L->n_kv * D;
-    int rc = grow(h, &L->d_buf, &L->buf_floats, 3 * nq + nk, s, "pi_attn_layer_forward_dev staging", false);
+    const int W = L->pdim;
+    const size_t nqw = (size_t)n_tokens * L->n_heads * W, nkw = (size_t)n_tokens * L->n_kv * W;
+    int rc = grow(h, &L->d_buf, &L->buf_floats, 3 * nqw + nkw + (wide ? nkw : 0), s,
+                  "pi_attn_layer_forward_dev staging", false);
     if (rc) return rc;
-    float *dq = L->d_buf, *dg = dq + nq, *dv = dg + nq, *ds = dv + nk;
-    if ((rc = pack_layer_inputs(h, L, d_q, d_v, d_gate, n_tokens, dq, dv, dg, hipMemcpyDeviceToDevice, s, what))) return rc;
-    if ((rc = attn_layer_step(h, L, dq, d_k, dv, d_gate ? dg : nullptr, n_tokens, out_ok ? d_out : ds, s))) return rc;
-    if (!out_ok) PI_HIP(h, hipMemcpyAsync(d_out, ds, nq * 4, hipMemcpyDeviceToDevice, s), what);
-    return copy_rows(h, d_q, L->q_dim, dq, D, D, (size_t)n_tokens * L->n_heads, hipMemcpyDeviceToDevice, s, what);
+    // [q | gate | v | out | k (pdim wide rows, when wider than head_dim)]
+    float *dq = L->d_buf, *dg = dq + nqw, *dv = dg + nqw, *ds = dv + nkw, *dkw = wide ? ds + nqw : nullptr;
+    if ((rc = pack_layer_inputs(h, L, d_q, d_k, d_v, d_gate, n_tokens, dq, dkw, dv, dg, s, what))) return rc;
+    const bool direct = out_ok && !wide;  // out written in place
+    if ((rc = attn_layer_step(h, L, dq, wide ? dkw : d_k, dv, d_gate ? dg : nullptr, n_tokens,
+                              direct ? d_out : ds, s)))
+        return rc;
+    if (!direct && !wide) PI_HIP(h, hipMemcpyAsync(d_out, ds, nqw * 4, hipMemcpyDeviceToDevice, s), what);
+    return unpack_layer_outputs(h, L, n_tokens, dq, d_q, dkw, d_k, wide ? ds : nullptr, d_out, s, what);
 }
 
 // ---- gated-DeltaNet layer state -------------------------------------------------------

@@ -135,13 +135,22 @@ hipError_t launch_softmax(float* x, int32_t n, hipStream_t s);
 hipError_t launch_apply_gate(float* out, const float* gate, size_t n, hipStream_t s);
 hipError_t launch_fill_iota(int32_t* dst, int32_t n, int32_t first, hipStream_t s);
 hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t s);
+// Row (t, r), t < n_tok, r < n_rows: `width` floats from src + t * s_tok + r * s_row to
+// dst + t * d_tok + r * d_row, zero-filled out to `pad` floats (width <= pad; src and dst
+// must not overlap).
+hipError_t launch_pack_rows(float* dst, const float* src, int32_t n_tok, int32_t n_rows,
+                           int32_t width, int32_t pad, size_t s_tok, size_t s_row, size_t d_tok,
+                           size_t d_row, hipStream_t s);
 hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
                                 const float* k_norm_w, float eps, const RopeFreqs& freqs,
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,
                                 const int32_t* page_table, int32_t max_pages,
                                 const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
                                 int32_t n_q_heads, hipStream_t s, int32_t start_scalar = 0,
-                                int32_t* ctx_out = nullptr, int32_t n_ctx = 0);
+                                int32_t* ctx_out = nullptr, int32_t n_ctx = 0, int32_t norm_dim = 0);
+// norm_dim: the divisor of the per-head RMSNorm's mean square (0: g.head_dim).  A head
+// narrower than the pool's head_dim sits in the first norm_dim dims of its row, the rest
+// zero; the norm weights past norm_dim are zero so the padding stays zero.
 
 // Causal (or full) flash attention of seq_len query rows per sequence over
 // n_keys keys; query row i sits at key position q_off + i (a fresh prompt:

@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
     float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ qn, const float* __restrict__ kn, float eps, RopeFreqs f,
     int n_pairs, int neox, KvGeom g, const int32_t* __restrict__ pt, int max_pages,
-    PrologueStart start_pos, int n_seq, int n_tok, int hq) {
+    PrologueStart start_pos, int n_seq, int n_tok, int hq, int norm_d) {
     __shared__ float row_s[4][256];
     __shared__ float cs_s[2][128];  // cos, sin of pair i at this token's position
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(256) void attn_prologue_kernel(
         if (nw) {  // ops::rms_norm (src/ops.rs:13-27) per head
 #pragma unroll
             for (int m = 32; m >= 1; m >>= 1) ss = wave_sum_xor(ss, m);
-            const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+            const float inv = 1.0f / sqrtf(ss / (float)norm_d + eps);
             for (int d = lane; d < D; d += 64) r[d] = (r[d] * inv) * nw[d];
         }
         __builtin_amdgcn_wave_barrier();
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
     float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ qn, const float* __restrict__ kn, float eps, RopeFreqs f,
     int n_pairs, int neox, KvGeom g, const int32_t* __restrict__ pt, int max_pages,
-    PrologueStart start_pos, int n_seq, int n_tok, int hq) {
+    PrologueStart start_pos, int n_seq, int n_tok, int hq, int norm_d) {
     constexpr int D = 64 * EPL;
     __shared__ float cs_s[2][128];  // cos, sin of pair i at this token's position
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -433,7 +433,7 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
                 for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
 #pragma unroll
                 for (int sh = 32; sh >= 1; sh >>= 1) ss = wave_sum_xor(ss, sh);
-                const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+                const float inv = 1.0f / sqrtf(ss / (float)norm_d + eps);
                 float wv_[EPL];
                 load_vec<EPL>(wv_, nw + e0);
 #pragma unroll
@@ -574,8 +574,10 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
                                 const int32_t* page_table, int32_t max_pages,
                                 const int32_t* start_pos, int32_t n_seq, int32_t n_tok,
                                 int32_t n_q_heads, hipStream_t s, int32_t start_scalar,
-                                int32_t* ctx_out, int32_t n_ctx) {
+                                int32_t* ctx_out, int32_t n_ctx, int32_t norm_dim) {
     if (!start_pos && n_seq != 1) return hipErrorInvalidValue;
+    const int norm_d = norm_dim > 0 ? norm_dim : g.head_dim;
+    if (norm_d > g.head_dim) return hipErrorInvalidValue;
     const PrologueStart sp{start_pos, start_scalar, ctx_out, ctx_out ? n_ctx : 0};
     const long long toks = (long long)n_seq * n_tok;
     if (toks <= 0) return hipSuccess;
@@ -592,7 +594,7 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
 #define PI_PROLOGUE_VEC(PT, E)                                                                     \
     hipLaunchKernelGGL((attn_prologue_vec_kernel<PT, E>), grid, dim3(256), 0, s, q, k, v, q_norm_w, \
                        k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages, sp,           \
-                       n_seq, n_tok, n_q_heads)
+                       n_seq, n_tok, n_q_heads, norm_d)
         const bool hp = g.dtype == 1;
         switch (epl) {
             case 1: if (hp) PI_PROLOGUE_VEC(f16, 1); else PI_PROLOGUE_VEC(float, 1); break;
@@ -605,11 +607,11 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
     if (g.dtype == 1)
         hipLaunchKernelGGL(attn_prologue_kernel<f16>, grid, dim3(256), 0, s, q, k, v, q_norm_w,
                            k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages,
-                           sp, n_seq, n_tok, n_q_heads);
+                           sp, n_seq, n_tok, n_q_heads, norm_d);
     else
         hipLaunchKernelGGL(attn_prologue_kernel<float>, grid, dim3(256), 0, s, q, k, v, q_norm_w,
                            k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages,
-                           sp, n_seq, n_tok, n_q_heads);
+                           sp, n_seq, n_tok, n_q_heads, norm_d);
     return hipGetLastError();
 }
 
@@ -627,6 +629,24 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ dst,
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x)
         dst[i] = 0.f;
+}
+
+// Row (t, r) of an n_tok x n_rows grid: `width` floats from src + t * s_tok + r * s_row
+// to dst + t * d_tok + r * d_row, then zeros out to `pad` floats.  One wave per row.
+__global__ __launch_bounds__(256) void pack_rows_kernel(float* __restrict__ dst,
+                                                        const float* __restrict__ src, long long n,
+                                                        int n_rows, int width, int pad,
+                                                        long long s_tok, long long s_row,
+                                                        long long d_tok, long long d_row) {
+    const int lane = threadIdx.x & 63;
+    for (long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6); row < n;
+         row += (long long)gridDim.x * 4) {
+        const long long t = row / n_rows;
+        const long long r = row - t * n_rows;
+        const float* sp = src + t * s_tok + r * s_row;
+        float* dp = dst + t * d_tok + r * d_row;
+        for (int c = lane; c < pad; c += 64) dp[c] = c < width ? sp[c] : 0.f;
+    }
 }
 
 // dst[i] = first + i for i < n (device-side positions and context lengths, so a
@@ -653,6 +673,19 @@ static unsigned grid_1d(size_t n) {
 hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_1d(n)), dim3(256), 0, s, dst, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_rows(float* dst, const float* src, int32_t n_tok, int32_t n_rows,
+                           int32_t width, int32_t pad, size_t s_tok, size_t s_row, size_t d_tok,
+                           size_t d_row, hipStream_t s) {
+    const long long n = (long long)n_tok * n_rows;
+    if (n <= 0 || pad <= 0) return hipSuccess;
+    if (width < 0 || width > pad) return hipErrorInvalidValue;
+    const long long blocks = (n + 3) / 4;
+    hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)(blocks > 65536 ? 65536 : blocks)), dim3(256), 0, s,
+                       dst, src, n, n_rows, width, pad, (long long)s_tok, (long long)s_row,
+                       (long long)d_tok, (long long)d_row);
     return hipGetLastError();
 }
 

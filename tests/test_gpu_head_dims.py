@@ -4,7 +4,8 @@ and value heads may have different widths; ops::attention_head takes any head_di
 - the f32 KV pool at head_dim 256 (decode against the oracle, max-abs 2e-3);
 - ops::attention_head (src/ops.rs:213-247) with head_dim 129..256 (padded to a kernel width);
 - the LayerCache attention step with q_head_dim > head_dim and v_head_dim below and above
-  head_dim, through the host and the device-pointer entries, against or_attn_layer_tokens
+  head_dim, and with key head widths that are no kernel width (33, 48, 80, 96, 160, 192,
+  200: run zero-padded to the next of 64 / 128 / 256), through the host and the device-pointer entries, against or_attn_layer_tokens
   (which carries the three widths as the reference does): max-abs 2e-3 with an f32 cache,
   per-row relative 1e-2 with an f16 cache; q comes back normalised and rotated in its first
   head_dim dims and untouched past them.
@@ -126,6 +127,90 @@ def test_layer_distinct_widths_device_entry(dq, dk, dv, dtype, gated):
         np.testing.assert_array_equal(out_d.cpu().numpy(), out_h)
         np.testing.assert_array_equal(tq.cpu().numpy(), qh)
         np.testing.assert_array_equal(tk.cpu().numpy(), kh)
+
+
+PADDED = [
+    # (q_head_dim, head_dim, v_head_dim, cache dtype, gate, rope_dim): key heads that are no
+    # kernel width run zero-padded to the next of 64 / 128 / 256
+    (80, 80, 80, torch.float16, True, None),
+    (96, 96, 96, torch.float32, False, 32),
+    (64, 48, 40, torch.float16, True, None),
+    (160, 160, 160, torch.float16, False, 64),
+    (192, 192, 192, torch.float32, True, None),
+    (33, 33, 33, torch.float16, True, None),
+    (256, 200, 224, torch.float16, True, None),
+]
+
+
+@pytest.mark.parametrize("dq,dk,dv,dtype,gated,rope_dim", PADDED)
+def test_layer_padded_head_dim(dq, dk, dv, dtype, gated, rope_dim):
+    """A 150-token prompt, two decode tokens and a 40-token continued chunk, 8/2 heads with
+    Q/K RMSNorm over head_dim (not the padded width), NORM RoPE over rope_dim (an odd
+    head_dim leaves its last dim unrotated) and scale 1/sqrt(head_dim)."""
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    rng = np.random.default_rng(dq * 11 + dk * 5 + dv)
+    hq, hkv, eps, base = 8, 2, 1e-6, 1e6
+    qn = rng.uniform(0.5, 1.5, dk).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, dk).astype(np.float32)
+    layer = rt.AttnLayer(dev, 256, hq, hkv, dk, dtype, q_norm_w=qn, k_norm_w=kn, eps=eps,
+                         rope_base=base, rope_dim=rope_dim, q_head_dim=dq, v_head_dim=dv)
+    kw = dict(q_norm_w=qn, k_norm_w=kn, eps=eps, rope_base=base,
+              rope_dim=dk if rope_dim is None else rope_dim)
+    kc = vc = None
+    prev = 0
+    for n in (150, 1, 1, 40):
+        q, k, v, g = _inputs(rng, n, hq, hkv, dq, dk, dv, gated)
+        ref, kc, vc = orc.attn_layer_tokens(q, k, v, gate=g, key_cache=kc, value_cache=vc,
+                                            prev_seq_len=prev, **kw)
+        qr, kr = orc.attn_prepare(q, k, hq, hkv, dk, pos0=prev, q_head_dim=dq, **kw)
+        qg, kg = q.copy(), k.copy()
+        out = layer.forward(qg, kg, v, gate=g)
+        assert out.shape == (n, hq, dk)
+        if dtype == torch.float32:
+            err = float(np.abs(out - ref).max())
+            assert err <= 2e-3, f"chunk {n} at {prev}: max-abs {err}"
+        else:
+            for i in range(n):
+                err = row_rel_err(out[i], ref[i])
+                assert err <= 1e-2, f"chunk {n} at {prev}: token {i} rel err {err}"
+        if dv < dk:
+            assert not out[:, :, dv:].any()
+        assert np.abs(qg - qr).max() <= 1e-5 and np.abs(kg - kr).max() <= 1e-5
+        np.testing.assert_array_equal(qg[:, :, dk:], q[:, :, dk:])
+        prev += n
+        assert layer.seq_len == prev
+
+
+@pytest.mark.parametrize("dq,dk,dv,dtype,gated,rope_dim", [PADDED[0], PADDED[2], PADDED[4]])
+def test_layer_padded_head_dim_device_entry(dq, dk, dv, dtype, gated, rope_dim):
+    """pi_attn_layer_forward_dev at a padded head_dim gives pi_attn_layer_forward's bits
+    (outputs, and q / k written back) over a prompt, a decode token and a chunk."""
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    rng = np.random.default_rng(0xAD + dq + dk + dv)
+    hq, hkv = 8, 2
+    kn = rng.uniform(0.5, 1.5, dk).astype(np.float32)
+    mk = lambda: rt.AttnLayer(dev, 160, hq, hkv, dk, dtype, k_norm_w=kn, rope_base=1e4,  # noqa: E731
+                              rope_dim=rope_dim, q_head_dim=dq, v_head_dim=dv)
+    host, devl = mk(), mk()
+    for n in (70, 1, 9):
+        q, k, v, g = _inputs(rng, n, hq, hkv, dq, dk, dv, gated)
+        qh, kh = q.copy(), k.copy()
+        out_h = host.forward(qh, kh, v, gate=g)
+        tq, tk = to_dev(q), to_dev(k)
+        out_d = devl.forward_dev(tq, tk, to_dev(v), gate=None if g is None else to_dev(g))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out_d.cpu().numpy(), out_h)
+        np.testing.assert_array_equal(tq.cpu().numpy(), qh)
+        np.testing.assert_array_equal(tk.cpu().numpy(), kh)
+
+
+def test_layer_rejects_head_dim_past_256():
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    with pytest.raises(rt.Unsupported):
+        rt.AttnLayer(dev, 16, 4, 2, 320, torch.float16)
 
 
 def test_layer_rejects_narrow_query_heads():
