@@ -167,8 +167,11 @@ int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
  * reference's per-token loop computes (src/model/mod.rs:668,1140-1190).
  * d_q [batch][seq_len][n_q_heads][D], d_k/d_v [batch][seq_len][n_kv_heads][D]
  * in dtype (PI_BF16 or PI_F16); d_out [batch][seq_len][n_q_heads][D] f32.
- * MFMA flash attention with fp32 softmax/accumulation; D = 128 or 256.  Head
- * counts as pi_attn_decode. */
+ * MFMA flash attention with fp32 softmax/accumulation.  D = head_dim is 1..256:
+ * 128 and 256 run directly; another width runs zero-padded to the next of
+ * them (q, k, v copied into padded rows of a handle workspace, the output cut
+ * back; zero dims change no q.k), at that width's cost.  Head counts as
+ * pi_attn_decode. */
 int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d_v, int32_t dtype,
                     int32_t batch, int32_t seq_len, int32_t n_q_heads, int32_t n_kv_heads,
                     int32_t head_dim, int32_t causal, int32_t gqa_mode, float scale, float* d_out,

@@ -30,6 +30,8 @@ struct pi_handle_s {
     size_t tq_qv_floats = 0;
     float* pfs_buf = nullptr;      // prefill key-split partials
     size_t pfs_floats = 0;
+    float* pad_buf = nullptr;      // pi_attn_prefill's padded rows at a head_dim of no kernel
+    size_t pad_floats = 0;
     float* pin = nullptr;          // pinned host staging of the small host-slice layer calls
     size_t pin_floats = 0;
     // Ordering of the workspaces above across caller streams: ws_event marks
@@ -286,6 +288,7 @@ void pi_destroy(pi_handle h) {
     (void)hipFree(h->h2d_scratch);
     (void)hipFree(h->tq_qv);
     (void)hipFree(h->pfs_buf);
+    (void)hipFree(h->pad_buf);
     if (h->pin) (void)hipHostFree(h->pin);
     if (h->ws_event) (void)hipEventDestroy(h->ws_event);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -603,8 +606,8 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill: gqa_mode %d", gqa_mode);
     if (dtype != PI_BF16 && dtype != PI_F16)
         return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: dtype %d (bf16 or f16)", dtype);
-    if (head_dim != 128 && head_dim != 256)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: head_dim %d (128 or 256)", head_dim);
+    if (head_dim <= 0 || head_dim > 256)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: head_dim %d (1..256)", head_dim);
     if (gqa_mode == PI_GQA_GROUPED && n_q_heads % n_kv_heads != 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_attn_prefill: grouped head map with n_q_heads %d not a multiple of n_kv_heads %d",
                     n_q_heads, n_kv_heads);
@@ -613,12 +616,42 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
     hipStream_t s = pick(h, stream);
     int rc;
     if ((rc = ws_begin(h, s, "pi_attn_prefill"))) return rc;
-    const size_t need = pi::prefill_ws_floats(batch, seq_len, n_q_heads, n_kv_heads, head_dim, causal ? 1 : 0);
+    // The kernels run at 128 or 256 dims; another head_dim runs zero-padded to the next of
+    // them (zero dims change no q.k and give zero output dims; the caller's scale stands)
+    const int W = head_dim <= 128 ? 128 : 256;
+    const size_t need = pi::prefill_ws_floats(batch, seq_len, n_q_heads, n_kv_heads, W, causal ? 1 : 0);
     if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "pi_attn_prefill workspace", false))) return rc;
-    PI_HIP(h, pi::launch_prefill(d_q, d_k, d_v, dtype, batch, seq_len, seq_len, 0, n_q_heads,
-                                 n_kv_heads, head_dim, causal ? 1 : 0, gqa_mode, scale, d_out,
+    const void *q = d_q, *k = d_k, *v = d_v;
+    float* out = d_out;
+    const size_t rq = (size_t)batch * seq_len * n_q_heads, rkv = (size_t)batch * seq_len * n_kv_heads;
+    if (W != head_dim) {
+        if (rq > (size_t)INT32_MAX)
+            return fail(h, PI_ERR_UNSUPPORTED, "pi_attn_prefill: %zu query rows at a padded head_dim", rq);
+        // [out rows (f32) | q | k | v rows (16-bit)], all W wide
+        const size_t half_rows = (rq + 2 * rkv) * W;
+        if ((rc = grow(h, &h->pad_buf, &h->pad_floats, rq * W + (half_rows + 1) / 2, s,
+                       "pi_attn_prefill padding", false)))
+            return rc;
+        out = h->pad_buf;
+        uint16_t* pq = reinterpret_cast<uint16_t*>(h->pad_buf + rq * W);
+        uint16_t *pk = pq + rq * W, *pv = pk + rkv * W;
+        const struct { uint16_t* dst; const void* src; size_t rows; } ins[] = {
+            {pq, d_q, rq}, {pk, d_k, rkv}, {pv, d_v, rkv}};
+        for (const auto& c : ins)
+            PI_HIP(h, pi::launch_pack_rows16(c.dst, static_cast<const uint16_t*>(c.src), (int32_t)c.rows, 1,
+                                             head_dim, W, head_dim, 0, W, 0, s),
+                   "pi_attn_prefill");
+        q = pq;
+        k = pk;
+        v = pv;
+    }
+    PI_HIP(h, pi::launch_prefill(q, k, v, dtype, batch, seq_len, seq_len, 0, n_q_heads,
+                                 n_kv_heads, W, causal ? 1 : 0, gqa_mode, scale, out,
                                  h->pfs_buf, h->pfs_floats, s),
            "pi_attn_prefill");
+    if (W != head_dim)
+        PI_HIP(h, pi::launch_pack_rows(d_out, out, (int32_t)rq, 1, head_dim, head_dim, W, 0, head_dim, 0, s),
+               "pi_attn_prefill");
     return ws_end(h, s, "pi_attn_prefill");
 }
 

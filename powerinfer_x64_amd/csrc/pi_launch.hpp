@@ -141,6 +141,10 @@ hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t s);
 hipError_t launch_pack_rows(float* dst, const float* src, int32_t n_tok, int32_t n_rows,
                            int32_t width, int32_t pad, size_t s_tok, size_t s_row, size_t d_tok,
                            size_t d_row, hipStream_t s);
+// The same for 16-bit elements (f16 / bf16 bits; zero bits are +0 in both).
+hipError_t launch_pack_rows16(uint16_t* dst, const uint16_t* src, int32_t n_tok, int32_t n_rows,
+                             int32_t width, int32_t pad, size_t s_tok, size_t s_row, size_t d_tok,
+                             size_t d_row, hipStream_t s);
 hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float* q_norm_w,
                                 const float* k_norm_w, float eps, const RopeFreqs& freqs,
                                 int32_t n_pairs, int32_t neox, const KvGeom& g,

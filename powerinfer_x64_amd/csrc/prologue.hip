@@ -633,8 +633,9 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ dst,
 
 // Row (t, r) of an n_tok x n_rows grid: `width` floats from src + t * s_tok + r * s_row
 // to dst + t * d_tok + r * d_row, then zeros out to `pad` floats.  One wave per row.
-__global__ __launch_bounds__(256) void pack_rows_kernel(float* __restrict__ dst,
-                                                        const float* __restrict__ src, long long n,
+template <typename E>
+__global__ __launch_bounds__(256) void pack_rows_kernel(E* __restrict__ dst,
+                                                        const E* __restrict__ src, long long n,
                                                         int n_rows, int width, int pad,
                                                         long long s_tok, long long s_row,
                                                         long long d_tok, long long d_row) {
@@ -643,9 +644,9 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(float* __restrict__ dst,
          row += (long long)gridDim.x * 4) {
         const long long t = row / n_rows;
         const long long r = row - t * n_rows;
-        const float* sp = src + t * s_tok + r * s_row;
-        float* dp = dst + t * d_tok + r * d_row;
-        for (int c = lane; c < pad; c += 64) dp[c] = c < width ? sp[c] : 0.f;
+        const E* sp = src + t * s_tok + r * s_row;
+        E* dp = dst + t * d_tok + r * d_row;
+        for (int c = lane; c < pad; c += 64) dp[c] = c < width ? sp[c] : E(0);
     }
 }
 
@@ -676,17 +677,30 @@ hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_pack_rows(float* dst, const float* src, int32_t n_tok, int32_t n_rows,
-                           int32_t width, int32_t pad, size_t s_tok, size_t s_row, size_t d_tok,
-                           size_t d_row, hipStream_t s) {
+template <typename E>
+static hipError_t pack_rows(E* dst, const E* src, int32_t n_tok, int32_t n_rows, int32_t width,
+                            int32_t pad, size_t s_tok, size_t s_row, size_t d_tok, size_t d_row,
+                            hipStream_t s) {
     const long long n = (long long)n_tok * n_rows;
     if (n <= 0 || pad <= 0) return hipSuccess;
     if (width < 0 || width > pad) return hipErrorInvalidValue;
     const long long blocks = (n + 3) / 4;
-    hipLaunchKernelGGL(pack_rows_kernel, dim3((unsigned)(blocks > 65536 ? 65536 : blocks)), dim3(256), 0, s,
-                       dst, src, n, n_rows, width, pad, (long long)s_tok, (long long)s_row,
+    hipLaunchKernelGGL(pack_rows_kernel<E>, dim3((unsigned)(blocks > 65536 ? 65536 : blocks)), dim3(256), 0,
+                       s, dst, src, n, n_rows, width, pad, (long long)s_tok, (long long)s_row,
                        (long long)d_tok, (long long)d_row);
     return hipGetLastError();
+}
+
+hipError_t launch_pack_rows(float* dst, const float* src, int32_t n_tok, int32_t n_rows,
+                           int32_t width, int32_t pad, size_t s_tok, size_t s_row, size_t d_tok,
+                           size_t d_row, hipStream_t s) {
+    return pack_rows(dst, src, n_tok, n_rows, width, pad, s_tok, s_row, d_tok, d_row, s);
+}
+
+hipError_t launch_pack_rows16(uint16_t* dst, const uint16_t* src, int32_t n_tok, int32_t n_rows,
+                             int32_t width, int32_t pad, size_t s_tok, size_t s_row, size_t d_tok,
+                             size_t d_row, hipStream_t s) {
+    return pack_rows(dst, src, n_tok, n_rows, width, pad, s_tok, s_row, d_tok, d_row, s);
 }
 
 hipError_t launch_fill_iota(int32_t* dst, int32_t n, int32_t first, hipStream_t s) {

@@ -120,6 +120,32 @@ def test_prefill_batch_of_two(causal):
         assert row_rel_err(out[bi], ref) <= 1e-2, bi
 
 
+@pytest.mark.parametrize("d,s,dtype,causal", [
+    (64, 300, torch.bfloat16, True), (80, 200, torch.float16, True),
+    (96, 129, torch.bfloat16, False), (192, 300, torch.bfloat16, True),
+    (33, 70, torch.float16, True), (200, 150, torch.float16, False)])
+def test_prefill_padded_head_dims(d, s, dtype, causal):
+    """Head widths with no kernel of their own (run zero-padded to 128 / 256 dims), two
+    sequences in one launch with 8 / 2 heads: every row against the oracle's per-row
+    decode (causal) or float64 brute force (no mask); scale 1/sqrt(d)."""
+    from powerinfer_x64_amd import runtime as rt
+    dev = device()
+    rng = np.random.default_rng(7 * d + s)
+    seqs = [_inputs(rng, s, 8, 2, d, dtype=dtype) for _ in range(2)]
+    q, k, v = (torch.stack([t[i] for t in seqs]).cuda() for i in range(3))
+    out = rt.attn_prefill(dev, q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy()
+    assert out.shape == (2, s, 8, d)
+    for bi, (tq, tk, tv) in enumerate(seqs):
+        if causal:
+            ref = _oracle_rows(tq, tk, tv, range(s))
+        else:
+            qf, kf, vf = (t.float().numpy() for t in (tq, tk, tv))
+            ref = np.stack([ref64.attention(qf[i], kf, vf, lambda h: h % 2) for i in range(s)])
+        assert row_rel_err(out[bi], ref) <= 1e-2, bi
+
+
 @pytest.mark.parametrize("s,dtype", [(1, torch.bfloat16), (70, torch.bfloat16),
                                      (300, torch.float16), (700, torch.bfloat16)])
 def test_prefill_head_dim_256(s, dtype):
