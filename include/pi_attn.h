@@ -370,11 +370,12 @@ int pi_gdn_layer_forward_dev(pi_handle h, pi_gdn_layer layer, const float* d_qkv
 int pi_gdn_layer_reset(pi_handle h, pi_gdn_layer layer);
 
 /* ---- TurboQuant compressed KV (src/turboquant/mod.rs:408-566) -------------------------
- * CompressedKVCache with head_dim D = 128 or 256: per KV head h a TurboQuant(3 bits, D, D QJL
+ * CompressedKVCache with head_dim D = 1..256: per KV head h a TurboQuant(3 bits, D, D QJL
  * bits, seed 0xCAFEBABE + h) key quantizer (:430-437) and f16 values.  Keys are stored as
- * D/2-byte records (3-bit Lloyd-Max codes of the rotated unit key, then the D QJL sign bits,
- * LSB first, byte-identical to quantize_vector, :128-187) plus their f32 L2 norm, in pages of
- * 16 tokens addressed by the caller's page table, like pi_kv_pool. */
+ * ceil(4D/8)-byte records (3-bit Lloyd-Max codes of the rotated unit key, then the D QJL sign
+ * bits, LSB first, byte-identical to quantize_vector / pack_compressed, :128-187,591-617)
+ * plus their f32 L2 norm, in pages of 16 tokens addressed by the caller's page table, like
+ * pi_kv_pool. */
 typedef struct pi_tq_pool_s* pi_tq_pool;
 /* Host only: the rotation [dim][dim] and QJL matrix [dim][dim] of TurboQuant::new(bits, dim,
  * dim, seed) (:76-103: Gram-Schmidt of a SplitMix64 / Box-Muller Gaussian matrix, and a
@@ -393,7 +394,7 @@ int pi_tq_append(pi_handle h, pi_tq_pool pool, const float* d_k, const float* d_
                  const int32_t* d_page_table, int32_t max_pages, const int32_t* d_start_pos,
                  int32_t n_seq, int32_t n_tok, void* stream);
 /* The stored records of positions start .. start+n_tok-1 of sequence `seq`: keys
- * [n_tok][n_kv_heads][D/2] bytes, norms [n_tok][n_kv_heads] f32, values [n_tok][n_kv_heads][D]
+ * [n_tok][n_kv_heads][ceil(4D/8)] bytes, norms [n_tok][n_kv_heads] f32, values [n_tok][n_kv_heads][D]
  * as f16 bits. */
 int pi_tq_read(pi_handle h, pi_tq_pool pool, const int32_t* d_page_table, int32_t max_pages,
                int32_t seq, int32_t start, int32_t n_tok, uint8_t* d_keys_out, float* d_norms_out,
@@ -401,9 +402,12 @@ int pi_tq_read(pi_handle h, pi_tq_pool pool, const int32_t* d_page_table, int32_
 /* The compressed-cache branch of the decode attention (src/model/mod.rs:1161-1166:
  * attention_scores with the precomputed query, softmax, weighted_value_sum) for every query
  * head, with the optional sigmoid gate (:1192-1196).  q [batch][n_q_heads][D], out likewise;
- * modulo (PI_GQA_MODULO) or grouped head map; the score scale is 1/sqrt(D) (:490).  The
- * reference skips weights below 1e-7 in the value sum (:526-529); this path keeps every
- * weight (a difference below the 1e-7-per-token mass it drops). */
+ * modulo (PI_GQA_MODULO) or grouped head map; the score scale is 1/sqrt(D) (:490).  D = 128
+ * and 256 run the MFMA decode, which keeps every weight (the reference skips weights below
+ * 1e-7 in the value sum, :526-529: a difference below the 1e-7-per-token mass it drops);
+ * every other D runs the reference's order (all scores, the softmax, then the value sum
+ * without the weights below 1e-7), one workgroup per (sequence, query head), with a
+ * workspace of batch * n_q_heads * max_pages * 16 floats. */
 int pi_tq_attn_decode(pi_handle h, const float* d_q, pi_tq_pool pool, const int32_t* d_page_table,
                       int32_t max_pages, const int32_t* d_ctx_len, int32_t batch,
                       int32_t n_q_heads, int32_t gqa_mode, const float* d_gate, float* d_out,

@@ -389,7 +389,7 @@ def tq_dot(q, packed, R, G, bits: int, qjl_bits: int) -> float:
 
 
 def tq_cache_append_keys(keys, R, G):
-    """keys [n_kv, dim] of one token -> (packed [n_kv, 64-byte records], norms [n_kv]);
+    """keys [n_kv, dim] of one token -> (packed [n_kv, ceil(4 dim / 8)-byte records], norms [n_kv]);
     R, G [n_kv, dim, dim] (CompressedKVCache::append, :455-486)."""
     k, R, G = _f32(keys), _f32(R), _f32(G)
     n_kv, dim = k.shape

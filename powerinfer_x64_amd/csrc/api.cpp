@@ -26,8 +26,10 @@ struct pi_handle_s {
     pi::GdnWorkspace gws{};
     float* h2d_scratch = nullptr;  // device staging for the host-slice drop-ins
     size_t h2d_floats = 0;
-    float* tq_qv = nullptr;        // TurboQuant virtual queries [batch][Hq][256]
+    float* tq_qv = nullptr;        // TurboQuant virtual queries [batch][Hq][2 head_dim]
     size_t tq_qv_floats = 0;
+    float* tq_sc = nullptr;        // TurboQuant scores of the in-order decode [batch][Hq][keys]
+    size_t tq_sc_floats = 0;
     float* pfs_buf = nullptr;      // prefill key-split partials
     size_t pfs_floats = 0;
     float* pad_buf = nullptr;      // pi_attn_prefill's padded rows at a head_dim of no kernel
@@ -287,6 +289,7 @@ void pi_destroy(pi_handle h) {
     (void)hipFree(h->gws.buf);
     (void)hipFree(h->h2d_scratch);
     (void)hipFree(h->tq_qv);
+    (void)hipFree(h->tq_sc);
     (void)hipFree(h->pfs_buf);
     (void)hipFree(h->pad_buf);
     if (h->pin) (void)hipHostFree(h->pin);
@@ -1639,8 +1642,8 @@ int pi_tq_pool_create(pi_handle h, int32_t n_pages, int32_t page_tokens, int32_t
         return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_pool_create: page_tokens must be 16 (got %d)", page_tokens);
     if (n_pages <= 0 || n_kv_heads <= 0)
         return fail(h, PI_ERR_INVALID_ARG, "pi_tq_pool_create: n_pages=%d n_kv_heads=%d", n_pages, n_kv_heads);
-    if (head_dim != 128 && head_dim != 256)
-        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_pool_create: head_dim %d (128 or 256)", head_dim);
+    if (head_dim < 1 || head_dim > pi::kTqMaxDim)
+        return fail(h, PI_ERR_UNSUPPORTED, "pi_tq_pool_create: head_dim %d (1..%d)", head_dim, pi::kTqMaxDim);
     const int D = head_dim;
     const size_t nblk = (size_t)n_pages * n_kv_heads;
     const size_t kbytes = nblk * pi::kPageTokens * (pi::tq_key_bytes(D) + 4);
@@ -1769,15 +1772,27 @@ int pi_tq_attn_decode(pi_handle h, const float* d_q, pi_tq_pool pool, const int3
     hipStream_t s = pick(h, stream);
     PI_HIP(h, hipSetDevice(h->device), "pi_tq_attn_decode");
     if ((rc = ws_begin(h, s, "pi_tq_attn_decode"))) return rc;
+    const size_t need_qv = (size_t)batch * n_q_heads * 2 * g.head_dim;
+    if ((rc = grow(h, &h->tq_qv, &h->tq_qv_floats, need_qv, s, "pi_tq_attn_decode workspace", false))) return rc;
+    if (!pi::tq_mfma_dim(g.head_dim)) {
+        // the reference's order: every score, the softmax, the value sum without weights < 1e-7
+        const size_t need_sc = (size_t)batch * n_q_heads * max_pages * pi::kPageTokens;
+        if ((rc = grow(h, &h->tq_sc, &h->tq_sc_floats, need_sc, s, "pi_tq_attn_decode workspace", false)))
+            return rc;
+        PI_HIP(h, pi::launch_tq_query(pool->t, d_q, h->tq_qv, batch, n_q_heads, gqa_mode, s),
+               "pi_tq_attn_decode");
+        PI_HIP(h, pi::launch_tq_decode_any(pool->t, h->tq_qv, d_page_table, max_pages, d_ctx_len, batch,
+                                           n_q_heads, gqa_mode, d_gate, d_out, h->tq_sc, s),
+               "pi_tq_attn_decode");
+        return ws_end(h, s, "pi_tq_attn_decode");
+    }
     const pi::DecodePlan plan = pi::decode_plan(g, batch, max_pages, n_q_heads, gqa_mode, h->device);
     const size_t need_o = pi::decode_ws_floats_o(g, plan);
     const size_t need_ml = need_o / g.head_dim * 2;
-    const size_t need_qv = (size_t)batch * n_q_heads * 2 * g.head_dim;
     if ((rc = grow(h, &h->dws.partial_o, &h->dws.capacity_o, need_o, s, "pi_tq_attn_decode workspace", false))) return rc;
     if ((rc = grow(h, &h->dws.partial_ml, &h->dws.capacity_ml, need_ml, s, "pi_tq_attn_decode workspace", false))) return rc;
     if ((rc = grow(h, &h->dws.seg_runs, &h->dws.capacity_runs, pi::decode_ws_ints_runs(g, plan), s,
                    "pi_tq_attn_decode workspace", false))) return rc;
-    if ((rc = grow(h, &h->tq_qv, &h->tq_qv_floats, need_qv, s, "pi_tq_attn_decode workspace", false))) return rc;
     PI_HIP(h, pi::launch_tq_query(pool->t, d_q, h->tq_qv, batch, n_q_heads, gqa_mode, s),
            "pi_tq_attn_decode");
     // the score scale is 1/sqrt(d) (src/turboquant/mod.rs:490)

@@ -11,9 +11,13 @@ namespace pi {
 constexpr int kPageTokens = 16;  // tokens per KV page
 constexpr int kItemPages = 16;   // max pages per decode work item (the balancing unit)
 constexpr int kMaxBatch = 4096;  // sequences per decode launch (LDS prefix scan)
-constexpr int kTqDtype = 3;      // KvGeom::dtype of a TurboQuant pool (head_dim 128 or 256)
+constexpr int kTqDtype = 3;      // KvGeom::dtype of a TurboQuant pool (head_dim 1..256)
+constexpr int kTqMaxDim = 256;
 // Bytes of one packed TurboQuant key of head_dim d: 3 d code bits + d QJL sign bits.
-constexpr int tq_key_bytes(int d) { return d / 2; }
+// bytes of a TurboQuant key record: 3 code bits and 1 QJL sign bit per coordinate
+constexpr int tq_key_bytes(int d) { return (4 * d + 7) / 8; }
+// head widths whose decode runs on the MFMA tile (the others on the in-order kernels)
+constexpr bool tq_mfma_dim(int d) { return d == 128 || d == 256; }
 
 // KV pool geometry: one K and one V block of kPageTokens x head_dim elements
 // per (page, kv head).  K block layout: [head_dim/E][16 tokens][E] with
@@ -36,7 +40,7 @@ struct KvGeom {
     size_t vstride;     // bytes from one V block to the next
 };
 
-// TurboQuant compressed pool (head_dim d = 128 or 256): g.k holds per (page,
+// TurboQuant compressed pool (head_dim d = 1..256): g.k holds per (page,
 // KV head) 16 packed keys of tq_key_bytes(d) then their 16 f32 norms, g.v the
 // f16 V block [d][16]; rt / gt are the per-head rotation and QJL matrices,
 // transposed ([h][j][i] = M[h][i][j]) so that lane i reads row i coalesced.
@@ -119,9 +123,16 @@ hipError_t launch_tq_append(const TqPool& t, const float* k, const float* v,
 hipError_t launch_tq_read(const TqPool& t, const int32_t* page_table, int32_t max_pages,
                           int32_t seq, int32_t start, int32_t n_tok, uint8_t* keys_out,
                           float* norms_out, uint16_t* v_out, hipStream_t s);
-// Virtual queries [batch][n_q_heads][256] for the TurboQuant decode.
+// Virtual queries [batch][n_q_heads][2 head_dim] for the TurboQuant decode.
 hipError_t launch_tq_query(const TqPool& t, const float* q, float* qv, int32_t batch,
                            int32_t n_q_heads, int32_t gqa_mode, hipStream_t s);
+// The decode of a pool whose head_dim has no MFMA tile (tq_mfma_dim false): qv from
+// launch_tq_query ([q_rot | qjl_proj] / sqrt(d) per head row), scores a workspace of
+// batch * n_q_heads * max_pages * 16 floats.
+hipError_t launch_tq_decode_any(const TqPool& t, const float* qv, const int32_t* page_table,
+                                int32_t max_pages, const int32_t* ctx_len, int32_t batch,
+                                int32_t n_q_heads, int32_t gqa_mode, const float* gate, float* out,
+                                float* scores, hipStream_t s);
 
 struct RopeFreqs {
     float f[128];  // up to head_dim 256 -> 128 pairs

@@ -323,14 +323,14 @@ class GdnLayer:
 
 class TqPool:
     """TurboQuant compressed KV cache (CompressedKVCache, src/turboquant/mod.rs:408-566) in
-    16-token pages: head_dim/2-byte 3-bit + QJL key records with f32 norms, f16 values;
-    head_dim 128 or 256."""
+    16-token pages: ceil(head_dim/2)-byte 3-bit + QJL key records with f32 norms, f16
+    values; head_dim 1..256."""
 
     def __init__(self, dev: Device, n_pages: int, n_kv_heads: int, head_dim: int = 128,
                  page_tokens: int = PAGE_TOKENS):
         self.dev = dev
         self.n_pages, self.n_kv_heads, self.head_dim = n_pages, n_kv_heads, head_dim
-        self.KEY_BYTES = head_dim // 2
+        self.KEY_BYTES = (4 * head_dim + 7) // 8
         p = ctypes.c_void_p()
         dev.check(dev.lib.pi_tq_pool_create(dev.h, n_pages, page_tokens, n_kv_heads, head_dim,
                                             ctypes.byref(p)))
@@ -368,8 +368,8 @@ class TqPool:
                                    page_table.shape[1], _vp(start_pos), n_seq, n_tok, d.stream()))
 
     def read(self, page_table: torch.Tensor, seq: int, start: int, n_tok: int):
-        """(keys [n_tok, Hkv, head_dim/2] uint8, norms [n_tok, Hkv] f32, values [n_tok, Hkv,
-        head_dim] f16)."""
+        """(keys [n_tok, Hkv, ceil(head_dim/2)] uint8, norms [n_tok, Hkv] f32, values
+        [n_tok, Hkv, head_dim] f16)."""
         d = self.dev
         _need(page_table, "page_table", torch.int32, dev=d.torch_device)
         ko = torch.empty((n_tok, self.n_kv_heads, self.KEY_BYTES), dtype=torch.uint8,
