@@ -222,9 +222,9 @@ int pi_gdn_rmsnorm_gated(pi_handle h, float* d_o, const float* d_z, const float*
  * [batch][n_k_heads][k_hd], v [batch][n_v_heads][v_hd], beta/g [batch][n_v_heads],
  * state [batch][n_v_heads][k_hd][v_hd] f32 in/out (ssm::create_ssm_state,
  * src/ssm/mod.rs:164-166: zero-initialised by the caller), out
- * [batch][n_v_heads][v_hd] (before RMSNormGated).  Any k_hd <= 256 and v_hd, any head
+ * [batch][n_v_heads][v_hd] (before RMSNormGated).  Any k_hd <= 1024 and v_hd, any head
  * counts (V head vh reads K head vh % n_k_heads); k_hd = v_hd = 128 runs the tuned kernel,
- * other widths a per-token kernel (one wavefront per 8 state columns). */
+ * other widths a per-token kernel (one wavefront per 8 state columns, 2 above k_hd 256). */
 int pi_gdn_decode(pi_handle h, const float* d_q, const float* d_k, const float* d_v,
                   const float* d_beta, const float* d_g, float* d_state, float* d_out,
                   int32_t batch, int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd,

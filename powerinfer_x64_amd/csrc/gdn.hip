@@ -447,17 +447,17 @@ __global__ __launch_bounds__(512) void gdn_step_kernel(const float* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Any head widths (k_hd <= 256, any v_hd): the per-token recurrence of
-// src/model/mod.rs:841-916 itself, token after token.  A wavefront owns 8
-// state columns of one (sequence, V head): lane (r = lane / 8, c = lane % 8)
-// holds rows r + 8 i (i < NR) of column c0 + c in registers, so every column
-// sum (the norms, S^T k, S^T q) is a 3-step shuffle over the 8 row groups and
-// no wavefront waits for another.  The next token's q, k, v, beta and g are
+// Any head widths (k_hd <= 1024, any v_hd): the per-token recurrence of
+// src/model/mod.rs:841-916 itself, token after token.  A wavefront owns CG
+// state columns of one (sequence, V head): lane (r = lane / CG, c = lane % CG)
+// holds rows r + (64 / CG) i (i < NR) of column c0 + c in registers, so every
+// column sum (the norms, S^T k, S^T q) is a shuffle over the 64 / CG row groups
+// and no wavefront waits for another (CG 8 up to k_hd 256, CG 2 above).  The next token's q, k, v, beta and g are
 // loaded while the current one computes.  `stride` is the token pitch of the
 // q / k / v / beta / g rows: n_tok consecutive tokens of one sequence
 // (prefill), or one token of each of `batch` sequences (decode, n_tok = 1).
 // ---------------------------------------------------------------------------
-template <int NR>
+template <int NR, int CG>
 __global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict__ q,
                                                         const float* __restrict__ k,
                                                         const float* __restrict__ v,
@@ -466,11 +466,12 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict_
                                                         float* __restrict__ state,
                                                         float* __restrict__ out, int n_tok,
                                                         int hk, int hv, int dk, int dv) {
+    constexpr int RG = 64 / CG;  // row groups
     const int lane = threadIdx.x & 63;
-    const int c0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 8;
+    const int c0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * CG;
     if (c0 >= dv) return;  // a whole wavefront past the last column
     const int vh = blockIdx.y, b = blockIdx.z, kh = vh % hk;
-    const int r = lane >> 3, col = c0 + (lane & 7);
+    const int r = lane / CG, col = c0 + lane % CG;
     const bool con = col < dv;
     // token t of this (sequence, V head): rows of q / k at ((b + t) * hk + kh) * dk, ...
     const size_t sh = (size_t)b * hv + vh;
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict_
     float s[NR];
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-        const int row = r + 8 * i;
+        const int row = r + RG * i;
         s[i] = (con && row < dk) ? S[(size_t)row * dv] : 0.f;
     }
     const float qs = 1.0f / sqrtf((float)dk);
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict_
         const float* kr = k + (tok * hk + kh) * dk;
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
-            const int row = r + 8 * i;
+            const int row = r + RG * i;
             qn[i] = row < dk ? qr[row] : 0.f;
             kn[i] = row < dk ? kr[row] : 0.f;
         }
@@ -511,7 +512,7 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict_
         const float vc = vx, bc = bt, decay = expf(gx);
         if (t + 1 < n_tok) fetch(t + 1);
 #pragma unroll
-        for (int m = 8; m <= 32; m <<= 1) {
+        for (int m = CG; m <= 32; m <<= 1) {
             sq = wave_sum_xor(sq, m);
             sk = wave_sum_xor(sk, m);
         }
@@ -527,7 +528,7 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict_
             kv += s[i] * kc[i];
         }
 #pragma unroll
-        for (int m = 8; m <= 32; m <<= 1) kv = wave_sum_xor(kv, m);
+        for (int m = CG; m <= 32; m <<= 1) kv = wave_sum_xor(kv, m);
         // delta = (v - kv_mem) beta; S += k delta^T; o = S^T q (:899-916)
         const float delta = (vc - kv) * bc;
         float o = 0.f;
@@ -537,12 +538,12 @@ __global__ __launch_bounds__(256) void gdn_recur_kernel(const float* __restrict_
             o += s[i] * qc[i];
         }
 #pragma unroll
-        for (int m = 8; m <= 32; m <<= 1) o = wave_sum_xor(o, m);
+        for (int m = CG; m <= 32; m <<= 1) o = wave_sum_xor(o, m);
         if (r == 0 && con) out[(((size_t)b + t) * hv + vh) * dv + col] = o;
     }
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-        const int row = r + 8 * i;
+        const int row = r + RG * i;
         if (con && row < dk) S[(size_t)row * dv] = s[i];
     }
 }
@@ -1289,15 +1290,20 @@ hipError_t launch_gdn_recur(const float* q, const float* k, const float* v, cons
                             hipStream_t s) {
     if (k_hd <= 0 || k_hd > kGdnMaxKhd || v_hd <= 0 || (batch > 1 && n_tok != 1))
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((v_hd + 31) / 32), (unsigned)n_v_heads, (unsigned)batch);
-    const int nr = (k_hd + 7) / 8;
-#define PI_GDN_RECUR(N)                                                                           \
-    hipLaunchKernelGGL(gdn_recur_kernel<N>, grid, dim3(256), 0, s, q, k, v, beta, g, state, out, \
+    // 8 columns per wavefront (8 row groups) up to k_hd 256, then 2 (32 row groups)
+    const int cg = k_hd <= 256 ? 8 : 2;
+    const dim3 grid((unsigned)((v_hd + 4 * cg - 1) / (4 * cg)), (unsigned)n_v_heads, (unsigned)batch);
+    const int nr = (k_hd + 64 / cg - 1) / (64 / cg);
+#define PI_GDN_RECUR(N, C)                                                                           \
+    hipLaunchKernelGGL((gdn_recur_kernel<N, C>), grid, dim3(256), 0, s, q, k, v, beta, g, state, out, \
                        n_tok, n_k_heads, n_v_heads, k_hd, v_hd)
-    if (nr <= 4) PI_GDN_RECUR(4);
-    else if (nr <= 8) PI_GDN_RECUR(8);
-    else if (nr <= 16) PI_GDN_RECUR(16);
-    else PI_GDN_RECUR(32);
+    if (cg == 2) {
+        if (nr <= 16) PI_GDN_RECUR(16, 2);
+        else PI_GDN_RECUR(32, 2);
+    } else if (nr <= 4) PI_GDN_RECUR(4, 8);
+    else if (nr <= 8) PI_GDN_RECUR(8, 8);
+    else if (nr <= 16) PI_GDN_RECUR(16, 8);
+    else PI_GDN_RECUR(32, 8);
 #undef PI_GDN_RECUR
     return hipGetLastError();
 }

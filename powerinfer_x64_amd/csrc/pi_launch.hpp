@@ -214,7 +214,7 @@ hipError_t launch_gdn_step(const float* x, const float* cs_in, float* cs_out, co
                            hipStream_t s);
 // Largest key head width of the gated-DeltaNet kernels; k_hd = v_hd = 128
 // run the tuned decode / chunked kernels, other widths the per-token kernel.
-constexpr int kGdnMaxKhd = 256;
+constexpr int kGdnMaxKhd = 1024;
 hipError_t launch_gdn_decode(const float* q, const float* k, const float* v, const float* beta,
                              const float* g, float* state, float* out, int32_t batch,
                              int32_t n_k_heads, int32_t n_v_heads, int32_t k_hd, int32_t v_hd,

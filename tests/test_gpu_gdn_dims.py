@@ -1,6 +1,6 @@
 """Gated-DeltaNet at head widths other than 128 and with the token-by-token prefill
 (src/model/mod.rs:841-916 takes any k_hd / v_hd and any head counts, V head vh reading
-K head vh % n_k_heads), against the oracle's per-token recurrence: max-abs <= 2e-3 on
+K head vh % n_k_heads; here k_hd up to 1024), against the oracle's per-token recurrence: max-abs <= 2e-3 on
 outputs and on the state, as for the 128-wide kernels.
 """
 import numpy as np
@@ -13,7 +13,9 @@ from tests.gpu_util import device, to_dev
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
-DIMS = [(64, 64), (96, 80), (256, 128), (128, 200), (32, 17), (200, 128)]
+# k_hd above 256 runs with 2 state columns per wavefront (32 row groups), up to 1024
+DIMS = [(64, 64), (96, 80), (256, 128), (128, 200), (32, 17), (200, 128), (257, 40), (512, 33),
+        (1024, 16)]
 
 
 def _inputs(rng, lead, hk, hv, dk, dv):
@@ -102,8 +104,8 @@ def test_gdn_rejects_unsupported_widths_and_chunks():
     from powerinfer_x64_amd import runtime as rt
     dev = device()
     rng = np.random.default_rng(3)
-    x = _inputs(rng, (4,), 1, 1, 300, 8)
-    state = torch.zeros((1, 300, 8), device="cuda")
+    x = _inputs(rng, (4,), 1, 1, 1025, 8)
+    state = torch.zeros((1, 1025, 8), device="cuda")
     with pytest.raises(rt.Unsupported):
         rt.gdn_prefill(dev, *(to_dev(a) for a in x), state)
     x = _inputs(rng, (4,), 1, 1, 128, 128)
