@@ -168,7 +168,7 @@ int pi_attn_decode_noalloc(pi_handle h, const float* d_q, pi_kv_pool pool,
  * d_q [batch][seq_len][n_q_heads][D], d_k/d_v [batch][seq_len][n_kv_heads][D]
  * in dtype (PI_BF16 or PI_F16); d_out [batch][seq_len][n_q_heads][D] f32.
  * MFMA flash attention with fp32 softmax/accumulation.  D = head_dim is 1..256:
- * 128 and 256 run directly; another width runs zero-padded to the next of
+ * 64, 128 and 256 run directly; another width runs zero-padded to the next of
  * them (q, k, v copied into padded rows of a handle workspace, the output cut
  * back; zero dims change no q.k), at that width's cost.  Head counts as
  * pi_attn_decode. */

@@ -619,9 +619,9 @@ int pi_attn_prefill(pi_handle h, const void* d_q, const void* d_k, const void* d
     hipStream_t s = pick(h, stream);
     int rc;
     if ((rc = ws_begin(h, s, "pi_attn_prefill"))) return rc;
-    // The kernels run at 128 or 256 dims; another head_dim runs zero-padded to the next of
-    // them (zero dims change no q.k and give zero output dims; the caller's scale stands)
-    const int W = head_dim <= 128 ? 128 : 256;
+    // The kernels run at 64, 128 or 256 dims; another head_dim runs zero-padded to the next
+    // of them (zero dims change no q.k and give zero output dims; the caller's scale stands)
+    const int W = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
     const size_t need = pi::prefill_ws_floats(batch, seq_len, n_q_heads, n_kv_heads, W, causal ? 1 : 0);
     if (need && (rc = grow(h, &h->pfs_buf, &h->pfs_floats, need, s, "pi_attn_prefill workspace", false))) return rc;
     const void *q = d_q, *k = d_k, *v = d_v;

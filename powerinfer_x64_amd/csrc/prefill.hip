@@ -167,9 +167,12 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     constexpr int V_INSTR = BN * D * 2 / 1024;  // direct loads of 1 KB per V tile (16 or 32)
     constexpr int VJ = V_INSTR / NW;  // V loads per wavefront
     constexpr int VRPI = 1024 / (2 * D);  // V rows per load (4 or 2)
-    constexpr int VCPR = D / 8;       // 16-byte chunks per V row (16 or 32)
+    constexpr int VCPR = D / 8;       // 16-byte chunks per V row (8, 16 or 32)
+    // contiguous V rows: the 32-dim group of a chunk is XORed with the row's low bits (two
+    // at D >= 128, one at D = 64, whose rows hold two groups)
+    constexpr int VSW = NDT >= 4 ? 3 : 1;
     // buffer u % NB holds K of tile u and V of tile u - 1.  Contiguous source: K [key][dim] with
-    // padded rows, V [key][dim] with 2D-byte rows, chunk c of row r at c ^ 4*(r % 4).  Paged
+    // padded rows, V [key][dim] with 2D-byte rows, chunk c of row r at c ^ 4*(r % 4) (c ^ 4*(r % 2) at D = 64).  Paged
     // source, page-major like the pool's blocks: K [4 pages][D/8][16 keys][8] with key pi(s)
     // in slot s (pi swaps bits 2 and 3), V [4 pages][D][16 keys] with the 8-key halves of
     // dim d's 32-byte row swapped when bit 2 ^ bit 3 of d is set (16 consecutive dims then
@@ -318,7 +321,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     for (int j = 0; j < VJ; ++j) {
         const int i = VJ * wave + j;
         const int row = VRPI * i + lane / VCPR;
-        const int cc = (lane % VCPR) ^ (4 * (row & 3));
+        const int cc = (lane % VCPR) ^ (4 * (row & VSW));
         v_row[j] = row;
         v_off[j] = (unsigned)(((size_t)row * tok_stride + 8 * cc) * sizeof(T));
     }
@@ -499,7 +502,7 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     int voff[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
-        voff[dt] = vrow * D + 32 * (dt ^ ((jg >> 2) & 3)) + 8 * vq + 4 * (jg & 1);
+        voff[dt] = vrow * D + 32 * (dt ^ ((jg >> 2) & VSW)) + 8 * vq + 4 * (jg & 1);
     // paged: lane i of dim tile dt reads dim 32 dt + i, keys 16 ks + 8 hh .. +7 (page ks)
     const int vdl = lane & 31;
     const lds_ptr v_lane_pg = (lds_ptr)&sv[0][vdl * 16 + 8 * (hh ^ (((vdl >> 2) ^ (vdl >> 3)) & 1))];
@@ -1678,7 +1681,7 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
                           int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, int32_t causal,
                           int32_t gqa_mode, float scale, float* out, float* ws, size_t ws_floats,
                           hipStream_t s, const float* gate) {
-    if (head_dim != 128 && head_dim != 256) return hipErrorInvalidValue;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return hipErrorInvalidValue;
     if (q_off < 0 || n_keys < 1 || (causal && q_off + seq_len > n_keys)) return hipErrorInvalidValue;
     PrefillArgs a;
     a.q = q;
@@ -1712,7 +1715,8 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
         a.part_ml = ws + (size_t)sc.ksplit * rows * head_dim;
         q0 = split_plan(a, ROWS * (head_dim == 256 ? PrefillCfg<256>::NW : PrefillCfg<128>::NW) / sc.hpw);
     }
-    if (head_dim == 128) launch_d<128>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
+    if (head_dim == 64) launch_d<64>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
+    else if (head_dim == 128) launch_d<128>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
     else launch_d<256>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.ksplit == 1) return e;

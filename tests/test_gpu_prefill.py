@@ -120,12 +120,49 @@ def test_prefill_batch_of_two(causal):
         assert row_rel_err(out[bi], ref) <= 1e-2, bi
 
 
+@pytest.mark.parametrize("s,hq,hkv,dtype,causal,gqa_mode", [
+    (1, 8, 2, torch.bfloat16, True, 0), (200, 32, 8, torch.bfloat16, True, 0),
+    (513, 16, 4, torch.float16, True, 1), (300, 12, 4, torch.bfloat16, False, 0),
+    (1000, 8, 8, torch.float16, True, 0), (129, 6, 2, torch.bfloat16, True, 0)])
+def test_prefill_head_dim_64(s, hq, hkv, dtype, causal, gqa_mode):
+    """head_dim 64 on its own kernel (8 dims of a V row's two 32-dim groups swizzled by row
+    parity): every row against the oracle's per-row decode (causal) or float64 brute force."""
+    rng = np.random.default_rng(6400 + s + hq)
+    tq, tk, tv = _inputs(rng, s, hq, hkv, 64, dtype=dtype)
+    out = _run(tq, tk, tv, causal=causal, gqa_mode=gqa_mode)
+    group = hq // hkv
+    kv_of = (lambda h: h // group) if gqa_mode else (lambda h: h % hkv)
+    if causal and gqa_mode == 0:
+        ref = _oracle_rows(tq, tk, tv, range(s))
+    else:
+        qf, kf, vf = (t.float().numpy() for t in (tq, tk, tv))
+        ref = np.stack([ref64.attention(qf[i], kf[:i + 1] if causal else kf,
+                                        vf[:i + 1] if causal else vf, kv_of) for i in range(s)])
+    assert row_rel_err(out, ref) <= 1e-2
+    n, mism, ties = argmax_agreement(out, ref)
+    assert mism == 0
+
+
+@pytest.mark.parametrize("paired,ksplit", [("1", None), (None, "3")])
+def test_prefill_head_dim_64_forced_schedules(monkeypatch, paired, ksplit):
+    """D 64 under the paired schedule and a three-way key split with its merge."""
+    if paired:
+        monkeypatch.setenv("PI_PREFILL_PAIRED", paired)
+    if ksplit:
+        monkeypatch.setenv("PI_PREFILL_PAIRED", "0")
+        monkeypatch.setenv("PI_PREFILL_KSPLIT", ksplit)
+    rng = np.random.default_rng(6464)
+    tq, tk, tv = _inputs(rng, 300, 16, 4, 64)
+    out = _run(tq, tk, tv)
+    assert row_rel_err(out, _oracle_rows(tq, tk, tv, range(300))) <= 1e-2
+
+
 @pytest.mark.parametrize("d,s,dtype,causal", [
-    (64, 300, torch.bfloat16, True), (80, 200, torch.float16, True),
+    (48, 300, torch.bfloat16, True), (80, 200, torch.float16, True),
     (96, 129, torch.bfloat16, False), (192, 300, torch.bfloat16, True),
     (33, 70, torch.float16, True), (200, 150, torch.float16, False)])
 def test_prefill_padded_head_dims(d, s, dtype, causal):
-    """Head widths with no kernel of their own (run zero-padded to 128 / 256 dims), two
+    """Head widths with no kernel of their own (run zero-padded to 64 / 128 / 256 dims), two
     sequences in one launch with 8 / 2 heads: every row against the oracle's per-row
     decode (causal) or float64 brute force (no mask); scale 1/sqrt(d)."""
     from powerinfer_x64_amd import runtime as rt
