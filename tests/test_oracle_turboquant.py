@@ -123,6 +123,29 @@ def test_bit_packing_round_trip_3bit():
     assert np.array_equal(bits[384:], sg)
 
 
+def test_odd_width_record_is_the_bit_stream():
+    """At d = 33 pack_compressed (:591-617) emits ceil(4 d / 8) = 17 bytes: the 99 code bits,
+    then the signs from bit 99 on (inside byte 12), while compressed_bytes() (:111-117) counts
+    ceil(3 d / 8) + ceil(d / 8) = 18.  The oracle's quantizer writes the bit stream into an
+    18-byte record whose last byte stays zero; the device records are the 17 stream bytes."""
+    rng = np.random.default_rng(33)
+    d = 33
+    idx = rng.integers(0, 8, d).astype(np.uint8)
+    sg = rng.integers(0, 2, d).astype(np.uint8)
+    packed = o.tq_pack(idx, 3, sg)
+    assert packed.size == 17 and o.tq_compressed_bytes(3, d, d) == 18
+    bits = np.unpackbits(packed, bitorder="little")
+    assert np.array_equal(bits[0:99:3] + 2 * bits[1:99:3] + 4 * bits[2:99:3], idx)
+    assert np.array_equal(bits[99:132], sg) and not bits[132:].any()
+    R, G = o.tq_matrices(d, 7)
+    x = rng.standard_normal(d).astype(np.float32)
+    x /= np.linalg.norm(x)
+    q = o.tq_quantize(x, R, G, 3, d)
+    assert q.size == 18 and q[17] == 0
+    i2, s2 = o.tq_unpack(q[:17], d, 3, d)
+    assert np.array_equal(o.tq_pack(i2, 3, s2), q[:17])
+
+
 def test_compressed_sizes():
     # src/turboquant/mod.rs:918-951
     assert o.tq_compressed_bytes(3, 128, 128) == 64
