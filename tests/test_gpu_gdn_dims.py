@@ -100,6 +100,25 @@ def test_gdn_layer_other_widths():
     layer.close()
 
 
+def test_gdn_layer_wide_key_heads():
+    """The layer step at k_hd 384 (two state columns per wavefront of the per-token kernel),
+    v_hd 64: a prompt, a decode token and a continued chunk against the oracle's layer."""
+    from powerinfer_x64_amd import runtime as rt
+    from tests.test_gpu_gdn_layer import _OracleLayer, _inputs as layer_inputs, _weights
+    dev = device()
+    rng = np.random.default_rng(0x384)
+    hk, hv, dk, dv = 1, 2, 384, 64
+    w = _weights(rng, hk, hv, dk, dv, 4)
+    layer = rt.GdnLayer(dev, hk, hv, dk, dv, *w, eps=1e-6)
+    ref = _OracleLayer(hk, hv, dk, dv, *w, 1e-6)
+    for n in (40, 1, 9):
+        x = layer_inputs(rng, n, hk, hv, dk, dv)
+        want, tol = ref.forward(*x)
+        got = layer.forward(*x)
+        assert (np.abs(got - want) <= tol).all(), (n, float((np.abs(got - want) / tol).max()))
+    layer.close()
+
+
 def test_gdn_rejects_unsupported_widths_and_chunks():
     from powerinfer_x64_amd import runtime as rt
     dev = device()

@@ -80,6 +80,25 @@ def test_layer_qwen35_gated_d256_norm_imrope():
     _drive(layer, [100, 1, 1, 20], kw, _rel(1e-2), rng, 16, 2, 256, gate=True)
 
 
+@pytest.mark.parametrize("d,dtype", [(192, torch.float16), (96, torch.float32)])
+def test_layer_padded_width_norm_imrope(d, dtype):
+    """A key head width with no kernel of its own (run padded to 256 / 128) under the Qwen3.5
+    layer's options: per-head Q/K RMSNorm over d, IMRoPE on the first 64 dims (sections
+    [11, 11, 10, 0], base 1e7) and the sigmoid gate."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    rng = np.random.default_rng(0x1A2 + d)
+    qn = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    sec = [11, 11, 10, 0]
+    freqs = orc.compute_imrope_freqs(1e7, 64, sec)
+    layer = rt.AttnLayer(dev, 256, 16, 2, d, dtype, q_norm_w=qn, k_norm_w=kn,
+                         rope_dim=64, rope_base=1e7, sections=sec)
+    kw = dict(q_norm_w=qn, k_norm_w=kn, rope_dim=64, rope_base=1e7, freqs=freqs)
+    chk = _rel(1e-2) if dtype == torch.float16 else _abs(2e-3)
+    _drive(layer, [100, 1, 1, 20], kw, chk, rng, 16, 2, d, gate=True)
+
+
 def test_layer_llama2_mha_f32_cache():
     """32/32 heads, D 128, theta 1e4, f32 cache: max-abs <= 2e-3."""
     dev = device()

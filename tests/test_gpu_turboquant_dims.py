@@ -99,6 +99,29 @@ def test_weights_below_1e7_are_skipped():
     assert np.all(out[n:] == 0.0)
 
 
+def test_any_width_pages_outside_the_pool_hold_no_tokens():
+    """A page id outside [0, n_pages) in a sequence's table holds no tokens (as in the
+    decode of the other pools): its keys leave the softmax, the rest match the oracle over
+    the keys that remain."""
+    dev = device()
+    rng = np.random.default_rng(0x7D02)
+    d, hq, hkv = 48, 4, 2
+    case = TqCase(rng, [80], hkv, d=d)
+    case.build(dev)
+    pt = case.pt.copy()
+    pt[0, 2] = case.n_pages + 5  # tokens 32 .. 47
+    q = rng.standard_normal((1, hq, d)).astype(np.float32)
+    out = rt.tq_attn_decode(dev, to_dev(q), case.pool, to_dev(pt),
+                            to_dev(np.array([80], np.int32))).cpu().numpy()[0]
+    packed, norms, vals = case.oracle_cache(0)
+    keep = np.r_[0:32, 48:80]
+    for h in range(hq):
+        kvh = h % hkv
+        ref = o.tq_cache_attend(q[0, h], packed[keep], norms[keep], vals[keep], case.R[kvh],
+                                case.G[kvh], kvh)
+        assert row_rel_err(out[h], ref) <= 2e-5, h
+
+
 @pytest.mark.parametrize("d", [0, 257])
 def test_width_outside_range_raises(d):
     dev = device()
