@@ -408,6 +408,9 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
     // A wavefront's heads are head0, head0 + 4, ...: the rows of up to MH of them (and the V
     // rows of its K heads) are loaded before any is processed, so their loads overlap.
     constexpr int MH = 6;
+    // the norm weights (the same for every row of a kind) are read once, beside the rows
+    float qw[EPL], kw[EPL];
+    bool wl = false;
     for (int head0 = blockIdx.y * per + wv; head0 < h1; head0 += 4 * MH) {
         float xs[MH][EPL], vs[MH][EPL];
 #pragma unroll
@@ -418,6 +421,11 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
                 if (head >= hq) load_vec<EPL>(vs[m], v + (((size_t)sq * n_tok + t) * hkv + (head - hq)) * D + e0);
             }
         }
+        if (!wl) {
+            if (qn) load_vec<EPL>(qw, qn + e0);
+            if (kn) load_vec<EPL>(kw, kn + e0);
+            wl = true;
+        }
 #pragma unroll
         for (int m = 0; m < MH; ++m) {
             const int head = head0 + 4 * m;
@@ -425,19 +433,16 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
             const bool is_q = head < hq;
             const int kvh = head - hq;
             float* x = row_of(head);
-            const float* nw = is_q ? qn : kn;
             float* xv = xs[m];
-            if (nw) {  // ops::rms_norm (src/ops.rs:13-27) per head
+            if (is_q ? qn != nullptr : kn != nullptr) {  // ops::rms_norm (src/ops.rs:13-27) per head
                 float ss = 0.f;
 #pragma unroll
                 for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
 #pragma unroll
                 for (int sh = 32; sh >= 1; sh >>= 1) ss = wave_sum_xor(ss, sh);
                 const float inv = 1.0f / sqrtf(ss / (float)norm_d + eps);
-                float wv_[EPL];
-                load_vec<EPL>(wv_, nw + e0);
 #pragma unroll
-                for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * wv_[j];
+                for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * (is_q ? qw[j] : kw[j]);
             }
             // ops::apply_rope / apply_rope_with_freqs: pair i is (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
             if (neox) {
