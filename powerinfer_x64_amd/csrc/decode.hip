@@ -585,6 +585,15 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     // dependent memory round trips, so every load that can is issued beside another.
     const int ctx = p.ctx_len[b];
     const int wg1 = ws.seg_runs[2 * seg], n_runs_raw = ws.seg_runs[2 * seg + 1];
+    // the gate of wavefront 0's outputs too (it needs no merged value)
+    const int e = e0 + V * lane;
+    const bool on = e < GD;  // GD is a multiple of 4 (D >= 64)
+    VT gt = VT{};
+    if (p.gate && wave == 0 && on) {
+        const int c = e / D, d = e - c * D;
+        const int h = seg_head(p, sidx, c, n_kv);
+        if (h >= 0) gt = *reinterpret_cast<const VT*>(p.gate + ((size_t)b * p.n_q_heads + h) * D + d);
+    }
     if (sched::seq_tokens(ctx, p.max_pages) == 0) {
         // empty context: softmax over nothing leaves zeros (src/ops.rs:161)
         const int idx = e0 + tid;
@@ -604,8 +613,6 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     // thread (wave, lane): values e0 + 4 lane .. +3 of runs wave, wave + 4, ...; the first
     // kPre of those runs are loaded now, beside the (max, sum) pairs, before any weight is known
     constexpr int kPre = 4;
-    const int e = e0 + V * lane;
-    const bool on = e < GD;  // GD is a multiple of 4 (D >= 64)
     const float* po = ws.partial_o + (on ? e : 0);
     auto part = [&](int r) { return *reinterpret_cast<const VT*>(po + (size_t)s_slot[r] * GD); };
     const VT zero = VT{};
@@ -667,7 +674,6 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p, Decod
     const size_t oi = ((size_t)b * p.n_q_heads + h) * D + d;
     VT res = acc * inv;
     if (p.gate) {
-        const VT gt = *reinterpret_cast<const VT*>(p.gate + oi);
         float* rp = reinterpret_cast<float*>(&res);
         const float* gp = reinterpret_cast<const float*>(&gt);
 #pragma unroll

@@ -353,6 +353,12 @@ __global__ __launch_bounds__(512) void gdn_step_kernel(const float* __restrict__
         n2 = x[c1];
     }
     const float braw = beta_raw[vh], araw = a_raw[vh], dtb = dt_bias[vh], sa = ssm_a[vh];
+    // z and the norm weights of the RMSNormGated (wavefront 0 applies it) load here too
+    f32x4 zv = {0.f, 0.f, 0.f, 0.f}, nw = zv;
+    if (wave == 0 && lane < 32) {
+        zv = *reinterpret_cast<const f32x4*>(z + (size_t)vh * DV + 4 * cg);
+        nw = *reinterpret_cast<const f32x4*>(norm_w + 4 * cg);
+    }
     f32x4 s[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) s[i] = *reinterpret_cast<const f32x4*>(S + (size_t)(rr + 16 * i) * DV);
@@ -437,8 +443,6 @@ __global__ __launch_bounds__(512) void gdn_step_kernel(const float* __restrict__
 #pragma unroll
         for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
         const float sc = 1.0f / sqrtf(ss / (float)DV + eps);
-        const f32x4 zv = *reinterpret_cast<const f32x4*>(z + (size_t)vh * DV + 4 * cg);
-        const f32x4 nw = *reinterpret_cast<const f32x4*>(norm_w + 4 * cg);
         f32x4 r;
 #pragma unroll
         for (int e = 0; e < 4; ++e) r[e] = (o[e] * sc * nw[e]) * (zv[e] / (1.0f + expf(-zv[e])));
