@@ -228,9 +228,10 @@ struct PrologueStart {
     int32_t scalar;
     int32_t* ctx_out;
     int32_t n_ctx;
+    int32_t wg0;  // the workgroup (x) that writes ctx_out: the first token workgroup
     __device__ __forceinline__ int of(int sq) const { return dev ? dev[sq] : scalar; }
     __device__ __forceinline__ void write_ctx() const {
-        if (ctx_out && blockIdx.x == 0 && blockIdx.y == 0)
+        if (ctx_out && (int)blockIdx.x == wg0 && blockIdx.y == 0)
             for (int i = threadIdx.x; i < n_ctx; i += blockDim.x) ctx_out[i] = scalar + 1 + i;
     }
 };
@@ -362,24 +363,190 @@ __device__ __forceinline__ void store_vec(float* d, const float* s) {
     }
 }
 
+// One head row held EPL values a lane (element e0 + j of lane l, e0 = EPL l): RMS-normed
+// with the weights w (none: no norm) and rotated; cos_sin(i, &c, &s) gives pair i's angle.
+template <int EPL, typename CS>
+__device__ __forceinline__ void norm_rope_row(float* xv, bool has_w, const float* w, float eps,
+                                              int norm_d, int n_pairs, int neox, int lane,
+                                              CS cos_sin) {
+    const int e0 = EPL * lane;
+    if (has_w) {  // ops::rms_norm (src/ops.rs:13-27) per head
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) ss = wave_sum_xor(ss, sh);
+        const float inv = 1.0f / sqrtf(ss / (float)norm_d + eps);
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * w[j];
+    }
+    // ops::apply_rope / apply_rope_with_freqs: pair i is (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
+    if (neox) {
+        const int off = n_pairs / EPL;  // lanes between the two elements of a pair
+        const int src = lane < off ? lane + off : lane - off;
+        float pv[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) pv[j] = __shfl(xv[j], src < 64 ? src : lane, 64);
+        if (lane < 2 * off) {
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                const bool first = lane < off;
+                const int i = first ? e0 + j : e0 + j - n_pairs;
+                float c, sn;
+                cos_sin(i, &c, &sn);
+                xv[j] = first ? xv[j] * c - pv[j] * sn : pv[j] * sn + xv[j] * c;
+            }
+        }
+    } else if constexpr (EPL >= 2) {
+#pragma unroll
+        for (int j = 0; j < EPL; j += 2) {
+            const int i = (e0 + j) >> 1;
+            if (i < n_pairs) {
+                float c, sn;
+                cos_sin(i, &c, &sn);
+                const float x0 = xv[j], x1 = xv[j + 1];
+                xv[j] = x0 * c - x1 * sn;
+                xv[j + 1] = x0 * sn + x1 * c;
+            }
+        }
+    } else {
+        const float pv0 = __shfl_xor(xv[0], 1, 64);
+        const int i = e0 >> 1;
+        if (i < n_pairs) {
+            float c, sn;
+            cos_sin(i, &c, &sn);
+            xv[0] = (lane & 1) ? pv0 * sn + xv[0] * c : xv[0] * c - pv0 * sn;
+        }
+    }
+}
+
+// The K / V side of a prompt launch, one workgroup per (16-position page, K head): the
+// K head's rows of the launch's tokens on page lp = floor(start / 16) + j (the launch's
+// first and last pages may also hold positions outside it, left alone) are RMS-normed,
+// rotated at their positions and written back in f32, and their K and V values go to
+// the page's blocks through LDS as whole 16-byte chunks.  Per token, K's values lie in
+// 16-byte chunks 256 bytes apart and V's are single elements 32 bytes apart, which as
+// per-token writes cost a prompt a quarter of its prologue.  pw = workgroup index
+// among the page workgroups, ppn = pages a sequence's launch can touch.  The blocks and
+// the cos / sin table live in the launch's dynamic LDS (prologue_page_lds bytes).
+extern __shared__ __attribute__((aligned(16))) unsigned char pi_prologue_dyn[];
+template <typename PT, int EPL>
+__device__ __forceinline__ void prologue_page(float* __restrict__ k, const float* __restrict__ v,
+                                              const float* __restrict__ kn, float eps,
+                                              const RopeFreqs& f, int n_pairs, int neox,
+                                              const KvGeom& g, const int32_t* __restrict__ pt,
+                                              int max_pages, const PrologueStart& start_pos,
+                                              int n_tok, int norm_d, int pw, int ppn) {
+    constexpr int D = 64 * EPL;
+    constexpr int E = 16 / (int)sizeof(PT);  // pool values per 16-byte chunk
+    typedef PT pv __attribute__((ext_vector_type(E)));
+    PT* kb_s = reinterpret_cast<PT*>(pi_prologue_dyn);  // the K block
+    PT* vb_s = kb_s + kPageTokens * D;                  // the V block
+    float* cs_c = reinterpret_cast<float*>(vb_s + kPageTokens * D);  // cos [slot][pair]
+    float* cs_n = cs_c + kPageTokens * n_pairs;                       // sin
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int hkv = g.n_kv_heads;
+    const int sq = pw / (ppn * hkv), rem = pw % (ppn * hkv);
+    const int j = rem / hkv, h = rem % hkv;
+    const int start = start_pos.of(sq);
+    const int p0 = start >= 0 ? start / kPageTokens : -((kPageTokens - 1 - start) / kPageTokens);
+    const int lp = p0 + j, pa = lp * kPageTokens;
+    const int t0 = max(start, pa), t1 = min(start + n_tok, pa + kPageTokens);
+    if (t0 >= t1) return;  // uniform: no position of the launch on this page
+    const int s0 = t0 - pa, s1 = t1 - pa;  // the launch's slots [s0, s1)
+    const int page = lp >= 0 && lp < max_pages ? pt[(size_t)sq * max_pages + lp] : -1;
+    const bool app = page >= 0 && page < g.n_pages;  // uniform
+    const int e0 = EPL * lane;
+    // this wavefront's slots s0 + wv + 4 m: the rows and the norm weights first
+    float xs[4][EPL], vs[4][EPL], kw[EPL];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int sl = s0 + wv + 4 * m;
+        if (sl < s1) {
+            const size_t row = (((size_t)sq * n_tok + (pa + sl - start)) * hkv + h) * D + e0;
+            load_vec<EPL>(xs[m], k + row);
+            load_vec<EPL>(vs[m], v + row);
+        }
+    }
+    if (kn) load_vec<EPL>(kw, kn + e0);
+    for (int i = threadIdx.x; i < (s1 - s0) * n_pairs; i += 256) {
+        const int sl = s0 + i / n_pairs, pr = i % n_pairs;
+        const float theta = (float)(pa + sl) * f.f[pr];
+        cs_c[sl * n_pairs + pr] = cosf(theta);
+        cs_n[sl * n_pairs + pr] = sinf(theta);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int sl = s0 + wv + 4 * m;
+        if (sl >= s1) break;
+        float* xv = xs[m];
+        norm_rope_row<EPL>(xv, kn != nullptr, kw, eps, norm_d, n_pairs, neox, lane,
+                           [&](int i, float* c, float* sn) {
+                               *c = cs_c[sl * n_pairs + i];
+                               *sn = cs_n[sl * n_pairs + i];
+                           });
+        store_vec<EPL>(k + (((size_t)sq * n_tok + (pa + sl - start)) * hkv + h) * D + e0, xv);
+        if (app) {
+#pragma unroll
+            for (int jj = 0; jj < EPL; ++jj) {
+                kb_s[k_index<PT>(sl, e0 + jj)] = from_f32<PT>(xv[jj]);
+                vb_s[v_index(sl, e0 + jj)] = from_f32<PT>(vs[m][jj]);
+            }
+        }
+    }
+    if (!app) return;  // uniform
+    __syncthreads();
+    const size_t blk = (size_t)page * hkv + h;
+    PT* kp = reinterpret_cast<PT*>(static_cast<char*>(g.k) + blk * g.kstride);
+    PT* vp = reinterpret_cast<PT*>(static_cast<char*>(g.v) + blk * g.vstride);
+    // K block [D / E][16][E]: chunk c = (dims E (c / 16) .., slot c % 16)
+    for (int c = threadIdx.x; c < D / E * kPageTokens; c += 256) {
+        const int slot = c % kPageTokens;
+        if (slot >= s0 && slot < s1) *reinterpret_cast<pv*>(kp + (size_t)E * c) = *reinterpret_cast<const pv*>(kb_s + E * c);
+    }
+    // V block [D][16]: chunk c = (dim c / (16 / E), slots E (c % (16 / E)) ..)
+    constexpr int CPR = kPageTokens / E;  // chunks per dim row
+    for (int c = threadIdx.x; c < D * CPR; c += 256) {
+        const int sl0 = E * (c % CPR);
+        if (sl0 + E <= s0 || sl0 >= s1) continue;
+        if (sl0 >= s0 && sl0 + E <= s1) {
+            *reinterpret_cast<pv*>(vp + (size_t)E * c) = *reinterpret_cast<const pv*>(vb_s + E * c);
+        } else {  // a chunk the launch covers in part: its own slots only
+            for (int e = 0; e < E; ++e)
+                if (sl0 + e >= s0 && sl0 + e < s1) vp[(size_t)E * c + e] = vb_s[E * c + e];
+        }
+    }
+}
+
 template <typename PT, int EPL>
 __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
     float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ qn, const float* __restrict__ kn, float eps, RopeFreqs f,
     int n_pairs, int neox, KvGeom g, const int32_t* __restrict__ pt, int max_pages,
-    PrologueStart start_pos, int n_seq, int n_tok, int hq, int norm_d) {
+    PrologueStart start_pos, int n_seq, int n_tok, int hq, int norm_d, int ppn) {
     constexpr int D = 64 * EPL;
     __shared__ float cs_s[2][128];  // cos, sin of pair i at this token's position
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int hkv = g.n_kv_heads, heads = hq + hkv;
+    // ppn > 0: the first n_seq * ppn * n_kv_heads workgroups take the K / V side by page
+    // (dispatched first, so they run beside the token workgroups), and the token workgroups
+    // after them only the q heads
+    const int toks = n_seq * n_tok;
+    const int n_pg = ppn > 0 ? n_seq * ppn * g.n_kv_heads : 0;
+    if ((int)blockIdx.x < n_pg) {
+        prologue_page<PT, EPL>(k, v, kn, eps, f, n_pairs, neox, g, pt, max_pages, start_pos, n_tok,
+                               norm_d, (int)blockIdx.x, ppn);
+        return;
+    }
+    const int hkv = g.n_kv_heads, heads = ppn > 0 ? hq : hq + hkv;
     const bool table = gridDim.y == 1;  // uniform per launch: the token remap below
     // A prompt launch keeps each run of 16 consecutive tokens (a page of K and V when
     // the prompt starts on a page) on one XCD: workgroups are dispatched round-robin
     // over the 8 XCDs, and workgroup 8 (16 g + i) + x takes token 128 g + 16 x + i, so
     // the partial-line writes of the page's 2-byte K / V values merge in that XCD's L2
     // instead of reaching HBM from eight caches.
-    int u = blockIdx.x;
-    if (table && u < (int)(gridDim.x / 128) * 128) {
+    int u = (int)blockIdx.x - n_pg;
+    if (table && u < toks / 128 * 128) {
         const int x = u & 7, m = u >> 3;
         u = (m >> 4) * 128 + x * 16 + (m & 15);
     }
@@ -434,54 +601,8 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
             const int kvh = head - hq;
             float* x = row_of(head);
             float* xv = xs[m];
-            if (is_q ? qn != nullptr : kn != nullptr) {  // ops::rms_norm (src/ops.rs:13-27) per head
-                float ss = 0.f;
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
-#pragma unroll
-                for (int sh = 32; sh >= 1; sh >>= 1) ss = wave_sum_xor(ss, sh);
-                const float inv = 1.0f / sqrtf(ss / (float)norm_d + eps);
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * (is_q ? qw[j] : kw[j]);
-            }
-            // ops::apply_rope / apply_rope_with_freqs: pair i is (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
-            if (neox) {
-                const int off = n_pairs / EPL;  // lanes between the two elements of a pair
-                const int src = lane < off ? lane + off : lane - off;
-                float pv[EPL];
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) pv[j] = __shfl(xv[j], src < 64 ? src : lane, 64);
-                if (lane < 2 * off) {
-#pragma unroll
-                    for (int j = 0; j < EPL; ++j) {
-                        const bool first = lane < off;
-                        const int i = first ? e0 + j : e0 + j - n_pairs;
-                        float c, sn;
-                        cos_sin(i, &c, &sn);
-                        xv[j] = first ? xv[j] * c - pv[j] * sn : pv[j] * sn + xv[j] * c;
-                    }
-                }
-            } else if constexpr (EPL >= 2) {
-#pragma unroll
-                for (int j = 0; j < EPL; j += 2) {
-                    const int i = (e0 + j) >> 1;
-                    if (i < n_pairs) {
-                        float c, sn;
-                        cos_sin(i, &c, &sn);
-                        const float x0 = xv[j], x1 = xv[j + 1];
-                        xv[j] = x0 * c - x1 * sn;
-                        xv[j + 1] = x0 * sn + x1 * c;
-                    }
-                }
-            } else {
-                const float pv0 = __shfl_xor(xv[0], 1, 64);
-                const int i = e0 >> 1;
-                if (i < n_pairs) {
-                    float c, sn;
-                    cos_sin(i, &c, &sn);
-                    xv[0] = (lane & 1) ? pv0 * sn + xv[0] * c : xv[0] * c - pv0 * sn;
-                }
-            }
+            norm_rope_row<EPL>(xv, is_q ? qn != nullptr : kn != nullptr, is_q ? qw : kw, eps, norm_d,
+                               n_pairs, neox, lane, cos_sin);
             store_vec<EPL>(x + e0, xv);
             // append-then-attend (src/model/mod.rs:1140-1146): K (normed, rotated) and V at pos
             const int lp = pos / kPageTokens;
@@ -583,7 +704,7 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
     if (!start_pos && n_seq != 1) return hipErrorInvalidValue;
     const int norm_d = norm_dim > 0 ? norm_dim : g.head_dim;
     if (norm_d > g.head_dim) return hipErrorInvalidValue;
-    const PrologueStart sp{start_pos, start_scalar, ctx_out, ctx_out ? n_ctx : 0};
+    const PrologueStart sp{start_pos, start_scalar, ctx_out, ctx_out ? n_ctx : 0, 0};
     const long long toks = (long long)n_seq * n_tok;
     if (toks <= 0) return hipSuccess;
     if (toks > 0x7fffffffLL || n_pairs > 128) return hipErrorInvalidValue;
@@ -596,10 +717,24 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
                            (uintptr_t)k_norm_w) & amask) == 0;
     if ((g.head_dim == 64 || g.head_dim == 128 || g.head_dim == 256) && (!neox || n_pairs % epl == 0) &&
         2 * n_pairs <= g.head_dim && aligned && use_vec_prologue()) {
-#define PI_PROLOGUE_VEC(PT, E)                                                                     \
-    hipLaunchKernelGGL((attn_prologue_vec_kernel<PT, E>), grid, dim3(256), 0, s, q, k, v, q_norm_w, \
-                       k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages, sp,           \
-                       n_seq, n_tok, n_q_heads, norm_d)
+        // A prompt of 1024+ tokens (one workgroup per token, its cos / sin table shared by the
+        // heads) takes the K / V side by page: one more workgroup per (page a sequence's
+        // launch can touch, K head), the token workgroups keeping the q heads.
+        const bool by_page = toks >= 1024 && n_tok >= kPageTokens;
+        const int ppn = by_page ? (n_tok + kPageTokens - 1) / kPageTokens + 1 : 0;
+        const long long n_pg = by_page ? (long long)n_seq * ppn * g.n_kv_heads : 0;
+        if (toks + n_pg > 0x7fffffffLL) return hipErrorInvalidValue;
+        const dim3 grid_v((unsigned)(toks + n_pg), grid.y);
+        PrologueStart spv = sp;
+        spv.wg0 = (int32_t)n_pg;
+        // the page workgroups' K and V blocks and cos / sin table
+        const size_t lds = by_page ? (size_t)2 * kPageTokens * g.head_dim * (g.dtype == 1 ? 2 : 4) +
+                                         (size_t)2 * kPageTokens * n_pairs * sizeof(float)
+                                   : 0;
+#define PI_PROLOGUE_VEC(PT, E)                                                                       \
+    hipLaunchKernelGGL((attn_prologue_vec_kernel<PT, E>), grid_v, dim3(256), lds, s, q, k, v,       \
+                       q_norm_w, k_norm_w, eps, freqs, n_pairs, neox, g, page_table, max_pages, spv, \
+                       n_seq, n_tok, n_q_heads, norm_d, ppn)
         const bool hp = g.dtype == 1;
         switch (epl) {
             case 1: if (hp) PI_PROLOGUE_VEC(f16, 1); else PI_PROLOGUE_VEC(float, 1); break;

@@ -134,6 +134,74 @@ def test_kv_append_page_edges(pool_dtype, d):
         np.testing.assert_array_equal(vo.cpu().numpy()[written], want_v[written])
 
 
+@pytest.mark.parametrize("pool_dtype,d,mode", [(torch.float16, 256, "imrope"),
+                                              (torch.float16, 128, "norm"),
+                                              (torch.float32, 64, "norm")])
+def test_prologue_prompt_appends_by_page(pool_dtype, d, mode):
+    """A launch of 2 x 1030 tokens, enough for the K / V side to run by page: sequence 0
+    starts inside a page (7) and sequence 1 below 0 (-20: those positions are dropped), both
+    run past a 60-page table (positions >= 960 dropped), and one page id of sequence 0 lies
+    outside the pool. q and k come back normed and rotated at every position (against the
+    oracle where the position is >= 0); every slot the launch owns holds its K / V, every
+    other slot keeps what an earlier append put there."""
+    rt = _rt()
+    dev = device()
+    rng = np.random.default_rng(0xB1 + d)
+    n_seq, n, hq, hkv, mp, n_pages = 2, 1030, 4, 2, 60, 130
+    starts = [7, -20]
+    cap = 16 * mp
+    table = rng.permutation(n_pages)[:2 * mp].reshape(2, mp).astype(np.int32)
+    table[0, 10] = n_pages + 3  # positions 160 .. 175 of sequence 0 have no page
+    pool = rt.KvPool(dev, n_pages, hkv, d, dtype=pool_dtype)
+    pt = to_dev(table)
+    # earlier contents of every slot
+    k0 = rng.standard_normal((n_seq, cap, hkv, d)).astype(np.float32)
+    v0 = rng.standard_normal((n_seq, cap, hkv, d)).astype(np.float32)
+    pool.append(to_dev(k0), to_dev(v0), pt, to_dev(np.zeros(n_seq, np.int32)))
+    q = rng.standard_normal((n_seq, n, hq, d)).astype(np.float32)
+    k = rng.standard_normal((n_seq, n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n_seq, n, hkv, d)).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    if mode == "norm":
+        kw = dict(rope_dim=d, rope_base=1e6)
+        sec, freqs = None, None
+    else:
+        sec = [11, 11, 10, 0]
+        kw = dict(rope_dim=64, rope_base=1e7)
+        freqs = orc.compute_imrope_freqs(1e7, 64, sec)
+    tq, tk = to_dev(q), to_dev(k)
+    rt.attn_prologue(dev, tq, tk, to_dev(v), pool, pt, to_dev(np.array(starts, np.int32)),
+                     q_norm_w=to_dev(qn), k_norm_w=to_dev(kn), eps=1e-6, sections=sec, **kw)
+    torch.cuda.synchronize()
+    gq, gk = tq.cpu().numpy(), tk.cpu().numpy()
+    rk = np.zeros_like(k)
+    for s_ in range(n_seq):
+        t0 = max(0, -starts[s_])  # first token at a position >= 0
+        eq, ek = orc.attn_prepare(q[s_, t0:], k[s_, t0:], hq, hkv, d, q_norm_w=qn, k_norm_w=kn,
+                                  eps=1e-6, freqs=freqs, pos0=starts[s_] + t0, **kw)
+        np.testing.assert_allclose(gq[s_, t0:], eq, atol=2e-5, rtol=0)
+        np.testing.assert_allclose(gk[s_, t0:], ek, atol=2e-5, rtol=0)
+        rk[s_, t0:] = gk[s_, t0:]
+    for s_ in range(n_seq):
+        want_k = k0[s_].copy()
+        want_v = v0[s_].copy()
+        for t in range(n):
+            p = starts[s_] + t
+            if 0 <= p < cap:
+                want_k[p] = rk[s_, t]
+                want_v[p] = v[s_, t]
+        if s_ == 0:
+            want_k[160:176] = 0.0  # read back through an id outside the pool: zeros
+            want_v[160:176] = 0.0
+        ko, vo = pool.read(pt, s_, 0, cap)
+        torch.cuda.synchronize()
+        rd = lambda a: torch.from_numpy(a).to(pool_dtype).float().numpy()  # noqa: E731
+        np.testing.assert_array_equal(vo.cpu().numpy(), rd(want_v))
+        # K: the stored value is the device's rotated k rounded to the pool's type
+        np.testing.assert_array_equal(ko.cpu().numpy(), rd(want_k))
+
+
 def test_pool_rejects_bad_shapes():
     rt = _rt()
     dev = device()
