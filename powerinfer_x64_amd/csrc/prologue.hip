@@ -534,8 +534,9 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
     const int toks = n_seq * n_tok;
     const int n_pg = ppn > 0 ? n_seq * ppn * g.n_kv_heads : 0;
     if ((int)blockIdx.x < n_pg) {
-        prologue_page<PT, EPL>(k, v, kn, eps, f, n_pairs, neox, g, pt, max_pages, start_pos, n_tok,
-                               norm_d, (int)blockIdx.x, ppn);
+        if (blockIdx.y == 0)  // launches that split the token's heads over y: one copy
+            prologue_page<PT, EPL>(k, v, kn, eps, f, n_pairs, neox, g, pt, max_pages, start_pos,
+                                   n_tok, norm_d, (int)blockIdx.x, ppn);
         return;
     }
     const int hkv = g.n_kv_heads, heads = ppn > 0 ? hq : hq + hkv;
@@ -717,10 +718,10 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
                            (uintptr_t)k_norm_w) & amask) == 0;
     if ((g.head_dim == 64 || g.head_dim == 128 || g.head_dim == 256) && (!neox || n_pairs % epl == 0) &&
         2 * n_pairs <= g.head_dim && aligned && use_vec_prologue()) {
-        // A prompt of 1024+ tokens (one workgroup per token, its cos / sin table shared by the
-        // heads) takes the K / V side by page: one more workgroup per (page a sequence's
-        // launch can touch, K head), the token workgroups keeping the q heads.
-        const bool by_page = toks >= 1024 && n_tok >= kPageTokens;
+        // A launch of 16+ tokens a sequence takes the K / V side by page: one more workgroup
+        // per (page a sequence's launch can touch, K head), the token workgroups keeping the
+        // q heads.
+        const bool by_page = n_tok >= kPageTokens;
         const int ppn = by_page ? (n_tok + kPageTokens - 1) / kPageTokens + 1 : 0;
         const long long n_pg = by_page ? (long long)n_seq * ppn * g.n_kv_heads : 0;
         if (toks + n_pg > 0x7fffffffLL) return hipErrorInvalidValue;
