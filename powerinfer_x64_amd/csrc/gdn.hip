@@ -938,10 +938,11 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
     }  // chunks
 }
 
-// gdn_scan_kernel: 8 wavefronts walk the chunks in order for one (V head, 16
-// state columns).  Waves 0-3 own the K side (K.S, R, Delta) and waves 4-7 the
-// Q side (Q.S, O) of chunk row block w % 4; the state update is split over all
-// 8 (16 state rows each).
+// gdn_scan_kernel: 8 compute wavefronts walk the chunks in order for one (V
+// head, 16 state columns), beside 4 loader wavefronts (data movement, below).
+// Waves 0-3 own the K side (K.S, R, Delta) and waves 4-7 the Q side (Q.S, O)
+// of chunk row block w % 4; the state update is split over all 8 (16 state
+// rows each).
 //
 // Precision: the state S stays in f32 in registers (wave w holds rows
 // 16w..16w+15 of S^T in the MFMA C layout).  The K.S, Q.S and K^T.Dp
@@ -952,13 +953,16 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
 //
 // Data movement: chunk n+1's q, k, T and M tiles (64 KB) arrive in the other
 // half of a double buffer by direct global -> LDS loads while chunk n
-// computes, issued by each wave group in the phase where it would otherwise
-// wait (Q side in phase 2, K side in phase 3); K^T comes from transposing
+// computes.  Four more wavefronts (8-11) issue them, one tile each, at the
+// start of the chunk and wait for them before its last barrier: the 64
+// load instructions a chunk takes keep the CU's address unit busy for about
+// a thousand cycles, and a compute wave that issued them would stall behind
+// that queue on the chunk's dependent chain.  K^T comes from transposing
 // reads of the k tile.  The small per-chunk loads are unmasked (clamped), so
 // no compiler-inserted wait lands inside a phase.
 constexpr int KT_ = GC + 16;  // f16 row stride of the [16][64] R^T, Delta^T tiles (160 B, as KH_)
 
-__global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__ q,
+__global__ __launch_bounds__(768) void gdn_scan_kernel(const float* __restrict__ q,
                                                        const float* __restrict__ k,
                                                        const float* __restrict__ v,
                                                        const float* __restrict__ beta,
@@ -994,6 +998,71 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     const int n_chunks = (n_tok + GC - 1) / GC;
     float* S = state + (size_t)vh * DK * DV;
 
+    // Direct loads (16 bytes per lane; lane i lands at base + 16 i), issued
+    // from inline assembly so that the compiler adds no waits before LDS
+    // reads; M0 (the LDS destination) is saved and restored.
+    typedef __attribute__((address_space(3))) void lds_void;
+    auto dma16s = [](const void* base, unsigned voff, lds_void* dst) {
+        const unsigned lds = (unsigned)(uintptr_t)dst;
+        unsigned saved;
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+                     "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(voff), "s"(base), "s"(lds) : "memory");
+    };
+    if (wave >= 8) {
+        // loader wave: tile lt (0 q, 1 k, 2 T pair, 3 M pair) of every chunk,
+        // 16 loads of 1 KB: q / k rows 4 j + lane / 16, T / M rows 8 j +
+        // lane / 8 of the [128][64] hi / lo pair
+        const int lt = wave - 8;
+        unsigned doff[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (lt < 2) {
+                const int r = 4 * j + (lane >> 4), c = (lane & 15) ^ (r & 15);
+                doff[j] = (unsigned)((r * DK + 8 * c) * 2);
+            } else {
+                const int r = 8 * j + (lane >> 3), rr = r & 63, c = (lane & 7) ^ ((rr >> 1) & 7);
+                doff[j] = (unsigned)(((r >> 6) * GC * GC + rr * GC + 8 * c) * 2);
+            }
+        }
+        auto issue = [&](int n, int j0, int j1) {
+            const int b = n & 1;
+            const size_t qb = ((size_t)n * hk + kh) * GC * DK;
+            const size_t tb = ((size_t)n * hv + vh) * GC * GC * 2;  // f16 elements of a T / M pair
+            const f16* tm = reinterpret_cast<const f16*>(w.tm);
+            const f16* mm = reinterpret_cast<const f16*>(w.mm);
+            const f16* src = lt == 0 ? w.q16 + qb : lt == 1 ? w.k16 + qb : lt == 2 ? tm + tb : mm + tb;
+            f16* dst = lt == 0 ? sq_[b] : lt == 1 ? sk_[b] : lt == 2 ? st_[b] : sm_[b];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (j >= j0 && j < j1) dma16s(src, doff[j], (lds_void*)&dst[512 * j]);
+        };
+        // The same barriers as the compute waves: one before the chunk loop,
+        // three per chunk.  Chunk n+1's buffer held chunk n-1's tiles, last
+        // read before chunk n-1's final barrier.  A wave's 16 loads take about
+        // a third of a chunk to issue (the CU's address unit is shared by the
+        // four loaders), so they are spread over the chunk's three phases
+        // instead of holding the first barrier.
+        // The M tile's buffer holds chunk n-1's M until the Q side has formed
+        // that chunk's O in phase 1 of chunk n, so M loads wait for the first
+        // barrier.
+        const int j1 = lt == 3 ? 0 : 6, j2 = lt == 3 ? 8 : 11;
+        issue(0, 0, 16);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        for (int n = 0; n < n_chunks; ++n) {
+            const bool more = n + 1 < n_chunks;
+            if (more) issue(n + 1, 0, j1);
+            __syncthreads();
+            if (more) issue(n + 1, j1, j2);
+            __syncthreads();
+            if (more) issue(n + 1, j2, 16);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+        return;
+    }
+
     // master state: sv[r] = S^T[c = 4 g4 + r][dim = row0 + ln] (MFMA C layout)
     f32x4 sv;
 #pragma unroll
@@ -1008,51 +1077,6 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     };
     put_state();
 
-    // Direct loads (16 bytes per lane; lane i lands at base + 16 i), issued
-    // from inline assembly so that the compiler adds no waits before LDS
-    // reads; M0 (the LDS destination) is saved and restored.  Wave w issues
-    // loads 8w .. 8w+7 of a chunk: 0-15 q, 16-31 k (4 rows each), 32-47 T,
-    // 48-63 M (8 rows each).
-    typedef __attribute__((address_space(3))) void lds_void;
-    auto dma16s = [](const void* base, unsigned voff, lds_void* dst) {
-        const unsigned lds = (unsigned)(uintptr_t)dst;
-        unsigned saved;
-        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
-                     "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-                     : "=&s"(saved) : "v"(voff), "s"(base), "s"(lds) : "memory");
-    };
-    // this lane's source byte offset within its tile for each of its 8 loads;
-    // the Q-side waves load q and k (in phase 2, where they are idle), the
-    // K-side waves T and M (in phase 3)
-    const int lw = kside ? 4 + wave : wave - 4;
-    unsigned doff[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int i = 8 * lw + j, ti = i & 15;
-        if (i < 32) {  // q or k: rows 4 ti + lane / 16
-            const int r = 4 * ti + (lane >> 4), c = (lane & 15) ^ (r & 15);
-            doff[j] = (unsigned)((r * DK + 8 * c) * 2);
-        } else {       // T or M hi / lo: rows 8 ti' + lane / 8 of the [128][64] pair
-            const int r = 8 * ti + (lane >> 3), rr = r & 63, c = (lane & 7) ^ ((rr >> 1) & 7);
-            doff[j] = (unsigned)(((r >> 6) * GC * GC + rr * GC + 8 * c) * 2);
-        }
-    }
-    // A wave's 8 loads all come from one tile (lw / 2: q, k, T pair, M pair),
-    // so the source and LDS bases are picked once per call (wave-uniform
-    // selects) and the loads issue back to back, without branches between.
-    const int ltile = lw >> 1;
-    auto issue = [&](int n, int j0 = 0, int j1 = 8) {
-        const int b = n & 1;
-        const size_t qb = ((size_t)n * hk + kh) * GC * DK;
-        const size_t tb = ((size_t)n * hv + vh) * GC * GC * 2;  // f16 elements of a T / M pair
-        const f16* tm = reinterpret_cast<const f16*>(w.tm);
-        const f16* mm = reinterpret_cast<const f16*>(w.mm);
-        const f16* src = ltile == 0 ? w.q16 + qb : ltile == 1 ? w.k16 + qb : ltile == 2 ? tm + tb : mm + tb;
-        f16* dst = ltile == 0 ? sq_[b] : ltile == 1 ? sk_[b] : ltile == 2 ? st_[b] : sm_[b];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (j >= j0 && j < j1) dma16s(src, doff[j], (lds_void*)&dst[512 * ((8 * (lw & 1)) + j)]);
-    };
     // V tile (K-side waves, MFMA C layout: rows 16 rb + 4 g4 + r, column ln), lg and beta
     float pv[4], plg = 0.f, plc = 0.f, pb = 0.f;
     bool pbm = false;
@@ -1094,17 +1118,18 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     // hi, lo) and Y^T ([16][64] hi, lo, row stride KT_): hi.hi + hi.lo + lo.hi
     auto mm_split_sw = [&](const f16* xh, const f16* xl, const f16* yh, const f16* yl, int r0,
                            int nkb) {
-        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+        // two accumulation chains (hi.hi + lo.hi, hi.lo) halve the dependent MFMA run
+        f32x4 c = {0.f, 0.f, 0.f, 0.f}, d = c;
         for (int kb = 0; kb < nkb; ++kb) {
             const f16x8 ah = frag_tm(xh, r0 + ln, 4 * kb + g4);
             const f16x8 al = frag_tm(xl, r0 + ln, 4 * kb + g4);
             const f16x8 bh = *reinterpret_cast<const f16x8*>(yh + ln * KT_ + 8 * g4 + 32 * kb);
             const f16x8 bl = *reinterpret_cast<const f16x8*>(yl + ln * KT_ + 8 * g4 + 32 * kb);
             c = mfma16(ah, bh, c);
-            c = mfma16(ah, bl, c);
+            d = mfma16(ah, bl, d);
             c = mfma16(al, bh, c);
         }
-        return c;
+        return c + d;
     };
     // K^T operand of the state update by two transposing reads: in each
     // 16-lane group, lane j points at token kb0 + j/4, dims row0 + 4 (j % 4)
@@ -1129,10 +1154,15 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
     };
 
     float vcur[4] = {0.f, 0.f, 0.f, 0.f};
-    // O of the previous chunk (Q-side waves): stored in the next chunk's
-    // phase 2, where these waves only issue their loads, instead of in phase
-    // 3 beside the K side's loads
+    // O of a chunk (Q-side waves) is formed in phase 1 of the next chunk, off
+    // the chain from one state to the next, and stored in that chunk's phase 2
     float opend[4] = {0.f, 0.f, 0.f, 0.f};
+    f32x4 xprev = {0.f, 0.f, 0.f, 0.f};  // Q S of the previous chunk
+    auto form_o = [&](int cp) {  // O = gamma Q S + M Delta of the chunk in buffer cp
+        const f32x4 o = mm_split_sw(sm_[cp], sm_[cp] + GC * GC, sdth, sdtl, 16 * rb, (rb >> 1) + 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) opend[r] = sgam[cp][16 * rb + 4 * g4 + r] * xprev[r] + o[r];
+    };
     auto store_o = [&](int tp) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -1140,7 +1170,6 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             if (t < n_tok) out[((size_t)t * hv + vh) * DV + c0 + ln] = opend[r];
         }
     };
-    issue(0);
     fetch_small(0);
     __builtin_amdgcn_s_waitcnt(0);
     stage_small(0);
@@ -1153,18 +1182,22 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         const f16* tq = sq_[cb];
         const f16* tk = sk_[cb];
         const float gC = sgam[cb][GC - 1];
-        // phase 1: K.S (waves 0-3) or Q.S (waves 4-7), rows 16 rb ..
-        f32x4 xs = {0.f, 0.f, 0.f, 0.f};
+        // phase 1: O of chunk n-1 (waves 4-7, from Delta^T and M still in
+        // place), then K.S (waves 0-3) or Q.S (waves 4-7), rows 16 rb ..
+        if (!kside && n >= 1) form_o(cb ^ 1);
+        f32x4 xs;
         {
             const f16* xt = kside ? tk : tq;
             const f16* sh = ssh + ln * KH_ + 8 * g4;
             const f16* sl = ssl + ln * KH_ + 8 * g4;
+            f32x4 xa = {0.f, 0.f, 0.f, 0.f}, xb = xa;  // S^T hi / lo chains
 #pragma unroll
             for (int kb = 0; kb < DK / 32; ++kb) {
                 const f16x8 a = frag_qk(xt, 16 * rb + ln, 4 * kb + g4);
-                xs = mfma16(a, *reinterpret_cast<const f16x8*>(sh + 32 * kb), xs);
-                xs = mfma16(a, *reinterpret_cast<const f16x8*>(sl + 32 * kb), xs);
+                xa = mfma16(a, *reinterpret_cast<const f16x8*>(sh + 32 * kb), xa);
+                xb = mfma16(a, *reinterpret_cast<const f16x8*>(sl + 32 * kb), xb);
             }
+            xs = xa + xb;
         }
         if (kside) {  // R = beta (V - gamma KS), written transposed as hi / lo
             f16x4 rh, rl;
@@ -1179,7 +1212,6 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             *reinterpret_cast<f16x4*>(srtl + ln * KT_ + 16 * rb + 4 * g4) = rl;
         }
         __syncthreads();
-        if (!kside && n + 1 < n_chunks) issue(n + 1);
         if (!kside && n >= 1) store_o(t0 - GC);
         // phase 2: Delta = T R (T lower triangular: column blocks <= rb)
         if (kside) {
@@ -1198,35 +1230,25 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
             *reinterpret_cast<f16x4*>(sdtl + ln * KT_ + 16 * rb + 4 * g4) = dlo;
             *reinterpret_cast<f16x4*>(sdph + ln * KT_ + 16 * rb + 4 * g4) = ph;
             *reinterpret_cast<f16x4*>(sdpl + ln * KT_ + 16 * rb + 4 * g4) = pl;
-            // chunk n+1's tiles go to the other buffer (last read in chunk
-            // n-1): the K side issues 5 of its 8 loads here, where it
-            // finishes phase 2 before the Q side, and the rest in phase 3
-            if (n + 1 < n_chunks) issue(n + 1, 0, 5);
         }
         __syncthreads();
-        if (kside && n + 1 < n_chunks) issue(n + 1, 5, 8);
-        // phase 3a: O = gamma QS + M Delta (waves 4-7)
-        if (!kside) {
-            const f32x4 o = mm_split_sw(sm_[cb], sm_[cb] + GC * GC, sdth, sdtl, 16 * rb, (rb >> 1) + 1);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) opend[r] = sgam[cb][16 * rb + 4 * g4 + r] * xs[r] + o[r];
-        }
-        // phase 3b: S'^T = exp(lgC) S^T + Dp^T K for state rows row0 .. row0 + 15
+        // phase 3: S'^T = exp(lgC) S^T + Dp^T K for state rows row0 .. row0 + 15
         {
-            f32x4 acc = sv * gC;
+            f32x4 acc = sv * gC, acl = {0.f, 0.f, 0.f, 0.f};
             const f16* ah = sdph + ln * KT_ + 8 * g4;
             const f16* al = sdpl + ln * KT_ + 8 * g4;
 #pragma unroll
             for (int kb = 0; kb < GC / 32; ++kb) {
                 const f16x8 b = frag_kt(tk, kb);
                 acc = mfma16(*reinterpret_cast<const f16x8*>(ah + 32 * kb), b, acc);
-                acc = mfma16(*reinterpret_cast<const f16x8*>(al + 32 * kb), b, acc);
+                acl = mfma16(*reinterpret_cast<const f16x8*>(al + 32 * kb), b, acl);
             }
-            sv = acc;
+            sv = acc + acl;
         }
+        if (!kside) xprev = xs;
         // S^T hi / lo were last read in phase 1 (before two barriers)
         put_state();
-        __builtin_amdgcn_s_waitcnt(0);  // chunk n+1's loads (direct and small)
+        __builtin_amdgcn_s_waitcnt(0);  // chunk n+1's small loads
         if (n + 1 < n_chunks) {
             stage_small(n + 1);
 #pragma unroll
@@ -1234,7 +1256,10 @@ __global__ __launch_bounds__(512) void gdn_scan_kernel(const float* __restrict__
         }
         __syncthreads();
     }
-    if (!kside && n_chunks >= 1) store_o((n_chunks - 1) * GC);
+    if (!kside && n_chunks >= 1) {  // the last chunk's O
+        form_o((n_chunks - 1) & 1);
+        store_o((n_chunks - 1) * GC);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) S[(size_t)(row0 + ln) * DV + c0 + 4 * g4 + r] = sv[r];
 }
@@ -1382,7 +1407,7 @@ hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, co
                        n_tok, n_k_heads, n_v_heads, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3(n_v_heads * (DV / SCOLS)), dim3(512), 0, s, q, k, v,
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(n_v_heads * (DV / SCOLS)), dim3(768), 0, s, q, k, v,
                        beta, state, out, n_tok, n_k_heads, n_v_heads, w);
     return hipGetLastError();
 }
