@@ -711,7 +711,7 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
     __shared__ __attribute__((aligned(16))) float s_big[BIG];   // sk | sq, then 2 x (sa | st | sx)
     __shared__ __attribute__((aligned(16))) float skk[GC * TS_];  // K K^T (lower tiles)
     __shared__ __attribute__((aligned(16))) float sqk[GC * TS_];  // Q K^T (lower tiles)
-    __shared__ float slg[2][GC], sb[2][GC];
+    __shared__ __attribute__((aligned(16))) float slg[2][GC], sb[2][GC];
     // phase A: the normalised k / q rows as f16 hi + lo parts (row stride KH_
     // halves, 288 bytes: conflict-free 16-byte reads down 16 rows)
     f16* skh = reinterpret_cast<f16*>(s_big);
@@ -732,21 +732,20 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
     const int row = tid >> 3, part = tid & 7;
     f32x4 a[4], b[4];
     float g_nx = 0.f, b_nx = 0.f;
-    auto fetch = [&](int n) {
+    // part j of the rows: pieces part + 8 j (part 0 also brings g and beta)
+    auto fetch = [&](int n, int j) {
         const int t0 = n * GC;
         const int vh = kh + half * hk, tg = min(t0 + lane, n_tok - 1);
-        if (wl == 0 && vh < hv) {
+        if (j == 0 && wl == 0 && vh < hv) {
             g_nx = g[(size_t)tg * hv + vh];
             b_nx = beta[(size_t)tg * hv + vh];
         }
         const size_t src = ((size_t)min(t0 + row, n_tok - 1) * hk + kh) * DK;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            a[j] = *reinterpret_cast<const f32x4*>(q + src + 4 * (part + 8 * j));
-            b[j] = *reinterpret_cast<const f32x4*>(k + src + 4 * (part + 8 * j));
-        }
+        a[j] = *reinterpret_cast<const f32x4*>(q + src + 4 * (part + 8 * j));
+        b[j] = *reinterpret_cast<const f32x4*>(k + src + 4 * (part + 8 * j));
     };
-    fetch(blockIdx.x);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fetch(blockIdx.x, j);
     for (int n = blockIdx.x; n < n_chunks; n += gridDim.x) {
     const int t0 = n * GC;
     float g_pre = g_nx, b_pre = b_nx;
@@ -795,7 +794,6 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
                 f16x4{to_f16(y[0]), to_f16(y[1]), to_f16(y[2]), to_f16(y[3])};
         }
     }
-    if (n + (int)gridDim.x < n_chunks) fetch(n + gridDim.x);
     __syncthreads();
     // lower-triangular 16x16 tiles: 10 of K K^T, then 10 of Q K^T
     const int ln = lane & 15, lg4 = lane >> 4;
@@ -825,6 +823,13 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
         for (int r = 0; r < 4; ++r) dst[(16 * ib + 4 * lg4 + r) * TS_ + 16 * jb + ln] = acc[r];
     }
     __syncthreads();  // q / k rows are dead: s_big now holds two halves of A, T, scratch
+    // The next chunk's rows load in quarters, after the barriers that end the
+    // cumulative sum, A / M, the diagonal blocks and the first block round:
+    // the 64 KB a chunk keep the CU's address unit busy for thousands of
+    // cycles, and issued at once (at the end of phase A, or all here) they
+    // stalled the issuing wavefronts before the next barrier; ahead of the
+    // cumulative sum (one wavefront per half) a quarter still cost ~1 700.
+    const bool nxt = n + (int)gridDim.x < n_chunks;
 
     float* sa = s_big + half * PREP_B;  // A
     float* st = sa + GC * TS_;          // T = (I + A)^-1
@@ -852,24 +857,27 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
             w.lg[((size_t)n * hv + vh) * GC + lane] = x;
         }
         __syncthreads();
+        if (nxt && v0 == kh) fetch(n + gridDim.x, 0);
         if (on) {
             // thread: row i, columns 4 j4 .. 4 j4 + 3; entries above the
             // diagonal are 0 (and need no exp)
             f16* mm = reinterpret_cast<f16*>(w.mm + ((size_t)n * hv + vh) * GC * GC);
             for (int e = ht; e < GC * GC / 4; e += 256) {
                 const int i = e / (GC / 4), j0 = 4 * (e % (GC / 4));
-                f32x4 av = {0.f, 0.f, 0.f, 0.f}, mv = av;
-                if (j0 <= i) {
-                    const float li = hlg[i], bi = hb[i];
+                // branch-free: 16-byte reads of lg and of the K K^T / Q K^T
+                // rows, masked by selects (entries above the diagonal, whose
+                // tiles were never written, are read and discarded)
+                const float li = hlg[i], bi = hb[i];
+                const f32x4 lj = *reinterpret_cast<const f32x4*>(hlg + j0);
+                const f32x4 kk = *reinterpret_cast<const f32x4*>(skk + i * TS_ + j0);
+                const f32x4 qk = *reinterpret_cast<const f32x4*>(sqk + i * TS_ + j0);
+                f32x4 av, mv;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int j = j0 + r;
-                        if (j <= i) {
-                            const float dec = fast_exp2(li - hlg[j]);
-                            if (j < i) av[r] = bi * dec * skk[i * TS_ + j];
-                            mv[r] = dec * sqk[i * TS_ + j];
-                        }
-                    }
+                for (int r = 0; r < 4; ++r) {
+                    const int j = j0 + r;
+                    const float dec = fast_exp2(li - lj[r]);
+                    av[r] = j < i ? bi * dec * kk[r] : 0.f;
+                    mv[r] = j <= i ? dec * qk[r] : 0.f;
                 }
                 *reinterpret_cast<f32x4*>(sa + i * TS_ + j0) = av;
                 *reinterpret_cast<f32x4*>(st + i * TS_ + j0) = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -884,6 +892,7 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
             }
         }
         __syncthreads();
+        if (nxt && v0 == kh) fetch(n + gridDim.x, 1);
         // T = (I + A)^-1, A strictly lower triangular, by 16x16 blocks:
         //   T_ii = (I + A_ii)^-1                      (forward substitution, wave i)
         //   T_ij = -T_ii . sum_{j <= k < i} A_ik T_kj  (i > j, by block distance)
@@ -901,8 +910,10 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
             }
         }
         __syncthreads();
+        if (nxt && v0 == kh) fetch(n + gridDim.x, 2);
         float* sxw = sx + wl * 16 * TS_;  // this wave's 16x16 scratch
         for (int d = 1; d < 4; ++d) {
+            if (d == 2 && nxt && v0 == kh) fetch(n + gridDim.x, 3);
             if (on && wl < 4 - d) {
                 const int j = wl, i = wl + d;
                 f32x4 x = {0.f, 0.f, 0.f, 0.f};
