@@ -1053,11 +1053,12 @@ __global__ __launch_bounds__(768) void gdn_scan_kernel(const float* __restrict__
         // read before chunk n-1's final barrier.  A wave's 16 loads take about
         // a third of a chunk to issue (the CU's address unit is shared by the
         // four loaders), so they are spread over the chunk's three phases
-        // instead of holding the first barrier.
+        // instead of holding the first barrier, most of them before the first
+        // two so that few remain in flight at the chunk's last barrier.
         // The M tile's buffer holds chunk n-1's M until the Q side has formed
         // that chunk's O in phase 1 of chunk n, so M loads wait for the first
         // barrier.
-        const int j1 = lt == 3 ? 0 : 6, j2 = lt == 3 ? 8 : 11;
+        const int j1 = lt == 3 ? 0 : 9, j2 = lt == 3 ? 10 : 16;
         issue(0, 0, 16);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -1259,7 +1260,8 @@ __global__ __launch_bounds__(768) void gdn_scan_kernel(const float* __restrict__
         if (!kside) xprev = xs;
         // S^T hi / lo were last read in phase 1 (before two barriers)
         put_state();
-        __builtin_amdgcn_s_waitcnt(0);  // chunk n+1's small loads
+        // chunk n+1's small loads are waited for by the compiler where they are
+        // used (below); the Q side, which issued only output stores, waits for none
         if (n + 1 < n_chunks) {
             stage_small(n + 1);
 #pragma unroll
