@@ -1402,6 +1402,7 @@ hipError_t launch_gdn_prefill(const float* q, const float* k, const float* v, co
                               int32_t n_k_heads, int32_t n_v_heads, int32_t chunk,
                               const GdnWorkspace& ws, hipStream_t s) {
     if (chunk != GC) return hipErrorInvalidValue;
+    if (n_tok <= 0) return hipSuccess;  // the kernels clamp token indices to n_tok - 1
     const size_t nc = (size_t)(n_tok + GC - 1) / GC;
     GdnWs w;
     const size_t qk = nc * n_k_heads * GC * DK;  // f16 elements of one of q16 / k16
