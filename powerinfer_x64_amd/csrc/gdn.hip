@@ -953,7 +953,8 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
 // head, 16 state columns), beside 4 loader wavefronts (data movement, below).
 // Waves 0-3 own the K side (K.S, R, Delta) and waves 4-7 the Q side (Q.S, O)
 // of chunk row block w % 4; the state update is split over all 8 (16 state
-// rows each).
+// rows each).  The Q side forms a chunk's O in the next chunk's first phase,
+// off the chain from one state to the next.
 //
 // Precision: the state S stays in f32 in registers (wave w holds rows
 // 16w..16w+15 of S^T in the MFMA C layout).  The K.S, Q.S and K^T.Dp
@@ -964,10 +965,10 @@ __global__ __launch_bounds__(512) void gdn_prep_kernel(const float* __restrict__
 //
 // Data movement: chunk n+1's q, k, T and M tiles (64 KB) arrive in the other
 // half of a double buffer by direct global -> LDS loads while chunk n
-// computes.  Four more wavefronts (8-11) issue them, one tile each, at the
-// start of the chunk and wait for them before its last barrier: the 64
+// computes.  Four more wavefronts (8-11) issue them, one tile each, spread
+// over the chunk's phases, and wait for them before its last barrier: the 64
 // load instructions a chunk takes keep the CU's address unit busy for about
-// a thousand cycles, and a compute wave that issued them would stall behind
+// two thousand cycles, and a compute wave that issued them would stall behind
 // that queue on the chunk's dependent chain.  K^T comes from transposing
 // reads of the k tile.  The small per-chunk loads are unmasked (clamped), so
 // no compiler-inserted wait lands inside a phase.
