@@ -1466,38 +1466,60 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillF32Args a) {
 }
 
 // The key splits of a prefill launch combined per (batch, query row, head): the
-// log-sum-exp merge of the splits' (max, sum) in log2 units and their O.  One
-// wavefront per row, D / 64 values per lane.
+// log-sum-exp merge of the splits' (max, sum) in log2 units and their O.  Each thread
+// takes 4 consecutive values of a row (D / 4 threads a row) in MR rows, and requests every
+// split's (max, sum) and O and the gate of all of them before it uses any: one memory round
+// trip a thread with 16-byte loads, and few enough workgroups that they all fit at once.
 // Rows of query positions below q0 (blocks that were not split) are already written; the
 // launch starts at row `first`.
 template <int D>
+constexpr int merge_rows() { return D == 256 ? 1 : 2; }  // MR: rows per thread
+template <int D, int KS>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
                                                             const float* __restrict__ part_ml,
                                                             float* __restrict__ out, long long rows,
-                                                            int ksplit, const float* __restrict__ gate,
+                                                            const float* __restrict__ gate,
                                                             long long first, int S, int hq, int q0) {
-    constexpr int V = D / 64;
-    typedef float fv __attribute__((ext_vector_type(V)));
-    const long long row = first + (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows || (row / hq) % S < q0) return;
-    const int lane = threadIdx.x & 63;
-    float M = -1e30f;
-    for (int k = 0; k < ksplit; ++k) M = fmaxf(M, part_ml[2 * (k * rows + row)]);
-    float L = 0.f;
-    fv acc = {};
-    for (int k = 0; k < ksplit; ++k) {
-        const long long r = k * rows + row;
-        const float w = fast_exp2(part_ml[2 * r] - M);
-        L += w * part_ml[2 * r + 1];
-        acc += w * *reinterpret_cast<const fv*>(part_o + r * D + V * lane);
-    }
-    acc *= 1.0f / L;
-    if (gate) {
-        const fv gt = *reinterpret_cast<const fv*>(gate + row * D + V * lane);
+    constexpr int LPR = D / 4, RPP = 256 / LPR, MR = merge_rows<D>();
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const int c = 4 * ((int)threadIdx.x % LPR);
+    long long rw[MR];
+    bool live[MR];
+    f2 ml[MR][KS];
+    f32x4 o[MR][KS], gt[MR];
 #pragma unroll
-        for (int e = 0; e < V; ++e) acc[e] *= gate_sigmoid(gt[e]);
+    for (int m = 0; m < MR; ++m) {
+        rw[m] = first + ((long long)blockIdx.x * MR + m) * RPP + (int)threadIdx.x / LPR;
+        live[m] = rw[m] < rows && (rw[m] / hq) % S >= q0;
+        const long long rl = live[m] ? rw[m] : first;  // a row that exists: loads stay unconditional
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const long long r = k * rows + rl;
+            ml[m][k] = *reinterpret_cast<const f2*>(part_ml + 2 * r);
+            o[m][k] = *reinterpret_cast<const f32x4*>(part_o + r * D + c);
+        }
+        if (gate) gt[m] = *reinterpret_cast<const f32x4*>(gate + rl * D + c);
     }
-    *reinterpret_cast<fv*>(out + row * D + V * lane) = acc;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        float M = ml[m][0][0];
+#pragma unroll
+        for (int k = 1; k < KS; ++k) M = fmaxf(M, ml[m][k][0]);
+        float L = 0.f;
+        f32x4 acc = {};
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const float w = fast_exp2(ml[m][k][0] - M);
+            L += w * ml[m][k][1];
+            acc += w * o[m][k];
+        }
+        acc *= 1.0f / L;
+        if (gate) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] *= gate_sigmoid(gt[m][e]);
+        }
+        if (live[m]) *reinterpret_cast<f32x4*>(out + rw[m] * D + c) = acc;
+    }
 }
 
 }  // namespace
@@ -1656,14 +1678,24 @@ hipError_t launch_merge(int D, const PrefillArgs& a, int batch, int q0, float* o
     if (q0 >= a.S) return hipSuccess;
     const long long rows = (long long)batch * a.S * a.hq;
     const long long first = batch == 1 ? (long long)q0 * a.hq : 0;
-    const dim3 grid((unsigned)((rows - first + 3) / 4));
+    const long long per_wg = (D == 256 ? merge_rows<256>() : D == 128 ? merge_rows<128>() : merge_rows<64>()) *
+                             (256 / (D / 4));
+    const dim3 grid((unsigned)((rows - first + per_wg - 1) / per_wg));
+#define PI_MERGE_K(DD, KK)                                                                         \
+    hipLaunchKernelGGL((prefill_merge_kernel<DD, KK>), grid, dim3(256), 0, s, a.part_o, a.part_ml, out, \
+                       rows, a.gate, first, a.S, a.hq, q0)
 #define PI_MERGE(DD)                                                                               \
-    hipLaunchKernelGGL(prefill_merge_kernel<DD>, grid, dim3(256), 0, s, a.part_o, a.part_ml, out, rows, \
-                       a.ksplit, a.gate, first, a.S, a.hq, q0)
-    if (D == 256) PI_MERGE(256);
-    else if (D == 128) PI_MERGE(128);
-    else PI_MERGE(64);
+    switch (a.ksplit) {                                                                            \
+        case 2: PI_MERGE_K(DD, 2); break;                                                          \
+        case 3: PI_MERGE_K(DD, 3); break;                                                          \
+        default: PI_MERGE_K(DD, 4);                                                                \
+    }
+    if (a.ksplit < 2 || a.ksplit > 4) return hipErrorInvalidValue;
+    if (D == 256) PI_MERGE(256)
+    else if (D == 128) PI_MERGE(128)
+    else PI_MERGE(64)
 #undef PI_MERGE
+#undef PI_MERGE_K
     return hipGetLastError();
 }
 }  // namespace
