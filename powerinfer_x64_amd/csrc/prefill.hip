@@ -76,10 +76,11 @@ struct PrefillArgs {
     // the chip evenly (else: one block each, heaviest first)
     int paired;
     // key split (a launch with fewer workgroups than CUs): blockIdx.z = batch * ksplit +
-    // split; split k of a workgroup's n key tiles takes tiles [k p, (k+1) p), p = ceil(n /
-    // ksplit), and leaves its unnormalised O and (max, sum) for prefill_merge_kernel.  A
-    // query block of at most kthr tiles is not split: split 0 takes all its tiles and
-    // writes the output, the other splits skip it.
+    // split.  A query block of n <= kthr key tiles is not split: split 0 takes all its
+    // tiles and writes the output, the other splits skip it.  A longer one runs in
+    // split_pieces(n) = min(ksplit, ceil(n / kthr)) pieces: piece k takes tiles [k p,
+    // (k+1) p), p = ceil(n / pieces), and leaves its unnormalised O and (max, sum) for
+    // prefill_merge_kernel; splits past the block's pieces skip it.
     int ksplit;
     int kthr;
     float* part_o;   // [ksplit][B][S][Hq][D]
@@ -99,6 +100,11 @@ struct PrefillArgs {
 };
 
 __device__ __forceinline__ float gate_sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// Pieces of a query block of n key tiles under a key split (1: the block runs whole).
+__host__ __device__ __forceinline__ int split_pieces(int n, int ksplit, int kthr) {
+    return ksplit > 1 && kthr > 0 && n > kthr ? min(ksplit, (n + kthr - 1) / kthr) : 1;
+}
 
 __device__ __forceinline__ int head_of(int kvh, int c, int hkv, int group, int mode) {
     return mode == 0 ? kvh + c * hkv : kvh * group + c;
@@ -218,9 +224,10 @@ __global__ __launch_bounds__(64 * PrefillCfg<D>::NW, 1) void prefill_fa_kernel(P
     const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
     const int n_tiles = (wg_keys + BN - 1) / BN;
     // this workgroup's key tiles: [tb, tb + nloc); step t below works on tile tb + t
-    const bool split = a.ksplit > 1 && n_tiles > a.kthr;
-    if (!split && ksp > 0) continue;  // split 0 runs the whole block (uniform per workgroup)
-    const int kper = split ? (n_tiles + a.ksplit - 1) / a.ksplit : n_tiles;
+    const int pieces = split_pieces(n_tiles, a.ksplit, a.kthr);
+    if (ksp >= pieces) continue;  // uniform per workgroup
+    const bool split = pieces > 1;
+    const int kper = (n_tiles + pieces - 1) / pieces;
     const int tb = min(n_tiles, ksp * kper);
     const int nloc = min(n_tiles, tb + kper) - tb;
     const int w_keys = a.causal ? min(Sk, q_off + p0 + ROWS) : Sk;
@@ -837,9 +844,10 @@ __global__ __launch_bounds__(512, 1) void prefill_fa256_kernel(PrefillArgs a) {
     const int p0 = qb * WROWS + rt * R;
     const int wg_keys = a.causal ? min(Sk, q_off + qb * WROWS + WROWS) : Sk;
     const int n_tiles = (wg_keys + BN - 1) / BN;
-    const bool split = a.ksplit > 1 && n_tiles > a.kthr;
-    if (!split && ksp > 0) continue;  // split 0 runs the whole block (uniform per workgroup)
-    const int kper = split ? (n_tiles + a.ksplit - 1) / a.ksplit : n_tiles;
+    const int pieces = split_pieces(n_tiles, a.ksplit, a.kthr);
+    if (ksp >= pieces) continue;  // uniform per workgroup
+    const bool split = pieces > 1;
+    const int kper = (n_tiles + pieces - 1) / pieces;
     const int tb = min(n_tiles, ksp * kper);
     const int nloc = min(n_tiles, tb + kper) - tb;
     const int w_keys = a.causal ? min(Sk, q_off + p0 + R) : Sk;
@@ -1479,22 +1487,28 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
                                                             const float* __restrict__ part_ml,
                                                             float* __restrict__ out, long long rows,
                                                             const float* __restrict__ gate,
-                                                            long long first, int S, int hq, int q0) {
+                                                            long long first, int S, int hq, int q0,
+                                                            int kthr, int wrows, int q_off, int Sk,
+                                                            int causal) {
     constexpr int LPR = D / 4, RPP = 256 / LPR, MR = merge_rows<D>();
     typedef float f2 __attribute__((ext_vector_type(2)));
     const int c = 4 * ((int)threadIdx.x % LPR);
     long long rw[MR];
     bool live[MR];
+    int pcs[MR];
     f2 ml[MR][KS];
     f32x4 o[MR][KS], gt[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         rw[m] = first + ((long long)blockIdx.x * MR + m) * RPP + (int)threadIdx.x / LPR;
-        live[m] = rw[m] < rows && (rw[m] / hq) % S >= q0;
+        const int qpos = (int)((rw[m] / hq) % S);
+        const int keys = causal ? min(Sk, q_off + (qpos / wrows) * wrows + wrows) : Sk;
+        pcs[m] = split_pieces((keys + BN - 1) / BN, KS, kthr);  // the row's block's pieces
+        live[m] = rw[m] < rows && qpos >= q0 && pcs[m] > 1;
         const long long rl = live[m] ? rw[m] : first;  // a row that exists: loads stay unconditional
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-            const long long r = k * rows + rl;
+            const long long r = (k < pcs[m] ? k : 0) * rows + rl;  // slots past the pieces: weight 0
             ml[m][k] = *reinterpret_cast<const f2*>(part_ml + 2 * r);
             o[m][k] = *reinterpret_cast<const f32x4*>(part_o + r * D + c);
         }
@@ -1509,7 +1523,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
         f32x4 acc = {};
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-            const float w = fast_exp2(ml[m][k][0] - M);
+            const float w = k < pcs[m] ? fast_exp2(ml[m][k][0] - M) : 0.f;
             L += w * ml[m][k][1];
             acc += w * o[m][k];
         }
@@ -1628,12 +1642,14 @@ int cu_count() {
 
 struct PrefillSched {
     int hpw, paired, ksplit;
+    bool forced;  // ksplit from PI_PREFILL_KSPLIT
 };
 
 // The schedule of a launch.  Causal launches whose pairs of query blocks fill every CU
 // once or more pair them (equal work per workgroup).  Otherwise, a launch with fewer
-// workgroups than CUs splits each workgroup's keys over up to 4 workgroups (more CUs
-// busy, one merge launch after).  PI_PREFILL_PAIRED=0 / 1 and PI_PREFILL_KSPLIT=n
+// workgroups than CUs may split a workgroup's keys over up to 4 workgroups (more CUs
+// busy, one merge launch after); ksplit is the number of partial slots the workspace
+// holds, split_plan picks the pieces.  PI_PREFILL_PAIRED=0 / 1 and PI_PREFILL_KSPLIT=n
 // force either choice.
 PrefillSched prefill_sched(int batch, int seq_len, int n_q_heads, int n_kv_heads, int head_dim,
                            int causal) {
@@ -1651,30 +1667,54 @@ PrefillSched prefill_sched(int batch, int seq_len, int n_q_heads, int n_kv_heads
     const char* env_p = std::getenv("PI_PREFILL_PAIRED");  // read per call, as is PI_PREFILL_KSPLIT
     if (env_p && causal) sc.paired = env_p[0] == '1';
     sc.ksplit = 1;
-    if (!sc.paired && n_cu > 0 && wgs < n_cu) sc.ksplit = (int)std::min<long long>(4, n_cu / wgs);
+    sc.forced = false;
+    if (!sc.paired && n_cu > 0 && wgs < n_cu) sc.ksplit = (int)std::min<long long>(4, 2 * (n_cu / wgs));
     const char* env_k = std::getenv("PI_PREFILL_KSPLIT");
-    if (env_k && !sc.paired) sc.ksplit = std::max(1, std::min(4, std::atoi(env_k)));
+    if (env_k && !sc.paired) {
+        sc.ksplit = std::max(1, std::min(4, std::atoi(env_k)));
+        sc.forced = true;
+    }
     return sc;
 }
 
-// The selective key split of a launch with a.ksplit > 1 and wrows query rows per block:
-// blocks of at most kthr = ceil(most tiles / ksplit) tiles run whole (no more work than a
-// split piece of the longest block), the longer ones are split.  Sets a.kthr; returns the
-// first query row of a split block (S when none is: nothing to merge).
-int split_plan(PrefillArgs& a, int wrows) {
+// The key split of a launch with a.ksplit > 1 slots, wrows query rows per block and hsets
+// workgroups per query block (head sets x batch).  Picks the piece size kthr: the smallest
+// for which every block fits the slots and all pieces together fit the CUs once (one
+// workgroup a CU: the longest piece sets the launch's time), so short causal blocks run
+// whole and long ones in two to four pieces; forced, kthr = ceil(most tiles / ksplit).
+// Sets a.kthr and a.ksplit (the most pieces of a block; 1: no split); returns the first
+// query row of a split block (S when none is: nothing to merge).
+int split_plan(PrefillArgs& a, int wrows, long long hsets, bool forced) {
     const int nqb = (a.S + wrows - 1) / wrows;
     auto tiles = [&](int qb) {
         const int keys = a.causal ? std::min(a.Sk, a.q_off + qb * wrows + wrows) : a.Sk;
         return (keys + BN - 1) / BN;
     };
-    a.kthr = (tiles(nqb - 1) + a.ksplit - 1) / a.ksplit;
+    const int most = tiles(nqb - 1);  // tiles grow with the block (causal) or are equal
+    int p = (most + a.ksplit - 1) / a.ksplit;
+    if (!forced) {
+        const long long n_cu = cu_count();
+        for (; p < most; ++p) {
+            long long tot = 0;
+            for (int qb = 0; qb < nqb; ++qb) tot += (tiles(qb) + p - 1) / p;
+            if (tot * hsets <= n_cu) break;
+        }
+    }
+    a.kthr = std::max(1, p);
+    a.ksplit = std::min(a.ksplit, (most + a.kthr - 1) / a.kthr);
+    if (a.ksplit <= 1) {
+        a.ksplit = 1;
+        a.kthr = 0;
+        return a.S;
+    }
     for (int qb = 0; qb < nqb; ++qb)
         if (tiles(qb) > a.kthr) return qb * wrows;
     return a.S;
 }
 
 // The merge of the split blocks' rows (batch, query row >= q0, head) into out.
-hipError_t launch_merge(int D, const PrefillArgs& a, int batch, int q0, float* out, hipStream_t s) {
+hipError_t launch_merge(int D, const PrefillArgs& a, int batch, int q0, int wrows, float* out,
+                        hipStream_t s) {
     if (q0 >= a.S) return hipSuccess;
     const long long rows = (long long)batch * a.S * a.hq;
     const long long first = batch == 1 ? (long long)q0 * a.hq : 0;
@@ -1683,7 +1723,7 @@ hipError_t launch_merge(int D, const PrefillArgs& a, int batch, int q0, float* o
     const dim3 grid((unsigned)((rows - first + per_wg - 1) / per_wg));
 #define PI_MERGE_K(DD, KK)                                                                         \
     hipLaunchKernelGGL((prefill_merge_kernel<DD, KK>), grid, dim3(256), 0, s, a.part_o, a.part_ml, out, \
-                       rows, a.gate, first, a.S, a.hq, q0)
+                       rows, a.gate, first, a.S, a.hq, q0, a.kthr, wrows, a.q_off, a.Sk, a.causal)
 #define PI_MERGE(DD)                                                                               \
     switch (a.ksplit) {                                                                            \
         case 2: PI_MERGE_K(DD, 2); break;                                                          \
@@ -1741,18 +1781,19 @@ hipError_t launch_prefill(const void* q, const void* k, const void* v, int32_t d
     a.gate = gate;
     const size_t rows = (size_t)batch * seq_len * n_q_heads;
     int q0 = seq_len;
+    const int wrows = ROWS * (head_dim == 256 ? PrefillCfg<256>::NW : PrefillCfg<128>::NW) / sc.hpw;
     if (sc.ksplit > 1 && ws && ws_floats >= (size_t)sc.ksplit * rows * (head_dim + 2)) {
         a.ksplit = sc.ksplit;
         a.part_o = ws;
         a.part_ml = ws + (size_t)sc.ksplit * rows * head_dim;
-        q0 = split_plan(a, ROWS * (head_dim == 256 ? PrefillCfg<256>::NW : PrefillCfg<128>::NW) / sc.hpw);
+        q0 = split_plan(a, wrows, (long long)n_kv_heads * (a.group / sc.hpw) * batch, sc.forced);
     }
     if (head_dim == 64) launch_d<64>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
     else if (head_dim == 128) launch_d<128>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
     else launch_d<256>(a, sc.hpw, n_kv_heads, seq_len, batch, bf, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.ksplit == 1) return e;
-    return launch_merge(head_dim, a, batch, q0, out, s);
+    return launch_merge(head_dim, a, batch, q0, wrows, out, s);
 }
 
 hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, const int32_t* page_table,
@@ -1798,7 +1839,7 @@ hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, co
         a.ksplit = sc.ksplit;
         a.part_o = ws;
         a.part_ml = ws + (size_t)sc.ksplit * rows * D;
-        q0 = split_plan(a, wrows);
+        q0 = split_plan(a, wrows, (long long)g.n_kv_heads * (a.group / sc.hpw), sc.forced);
     }
     const int nqb = (n_tok + wrows - 1) / wrows;
     const dim3 grid(g.n_kv_heads * (a.group / sc.hpw), a.paired ? (nqb + 1) / 2 : nqb, a.ksplit);
@@ -1823,7 +1864,7 @@ hipError_t launch_prefill_pool(const KvGeom& g, const void* q, int32_t q_f32, co
 #undef PI_PAGED
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.ksplit == 1) return e;
-    return launch_merge(D, a, 1, q0, out, s);
+    return launch_merge(D, a, 1, q0, wrows, out, s);
 }
 
 }  // namespace pi
