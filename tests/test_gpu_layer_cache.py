@@ -151,6 +151,18 @@ def test_layer_f16_cache_gated_prompt_and_key_split(hq, hkv, d, chunks):
            np.random.default_rng(0x1A8 + d), hq, hkv, d, gate=True)
 
 
+def test_layer_c4_prompt_1024_split_pieces():
+    """The C4 layer's fresh 1024-token prompt (16/2 heads, D 256, gated, f16 cache) under the
+    default schedule: on a 256-CU chip its 128 query blocks of 1-16 key tiles run whole up to 6
+    tiles and in two or three pieces beyond, so the merge combines rows of two and of three
+    pieces and skips the rows the epilogue wrote."""
+    dev = device()
+    from powerinfer_x64_amd import runtime as rt
+    layer = rt.AttnLayer(dev, 1024 + 16, 16, 2, 256, torch.float16, rope_base=1e6)
+    _drive(layer, [1024], dict(rope_base=1e6), _rel(1e-2), np.random.default_rng(0x1B9), 16, 2, 256,
+           gate=True)
+
+
 @pytest.mark.parametrize("paired,ksplit", [("1", None), (None, "2"), (None, "3"), (None, "4")])
 @pytest.mark.parametrize("hq,hkv,d", [(16, 2, 256), (32, 8, 128), (8, 2, 64)])
 def test_layer_f16_cache_gated_forced_schedules(monkeypatch, paired, ksplit, hq, hkv, d):
