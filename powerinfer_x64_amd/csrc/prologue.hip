@@ -440,9 +440,15 @@ __device__ __forceinline__ void prologue_page(float* __restrict__ k, const float
     constexpr int D = 64 * EPL;
     constexpr int E = 16 / (int)sizeof(PT);  // pool values per 16-byte chunk
     typedef PT pv __attribute__((ext_vector_type(E)));
-    PT* kb_s = reinterpret_cast<PT*>(pi_prologue_dyn);  // the K block
-    PT* vb_s = kb_s + kPageTokens * D;                  // the V block
-    float* cs_c = reinterpret_cast<float*>(vb_s + kPageTokens * D);  // cos [slot][pair]
+    // K and V rows staged by slot, [16][KP] with a 16-byte pad a row: a row's values are
+    // written contiguously, and the block writes below read a K chunk (E dims of one slot)
+    // as one 16-byte read and a V chunk (E slots of one dim) as E reads, 16 rows spread
+    // over the banks by the pad.  (Staging in the pool's block layouts made each 2-byte
+    // write land on one or two banks across the wavefront.)
+    constexpr int KP = D + E;
+    PT* kb_s = reinterpret_cast<PT*>(pi_prologue_dyn);
+    PT* vb_s = kb_s + kPageTokens * KP;
+    float* cs_c = reinterpret_cast<float*>(vb_s + kPageTokens * KP);  // cos [slot][pair]
     float* cs_n = cs_c + kPageTokens * n_pairs;                       // sin
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int hkv = g.n_kv_heads;
@@ -490,8 +496,8 @@ __device__ __forceinline__ void prologue_page(float* __restrict__ k, const float
         if (app) {
 #pragma unroll
             for (int jj = 0; jj < EPL; ++jj) {
-                kb_s[k_index<PT>(sl, e0 + jj)] = from_f32<PT>(xv[jj]);
-                vb_s[v_index(sl, e0 + jj)] = from_f32<PT>(vs[m][jj]);
+                kb_s[sl * KP + e0 + jj] = from_f32<PT>(xv[jj]);
+                vb_s[sl * KP + e0 + jj] = from_f32<PT>(vs[m][jj]);
             }
         }
     }
@@ -503,18 +509,22 @@ __device__ __forceinline__ void prologue_page(float* __restrict__ k, const float
     // K block [D / E][16][E]: chunk c = (dims E (c / 16) .., slot c % 16)
     for (int c = threadIdx.x; c < D / E * kPageTokens; c += 256) {
         const int slot = c % kPageTokens;
-        if (slot >= s0 && slot < s1) *reinterpret_cast<pv*>(kp + (size_t)E * c) = *reinterpret_cast<const pv*>(kb_s + E * c);
+        if (slot >= s0 && slot < s1)
+            *reinterpret_cast<pv*>(kp + (size_t)E * c) = *reinterpret_cast<const pv*>(kb_s + slot * KP + E * (c / kPageTokens));
     }
     // V block [D][16]: chunk c = (dim c / (16 / E), slots E (c % (16 / E)) ..)
     constexpr int CPR = kPageTokens / E;  // chunks per dim row
     for (int c = threadIdx.x; c < D * CPR; c += 256) {
-        const int sl0 = E * (c % CPR);
+        const int sl0 = E * (c % CPR), dim = c / CPR;
         if (sl0 + E <= s0 || sl0 >= s1) continue;
         if (sl0 >= s0 && sl0 + E <= s1) {
-            *reinterpret_cast<pv*>(vp + (size_t)E * c) = *reinterpret_cast<const pv*>(vb_s + E * c);
+            pv t;
+#pragma unroll
+            for (int e = 0; e < E; ++e) t[e] = vb_s[(sl0 + e) * KP + dim];
+            *reinterpret_cast<pv*>(vp + (size_t)E * c) = t;
         } else {  // a chunk the launch covers in part: its own slots only
             for (int e = 0; e < E; ++e)
-                if (sl0 + e >= s0 && sl0 + e < s1) vp[(size_t)E * c + e] = vb_s[E * c + e];
+                if (sl0 + e >= s0 && sl0 + e < s1) vp[(size_t)E * c + e] = vb_s[(sl0 + e) * KP + dim];
         }
     }
 }
@@ -728,8 +738,8 @@ hipError_t launch_attn_prologue(float* q, float* k, const float* v, const float*
         const dim3 grid_v((unsigned)(toks + n_pg), grid.y);
         PrologueStart spv = sp;
         spv.wg0 = (int32_t)n_pg;
-        // the page workgroups' K and V blocks and cos / sin table
-        const size_t lds = by_page ? (size_t)2 * kPageTokens * g.head_dim * (g.dtype == 1 ? 2 : 4) +
+        // the page workgroups' staged K and V rows and cos / sin table
+        const size_t lds = by_page ? (size_t)2 * kPageTokens * (g.head_dim * (g.dtype == 1 ? 2 : 4) + 16) +
                                          (size_t)2 * kPageTokens * n_pairs * sizeof(float)
                                    : 0;
 #define PI_PROLOGUE_VEC(PT, E)                                                                       \
