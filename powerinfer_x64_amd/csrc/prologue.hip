@@ -366,8 +366,20 @@ __device__ __forceinline__ void store_vec(float* d, const float* s) {
 // One head row held EPL values a lane (element e0 + j of lane l, e0 = EPL l): RMS-normed
 // with the weights w (none: no norm) and rotated; cos_sin(i, &c, &s) gives pair i's angle.
 template <int EPL, typename CS>
-__device__ __forceinline__ void rope_row(float* xv, int n_pairs, int neox, int lane, CS cos_sin) {
+__device__ __forceinline__ void norm_rope_row(float* xv, bool has_w, const float* w, float eps,
+                                              int norm_d, int n_pairs, int neox, int lane,
+                                              CS cos_sin) {
     const int e0 = EPL * lane;
+    if (has_w) {  // ops::rms_norm (src/ops.rs:13-27) per head
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) ss = wave_sum_xor(ss, sh);
+        const float inv = 1.0f / sqrtf(ss / (float)norm_d + eps);
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * w[j];
+    }
     // ops::apply_rope / apply_rope_with_freqs: pair i is (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
     if (neox) {
         const int off = n_pairs / EPL;  // lanes between the two elements of a pair
@@ -406,57 +418,6 @@ __device__ __forceinline__ void rope_row(float* xv, int n_pairs, int neox, int l
             xv[0] = (lane & 1) ? pv0 * sn + xv[0] * c : xv[0] * c - pv0 * sn;
         }
     }
-}
-
-
-template <int EPL, typename CS>
-__device__ __forceinline__ void norm_rope_row(float* xv, bool has_w, const float* w, float eps,
-                                              int norm_d, int n_pairs, int neox, int lane,
-                                              CS cos_sin) {
-    if (has_w) {  // ops::rms_norm (src/ops.rs:13-27) per head
-        float ss = 0.f;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) ss += xv[j] * xv[j];
-#pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) ss = wave_sum_xor(ss, sh);
-        const float inv = 1.0f / sqrtf(ss / (float)norm_d + eps);
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) xv[j] = (xv[j] * inv) * w[j];
-    }
-    rope_row<EPL>(xv, n_pairs, neox, lane, cos_sin);
-}
-
-// norm_rope_row over MR rows of a wavefront at once: the rows' RMSNorm sums are reduced
-// together (MR independent chains in each cross-lane step, each in the same order as
-// norm_rope_row's) and their rotations follow back to back, so the cross-lane latencies
-// overlap instead of adding up row after row.  cos_sin(m, i, c, s) gives row m's pair i.
-template <int EPL, int MR, typename CS>
-__device__ __forceinline__ void norm_rope_rows(float (*xv)[EPL], const bool* has_w,
-                                               const float* const* w, float eps, int norm_d,
-                                               int n_pairs, int neox, int lane, CS cos_sin) {
-    float ss[MR];
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        ss[m] = 0.f;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) ss[m] += xv[m][j] * xv[m][j];
-    }
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m) ss[m] = wave_sum_xor(ss[m], sh);
-    }
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        if (has_w[m]) {  // ops::rms_norm (src/ops.rs:13-27) per head
-            const float inv = 1.0f / sqrtf(ss[m] / (float)norm_d + eps);
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) xv[m][j] = (xv[m][j] * inv) * w[m][j];
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
-        rope_row<EPL>(xv[m], n_pairs, neox, lane, [&](int i, float* c, float* sn) { cos_sin(m, i, c, sn); });
 }
 
 // The K / V side of a prompt launch, one workgroup per (16-position page, K head): the
@@ -511,9 +472,6 @@ __device__ __forceinline__ void prologue_page(float* __restrict__ k, const float
             const size_t row = (((size_t)sq * n_tok + (pa + sl - start)) * hkv + h) * D + e0;
             load_vec<EPL>(xs[m], k + row);
             load_vec<EPL>(vs[m], v + row);
-        } else {
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) xs[m][j] = vs[m][j] = 0.f;
         }
     }
     if (kn) load_vec<EPL>(kw, kn + e0);
@@ -524,26 +482,16 @@ __device__ __forceinline__ void prologue_page(float* __restrict__ k, const float
         cs_n[sl * n_pairs + pr] = sinf(theta);
     }
     __syncthreads();
-    {
-        bool hw[4];
-        const float* wp[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            hw[m] = kn != nullptr && s0 + wv + 4 * m < s1;
-            wp[m] = kw;
-        }
-        norm_rope_rows<EPL, 4>(xs, hw, wp, eps, norm_d, n_pairs, neox, lane,
-                               [&](int m, int i, float* c, float* sn) {
-                                   const int sl = min(s0 + wv + 4 * m, kPageTokens - 1);  // rows past s1: unused
-                                   *c = cs_c[sl * n_pairs + i];
-                                   *sn = cs_n[sl * n_pairs + i];
-                               });
-    }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const int sl = s0 + wv + 4 * m;
         if (sl >= s1) break;
         float* xv = xs[m];
+        norm_rope_row<EPL>(xv, kn != nullptr, kw, eps, norm_d, n_pairs, neox, lane,
+                           [&](int i, float* c, float* sn) {
+                               *c = cs_c[sl * n_pairs + i];
+                               *sn = cs_n[sl * n_pairs + i];
+                           });
         store_vec<EPL>(k + (((size_t)sq * n_tok + (pa + sl - start)) * hkv + h) * D + e0, xv);
         if (app) {
 #pragma unroll
@@ -649,27 +597,12 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
             if (head < h1) {
                 load_vec<EPL>(xs[m], row_of(head) + e0);
                 if (head >= hq) load_vec<EPL>(vs[m], v + (((size_t)sq * n_tok + t) * hkv + (head - hq)) * D + e0);
-            } else {
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) xs[m][j] = 0.f;
             }
         }
         if (!wl) {
             if (qn) load_vec<EPL>(qw, qn + e0);
             if (kn) load_vec<EPL>(kw, kn + e0);
             wl = true;
-        }
-        {
-            bool hw[MH];
-            const float* wp[MH];
-#pragma unroll
-            for (int m = 0; m < MH; ++m) {
-                const int head = head0 + 4 * m;
-                hw[m] = head < h1 && (head < hq ? qn != nullptr : kn != nullptr);
-                wp[m] = head < hq ? qw : kw;
-            }
-            norm_rope_rows<EPL, MH>(xs, hw, wp, eps, norm_d, n_pairs, neox, lane,
-                                    [&](int, int i, float* c, float* sn) { cos_sin(i, c, sn); });
         }
 #pragma unroll
         for (int m = 0; m < MH; ++m) {
@@ -679,6 +612,8 @@ __global__ __launch_bounds__(256) void attn_prologue_vec_kernel(
             const int kvh = head - hq;
             float* x = row_of(head);
             float* xv = xs[m];
+            norm_rope_row<EPL>(xv, is_q ? qn != nullptr : kn != nullptr, is_q ? qw : kw, eps, norm_d,
+                               n_pairs, neox, lane, cos_sin);
             store_vec<EPL>(x + e0, xv);
             // append-then-attend (src/model/mod.rs:1140-1146): K (normed, rotated) and V at pos
             const int lp = pos / kPageTokens;
